@@ -1,0 +1,190 @@
+"""Independent big-integer brute force of the projection contract (this project's own code).
+
+Used to pin the C oracle: every quantity is derived from first principles with Python's
+unbounded integers and ``fractions.Fraction`` -- the f16 and f32 values come from numpy's
+IEEE conversions (exact in float64), not from any bit-level decode shared with the oracle.
+
+* f16 scale      -> exact real value * 2^32 (an integer for every finite f16)
+* f32 activation -> round-half-away(v * 2^32)
+* act scale      -> the least power of two S with 127*S >= absmax (searched, not computed)
+* codes          -> round-half-away(x / S)
+* weights        -> the documented GGUF formulas on exact values
+* output         -> floor((sum w*xhat + 2^31) / 2^32)
+"""
+from __future__ import annotations
+
+from fractions import Fraction
+import math
+
+import numpy as np
+
+TWO32 = 1 << 32
+
+
+def f16_value(word: int) -> Fraction | None:
+    v = np.array([word], dtype=np.uint16).view(np.float16)[0]
+    if not np.isfinite(v):
+        return None
+    return Fraction(float(v))
+
+
+def f16_q32(word: int) -> int | None:
+    v = f16_value(word)
+    if v is None:
+        return None
+    q = v * TWO32
+    assert q.denominator == 1
+    return int(q)
+
+
+def round_half_away(fr: Fraction) -> int:
+    sign = -1 if fr < 0 else 1
+    a = abs(fr)
+    fl = math.floor(a)
+    if a - fl >= Fraction(1, 2):
+        fl += 1
+    return sign * fl
+
+
+def f32_q32(bits: int) -> int | None:
+    v = np.array([bits], dtype=np.uint32).view(np.float32)[0]
+    if not np.isfinite(v):
+        return None
+    q = round_half_away(Fraction(float(v)) * TWO32)
+    if q < -(1 << 63) or q >= (1 << 63):
+        return None
+    return q
+
+
+def least_pow2_scale(absmax: int) -> int | None:
+    if absmax == 0:
+        return 0
+    s = 1
+    while 127 * s < absmax:
+        s *= 2
+        if s > (1 << 62):
+            return None
+    return s
+
+
+def quant_act(x: list[int]):
+    codes, scales = [], []
+    for b in range(0, len(x), 32):
+        blk = x[b:b + 32]
+        s = least_pow2_scale(max(abs(v) for v in blk))
+        if s is None:
+            return None
+        scales.append(s)
+        for v in blk:
+            c = 0 if s == 0 else round_half_away(Fraction(v, s))
+            if abs(c) > 127:
+                return None
+            codes.append(c)
+    for i, c in enumerate(codes):
+        if not -(1 << 63) <= scales[i // 32] * c < (1 << 63):
+            return None
+    return codes, scales
+
+
+def q4k_pairs(sc12: bytes) -> list[tuple[int, int]]:
+    """Sub-block (scale, min) pairs by the ggml packing rule, written from the format notes."""
+    out = []
+    for j in range(8):
+        if j < 4:
+            out.append((sc12[j] & 63, sc12[j + 4] & 63))
+        else:
+            lo = sc12[j + 4]
+            out.append(((lo & 0xF) | ((sc12[j - 4] >> 6) << 4), (lo >> 4) | ((sc12[j] >> 6) << 4)))
+    return out
+
+
+def weights_row(ggml_type: int, row: bytes, n: int) -> list[int] | None:
+    """Exact Q32.32 weights of one row, or None for a non-finite scale."""
+    w: list[int] = []
+    if ggml_type == 8:
+        for b in range(-(-n // 32)):
+            blk = row[34 * b:34 * b + 34]
+            d = f16_q32(blk[0] | (blk[1] << 8))
+            if d is None:
+                return None
+            w += [d * (c - 256 if c > 127 else c) for c in blk[2:34]]
+    elif ggml_type == 12:
+        for s in range(-(-n // 256)):
+            blk = row[144 * s:144 * s + 144]
+            d, dm = f16_q32(blk[0] | (blk[1] << 8)), f16_q32(blk[2] | (blk[3] << 8))
+            if d is None or dm is None:
+                return None
+            pairs = q4k_pairs(blk[4:16])
+            vals = [0] * 256
+            for j in range(8):
+                sc, m = pairs[j]
+                for l in range(32):
+                    byte = blk[16 + 32 * (j // 2) + l]
+                    q = (byte >> 4) if j % 2 else (byte & 0xF)
+                    vals[32 * j + l] = d * sc * q - dm * m
+            w += vals
+    elif ggml_type == 14:
+        for s in range(-(-n // 256)):
+            blk = row[210 * s:210 * s + 210]
+            d = f16_q32(blk[208] | (blk[209] << 8))
+            if d is None:
+                return None
+            vals = [0] * 256
+            for e in range(256):
+                half, r = divmod(e, 128)
+                t, l = divmod(r, 32)
+                qlb = blk[64 * half + l + 32 * (t & 1)]
+                lo = (qlb & 0xF) if t < 2 else (qlb >> 4)
+                hi = (blk[128 + 32 * half + l] >> (2 * t)) & 3
+                sc = blk[192 + e // 16]
+                sc = sc - 256 if sc > 127 else sc
+                vals[e] = d * sc * ((lo | (hi << 4)) - 32)
+            w += vals
+    else:
+        raise ValueError(ggml_type)
+    return w[:n]
+
+
+def matvec(ggml_type: int, raw: bytes, n_out: int, n_in: int, xhat: list[int]):
+    """floor((sum w*xhat + 2^31) / 2^32) per row, or None on a refusal."""
+    rb = {8: 34 * -(-n_in // 32), 12: 144 * -(-n_in // 256), 14: 210 * -(-n_in // 256)}[ggml_type]
+    ys = []
+    for o in range(n_out):
+        w = weights_row(ggml_type, raw[o * rb:(o + 1) * rb], n_in)
+        if w is None:
+            return None
+        acc = sum(a * b for a, b in zip(w, xhat))
+        ys.append((acc + (1 << 31)) >> 32)
+    return ys
+
+
+def block_dots(ggml_type: int, row: bytes, n_in: int, codes: list[int]):
+    """Exact integer group dots: per-32 (Q8_0 codes, Q4_K nibbles), per-16 (Q6_K u-32)."""
+    w_codes: list[int] = []
+    if ggml_type == 8:
+        for b in range(-(-n_in // 32)):
+            w_codes += [c - 256 if c > 127 else c for c in row[34 * b + 2:34 * b + 34]]
+        g = 32
+    elif ggml_type == 12:
+        for s in range(-(-n_in // 256)):
+            blk = row[144 * s:144 * s + 144]
+            for j in range(8):
+                for l in range(32):
+                    byte = blk[16 + 32 * (j // 2) + l]
+                    w_codes.append((byte >> 4) if j % 2 else (byte & 0xF))
+        g = 32
+    else:
+        for s in range(-(-n_in // 256)):
+            blk = row[210 * s:210 * s + 210]
+            for e in range(256):
+                half, r = divmod(e, 128)
+                t, l = divmod(r, 32)
+                qlb = blk[64 * half + l + 32 * (t & 1)]
+                lo = (qlb & 0xF) if t < 2 else (qlb >> 4)
+                hi = (blk[128 + 32 * half + l] >> (2 * t)) & 3
+                w_codes.append((lo | (hi << 4)) - 32)
+        g = 16
+    dots = []
+    for b in range(-(-n_in // g)):
+        dots.append(sum(w_codes[i] * codes[i] for i in range(b * g, min(n_in, b * g + g))))
+    return dots

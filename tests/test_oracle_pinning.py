@@ -1,0 +1,309 @@
+"""Pins the C oracle before anything is checked against it.
+
+Each oracle function is compared with (a) the reference's own known-answer tests, restated
+here with their file:line, (b) this project's independent big-integer brute force
+(tests/golden/bruteforce.py), and (c) invariants the mathematics fixes.
+"""
+import numpy as np
+import pytest
+
+import bruteforce as bf
+import oracle
+from apeiron_amd import synth
+
+ONE = 1 << 32
+I64_MIN, I64_MAX = -(1 << 63), (1 << 63) - 1
+
+
+def test_f16_to_fixed_exhaustive():
+    # chart/tests.rs:85-102 checks all 65536 words; here against an exact rational decode.
+    for h in range(65536):
+        st, v = oracle.f16_to_fixed(h)
+        want = bf.f16_q32(h)
+        if want is None:
+            assert st == 6, hex(h)  # NonFiniteScale
+        else:
+            assert st == 0 and v == want, hex(h)
+
+
+def _f32_words(rng, n):
+    edge = [0, 0x80000000, 1, 0x80000001, 0x007FFFFF, 0x00800000, 0x3F800000, 0xBF800000,
+            0x2F800000, 0x2F000000, 0x2EFFFFFF, 0x2F000001, 0xAF000000, 0x30000000,
+            0x4EFFFFFF, 0x4F000000, 0xCF000000, 0xCF000001, 0x7F7FFFFF, 0x7F800000,
+            0xFF800000, 0x7FC00000, 0x33800000, 0x34000000, 0x33FFFFFF]
+    # ties: v*2^32 = k + 1/2 at small exponents
+    for k in range(1, 40):
+        edge.append(int(np.array([np.float32((2 * k + 1) / 2 ** 33)]).view(np.uint32)[0]))
+        edge.append(int(np.array([np.float32(-(2 * k + 1) / 2 ** 33)]).view(np.uint32)[0]))
+    rnd = rng.integers(0, 1 << 32, size=n, dtype=np.uint64).tolist()
+    normals = rng.standard_normal(n).astype(np.float32).view(np.uint32).tolist()
+    return edge + rnd + normals
+
+
+def test_to_q32_against_exact_rounding():
+    rng = np.random.default_rng(7)
+    for w in _f32_words(rng, 4000):
+        st, v = oracle.to_q32(w)
+        f = np.array([w], dtype=np.uint32).view(np.float32)[0]
+        want = bf.f32_q32(w)
+        if not np.isfinite(f):
+            assert st == 10, hex(w)
+        elif want is None:
+            assert st == 11, hex(w)
+        else:
+            assert st == 0 and v == want, hex(w)
+
+
+def test_act_scale_reference_samples_and_bruteforce():
+    # kern/pow2.rs:105-135 sample table and its properties.
+    samples = [0, 1, 126, 127, 128, 254, 255, 1 << 20, (1 << 20) + 1, 127 << 40, (127 << 40) + 1,
+               127 << 56, (127 << 56) + 1, (1 << 64) - 1]
+    rng = np.random.default_rng(3)
+    samples += [int(v) for v in rng.integers(0, 1 << 63, size=300, dtype=np.uint64)]
+    for a in samples:
+        s = oracle.act_scale(a)
+        c = -(-a // 127)
+        if s is None:
+            assert c > (1 << 62), a
+            continue
+        if s == 0:
+            assert a == 0
+            continue
+        assert s & (s - 1) == 0
+        assert s * 127 >= a
+        assert s == 1 or (s // 2) * 127 < a
+        assert s < 2 * max(c, 1)
+        assert s == bf.least_pow2_scale(a)
+
+
+def test_quant_act_reference_kats():
+    # chart/tests.rs:397-415
+    st, codes, scales = oracle.quant_act([3, 130, -3])
+    assert st == 0 and codes[0] == 2 and codes[2] == -2 and scales[0] == 2
+    st, codes, scales = oracle.quant_act([0] * 64)
+    assert st == 0 and not codes.any() and not scales.any()
+    st, _, _ = oracle.quant_act([I64_MAX] * 32)
+    assert st == 7  # FixedOverflow: code 64 * 2^57 leaves i64
+    st, codes, scales = oracle.quant_act([I64_MIN] * 32)
+    assert st == 0 and scales.tolist() == [1 << 57]
+    st, xhat = oracle.dequant_act(codes, scales)
+    assert st == 0 and xhat.tolist() == [I64_MIN] * 32
+    st, codes, scales = oracle.quant_act([127 << 56] * 32)
+    assert st == 0
+    assert oracle.dequant_act(codes, scales)[1].tolist() == [127 << 56] * 32
+
+
+def test_quant_act_invariants_and_bruteforce():
+    # chart/tests.rs:373-395 properties, plus equality with the brute force.
+    for seed in range(16):
+        rng = np.random.default_rng(0x5EED1000 + seed)
+        x = ((rng.integers(0, 4096, size=200) - 2048) * 1_000_003).astype(np.int64)
+        st, codes, scales = oracle.quant_act(x)
+        assert st == 0
+        assert codes.shape == (200,) and scales.shape == (7,)
+        xhat = oracle.dequant_act(codes, scales)[1]
+        for j, xv in enumerate(x.tolist()):
+            s = int(scales[j // 32])
+            assert abs(int(codes[j])) <= 127
+            if s == 0:
+                assert codes[j] == 0
+            assert 2 * abs(xv - int(xhat[j])) <= s
+        ref = bf.quant_act(x.tolist())
+        assert codes.tolist() == ref[0] and scales.tolist() == ref[1]
+    # wide magnitude spread, zero blocks, ragged tail
+    rng = np.random.default_rng(11)
+    x = [0] * 32 + [int(v) for v in rng.integers(-(1 << 62), 1 << 62, size=71)]
+    st, codes, scales = oracle.quant_act(x)
+    ref = bf.quant_act(x)
+    assert st == 0 and codes.tolist() == ref[0] and scales.tolist() == ref[1]
+
+
+def test_quant_act_f32_matches_bruteforce():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(896).astype(np.float32)
+    x[:32] = 0
+    x[40] = 1e-12
+    st, codes, scales = oracle.quant_act_f32(x)
+    q = [bf.f32_q32(int(w)) for w in x.view(np.uint32)]
+    ref = bf.quant_act(q)
+    assert st == 0 and codes.tolist() == ref[0] and scales.tolist() == ref[1]
+    assert oracle.quant_act_f32(np.array([np.inf], np.float32))[0] == 10
+    assert oracle.quant_act_f32(np.array([3e9], np.float32))[0] == 11
+
+
+def test_format_unpack_kats():
+    # format/quant.rs:873-883: Q4_K codes[0]=3, codes[32]=0xA, pair (5,7) -- read through the
+    # dequantizer with d = dmin = 1.0 so w = sc*q - m.
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = [0x00, 0x3C]
+    blk[2:4] = [0x00, 0x3C]
+    blk[4], blk[8], blk[16] = 5, 7, 0xA3
+    st, w = oracle.dequant_row(12, blk, 256)
+    assert st == 0
+    assert w[0] == (5 * 3 - 7) * ONE
+    # sub-block 1 (high nibble) uses pair 1 = (scales[1]&63, scales[5]&63) = (0, 0)
+    assert w[32] == 0
+    # format/quant.rs:886-897: Q6_K codes[0] = -15, codes[32] = -32, with d = 1, sc = 1
+    b6 = np.zeros(210, np.uint8)
+    b6[0], b6[128] = 0x01, 0x01
+    b6[192:208] = 1
+    b6[208:210] = [0x00, 0x3C]
+    st, w = oracle.dequant_row(14, b6, 256)
+    assert st == 0 and w[0] == -15 * ONE and w[32] == -32 * ONE
+    # Q8_0 (format/quant.rs:858-869): d = 0.5, codes 2 and -2
+    b8 = np.zeros(34, np.uint8)
+    b8[0:2] = [0x00, 0x38]
+    b8[2], b8[3] = 2, 0xFE
+    st, w = oracle.dequant_row(8, b8, 32)
+    assert st == 0 and w[0] == ONE and w[1] == -ONE
+
+
+def test_matvec_fixed_reference_kats():
+    # engine/tests.rs:389-407: 2x2 Q8_0, d = 0.5, codes 3 and 2, x = [1, 1] -> y = [2, 1].
+    raw = np.zeros(68, np.uint8)
+    raw[0:2] = [0x00, 0x38]
+    raw[34:36] = [0x00, 0x38]
+    raw[2], raw[36] = 3, 2
+    st, y = oracle.matvec_fixed(8, raw, 2, 2, [1, 1])
+    assert st == 0 and y.tolist() == [2, 1]
+    # engine/tests.rs:435-439 ties via a one-weight row of value ONE/2: 1.5 -> 2, -1.5 -> -1, 0.5 -> 1
+    r1 = np.zeros(34, np.uint8)
+    r1[0:2] = [0x00, 0x38]
+    r1[2] = 1
+    assert oracle.matvec_fixed(8, r1, 1, 1, [3])[1].tolist() == [2]
+    assert oracle.matvec_fixed(8, r1, 1, 1, [-3])[1].tolist() == [-1]
+    assert oracle.matvec_fixed(8, r1, 1, 1, [1])[1].tolist() == [1]
+    # engine/tests.rs:409-432 refusals
+    assert oracle.matvec_fixed(8, np.zeros(68, np.uint8), 2, 2, [ONE])[0] == 1
+    assert oracle.matvec_fixed(8, np.zeros(34, np.uint8), 2, 2, [ONE, ONE])[0] == 3
+    assert oracle.matvec_fixed(999, np.zeros(4, np.uint8), 1, 1, [ONE])[0] == 5
+
+
+SHAPES = [(4, 32), (3, 48), (2, 33), (2, 300), (1, 64), (5, 0), (1, 256), (2, 512), (2, 256)]
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+def test_matvec_random_payloads_vs_bruteforce(t):
+    # chart/tests.rs:222-267 shapes, random block bytes with d = dmin = 0x3800.
+    rng = np.random.default_rng(0x12345678 + t)
+    for rows, n_in in SHAPES + [(2, w) for w in (33, 47, 65, 257, 300, 271)]:
+        raw = synth.random_bytes_payload(rng, t, rows, n_in, 0x3800, 0x3800)
+        x = (rng.integers(0, 4096, size=n_in) - 2048).astype(np.int64)
+        st, codes, scales = oracle.quant_act(x)
+        assert st == 0
+        st, y = oracle.matvec_q8act(t, raw, rows, n_in, codes, scales)
+        xhat = oracle.dequant_act(codes, scales)[1]
+        want = bf.matvec(t, raw.tobytes(), rows, n_in, xhat.tolist())
+        assert st == 0 and y.tolist() == want, (t, rows, n_in)
+        stf, yf = oracle.matvec_q8act_fast(t, raw, rows, n_in, codes, scales, 2)
+        assert stf == 0 and yf.tolist() == want, (t, rows, n_in)
+        for r in range(rows):
+            rb = synth.row_bytes(t, n_in)
+            row = raw[r * rb:(r + 1) * rb]
+            st, dots, xs = oracle.block_dots(t, row, n_in, codes)
+            assert st == 0
+            assert dots.tolist() == bf.block_dots(t, row.tobytes(), n_in, codes.tolist())
+            assert xs.tolist() == [int(codes[b:b + 32].astype(np.int64).sum()) for b in range(0, n_in, 32)]
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+def test_extreme_scales_and_codes(t):
+    # chart/tests.rs:269-307: largest finite scale 0x7BFF, codes +-127 at unit scale.
+    rng = np.random.default_rng(0x51FF0000 + t)
+    raw = synth.random_bytes_payload(rng, t, 2, 256, 0x7BFF, 0x7BFF)
+    codes = np.array([127 if j % 2 == 0 else -127 for j in range(256)], np.int8)
+    scales = np.ones(8, np.int64)
+    st, y = oracle.matvec_q8act(t, raw, 2, 256, codes, scales)
+    want = bf.matvec(t, raw.tobytes(), 2, 256, [int(c) for c in codes])
+    assert st == 0 and y.tolist() == want
+    assert oracle.matvec_q8act_fast(t, raw, 2, 256, codes, scales, 1)[1].tolist() == want
+
+
+def test_q8_0_scale_sets_and_spread():
+    # kern/gemm.rs:2613-2617 scale-word sets (subnormal, negative, zero, largest) and wide
+    # activation spreads (kern/gemm.rs:2490-2506).
+    sets = [[0x2000, 0x2400, 0x1C00, 0xA000], [0x0001, 0x03FF, 0x0400, 0x8200],
+            [0x0000, 0x3C00, 0x0010, 0x7BFF]]
+    rng = np.random.default_rng(0x6E6D6D71)
+    for si, words in enumerate(sets):
+        for rng_bits in (1, 8, 30):
+            n_out, n_in = 5, 96
+            raw = rng.integers(0, 256, size=(n_out * 3, 34), dtype=np.uint8)
+            w = rng.choice(words, size=n_out * 3)
+            raw[:, 0], raw[:, 1] = w & 0xFF, w >> 8
+            raw = raw.reshape(-1)
+            mags = 1 << (20 + rng.integers(0, rng_bits, size=n_in))
+            x = np.array([int(rng.integers(-m, m + 1)) if (j // 32) % 7 != 3 else 0
+                          for j, m in enumerate(mags.tolist())], dtype=np.int64)
+            st, codes, scales = oracle.quant_act(x)
+            assert st == 0
+            xhat = oracle.dequant_act(codes, scales)[1]
+            want = bf.matvec(8, raw.tobytes(), n_out, n_in, xhat.tolist())
+            st, y = oracle.matvec_q8act(8, raw, n_out, n_in, codes, scales)
+            stf, yf = oracle.matvec_q8act_fast(8, raw, n_out, n_in, codes, scales, 3)
+            if any(not I64_MIN <= v <= I64_MAX for v in want):
+                # the contract refuses an output that leaves i64 (ops/matvec.rs:113-115)
+                assert st == 9 and stf == 9, (si, rng_bits)
+                continue
+            assert st == 0 and y.tolist() == want, (si, rng_bits)
+            assert stf == 0 and yf.tolist() == want
+
+
+def test_nonfinite_scale_refuses():
+    # kern/gemm.rs:2756-2763: an f16 +inf scale refuses (NonFiniteScale), also on the fast path.
+    rng = np.random.default_rng(1)
+    for t in (8, 12, 14):
+        raw = synth.random_bytes_payload(rng, t, 3, 256, 0x3800, 0x3800)
+        rb = synth.row_bytes(t, 256)
+        off = rb + (208 if t == 14 else 0)
+        raw[off:off + 2] = [0x00, 0x7C]
+        st, codes, scales = oracle.quant_act(np.arange(256, dtype=np.int64) - 100)
+        assert oracle.matvec_q8act(t, raw, 3, 256, codes, scales)[0] == 6
+        assert oracle.matvec_q8act_fast(t, raw, 3, 256, codes, scales, 2)[0] == 6
+
+
+def test_zero_activation_blocks():
+    # chart/tests.rs:336-371
+    x = np.zeros(96, np.int64)
+    x[64:] = 1000 - 100 * np.arange(64, 96)
+    st, codes, scales = oracle.quant_act(x)
+    assert st == 0 and not codes[:64].any() and scales[0] == 0 and scales[1] == 0
+    rng = np.random.default_rng(0x9000)
+    for t in (8, 12, 14):
+        raw = synth.random_bytes_payload(rng, t, 1, 96, 0x3800, 0x3800)
+        xhat = oracle.dequant_act(codes, scales)[1]
+        want = bf.matvec(t, raw.tobytes(), 1, 96, xhat.tolist())
+        assert oracle.matvec_q8act(t, raw, 1, 96, codes, scales)[1].tolist() == want
+
+
+def test_matmat_fast_equals_per_column_contract():
+    # kern/matmat.rs:973-1149 shape: every column equals the per-column contract.
+    rng = np.random.default_rng(21)
+    for t, n_out, n_in in [(8, 17, 64), (12, 9, 512), (14, 7, 256), (12, 5, 896), (8, 3, 96)]:
+        raw = synth.payload(t, rng, n_out, n_in)
+        x = synth.activations(rng, n_in, 9)
+        st, codes, scales = oracle.quant_act_f32_batch(x)
+        assert st == 0
+        st, y = oracle.matmat_q8act_fast(t, raw, n_out, n_in, codes, scales, 3)
+        assert st == 0
+        for c in range(9):
+            assert y[c].tolist() == oracle.matvec_q8act(t, raw, n_out, n_in, codes[c], scales[c])[1].tolist()
+
+
+def test_synth_generators_roundtrip():
+    # The packers invert the reference unpack rules (format/quant.rs:482-491, :574-599).
+    rng = np.random.default_rng(4)
+    sc = rng.integers(0, 64, size=(50, 8))
+    m = rng.integers(0, 64, size=(50, 8))
+    packed = synth.pack_q4_k_scales(sc, m)
+    for i in range(50):
+        assert bf.q4k_pairs(bytes(packed[i])) == list(zip(sc[i].tolist(), m[i].tolist()))
+    u = rng.integers(0, 64, size=(3, 256))
+    ql, qh = synth.pack_q6_k_codes(u)
+    for i in range(3):
+        blk = np.zeros(210, np.uint8)
+        blk[:128], blk[128:192] = ql[i], qh[i]
+        blk[192:208] = 1
+        blk[208:210] = [0x00, 0x3C]
+        w = oracle.dequant_row(14, blk, 256)[1]
+        assert (w // ONE + 32).tolist() == u[i].tolist()

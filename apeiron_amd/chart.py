@@ -1,0 +1,235 @@
+"""Host-side mirror of apeiron's int8-activation projection interface, backed by the HIP C ABI.
+
+Mirrors, with the same names, argument meaning and refusal behaviour:
+
+* ``QuantAct``          -- chart/mod.rs:67-81 (codes int8 [n_in], scales int64 [ceil(n_in/32)])
+* ``quant_act(x)``      -- chart/mod.rs:258 (x: Q32.32 int64); returns None where the reference
+                           returns None (an activation with no Q32.32 value)
+* ``matvec_q8act``      -- chart/mod.rs:1887 (returns f32 real outputs, see below)
+* ``matmat_q8act``      -- kern/matmat.rs:134 (one output vector per column)
+* ``MatvecError``       -- ops/matvec.rs:11-48, raised instead of returned
+
+Outputs are f32 real values: the reference's Q32.32 result of row o is
+round_shift_32(sum_i w_oi*xhat_i); ours is that sum * 2^-32 from exact integer group dots,
+accumulated in f32.  ``to_q32`` converts back to the engine's Q32.32 type where needed.
+
+Device memory here comes from PyTorch (plumbing only); every computation runs in
+libapeiron_hip.so.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+
+Q8_0, Q4_K, Q6_K = 8, 12, 14
+
+
+class MatvecError(Exception):
+    """A refused projection; ``kind`` is the MatvecError variant name (ops/matvec.rs:11-48)."""
+
+    def __init__(self, status: int, where: str = ""):
+        self.status = status
+        self.kind = _lib.STATUS.get(status, f"status{status}")
+        super().__init__(f"{self.kind}{(' in ' + where) if where else ''}")
+
+
+def _check(status: int, where: str) -> None:
+    if status != 0:
+        raise MatvecError(status, where)
+
+
+@dataclass
+class QuantAct:
+    scales: np.ndarray  # int64 [ceil(n/32)]
+    codes: np.ndarray   # int8 [n]
+
+    def __len__(self) -> int:
+        return int(self.codes.shape[0])
+
+
+class Device:
+    """One ah_ctx on one GPU (the backend's context; not thread-safe, like the reference pool)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _lib.load()
+        h = ctypes.c_void_p()
+        _check(self.lib.ah_init(device, ctypes.byref(h)), "ah_init")
+        self.h = h
+        self.device = device
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.ah_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def upload(self, ggml_type: int, raw: np.ndarray, n_out: int, n_in: int) -> "Tensor":
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        t = ctypes.c_void_p()
+        _check(self.lib.ah_upload_weight(self.h, ggml_type, raw.ctypes.data_as(ctypes.c_void_p),
+                                         raw.nbytes, n_out, n_in, ctypes.byref(t)), "upload")
+        return Tensor(self, t, ggml_type, n_out, n_in)
+
+    def wrap(self, ggml_type: int, dev_ptr: int, nbytes: int, n_out: int, n_in: int) -> "Tensor":
+        t = ctypes.c_void_p()
+        _check(self.lib.ah_wrap_weight_dev(self.h, ggml_type, dev_ptr, nbytes, n_out, n_in,
+                                           ctypes.byref(t)), "wrap")
+        return Tensor(self, t, ggml_type, n_out, n_in)
+
+    def sync_status(self, stream: int | None = None) -> int:
+        return self.lib.ah_sync_status(self.h, stream)
+
+    # device-pointer forms (enqueue only) -------------------------------------------------
+    def quant_act_f32_dev(self, x_ptr: int, n_tok: int, n_in: int, codes_ptr: int,
+                          scales_ptr: int, stream: int | None = None) -> None:
+        _check(self.lib.ah_quant_act_f32_dev(self.h, x_ptr, n_tok, n_in, codes_ptr, scales_ptr,
+                                             stream), "quant_act_f32_dev")
+
+    def quant_act_q32_dev(self, x_ptr: int, n_tok: int, n_in: int, codes_ptr: int,
+                          scales_ptr: int, stream: int | None = None) -> None:
+        _check(self.lib.ah_quant_act_q32_dev(self.h, x_ptr, n_tok, n_in, codes_ptr, scales_ptr,
+                                             stream), "quant_act_q32_dev")
+
+    # host forms -------------------------------------------------------------------------
+    def quant_act(self, x) -> QuantAct | None:
+        """chart/mod.rs:258: None exactly where the reference refuses."""
+        x = np.ascontiguousarray(x, dtype=np.int64)
+        n = x.shape[0]
+        codes = np.zeros(max(n, 1), np.int8)
+        scales = np.zeros(max(-(-n // 32), 1), np.int64)
+        st = self.lib.ah_quant_act(self.h, x.ctypes.data_as(ctypes.c_void_p), n,
+                                   codes.ctypes.data_as(ctypes.c_void_p),
+                                   scales.ctypes.data_as(ctypes.c_void_p))
+        if st == 7:
+            return None
+        _check(st, "quant_act")
+        return QuantAct(scales[: -(-n // 32)], codes[:n])
+
+
+class Tensor:
+    """A device-resident GGUF weight (unchanged layout)."""
+
+    def __init__(self, dev: Device, handle: ctypes.c_void_p, ggml_type: int, n_out: int, n_in: int):
+        self.dev, self.h = dev, handle
+        self.ggml_type, self.n_out, self.n_in = ggml_type, n_out, n_in
+
+    def free(self) -> None:
+        if self.h:
+            self.dev.lib.ah_free_tensor(self.dev.h, self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.dev.h:
+                self.free()
+        except Exception:
+            pass
+
+    def gemv_f32_dev(self, x_ptr: int, y_ptr: int, stream: int | None = None) -> None:
+        _check(self.dev.lib.ah_gemv_f32_dev(self.dev.h, self.h, x_ptr, y_ptr, stream), "gemv_f32")
+
+    def gemv_q8_dev(self, codes_ptr: int, scales_ptr: int, y_ptr: int, stream: int | None = None) -> None:
+        _check(self.dev.lib.ah_gemv_q8_dev(self.dev.h, self.h, codes_ptr, scales_ptr, y_ptr, stream),
+               "gemv_q8")
+
+    def gemv_q8_dots_dev(self, codes_ptr: int, scales_ptr: int, y_ptr: int, dots_ptr: int,
+                         stream: int | None = None) -> None:
+        _check(self.dev.lib.ah_gemv_q8_dots_dev(self.dev.h, self.h, codes_ptr, scales_ptr, y_ptr,
+                                                dots_ptr, stream), "gemv_q8_dots")
+
+    def gemm_f32_dev(self, x_ptr: int, n_tok: int, y_ptr: int, stream: int | None = None) -> None:
+        _check(self.dev.lib.ah_gemm_f32_dev(self.dev.h, self.h, x_ptr, n_tok, y_ptr, stream), "gemm_f32")
+
+    def gemm_q8_dev(self, codes_ptr: int, scales_ptr: int, n_tok: int, y_ptr: int,
+                    stream: int | None = None) -> None:
+        _check(self.dev.lib.ah_gemm_q8_dev(self.dev.h, self.h, codes_ptr, scales_ptr, n_tok, y_ptr,
+                                           stream), "gemm_q8")
+
+
+class GemvPlan:
+    """A grouped GEMV launch over fixed device pointers (ah_gemv_plan_*)."""
+
+    def __init__(self, dev: Device, tensors: list[Tensor], x_ptrs: list[int], y_ptrs: list[int]):
+        n = len(tensors)
+        W = (ctypes.c_void_p * n)(*[t.h.value for t in tensors])
+        X = (ctypes.c_void_p * n)(*x_ptrs)
+        Y = (ctypes.c_void_p * n)(*y_ptrs)
+        h = ctypes.c_void_p()
+        _check(dev.lib.ah_gemv_plan_create(dev.h, n, W, X, Y, ctypes.byref(h)), "gemv_plan_create")
+        self.dev, self.h, self.keep = dev, h, tensors
+
+    def run(self, stream: int | None = None) -> None:
+        _check(self.dev.lib.ah_gemv_plan_run(self.dev.h, self.h, stream), "gemv_plan_run")
+
+    def free(self) -> None:
+        if self.h:
+            self.dev.lib.ah_gemv_plan_free(self.dev.h, self.h)
+            self.h = None
+
+
+_default: Device | None = None
+
+
+def device() -> Device:
+    global _default
+    if _default is None:
+        _default = Device(0)
+    return _default
+
+
+def quant_act(x) -> QuantAct | None:
+    return device().quant_act(x)
+
+
+def matvec_q8act(ggml_type: int, raw: np.ndarray, n_out: int, n_in: int, q: QuantAct) -> np.ndarray:
+    """chart/mod.rs:1887 over the GPU: raises MatvecError where the reference returns Err."""
+    dev = device()
+    if len(q) != n_in:
+        raise MatvecError(1, "matvec_q8act")
+    w = dev.upload(ggml_type, raw, n_out, n_in)
+    try:
+        y = np.zeros(max(n_out, 1), np.float32)
+        codes = np.ascontiguousarray(q.codes, np.int8)
+        scales = np.ascontiguousarray(q.scales, np.int64)
+        _check(dev.lib.ah_matvec_q8act(dev.h, w.h, codes.ctypes.data_as(ctypes.c_void_p),
+                                       scales.ctypes.data_as(ctypes.c_void_p), len(q),
+                                       y.ctypes.data_as(ctypes.c_void_p)), "matvec_q8act")
+        return y[:n_out]
+    finally:
+        w.free()
+
+
+def matmat_q8act(ggml_type: int, raw: np.ndarray, n_out: int, n_in: int,
+                 qs: list[QuantAct]) -> np.ndarray:
+    """kern/matmat.rs:134 over the GPU: y[c] = matvec_q8act(..., qs[c]); returns [n_tok][n_out]."""
+    dev = device()
+    for q in qs:
+        if len(q) != n_in:
+            raise MatvecError(1, "matmat_q8act")
+    n_tok = len(qs)
+    w = dev.upload(ggml_type, raw, n_out, n_in)
+    try:
+        codes = np.ascontiguousarray(np.stack([q.codes for q in qs]) if qs else np.zeros((0, n_in)), np.int8)
+        scales = np.ascontiguousarray(np.stack([q.scales for q in qs]) if qs else np.zeros((0, 1)), np.int64)
+        y = np.zeros((max(n_tok, 1), max(n_out, 1)), np.float32)
+        _check(dev.lib.ah_matmat_q8act(dev.h, w.h, codes.ctypes.data_as(ctypes.c_void_p),
+                                       scales.ctypes.data_as(ctypes.c_void_p), n_tok,
+                                       y.ctypes.data_as(ctypes.c_void_p)), "matmat_q8act")
+        return y[:n_tok, :n_out]
+    finally:
+        w.free()
+
+
+def to_q32(y: np.ndarray) -> np.ndarray:
+    """f32 real outputs -> the engine's Q32.32 int64 (round half away, as F32::to_q32)."""
+    v = np.asarray(y, np.float64) * 4294967296.0
+    return (np.sign(v) * np.floor(np.abs(v) + 0.5)).astype(np.int64)

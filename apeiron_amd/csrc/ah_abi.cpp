@@ -1,0 +1,605 @@
+// ah_abi.cpp -- host side of the C ABI declared in include/apeiron_hip.h.
+//
+// Owns the device context (one HIP stream, a device status word, scratch), validates GGUF
+// geometry exactly like matvec_fixed (ops/matvec.rs:160-175), scans f16 block scales for the
+// NonFiniteScale refusal (num/dequant.rs:25-41), and plans the kernel launches.
+#include "apeiron_hip.h"
+#include "ah_internal.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <new>
+
+// launchers (ah_gemv.hip, ah_gemm.hip)
+hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart *d_parts,
+                          uint32_t n_parts, uint32_t grid, uint32_t kpad_max,
+                          unsigned long long *status, hipStream_t stream);
+hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream);
+hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes, uint32_t off0,
+                          uint32_t off1, int *d_bad, hipStream_t stream);
+hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes,
+                          uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t kpad,
+                          const _Float16 *xh, const _Float16 *xmin, const float *tok_scale,
+                          float *y, float *partials, uint32_t splits, hipStream_t stream);
+uint32_t ah_gemm_splits_used(uint32_t type, uint32_t n_in, uint32_t splits);
+hipError_t ah_launch_q4k_min(const int8_t *codes, const int64_t *scales, const float *tok_scale,
+                             uint32_t n_tok, uint32_t n_in, uint32_t kpad, _Float16 *xmin,
+                             hipStream_t stream);
+
+struct ah_ctx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    unsigned long long *d_status = nullptr;
+    int last_hip = 0;
+    int cu_count = 256;
+    void *scratch = nullptr;  // device scratch for GEMM operands / host-form staging
+    size_t scratch_bytes = 0;
+};
+
+struct ah_tensor {
+    uint32_t type = 0;
+    size_t n_out = 0, n_in = 0, row_bytes = 0, bytes = 0;
+    uint8_t *d = nullptr;
+    bool owned = false;
+};
+
+struct ah_gemv_plan {
+    uint32_t type = 0, n_parts = 0, grid = 0, kpad_max = 0;
+    GemvPart *d_parts = nullptr;
+};
+
+#define AH_HIP(ctx, call)                                                                       \
+    do {                                                                                        \
+        hipError_t e_ = (call);                                                                 \
+        if (e_ != hipSuccess) {                                                                 \
+            if (ctx) (ctx)->last_hip = (int)e_;                                                 \
+            return AH_ERR_HIP;                                                                  \
+        }                                                                                       \
+    } while (0)
+
+namespace {
+
+bool geom(uint32_t t, size_t &qk, size_t &bb) {
+    switch (t) {
+    case AH_GGML_Q8_0: qk = 32; bb = 34; return true;
+    case AH_GGML_Q4_K: qk = 256; bb = 144; return true;
+    case AH_GGML_Q6_K: qk = 256; bb = 210; return true;
+    default: return false;
+    }
+}
+
+// matvec_fixed's refusal order: type, then row stride / payload size overflow, then length.
+int32_t validate(uint32_t t, size_t raw_len, size_t n_out, size_t n_in, size_t &row_bytes,
+                 size_t &need) {
+    size_t qk, bb;
+    if (!geom(t, qk, bb)) return AH_ERR_UNSUPPORTED_QUANT;
+    const size_t blocks = n_in / qk + (n_in % qk != 0);
+    if (__builtin_mul_overflow(blocks, bb, &row_bytes)) return AH_ERR_LENGTH_OVERFLOW;
+    if (__builtin_mul_overflow(n_out, row_bytes, &need)) return AH_ERR_LENGTH_OVERFLOW;
+    if (raw_len < need) return AH_ERR_SHORT_PAYLOAD;
+    // Device limits of this backend: 32-bit buffer ranges and the LDS-resident activation.
+    if (need >= 0xFFFFFF00ull || n_in > AH_MAX_N_IN || n_out >= (1ull << 31)) return AH_ERR_INVALID_ARG;
+    return AH_OK;
+}
+
+void scale_offsets(uint32_t t, uint32_t &o0, uint32_t &o1, uint32_t &bb) {
+    if (t == AH_GGML_Q8_0) { o0 = o1 = 0; bb = 34; }
+    else if (t == AH_GGML_Q4_K) { o0 = 0; o1 = 2; bb = 144; }
+    else { o0 = o1 = 208; bb = 210; }
+}
+
+bool f16_nonfinite(uint16_t h) { return ((h >> 10) & 0x1f) == 0x1f; }
+
+hipStream_t pick(ah_ctx *ctx, void *stream) {
+    return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+}
+
+int32_t ensure_scratch(ah_ctx *ctx, size_t bytes) {
+    if (bytes <= ctx->scratch_bytes) return AH_OK;
+    if (ctx->scratch) {
+        // the old scratch may still be read by queued kernels
+        AH_HIP(ctx, hipDeviceSynchronize());
+        AH_HIP(ctx, hipFree(ctx->scratch));
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+    }
+    size_t want = bytes + (bytes >> 2) + 4096;
+    if (hipMalloc(&ctx->scratch, want) != hipSuccess) {
+        ctx->scratch = nullptr;
+        return AH_ERR_OUT_OF_MEMORY;
+    }
+    ctx->scratch_bytes = want;
+    return AH_OK;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+uint32_t units_per_row(uint32_t t, uint32_t n_in) {
+    return t == AH_GGML_Q8_0 ? (n_in + 31) / 32 : (n_in + 255) / 256;
+}
+
+// Lanes per row: the power of two in [4, 64] wasting the fewest unit slots (ties -> more lanes).
+uint32_t choose_log2g(uint32_t units) {
+    uint32_t best = 2, best_slots = ~0u;
+    for (uint32_t l = 2; l <= 6; ++l) {
+        const uint32_t G = 1u << l;
+        const uint32_t slots = (units + G - 1) / G * G;
+        if (slots <= best_slots) {
+            best_slots = slots;
+            best = l;
+        }
+    }
+    return best;
+}
+
+uint32_t gemv_grid(const ah_ctx *ctx, uint32_t n_out, uint32_t log2g) {
+    const uint32_t rows_per_iter = 4u * (64u >> log2g);
+    uint32_t g = (n_out + rows_per_iter - 1) / rows_per_iter;
+    const uint32_t cap = 4u * (uint32_t)ctx->cu_count;
+    if (g > cap) g = cap;
+    return g ? g : 1;
+}
+
+uint32_t kpad_of(size_t n_in) { return (uint32_t)((n_in + 255) / 256 * 256); }
+
+GemvPart make_part(const ah_tensor *w, uint32_t src, const void *x, const int64_t *scales, float *y,
+                   int32_t *dots) {
+    GemvPart P;
+    std::memset(&P, 0, sizeof(P));
+    P.w = w->d;
+    P.w_bytes = w->bytes;
+    P.x = x;
+    P.scales = scales;
+    P.y = y;
+    P.dots = dots;
+    P.n_out = (uint32_t)w->n_out;
+    P.n_in = (uint32_t)w->n_in;
+    P.row_bytes = (uint32_t)w->row_bytes;
+    P.wg_begin = 0;
+    P.log2g = choose_log2g(units_per_row(w->type, P.n_in));
+    P.src = src;
+    return P;
+}
+
+int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
+                    const int64_t *scales, float *y, int32_t *dots, void *stream) {
+    if (!ctx || !w || (!x && w->n_in) || (!y && w->n_out)) return AH_ERR_INVALID_ARG;
+    if (src == AH_SRC_CODES && !scales && w->n_in) return AH_ERR_INVALID_ARG;
+    if (w->n_out == 0) return AH_OK;
+    const GemvPart P = make_part(w, src, x, scales, y, dots);
+    const uint32_t grid = gemv_grid(ctx, P.n_out, P.log2g);
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, ah_launch_gemv(w->type, P, nullptr, 1, grid, kpad_of(w->n_in), ctx->d_status,
+                               pick(ctx, stream)));
+    return AH_OK;
+}
+
+int32_t reset_status(ah_ctx *ctx) {
+    const unsigned long long none = AH_ST_NONE;
+    AH_HIP(ctx, hipMemcpy(ctx->d_status, &none, sizeof(none), hipMemcpyHostToDevice));
+    return AH_OK;
+}
+
+// GEMM operand preparation + launch.  src = AH_SRC_F32 (x = f32 [n_tok][n_in]) or AH_SRC_CODES.
+int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
+                    const int64_t *scales_in, size_t n_tok, float *y, void *stream) {
+    if (!ctx || !w || !y || (!x && n_tok && w->n_in)) return AH_ERR_INVALID_ARG;
+    if (n_tok == 0 || w->n_out == 0) return AH_OK;
+    if (n_tok >= (1ull << 24)) return AH_ERR_INVALID_ARG;
+    const uint32_t n_in = (uint32_t)w->n_in, n_out = (uint32_t)w->n_out, N = (uint32_t)n_tok;
+    const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
+    // split-K so the grid covers the chip about twice
+    const uint32_t tiles = ((n_out + 127) / 128) * ((N + 127) / 128);
+    uint32_t want = tiles >= 2u * (uint32_t)ctx->cu_count ? 1u : (2u * (uint32_t)ctx->cu_count + tiles - 1) / tiles;
+    const uint32_t max_splits = w->type == AH_GGML_Q8_0 ? (n_in + 63) / 64 : nsb;
+    if (want > max_splits) want = max_splits;
+    if (want < 1) want = 1;
+    const uint32_t splits = ah_gemm_splits_used(w->type, n_in, want);
+
+    size_t off = 0;
+    const size_t o_codes = off; off = align256(off + (src == AH_SRC_F32 ? (size_t)N * n_in : 0));
+    const size_t o_scales = off; off = align256(off + (src == AH_SRC_F32 ? (size_t)N * nb32 * 8 : 0));
+    const size_t o_xh = off; off = align256(off + (size_t)N * kpad * 2);
+    const size_t o_ts = off; off = align256(off + (size_t)N * 4);
+    const size_t o_xmin = off; off = align256(off + (w->type == AH_GGML_Q4_K ? (size_t)N * nsb * 32 : 0));
+    const size_t o_part = off; off = align256(off + (splits > 1 ? (size_t)splits * N * n_out * 4 : 0));
+    int32_t st = ensure_scratch(ctx, off);
+    if (st) return st;
+    uint8_t *S = static_cast<uint8_t *>(ctx->scratch);
+    int8_t *codes = src == AH_SRC_F32 ? reinterpret_cast<int8_t *>(S + o_codes)
+                                      : const_cast<int8_t *>(static_cast<const int8_t *>(x));
+    int64_t *scales = src == AH_SRC_F32 ? reinterpret_cast<int64_t *>(S + o_scales)
+                                        : const_cast<int64_t *>(scales_in);
+    _Float16 *xh = reinterpret_cast<_Float16 *>(S + o_xh);
+    float *ts = reinterpret_cast<float *>(S + o_ts);
+    _Float16 *xmin = reinterpret_cast<_Float16 *>(S + o_xmin);
+    float *part = reinterpret_cast<float *>(S + o_part);
+    hipStream_t s = pick(ctx, stream);
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+
+    QuantArgs q;
+    q.x = src == AH_SRC_F32 ? x : nullptr;
+    q.codes = codes;
+    q.scales = scales;
+    q.xh = xh;
+    q.tok_scale = ts;
+    q.n_tok = N;
+    q.n_in = n_in;
+    q.nb32 = nb32;
+    q.kpad = kpad;
+    q.src = src;
+    q.status = ctx->d_status;
+    AH_HIP(ctx, ah_launch_quant(q, s));
+    if (w->type == AH_GGML_Q4_K) AH_HIP(ctx, ah_launch_q4k_min(codes, scales, ts, N, n_in, kpad, xmin, s));
+    AH_HIP(ctx, ah_launch_gemm(w->type, w->d, (uint32_t)w->bytes, (uint32_t)w->row_bytes, n_out, n_in, N,
+                               kpad, xh, xmin, ts, y, part, splits, s));
+    return AH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *ah_status_str(int32_t s) {
+    switch (s) {
+    case AH_OK: return "ok";
+    case AH_ERR_SHAPE_MISMATCH: return "shape mismatch";
+    case AH_ERR_ROW_LENGTH: return "row length";
+    case AH_ERR_SHORT_PAYLOAD: return "short payload";
+    case AH_ERR_LENGTH_OVERFLOW: return "length overflow";
+    case AH_ERR_UNSUPPORTED_QUANT: return "unsupported quant";
+    case AH_ERR_NONFINITE_SCALE: return "non-finite scale";
+    case AH_ERR_FIXED_OVERFLOW: return "fixed overflow";
+    case AH_ERR_ACCUMULATOR_OVERFLOW: return "accumulator overflow";
+    case AH_ERR_OUTPUT_OVERFLOW: return "output overflow";
+    case AH_ERR_NONFINITE_INPUT: return "non-finite input";
+    case AH_ERR_INPUT_RANGE: return "input out of range";
+    case AH_ERR_NO_DEVICE: return "no gfx950 device";
+    case AH_ERR_INVALID_ARG: return "invalid argument";
+    case AH_ERR_HIP: return "hip error";
+    case AH_ERR_OUT_OF_MEMORY: return "out of device memory";
+    default: return "unknown status";
+    }
+}
+
+int32_t ah_init(int32_t device, ah_ctx **out) {
+    if (!out) return AH_ERR_INVALID_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) return AH_ERR_NO_DEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return AH_ERR_NO_DEVICE;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return AH_ERR_NO_DEVICE;
+    ah_ctx *ctx = new (std::nothrow) ah_ctx();
+    if (!ctx) return AH_ERR_OUT_OF_MEMORY;
+    ctx->device = device;
+    ctx->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess ||
+        hipMalloc(&ctx->d_status, sizeof(unsigned long long)) != hipSuccess) {
+        delete ctx;
+        return AH_ERR_HIP;
+    }
+    if (reset_status(ctx) != AH_OK) {
+        hipFree(ctx->d_status);
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return AH_ERR_HIP;
+    }
+    *out = ctx;
+    return AH_OK;
+}
+
+int32_t ah_destroy(ah_ctx *ctx) {
+    if (!ctx) return AH_ERR_INVALID_ARG;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    if (ctx->scratch) hipFree(ctx->scratch);
+    hipFree(ctx->d_status);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return AH_OK;
+}
+
+int32_t ah_last_hip_error(const ah_ctx *ctx) { return ctx ? ctx->last_hip : 0; }
+
+int32_t ah_upload_weight(ah_ctx *ctx, uint32_t type, const void *raw, size_t raw_len, size_t n_out,
+                         size_t n_in, ah_tensor **out) {
+    if (!ctx || !out || (!raw && raw_len)) return AH_ERR_INVALID_ARG;
+    *out = nullptr;
+    size_t row_bytes, need;
+    int32_t st = validate(type, raw_len, n_out, n_in, row_bytes, need);
+    if (st) return st;
+    uint32_t o0, o1, bb;
+    scale_offsets(type, o0, o1, bb);
+    const uint8_t *b = static_cast<const uint8_t *>(raw);
+    for (size_t off = 0; off < need; off += bb) {
+        const uint16_t h0 = (uint16_t)(b[off + o0] | (b[off + o0 + 1] << 8));
+        const uint16_t h1 = (uint16_t)(b[off + o1] | (b[off + o1 + 1] << 8));
+        if (f16_nonfinite(h0) || f16_nonfinite(h1)) return AH_ERR_NONFINITE_SCALE;
+    }
+    ah_tensor *t = new (std::nothrow) ah_tensor();
+    if (!t) return AH_ERR_OUT_OF_MEMORY;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    if (hipMalloc(&t->d, need + 256) != hipSuccess) {
+        delete t;
+        return AH_ERR_OUT_OF_MEMORY;
+    }
+    if (hipMemcpy(t->d, raw, need, hipMemcpyHostToDevice) != hipSuccess) {
+        hipFree(t->d);
+        delete t;
+        return AH_ERR_HIP;
+    }
+    t->type = type;
+    t->n_out = n_out;
+    t->n_in = n_in;
+    t->row_bytes = row_bytes;
+    t->bytes = need;
+    t->owned = true;
+    *out = t;
+    return AH_OK;
+}
+
+int32_t ah_wrap_weight_dev(ah_ctx *ctx, uint32_t type, const void *d_raw, size_t raw_len, size_t n_out,
+                           size_t n_in, ah_tensor **out) {
+    if (!ctx || !out || (!d_raw && raw_len)) return AH_ERR_INVALID_ARG;
+    *out = nullptr;
+    size_t row_bytes, need;
+    int32_t st = validate(type, raw_len, n_out, n_in, row_bytes, need);
+    if (st) return st;
+    uint32_t o0, o1, bb;
+    scale_offsets(type, o0, o1, bb);
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    int *d_bad = nullptr;
+    AH_HIP(ctx, hipMalloc(&d_bad, sizeof(int)));
+    int bad = 0;
+    hipError_t e = hipMemcpy(d_bad, &bad, sizeof(int), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = ah_launch_scan(static_cast<const uint8_t *>(d_raw), need / bb, bb, o0, o1, d_bad, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = hipMemcpy(&bad, d_bad, sizeof(int), hipMemcpyDeviceToHost);
+    hipFree(d_bad);
+    if (e != hipSuccess) {
+        ctx->last_hip = (int)e;
+        return AH_ERR_HIP;
+    }
+    if (bad) return AH_ERR_NONFINITE_SCALE;
+    ah_tensor *t = new (std::nothrow) ah_tensor();
+    if (!t) return AH_ERR_OUT_OF_MEMORY;
+    t->type = type;
+    t->n_out = n_out;
+    t->n_in = n_in;
+    t->row_bytes = row_bytes;
+    t->bytes = need;
+    t->d = static_cast<uint8_t *>(const_cast<void *>(d_raw));
+    t->owned = false;
+    *out = t;
+    return AH_OK;
+}
+
+int32_t ah_free_tensor(ah_ctx *ctx, ah_tensor *t) {
+    if (!ctx || !t) return AH_ERR_INVALID_ARG;
+    if (t->owned && t->d) {
+        hipSetDevice(ctx->device);
+        hipStreamSynchronize(ctx->stream);
+        hipFree(t->d);
+    }
+    delete t;
+    return AH_OK;
+}
+
+int32_t ah_tensor_info(const ah_tensor *t, uint32_t *type, size_t *n_out, size_t *n_in,
+                       size_t *row_bytes, const void **d_raw) {
+    if (!t) return AH_ERR_INVALID_ARG;
+    if (type) *type = t->type;
+    if (n_out) *n_out = t->n_out;
+    if (n_in) *n_in = t->n_in;
+    if (row_bytes) *row_bytes = t->row_bytes;
+    if (d_raw) *d_raw = t->d;
+    return AH_OK;
+}
+
+static int32_t quant_dev(ah_ctx *ctx, uint32_t src, const void *d_x, size_t n_tok, size_t n_in,
+                         int8_t *d_codes, int64_t *d_scales, void *stream) {
+    if (!ctx || ((!d_x || !d_codes || !d_scales) && n_tok && n_in)) return AH_ERR_INVALID_ARG;
+    if (n_tok == 0 || n_in == 0) return AH_OK;
+    if (n_in >= (1ull << 31) || n_tok >= (1ull << 31)) return AH_ERR_INVALID_ARG;
+    QuantArgs q;
+    q.x = d_x;
+    q.codes = d_codes;
+    q.scales = d_scales;
+    q.xh = nullptr;
+    q.tok_scale = nullptr;
+    q.n_tok = (uint32_t)n_tok;
+    q.n_in = (uint32_t)n_in;
+    q.nb32 = (uint32_t)((n_in + 31) / 32);
+    q.kpad = kpad_of(n_in);
+    q.src = src;
+    q.status = ctx->d_status;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, ah_launch_quant(q, pick(ctx, stream)));
+    return AH_OK;
+}
+
+int32_t ah_quant_act_f32_dev(ah_ctx *ctx, const float *d_x, size_t n_tok, size_t n_in,
+                             int8_t *d_codes, int64_t *d_scales, void *stream) {
+    return quant_dev(ctx, AH_SRC_F32, d_x, n_tok, n_in, d_codes, d_scales, stream);
+}
+
+int32_t ah_quant_act_q32_dev(ah_ctx *ctx, const int64_t *d_x, size_t n_tok, size_t n_in,
+                             int8_t *d_codes, int64_t *d_scales, void *stream) {
+    return quant_dev(ctx, AH_SRC_Q32, d_x, n_tok, n_in, d_codes, d_scales, stream);
+}
+
+int32_t ah_gemv_f32_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, float *d_y, void *stream) {
+    return gemv_launch(ctx, w, AH_SRC_F32, d_x, nullptr, d_y, nullptr, stream);
+}
+
+int32_t ah_gemv_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
+                       const int64_t *d_scales, float *d_y, void *stream) {
+    return gemv_launch(ctx, w, AH_SRC_CODES, d_codes, d_scales, d_y, nullptr, stream);
+}
+
+int32_t ah_gemv_q8_dots_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
+                            const int64_t *d_scales, float *d_y, int32_t *d_dots, void *stream) {
+    if (!d_dots) return AH_ERR_INVALID_ARG;
+    return gemv_launch(ctx, w, AH_SRC_CODES, d_codes, d_scales, d_y, d_dots, stream);
+}
+
+int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w,
+                            const float *const *d_x, float *const *d_y, ah_gemv_plan **out) {
+    if (!ctx || !out || !w || !d_x || !d_y || n_parts == 0 || n_parts > 65536) return AH_ERR_INVALID_ARG;
+    *out = nullptr;
+    const uint32_t type = w[0]->type;
+    GemvPart *parts = static_cast<GemvPart *>(std::calloc(n_parts, sizeof(GemvPart)));
+    if (!parts) return AH_ERR_OUT_OF_MEMORY;
+    uint32_t wg = 0, kpad_max = 0;
+    for (size_t i = 0; i < n_parts; ++i) {
+        if (!w[i] || w[i]->type != type || !d_x[i] || !d_y[i] || w[i]->n_out == 0) {
+            std::free(parts);
+            return AH_ERR_INVALID_ARG;
+        }
+        parts[i] = make_part(w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr);
+        parts[i].wg_begin = wg;
+        wg += gemv_grid(ctx, parts[i].n_out, parts[i].log2g);
+        const uint32_t kp = kpad_of(w[i]->n_in);
+        kpad_max = kp > kpad_max ? kp : kpad_max;
+    }
+    ah_gemv_plan *p = new (std::nothrow) ah_gemv_plan();
+    if (!p) {
+        std::free(parts);
+        return AH_ERR_OUT_OF_MEMORY;
+    }
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMalloc(&p->d_parts, n_parts * sizeof(GemvPart));
+    if (e == hipSuccess) e = hipMemcpy(p->d_parts, parts, n_parts * sizeof(GemvPart), hipMemcpyHostToDevice);
+    std::free(parts);
+    if (e != hipSuccess) {
+        if (p->d_parts) hipFree(p->d_parts);
+        delete p;
+        ctx->last_hip = (int)e;
+        return AH_ERR_HIP;
+    }
+    p->type = type;
+    p->n_parts = (uint32_t)n_parts;
+    p->grid = wg;
+    p->kpad_max = kpad_max;
+    *out = p;
+    return AH_OK;
+}
+
+int32_t ah_gemv_plan_run(ah_ctx *ctx, const ah_gemv_plan *plan, void *stream) {
+    if (!ctx || !plan) return AH_ERR_INVALID_ARG;
+    GemvPart none;
+    std::memset(&none, 0, sizeof(none));
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, ah_launch_gemv(plan->type, none, plan->d_parts, plan->n_parts, plan->grid,
+                               plan->kpad_max, ctx->d_status, pick(ctx, stream)));
+    return AH_OK;
+}
+
+int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan) {
+    if (!ctx || !plan) return AH_ERR_INVALID_ARG;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    hipFree(plan->d_parts);
+    delete plan;
+    return AH_OK;
+}
+
+int32_t ah_gemm_f32_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, size_t n_tok, float *d_y,
+                        void *stream) {
+    return gemm_launch(ctx, w, AH_SRC_F32, d_x, nullptr, n_tok, d_y, stream);
+}
+
+int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes, const int64_t *d_scales,
+                       size_t n_tok, float *d_y, void *stream) {
+    if (!d_scales && n_tok) return AH_ERR_INVALID_ARG;
+    return gemm_launch(ctx, w, AH_SRC_CODES, d_codes, d_scales, n_tok, d_y, stream);
+}
+
+int32_t ah_sync_status(ah_ctx *ctx, void *stream) {
+    if (!ctx) return AH_ERR_INVALID_ARG;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, hipStreamSynchronize(pick(ctx, stream)));
+    unsigned long long key = AH_ST_NONE;
+    AH_HIP(ctx, hipMemcpy(&key, ctx->d_status, sizeof(key), hipMemcpyDeviceToHost));
+    if (key == AH_ST_NONE) return AH_OK;
+    int32_t r = reset_status(ctx);
+    if (r) return r;
+    return (int32_t)(key & 0xffu);
+}
+
+// ---- host convenience forms ----
+
+int32_t ah_matvec_q8act(ah_ctx *ctx, const ah_tensor *w, const int8_t *codes, const int64_t *scales,
+                        size_t n_codes, float *y) {
+    if (!ctx || !w || (!y && w->n_out)) return AH_ERR_INVALID_ARG;
+    if (n_codes != w->n_in) return AH_ERR_SHAPE_MISMATCH;
+    const size_t nb = (w->n_in + 31) / 32;
+    const size_t oc = 0, os = align256(w->n_in), oy = align256(os + nb * 8);
+    int32_t st = ensure_scratch(ctx, oy + w->n_out * 4);
+    if (st) return st;
+    uint8_t *S = static_cast<uint8_t *>(ctx->scratch);
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    if (w->n_in) {
+        AH_HIP(ctx, hipMemcpy(S + oc, codes, w->n_in, hipMemcpyHostToDevice));
+        AH_HIP(ctx, hipMemcpy(S + os, scales, nb * 8, hipMemcpyHostToDevice));
+    }
+    st = gemv_launch(ctx, w, AH_SRC_CODES, S + oc, reinterpret_cast<int64_t *>(S + os),
+                     reinterpret_cast<float *>(S + oy), nullptr, nullptr);
+    if (st) return st;
+    st = ah_sync_status(ctx, nullptr);
+    if (st) return st;
+    if (w->n_out) AH_HIP(ctx, hipMemcpy(y, S + oy, w->n_out * 4, hipMemcpyDeviceToHost));
+    return AH_OK;
+}
+
+int32_t ah_matmat_q8act(ah_ctx *ctx, const ah_tensor *w, const int8_t *codes, const int64_t *scales,
+                        size_t n_tok, float *y) {
+    if (!ctx || !w || (!y && n_tok && w->n_out)) return AH_ERR_INVALID_ARG;
+    if (n_tok == 0 || w->n_out == 0) return AH_OK;
+    const size_t nb = (w->n_in + 31) / 32;
+    // inputs live in a separate allocation: gemm_launch grows ctx->scratch for its operands
+    const size_t in_bytes = align256(n_tok * w->n_in) + align256(n_tok * nb * 8) + n_tok * w->n_out * 4;
+    uint8_t *buf = nullptr;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    if (hipMalloc(&buf, in_bytes) != hipSuccess) return AH_ERR_OUT_OF_MEMORY;
+    int8_t *dc = reinterpret_cast<int8_t *>(buf);
+    int64_t *ds = reinterpret_cast<int64_t *>(buf + align256(n_tok * w->n_in));
+    float *dy = reinterpret_cast<float *>(buf + align256(n_tok * w->n_in) + align256(n_tok * nb * 8));
+    hipError_t e = hipSuccess;
+    if (w->n_in) {
+        e = hipMemcpy(dc, codes, n_tok * w->n_in, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(ds, scales, n_tok * nb * 8, hipMemcpyHostToDevice);
+    }
+    int32_t st = e == hipSuccess ? gemm_launch(ctx, w, AH_SRC_CODES, dc, ds, n_tok, dy, nullptr) : AH_ERR_HIP;
+    if (st == AH_OK) st = ah_sync_status(ctx, nullptr);
+    if (st == AH_OK && hipMemcpy(y, dy, n_tok * w->n_out * 4, hipMemcpyDeviceToHost) != hipSuccess) st = AH_ERR_HIP;
+    hipFree(buf);
+    if (e != hipSuccess) ctx->last_hip = (int)e;
+    return st;
+}
+
+int32_t ah_quant_act(ah_ctx *ctx, const int64_t *x, size_t n, int8_t *codes, int64_t *scales) {
+    if (!ctx || ((!x || !codes || !scales) && n)) return AH_ERR_INVALID_ARG;
+    if (n == 0) return AH_OK;
+    const size_t nb = (n + 31) / 32;
+    const size_t ox = 0, oc = align256(n * 8), os = align256(oc + n);
+    int32_t st = ensure_scratch(ctx, os + nb * 8);
+    if (st) return st;
+    uint8_t *S = static_cast<uint8_t *>(ctx->scratch);
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, hipMemcpy(S + ox, x, n * 8, hipMemcpyHostToDevice));
+    st = quant_dev(ctx, AH_SRC_Q32, S + ox, 1, n, reinterpret_cast<int8_t *>(S + oc),
+                   reinterpret_cast<int64_t *>(S + os), nullptr);
+    if (st) return st;
+    st = ah_sync_status(ctx, nullptr);
+    if (st) return st;
+    AH_HIP(ctx, hipMemcpy(codes, S + oc, n, hipMemcpyDeviceToHost));
+    AH_HIP(ctx, hipMemcpy(scales, S + os, nb * 8, hipMemcpyDeviceToHost));
+    return AH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,126 @@
+// ah_internal.h -- shared device helpers and kernel argument blocks of the gfx950 backend.
+//
+// The arithmetic restated here follows the reference contract:
+//   to_q32            num/fp.rs:186-230 (round half away from zero, exact on the f32 fields)
+//   act_scale         kern/pow2.rs:11-39 (least power of two S with 127*S >= absmax)
+//   quant_act codes   chart/mod.rs:258-334 (q + [2r >= S], sign applied, |code| <= 127)
+//   dequantizes       chart/mod.rs:105-134 (every S*code must fit int64)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "apeiron_hip.h"
+
+#define AH_DEV __device__ __forceinline__
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Status word: the earliest failing element wins (atomicMin over (index << 8) | code).  Input
+// conversion failures are ordered before quantizer failures, as the boundary converts the whole
+// f32 vector before quant_act runs.
+#define AH_ST_NONE 0xFFFFFFFFFFFFFFFFull
+#define AH_QUANT_ORDER_BASE (1ull << 48)
+
+AH_DEV void ah_record(unsigned long long *st, unsigned long long key) {
+    if (st) atomicMin(st, key);
+}
+
+// ---- buffer resources: range-checked loads (out-of-range lanes read 0, never fault) ----
+
+AH_DEV __amdgpu_buffer_rsrc_t ah_rsrc(const void *p, uint32_t bytes) {
+    // word3 0x00020000: the gfx9-family raw buffer format (32-bit data, no swizzle).
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+AH_DEV u32x4 ah_ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+AH_DEV uint32_t ah_ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+// ---- exact integer helpers ----
+
+AH_DEV int32_t ah_sdot4(uint32_t a, uint32_t b, int32_t c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+AH_DEV uint32_t ah_alignbyte(uint32_t hi, uint32_t lo, uint32_t sh) {
+    return __builtin_amdgcn_alignbyte(hi, lo, sh);
+}
+AH_DEV float ah_f16_bits_to_f32(uint32_t bits16) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+    return (float)h;  // exact (v_cvt_f32_f16 keeps subnormals)
+}
+
+// f32 bits -> |round_half_away(v * 2^32)| and sign; returns 0, 10 (non-finite) or 11 (range).
+AH_DEV int ah_to_q32_mag(uint32_t bits, uint64_t &mag, bool &neg) {
+    uint32_t e = (bits >> 23) & 0xffu;
+    neg = (bits >> 31) != 0;
+    if (e == 0xffu) return 10;
+    uint32_t frac = bits & 0x7fffffu;
+    uint64_t m = e ? (uint64_t)(frac | 0x800000u) : (uint64_t)frac;
+    uint32_t ee = e ? e : 1u;
+    if (ee >= 118u) {
+        uint32_t k = ee - 118u;
+        if (k > 40u) return 11;
+        mag = m << k;  // m < 2^24, k <= 40: below 2^64
+    } else {
+        uint32_t sh = 118u - ee;
+        mag = sh > 24u ? 0ull : ((m + (1ull << (sh - 1u))) >> sh);
+    }
+    const uint64_t lim = 1ull << 63;
+    if (neg ? mag > lim : mag >= lim) return 11;
+    return 0;
+}
+
+// Exponent of the activation scale: -1 for absmax == 0 (S = 0), 63 for act_scale's None,
+// else e with S = 2^e the least power of two such that 127*S >= absmax.
+AH_DEV int ah_act_scale_exp(uint64_t absmax) {
+    if (absmax == 0) return -1;
+    uint64_t need = absmax / 127u + (absmax % 127u != 0);
+    if (need <= 1) return 0;
+    int e = 64 - __builtin_clzll(need - 1);  // ceil(log2(need))
+    return e > 62 ? 63 : e;
+}
+
+// The quant_act code of one magnitude under S = 2^e (e >= 0): q + [2r >= S] with the sign.
+// Sets `bad` when S*code leaves int64 (QuantAct::dequantizes).
+AH_DEV int ah_act_code(uint64_t mag, bool neg, int e, bool &bad) {
+    uint64_t c = e == 0 ? mag : (mag >> e) + ((mag >> (e - 1)) & 1ull);
+    // c <= 127 by the choice of S.  The product c*2^e must fit: positive < 2^63, negative <= 2^63.
+    if (e >= 56) {
+        uint64_t lim = 1ull << (63 - e);
+        if (neg ? c > lim : c >= lim) bad = true;
+    }
+    return neg ? -(int)c : (int)c;
+}
+
+// ---- kernel argument blocks ----
+
+enum { AH_SRC_F32 = 0, AH_SRC_Q32 = 1, AH_SRC_CODES = 2 };
+
+struct GemvPart {
+    const uint8_t *w;      // GGUF payload (device)
+    uint64_t w_bytes;      // n_out * row_bytes
+    const void *x;         // f32 / int64 activation, or int8 codes
+    const int64_t *scales; // with AH_SRC_CODES
+    float *y;
+    int32_t *dots;         // optional exact group dots [n_out][ngroups]
+    uint32_t n_out, n_in, row_bytes;
+    uint32_t wg_begin;     // first workgroup of this part in a grouped launch
+    uint32_t log2g;        // lanes per row = 1 << log2g
+    uint32_t src;          // AH_SRC_*
+};
+
+struct QuantArgs {
+    const void *x;         // f32 or int64 [n_tok][n_in]
+    int8_t *codes;         // [n_tok][n_in]
+    int64_t *scales;       // [n_tok][nb32]
+    _Float16 *xh;          // optional: GEMM operand [n_tok][kpad] f16, xq * 2^(e_b - E_tok)
+    float *tok_scale;      // optional: [n_tok] 2^(E_tok - 32) (0 for an all-zero token)
+    uint32_t n_tok, n_in, nb32, kpad;
+    uint32_t src;          // AH_SRC_F32 / AH_SRC_Q32 / AH_SRC_CODES (codes+scales given)
+    unsigned long long *status;
+};

@@ -1,0 +1,167 @@
+/*
+ * apeiron_hip.h -- C ABI of the MI355X (gfx950) backend for apeiron's quantized
+ * linear-layer path: GGUF block-quantized weights (Q8_0, Q4_K, Q6_K) times the
+ * power-of-two int8 activation quantizer, as a GEMV at decode (N = 1) and a GEMM at
+ * prefill (N > 1).
+ *
+ * Every function is extern "C", takes plain pointers and sizes, and returns an int32
+ * status.  No exceptions cross the ABI.  All paths cited below are in the apeiron tree.
+ *
+ * Conventions
+ *   - Weights live on the device in their unchanged GGUF byte layout: n_out rows of
+ *     ceil(n_in/qk) whole blocks (ops/matvec.rs:164-175).
+ *   - Activations are f32 (converted exactly as F32::to_q32, num/fp.rs:186-230) or
+ *     Q32.32 int64 (the engine's own type, engine/mod.rs:58-80), or already quantized
+ *     (codes int8 + scales int64, the QuantAct of chart/mod.rs:67-81).
+ *   - Outputs are f32 real values.  The reference's Q32.32 value of row o is
+ *     round_shift_32(sum_i w_oi * xhat_i); the f32 output is that sum * 2^-32 computed
+ *     from exact per-group integer dots with f32 accumulation.
+ *   - Functions suffixed _dev take DEVICE pointers and enqueue on `stream`
+ *     (a hipStream_t; NULL = the context's own stream); they return once enqueued.
+ *     Data-dependent refusals (non-finite or out-of-range input, an activation with no
+ *     Q32.32 value) are recorded on the device and returned by ah_sync_status().
+ *   - Functions without the suffix take HOST pointers and are synchronous.
+ *   - A context is not thread-safe; callers serialise on it (as the reference's pool lock,
+ *     chart/pool.rs:496-505).
+ */
+#ifndef APEIRON_HIP_H
+#define APEIRON_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: one per MatvecError variant (ops/matvec.rs:11-48) + boundary codes ---- */
+#define AH_OK 0
+#define AH_ERR_SHAPE_MISMATCH 1       /* MatvecError::ShapeMismatch                       */
+#define AH_ERR_ROW_LENGTH 2           /* MatvecError::RowLength                           */
+#define AH_ERR_SHORT_PAYLOAD 3        /* MatvecError::ShortPayload                        */
+#define AH_ERR_LENGTH_OVERFLOW 4      /* MatvecError::LengthOverflow                      */
+#define AH_ERR_UNSUPPORTED_QUANT 5    /* MatvecError::UnsupportedQuant                    */
+#define AH_ERR_NONFINITE_SCALE 6      /* MatvecError::Dequant(EngineError::NonFiniteScale)*/
+#define AH_ERR_FIXED_OVERFLOW 7       /* MatvecError::Dequant(EngineError::FixedOverflow) */
+#define AH_ERR_ACCUMULATOR_OVERFLOW 8 /* MatvecError::AccumulatorOverflow                 */
+#define AH_ERR_OUTPUT_OVERFLOW 9      /* MatvecError::OutputOverflow                      */
+#define AH_ERR_NONFINITE_INPUT 10     /* F32Error::NonFinite (num/f32_convert.rs:44-49)   */
+#define AH_ERR_INPUT_RANGE 11         /* F32Error::OutOfRange                             */
+#define AH_ERR_NO_DEVICE 20           /* no usable gfx950 device (the honest skip of       */
+                                      /* Vk::load, gpu/vulkan.rs:1097-1106)               */
+#define AH_ERR_INVALID_ARG 21         /* null pointer / bad handle / limits exceeded       */
+#define AH_ERR_HIP 22                 /* a HIP runtime call failed                         */
+#define AH_ERR_OUT_OF_MEMORY 23
+
+/* ggml type ids (format/quant.rs:20-49) */
+#define AH_GGML_Q8_0 8
+#define AH_GGML_Q4_K 12
+#define AH_GGML_Q6_K 14
+
+/* Largest n_in the GEMV keeps in LDS and the GEMM stages (both kernels refuse beyond). */
+#define AH_MAX_N_IN 65536
+
+typedef struct ah_ctx ah_ctx;
+typedef struct ah_tensor ah_tensor;
+
+/* ---- lifecycle ---------------------------------------------------------------------------- */
+
+/* Open device `device`, create the context stream.  AH_ERR_NO_DEVICE when there is no GPU
+ * or it is not gfx950.  (Boundary analogue of Vk::load, gpu/vulkan.rs:1097-1106.) */
+int32_t ah_init(int32_t device, ah_ctx **out);
+int32_t ah_destroy(ah_ctx *ctx);
+/* Human-readable name of a status code (static string). */
+const char *ah_status_str(int32_t status);
+/* The last HIP error the context saw (hipError_t as int), for diagnostics. */
+int32_t ah_last_hip_error(const ah_ctx *ctx);
+
+/* ---- weights -------------------------------------------------------------------------------- */
+
+/* Copy an n_out x n_in GGUF payload (host bytes, unchanged layout) to the device.
+ * Validates geometry like matvec_fixed (ops/matvec.rs:160-175: UNSUPPORTED_QUANT,
+ * LENGTH_OVERFLOW, SHORT_PAYLOAD) and scans every f16 block scale (d, dmin) for Inf/NaN:
+ * a non-finite tensor is refused with AH_ERR_NONFINITE_SCALE, the refusal the reference's
+ * row dequantizer makes for it (num/dequant.rs:25-41), so the caller keeps its CPU path.
+ * Replaces the resident-GGUF borrow of the reference (loader.rs:421-434, step.rs:375). */
+int32_t ah_upload_weight(ah_ctx *ctx, uint32_t ggml_type, const void *raw, size_t raw_len,
+                         size_t n_out, size_t n_in, ah_tensor **out);
+/* Wrap a payload already in device memory (not copied, not owned; must outlive the tensor).
+ * The f16 scale scan runs on the device. */
+int32_t ah_wrap_weight_dev(ah_ctx *ctx, uint32_t ggml_type, const void *d_raw, size_t raw_len,
+                           size_t n_out, size_t n_in, ah_tensor **out);
+int32_t ah_free_tensor(ah_ctx *ctx, ah_tensor *t);
+/* Geometry of a tensor: ggml type, n_out, n_in, row stride in bytes, device pointer. */
+int32_t ah_tensor_info(const ah_tensor *t, uint32_t *ggml_type, size_t *n_out, size_t *n_in,
+                       size_t *row_bytes, const void **d_raw);
+
+/* ---- activation quantizer (chart/mod.rs:258 quant_act; chart/ffn.rs:130,200 pooled forms) ---- */
+
+/* n_tok rows of n_in activations -> codes[n_tok][n_in] int8 and scales[n_tok][ceil(n_in/32)]
+ * int64 (Q32.32 power-of-two scales), bit-exact to quant_act(to_q32(x)) per row. */
+int32_t ah_quant_act_f32_dev(ah_ctx *ctx, const float *d_x, size_t n_tok, size_t n_in,
+                             int8_t *d_codes, int64_t *d_scales, void *stream);
+/* Same from Q32.32 int64 activations (the engine's native Vec<i64>). */
+int32_t ah_quant_act_q32_dev(ah_ctx *ctx, const int64_t *d_x, size_t n_tok, size_t n_in,
+                             int8_t *d_codes, int64_t *d_scales, void *stream);
+
+/* ---- decode GEMV, N = 1 (chart/mod.rs:1887 matvec_q8act; chart/ffn.rs:667 chunked form) ---- */
+
+/* y[n_out] = W x with the quantizer fused into the kernel prologue. */
+int32_t ah_gemv_f32_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, float *d_y,
+                        void *stream);
+/* y[n_out] = W x from pre-quantized codes[n_in] + scales[ceil(n_in/32)]. */
+int32_t ah_gemv_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
+                       const int64_t *d_scales, float *d_y, void *stream);
+
+/* Grouped GEMV: n_parts independent projections in ONE launch, each with its own weight,
+ * f32 input and output (chart/ffn.rs:925 projections_q8act shares one dispatch for q/k/v;
+ * here every part may have its own input).  All parts share one ggml type.  A plan fixes the
+ * device pointers once (descriptors are uploaded at creation), so running it is one launch
+ * with no host-device traffic -- the form a per-token projection sequence replays. */
+typedef struct ah_gemv_plan ah_gemv_plan;
+int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w,
+                            const float *const *d_x, float *const *d_y, ah_gemv_plan **out);
+int32_t ah_gemv_plan_run(ah_ctx *ctx, const ah_gemv_plan *plan, void *stream);
+int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan);
+
+/* ---- prefill GEMM, N = n_tok > 1 (kern/matmat.rs:134 matmat_q8act) ---- */
+
+/* y[n_tok][n_out] (token-major) = X W^T for X[n_tok][n_in] f32; quantization is a separate
+ * in-stream pass into context scratch (grown on demand, never shrunk). */
+int32_t ah_gemm_f32_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, size_t n_tok,
+                        float *d_y, void *stream);
+/* Same from pre-quantized codes[n_tok][n_in] + scales[n_tok][ceil(n_in/32)]. */
+int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
+                       const int64_t *d_scales, size_t n_tok, float *d_y, void *stream);
+
+/* ---- debug: exact integer group dots (the bit-exact quantity of the contract) ---- */
+
+/* ah_gemv_q8_dev that ALSO stores, from inside the same production kernel, the exact integer
+ * group dots it folds: d_dots is [n_out][ngroups] int32 with ngroups = ceil(n_in/32) for Q8_0
+ * (sum q*xq) and Q4_K (sum nibble*xq), ceil(n_in/16) for Q6_K (sum (u-32)*xq).  These are
+ * RowAcc::emit's `dot` (chart/mod.rs:501-514), compared bit for bit with the CPU contract. */
+int32_t ah_gemv_q8_dots_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
+                            const int64_t *d_scales, float *d_y, int32_t *d_dots, void *stream);
+
+/* ---- status ---- */
+
+/* Synchronize `stream` and return (then clear) the first data-dependent refusal recorded by
+ * kernels since the last call: AH_ERR_NONFINITE_INPUT, AH_ERR_INPUT_RANGE or
+ * AH_ERR_FIXED_OVERFLOW, else AH_OK (or AH_ERR_HIP if the stream faulted). */
+int32_t ah_sync_status(ah_ctx *ctx, void *stream);
+
+/* ---- host convenience forms (synchronous; copy in and out) ---- */
+
+/* matvec_q8act (chart/mod.rs:1887): codes[n_in], scales[ceil(n_in/32)] host -> y[n_out] host. */
+int32_t ah_matvec_q8act(ah_ctx *ctx, const ah_tensor *w, const int8_t *codes,
+                        const int64_t *scales, size_t n_codes, float *y);
+/* matmat_q8act (kern/matmat.rs:134): codes[n_tok][n_in], scales[n_tok][nb] -> y[n_tok][n_out]. */
+int32_t ah_matmat_q8act(ah_ctx *ctx, const ah_tensor *w, const int8_t *codes,
+                        const int64_t *scales, size_t n_tok, float *y);
+/* quant_act (chart/mod.rs:258) on host Q32.32 input. */
+int32_t ah_quant_act(ah_ctx *ctx, const int64_t *x, size_t n, int8_t *codes, int64_t *scales);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,348 @@
+"""GPU parity: the HIP path (through the C ABI) against the exact CPU oracle.
+
+Bar (from the path's contract):
+  * activation codes and scales: bit-exact to quant_act(to_q32(x));
+  * per-group integer dots (D_b per 32, Q6_K per 16): bit-exact, read from inside the
+    production GEMV kernel;
+  * f32 outputs: |y_gpu - y_ref| <= 1e-4 * sum_i |w_i * xhat_i| + 2^-32 per row, where y_ref is
+    the oracle's exact Q32.32 result (the 2^-32 term is the reference's own output quantum).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from apeiron_amd import chart, synth
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+TOL = 1e-4
+Q32 = 2.0 ** -32
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    d = chart.Device(0)
+    yield d
+    d.close()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def ptr(t):
+    return t.data_ptr()
+
+
+def gemv_q8(dev, w, codes, scales, dots=False):
+    n_out = w.n_out
+    dc, ds = to_dev(codes), to_dev(scales)
+    y = torch.empty(max(n_out, 1), dtype=torch.float32, device="cuda")
+    if dots:
+        ng = -(-w.n_in // 16) if w.ggml_type == 14 else -(-w.n_in // 32)
+        dd = torch.full((max(n_out, 1), max(ng, 1)), -7, dtype=torch.int32, device="cuda")
+        w.gemv_q8_dots_dev(ptr(dc), ptr(ds), ptr(y), ptr(dd), stream())
+        assert dev.sync_status(stream()) == 0
+        return y.cpu().numpy()[:n_out], dd.cpu().numpy()[:n_out, :ng]
+    w.gemv_q8_dev(ptr(dc), ptr(ds), ptr(y), stream())
+    assert dev.sync_status(stream()) == 0
+    return y.cpu().numpy()[:n_out]
+
+
+def assert_close(y, yref_q32, absdot, what=""):
+    ref = np.asarray(yref_q32, np.float64) * Q32
+    err = np.abs(np.asarray(y, np.float64) - ref)
+    tol = TOL * np.asarray(absdot) + Q32
+    bad = np.nonzero(err > tol)[0]
+    assert bad.size == 0, f"{what}: rows {bad[:8]} err {err[bad[:8]]} tol {tol[bad[:8]]}"
+
+
+def golden_cases():
+    z = np.load(GOLDEN, allow_pickle=False)
+    for i in range(int(z["count"])):
+        p = f"c{i:03d}_"
+        t, rows, n_in = (int(v) for v in z[p + "meta"])
+        yield dict(kind=str(z[p + "kind"]), t=t, rows=rows, n_in=n_in, raw=z[p + "raw"], x=z[p + "x"],
+                   codes=z[p + "codes"], scales=z[p + "scales"], y=z[p + "y"], dots=z[p + "dots"],
+                   xf=z[p + "xf"] if p + "xf" in z else None)
+
+
+# ---- activation quantizer -----------------------------------------------------------------
+
+def quant_f32_gpu(dev, x2d):
+    n_tok, n_in = x2d.shape
+    dx = to_dev(x2d.astype(np.float32))
+    dc = torch.zeros((n_tok, n_in), dtype=torch.int8, device="cuda")
+    ds = torch.zeros((n_tok, -(-n_in // 32)), dtype=torch.int64, device="cuda")
+    dev.quant_act_f32_dev(ptr(dx), n_tok, n_in, ptr(dc), ptr(ds), stream())
+    st = dev.sync_status(stream())
+    return st, dc.cpu().numpy(), ds.cpu().numpy()
+
+
+def test_quant_act_f32_bit_exact(dev):
+    rng = np.random.default_rng(1)
+    for n_tok, n_in in [(1, 896), (3, 33), (5, 4864), (2, 300), (7, 1536)]:
+        x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
+        x[0, :32] = 0.0
+        x[-1, 5] = 1e-20
+        x[-1, 7] = -2.0e9
+        st, c, s = quant_f32_gpu(dev, x)
+        assert st == 0
+        for r in range(n_tok):
+            ost, oc, os_ = oracle.quant_act_f32(x[r])
+            assert ost == 0
+            assert (c[r] == oc).all() and (s[r] == os_).all(), (n_tok, n_in, r)
+
+
+def test_quant_act_f32_refusals(dev):
+    x = np.ones((1, 64), np.float32)
+    x[0, 40] = np.inf
+    assert quant_f32_gpu(dev, x)[0] == 10
+    x = np.ones((1, 64), np.float32)
+    x[0, 3] = 3e9
+    x[0, 50] = np.nan
+    assert quant_f32_gpu(dev, x)[0] == 11  # the earlier element decides
+    x = np.full((1, 32), 2147483520.0, np.float32)  # code 64 * 2^57 leaves i64
+    assert quant_f32_gpu(dev, x)[0] == 7
+    assert quant_f32_gpu(dev, np.ones((1, 64), np.float32))[0] == 0  # status was cleared
+
+
+def test_quant_act_q32_reference_kats(dev):
+    # chart/tests.rs:397-415
+    q = dev.quant_act([3, 130, -3])
+    assert q.codes.tolist() == [2, 65, -2] and q.scales.tolist() == [2]
+    assert dev.quant_act([(1 << 63) - 1] * 32) is None
+    q = dev.quant_act([-(1 << 63)] * 32)
+    assert q.scales.tolist() == [1 << 57] and (q.codes == -64).all()
+    q = dev.quant_act([127 << 56] * 32)
+    assert (q.codes == 127).all() and q.scales.tolist() == [1 << 56]
+    rng = np.random.default_rng(2)
+    for seed in range(4):
+        x = (rng.integers(-(1 << 62), 1 << 62, size=203) >> rng.integers(0, 60, size=203)).astype(np.int64)
+        x[:32] = 0
+        q = dev.quant_act(x)
+        st, oc, os_ = oracle.quant_act(x)
+        assert st == 0 and (q.codes == oc).all() and (q.scales == os_).all()
+
+
+# ---- GEMV ------------------------------------------------------------------------------------
+
+def test_gemv_golden_fixtures(dev):
+    n = 0
+    for c in golden_cases():
+        w = dev.upload(c["t"], c["raw"], c["rows"], c["n_in"])
+        y, dots = gemv_q8(dev, w, c["codes"], c["scales"], dots=True)
+        assert (dots == c["dots"]).all(), (c["kind"], c["t"], c["n_in"])
+        st, absdot = oracle.row_absdot(c["t"], c["raw"], c["rows"], c["n_in"], c["codes"], c["scales"])
+        assert_close(y, c["y"], absdot, f"{c['kind']} t{c['t']} K{c['n_in']}")
+        if c["xf"] is not None:
+            yf = torch.empty(c["rows"], dtype=torch.float32, device="cuda")
+            dx = to_dev(c["xf"])
+            w.gemv_f32_dev(ptr(dx), ptr(yf), stream())
+            assert dev.sync_status(stream()) == 0
+            assert (yf.cpu().numpy() == y).all()  # fused quantizer == pre-quantized path
+        w.free()
+        n += 1
+    assert n >= 40
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("n_out,n_in", [(4864, 896), (896, 4864), (128, 896), (333, 1536), (37, 8960), (5, 100)])
+def test_gemv_config_shapes(dev, t, n_out, n_in):
+    rng = synth.rng_for(1, t * 1000 + n_in)
+    raw = synth.payload(t, rng, n_out, n_in)
+    x = synth.activations(rng, n_in)
+    st, codes, scales = oracle.quant_act_f32(x)
+    assert st == 0
+    w = dev.upload(t, raw, n_out, n_in)
+    y, dots = gemv_q8(dev, w, codes, scales, dots=True)
+    # exact oracle on every row for the small shapes, a row sample for the big ones
+    rows = np.arange(n_out) if n_out * n_in <= 1_000_000 else np.unique(rng.integers(0, n_out, 64))
+    rb = synth.row_bytes(t, n_in)
+    sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in rows])
+    st, yref = oracle.matvec_q8act(t, sub, len(rows), n_in, codes, scales)
+    assert st == 0
+    st, absdot = oracle.row_absdot(t, sub, len(rows), n_in, codes, scales)
+    assert_close(y[rows], yref, absdot, f"t{t} {n_out}x{n_in}")
+    for i, r in enumerate(rows[:16]):
+        st, od, _ = oracle.block_dots(t, sub[i * rb:(i + 1) * rb], n_in, codes)
+        assert (dots[r] == od).all(), (t, n_out, n_in, r)
+    # fused f32 path is the same arithmetic
+    yf = torch.empty(n_out, dtype=torch.float32, device="cuda")
+    dx = to_dev(x)
+    w.gemv_f32_dev(ptr(dx), ptr(yf), stream())
+    assert dev.sync_status(stream()) == 0
+    assert (yf.cpu().numpy() == y).all()
+    w.free()
+
+
+def test_gemv_vocab_head_q6_k_and_q8_0(dev):
+    # config 2: 151936 x 896; exact oracle on a row sample, all rows finite and deterministic.
+    for t in (14, 8):
+        rng = synth.rng_for(2, t)
+        n_out, n_in = 151936, 896
+        raw = synth.payload(t, rng, n_out, n_in)
+        x = synth.activations(rng, n_in)
+        st, codes, scales = oracle.quant_act_f32(x)
+        w = dev.upload(t, raw, n_out, n_in)
+        y1 = gemv_q8(dev, w, codes, scales)
+        y2 = gemv_q8(dev, w, codes, scales)
+        assert (y1 == y2).all() and np.isfinite(y1).all()
+        rows = np.unique(np.concatenate([[0, 1, n_out - 1], rng.integers(0, n_out, 200)]))
+        rb = synth.row_bytes(t, n_in)
+        sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in rows])
+        st, yref = oracle.matvec_q8act(t, sub, len(rows), n_in, codes, scales)
+        st2, absdot = oracle.row_absdot(t, sub, len(rows), n_in, codes, scales)
+        assert st == 0 and st2 == 0
+        assert_close(y1[rows], yref, absdot, f"head t{t}")
+        w.free()
+
+
+def test_gemv_linearity_full_size(dev):
+    # size-independent property at a full config size: W(x) for codes c and the same codes with
+    # every block scale doubled gives exactly 2x (power-of-two scales are exact in f32).
+    rng = synth.rng_for(4, 7)
+    raw = synth.payload(12, rng, 8960, 1536)
+    x = synth.activations(rng, 1536)
+    st, codes, scales = oracle.quant_act_f32(x)
+    w = dev.upload(12, raw, 8960, 1536)
+    y1 = gemv_q8(dev, w, codes, scales)
+    y2 = gemv_q8(dev, w, codes, scales * 2)
+    assert (y2 == 2 * y1).all()
+    w.free()
+
+
+def test_grouped_plan_matches_single_launches(dev):
+    rng = synth.rng_for(1, 99)
+    shapes = [(896, 896), (128, 896), (128, 896), (896, 896), (4864, 896), (4864, 896), (896, 4864)]
+    ws, xs, ys, singles = [], [], [], []
+    for n_out, n_in in shapes:
+        raw = synth.payload(12, rng, n_out, n_in)
+        w = dev.upload(12, raw, n_out, n_in)
+        x = to_dev(synth.activations(rng, n_in))
+        y = torch.zeros(n_out, dtype=torch.float32, device="cuda")
+        ys1 = torch.zeros(n_out, dtype=torch.float32, device="cuda")
+        w.gemv_f32_dev(ptr(x), ptr(ys1), stream())
+        ws.append(w), xs.append(x), ys.append(y), singles.append(ys1)
+    plan = chart.GemvPlan(dev, ws, [ptr(x) for x in xs], [ptr(y) for y in ys])
+    for _ in range(3):
+        plan.run(stream())
+    assert dev.sync_status(stream()) == 0
+    for y, s in zip(ys, singles):
+        assert torch.equal(y, s)
+    plan.free()
+    for w in ws:
+        w.free()
+
+
+def test_upload_refusals(dev):
+    raw = synth.payload(8, synth.rng_for(0, 1), 4, 64)
+    with pytest.raises(chart.MatvecError) as e:
+        dev.upload(8, raw[:-1], 4, 64)
+    assert e.value.kind == "ShortPayload"
+    with pytest.raises(chart.MatvecError) as e:
+        dev.upload(3, raw, 4, 64)
+    assert e.value.kind == "UnsupportedQuant"
+    for t, off in ((8, 34), (12, 146), (14, 210 + 208)):
+        raw = synth.payload(t, synth.rng_for(0, t), 3, 256)
+        raw[off:off + 2] = [0x00, 0x7C]  # +inf scale in a later block
+        with pytest.raises(chart.MatvecError) as e:
+            dev.upload(t, raw, 3, 256)
+        assert e.value.kind == "NonFiniteScale"
+
+
+def test_host_forms_mirror_reference_interface(dev):
+    rng = synth.rng_for(0, 5)
+    raw = synth.payload(12, rng, 40, 512)
+    x = (rng.integers(-2048, 2048, size=512)).astype(np.int64)
+    q = chart.quant_act(x)
+    st, oc, os_ = oracle.quant_act(x)
+    assert (q.codes == oc).all() and (q.scales == os_).all()
+    y = chart.matvec_q8act(12, raw, 40, 512, q)
+    st, yref = oracle.matvec_q8act(12, raw, 40, 512, oc, os_)
+    st2, absdot = oracle.row_absdot(12, raw, 40, 512, oc, os_)
+    assert_close(y, yref, absdot, "host matvec")
+    with pytest.raises(chart.MatvecError) as e:
+        chart.matvec_q8act(12, raw, 40, 256, q)
+    assert e.value.kind == "ShapeMismatch"
+    qs = [chart.quant_act(rng.integers(-5000, 5000, size=512).astype(np.int64)) for _ in range(5)]
+    Y = chart.matmat_q8act(12, raw, 40, 512, qs)
+    for c, qc in enumerate(qs):
+        st, yc = oracle.matvec_q8act(12, raw, 40, 512, qc.codes, qc.scales)
+        st2, ad = oracle.row_absdot(12, raw, 40, 512, qc.codes, qc.scales)
+        assert_close(Y[c], yc, ad, f"host matmat col {c}")
+
+
+# ---- GEMM ------------------------------------------------------------------------------------
+
+def gemm_check(dev, t, n_out, n_in, n_tok, sample_cols=None, seed=0):
+    rng = synth.rng_for(3, seed * 100 + t)
+    raw = synth.payload(t, rng, n_out, n_in)
+    x = synth.activations(rng, n_in, n_tok).reshape(n_tok, n_in)
+    w = dev.upload(t, raw, n_out, n_in)
+    dx = to_dev(x)
+    y = torch.full((n_tok, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    w.gemm_f32_dev(ptr(dx), n_tok, ptr(y), stream())
+    assert dev.sync_status(stream()) == 0
+    Y = y.cpu().numpy()
+    assert np.isfinite(Y).all()
+    cols = range(n_tok) if sample_cols is None else sample_cols
+    rows = np.arange(n_out) if n_out <= 1024 else np.unique(rng.integers(0, n_out, 96))
+    rb = synth.row_bytes(t, n_in)
+    sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in rows])
+    for c in cols:
+        st, codes, scales = oracle.quant_act_f32(x[c])
+        st, yref = oracle.matvec_q8act(t, sub, len(rows), n_in, codes, scales)
+        st2, absdot = oracle.row_absdot(t, sub, len(rows), n_in, codes, scales)
+        assert st == 0 and st2 == 0
+        assert_close(Y[c, rows], yref, absdot, f"gemm t{t} {n_out}x{n_in} N{n_tok} col {c}")
+    # deterministic
+    y2 = torch.empty_like(y)
+    w.gemm_f32_dev(ptr(dx), n_tok, ptr(y2), stream())
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    w.free()
+    return Y
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(64, 256, 8), (96, 300, 33), (200, 896, 130), (33, 64, 2)])
+def test_gemm_small_shapes(dev, t, n_out, n_in, n_tok):
+    gemm_check(dev, t, n_out, n_in, n_tok)
+
+
+@pytest.mark.parametrize("t", [8, 12])
+@pytest.mark.parametrize("n_out,n_in", [(4864, 896), (896, 4864), (8960, 1536), (1536, 8960)])
+def test_gemm_config3_shapes(dev, t, n_out, n_in):
+    gemm_check(dev, t, n_out, n_in, 512, sample_cols=[0, 1, 127, 128, 255, 300, 511])
+
+
+def test_gemm_q6_k_config4_shapes(dev):
+    gemm_check(dev, 14, 256, 1536, 512, sample_cols=[0, 200, 511])
+    gemm_check(dev, 14, 1536, 8960, 512, sample_cols=[0, 511])
+
+
+def test_gemm_n1_equals_gemv_within_tolerance(dev):
+    rng = synth.rng_for(3, 77)
+    for t in (8, 12, 14):
+        raw = synth.payload(t, rng, 300, 896)
+        x = synth.activations(rng, 896)
+        w = dev.upload(t, raw, 300, 896)
+        dx = to_dev(x.reshape(1, -1))
+        y = torch.empty((1, 300), dtype=torch.float32, device="cuda")
+        w.gemm_f32_dev(ptr(dx), 1, ptr(y), stream())
+        assert dev.sync_status(stream()) == 0
+        st, codes, scales = oracle.quant_act_f32(x)
+        st, yref = oracle.matvec_q8act(t, raw, 300, 896, codes, scales)
+        st2, absdot = oracle.row_absdot(t, raw, 300, 896, codes, scales)
+        assert_close(y.cpu().numpy()[0], yref, absdot, f"gemm N=1 t{t}")
+        w.free()

@@ -30,8 +30,12 @@ AH_DEV void ah_record(unsigned long long *st, unsigned long long key) {
 // ---- buffer resources: range-checked loads (out-of-range lanes read 0, never fault) ----
 
 AH_DEV __amdgpu_buffer_rsrc_t ah_rsrc(const void *p, uint32_t bytes) {
-    // word3 0x00020000: the gfx9-family raw buffer format (32-bit data, no swizzle).
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+    // The range check drops a whole dword that straddles the end, and GGUF payloads are only
+    // 2-byte multiples (34-, 210-byte blocks), so the range is rounded up to whole dwords.  The
+    // extra 0-3 bytes share an aligned dword with payload bytes, so they can never touch a page
+    // the payload does not.  word3 0x00020000: the gfx9-family raw buffer format.
+    const uint32_t rounded = bytes > 0xFFFFFFFCu ? 0xFFFFFFFCu : (bytes + 3u) & ~3u;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)rounded,
                                              0x00020000);
 }
 AH_DEV u32x4 ah_ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {

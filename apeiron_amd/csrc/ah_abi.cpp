@@ -24,9 +24,8 @@ hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uin
                           const _Float16 *xh, const _Float16 *xmin, const float *tok_scale,
                           float *y, float *partials, uint32_t splits, hipStream_t stream);
 uint32_t ah_gemm_splits_used(uint32_t type, uint32_t n_in, uint32_t splits);
-hipError_t ah_launch_q4k_min(const int8_t *codes, const int64_t *scales, const float *tok_scale,
-                             uint32_t n_tok, uint32_t n_in, uint32_t kpad, _Float16 *xmin,
-                             hipStream_t stream);
+hipError_t ah_launch_operand(const OperandArgs &o, hipStream_t stream);
+uint32_t ah_gemv_nu(uint32_t type);
 
 struct ah_ctx {
     int device = -1;
@@ -120,32 +119,12 @@ uint32_t units_per_row(uint32_t t, uint32_t n_in) {
     return t == AH_GGML_Q8_0 ? (n_in + 31) / 32 : (n_in + 255) / 256;
 }
 
-// Lanes per row: the power of two in [4, 64] wasting the fewest unit slots (ties -> more lanes).
-uint32_t choose_log2g(uint32_t units) {
-    uint32_t best = 2, best_slots = ~0u;
-    for (uint32_t l = 2; l <= 6; ++l) {
-        const uint32_t G = 1u << l;
-        const uint32_t slots = (units + G - 1) / G * G;
-        if (slots <= best_slots) {
-            best_slots = slots;
-            best = l;
-        }
-    }
-    return best;
-}
-
-uint32_t gemv_grid(const ah_ctx *ctx, uint32_t n_out, uint32_t log2g) {
-    const uint32_t rows_per_iter = 4u * (64u >> log2g);
-    uint32_t g = (n_out + rows_per_iter - 1) / rows_per_iter;
-    const uint32_t cap = 4u * (uint32_t)ctx->cu_count;
-    if (g > cap) g = cap;
-    return g ? g : 1;
-}
-
 uint32_t kpad_of(size_t n_in) { return (uint32_t)((n_in + 255) / 256 * 256); }
 
-GemvPart make_part(const ah_tensor *w, uint32_t src, const void *x, const int64_t *scales, float *y,
-                   int32_t *dots) {
+// Units per row are cut into tiles of whole rows with at most 256*NU units per tile; each part
+// gets one workgroup per tile up to 4 per CU (workgroups then loop over tiles).
+GemvPart make_part(const ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
+                   const int64_t *scales, float *y, int32_t *dots) {
     GemvPart P;
     std::memset(&P, 0, sizeof(P));
     P.w = w->d;
@@ -157,8 +136,14 @@ GemvPart make_part(const ah_tensor *w, uint32_t src, const void *x, const int64_
     P.n_out = (uint32_t)w->n_out;
     P.n_in = (uint32_t)w->n_in;
     P.row_bytes = (uint32_t)w->row_bytes;
+    P.units = units_per_row(w->type, P.n_in);
+    const uint32_t cap_units = 256u * ah_gemv_nu(w->type);
+    P.rows_per_tile = P.units == 0 ? cap_units : (cap_units / P.units > 0 ? cap_units / P.units : 1);
+    const uint32_t n_tiles = (P.n_out + P.rows_per_tile - 1) / P.rows_per_tile;
+    const uint32_t cap = 4u * (uint32_t)ctx->cu_count;
+    P.wg_count = n_tiles < cap ? n_tiles : cap;
+    if (P.wg_count == 0) P.wg_count = 1;
     P.wg_begin = 0;
-    P.log2g = choose_log2g(units_per_row(w->type, P.n_in));
     P.src = src;
     return P;
 }
@@ -168,10 +153,9 @@ int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     if (!ctx || !w || (!x && w->n_in) || (!y && w->n_out)) return AH_ERR_INVALID_ARG;
     if (src == AH_SRC_CODES && !scales && w->n_in) return AH_ERR_INVALID_ARG;
     if (w->n_out == 0) return AH_OK;
-    const GemvPart P = make_part(w, src, x, scales, y, dots);
-    const uint32_t grid = gemv_grid(ctx, P.n_out, P.log2g);
+    const GemvPart P = make_part(ctx, w, src, x, scales, y, dots);
     AH_HIP(ctx, hipSetDevice(ctx->device));
-    AH_HIP(ctx, ah_launch_gemv(w->type, P, nullptr, 1, grid, kpad_of(w->n_in), ctx->d_status,
+    AH_HIP(ctx, ah_launch_gemv(w->type, P, nullptr, 1, P.wg_count, kpad_of(w->n_in), ctx->d_status,
                                pick(ctx, stream)));
     return AH_OK;
 }
@@ -219,20 +203,29 @@ int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     hipStream_t s = pick(ctx, stream);
     AH_HIP(ctx, hipSetDevice(ctx->device));
 
-    QuantArgs q;
-    q.x = src == AH_SRC_F32 ? x : nullptr;
-    q.codes = codes;
-    q.scales = scales;
-    q.xh = xh;
-    q.tok_scale = ts;
-    q.n_tok = N;
-    q.n_in = n_in;
-    q.nb32 = nb32;
-    q.kpad = kpad;
-    q.src = src;
-    q.status = ctx->d_status;
-    AH_HIP(ctx, ah_launch_quant(q, s));
-    if (w->type == AH_GGML_Q4_K) AH_HIP(ctx, ah_launch_q4k_min(codes, scales, ts, N, n_in, kpad, xmin, s));
+    if (src == AH_SRC_F32) {
+        QuantArgs q;
+        q.x = x;
+        q.codes = codes;
+        q.scales = scales;
+        q.n_tok = N;
+        q.n_in = n_in;
+        q.nb32 = nb32;
+        q.src = AH_SRC_F32;
+        q.status = ctx->d_status;
+        AH_HIP(ctx, ah_launch_quant(q, s));
+    }
+    OperandArgs o;
+    o.codes = codes;
+    o.scales = scales;
+    o.xh = xh;
+    o.tok_scale = ts;
+    o.xmin = w->type == AH_GGML_Q4_K ? xmin : nullptr;
+    o.n_tok = N;
+    o.n_in = n_in;
+    o.nb32 = nb32;
+    o.kpad = kpad;
+    AH_HIP(ctx, ah_launch_operand(o, s));
     AH_HIP(ctx, ah_launch_gemm(w->type, w->d, (uint32_t)w->bytes, (uint32_t)w->row_bytes, n_out, n_in, N,
                                kpad, xh, xmin, ts, y, part, splits, s));
     return AH_OK;
@@ -409,12 +402,9 @@ static int32_t quant_dev(ah_ctx *ctx, uint32_t src, const void *d_x, size_t n_to
     q.x = d_x;
     q.codes = d_codes;
     q.scales = d_scales;
-    q.xh = nullptr;
-    q.tok_scale = nullptr;
     q.n_tok = (uint32_t)n_tok;
     q.n_in = (uint32_t)n_in;
     q.nb32 = (uint32_t)((n_in + 31) / 32);
-    q.kpad = kpad_of(n_in);
     q.src = src;
     q.status = ctx->d_status;
     AH_HIP(ctx, hipSetDevice(ctx->device));
@@ -460,9 +450,9 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
             std::free(parts);
             return AH_ERR_INVALID_ARG;
         }
-        parts[i] = make_part(w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr);
+        parts[i] = make_part(ctx, w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr);
         parts[i].wg_begin = wg;
-        wg += gemv_grid(ctx, parts[i].n_out, parts[i].log2g);
+        wg += parts[i].wg_count;
         const uint32_t kp = kpad_of(w[i]->n_in);
         kpad_max = kp > kpad_max ? kp : kpad_max;
     }

@@ -322,38 +322,58 @@ __global__ void splitk_reduce(const float *part, uint32_t splits, uint32_t n_tok
     }
 }
 
-// Q4_K min-term operand: for each token and super-block, the 8 sub-block code sums X_j split
-// exactly into f16 pieces scaled like the activation operand: [64*floor(X/64), X mod 64] * 2^(e-E).
-__global__ void q4k_min_operand(const int8_t *codes, const int64_t *scales, const float *tok_scale,
-                                uint32_t n_tok, uint32_t n_in, uint32_t nb32, uint32_t kpad,
-                                _Float16 *xmin) {
-    const uint32_t nsb = kpad / 256;
-    const size_t total = (size_t)n_tok * nsb * 8;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const uint32_t tok = (uint32_t)(i / (nsb * 8));
-        const uint32_t g = (uint32_t)(i % (nsb * 8));  // sub-block index within the token
-        const uint32_t s = g / 8, e8 = g % 8;
-        int X = 0;
-        int ex = -1;
-        if (g < nb32) {
-            for (uint32_t l = 0; l < 32 && g * 32 + l < n_in; ++l) X += codes[(size_t)tok * n_in + g * 32 + l];
-            const int64_t S = scales[(size_t)tok * nb32 + g];
-            ex = S > 0 ? 63 - __builtin_clzll((uint64_t)S) : -1;
+// GEMM activation operand of one token per workgroup (OperandArgs): E_tok = the largest block
+// exponent, tok_scale = 2^(E_tok - 32), xh = xq * 2^(e_b - E_tok) in f16 (exact whenever
+// e_b - E_tok >= -24; a smaller block is at most 2^-24 of the token's largest), and for Q4_K the
+// min-term operand: per super-block, the 8 sub-block code sums X_j split exactly into f16 pieces
+// [64*floor(X/64), X mod 64] * 2^(e_j - E_tok), laid out [hi 0..7, lo 0..7].
+__global__ void __launch_bounds__(256) operand_kernel(OperandArgs o) {
+    __shared__ int red[256];
+    for (uint32_t tok = blockIdx.x; tok < o.n_tok; tok += gridDim.x) {
+        const int64_t *sc = o.scales + (size_t)tok * o.nb32;
+        int em = -1;
+        for (uint32_t b = threadIdx.x; b < o.nb32; b += 256) {
+            const int64_t S = sc[b];
+            const int e = S > 0 ? 63 - __builtin_clzll((uint64_t)S) : -1;
+            em = e > em ? e : em;
         }
-        float hi = 0.0f, lo = 0.0f;
-        const float ts = tok_scale[tok];
-        if (ex >= 0 && ts > 0.0f) {
-            // E_tok from tok_scale = 2^(E-32)
-            const int E = (int)((__builtin_bit_cast(uint32_t, ts) >> 23) & 0xffu) - 127 + 32;
-            const int xh = (X >= 0 ? X : X - 63) / 64;  // floor(X / 64)
-            const int xl = X - 64 * xh;                   // 0..63
-            hi = __builtin_ldexpf((float)(64 * xh), ex - E);
-            lo = __builtin_ldexpf((float)xl, ex - E);
+        red[threadIdx.x] = em;
+        __syncthreads();
+        for (uint32_t w = 128; w > 0; w >>= 1) {
+            if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] > red[threadIdx.x + w] ? red[threadIdx.x] : red[threadIdx.x + w];
+            __syncthreads();
         }
-        _Float16 *o = xmin + ((size_t)tok * nsb + s) * 16;
-        o[e8] = (_Float16)hi;
-        o[8 + e8] = (_Float16)lo;
+        const int E = red[0];
+        __syncthreads();
+        if (threadIdx.x == 0) o.tok_scale[tok] = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
+        const int8_t *codes = o.codes + (size_t)tok * o.n_in;
+        _Float16 *xh = o.xh + (size_t)tok * o.kpad;
+        for (uint32_t k = threadIdx.x; k < o.kpad; k += 256) {
+            float v = 0.0f;
+            if (k < o.n_in) {
+                const int64_t S = sc[k / 32];
+                if (S > 0) v = __builtin_ldexpf((float)codes[k], 63 - __builtin_clzll((uint64_t)S) - E);
+            }
+            xh[k] = (_Float16)v;
+        }
+        if (o.xmin) {
+            const uint32_t nsb = o.kpad / 256;
+            for (uint32_t g = threadIdx.x; g < nsb * 8; g += 256) {
+                float hi = 0.0f, lo = 0.0f;
+                if (g < o.nb32 && sc[g] > 0) {
+                    int X = 0;
+                    for (uint32_t l = 0; l < 32 && g * 32 + l < o.n_in; ++l) X += codes[g * 32 + l];
+                    const int ex = 63 - __builtin_clzll((uint64_t)sc[g]) - E;
+                    const int xhq = (X >= 0 ? X : X - 63) / 64;  // floor(X / 64)
+                    hi = __builtin_ldexpf((float)(64 * xhq), ex);
+                    lo = __builtin_ldexpf((float)(X - 64 * xhq), ex);
+                }
+                _Float16 *m = o.xmin + ((size_t)tok * nsb + g / 8) * 16;
+                m[g % 8] = (_Float16)hi;
+                m[8 + g % 8] = (_Float16)lo;
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -404,14 +424,9 @@ uint32_t ah_gemm_splits_used(uint32_t type, uint32_t n_in, uint32_t splits) {
     return (nstages + per - 1) / per;
 }
 
-hipError_t ah_launch_q4k_min(const int8_t *codes, const int64_t *scales, const float *tok_scale,
-                             uint32_t n_tok, uint32_t n_in, uint32_t kpad, _Float16 *xmin,
-                             hipStream_t stream) {
-    const size_t total = (size_t)n_tok * (kpad / 256) * 8;
-    if (total == 0) return hipSuccess;
-    uint32_t g = (uint32_t)((total + 255) / 256);
-    if (g > 8192) g = 8192;
-    hipLaunchKernelGGL(q4k_min_operand, dim3(g), dim3(256), 0, stream, codes, scales, tok_scale, n_tok,
-                       n_in, (n_in + 31) / 32, kpad, xmin);
+hipError_t ah_launch_operand(const OperandArgs &o, hipStream_t stream) {
+    if (o.n_tok == 0) return hipSuccess;
+    const uint32_t grid = o.n_tok < 2048 ? o.n_tok : 2048;
+    hipLaunchKernelGGL(operand_kernel, dim3(grid), dim3(256), 0, stream, o);
     return hipGetLastError();
 }

@@ -113,8 +113,10 @@ struct GemvPart {
     float *y;
     int32_t *dots;         // optional exact group dots [n_out][ngroups]
     uint32_t n_out, n_in, row_bytes;
+    uint32_t units;        // work units per row (Q8_0 blocks, K-quant super-blocks)
+    uint32_t rows_per_tile;// whole rows per workgroup tile (tile units <= 256 * NU)
     uint32_t wg_begin;     // first workgroup of this part in a grouped launch
-    uint32_t log2g;        // lanes per row = 1 << log2g
+    uint32_t wg_count;     // workgroups of this part
     uint32_t src;          // AH_SRC_*
 };
 
@@ -122,9 +124,19 @@ struct QuantArgs {
     const void *x;         // f32 or int64 [n_tok][n_in]
     int8_t *codes;         // [n_tok][n_in]
     int64_t *scales;       // [n_tok][nb32]
-    _Float16 *xh;          // optional: GEMM operand [n_tok][kpad] f16, xq * 2^(e_b - E_tok)
-    float *tok_scale;      // optional: [n_tok] 2^(E_tok - 32) (0 for an all-zero token)
-    uint32_t n_tok, n_in, nb32, kpad;
-    uint32_t src;          // AH_SRC_F32 / AH_SRC_Q32 / AH_SRC_CODES (codes+scales given)
+    uint32_t n_tok, n_in, nb32;
+    uint32_t src;          // AH_SRC_F32 / AH_SRC_Q32
     unsigned long long *status;
+};
+
+// GEMM activation operand built from a QuantAct: xh[tok][kpad] f16 = xq * 2^(e_b - E_tok) (exact
+// when e_b - E_tok >= -24), tok_scale[tok] = 2^(E_tok - 32), and for Q4_K the min-term operand
+// xmin[tok][kpad/256][16] (split sub-block code sums, see ah_gemm.hip).
+struct OperandArgs {
+    const int8_t *codes;
+    const int64_t *scales;
+    _Float16 *xh;
+    float *tok_scale;
+    _Float16 *xmin;        // nullptr unless Q4_K
+    uint32_t n_tok, n_in, nb32, kpad;
 };

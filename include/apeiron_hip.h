@@ -59,7 +59,7 @@ extern "C" {
 #define AH_GGML_Q6_K 14
 
 /* Largest n_in the GEMV keeps in LDS and the GEMM stages (both kernels refuse beyond). */
-#define AH_MAX_N_IN 65536
+#define AH_MAX_N_IN 32768
 
 typedef struct ah_ctx ah_ctx;
 typedef struct ah_tensor ah_tensor;

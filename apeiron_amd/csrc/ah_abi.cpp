@@ -14,8 +14,16 @@
 
 // launchers (ah_gemv.hip, ah_gemm.hip)
 hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart *d_parts,
-                          uint32_t n_parts, uint32_t grid, uint32_t kpad_max,
+                          const uint32_t *d_wg_part, uint32_t grid, uint32_t kpad_max, uint32_t nc,
                           unsigned long long *status, hipStream_t stream);
+uint32_t ah_gemv_nc(uint32_t row_bytes);
+uint32_t ah_gemv_rows_per_tile(uint32_t row_bytes, uint32_t units);
+hipError_t ah_gemv_init_attrs();
+bool ah_gemv_wave_geometry(uint32_t row_bytes, uint32_t units, uint32_t &nc, uint32_t &rows,
+                           uint32_t &lanes);
+hipError_t ah_launch_gemv_wave(uint32_t type, uint32_t nc, const GemvPart &single,
+                               const GemvPart *d_parts, const uint32_t *d_wg_part, uint32_t grid,
+                               uint32_t kpad_max, unsigned long long *status, hipStream_t stream);
 hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream);
 hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes, uint32_t off0,
                           uint32_t off1, int *d_bad, hipStream_t stream);
@@ -25,7 +33,6 @@ hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uin
                           float *y, float *partials, uint32_t splits, hipStream_t stream);
 uint32_t ah_gemm_splits_used(uint32_t type, uint32_t n_in, uint32_t splits);
 hipError_t ah_launch_operand(const OperandArgs &o, hipStream_t stream);
-uint32_t ah_gemv_nu(uint32_t type);
 
 struct ah_ctx {
     int device = -1;
@@ -45,8 +52,9 @@ struct ah_tensor {
 };
 
 struct ah_gemv_plan {
-    uint32_t type = 0, n_parts = 0, grid = 0, kpad_max = 0;
-    GemvPart *d_parts = nullptr;
+    uint32_t type = 0, n_parts = 0, grid = 0, kpad_max = 0, nc = 4, wave_nc = 0;
+    GemvPart *d_parts = nullptr;   // part descriptors
+    uint32_t *d_wg_part = nullptr; // workgroup -> part index (one load per workgroup)
 };
 
 #define AH_HIP(ctx, call)                                                                       \
@@ -121,10 +129,12 @@ uint32_t units_per_row(uint32_t t, uint32_t n_in) {
 
 uint32_t kpad_of(size_t n_in) { return (uint32_t)((n_in + 255) / 256 * 256); }
 
-// Units per row are cut into tiles of whole rows with at most 256*NU units per tile; each part
-// gets one workgroup per tile up to 4 per CU (workgroups then loop over tiles).
+// Two kernels serve the GEMV.  The wave-tile kernel (rows up to 16 KB) gives every wave its own
+// tiles of whole rows; the workgroup-tile kernel serves longer rows.  `wave_nc` is 0 for the
+// latter, else the wave tile size in KB.  Each part gets enough workgroups for one tile per wave,
+// up to 4 workgroups per CU (workgroups then loop over tiles).
 GemvPart make_part(const ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
-                   const int64_t *scales, float *y, int32_t *dots) {
+                   const int64_t *scales, float *y, int32_t *dots, uint32_t &wave_nc) {
     GemvPart P;
     std::memset(&P, 0, sizeof(P));
     P.w = w->d;
@@ -137,11 +147,22 @@ GemvPart make_part(const ah_ctx *ctx, const ah_tensor *w, uint32_t src, const vo
     P.n_in = (uint32_t)w->n_in;
     P.row_bytes = (uint32_t)w->row_bytes;
     P.units = units_per_row(w->type, P.n_in);
-    const uint32_t cap_units = 256u * ah_gemv_nu(w->type);
-    P.rows_per_tile = P.units == 0 ? cap_units : (cap_units / P.units > 0 ? cap_units / P.units : 1);
+    uint32_t nc = 0, rows = 0, lanes = 0, tiles_per_wg;
+    if (ah_gemv_wave_geometry(P.row_bytes, P.units, nc, rows, lanes)) {
+        wave_nc = nc;
+        P.rows_per_tile = rows;
+        P.lanes = lanes;
+        tiles_per_wg = 4;
+    } else {
+        wave_nc = 0;
+        P.rows_per_tile = ah_gemv_rows_per_tile(P.row_bytes, P.units);
+        P.lanes = 0;
+        tiles_per_wg = 1;
+    }
     const uint32_t n_tiles = (P.n_out + P.rows_per_tile - 1) / P.rows_per_tile;
+    const uint32_t need = (n_tiles + tiles_per_wg - 1) / tiles_per_wg;
     const uint32_t cap = 4u * (uint32_t)ctx->cu_count;
-    P.wg_count = n_tiles < cap ? n_tiles : cap;
+    P.wg_count = need < cap ? need : cap;
     if (P.wg_count == 0) P.wg_count = 1;
     P.wg_begin = 0;
     P.src = src;
@@ -153,10 +174,15 @@ int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     if (!ctx || !w || (!x && w->n_in) || (!y && w->n_out)) return AH_ERR_INVALID_ARG;
     if (src == AH_SRC_CODES && !scales && w->n_in) return AH_ERR_INVALID_ARG;
     if (w->n_out == 0) return AH_OK;
-    const GemvPart P = make_part(ctx, w, src, x, scales, y, dots);
+    uint32_t wave_nc = 0;
+    const GemvPart P = make_part(ctx, w, src, x, scales, y, dots, wave_nc);
     AH_HIP(ctx, hipSetDevice(ctx->device));
-    AH_HIP(ctx, ah_launch_gemv(w->type, P, nullptr, 1, P.wg_count, kpad_of(w->n_in), ctx->d_status,
-                               pick(ctx, stream)));
+    if (wave_nc)
+        AH_HIP(ctx, ah_launch_gemv_wave(w->type, wave_nc, P, nullptr, nullptr, P.wg_count,
+                                        kpad_of(w->n_in), ctx->d_status, pick(ctx, stream)));
+    else
+        AH_HIP(ctx, ah_launch_gemv(w->type, P, nullptr, nullptr, P.wg_count, kpad_of(w->n_in),
+                                   ah_gemv_nc(P.row_bytes), ctx->d_status, pick(ctx, stream)));
     return AH_OK;
 }
 
@@ -270,7 +296,8 @@ int32_t ah_init(int32_t device, ah_ctx **out) {
     ctx->device = device;
     ctx->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess ||
-        hipMalloc(&ctx->d_status, sizeof(unsigned long long)) != hipSuccess) {
+        hipMalloc(&ctx->d_status, sizeof(unsigned long long)) != hipSuccess ||
+        ah_gemv_init_attrs() != hipSuccess) {
         delete ctx;
         return AH_ERR_HIP;
     }
@@ -444,29 +471,69 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
     const uint32_t type = w[0]->type;
     GemvPart *parts = static_cast<GemvPart *>(std::calloc(n_parts, sizeof(GemvPart)));
     if (!parts) return AH_ERR_OUT_OF_MEMORY;
-    uint32_t wg = 0, kpad_max = 0;
+    uint32_t kpad_max = 0, nc = 4, wave_nc_max = 0;
+    bool all_wave = true;
     for (size_t i = 0; i < n_parts; ++i) {
         if (!w[i] || w[i]->type != type || !d_x[i] || !d_y[i] || w[i]->n_out == 0) {
             std::free(parts);
             return AH_ERR_INVALID_ARG;
         }
-        parts[i] = make_part(ctx, w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr);
-        parts[i].wg_begin = wg;
-        wg += parts[i].wg_count;
+        uint32_t wnc = 0;
+        parts[i] = make_part(ctx, w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr, wnc);
+        all_wave = all_wave && wnc != 0;
+        wave_nc_max = wnc > wave_nc_max ? wnc : wave_nc_max;
         const uint32_t kp = kpad_of(w[i]->n_in);
         kpad_max = kp > kpad_max ? kp : kpad_max;
+        const uint32_t nci = ah_gemv_nc(parts[i].row_bytes);
+        nc = nci > nc ? nci : nc;
     }
+    if (!all_wave) {  // one kernel serves the plan: re-cut every part as workgroup tiles
+        for (size_t i = 0; i < n_parts; ++i) {
+            GemvPart &q = parts[i];
+            q.rows_per_tile = ah_gemv_rows_per_tile(q.row_bytes, q.units);
+            q.lanes = 0;
+            const uint32_t n_tiles = (q.n_out + q.rows_per_tile - 1) / q.rows_per_tile;
+            const uint32_t cap = 4u * (uint32_t)ctx->cu_count;
+            q.wg_count = n_tiles < cap ? n_tiles : cap;
+        }
+    }
+    // About four resident workgroups per CU in total: a part's workgroups loop over its tiles,
+    // so each workgroup quantizes its input once for several tiles.
+    uint64_t total_wg = 0;
+    for (size_t i = 0; i < n_parts; ++i) total_wg += parts[i].wg_count;
+    const uint64_t target = 4ull * (uint64_t)ctx->cu_count;
+    uint32_t wg = 0;
+    for (size_t i = 0; i < n_parts; ++i) {
+        uint64_t c = parts[i].wg_count;
+        if (total_wg > target) c = (c * target + total_wg - 1) / total_wg;
+        if (c < 1) c = 1;
+        parts[i].wg_count = (uint32_t)c;
+        parts[i].wg_begin = wg;
+        wg += (uint32_t)c;
+    }
+    uint32_t *map = static_cast<uint32_t *>(std::malloc((size_t)wg * sizeof(uint32_t)));
+    if (!map) {
+        std::free(parts);
+        return AH_ERR_OUT_OF_MEMORY;
+    }
+    for (size_t i = 0; i < n_parts; ++i)
+        for (uint32_t k = 0; k < parts[i].wg_count; ++k) map[parts[i].wg_begin + k] = (uint32_t)i;
     ah_gemv_plan *p = new (std::nothrow) ah_gemv_plan();
     if (!p) {
         std::free(parts);
+        std::free(map);
         return AH_ERR_OUT_OF_MEMORY;
     }
     hipError_t e = hipSetDevice(ctx->device);
     if (e == hipSuccess) e = hipMalloc(&p->d_parts, n_parts * sizeof(GemvPart));
+    if (e == hipSuccess) e = hipMalloc(&p->d_wg_part, (size_t)wg * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemcpy(p->d_parts, parts, n_parts * sizeof(GemvPart), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(p->d_wg_part, map, (size_t)wg * sizeof(uint32_t), hipMemcpyHostToDevice);
     std::free(parts);
+    std::free(map);
     if (e != hipSuccess) {
-        if (p->d_parts) hipFree(p->d_parts);
+        if (p->d_parts) (void)hipFree(p->d_parts);
+        if (p->d_wg_part) (void)hipFree(p->d_wg_part);
         delete p;
         ctx->last_hip = (int)e;
         return AH_ERR_HIP;
@@ -475,6 +542,8 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
     p->n_parts = (uint32_t)n_parts;
     p->grid = wg;
     p->kpad_max = kpad_max;
+    p->nc = nc;
+    p->wave_nc = all_wave ? wave_nc_max : 0;
     *out = p;
     return AH_OK;
 }
@@ -484,8 +553,12 @@ int32_t ah_gemv_plan_run(ah_ctx *ctx, const ah_gemv_plan *plan, void *stream) {
     GemvPart none;
     std::memset(&none, 0, sizeof(none));
     AH_HIP(ctx, hipSetDevice(ctx->device));
-    AH_HIP(ctx, ah_launch_gemv(plan->type, none, plan->d_parts, plan->n_parts, plan->grid,
-                               plan->kpad_max, ctx->d_status, pick(ctx, stream)));
+    if (plan->wave_nc)
+        AH_HIP(ctx, ah_launch_gemv_wave(plan->type, plan->wave_nc, none, plan->d_parts, plan->d_wg_part,
+                                        plan->grid, plan->kpad_max, ctx->d_status, pick(ctx, stream)));
+    else
+        AH_HIP(ctx, ah_launch_gemv(plan->type, none, plan->d_parts, plan->d_wg_part, plan->grid,
+                                   plan->kpad_max, plan->nc, ctx->d_status, pick(ctx, stream)));
     return AH_OK;
 }
 
@@ -493,7 +566,8 @@ int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan) {
     if (!ctx || !plan) return AH_ERR_INVALID_ARG;
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
-    hipFree(plan->d_parts);
+    (void)hipFree(plan->d_parts);
+    (void)hipFree(plan->d_wg_part);
     delete plan;
     return AH_OK;
 }

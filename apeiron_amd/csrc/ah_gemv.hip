@@ -35,13 +35,18 @@ struct ActLds {
     float *fsc;      // [kpad/32]   S_b * 2^-32
     int32_t *xs32;   // [kpad/32]   sum of codes per 32-block
     int32_t *xs16;   // [kpad/16]   sum of codes per 16-group
-    float *red;      // [256 * NU]  unit partials of one tile
+    float *red;      // [1024]      unit partials of one tile (the tile copy follows)
 };
+
+// Activation codes sit in LDS with 16 bytes of padding after every 256: lanes working on
+// consecutive super-blocks read codes 256 bytes apart, which would all map to one LDS bank.
+AH_DEV uint32_t pad_k(uint32_t k) { return k + ((k >> 8) << 4); }
+AH_DEV uint32_t codes_bytes(uint32_t kpad) { return kpad + kpad / 16; }
 
 AH_DEV ActLds carve(uint8_t *smem, uint32_t kpad) {
     ActLds a;
     a.codes = reinterpret_cast<int8_t *>(smem);
-    a.fsc = reinterpret_cast<float *>(smem + kpad);
+    a.fsc = reinterpret_cast<float *>(smem + codes_bytes(kpad));
     a.xs32 = reinterpret_cast<int32_t *>(a.fsc + kpad / 32);
     a.xs16 = a.xs32 + kpad / 32;
     a.red = reinterpret_cast<float *>(a.xs16 + kpad / 16);
@@ -203,7 +208,7 @@ AH_DEV void load_activation(const GemvPart &P, uint32_t kpad, const ActLds &A,
             fsc = o.e < 0 ? 0.0f : __builtin_ldexpf(1.0f, o.e - 32);
         }
         if (b < nbp) {
-            u32x2 *dst = reinterpret_cast<u32x2 *>(A.codes + 32 * b + 8 * q);
+            u32x2 *dst = reinterpret_cast<u32x2 *>(A.codes + pad_k(32 * b + 8 * q));
             *dst = (u32x2){o.c0, o.c1};
             if (q == 0) {
                 A.fsc[b] = fsc;
@@ -216,32 +221,24 @@ AH_DEV void load_activation(const GemvPart &P, uint32_t kpad, const ActLds &A,
     }
 }
 
-// ---- per-family units: load (issued early) and compute ---------------------------------------
+// ---- per-family units, read from the LDS copy of the tile -------------------------------------
 
-// Q8_0 block b (format/quant.rs:238-250): f16 d at byte 0, 32 int8 codes at 2..33; blocks are
-// 2-byte aligned, so the 40-byte window from the 4-aligned address below is realigned.
-struct UnitQ8 {
-    u32x4 a0, a1;
-    u32x2 a2;
-    uint32_t sh;
-};
-AH_DEV void load_q8(__amdgpu_buffer_rsrc_t rs, uint32_t blk, UnitQ8 &u) {
-    const uint32_t base = blk & ~3u;
-    u.sh = blk & 3u;
-    u.a0 = ah_ld128(rs, base);
-    u.a1 = ah_ld128(rs, base + 16);
-    u.a2 = ah_ld64(rs, base + 32);
-}
-AH_DEV float comp_q8(const UnitQ8 &u, uint32_t b, const ActLds &A, int32_t *dots) {
-    const uint32_t w[10] = {u.a0.x, u.a0.y, u.a0.z, u.a0.w, u.a1.x, u.a1.y, u.a1.z, u.a1.w, u.a2.x, u.a2.y};
-    const uint32_t d16 = (u.sh ? (w[0] >> 16) : w[0]) & 0xffffu;
-    const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + 32 * b);
+// Q8_0 block at byte `off` of the tile (format/quant.rs:238-250): f16 d at byte 0, 32 int8 codes
+// at 2..33.  Blocks are 2-byte aligned: 9 dwords from the 4-aligned address below are realigned.
+AH_DEV float unit_q8(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &A, int32_t *dots) {
+    const uint32_t sh = off & 3u;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(tl + (off & ~3u));
+    uint32_t w[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) w[i] = p[i];
+    const uint32_t d16 = (sh ? (w[0] >> 16) : w[0]) & 0xffffu;
+    const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * b));
     const u32x4 x0 = xv[0], x1 = xv[1];
     const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
     int32_t D = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const uint32_t c = u.sh ? w[i + 1] : ah_alignbyte(w[i + 1], w[i], 2);
+        const uint32_t c = sh ? w[i + 1] : ah_alignbyte(w[i + 1], w[i], 2);
         D = ah_sdot4(c, xw[i], D);
     }
     if (dots) dots[b] = D;
@@ -266,29 +263,13 @@ AH_DEV void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &m
 
 // Q4_K super-block s (format/quant.rs:481-510): d, dmin, 12 packed 6-bit (scale, min) pairs,
 // 128 bytes of nibbles; sub-block j takes the low (j even) / high (j odd) nibbles of
-// qs[32*(j/2) + l].  Only the qs windows a ragged row uses are loaded.
-struct UnitQ4 {
-    u32x4 v[9];
-};
-AH_DEV void load_q4(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t npairs, UnitQ4 &u) {
-    u.v[0] = ah_ld128(rs, off);
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        if ((uint32_t)p < npairs) {
-            u.v[1 + 2 * p] = ah_ld128(rs, off + 16 + 32 * p);
-            u.v[2 + 2 * p] = ah_ld128(rs, off + 32 + 32 * p);
-        } else {
-            u.v[1 + 2 * p] = (u32x4){0u, 0u, 0u, 0u};
-            u.v[2 + 2 * p] = (u32x4){0u, 0u, 0u, 0u};
-        }
-    }
-}
+// qs[32*(j/2) + l].  Term per sub-block: S_j * (d*sc_j*D_j - dmin*m_j*X_j).
 template <int P>
-AH_DEV float q4k_pair(const UnitQ4 &u, float fd, float fdm, uint32_t g0, uint32_t nb32,
-                      const ActLds &A, int32_t *dots) {
-    const uint32_t q[8] = {u.v[1 + 2 * P].x, u.v[1 + 2 * P].y, u.v[1 + 2 * P].z, u.v[1 + 2 * P].w,
-                           u.v[2 + 2 * P].x, u.v[2 + 2 * P].y, u.v[2 + 2 * P].z, u.v[2 + 2 * P].w};
-    const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + 32 * g0);
+AH_DEV float q4k_pair(const u32x4 *sb, uint32_t s0, uint32_t s1, uint32_t s2, float fd, float fdm,
+                      uint32_t g0, uint32_t nb32, const ActLds &A, int32_t *dots) {
+    const u32x4 qa = sb[1 + 2 * P], qb = sb[2 + 2 * P];
+    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g0));
     const u32x4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
     const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
     const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
@@ -299,8 +280,8 @@ AH_DEV float q4k_pair(const UnitQ4 &u, float fd, float fdm, uint32_t g0, uint32_
         Dhi = ah_sdot4((q[i] >> 4) & 0x0F0F0F0Fu, xh[i], Dhi);
     }
     int sl, ml, shh, mh;
-    q4k_scale_min<2 * P>(u.v[0].y, u.v[0].z, u.v[0].w, sl, ml);
-    q4k_scale_min<2 * P + 1>(u.v[0].y, u.v[0].z, u.v[0].w, shh, mh);
+    q4k_scale_min<2 * P>(s0, s1, s2, sl, ml);
+    q4k_scale_min<2 * P + 1>(s0, s1, s2, shh, mh);
     if (dots) {
         dots[g0] = Dlo;
         if (g0 + 1 < nb32) dots[g0 + 1] = Dhi;  // a ragged row ends on an odd sub-block
@@ -309,59 +290,45 @@ AH_DEV float q4k_pair(const UnitQ4 &u, float fd, float fdm, uint32_t g0, uint32_
     const float thi = fd * (float)(shh * Dhi) - fdm * (float)(mh * A.xs32[g0 + 1]);
     return A.fsc[g0] * tlo + A.fsc[g0 + 1] * thi;
 }
-AH_DEV float comp_q4(const UnitQ4 &u, uint32_t s, uint32_t npairs, uint32_t nb32, const ActLds &A,
+AH_DEV float unit_q4(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in, const ActLds &A,
                      int32_t *dots) {
-    const float fd = ah_f16_bits_to_f32(u.v[0].x & 0xffffu), fdm = ah_f16_bits_to_f32(u.v[0].x >> 16);
+    const u32x4 *sb = reinterpret_cast<const u32x4 *>(tl + off);  // 16-byte aligned
+    const u32x4 h = sb[0];
+    const float fd = ah_f16_bits_to_f32(h.x & 0xffffu), fdm = ah_f16_bits_to_f32(h.x >> 16);
+    const uint32_t nb32 = (n_in + 31) / 32, rem = n_in - 256 * s;
+    const uint32_t npairs = rem >= 256 ? 4u : (rem + 63) / 64;  // a ragged row uses fewer pairs
     const uint32_t g = 8 * s;
-    float acc = q4k_pair<0>(u, fd, fdm, g, nb32, A, dots);
-    if (npairs > 1) acc += q4k_pair<1>(u, fd, fdm, g + 2, nb32, A, dots);
-    if (npairs > 2) acc += q4k_pair<2>(u, fd, fdm, g + 4, nb32, A, dots);
-    if (npairs > 3) acc += q4k_pair<3>(u, fd, fdm, g + 6, nb32, A, dots);
+    float acc = q4k_pair<0>(sb, h.y, h.z, h.w, fd, fdm, g, nb32, A, dots);
+    if (npairs > 1) acc += q4k_pair<1>(sb, h.y, h.z, h.w, fd, fdm, g + 2, nb32, A, dots);
+    if (npairs > 2) acc += q4k_pair<2>(sb, h.y, h.z, h.w, fd, fdm, g + 4, nb32, A, dots);
+    if (npairs > 3) acc += q4k_pair<3>(sb, h.y, h.z, h.w, fd, fdm, g + 6, nb32, A, dots);
     return acc;
 }
 
 // Q6_K super-block s (format/quant.rs:556-599): ql[128] @0, qh[64] @128, int8 sc[16] @192,
 // f16 d @208.  Element 128n + 32t + l = (nibble t/2 of ql[64n + 32(t&1) + l]
-// | ((qh[32n + l] >> 2t) & 3) << 4) - 32.  Super-blocks are 2-byte aligned: the 216-byte window
-// from the 4-aligned address below is realigned in registers.
-struct UnitQ6 {
-    u32x4 v[13];
-    u32x2 t;
-    uint32_t sh;
-};
-AH_DEV void load_q6(__amdgpu_buffer_rsrc_t rs, uint32_t addr, UnitQ6 &u) {
-    const uint32_t base = addr & ~3u;
-    u.sh = addr & 3u;
-#pragma unroll
-    for (int i = 0; i < 13; ++i) u.v[i] = ah_ld128(rs, base + 16 * i);
-    u.t = ah_ld64(rs, base + 208);
-}
-AH_DEV float comp_q6(const UnitQ6 &u, uint32_t s, uint32_t nb32, uint32_t nb16, const ActLds &A,
+// | ((qh[32n + l] >> 2t) & 3) << 4) - 32.  Super-blocks are 2-byte aligned: 54 dwords from the
+// 4-aligned address below are realigned.
+AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in, const ActLds &A,
                      int32_t *dots16) {
-    uint32_t w[54];
-#pragma unroll
-    for (int i = 0; i < 13; ++i) {
-        w[4 * i] = u.v[i].x;
-        w[4 * i + 1] = u.v[i].y;
-        w[4 * i + 2] = u.v[i].z;
-        w[4 * i + 3] = u.v[i].w;
-    }
-    w[52] = u.t.x;
-    w[53] = u.t.y;
-    const uint32_t sh = u.sh;
-    auto V = [&](int i) -> uint32_t { return ah_alignbyte(w[i + 1], w[i], sh); };
+    const uint32_t sh = off & 3u;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(tl + (off & ~3u));
+    const uint32_t nb32 = (n_in + 31) / 32, nb16 = (n_in + 15) / 16;
+    auto V = [&](int i) -> uint32_t { return ah_alignbyte(p[i + 1], p[i], sh); };
     const float fd = ah_f16_bits_to_f32(V(52) & 0xffffu);
     float acc = 0.0f;
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
+        if (8 * s + 4 * n >= nb32) break;  // a ragged row may end after the first half
         uint32_t qh[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) qh[i] = V(32 + 8 * n + i);
+        const uint32_t scw0 = V(48 + 2 * n), scw1 = V(49 + 2 * n);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const uint32_t g = 8 * s + 4 * n + t;
             if (g >= nb32) break;
-            const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + 32 * g);
+            const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g));
             const u32x4 x0 = xv[0], x1 = xv[1];
             const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             int32_t Dlo = 0, Dhi = 0;
@@ -377,7 +344,7 @@ AH_DEV float comp_q6(const UnitQ6 &u, uint32_t s, uint32_t nb32, uint32_t nb16, 
             }
             Dlo -= 32 * A.xs16[2 * g];
             Dhi -= 32 * A.xs16[2 * g + 1];
-            const uint32_t scw = V(48 + 2 * n + (t >> 1));
+            const uint32_t scw = (t >> 1) ? scw1 : scw0;
             const int sclo = (int)(int8_t)((scw >> (16 * (t & 1))) & 0xffu);
             const int schi = (int)(int8_t)((scw >> (16 * (t & 1) + 8)) & 0xffu);
             if (dots16) {
@@ -391,128 +358,86 @@ AH_DEV float comp_q6(const UnitQ6 &u, uint32_t s, uint32_t nb32, uint32_t nb16, 
 }
 
 template <int TYPE>
-struct UnitOf;
-template <>
-struct UnitOf<AH_GGML_Q8_0> {
-    typedef UnitQ8 T;
-};
-template <>
-struct UnitOf<AH_GGML_Q4_K> {
-    typedef UnitQ4 T;
-};
-template <>
-struct UnitOf<AH_GGML_Q6_K> {
-    typedef UnitQ6 T;
-};
-
-template <int TYPE>
-AH_DEV void load_unit(__amdgpu_buffer_rsrc_t rs, const GemvPart &P, uint32_t row, uint32_t u,
-                      typename UnitOf<TYPE>::T &x) {
-    if constexpr (TYPE == AH_GGML_Q8_0) {
-        load_q8(rs, row * P.row_bytes + 34 * u, x);
-    } else if constexpr (TYPE == AH_GGML_Q4_K) {
-        const uint32_t rem = P.n_in - 256 * u;
-        load_q4(rs, row * P.row_bytes + 144 * u, rem >= 256 ? 4u : (rem + 63) / 64, x);
-    } else {
-        load_q6(rs, row * P.row_bytes + 210 * u, x);
-    }
-}
-
-template <int TYPE>
-AH_DEV float comp_unit(const GemvPart &P, uint32_t row, uint32_t u, const typename UnitOf<TYPE>::T &x,
+AH_DEV float comp_unit(const GemvPart &P, const uint8_t *tl, uint32_t off, uint32_t row, uint32_t u,
                        const ActLds &A) {
-    const uint32_t nb32 = (P.n_in + 31) / 32;
     if constexpr (TYPE == AH_GGML_Q8_0) {
-        return comp_q8(x, u, A, P.dots ? P.dots + (size_t)row * nb32 : nullptr);
+        const uint32_t nb32 = (P.n_in + 31) / 32;
+        return unit_q8(tl, off, u, A, P.dots ? P.dots + (size_t)row * nb32 : nullptr);
     } else if constexpr (TYPE == AH_GGML_Q4_K) {
-        const uint32_t rem = P.n_in - 256 * u;
-        return comp_q4(x, u, rem >= 256 ? 4u : (rem + 63) / 64, nb32, A,
-                       P.dots ? P.dots + (size_t)row * nb32 : nullptr);
+        const uint32_t nb32 = (P.n_in + 31) / 32;
+        return unit_q4(tl, off, u, P.n_in, A, P.dots ? P.dots + (size_t)row * nb32 : nullptr);
     } else {
         const uint32_t nb16 = (P.n_in + 15) / 16;
-        return comp_q6(x, u, nb32, nb16, A, P.dots ? P.dots + (size_t)row * nb16 : nullptr);
+        return unit_q6(tl, off, u, P.n_in, A, P.dots ? P.dots + (size_t)row * nb16 : nullptr);
     }
 }
 
-template <int TYPE, int NU>
+constexpr uint32_t kUnitBytes(int type) { return type == AH_GGML_Q8_0 ? 34u : type == AH_GGML_Q4_K ? 144u : 210u; }
+constexpr uint32_t kRedSlots = 1024;  // unit partials of one tile
+constexpr uint32_t kTileSlack = 64;   // bytes past a tile that realigned unit reads may touch
+
+// One workgroup streams whole-row tiles of a part.  A tile's bytes are loaded with 16-byte
+// buffer loads in which consecutive lanes take consecutive chunks (each wave instruction reads
+// 1 KB contiguous), held in registers until the previous tile is done, then copied to LDS; each
+// lane then reads its (row, unit) pairs out of LDS.  The next tile's loads are issued as soon as
+// the current tile reaches LDS, so they overlap its arithmetic and reduction.
+template <int TYPE, int NC>
 __global__ void __launch_bounds__(kThreads)
-    gemv_kernel(GemvPart single, const GemvPart *__restrict__ parts, uint32_t n_parts,
-                uint32_t kpad_max, unsigned long long *status) {
+    gemv_kernel(GemvPart single, const GemvPart *__restrict__ parts,
+                const uint32_t *__restrict__ wg_part, uint32_t kpad_max,
+                unsigned long long *status) {
     extern __shared__ __align__(16) uint8_t smem[];
-    typedef typename UnitOf<TYPE>::T Unit;
-    GemvPart P = single;
-    if (parts) {
-        uint32_t lo = 0, hi = n_parts;  // last part with wg_begin <= blockIdx.x
-        while (hi - lo > 1) {
-            const uint32_t mid = (lo + hi) / 2;
-            if (parts[mid].wg_begin <= blockIdx.x) lo = mid;
-            else hi = mid;
-        }
-        P = parts[lo];
-    }
+    const GemvPart P = parts ? parts[wg_part[blockIdx.x]] : single;
     const uint32_t wg_local = blockIdx.x - P.wg_begin;
     const uint32_t kpad = (P.n_in + 255) / 256 * 256;
     const ActLds A = carve(smem, kpad_max);
+    uint8_t *tl = reinterpret_cast<uint8_t *>(A.red + kRedSlots);
     const __amdgpu_buffer_rsrc_t rs = ah_rsrc(P.w, (uint32_t)P.w_bytes);
-    const uint32_t U = P.units, R = P.rows_per_tile, TU = R * U;
+    const uint32_t U = P.units, R = P.rows_per_tile, TU = R * U, RB = P.row_bytes;
     const uint32_t n_tiles = (P.n_out + R - 1) / R;
 
-    // (row, unit) of this thread's j-th unit in tile `tile`, or row = n_out when idle
-    auto slot = [&](uint32_t tile, int j, uint32_t &row, uint32_t &u) {
-        const uint32_t f = threadIdx.x + kThreads * j;
-        row = P.n_out;
-        u = 0;
-        if (f < TU) {
-            const uint32_t r = f / U;
-            u = f - r * U;
-            row = tile * R + r;
-            if (row > P.n_out) row = P.n_out;
+    u32x4 chunk[NC];
+    auto load_tile = [&](uint32_t tile) {
+        const uint32_t start = tile * R * RB;
+        const uint32_t rows = P.n_out - tile * R < R ? P.n_out - tile * R : R;
+        const uint32_t a0 = start & ~15u;
+        const uint32_t nch = (rows * RB + (start - a0) + 15) / 16;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const uint32_t c = threadIdx.x + kThreads * i;
+            chunk[i] = c < nch ? ah_ld128(rs, a0 + 16 * c) : (u32x4){0u, 0u, 0u, 0u};
         }
     };
 
-    Unit cur[NU], nxt[NU];
     uint32_t tile = wg_local;
-    if (tile < n_tiles) {
-#pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            uint32_t row, u;
-            slot(tile, j, row, u);
-            if (row < P.n_out) load_unit<TYPE>(rs, P, row, u, cur[j]);
-        }
-    }
+    if (tile < n_tiles) load_tile(tile);
     load_activation(P, kpad, A, status);
-    __syncthreads();
 
     for (; tile < n_tiles; tile += P.wg_count) {
+        __syncthreads();  // the previous tile is consumed; the activation is in LDS
+#pragma unroll
+        for (int i = 0; i < NC; ++i) reinterpret_cast<u32x4 *>(tl)[threadIdx.x + kThreads * i] = chunk[i];
         const uint32_t next = tile + P.wg_count;
-        if (next < n_tiles) {
-#pragma unroll
-            for (int j = 0; j < NU; ++j) {
-                uint32_t row, u;
-                slot(next, j, row, u);
-                if (row < P.n_out) load_unit<TYPE>(rs, P, row, u, nxt[j]);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            uint32_t row, u;
-            slot(tile, j, row, u);
-            if (row < P.n_out) A.red[threadIdx.x + kThreads * j] = comp_unit<TYPE>(P, row, u, cur[j], A);
+        if (next < n_tiles) load_tile(next);
+        __syncthreads();
+        const uint32_t toff = (tile * R * RB) & 15u;
+        for (uint32_t f = threadIdx.x; f < TU; f += kThreads) {
+            const uint32_t r = f / U, u = f - r * U, row = tile * R + r;
+            float v = 0.0f;
+            if (row < P.n_out) v = comp_unit<TYPE>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
+            A.red[f] = v;
         }
         __syncthreads();
         // row sums in fixed order: G lanes per row, G a power of two with R*G <= 256
         uint32_t G = 64;
         while (G > 1 && R * G > kThreads) G >>= 1;
         const uint32_t r = threadIdx.x / G, gl = threadIdx.x & (G - 1);
-        float s = 0.0f;
+        float sum = 0.0f;
         if (r < R)
-            for (uint32_t i = gl; i < U; i += G) s += A.red[r * U + i];
-        for (uint32_t o = 1; o < G; o <<= 1) s += __shfl_xor(s, (int)o, 64);
+            for (uint32_t i = gl; i < U; i += G) sum += A.red[r * U + i];
+        for (uint32_t o = 1; o < G; o <<= 1) sum += __shfl_xor(sum, (int)o, 64);
         const uint32_t row = tile * R + r;
-        if (r < R && gl == 0 && row < P.n_out) P.y[row] = s;
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < NU; ++j) cur[j] = nxt[j];
+        if (r < R && gl == 0 && row < P.n_out) P.y[row] = sum;
     }
 }
 
@@ -557,30 +482,204 @@ __global__ void scan_scales_kernel(const uint8_t *w, uint64_t n_blocks, uint32_t
 
 // ---- launchers (called from ah_abi.cpp) ----
 
-// Units per thread per tile for each family (register budget of the double-buffered unit).
-uint32_t ah_gemv_nu(uint32_t type) { return type == AH_GGML_Q8_0 ? 4u : 1u; }
+// ---- wave-tile GEMV -------------------------------------------------------------------------
+//
+// Each wave streams its own tiles of whole rows (NC KB each) through a private slice of LDS, so
+// the tile loop has no workgroup barrier: the tile is loaded with 16-byte buffer loads in which
+// lane l takes chunks l, l+64, ... (each load instruction reads 1 KB contiguous), kept in
+// registers while the previous tile is computed, then stored to the wave's LDS slice.  A row is
+// owned by G = P.lanes consecutive lanes, lane g taking units g, g+G, ...; the G partial sums
+// meet through DPP row operations (and, for G > 16, lane shuffles) in a fixed order.
 
-size_t ah_gemv_lds_bytes(uint32_t type, uint32_t kpad_max) {
-    return kpad_max + (size_t)kpad_max / 32 * 8 + (size_t)kpad_max / 16 * 4 +
-           (size_t)kThreads * ah_gemv_nu(type) * 4;
+template <int CTRL>
+AH_DEV float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over aligned groups of G lanes (G a power of two <= 64); every lane gets its group's sum.
+AH_DEV float group_sum(float s, uint32_t G) {
+    if (G >= 2) s += dpp<0xB1>(s);   // quad_perm [1,0,3,2]: lane ^ 1
+    if (G >= 4) s += dpp<0x4E>(s);   // quad_perm [2,3,0,1]: lane ^ 2
+    if (G >= 8) s += dpp<0x141>(s);  // row_half_mirror: the other quad of the half-row
+    if (G >= 16) s += dpp<0x140>(s); // row_mirror: the other half of the row
+    if (G >= 32) s += __shfl_xor(s, 16, 64);
+    if (G >= 64) s += __shfl_xor(s, 32, 64);
+    return s;
+}
+
+constexpr uint32_t kWaveSlack = 64;
+
+template <int TYPE, int NC>
+__global__ void __launch_bounds__(kThreads)
+    gemv_wave_kernel(GemvPart single, const GemvPart *__restrict__ parts,
+                     const uint32_t *__restrict__ wg_part, uint32_t kpad_max,
+                     unsigned long long *status) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const GemvPart P = parts ? parts[wg_part[blockIdx.x]] : single;
+    const uint32_t wg_local = blockIdx.x - P.wg_begin;
+    const uint32_t kpad = (P.n_in + 255) / 256 * 256;
+    const ActLds A = carve(smem, kpad_max);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint8_t *tl = reinterpret_cast<uint8_t *>(A.xs16 + kpad_max / 16) + wave * (NC * 1024 + kWaveSlack);
+    const __amdgpu_buffer_rsrc_t rs = ah_rsrc(P.w, (uint32_t)P.w_bytes);
+    const uint32_t U = P.units, RW = P.rows_per_tile, RB = P.row_bytes, G = P.lanes;
+    const uint32_t n_tiles = (P.n_out + RW - 1) / RW;
+    const uint32_t stride = P.wg_count * (kThreads / 64);
+
+    u32x4 chunk[NC];
+    auto load_tile = [&](uint32_t tile) {
+        const uint32_t start = tile * RW * RB;
+        const uint32_t rows = P.n_out - tile * RW < RW ? P.n_out - tile * RW : RW;
+        const uint32_t a0 = start & ~15u;
+        const uint32_t nch = (rows * RB + (start - a0) + 15) / 16;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const uint32_t c = lane + 64 * i;
+            chunk[i] = c < nch ? ah_ld128(rs, a0 + 16 * c) : (u32x4){0u, 0u, 0u, 0u};
+        }
+    };
+
+    uint32_t tile = wg_local * (kThreads / 64) + wave;
+    if (tile < n_tiles) load_tile(tile);
+    load_activation(P, kpad, A, status);
+    __syncthreads();
+
+    const uint32_t r = lane / G, g = lane & (G - 1);
+    for (; tile < n_tiles; tile += stride) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) reinterpret_cast<u32x4 *>(tl)[lane + 64 * i] = chunk[i];
+        const uint32_t next = tile + stride;
+        if (next < n_tiles) load_tile(next);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS stores have landed
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t toff = (tile * RW * RB) & 15u;
+        const uint32_t row = tile * RW + r;
+        float acc = 0.0f;
+        if (r < RW && row < P.n_out) {
+            for (uint32_t u = g; u < U; u += G)
+                acc += comp_unit<TYPE>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
+        }
+        acc = group_sum(acc, G);
+        if (g == 0 && r < RW && row < P.n_out) P.y[row] = acc;
+        __builtin_amdgcn_wave_barrier();  // all lanes are done reading the slice before it is refilled
+    }
+}
+
+// Wave-tile geometry for a row of RB bytes and U units: chunks per lane (NC KB per wave tile),
+// whole rows per tile, lanes per row.  Returns false when a row does not fit 16 KB (the
+// workgroup-tile kernel then serves the part).
+bool ah_gemv_wave_geometry(uint32_t row_bytes, uint32_t units, uint32_t &nc, uint32_t &rows, uint32_t &lanes) {
+    if (row_bytes + 16 > 16 * 1024) return false;
+    nc = row_bytes + 16 <= 8 * 1024 ? 8u : 16u;
+    uint32_t fit = (nc * 1024 - 16) / (row_bytes ? row_bytes : 1);
+    if (fit < 1) fit = 1;
+    uint32_t G = 64;
+    while (G > 1 && G * fit > 64) G >>= 1;      // lanes so that the tile's rows cover the wave
+    uint32_t cap = 1;
+    while (cap < units && cap < 64) cap <<= 1;  // no more lanes than units
+    if (G > cap) G = cap;
+    lanes = G;
+    rows = fit < 64 / G ? fit : 64 / G;
+    return true;
+}
+
+size_t ah_gemv_wave_lds_bytes(uint32_t nc, uint32_t kpad_max) {
+    return kpad_max + kpad_max / 16 + (size_t)kpad_max / 32 * 8 + (size_t)kpad_max / 16 * 4 +
+           4 * ((size_t)nc * 1024 + kWaveSlack);
+}
+
+hipError_t ah_launch_gemv_wave(uint32_t type, uint32_t nc, const GemvPart &single, const GemvPart *d_parts,
+                               const uint32_t *d_wg_part, uint32_t grid, uint32_t kpad_max,
+                               unsigned long long *status, hipStream_t stream) {
+    const size_t lds = ah_gemv_wave_lds_bytes(nc, kpad_max);
+#define AH_WLAUNCH(T)                                                                              \
+    if (nc <= 8)                                                                                   \
+        hipLaunchKernelGGL((gemv_wave_kernel<T, 8>), dim3(grid), dim3(kThreads), lds, stream,      \
+                           single, d_parts, d_wg_part, kpad_max, status);                         \
+    else                                                                                           \
+        hipLaunchKernelGGL((gemv_wave_kernel<T, 16>), dim3(grid), dim3(kThreads), lds, stream,     \
+                           single, d_parts, d_wg_part, kpad_max, status);
+    switch (type) {
+    case AH_GGML_Q8_0: AH_WLAUNCH(AH_GGML_Q8_0) break;
+    case AH_GGML_Q4_K: AH_WLAUNCH(AH_GGML_Q4_K) break;
+    case AH_GGML_Q6_K: AH_WLAUNCH(AH_GGML_Q6_K) break;
+    default: return hipErrorInvalidValue;
+    }
+#undef AH_WLAUNCH
+    return hipGetLastError();
+}
+
+// Chunks of 16 bytes per thread per tile: a tile holds whole rows, so rows longer than 16 KB
+// need the larger instantiations.
+uint32_t ah_gemv_nc(uint32_t row_bytes) {
+    const uint32_t need = row_bytes + 16;
+    return need <= 4 * 4096 ? 4u : need <= 8 * 4096 ? 8u : 12u;
+}
+
+// Whole rows per tile for a part: as many as fit the chunk budget, capped so the tile's units fit
+// the LDS partial slots.
+uint32_t ah_gemv_rows_per_tile(uint32_t row_bytes, uint32_t units) {
+    const uint32_t nc = ah_gemv_nc(row_bytes);
+    uint32_t R = (nc * 4096 - 16) / (row_bytes ? row_bytes : 1);
+    if (R < 1) R = 1;
+    if (units && R * units > kRedSlots) R = kRedSlots / units > 0 ? kRedSlots / units : 1;
+    return R;
+}
+
+size_t ah_gemv_lds_bytes(uint32_t nc, uint32_t kpad_max) {
+    return kpad_max + kpad_max / 16 + (size_t)kpad_max / 32 * 8 + (size_t)kpad_max / 16 * 4 + kRedSlots * 4 +
+           (size_t)nc * 4096 + kTileSlack;
+}
+
+template <int TYPE>
+static void launch_type(uint32_t nc, dim3 grid, size_t lds, hipStream_t stream, const GemvPart &single,
+                        const GemvPart *d_parts, const uint32_t *d_wg_part, uint32_t kpad_max,
+                        unsigned long long *status) {
+    if (nc <= 4)
+        hipLaunchKernelGGL((gemv_kernel<TYPE, 4>), grid, dim3(kThreads), lds, stream, single, d_parts,
+                           d_wg_part, kpad_max, status);
+    else if (nc <= 8)
+        hipLaunchKernelGGL((gemv_kernel<TYPE, 8>), grid, dim3(kThreads), lds, stream, single, d_parts,
+                           d_wg_part, kpad_max, status);
+    else
+        hipLaunchKernelGGL((gemv_kernel<TYPE, 12>), grid, dim3(kThreads), lds, stream, single, d_parts,
+                           d_wg_part, kpad_max, status);
+}
+
+// Allow the large-row instantiations more than 64 KB of dynamic LDS (once per context).
+hipError_t ah_gemv_init_attrs() {
+    const int lim = 160 * 1024;
+    hipError_t e = hipSuccess;
+#define AH_ATTR(T, N)                                                                              \
+    if (e == hipSuccess)                                                                           \
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_kernel<T, N>),                \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+    AH_ATTR(AH_GGML_Q8_0, 4) AH_ATTR(AH_GGML_Q8_0, 8) AH_ATTR(AH_GGML_Q8_0, 12)
+    AH_ATTR(AH_GGML_Q4_K, 4) AH_ATTR(AH_GGML_Q4_K, 8) AH_ATTR(AH_GGML_Q4_K, 12)
+    AH_ATTR(AH_GGML_Q6_K, 4) AH_ATTR(AH_GGML_Q6_K, 8) AH_ATTR(AH_GGML_Q6_K, 12)
+#undef AH_ATTR
+#define AH_WATTR(T, N)                                                                             \
+    if (e == hipSuccess)                                                                           \
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_wave_kernel<T, N>),           \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+    AH_WATTR(AH_GGML_Q8_0, 8) AH_WATTR(AH_GGML_Q8_0, 16) AH_WATTR(AH_GGML_Q4_K, 8)
+    AH_WATTR(AH_GGML_Q4_K, 16) AH_WATTR(AH_GGML_Q6_K, 8) AH_WATTR(AH_GGML_Q6_K, 16)
+#undef AH_WATTR
+    return e;
 }
 
 hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart *d_parts,
-                          uint32_t n_parts, uint32_t grid, uint32_t kpad_max,
+                          const uint32_t *d_wg_part, uint32_t grid, uint32_t kpad_max, uint32_t nc,
                           unsigned long long *status, hipStream_t stream) {
-    const size_t lds = ah_gemv_lds_bytes(type, kpad_max);
+    const size_t lds = ah_gemv_lds_bytes(nc, kpad_max);
     switch (type) {
     case AH_GGML_Q8_0:
-        hipLaunchKernelGGL((gemv_kernel<AH_GGML_Q8_0, 4>), dim3(grid), dim3(kThreads), lds, stream,
-                           single, d_parts, n_parts, kpad_max, status);
+        launch_type<AH_GGML_Q8_0>(nc, dim3(grid), lds, stream, single, d_parts, d_wg_part, kpad_max, status);
         break;
     case AH_GGML_Q4_K:
-        hipLaunchKernelGGL((gemv_kernel<AH_GGML_Q4_K, 1>), dim3(grid), dim3(kThreads), lds, stream,
-                           single, d_parts, n_parts, kpad_max, status);
+        launch_type<AH_GGML_Q4_K>(nc, dim3(grid), lds, stream, single, d_parts, d_wg_part, kpad_max, status);
         break;
     case AH_GGML_Q6_K:
-        hipLaunchKernelGGL((gemv_kernel<AH_GGML_Q6_K, 1>), dim3(grid), dim3(kThreads), lds, stream,
-                           single, d_parts, n_parts, kpad_max, status);
+        launch_type<AH_GGML_Q6_K>(nc, dim3(grid), lds, stream, single, d_parts, d_wg_part, kpad_max, status);
         break;
     default:
         return hipErrorInvalidValue;

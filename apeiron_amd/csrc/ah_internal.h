@@ -81,11 +81,13 @@ AH_DEV int ah_to_q32_mag(uint32_t bits, uint64_t &mag, bool &neg) {
 
 // Exponent of the activation scale: -1 for absmax == 0 (S = 0), 63 for act_scale's None,
 // else e with S = 2^e the least power of two such that 127*S >= absmax.
+// With b = bit length of absmax and e0 = max(0, b - 7): 127 * 2^(e0 - 1) < 2^(b-1) <= absmax,
+// so the least e is e0 when 127 * 2^e0 >= absmax and e0 + 1 otherwise (127 * 2^(e0+1) >= 2^b).
 AH_DEV int ah_act_scale_exp(uint64_t absmax) {
     if (absmax == 0) return -1;
-    uint64_t need = absmax / 127u + (absmax % 127u != 0);
-    if (need <= 1) return 0;
-    int e = 64 - __builtin_clzll(need - 1);  // ceil(log2(need))
+    const int b = 64 - __builtin_clzll(absmax);
+    const int e0 = b > 7 ? b - 7 : 0;
+    const int e = e0 + (absmax > (127ull << e0) ? 1 : 0);
     return e > 62 ? 63 : e;
 }
 
@@ -114,7 +116,8 @@ struct GemvPart {
     int32_t *dots;         // optional exact group dots [n_out][ngroups]
     uint32_t n_out, n_in, row_bytes;
     uint32_t units;        // work units per row (Q8_0 blocks, K-quant super-blocks)
-    uint32_t rows_per_tile;// whole rows per workgroup tile (tile units <= 256 * NU)
+    uint32_t rows_per_tile;// whole rows per tile (per workgroup tile or per wave tile)
+    uint32_t lanes;        // wave-tile kernel: lanes per row (a power of two <= 64)
     uint32_t wg_begin;     // first workgroup of this part in a grouped launch
     uint32_t wg_count;     // workgroups of this part
     uint32_t src;          // AH_SRC_*

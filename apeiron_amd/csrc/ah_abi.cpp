@@ -19,11 +19,13 @@ hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart 
 uint32_t ah_gemv_nc(uint32_t row_bytes);
 uint32_t ah_gemv_rows_per_tile(uint32_t row_bytes, uint32_t units);
 hipError_t ah_gemv_init_attrs();
-bool ah_gemv_wave_geometry(uint32_t row_bytes, uint32_t units, uint32_t &nc, uint32_t &rows,
-                           uint32_t &lanes);
-hipError_t ah_launch_gemv_wave(uint32_t type, uint32_t nc, const GemvPart &single,
-                               const GemvPart *d_parts, const uint32_t *d_wg_part, uint32_t grid,
-                               uint32_t kpad_max, unsigned long long *status, hipStream_t stream);
+bool ah_gemv_stream_geometry(uint32_t row_bytes, uint32_t units, uint32_t &rows, uint32_t &lanes);
+size_t ah_gemv_stream_lds_bytes(uint32_t kpad_max);
+uint32_t ah_gemv_stream_threads();
+int ah_gemv_stream_occupancy(uint32_t type, size_t lds);
+hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single,
+                                 const GemvPart *d_parts, const uint32_t *d_wg_part, uint32_t grid,
+                                 uint32_t kpad_max, unsigned long long *status, hipStream_t stream);
 hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream);
 hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes, uint32_t off0,
                           uint32_t off1, int *d_bad, hipStream_t stream);
@@ -52,7 +54,8 @@ struct ah_tensor {
 };
 
 struct ah_gemv_plan {
-    uint32_t type = 0, n_parts = 0, grid = 0, kpad_max = 0, nc = 4, wave_nc = 0;
+    uint32_t type = 0, n_parts = 0, grid = 0, kpad_max = 0, nc = 4;
+    bool stream = false;  // streaming kernel (else the workgroup-tile kernel)
     GemvPart *d_parts = nullptr;   // part descriptors
     uint32_t *d_wg_part = nullptr; // workgroup -> part index (one load per workgroup)
 };
@@ -129,12 +132,12 @@ uint32_t units_per_row(uint32_t t, uint32_t n_in) {
 
 uint32_t kpad_of(size_t n_in) { return (uint32_t)((n_in + 255) / 256 * 256); }
 
-// Two kernels serve the GEMV.  The wave-tile kernel (rows up to 16 KB) gives every wave its own
-// tiles of whole rows; the workgroup-tile kernel serves longer rows.  `wave_nc` is 0 for the
-// latter, else the wave tile size in KB.  Each part gets enough workgroups for one tile per wave,
-// up to 4 workgroups per CU (workgroups then loop over tiles).
-GemvPart make_part(const ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
-                   const int64_t *scales, float *y, int32_t *dots, uint32_t &wave_nc) {
+// Two kernels serve the GEMV.  The streaming kernel (rows up to one 8 KB tile) gives every wave a
+// contiguous range of whole rows; the workgroup-tile kernel serves longer rows.  make_part fills
+// a part's geometry; deal_wgs then sizes every part's workgroup count.
+
+GemvPart make_part(const ah_tensor *w, uint32_t src, const void *x, const int64_t *scales, float *y,
+                   int32_t *dots, bool &stream) {
     GemvPart P;
     std::memset(&P, 0, sizeof(P));
     P.w = w->d;
@@ -147,26 +150,91 @@ GemvPart make_part(const ah_ctx *ctx, const ah_tensor *w, uint32_t src, const vo
     P.n_in = (uint32_t)w->n_in;
     P.row_bytes = (uint32_t)w->row_bytes;
     P.units = units_per_row(w->type, P.n_in);
-    uint32_t nc = 0, rows = 0, lanes = 0, tiles_per_wg;
-    if (ah_gemv_wave_geometry(P.row_bytes, P.units, nc, rows, lanes)) {
-        wave_nc = nc;
+    uint32_t rows = 0, lanes = 0;
+    stream = ah_gemv_stream_geometry(P.row_bytes, P.units, rows, lanes);
+    if (stream) {
         P.rows_per_tile = rows;
         P.lanes = lanes;
-        tiles_per_wg = 4;
     } else {
-        wave_nc = 0;
         P.rows_per_tile = ah_gemv_rows_per_tile(P.row_bytes, P.units);
         P.lanes = 0;
-        tiles_per_wg = 1;
     }
-    const uint32_t n_tiles = (P.n_out + P.rows_per_tile - 1) / P.rows_per_tile;
-    const uint32_t need = (n_tiles + tiles_per_wg - 1) / tiles_per_wg;
-    const uint32_t cap = 4u * (uint32_t)ctx->cu_count;
-    P.wg_count = need < cap ? need : cap;
-    if (P.wg_count == 0) P.wg_count = 1;
-    P.wg_begin = 0;
     P.src = src;
     return P;
+}
+
+// Re-cut a part for the workgroup-tile kernel (a plan whose parts do not all stream).
+void recut_wg_tiles(GemvPart &P) {
+    P.rows_per_tile = ah_gemv_rows_per_tile(P.row_bytes, P.units);
+    P.lanes = 0;
+}
+
+// Workgroups that are resident on the whole device at once for the kernel serving these parts:
+// a launch never asks for more, so no workgroup waits for another to finish before it starts.
+uint64_t resident_wgs(const ah_ctx *ctx, uint32_t type, bool stream, uint32_t kpad_max) {
+    int occ = stream ? ah_gemv_stream_occupancy(type, ah_gemv_stream_lds_bytes(kpad_max)) : 4;
+    if (occ < 1) occ = 1;
+    return (uint64_t)occ * (uint64_t)ctx->cu_count;
+}
+
+// Deal `target` workgroups over the parts: one each, then one at a time to the part with the most
+// weight bytes per workgroup, never past one tile per wave (streaming) or per workgroup.  Returns
+// the grid size (wg_begin / wg_count filled), or 0 when the host is out of memory.
+uint32_t deal_wgs(GemvPart *parts, size_t n, uint64_t target, bool stream) {
+    struct Item {
+        double load;
+        uint32_t i;
+    };
+    Item *heap = static_cast<Item *>(std::malloc(n * sizeof(Item)));
+    if (!heap) return 0;
+    size_t hn = 0;
+    auto cap_of = [&](const GemvPart &P) -> uint32_t {
+        const uint32_t tiles = (P.n_out + P.rows_per_tile - 1) / P.rows_per_tile;
+        const uint32_t wv = ah_gemv_stream_threads() / 64;
+        const uint32_t c = stream ? (tiles + wv - 1) / wv : tiles;
+        return c ? c : 1u;
+    };
+    auto push = [&](Item it) {
+        size_t k = hn++;
+        while (k && heap[(k - 1) / 2].load < it.load) {
+            heap[k] = heap[(k - 1) / 2];
+            k = (k - 1) / 2;
+        }
+        heap[k] = it;
+    };
+    auto pop = [&]() {
+        const Item top = heap[0], last = heap[--hn];
+        size_t k = 0;
+        for (;;) {
+            size_t c = 2 * k + 1;
+            if (c >= hn) break;
+            if (c + 1 < hn && heap[c + 1].load > heap[c].load) ++c;
+            if (heap[c].load <= last.load) break;
+            heap[k] = heap[c];
+            k = c;
+        }
+        if (hn) heap[k] = last;
+        return top;
+    };
+    uint64_t used = n;
+    for (size_t i = 0; i < n; ++i) {
+        parts[i].wg_count = 1;
+        if (cap_of(parts[i]) > 1) push({(double)parts[i].w_bytes, (uint32_t)i});
+    }
+    while (used < target && hn) {
+        const Item it = pop();
+        GemvPart &P = parts[it.i];
+        ++P.wg_count;
+        ++used;
+        if (P.wg_count < cap_of(P)) push({(double)P.w_bytes / P.wg_count, it.i});
+    }
+    std::free(heap);
+    uint32_t wg = 0;
+    for (size_t i = 0; i < n; ++i) {
+        parts[i].wg_begin = wg;
+        wg += parts[i].wg_count;
+    }
+    return wg;
 }
 
 int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
@@ -174,15 +242,18 @@ int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     if (!ctx || !w || (!x && w->n_in) || (!y && w->n_out)) return AH_ERR_INVALID_ARG;
     if (src == AH_SRC_CODES && !scales && w->n_in) return AH_ERR_INVALID_ARG;
     if (w->n_out == 0) return AH_OK;
-    uint32_t wave_nc = 0;
-    const GemvPart P = make_part(ctx, w, src, x, scales, y, dots, wave_nc);
+    bool st = false;
+    GemvPart P = make_part(w, src, x, scales, y, dots, st);
+    const uint32_t kp = kpad_of(w->n_in);
     AH_HIP(ctx, hipSetDevice(ctx->device));
-    if (wave_nc)
-        AH_HIP(ctx, ah_launch_gemv_wave(w->type, wave_nc, P, nullptr, nullptr, P.wg_count,
-                                        kpad_of(w->n_in), ctx->d_status, pick(ctx, stream)));
+    const uint32_t grid = deal_wgs(&P, 1, resident_wgs(ctx, w->type, st, kp), st);
+    if (grid == 0) return AH_ERR_OUT_OF_MEMORY;
+    if (st)
+        AH_HIP(ctx, ah_launch_gemv_stream(w->type, P, nullptr, nullptr, grid, kp, ctx->d_status,
+                                          pick(ctx, stream)));
     else
-        AH_HIP(ctx, ah_launch_gemv(w->type, P, nullptr, nullptr, P.wg_count, kpad_of(w->n_in),
-                                   ah_gemv_nc(P.row_bytes), ctx->d_status, pick(ctx, stream)));
+        AH_HIP(ctx, ah_launch_gemv(w->type, P, nullptr, nullptr, grid, kp, ah_gemv_nc(P.row_bytes),
+                                   ctx->d_status, pick(ctx, stream)));
     return AH_OK;
 }
 
@@ -471,45 +542,33 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
     const uint32_t type = w[0]->type;
     GemvPart *parts = static_cast<GemvPart *>(std::calloc(n_parts, sizeof(GemvPart)));
     if (!parts) return AH_ERR_OUT_OF_MEMORY;
-    uint32_t kpad_max = 0, nc = 4, wave_nc_max = 0;
-    bool all_wave = true;
+    uint32_t kpad_max = 0, nc = 4;
+    bool all_stream = true;
     for (size_t i = 0; i < n_parts; ++i) {
         if (!w[i] || w[i]->type != type || !d_x[i] || !d_y[i] || w[i]->n_out == 0) {
             std::free(parts);
             return AH_ERR_INVALID_ARG;
         }
-        uint32_t wnc = 0;
-        parts[i] = make_part(ctx, w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr, wnc);
-        all_wave = all_wave && wnc != 0;
-        wave_nc_max = wnc > wave_nc_max ? wnc : wave_nc_max;
+        bool st = false;
+        parts[i] = make_part(w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr, st);
+        all_stream = all_stream && st;
         const uint32_t kp = kpad_of(w[i]->n_in);
         kpad_max = kp > kpad_max ? kp : kpad_max;
         const uint32_t nci = ah_gemv_nc(parts[i].row_bytes);
         nc = nci > nc ? nci : nc;
     }
-    if (!all_wave) {  // one kernel serves the plan: re-cut every part as workgroup tiles
-        for (size_t i = 0; i < n_parts; ++i) {
-            GemvPart &q = parts[i];
-            q.rows_per_tile = ah_gemv_rows_per_tile(q.row_bytes, q.units);
-            q.lanes = 0;
-            const uint32_t n_tiles = (q.n_out + q.rows_per_tile - 1) / q.rows_per_tile;
-            const uint32_t cap = 4u * (uint32_t)ctx->cu_count;
-            q.wg_count = n_tiles < cap ? n_tiles : cap;
-        }
+    if (!all_stream)  // one kernel serves the plan: every part as workgroup tiles
+        for (size_t i = 0; i < n_parts; ++i) recut_wg_tiles(parts[i]);
+    hipError_t e0 = hipSetDevice(ctx->device);
+    if (e0 != hipSuccess) {
+        std::free(parts);
+        ctx->last_hip = (int)e0;
+        return AH_ERR_HIP;
     }
-    // About four resident workgroups per CU in total: a part's workgroups loop over its tiles,
-    // so each workgroup quantizes its input once for several tiles.
-    uint64_t total_wg = 0;
-    for (size_t i = 0; i < n_parts; ++i) total_wg += parts[i].wg_count;
-    const uint64_t target = 4ull * (uint64_t)ctx->cu_count;
-    uint32_t wg = 0;
-    for (size_t i = 0; i < n_parts; ++i) {
-        uint64_t c = parts[i].wg_count;
-        if (total_wg > target) c = (c * target + total_wg - 1) / total_wg;
-        if (c < 1) c = 1;
-        parts[i].wg_count = (uint32_t)c;
-        parts[i].wg_begin = wg;
-        wg += (uint32_t)c;
+    const uint32_t wg = deal_wgs(parts, n_parts, resident_wgs(ctx, type, all_stream, kpad_max), all_stream);
+    if (wg == 0) {
+        std::free(parts);
+        return AH_ERR_OUT_OF_MEMORY;
     }
     uint32_t *map = static_cast<uint32_t *>(std::malloc((size_t)wg * sizeof(uint32_t)));
     if (!map) {
@@ -543,7 +602,7 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
     p->grid = wg;
     p->kpad_max = kpad_max;
     p->nc = nc;
-    p->wave_nc = all_wave ? wave_nc_max : 0;
+    p->stream = all_stream;
     *out = p;
     return AH_OK;
 }
@@ -553,9 +612,9 @@ int32_t ah_gemv_plan_run(ah_ctx *ctx, const ah_gemv_plan *plan, void *stream) {
     GemvPart none;
     std::memset(&none, 0, sizeof(none));
     AH_HIP(ctx, hipSetDevice(ctx->device));
-    if (plan->wave_nc)
-        AH_HIP(ctx, ah_launch_gemv_wave(plan->type, plan->wave_nc, none, plan->d_parts, plan->d_wg_part,
-                                        plan->grid, plan->kpad_max, ctx->d_status, pick(ctx, stream)));
+    if (plan->stream)
+        AH_HIP(ctx, ah_launch_gemv_stream(plan->type, none, plan->d_parts, plan->d_wg_part,
+                                          plan->grid, plan->kpad_max, ctx->d_status, pick(ctx, stream)));
     else
         AH_HIP(ctx, ah_launch_gemv(plan->type, none, plan->d_parts, plan->d_wg_part, plan->grid,
                                    plan->kpad_max, plan->nc, ctx->d_status, pick(ctx, stream)));

@@ -70,26 +70,123 @@ AH_DEV uint32_t quad_xor2(uint32_t v) { return (uint32_t)__builtin_amdgcn_update
 struct QuadOut {
     uint32_t c0, c1;
     int s16, s32, e;
+    float fsc;  // S_b * 2^-32 (0 for a zero or refused block)
 };
-AH_DEV QuadOut quant_quad(const void *x, uint32_t src, uint32_t n_in, size_t row_off, uint32_t b,
-                          bool valid, unsigned long long *status, unsigned long long key_base) {
+
+// The raw inputs of one quad lane for one 32-block, loaded apart from the arithmetic so that a
+// kernel can issue these loads ahead of its weight stream: 8 f32 bit patterns (w[0..7]), 8 Q32.32
+// values (lo/hi in w[2i], w[2i+1]), or 8 int8 codes (w[0..1]) with the block scale (w[2..3]).
+struct QuadIn {
+    uint32_t w[16];
+    uint32_t s0, s1;  // codes: the block scale
+    uint32_t take;
+};
+AH_DEV QuadIn quad_load(const void *x, const int64_t *scales, uint32_t src, uint32_t n_in, size_t row_off,
+                        uint32_t b, bool valid) {
+    QuadIn in;
     const uint32_t q = threadIdx.x & 3;
     const uint32_t k0 = b * 32 + 8 * q;
-    const uint32_t take = (valid && n_in > k0) ? (n_in - k0 < 8 ? n_in - k0 : 8) : 0;
+    in.take = (valid && n_in > k0) ? (n_in - k0 < 8 ? n_in - k0 : 8) : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) in.w[i] = 0;
+    if (src == AH_SRC_F32) {
+        const uint32_t *xb = static_cast<const uint32_t *>(x) + row_off + k0;
+        if (in.take == 8 && (reinterpret_cast<uintptr_t>(xb) & 15) == 0) {
+            const u32x4 a = reinterpret_cast<const u32x4 *>(xb)[0], c = reinterpret_cast<const u32x4 *>(xb)[1];
+            in.w[0] = a.x; in.w[1] = a.y; in.w[2] = a.z; in.w[3] = a.w;
+            in.w[4] = c.x; in.w[5] = c.y; in.w[6] = c.z; in.w[7] = c.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) in.w[i] = (uint32_t)i < in.take ? xb[i] : 0u;
+        }
+    } else if (src == AH_SRC_Q32) {
+        const uint64_t *xv = static_cast<const uint64_t *>(x) + row_off + k0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint64_t v = (uint32_t)i < in.take ? xv[i] : 0ull;
+            in.w[2 * i] = (uint32_t)v;
+            in.w[2 * i + 1] = (uint32_t)(v >> 32);
+        }
+    } else {
+        const int8_t *c = static_cast<const int8_t *>(x) + row_off + k0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t v = (uint32_t)i < in.take ? (uint32_t)(uint8_t)c[i] : 0u;
+            in.w[i >> 2] |= v << (8 * (i & 3));
+        }
+    }
+    in.s0 = in.s1 = 0;
+    if (src == AH_SRC_CODES && valid) {
+        const uint64_t s = (uint64_t)scales[b];
+        in.s0 = (uint32_t)s;
+        in.s1 = (uint32_t)(s >> 32);
+    }
+    return in;
+}
+
+// The same inputs for one activation row read through buffer resources: elements past n_in lie
+// past the resource's range and read as zero.  Every source kind issues the same five buffer loads
+// (offsets picked by `src`, unused ones out of range) and nothing here touches the loaded words,
+// so there is no branch and no wait: the loads return in issue order ahead of the weight stream,
+// and quad_quant, which waits for them, never waits for the weights.  Codes are read a whole dword
+// at a time (the base must be 4-byte aligned); quad_quant clears bytes past n_in.
+struct ActRsrc {
+    __amdgpu_buffer_rsrc_t x, s;
+};
+AH_DEV ActRsrc act_rsrc(const void *x, const int64_t *scales, uint32_t src, uint32_t n_in) {
+    ActRsrc r;
+    const uint32_t esz = src == AH_SRC_F32 ? 4u : src == AH_SRC_Q32 ? 8u : 1u;
+    r.x = ah_rsrc(x, n_in * esz);
+    r.s = ah_rsrc(scales, src == AH_SRC_CODES ? (n_in + 31) / 32 * 8 : 0u);
+    return r;
+}
+constexpr uint32_t kActOob = 0xFFFFFFF0u;  // past any activation resource
+AH_DEV QuadIn quad_load_row(const ActRsrc &r, uint32_t src, uint32_t n_in, uint32_t b) {
+    QuadIn in;
+    const uint32_t k0 = b * 32 + 8 * (threadIdx.x & 3);
+    in.take = n_in > k0 ? (n_in - k0 < 8 ? n_in - k0 : 8) : 0;
+    const bool f = src == AH_SRC_F32, q = src == AH_SRC_Q32;
+    const uint32_t base = f ? 4 * k0 : q ? 8 * k0 : k0;
+    const u32x4 l0 = ah_ld128(r.x, base);
+    const u32x4 l1 = ah_ld128(r.x, f || q ? base + 16 : kActOob);
+    const u32x4 l2 = ah_ld128(r.x, q ? base + 32 : kActOob);
+    const u32x4 l3 = ah_ld128(r.x, q ? base + 48 : kActOob);
+    const u32x2 sc = ah_ld64(r.s, f || q ? kActOob : 8 * b);
+    in.w[0] = l0.x; in.w[1] = l0.y; in.w[2] = l0.z; in.w[3] = l0.w;
+    in.w[4] = l1.x; in.w[5] = l1.y; in.w[6] = l1.z; in.w[7] = l1.w;
+    in.w[8] = l2.x; in.w[9] = l2.y; in.w[10] = l2.z; in.w[11] = l2.w;
+    in.w[12] = l3.x; in.w[13] = l3.y; in.w[14] = l3.z; in.w[15] = l3.w;
+    in.s0 = sc.x;
+    in.s1 = sc.y;
+    return in;
+}
+
+AH_DEV QuadOut quad_quant(const QuadIn &in, uint32_t src, uint32_t b, unsigned long long *status,
+                          unsigned long long key_base) {
+    const uint32_t q = threadIdx.x & 3;
+    const uint32_t k0 = b * 32 + 8 * q;
+    const uint32_t take = in.take;
+    QuadOut o;
+    if (src == AH_SRC_CODES) {
+        // precomputed codes (bytes past n_in cleared): only the code sums are derived here
+        o.c0 = in.w[0] & (take >= 4 ? 0xffffffffu : (1u << (8 * take)) - 1u);
+        o.c1 = in.w[1] & (take >= 8 ? 0xffffffffu : take <= 4 ? 0u : (1u << (8 * (take - 4))) - 1u);
+        int s8 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s8 += (int)(int8_t)((((i < 4) ? o.c0 : o.c1) >> (8 * (i & 3))) & 0xffu);
+        o.s16 = s8 + (int)quad_xor1((uint32_t)s8);
+        o.s32 = o.s16 + (int)quad_xor2((uint32_t)o.s16);
+        o.e = 0;
+        o.fsc = (float)(int64_t)(((uint64_t)in.s1 << 32) | in.s0) * 0x1p-32f;
+        return o;
+    }
     uint32_t bits[8];
     int64_t v64[8];
     uint32_t maxb = 0;
     uint64_t maxm = 0;
     if (src == AH_SRC_F32) {
-        const uint32_t *xb = static_cast<const uint32_t *>(x) + row_off + k0;
-        if (take == 8 && (reinterpret_cast<uintptr_t>(xb) & 15) == 0) {
-            const u32x4 a = reinterpret_cast<const u32x4 *>(xb)[0], c = reinterpret_cast<const u32x4 *>(xb)[1];
-            bits[0] = a.x; bits[1] = a.y; bits[2] = a.z; bits[3] = a.w;
-            bits[4] = c.x; bits[5] = c.y; bits[6] = c.z; bits[7] = c.w;
-        } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) bits[i] = (uint32_t)i < take ? xb[i] : 0u;
-        }
+        for (int i = 0; i < 8; ++i) bits[i] = in.w[i];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t a = bits[i] & 0x7fffffffu;
@@ -100,10 +197,9 @@ AH_DEV QuadOut quant_quad(const void *x, uint32_t src, uint32_t n_in, size_t row
         t = quad_xor2(maxb);
         maxb = t > maxb ? t : maxb;
     } else {
-        const int64_t *xv = static_cast<const int64_t *>(x) + row_off + k0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            v64[i] = (uint32_t)i < take ? xv[i] : 0;
+            v64[i] = (int64_t)(((uint64_t)in.w[2 * i + 1] << 32) | in.w[2 * i]);
             const uint64_t m = v64[i] < 0 ? 0ull - (uint64_t)v64[i] : (uint64_t)v64[i];
             maxm = m > maxm ? m : maxm;
         }
@@ -115,7 +211,6 @@ AH_DEV QuadOut quant_quad(const void *x, uint32_t src, uint32_t n_in, size_t row
         t = ((uint64_t)quad_xor2(hi) << 32) | quad_xor2(lo);
         maxm = t > maxm ? t : maxm;
     }
-    QuadOut o;
     o.c0 = o.c1 = 0;
     int s8 = 0;
     int e = -1;
@@ -172,53 +267,56 @@ AH_DEV QuadOut quant_quad(const void *x, uint32_t src, uint32_t n_in, size_t row
     o.s16 = s8 + (int)quad_xor1((uint32_t)s8);
     o.s32 = o.s16 + (int)quad_xor2((uint32_t)o.s16);
     o.e = e;
+    o.fsc = e < 0 ? 0.0f : __builtin_ldexpf(1.0f, e - 32);
     return o;
+}
+
+AH_DEV QuadOut quant_quad(const void *x, uint32_t src, uint32_t n_in, size_t row_off, uint32_t b,
+                          bool valid, unsigned long long *status, unsigned long long key_base) {
+    return quad_quant(quad_load(x, nullptr, src, n_in, row_off, b, valid), src, b, status, key_base);
+}
+
+// Store one quad's block to the LDS activation.
+AH_DEV void store_quad(const ActLds &A, uint32_t b, const QuadOut &o) {
+    const uint32_t q = threadIdx.x & 3;
+    u32x2 *dst = reinterpret_cast<u32x2 *>(A.codes + pad_k(32 * b + 8 * q));
+    *dst = (u32x2){o.c0, o.c1};
+    if (q == 0) {
+        A.fsc[b] = o.fsc;
+        A.xs32[b] = o.s32;
+        A.xs16[2 * b] = o.s16;
+    } else if (q == 2) {
+        A.xs16[2 * b + 1] = o.s16;
+    }
 }
 
 // Fill the LDS activation of part P: blocks past n_in (up to kpad) are zero, so ragged rows need
 // no special case -- padded lanes contribute nothing to any dot or code sum.
 AH_DEV void load_activation(const GemvPart &P, uint32_t kpad, const ActLds &A,
                             unsigned long long *status) {
-    const uint32_t nb32 = (P.n_in + 31) / 32, nbp = kpad / 32, q = threadIdx.x & 3;
+    const uint32_t nbp = kpad / 32;
+    const ActRsrc xr = act_rsrc(P.x, P.scales, P.src, P.n_in);
     for (uint32_t base = 0; base < nbp; base += kThreads / 4) {
         const uint32_t b = base + threadIdx.x / 4;
-        const bool valid = b < nb32;
-        QuadOut o;
-        float fsc = 0.0f;
-        if (P.src == AH_SRC_CODES) {
-            const uint32_t k0 = b * 32 + 8 * q;
-            const uint32_t take = (valid && P.n_in > k0) ? (P.n_in - k0 < 8 ? P.n_in - k0 : 8) : 0;
-            const int8_t *c = static_cast<const int8_t *>(P.x) + k0;
-            o.c0 = o.c1 = 0;
-            int s8 = 0;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int v = (uint32_t)i < take ? (int)c[i] : 0;
-                if (i < 4)
-                    o.c0 |= (uint32_t)(v & 0xff) << (8 * i);
-                else
-                    o.c1 |= (uint32_t)(v & 0xff) << (8 * (i - 4));
-                s8 += v;
-            }
-            o.s16 = s8 + (int)quad_xor1((uint32_t)s8);
-            o.s32 = o.s16 + (int)quad_xor2((uint32_t)o.s16);
-            if (valid) fsc = (float)P.scales[b] * 0x1p-32f;
-        } else {
-            o = quant_quad(P.x, P.src, P.n_in, 0, b, valid, status, 0);
-            fsc = o.e < 0 ? 0.0f : __builtin_ldexpf(1.0f, o.e - 32);
-        }
-        if (b < nbp) {
-            u32x2 *dst = reinterpret_cast<u32x2 *>(A.codes + pad_k(32 * b + 8 * q));
-            *dst = (u32x2){o.c0, o.c1};
-            if (q == 0) {
-                A.fsc[b] = fsc;
-                A.xs32[b] = o.s32;
-                A.xs16[2 * b] = o.s16;
-            } else if (q == 2) {
-                A.xs16[2 * b + 1] = o.s16;
-            }
-        }
+        const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, 0);
+        if (b < nbp) store_quad(A, b, o);
     }
+}
+
+// The workgroup's part: the launch argument, or its entry of a plan's part table.  The compiler
+// reads either through one generic pointer into vector registers; every word is moved to a scalar
+// register (the descriptor is the same for the whole workgroup), so buffer resources built from it
+// are uniform and need no per-lane loop.
+AH_DEV GemvPart load_part(const GemvPart &single, const GemvPart *__restrict__ parts,
+                          const uint32_t *__restrict__ wg_part) {
+    GemvPart P = parts ? parts[wg_part[blockIdx.x]] : single;
+    static_assert(sizeof(GemvPart) % 4 == 0, "descriptor is whole dwords");
+    uint32_t w[sizeof(GemvPart) / 4];
+    __builtin_memcpy(w, &P, sizeof(P));
+#pragma unroll
+    for (uint32_t i = 0; i < sizeof(GemvPart) / 4; ++i) w[i] = __builtin_amdgcn_readfirstlane(w[i]);
+    __builtin_memcpy(&P, w, sizeof(P));
+    return P;
 }
 
 // ---- per-family units, read from the LDS copy of the tile -------------------------------------
@@ -387,7 +485,7 @@ __global__ void __launch_bounds__(kThreads)
                 const uint32_t *__restrict__ wg_part, uint32_t kpad_max,
                 unsigned long long *status) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const GemvPart P = parts ? parts[wg_part[blockIdx.x]] : single;
+    const GemvPart P = load_part(single, parts, wg_part);
     const uint32_t wg_local = blockIdx.x - P.wg_begin;
     const uint32_t kpad = (P.n_in + 255) / 256 * 256;
     const ActLds A = carve(smem, kpad_max);
@@ -482,14 +580,21 @@ __global__ void scan_scales_kernel(const uint8_t *w, uint64_t n_blocks, uint32_t
 
 // ---- launchers (called from ah_abi.cpp) ----
 
-// ---- wave-tile GEMV -------------------------------------------------------------------------
+// ---- streaming GEMV ---------------------------------------------------------------------------
 //
-// Each wave streams its own tiles of whole rows (NC KB each) through a private slice of LDS, so
-// the tile loop has no workgroup barrier: the tile is loaded with 16-byte buffer loads in which
-// lane l takes chunks l, l+64, ... (each load instruction reads 1 KB contiguous), kept in
-// registers while the previous tile is computed, then stored to the wave's LDS slice.  A row is
-// owned by G = P.lanes consecutive lanes, lane g taking units g, g+G, ...; the G partial sums
-// meet through DPP row operations (and, for G > 16, lane shuffles) in a fixed order.
+// Each wave owns a contiguous range of whole rows of its part (the part's rows split evenly over
+// its waves) and streams them in tiles of whole rows, at most kStreamTile bytes each.  A tile is
+// read with 16-byte buffer loads in which lane l takes chunks l, l+64, ... (each load instruction
+// reads 1 KB contiguous; a chunk past the tile takes an out-of-range offset and reads nothing),
+// held in registers while the wave computes the previous tile from its LDS slot, then written to
+// the slot.  Eight waves share a workgroup and its quantized activation; the tile loop has no
+// workgroup barrier.
+//
+// The activation loads go out before the first tile's, so waiting for them does not wait for the
+// weights, and the quantizer runs while the first tile streams in.
+//
+// A row is owned by G = P.lanes consecutive lanes, lane g taking units g, g+G, ...; the G partial
+// sums meet through DPP row operations (and, for G > 16, lane shuffles) in a fixed order.
 
 template <int CTRL>
 AH_DEV float dpp(float v) {
@@ -506,72 +611,91 @@ AH_DEV float group_sum(float s, uint32_t G) {
     return s;
 }
 
-constexpr uint32_t kWaveSlack = 64;
+constexpr uint32_t kSThreads = 512;                // threads of a streaming workgroup
+constexpr uint32_t kSWaves = kSThreads / 64;
+constexpr uint32_t kChunks = 8;                    // 16-byte loads per lane per tile
+constexpr uint32_t kStreamTile = kChunks * 1024;   // bytes per tile
+constexpr uint32_t kSlotBytes = kStreamTile + 32;  // + what realigned unit reads touch past a tile
+constexpr uint32_t kOob = 0xFFFFFFF0u;             // past any payload (payloads stay below 4 GiB - 256)
 
-template <int TYPE, int NC>
-__global__ void __launch_bounds__(kThreads)
-    gemv_wave_kernel(GemvPart single, const GemvPart *__restrict__ parts,
-                     const uint32_t *__restrict__ wg_part, uint32_t kpad_max,
-                     unsigned long long *status) {
+template <int TYPE>
+__global__ void __launch_bounds__(kSThreads)
+    gemv_stream_kernel(GemvPart single, const GemvPart *__restrict__ parts,
+                       const uint32_t *__restrict__ wg_part, uint32_t kpad_max,
+                       unsigned long long *status) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const GemvPart P = parts ? parts[wg_part[blockIdx.x]] : single;
-    const uint32_t wg_local = blockIdx.x - P.wg_begin;
+    const GemvPart P = load_part(single, parts, wg_part);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t kpad = (P.n_in + 255) / 256 * 256;
     const ActLds A = carve(smem, kpad_max);
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint8_t *tl = reinterpret_cast<uint8_t *>(A.xs16 + kpad_max / 16) + wave * (NC * 1024 + kWaveSlack);
+    uint8_t *tl = reinterpret_cast<uint8_t *>(A.xs16 + kpad_max / 16) + wave * kSlotBytes;
     const __amdgpu_buffer_rsrc_t rs = ah_rsrc(P.w, (uint32_t)P.w_bytes);
     const uint32_t U = P.units, RW = P.rows_per_tile, RB = P.row_bytes, G = P.lanes;
-    const uint32_t n_tiles = (P.n_out + RW - 1) / RW;
-    const uint32_t stride = P.wg_count * (kThreads / 64);
+    const uint32_t n_waves = P.wg_count * kSWaves;
+    const uint32_t wl = (blockIdx.x - P.wg_begin) * kSWaves + wave;
+    const uint32_t r_begin = (uint32_t)((uint64_t)P.n_out * wl / n_waves);
+    const uint32_t r_end = (uint32_t)((uint64_t)P.n_out * (wl + 1) / n_waves);
+    const uint32_t n_t = (r_end - r_begin + RW - 1) / RW;
 
-    u32x4 chunk[NC];
-    auto load_tile = [&](uint32_t tile) {
-        const uint32_t start = tile * RW * RB;
-        const uint32_t rows = P.n_out - tile * RW < RW ? P.n_out - tile * RW : RW;
-        const uint32_t a0 = start & ~15u;
+    u32x4 chunk[kChunks];
+    auto load_tile = [&](uint32_t t) {
+        const uint32_t r0 = r_begin + t * RW;
+        const uint32_t rows = r_end - r0 < RW ? r_end - r0 : RW;
+        const uint32_t start = r0 * RB, a0 = start & ~15u;
         const uint32_t nch = (rows * RB + (start - a0) + 15) / 16;
 #pragma unroll
-        for (int i = 0; i < NC; ++i) {
+        for (uint32_t i = 0; i < kChunks; ++i) {
             const uint32_t c = lane + 64 * i;
-            chunk[i] = c < nch ? ah_ld128(rs, a0 + 16 * c) : (u32x4){0u, 0u, 0u, 0u};
+            chunk[i] = ah_ld128(rs, c < nch ? a0 + 16 * c : kOob);
         }
     };
 
-    uint32_t tile = wg_local * (kThreads / 64) + wave;
-    if (tile < n_tiles) load_tile(tile);
-    load_activation(P, kpad, A, status);
+    // activation: the first pass is loaded before the weight stream starts
+    const uint32_t nbp = kpad / 32, QB = kSThreads / 4;
+    const uint32_t passes = (nbp + QB - 1) / QB;
+    const ActRsrc xr = act_rsrc(P.x, P.scales, P.src, P.n_in);
+    const QuadIn x0 = quad_load_row(xr, P.src, P.n_in, threadIdx.x / 4);
+    __asm__ volatile("" ::: "memory");
+    if (n_t) load_tile(0);
+    __builtin_amdgcn_sched_barrier(0);  // nothing that reads the activation moves above the stream
+    {
+        const uint32_t b = threadIdx.x / 4;
+        const QuadOut o = quad_quant(x0, P.src, b, status, 0);
+        if (b < nbp) store_quad(A, b, o);
+    }
+    for (uint32_t p = 1; p < passes; ++p) {
+        const uint32_t b = p * QB + threadIdx.x / 4;
+        const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, 0);
+        if (b < nbp) store_quad(A, b, o);
+    }
     __syncthreads();
 
     const uint32_t r = lane / G, g = lane & (G - 1);
-    for (; tile < n_tiles; tile += stride) {
+    for (uint32_t t = 0; t < n_t; ++t) {
 #pragma unroll
-        for (int i = 0; i < NC; ++i) reinterpret_cast<u32x4 *>(tl)[lane + 64 * i] = chunk[i];
-        const uint32_t next = tile + stride;
-        if (next < n_tiles) load_tile(next);
+        for (uint32_t i = 0; i < kChunks; ++i) reinterpret_cast<u32x4 *>(tl)[lane + 64 * i] = chunk[i];
+        if (t + 1 < n_t) load_tile(t + 1);
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS stores have landed
         __builtin_amdgcn_wave_barrier();
-        const uint32_t toff = (tile * RW * RB) & 15u;
-        const uint32_t row = tile * RW + r;
+        const uint32_t r0 = r_begin + t * RW;
+        const uint32_t toff = (r0 * RB) & 15u;
+        const uint32_t row = r0 + r;
         float acc = 0.0f;
-        if (r < RW && row < P.n_out) {
+        if (r < RW && row < r_end) {
             for (uint32_t u = g; u < U; u += G)
                 acc += comp_unit<TYPE>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
         }
         acc = group_sum(acc, G);
-        if (g == 0 && r < RW && row < P.n_out) P.y[row] = acc;
-        __builtin_amdgcn_wave_barrier();  // all lanes are done reading the slice before it is refilled
+        if (g == 0 && r < RW && row < r_end) P.y[row] = acc;
+        __builtin_amdgcn_wave_barrier();  // all lanes are done reading the slot before it is refilled
     }
 }
 
-// Wave-tile geometry for a row of RB bytes and U units: chunks per lane (NC KB per wave tile),
-// whole rows per tile, lanes per row.  Returns false when a row does not fit 16 KB (the
-// workgroup-tile kernel then serves the part).
-bool ah_gemv_wave_geometry(uint32_t row_bytes, uint32_t units, uint32_t &nc, uint32_t &rows, uint32_t &lanes) {
-    if (row_bytes + 16 > 16 * 1024) return false;
-    nc = row_bytes + 16 <= 8 * 1024 ? 8u : 16u;
-    uint32_t fit = (nc * 1024 - 16) / (row_bytes ? row_bytes : 1);
-    if (fit < 1) fit = 1;
+// Stream geometry for a row of RB bytes and U units: whole rows per tile and lanes per row.
+// Returns false when a row does not fit one tile (the workgroup-tile kernel then serves the part).
+bool ah_gemv_stream_geometry(uint32_t row_bytes, uint32_t units, uint32_t &rows, uint32_t &lanes) {
+    if (row_bytes == 0 || row_bytes + 16 > kStreamTile) return false;
+    const uint32_t fit = (kStreamTile - 16) / row_bytes;
     uint32_t G = 64;
     while (G > 1 && G * fit > 64) G >>= 1;      // lanes so that the tile's rows cover the wave
     uint32_t cap = 1;
@@ -582,29 +706,50 @@ bool ah_gemv_wave_geometry(uint32_t row_bytes, uint32_t units, uint32_t &nc, uin
     return true;
 }
 
-size_t ah_gemv_wave_lds_bytes(uint32_t nc, uint32_t kpad_max) {
+size_t ah_gemv_stream_lds_bytes(uint32_t kpad_max) {
     return kpad_max + kpad_max / 16 + (size_t)kpad_max / 32 * 8 + (size_t)kpad_max / 16 * 4 +
-           4 * ((size_t)nc * 1024 + kWaveSlack);
+           (size_t)kSWaves * kSlotBytes;
 }
 
-hipError_t ah_launch_gemv_wave(uint32_t type, uint32_t nc, const GemvPart &single, const GemvPart *d_parts,
-                               const uint32_t *d_wg_part, uint32_t grid, uint32_t kpad_max,
-                               unsigned long long *status, hipStream_t stream) {
-    const size_t lds = ah_gemv_wave_lds_bytes(nc, kpad_max);
-#define AH_WLAUNCH(T)                                                                              \
-    if (nc <= 8)                                                                                   \
-        hipLaunchKernelGGL((gemv_wave_kernel<T, 8>), dim3(grid), dim3(kThreads), lds, stream,      \
-                           single, d_parts, d_wg_part, kpad_max, status);                         \
-    else                                                                                           \
-        hipLaunchKernelGGL((gemv_wave_kernel<T, 16>), dim3(grid), dim3(kThreads), lds, stream,     \
-                           single, d_parts, d_wg_part, kpad_max, status);
+uint32_t ah_gemv_stream_threads() { return kSThreads; }
+
+static const void *stream_fn(uint32_t type) {
     switch (type) {
-    case AH_GGML_Q8_0: AH_WLAUNCH(AH_GGML_Q8_0) break;
-    case AH_GGML_Q4_K: AH_WLAUNCH(AH_GGML_Q4_K) break;
-    case AH_GGML_Q6_K: AH_WLAUNCH(AH_GGML_Q6_K) break;
-    default: return hipErrorInvalidValue;
+    case AH_GGML_Q8_0: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q8_0>);
+    case AH_GGML_Q4_K: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q4_K>);
+    case AH_GGML_Q6_K: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q6_K>);
+    default: return nullptr;
     }
-#undef AH_WLAUNCH
+}
+
+// Workgroups of the streaming kernel that fit one CU at once with `lds` bytes of LDS each.
+int ah_gemv_stream_occupancy(uint32_t type, size_t lds) {
+    const void *fn = stream_fn(type);
+    int n = 0;
+    if (!fn || hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kSThreads, lds) != hipSuccess) return 0;
+    return n;
+}
+
+hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const GemvPart *d_parts,
+                                 const uint32_t *d_wg_part, uint32_t grid, uint32_t kpad_max,
+                                 unsigned long long *status, hipStream_t stream) {
+    const size_t lds = ah_gemv_stream_lds_bytes(kpad_max);
+    switch (type) {
+    case AH_GGML_Q8_0:
+        hipLaunchKernelGGL(gemv_stream_kernel<AH_GGML_Q8_0>, dim3(grid), dim3(kSThreads), lds, stream, single,
+                           d_parts, d_wg_part, kpad_max, status);
+        break;
+    case AH_GGML_Q4_K:
+        hipLaunchKernelGGL(gemv_stream_kernel<AH_GGML_Q4_K>, dim3(grid), dim3(kSThreads), lds, stream, single,
+                           d_parts, d_wg_part, kpad_max, status);
+        break;
+    case AH_GGML_Q6_K:
+        hipLaunchKernelGGL(gemv_stream_kernel<AH_GGML_Q6_K>, dim3(grid), dim3(kSThreads), lds, stream, single,
+                           d_parts, d_wg_part, kpad_max, status);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
@@ -657,13 +802,8 @@ hipError_t ah_gemv_init_attrs() {
     AH_ATTR(AH_GGML_Q4_K, 4) AH_ATTR(AH_GGML_Q4_K, 8) AH_ATTR(AH_GGML_Q4_K, 12)
     AH_ATTR(AH_GGML_Q6_K, 4) AH_ATTR(AH_GGML_Q6_K, 8) AH_ATTR(AH_GGML_Q6_K, 12)
 #undef AH_ATTR
-#define AH_WATTR(T, N)                                                                             \
-    if (e == hipSuccess)                                                                           \
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_wave_kernel<T, N>),           \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, lim);
-    AH_WATTR(AH_GGML_Q8_0, 8) AH_WATTR(AH_GGML_Q8_0, 16) AH_WATTR(AH_GGML_Q4_K, 8)
-    AH_WATTR(AH_GGML_Q4_K, 16) AH_WATTR(AH_GGML_Q6_K, 8) AH_WATTR(AH_GGML_Q6_K, 16)
-#undef AH_WATTR
+    for (uint32_t t : {AH_GGML_Q8_0, AH_GGML_Q4_K, AH_GGML_Q6_K})
+        if (e == hipSuccess) e = hipFuncSetAttribute(stream_fn(t), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     return e;
 }
 

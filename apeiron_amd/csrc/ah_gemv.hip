@@ -237,15 +237,14 @@ AH_DEV QuadOut quad_quant(const QuadIn &in, uint32_t src, uint32_t b, unsigned l
         if (e >= 0 && e < 63) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                uint64_t m;
-                bool n;
+                int c;
                 if (src == AH_SRC_F32) {
-                    (void)ah_to_q32_mag(bits[i], m, n);  // padded lanes are +0: code 0
+                    c = ah_act_code_f32(bits[i], e, bad);  // padded lanes are +0: code 0
                 } else {
-                    n = v64[i] < 0;
-                    m = n ? 0ull - (uint64_t)v64[i] : (uint64_t)v64[i];
+                    const bool n = v64[i] < 0;
+                    const uint64_t m = n ? 0ull - (uint64_t)v64[i] : (uint64_t)v64[i];
+                    c = ah_act_code(m, n, e, bad);
                 }
-                const int c = ah_act_code(m, n, e, bad);
                 if (i < 4)
                     o.c0 |= (uint32_t)(c & 0xff) << (8 * i);
                 else
@@ -503,7 +502,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
             const uint32_t c = threadIdx.x + kThreads * i;
-            chunk[i] = c < nch ? ah_ld128(rs, a0 + 16 * c) : (u32x4){0u, 0u, 0u, 0u};
+            chunk[i] = c < nch ? ah_ld128_nt(rs, a0 + 16 * c) : (u32x4){0u, 0u, 0u, 0u};
         }
     };
 
@@ -512,12 +511,12 @@ __global__ void __launch_bounds__(kThreads)
     load_activation(P, kpad, A, status);
 
     for (; tile < n_tiles; tile += P.wg_count) {
-        __syncthreads();  // the previous tile is consumed; the activation is in LDS
+        ah_lds_barrier();  // the previous tile is consumed; the activation is in LDS
 #pragma unroll
         for (int i = 0; i < NC; ++i) reinterpret_cast<u32x4 *>(tl)[threadIdx.x + kThreads * i] = chunk[i];
         const uint32_t next = tile + P.wg_count;
         if (next < n_tiles) load_tile(next);
-        __syncthreads();
+        ah_lds_barrier();
         const uint32_t toff = (tile * R * RB) & 15u;
         for (uint32_t f = threadIdx.x; f < TU; f += kThreads) {
             const uint32_t r = f / U, u = f - r * U, row = tile * R + r;
@@ -525,7 +524,7 @@ __global__ void __launch_bounds__(kThreads)
             if (row < P.n_out) v = comp_unit<TYPE>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
             A.red[f] = v;
         }
-        __syncthreads();
+        ah_lds_barrier();
         // row sums in fixed order: G lanes per row, G a power of two with R*G <= 256
         uint32_t G = 64;
         while (G > 1 && R * G > kThreads) G >>= 1;
@@ -618,13 +617,19 @@ constexpr uint32_t kStreamTile = kChunks * 1024;   // bytes per tile
 constexpr uint32_t kSlotBytes = kStreamTile + 32;  // + what realigned unit reads touch past a tile
 constexpr uint32_t kOob = 0xFFFFFFF0u;             // past any payload (payloads stay below 4 GiB - 256)
 
-template <int TYPE>
+// PLAN: the workgroup's part comes from a plan's table (else the launch argument); either way the
+// descriptor is read with scalar loads, which do not queue behind the vector memory stream.
+template <int TYPE, bool PLAN>
 __global__ void __launch_bounds__(kSThreads)
     gemv_stream_kernel(GemvPart single, const GemvPart *__restrict__ parts,
                        const uint32_t *__restrict__ wg_part, uint32_t kpad_max,
                        unsigned long long *status) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const GemvPart P = load_part(single, parts, wg_part);
+    GemvPart P;
+    if constexpr (PLAN)
+        P = parts[__builtin_amdgcn_readfirstlane(wg_part[blockIdx.x])];
+    else
+        P = single;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t kpad = (P.n_in + 255) / 256 * 256;
     const ActLds A = carve(smem, kpad_max);
@@ -637,57 +642,78 @@ __global__ void __launch_bounds__(kSThreads)
     const uint32_t r_end = (uint32_t)((uint64_t)P.n_out * (wl + 1) / n_waves);
     const uint32_t n_t = (r_end - r_begin + RW - 1) / RW;
 
+    // Tile t's loads.  Issued unconditionally (a tile past the wave's rows loads nothing) so that
+    // the compiler's load counting sees the same loads on every path and never waits for one that
+    // is still streaming when it only needs an older one.
     u32x4 chunk[kChunks];
     auto load_tile = [&](uint32_t t) {
         const uint32_t r0 = r_begin + t * RW;
-        const uint32_t rows = r_end - r0 < RW ? r_end - r0 : RW;
-        const uint32_t start = r0 * RB, a0 = start & ~15u;
-        const uint32_t nch = (rows * RB + (start - a0) + 15) / 16;
+        const uint32_t rows = t >= n_t ? 0u : (r_end - r0 < RW ? r_end - r0 : RW);
+        const uint32_t start = rows ? r0 * RB : 0u, a0 = start & ~15u;
+        const uint32_t nch = rows ? (rows * RB + (start - a0) + 15) / 16 : 0u;
 #pragma unroll
         for (uint32_t i = 0; i < kChunks; ++i) {
             const uint32_t c = lane + 64 * i;
-            chunk[i] = ah_ld128(rs, c < nch ? a0 + 16 * c : kOob);
+            chunk[i] = ah_ld128_nt(rs, c < nch ? a0 + 16 * c : kOob);
         }
     };
 
-    // activation: the first pass is loaded before the weight stream starts
+    // Prologue.  Every wave's activation loads go out before any tile load of the workgroup (the
+    // barrier orders issue, not completion), tile 0 follows at once, and the quantizer runs from
+    // registers while tile 0 streams in; then tile 0 is staged and tile 1 requested before the
+    // barrier that publishes the activation, so the stream does not stall on the prologue.
     const uint32_t nbp = kpad / 32, QB = kSThreads / 4;
     const uint32_t passes = (nbp + QB - 1) / QB;
     const ActRsrc xr = act_rsrc(P.x, P.scales, P.src, P.n_in);
     const QuadIn x0 = quad_load_row(xr, P.src, P.n_in, threadIdx.x / 4);
-    __asm__ volatile("" ::: "memory");
-    if (n_t) load_tile(0);
-    __builtin_amdgcn_sched_barrier(0);  // nothing that reads the activation moves above the stream
-    {
-        const uint32_t b = threadIdx.x / 4;
-        const QuadOut o = quad_quant(x0, P.src, b, status, 0);
-        if (b < nbp) store_quad(A, b, o);
-    }
-    for (uint32_t p = 1; p < passes; ++p) {
+    const QuadIn x1 = quad_load_row(xr, P.src, P.n_in, QB + threadIdx.x / 4);  // past the row: zeros
+    ah_lds_barrier();
+    load_tile(0);
+    // a wave whose 16 blocks all lie past the activation has nothing to quantize
+#pragma unroll
+    for (uint32_t p = 0; p < 2; ++p) {
         const uint32_t b = p * QB + threadIdx.x / 4;
+        if (p < passes && p * QB + wave * 16 < nbp) {
+            const QuadOut o = quad_quant(p ? x1 : x0, P.src, b, status, 0);
+            if (b < nbp) store_quad(A, b, o);
+        }
+    }
+    for (uint32_t p = 2; p < passes; ++p) {  // activations past 2 * 128 blocks (K > 8192)
+        const uint32_t b = p * QB + threadIdx.x / 4;
+        if (p * QB + wave * 16 >= nbp) break;
         const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, 0);
         if (b < nbp) store_quad(A, b, o);
     }
-    __syncthreads();
-
-    const uint32_t r = lane / G, g = lane & (G - 1);
-    for (uint32_t t = 0; t < n_t; ++t) {
+    auto stage = [&](uint32_t t) {  // tile t (in registers) to the slot; request tile t + 1
 #pragma unroll
         for (uint32_t i = 0; i < kChunks; ++i) reinterpret_cast<u32x4 *>(tl)[lane + 64 * i] = chunk[i];
-        if (t + 1 < n_t) load_tile(t + 1);
+        load_tile(t + 1);
+    };
+    stage(0);  // unconditional, like every tile load: a wave without rows stages zeros
+    ah_lds_barrier();
+
+    // Row sums leave through a buffer store that every lane issues (lanes that own no row store
+    // out of range, which writes nothing): a store behind a branch would make the compiler wait for
+    // its completion before the next tile is staged.
+    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(P.y, P.n_out * 4u);
+    const uint32_t r = lane / G, g = lane & (G - 1);
+    for (uint32_t t = 0; t < n_t; ++t) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS stores have landed
         __builtin_amdgcn_wave_barrier();
         const uint32_t r0 = r_begin + t * RW;
         const uint32_t toff = (r0 * RB) & 15u;
         const uint32_t row = r0 + r;
+        const bool owns = r < RW && row < r_end;
         float acc = 0.0f;
-        if (r < RW && row < r_end) {
+        if (owns) {
             for (uint32_t u = g; u < U; u += G)
                 acc += comp_unit<TYPE>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
         }
         acc = group_sum(acc, G);
-        if (g == 0 && r < RW && row < r_end) P.y[row] = acc;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), ry,
+                                              (g == 0 && owns) ? row * 4u : kOob, 0, 0);
         __builtin_amdgcn_wave_barrier();  // all lanes are done reading the slot before it is refilled
+        stage(t + 1);
     }
 }
 
@@ -713,43 +739,45 @@ size_t ah_gemv_stream_lds_bytes(uint32_t kpad_max) {
 
 uint32_t ah_gemv_stream_threads() { return kSThreads; }
 
-static const void *stream_fn(uint32_t type) {
+static const void *stream_fn(uint32_t type, bool plan) {
+#define AH_SFN(T) return plan ? reinterpret_cast<const void *>(&gemv_stream_kernel<T, true>)            \
+                              : reinterpret_cast<const void *>(&gemv_stream_kernel<T, false>);
     switch (type) {
-    case AH_GGML_Q8_0: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q8_0>);
-    case AH_GGML_Q4_K: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q4_K>);
-    case AH_GGML_Q6_K: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q6_K>);
+    case AH_GGML_Q8_0: AH_SFN(AH_GGML_Q8_0)
+    case AH_GGML_Q4_K: AH_SFN(AH_GGML_Q4_K)
+    case AH_GGML_Q6_K: AH_SFN(AH_GGML_Q6_K)
     default: return nullptr;
     }
+#undef AH_SFN
 }
 
 // Workgroups of the streaming kernel that fit one CU at once with `lds` bytes of LDS each.
 int ah_gemv_stream_occupancy(uint32_t type, size_t lds) {
-    const void *fn = stream_fn(type);
-    int n = 0;
-    if (!fn || hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kSThreads, lds) != hipSuccess) return 0;
-    return n;
+    int n0 = 0, n1 = 0;
+    const void *f0 = stream_fn(type, false), *f1 = stream_fn(type, true);
+    if (!f0 || hipOccupancyMaxActiveBlocksPerMultiprocessor(&n0, f0, kSThreads, lds) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n1, f1, kSThreads, lds) != hipSuccess) return 0;
+    return n0 < n1 ? n0 : n1;
 }
 
 hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const GemvPart *d_parts,
                                  const uint32_t *d_wg_part, uint32_t grid, uint32_t kpad_max,
                                  unsigned long long *status, hipStream_t stream) {
     const size_t lds = ah_gemv_stream_lds_bytes(kpad_max);
+#define AH_SLAUNCH(T)                                                                              \
+    if (d_parts)                                                                                   \
+        hipLaunchKernelGGL((gemv_stream_kernel<T, true>), dim3(grid), dim3(kSThreads), lds, stream, \
+                           single, d_parts, d_wg_part, kpad_max, status);                         \
+    else                                                                                           \
+        hipLaunchKernelGGL((gemv_stream_kernel<T, false>), dim3(grid), dim3(kSThreads), lds,       \
+                           stream, single, d_parts, d_wg_part, kpad_max, status);
     switch (type) {
-    case AH_GGML_Q8_0:
-        hipLaunchKernelGGL(gemv_stream_kernel<AH_GGML_Q8_0>, dim3(grid), dim3(kSThreads), lds, stream, single,
-                           d_parts, d_wg_part, kpad_max, status);
-        break;
-    case AH_GGML_Q4_K:
-        hipLaunchKernelGGL(gemv_stream_kernel<AH_GGML_Q4_K>, dim3(grid), dim3(kSThreads), lds, stream, single,
-                           d_parts, d_wg_part, kpad_max, status);
-        break;
-    case AH_GGML_Q6_K:
-        hipLaunchKernelGGL(gemv_stream_kernel<AH_GGML_Q6_K>, dim3(grid), dim3(kSThreads), lds, stream, single,
-                           d_parts, d_wg_part, kpad_max, status);
-        break;
-    default:
-        return hipErrorInvalidValue;
+    case AH_GGML_Q8_0: AH_SLAUNCH(AH_GGML_Q8_0) break;
+    case AH_GGML_Q4_K: AH_SLAUNCH(AH_GGML_Q4_K) break;
+    case AH_GGML_Q6_K: AH_SLAUNCH(AH_GGML_Q6_K) break;
+    default: return hipErrorInvalidValue;
     }
+#undef AH_SLAUNCH
     return hipGetLastError();
 }
 
@@ -803,7 +831,8 @@ hipError_t ah_gemv_init_attrs() {
     AH_ATTR(AH_GGML_Q6_K, 4) AH_ATTR(AH_GGML_Q6_K, 8) AH_ATTR(AH_GGML_Q6_K, 12)
 #undef AH_ATTR
     for (uint32_t t : {AH_GGML_Q8_0, AH_GGML_Q4_K, AH_GGML_Q6_K})
-        if (e == hipSuccess) e = hipFuncSetAttribute(stream_fn(t), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+        for (bool plan : {false, true})
+            if (e == hipSuccess) e = hipFuncSetAttribute(stream_fn(t, plan), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     return e;
 }
 

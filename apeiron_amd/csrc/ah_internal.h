@@ -41,9 +41,20 @@ AH_DEV __amdgpu_buffer_rsrc_t ah_rsrc(const void *p, uint32_t bytes) {
 AH_DEV u32x4 ah_ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
+// Streamed weight bytes: read once per launch, so the load carries the non-temporal hint (nt),
+// which keeps them from displacing cached lines and measurably raises the streaming rate.
+AH_DEV u32x4 ah_ld128_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2));
+}
 AH_DEV uint32_t ah_ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
+
+// Workgroup barrier for LDS traffic only: this wave's LDS operations are complete before it
+// arrives, and global loads stay in flight (__syncthreads also waits for every outstanding global
+// load, which would drain a prefetch).  The memory clobber keeps the compiler from moving memory
+// operations across it.
+AH_DEV void ah_lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // ---- exact integer helpers ----
 
@@ -98,6 +109,37 @@ AH_DEV int ah_act_code(uint64_t mag, bool neg, int e, bool &bad) {
     // c <= 127 by the choice of S.  The product c*2^e must fit: positive < 2^63, negative <= 2^63.
     if (e >= 56) {
         uint64_t lim = 1ull << (63 - e);
+        if (neg ? c > lim : c >= lim) bad = true;
+    }
+    return neg ? -(int)c : (int)c;
+}
+
+// The quant_act code of an f32 element under S = 2^e (0 <= e <= 62) in 32-bit arithmetic, equal
+// to ah_act_code(ah_to_q32_mag(bits), e).  With |x| = m * 2^(ee - 150) (m the 24-bit significand,
+// ee >= 1 the biased exponent, subnormals taking ee = 1), |x| * 2^32 = m * 2^(ee - 118).
+// rhu(v, k) = ((v >> (k - 1)) + 1) >> 1 rounds v / 2^k half up (k >= 1), which is to_q32's and
+// the code's rounding on magnitudes.  For ee >= 118, to_q32 is exact and the code is one rounding
+// of m by sh = e + 118 - ee (sh >= 17 in any block whose scale is 2^e: m >= 2^23, code <= 127);
+// for ee < 118, to_q32 rounds m by 2^(118 - ee) first and the code rounds that by 2^e.  Shift
+// counts are clamped at 25: m < 2^24 makes every larger shift give the same 0.
+AH_DEV int ah_act_code_f32(uint32_t bits, int e, bool &bad) {
+    const uint32_t eb = (bits >> 23) & 0xffu;
+    const uint32_t ee = eb ? eb : 1u;
+    const uint32_t m = (bits & 0x7fffffu) | (eb ? 0x800000u : 0u);
+    uint32_t c;
+    if (ee >= 118u) {
+        const int sh = e + 118 - (int)ee;
+        const uint32_t k = sh < 1 ? 0u : (sh - 1 > 25 ? 25u : (uint32_t)(sh - 1));
+        c = ((m >> k) + 1u) >> 1;
+    } else {
+        const uint32_t k1 = 117u - ee > 25u ? 25u : 117u - ee;
+        const uint32_t mag = ((m >> k1) + 1u) >> 1;
+        const uint32_t k = e < 1 ? 0u : (e - 1 > 25 ? 25u : (uint32_t)(e - 1));
+        c = e == 0 ? mag : ((mag >> k) + 1u) >> 1;
+    }
+    const bool neg = (bits >> 31) != 0;
+    if (e >= 56) {
+        const uint32_t lim = 1u << (63 - e);
         if (neg ? c > lim : c >= lim) bad = true;
     }
     return neg ? -(int)c : (int)c;

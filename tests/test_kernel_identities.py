@@ -51,3 +51,55 @@ def test_gemm_operands_exact_in_f16():
     lo = X - hi
     assert ((hi.astype(np.float16).astype(np.int64) + lo.astype(np.float16).astype(np.int64)) == X).all()
     assert lo.min() >= 0 and lo.max() <= 63
+
+
+def act_code_f32_32bit(bits: int, e: int) -> int:
+    """The kernels' 32-bit per-element code (ah_act_code_f32), restated on Python ints."""
+    eb = (bits >> 23) & 0xFF
+    ee = eb if eb else 1
+    m = (bits & 0x7FFFFF) | (0x800000 if eb else 0)
+    if ee >= 118:
+        sh = e + 118 - ee
+        k = 0 if sh < 1 else min(sh - 1, 25)
+        c = ((m >> k) + 1) >> 1
+    else:
+        k1 = min(117 - ee, 25)
+        mag = ((m >> k1) + 1) >> 1
+        k = 0 if e < 1 else min(e - 1, 25)
+        c = mag if e == 0 else ((mag >> k) + 1) >> 1
+    return -c if bits >> 31 else c
+
+
+def test_act_code_f32_32bit_matches_quant_act():
+    """Blocks of 32 f32 values: element 0 sets the block's scale, the rest sweep every exponent the
+    scale admits (tiny values that round twice, half-way points, subnormals, signed zeros); the
+    32-bit code must equal quant_act_f32's (kern/quant.rs via the oracle) for every element."""
+    rng = np.random.default_rng(17)
+    blocks = []
+    for top in list(range(-60, 31)) + [-126, -149]:
+        amax = np.float32(np.ldexp(1.0 + rng.random(), top)) if top > -149 else np.float32(np.ldexp(1.0, -149))
+        for _ in range(6):
+            rel = rng.integers(-40, 1, size=31)
+            body = np.ldexp(rng.random(31) + 0.5, top + rel).astype(np.float32)
+            body *= np.where(rng.random(31) < 0.5, -1, 1).astype(np.float32)
+            # exact half-way points of the code rounding and of to_q32's rounding
+            body[0] = np.float32(np.ldexp(1.5, top - 6))
+            body[1] = np.float32(np.ldexp(0.5, -32))
+            body[2] = np.float32(-np.ldexp(1.5, -33))
+            body[3] = np.float32(0.0)
+            body[4] = np.float32(-0.0)
+            body[5] = np.float32(np.ldexp(1.0, -149))
+            blocks.append(np.concatenate([[amax], body]).astype(np.float32))
+    x = np.concatenate(blocks)
+    st, codes, scales = oracle.quant_act_f32(x)
+    assert st == 0
+    bits = x.view(np.uint32)
+    n_checked = 0
+    for i in range(x.shape[0]):
+        s = int(scales[i // 32])
+        if s == 0:
+            continue
+        e = s.bit_length() - 1
+        assert act_code_f32_32bit(int(bits[i]), e) == int(codes[i]), (i, float(x[i]), e)
+        n_checked += 1
+    assert n_checked > 15000

@@ -178,8 +178,11 @@ uint64_t resident_wgs(const ah_ctx *ctx, uint32_t type, bool stream, uint32_t kp
 }
 
 // Deal `target` workgroups over the parts: one each, then one at a time to the part with the most
-// weight bytes per workgroup, never past one tile per wave (streaming) or per workgroup.  Returns
-// the grid size (wg_begin / wg_count filled), or 0 when the host is out of memory.
+// tiles per workgroup, never past one tile per wave (streaming) or per workgroup.  A tile is one
+// step of a wave's pipeline whatever its byte count (its arithmetic is one unit per lane), so
+// tiles, not bytes, measure a part's time: rows that fit a tile twice (e.g. K = 4864 Q4_K rows
+// in 8 KB tiles) make more, smaller tiles per byte.  Returns the grid size (wg_begin / wg_count
+// filled), or 0 when the host is out of memory.
 uint32_t deal_wgs(GemvPart *parts, size_t n, uint64_t target, bool stream) {
     struct Item {
         double load;
@@ -188,6 +191,9 @@ uint32_t deal_wgs(GemvPart *parts, size_t n, uint64_t target, bool stream) {
     Item *heap = static_cast<Item *>(std::malloc(n * sizeof(Item)));
     if (!heap) return 0;
     size_t hn = 0;
+    auto tiles_of = [](const GemvPart &P) -> double {
+        return (double)((P.n_out + P.rows_per_tile - 1) / P.rows_per_tile);
+    };
     auto cap_of = [&](const GemvPart &P) -> uint32_t {
         const uint32_t tiles = (P.n_out + P.rows_per_tile - 1) / P.rows_per_tile;
         const uint32_t wv = ah_gemv_stream_threads() / 64;
@@ -219,14 +225,14 @@ uint32_t deal_wgs(GemvPart *parts, size_t n, uint64_t target, bool stream) {
     uint64_t used = n;
     for (size_t i = 0; i < n; ++i) {
         parts[i].wg_count = 1;
-        if (cap_of(parts[i]) > 1) push({(double)parts[i].w_bytes, (uint32_t)i});
+        if (cap_of(parts[i]) > 1) push({tiles_of(parts[i]), (uint32_t)i});
     }
     while (used < target && hn) {
         const Item it = pop();
         GemvPart &P = parts[it.i];
         ++P.wg_count;
         ++used;
-        if (P.wg_count < cap_of(P)) push({(double)P.w_bytes / P.wg_count, it.i});
+        if (P.wg_count < cap_of(P)) push({tiles_of(P) / P.wg_count, it.i});
     }
     std::free(heap);
     uint32_t wg = 0;

@@ -247,6 +247,10 @@ int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
                     const int64_t *scales, float *y, int32_t *dots, void *stream) {
     if (!ctx || !w || (!x && w->n_in) || (!y && w->n_out)) return AH_ERR_INVALID_ARG;
     if (src == AH_SRC_CODES && !scales && w->n_in) return AH_ERR_INVALID_ARG;
+    // the kernels read codes a dword at a time, f32 / Q32.32 values at their natural alignment
+    const uintptr_t align = src == AH_SRC_CODES ? 4 : src == AH_SRC_F32 ? 4 : 8;
+    if (reinterpret_cast<uintptr_t>(x) % align || (scales && reinterpret_cast<uintptr_t>(scales) % 8))
+        return AH_ERR_INVALID_ARG;
     if (w->n_out == 0) return AH_OK;
     bool st = false;
     GemvPart P = make_part(w, src, x, scales, y, dots, st);
@@ -551,7 +555,8 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
     uint32_t kpad_max = 0, nc = 4;
     bool all_stream = true;
     for (size_t i = 0; i < n_parts; ++i) {
-        if (!w[i] || w[i]->type != type || !d_x[i] || !d_y[i] || w[i]->n_out == 0) {
+        if (!w[i] || w[i]->type != type || !d_x[i] || !d_y[i] || w[i]->n_out == 0 ||
+            reinterpret_cast<uintptr_t>(d_x[i]) % 4) {
             std::free(parts);
             return AH_ERR_INVALID_ARG;
         }

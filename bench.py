@@ -54,6 +54,22 @@ def proj_bytes(synth, t, n_out, n_in):
     return n_out * synth.needed_row_bytes(t, n_in) + 4 * n_in + 4 * n_out
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_stream_q4k_config1_token.md")
+
+
+def measured_traffic():
+    """HBM bytes per token-plan launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+    (copy-calibrated; the counters cannot be read from inside this process), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -180,8 +196,9 @@ def main() -> int:
         log(f"[bench] config1 {args.mode}: {ms_per_step * 1e3:.1f} us/step, {value:.0f} GB/s wall, "
             f"{step_bytes * args.steps / (ev_ms / 1e3) / 1e9:.0f} GB/s events")
 
-        # dominant kernel: the per-layer launch with the most time, HIP events per launch on the
-        # launch stream (eager launches, rotating layers)
+        # dominant kernel.  token: the plan launch, one per step, timed by the events over the timed
+        # region.  engine: the per-layer launch with the most time, HIP events around each launch
+        # on the launch stream (eager launches, rotating layers).
         kinds = {}
         if args.mode == "engine":
             kinds = {
@@ -193,10 +210,12 @@ def main() -> int:
                 "down": (lambda i, s: layers[i]["down"].gemv_f32_dev(ptr(xin["down"]), ptr(outs["down"]), s),
                          proj_bytes(synth, t, 896, 4864)),
             }
-        else:
-            kinds = {"token_group": (lambda i, s: plans[i % len(plans)].run(s), step_bytes)}
         per_kind = {}
-        reps = 64 if args.mode == "engine" else 32
+        if args.mode == "token":
+            # one launch per step: the timed region's events give the launch duration directly
+            us = ev_ms * 1e3 / args.steps
+            per_kind["token_plan"] = {"us": us, "bytes": step_bytes, "gbs": step_bytes / us / 1e3}
+        reps = 64
         for name, (fn, nbytes) in kinds.items():
             evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                    for _ in range(reps)]
@@ -210,9 +229,7 @@ def main() -> int:
             torch.cuda.synchronize()
             us = float(np.mean([a.elapsed_time(b) for a, b in evs[4:]])) * 1e3
             per_kind[name] = {"us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3}
-        dom = max(per_kind, key=lambda k: per_kind[k]["us"] * (1 if args.mode == "token" else 1))
-        if args.mode == "engine":
-            dom = max(per_kind, key=lambda k: per_kind[k]["us"] * (1 if k != "qkv" else 1))
+        dom = max(per_kind, key=lambda k: per_kind[k]["us"])
         d = per_kind[dom]
         result["gemv"] = {
             "mode": args.mode, "launches_per_step": launches_per_step,
@@ -223,9 +240,12 @@ def main() -> int:
         }
         result["_value"] = value
         result["_ms"] = ms_per_step
-        result["roofline"] = {"bound": "hbm", "kernel": f"gemv_kernel<Q4_K> ({dom})",
+        traffic = measured_traffic() if args.mode == "token" else None
+        result["roofline"] = {"bound": "hbm",
+                              "kernel": ("gemv_stream_kernel<Q4_K> (token plan: 168 projections per launch)"
+                                         if args.mode == "token" else f"gemv_stream_kernel<Q4_K> ({dom})"),
                               "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                              "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                              "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                               "bytes_per_launch": d["bytes"], "us_per_launch": round(d["us"], 3)}
 
     for p in plans:

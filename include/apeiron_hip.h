@@ -109,7 +109,8 @@ int32_t ah_quant_act_q32_dev(ah_ctx *ctx, const int64_t *d_x, size_t n_tok, size
 /* y[n_out] = W x with the quantizer fused into the kernel prologue. */
 int32_t ah_gemv_f32_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, float *d_y,
                         void *stream);
-/* y[n_out] = W x from pre-quantized codes[n_in] + scales[ceil(n_in/32)]. */
+/* y[n_out] = W x from pre-quantized codes[n_in] + scales[ceil(n_in/32)].  d_codes must be
+ * 4-byte aligned (the kernel reads codes a dword at a time; AH_ERR_INVALID_ARG otherwise). */
 int32_t ah_gemv_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
                        const int64_t *d_scales, float *d_y, void *stream);
 

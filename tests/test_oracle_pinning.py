@@ -197,9 +197,15 @@ def test_matvec_random_payloads_vs_bruteforce(t):
         assert st == 0 and y.tolist() == want, (t, rows, n_in)
         stf, yf = oracle.matvec_q8act_fast(t, raw, rows, n_in, codes, scales, 2)
         assert stf == 0 and yf.tolist() == want, (t, rows, n_in)
+        # the tolerance basis sum_i |w_i * xhat_i| (real units) against exact integers
+        sta, absdot = oracle.row_absdot(t, raw, rows, n_in, codes, scales)
+        assert sta == 0
         for r in range(rows):
             rb = synth.row_bytes(t, n_in)
             row = raw[r * rb:(r + 1) * rb]
+            wq = bf.weights_row(t, row.tobytes(), n_in)
+            exact = sum(abs(wi * xi) for wi, xi in zip(wq, xhat.tolist())) / 2.0 ** 64
+            assert abs(absdot[r] - exact) <= 1e-12 * exact, (t, rows, n_in, r)
             st, dots, xs = oracle.block_dots(t, row, n_in, codes)
             assert st == 0
             assert dots.tolist() == bf.block_dots(t, row.tobytes(), n_in, codes.tolist())

@@ -34,7 +34,7 @@ hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uin
                           const _Float16 *xh, const _Float16 *xmin, const float *tok_scale,
                           float *y, float *partials, uint32_t splits, hipStream_t stream);
 uint32_t ah_gemm_splits_used(uint32_t type, uint32_t n_in, uint32_t splits);
-hipError_t ah_launch_operand(const OperandArgs &o, hipStream_t stream);
+hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream);
 
 struct ah_ctx {
     int device = -1;
@@ -279,6 +279,8 @@ int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     if (!ctx || !w || !y || (!x && n_tok && w->n_in)) return AH_ERR_INVALID_ARG;
     if (n_tok == 0 || w->n_out == 0) return AH_OK;
     if (n_tok >= (1ull << 24)) return AH_ERR_INVALID_ARG;
+    // a workgroup's output rows (128 tokens x n_out f32) are addressed with 32-bit offsets
+    if (w->n_out > (0xFFFFFF00ull / (128 * 4))) return AH_ERR_INVALID_ARG;
     const uint32_t n_in = (uint32_t)w->n_in, n_out = (uint32_t)w->n_out, N = (uint32_t)n_tok;
     const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
     // split-K so the grid covers the chip about twice
@@ -290,8 +292,6 @@ int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     const uint32_t splits = ah_gemm_splits_used(w->type, n_in, want);
 
     size_t off = 0;
-    const size_t o_codes = off; off = align256(off + (src == AH_SRC_F32 ? (size_t)N * n_in : 0));
-    const size_t o_scales = off; off = align256(off + (src == AH_SRC_F32 ? (size_t)N * nb32 * 8 : 0));
     const size_t o_xh = off; off = align256(off + (size_t)N * kpad * 2);
     const size_t o_ts = off; off = align256(off + (size_t)N * 4);
     const size_t o_xmin = off; off = align256(off + (w->type == AH_GGML_Q4_K ? (size_t)N * nsb * 32 : 0));
@@ -299,10 +299,6 @@ int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     int32_t st = ensure_scratch(ctx, off);
     if (st) return st;
     uint8_t *S = static_cast<uint8_t *>(ctx->scratch);
-    int8_t *codes = src == AH_SRC_F32 ? reinterpret_cast<int8_t *>(S + o_codes)
-                                      : const_cast<int8_t *>(static_cast<const int8_t *>(x));
-    int64_t *scales = src == AH_SRC_F32 ? reinterpret_cast<int64_t *>(S + o_scales)
-                                        : const_cast<int64_t *>(scales_in);
     _Float16 *xh = reinterpret_cast<_Float16 *>(S + o_xh);
     float *ts = reinterpret_cast<float *>(S + o_ts);
     _Float16 *xmin = reinterpret_cast<_Float16 *>(S + o_xmin);
@@ -310,29 +306,20 @@ int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     hipStream_t s = pick(ctx, stream);
     AH_HIP(ctx, hipSetDevice(ctx->device));
 
-    if (src == AH_SRC_F32) {
-        QuantArgs q;
-        q.x = x;
-        q.codes = codes;
-        q.scales = scales;
-        q.n_tok = N;
-        q.n_in = n_in;
-        q.nb32 = nb32;
-        q.src = AH_SRC_F32;
-        q.status = ctx->d_status;
-        AH_HIP(ctx, ah_launch_quant(q, s));
-    }
+    // one pass from the input (or the codes) to the MFMA operand
     OperandArgs o;
-    o.codes = codes;
-    o.scales = scales;
+    o.x = x;
+    o.scales = scales_in;
     o.xh = xh;
     o.tok_scale = ts;
     o.xmin = w->type == AH_GGML_Q4_K ? xmin : nullptr;
+    o.status = ctx->d_status;
     o.n_tok = N;
     o.n_in = n_in;
     o.nb32 = nb32;
     o.kpad = kpad;
-    AH_HIP(ctx, ah_launch_operand(o, s));
+    o.src = src;
+    AH_HIP(ctx, ah_launch_gemm_operand(o, s));
     AH_HIP(ctx, ah_launch_gemm(w->type, w->d, (uint32_t)w->bytes, (uint32_t)w->row_bytes, n_out, n_in, N,
                                kpad, xh, xmin, ts, y, part, splits, s));
     return AH_OK;

@@ -84,26 +84,62 @@ struct GemmArgs {
     uint32_t splits;
 };
 
-// Stage the [kTN tokens][64 k] f16 activation slice at k0 into LDS (zeros past n_tok).
-AH_DEV void stage_act(const GemmArgs &a, uint32_t tok0, uint32_t k0, uint8_t *lds) {
-    for (int c = threadIdx.x; c < kTN * 8; c += kThreads) {
-        const int t = c >> 3, kc = c & 7;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (tok0 + t < a.n_tok)
-            v = *reinterpret_cast<const u32x4 *>(a.xh + (size_t)(tok0 + t) * a.kpad + k0 + 8 * kc);
-        *reinterpret_cast<u32x4 *>(lds + t * kPitch + 16 * kc) = v;
-    }
-}
-
 // The A operand of token tile `tile` for k-offset `kk` (elements) within the stage.
 AH_DEV f16x8 act_frag(const uint8_t *lds, int tile, int kk) {
     const int lane = threadIdx.x & 63;
     return *reinterpret_cast<const f16x8 *>(lds + (tile * 32 + (lane & 31)) * kPitch + 2 * kk);
 }
 
+constexpr uint32_t kOob = 0xFFFFFFF0u;  // a buffer offset past any operand: reads zeros
+
+// Weight bytes one lane needs for one 64-deep stage, fetched a stage ahead.
+//   Q8_0: per block, the lane half's 16 codes (the 4-aligned 20 bytes around them, realigned at
+//         use with a register shift -- no per-lane register indexing) and the dword holding d.
+//   Q4_K: the super-block header (d, dmin, 12 packed scales) and the lane half's 16 nibble bytes.
+struct WStage {
+    u32x4 a0, a1, b0, b1;
+    uint32_t a2, a3, b2, b3;
+};
+
+template <int TYPE>
+AH_DEV WStage fetch_w(__amdgpu_buffer_rsrc_t rs, uint32_t rbase, uint32_t st, uint32_t n_in, int h,
+                      bool live) {
+    WStage w;
+    const uint32_t k0 = st * kKS;
+    if constexpr (TYPE == AH_GGML_Q8_0) {
+        const uint32_t b = k0 / 32;
+        const uint32_t blk0 = rbase + 34 * b, blk1 = blk0 + 34;
+        const bool l0 = live && b * 32 < n_in, l1 = live && (b + 1) * 32 < n_in;
+        const uint32_t c0 = (blk0 + 2 + 16 * h) & ~3u, c1 = (blk1 + 2 + 16 * h) & ~3u;
+        w.a0 = ah_ld128_nt(rs, l0 ? c0 : kOob);
+        w.a2 = ah_ld32(rs, l0 ? c0 + 16 : kOob);
+        w.a3 = ah_ld32(rs, l0 ? (blk0 & ~3u) : kOob);
+        w.b0 = ah_ld128_nt(rs, l1 ? c1 : kOob);
+        w.b2 = ah_ld32(rs, l1 ? c1 + 16 : kOob);
+        w.b3 = ah_ld32(rs, l1 ? (blk1 & ~3u) : kOob);
+        w.a1 = w.b1 = (u32x4){0u, 0u, 0u, 0u};
+    } else if constexpr (TYPE == AH_GGML_Q4_K) {
+        const uint32_t sb = rbase + 144 * (k0 / 256), p = (k0 / 64) & 3;
+        w.a0 = ah_ld128(rs, live ? sb : kOob);
+        w.a1 = ah_ld128_nt(rs, live ? sb + 16 + 32 * p + 16 * h : kOob);
+        w.b0 = w.b1 = (u32x4){0u, 0u, 0u, 0u};
+        w.a2 = w.a3 = w.b2 = w.b3 = 0u;
+    } else {
+        w.a0 = w.a1 = w.b0 = w.b1 = (u32x4){0u, 0u, 0u, 0u};
+        w.a2 = w.a3 = w.b2 = w.b3 = 0u;
+    }
+    return w;
+}
+
+// Pipelined K loop.  The [kTN tokens][64 k] f16 activation slice of a stage is shared by the 4
+// waves through one of two LDS buffers: while the waves compute stage s from buffer s&1, every
+// thread holds stage s+1's slice in registers (loaded during stage s-1) and writes it to the other
+// buffer after its MFMAs, then requests stage s+2.  Weight bytes are fetched a stage ahead into
+// registers.  One LDS-only barrier per stage; every load is issued unconditionally (out-of-range
+// offsets read zeros), so the compiler's load counting never drains the prefetches.
 template <int TYPE>
 __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
-    __shared__ __align__(16) uint8_t lds[kTN * kPitch];
+    __shared__ __align__(16) uint8_t lds[2][kTN * kPitch];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 31, h = lane >> 5;
     const uint32_t row0 = blockIdx.x * 128 + wave * 32;
@@ -112,11 +148,32 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     const bool row_ok = my_row < a.n_out;
     const uint32_t rbase = (row_ok ? my_row : 0) * a.row_bytes;
     const __amdgpu_buffer_rsrc_t rs = ah_rsrc(a.w, a.w_bytes);
+    // this workgroup's token rows of the operand (at most kTN * 32768 * 2 bytes)
+    const uint32_t ntile = a.n_tok - tok0 < (uint32_t)kTN ? a.n_tok - tok0 : (uint32_t)kTN;
+    const __amdgpu_buffer_rsrc_t rx = ah_rsrc(a.xh + (size_t)tok0 * a.kpad, ntile * a.kpad * 2u);
 
     const uint32_t nstages = (a.n_in + kKS - 1) / kKS;
     const uint32_t st_begin = blockIdx.z * a.stages_per_split;
     uint32_t st_end = st_begin + a.stages_per_split;
     if (st_end > nstages) st_end = nstages;
+
+    u32x4 areg[kTN * 8 / kThreads];
+    auto act_load = [&](uint32_t st) {
+        const bool live = st < st_end;
+#pragma unroll
+        for (int i = 0; i < kTN * 8 / kThreads; ++i) {
+            const uint32_t c = threadIdx.x + kThreads * i, t = c >> 3, kc = c & 7;
+            const uint32_t off = (t * a.kpad + st * kKS + 8 * kc) * 2u;
+            areg[i] = ah_ld128(rx, live && t < ntile ? off : kOob);
+        }
+    };
+    auto act_store = [&](uint8_t *buf) {
+#pragma unroll
+        for (int i = 0; i < kTN * 8 / kThreads; ++i) {
+            const uint32_t c = threadIdx.x + kThreads * i, t = c >> 3, kc = c & 7;
+            *reinterpret_cast<u32x4 *>(buf + t * kPitch + 16 * kc) = areg[i];
+        }
+    };
 
     f32x16 acc[kNT];
 #pragma unroll
@@ -129,11 +186,16 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     uint32_t w6[54];                   // Q6_K super-block window
     uint32_t sh6 = 0;
 
+    act_load(st_begin);
+    act_store(lds[0]);
+    act_load(st_begin + 1);
+    WStage wc = fetch_w<TYPE>(rs, rbase, st_begin, a.n_in, h, st_begin < st_end);
+
     for (uint32_t st = st_begin; st < st_end; ++st) {
         const uint32_t k0 = st * kKS;
-        __syncthreads();
-        stage_act(a, tok0, k0, lds);
-        __syncthreads();
+        const uint8_t *cur = lds[(st - st_begin) & 1];
+        ah_lds_barrier();  // buffer `cur` is written; every wave is done with the other one
+        const WStage wn = fetch_w<TYPE>(rs, rbase, st + 1, a.n_in, h, st + 1 < st_end);
 
         if (TYPE == AH_GGML_Q8_0) {
             // two 32-blocks per stage; lane half h owns codes [16h, 16h+16) of each block
@@ -142,33 +204,29 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
                 const uint32_t b = k0 / 32 + bb;
                 if (b * 32 >= a.n_in) break;
                 const uint32_t blk = rbase + 34 * b;
-                const uint32_t base = blk & ~3u, sh = blk & 3u;
-                const u32x4 v0 = ah_ld128(rs, base), v1 = ah_ld128(rs, base + 16);
-                const uint32_t v2 = ah_ld32(rs, base + 32), v3 = ah_ld32(rs, base + 36);
-                const uint32_t w[10] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, v2, v3};
-                const float d = ah_f16_bits_to_f32(((sh ? (w[0] >> 16) : w[0]) & 0xffffu));
+                const uint32_t shc = (blk + 2 + 16 * h) & 3u;  // 0 or 2
+                const u32x4 v = bb ? wc.b0 : wc.a0;
+                const uint32_t w[5] = {v.x, v.y, v.z, v.w, bb ? wc.b2 : wc.a2};
+                const uint32_t dw = bb ? wc.b3 : wc.a3;
+                const float d = ah_f16_bits_to_f32((dw >> (8 * (blk & 3u))) & 0xffffu);
                 uint32_t c[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int wi = 4 * h + i;  // code dword index within the block
-                    c[i] = sh ? w[wi + 1] : ah_alignbyte(w[wi + 1], w[wi], 2);
-                }
+                for (int i = 0; i < 4; ++i) c[i] = ah_alignbyte(w[i + 1], w[i], shc);
                 uint32_t f[8];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) i8x4_to_f16(c[i], f[2 * i], f[2 * i + 1]);
                 const f16x8 b0 = pack8(f[0], f[1], f[2], f[3]), b1 = pack8(f[4], f[5], f[6], f[7]);
 #pragma unroll
                 for (int t = 0; t < kNT; ++t) {
-                    f32x16 p = mfma(act_frag(lds, t, 32 * bb + 16 * h), b0, (f32x16){});
-                    p = mfma(act_frag(lds, t, 32 * bb + 16 * h + 8), b1, p);
+                    f32x16 p = mfma(act_frag(cur, t, 32 * bb + 16 * h), b0, (f32x16){});
+                    p = mfma(act_frag(cur, t, 32 * bb + 16 * h + 8), b1, p);
                     acc[t] += d * p;
                 }
             }
         } else if (TYPE == AH_GGML_Q4_K) {
             const uint32_t s = k0 / 256, p = (k0 / 64) & 3;
-            const uint32_t sb = rbase + 144 * s;
             if (p == 0) {
-                const u32x4 hd = ah_ld128(rs, sb);
+                const u32x4 hd = wc.a0;
                 fd = ah_f16_bits_to_f32(hd.x & 0xffffu);
                 fdm = ah_f16_bits_to_f32(hd.x >> 16);
                 s0 = hd.y;
@@ -179,7 +237,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
             }
             // qs window p: lane half h takes bytes [16h, 16h+16) -> sub-block 2p (low nibbles)
             // and 2p+1 (high nibbles), k = 16h + 8m + e.
-            const u32x4 q = ah_ld128(rs, sb + 16 + 32 * p + 16 * h);
+            const u32x4 q = wc.a1;
             const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
             int scv[2];
             {
@@ -207,8 +265,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
                 const f16x8 b0 = pack8(f[0], f[1], f[2], f[3]), b1 = pack8(f[4], f[5], f[6], f[7]);
 #pragma unroll
                 for (int t = 0; t < kNT; ++t) {
-                    P[t] = mfma(act_frag(lds, t, 32 * hb + 16 * h), b0, P[t]);
-                    P[t] = mfma(act_frag(lds, t, 32 * hb + 16 * h + 8), b1, P[t]);
+                    P[t] = mfma(act_frag(cur, t, 32 * hb + 16 * h), b0, P[t]);
+                    P[t] = mfma(act_frag(cur, t, 32 * hb + 16 * h + 8), b1, P[t]);
                 }
             }
             if (p == 3 || k0 + kKS >= a.n_in) {
@@ -286,26 +344,34 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
                 const float coef = fd * (float)(int)(int8_t)((scw >> (8 * (G & 3))) & 0xffu);
 #pragma unroll
                 for (int tt = 0; tt < kNT; ++tt) {
-                    const f32x16 p = mfma(act_frag(lds, tt, 16 * gg + 8 * h), bq, (f32x16){});
+                    const f32x16 p = mfma(act_frag(cur, tt, 16 * gg + 8 * h), bq, (f32x16){});
                     acc[tt] += coef * p;
                 }
             }
         }
+
+        act_store(lds[((st - st_begin) & 1) ^ 1]);  // stage st+1 (zeros past the split)
+        act_load(st + 2);
+        wc = wn;
     }
 
     // D layout of a 32x32 MFMA: lane (j, h), register r -> row i = 8*(r/4) + 4*h + (r%4), col j.
-    if (!row_ok) return;
+    // Buffer stores relative to this workgroup's token rows; a lane past n_out or a token past
+    // n_tok stores out of range (nothing is written), so there is no branch per element.
+    float *ybase = a.splits == 1 ? a.y + (size_t)tok0 * a.n_out
+                                 : a.y + ((size_t)blockIdx.z * a.n_tok + tok0) * a.n_out;
+    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(ybase, ntile * a.n_out * 4u);
+    const __amdgpu_buffer_rsrc_t rt = ah_rsrc(a.tok_scale + tok0, ntile * 4u);
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t tok = tok0 + 32 * t + 8 * (r / 4) + 4 * h + (r % 4);
-            if (tok >= a.n_tok) continue;
-            const float v = acc[t][r];
-            if (a.splits == 1)
-                a.y[(size_t)tok * a.n_out + my_row] = v * a.tok_scale[tok];
-            else
-                a.y[((size_t)blockIdx.z * a.n_tok + tok) * a.n_out + my_row] = v;
+            const uint32_t tl = 32 * t + 8 * (r / 4) + 4 * h + (r % 4);
+            const bool ok = row_ok && tl < ntile;
+            float v = acc[t][r];
+            if (a.splits == 1) v *= __builtin_bit_cast(float, ah_ld32(rt, ok ? 4 * tl : kOob));
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
+                                                  ok ? (tl * a.n_out + my_row) * 4u : kOob, 0, 0);
         }
     }
 }
@@ -319,61 +385,6 @@ __global__ void splitk_reduce(const float *part, uint32_t splits, uint32_t n_tok
         float s = 0.0f;
         for (uint32_t z = 0; z < splits; ++z) s += part[z * n + i];
         y[i] = s * tok_scale[i / n_out];
-    }
-}
-
-// GEMM activation operand of one token per workgroup (OperandArgs): E_tok = the largest block
-// exponent, tok_scale = 2^(E_tok - 32), xh = xq * 2^(e_b - E_tok) in f16 (exact whenever
-// e_b - E_tok >= -24; a smaller block is at most 2^-24 of the token's largest), and for Q4_K the
-// min-term operand: per super-block, the 8 sub-block code sums X_j split exactly into f16 pieces
-// [64*floor(X/64), X mod 64] * 2^(e_j - E_tok), laid out [hi 0..7, lo 0..7].
-__global__ void __launch_bounds__(256) operand_kernel(OperandArgs o) {
-    __shared__ int red[256];
-    for (uint32_t tok = blockIdx.x; tok < o.n_tok; tok += gridDim.x) {
-        const int64_t *sc = o.scales + (size_t)tok * o.nb32;
-        int em = -1;
-        for (uint32_t b = threadIdx.x; b < o.nb32; b += 256) {
-            const int64_t S = sc[b];
-            const int e = S > 0 ? 63 - __builtin_clzll((uint64_t)S) : -1;
-            em = e > em ? e : em;
-        }
-        red[threadIdx.x] = em;
-        __syncthreads();
-        for (uint32_t w = 128; w > 0; w >>= 1) {
-            if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] > red[threadIdx.x + w] ? red[threadIdx.x] : red[threadIdx.x + w];
-            __syncthreads();
-        }
-        const int E = red[0];
-        __syncthreads();
-        if (threadIdx.x == 0) o.tok_scale[tok] = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
-        const int8_t *codes = o.codes + (size_t)tok * o.n_in;
-        _Float16 *xh = o.xh + (size_t)tok * o.kpad;
-        for (uint32_t k = threadIdx.x; k < o.kpad; k += 256) {
-            float v = 0.0f;
-            if (k < o.n_in) {
-                const int64_t S = sc[k / 32];
-                if (S > 0) v = __builtin_ldexpf((float)codes[k], 63 - __builtin_clzll((uint64_t)S) - E);
-            }
-            xh[k] = (_Float16)v;
-        }
-        if (o.xmin) {
-            const uint32_t nsb = o.kpad / 256;
-            for (uint32_t g = threadIdx.x; g < nsb * 8; g += 256) {
-                float hi = 0.0f, lo = 0.0f;
-                if (g < o.nb32 && sc[g] > 0) {
-                    int X = 0;
-                    for (uint32_t l = 0; l < 32 && g * 32 + l < o.n_in; ++l) X += codes[g * 32 + l];
-                    const int ex = 63 - __builtin_clzll((uint64_t)sc[g]) - E;
-                    const int xhq = (X >= 0 ? X : X - 63) / 64;  // floor(X / 64)
-                    hi = __builtin_ldexpf((float)(64 * xhq), ex);
-                    lo = __builtin_ldexpf((float)(X - 64 * xhq), ex);
-                }
-                _Float16 *m = o.xmin + ((size_t)tok * nsb + g / 8) * 16;
-                m[g % 8] = (_Float16)hi;
-                m[8 + g % 8] = (_Float16)lo;
-            }
-        }
-        __syncthreads();
     }
 }
 
@@ -424,9 +435,3 @@ uint32_t ah_gemm_splits_used(uint32_t type, uint32_t n_in, uint32_t splits) {
     return (nstages + per - 1) / per;
 }
 
-hipError_t ah_launch_operand(const OperandArgs &o, hipStream_t stream) {
-    if (o.n_tok == 0) return hipSuccess;
-    const uint32_t grid = o.n_tok < 2048 ? o.n_tok : 2048;
-    hipLaunchKernelGGL(operand_kernel, dim3(grid), dim3(256), 0, stream, o);
-    return hipGetLastError();
-}

@@ -559,6 +559,115 @@ __global__ void __launch_bounds__(kThreads) quant_kernel(QuantArgs q) {
     }
 }
 
+// Largest value over the wave (every lane gets it).
+AH_DEV int wave_max(int v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_xor(v, o, 64);
+        v = t > v ? t : v;
+    }
+    return v;
+}
+AH_DEV uint32_t wave_max_u(uint32_t v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = (uint32_t)__shfl_xor((int)v, o, 64);
+        v = t > v ? t : v;
+    }
+    return v;
+}
+
+// GEMM activation operand straight from the input, one wave per token.  The token's largest
+// block exponent E is the exponent of its largest magnitude (act_scale is monotone in absmax,
+// kern/pow2.rs:11-39), so a first pass reduces |x|; a second quantizes every 32-block bit-exactly
+// (quant_act, chart/mod.rs:258-334, refusals recorded as quant_kernel does) and writes
+//   xh   = xq * 2^(e_b - E) in f16 (exact whenever e_b - E >= -24),
+//   tok_scale = 2^(E - 32),
+//   xmin (Q4_K) = per 32-block code sum X split exactly as [64*floor(X/64), X mod 64] * 2^(e_b - E),
+//        laid out per super-block as [hi 0..7, lo 0..7].
+// With codes input (AH_SRC_CODES) the block exponents come from the power-of-two scales.
+__global__ void __launch_bounds__(kThreads) gemm_operand_kernel(OperandArgs o) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t tok = blockIdx.x * (kThreads / 64) + wave;
+    if (tok >= o.n_tok) return;  // wave-uniform
+    const size_t row = (size_t)tok * o.n_in;
+    const uint32_t esz = o.src == AH_SRC_F32 ? 4u : o.src == AH_SRC_Q32 ? 8u : 1u;
+    const ActRsrc r = act_rsrc(static_cast<const uint8_t *>(o.x) + row * esz,
+                               o.src == AH_SRC_CODES ? o.scales + (size_t)tok * o.nb32 : nullptr, o.src,
+                               o.n_in);
+    // pass 1: E
+    int E = -1;
+    if (o.src == AH_SRC_F32) {
+        uint32_t mb = 0;
+        for (uint32_t c = lane; 4 * c < o.n_in; c += 64) {
+            const u32x4 v = ah_ld128(r.x, 16 * c);
+            const uint32_t a = (v.x & 0x7fffffffu) > (v.y & 0x7fffffffu) ? (v.x & 0x7fffffffu) : (v.y & 0x7fffffffu);
+            const uint32_t b = (v.z & 0x7fffffffu) > (v.w & 0x7fffffffu) ? (v.z & 0x7fffffffu) : (v.w & 0x7fffffffu);
+            const uint32_t m = a > b ? a : b;
+            mb = m > mb ? m : mb;
+        }
+        mb = wave_max_u(mb);
+        uint64_t mag;
+        bool neg;
+        if (ah_to_q32_mag(mb, mag, neg) == 0) E = ah_act_scale_exp(mag);  // else refused below
+    } else if (o.src == AH_SRC_Q32) {
+        uint64_t mm = 0;
+        for (uint32_t c = lane; 2 * c < o.n_in; c += 64) {
+            const u32x4 v = ah_ld128(r.x, 16 * c);
+            const int64_t a = (int64_t)(((uint64_t)v.y << 32) | v.x), b = (int64_t)(((uint64_t)v.w << 32) | v.z);
+            const uint64_t ma = a < 0 ? 0ull - (uint64_t)a : (uint64_t)a, mbb = b < 0 ? 0ull - (uint64_t)b : (uint64_t)b;
+            const uint64_t m = ma > mbb ? ma : mbb;
+            mm = m > mm ? m : mm;
+        }
+        const uint32_t hi = wave_max_u((uint32_t)(mm >> 32));
+        const uint32_t lo = wave_max_u((uint32_t)(mm >> 32) == hi ? (uint32_t)mm : 0u);
+        E = ah_act_scale_exp(((uint64_t)hi << 32) | lo);
+    } else {
+        for (uint32_t b = lane; b < o.nb32; b += 64) {
+            const u32x2 sv = ah_ld64(r.s, 8 * b);
+            const uint64_t S = ((uint64_t)sv.y << 32) | sv.x;
+            const int e = (int64_t)S > 0 ? 63 - __builtin_clzll(S) : -1;
+            E = e > E ? e : E;
+        }
+        E = wave_max(E);
+    }
+    if (E > 62) E = 62;  // a block without a Q32.32 scale: the call is refused anyway
+    if (lane == 0) o.tok_scale[tok] = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
+    // pass 2: codes -> operand
+    const uint32_t nbp = o.kpad / 32, q = lane & 3;
+    _Float16 *xh = o.xh + (size_t)tok * o.kpad;
+    for (uint32_t base = 0; base < nbp; base += 16) {
+        const uint32_t b = base + lane / 4;
+        // codes rows start at tok * n_in bytes, not always a dword boundary: bytewise loads there
+        const QuadIn in = o.src == AH_SRC_CODES
+                              ? quad_load(o.x, o.scales + (size_t)tok * o.nb32, o.src, o.n_in, row, b, b < o.nb32)
+                              : quad_load_row(r, o.src, o.n_in, b);
+        const QuadOut qo = quad_quant(in, o.src, b, o.status, (unsigned long long)row);
+        int e = qo.e;
+        if (o.src == AH_SRC_CODES) {
+            const u32x2 sv = ah_ld64(r.s, 8 * b);
+            const uint64_t S = ((uint64_t)sv.y << 32) | sv.x;
+            e = (int64_t)S > 0 ? 63 - __builtin_clzll(S) : -1;
+        }
+        if (b >= nbp) continue;
+        const int sh = e - E;
+        _Float16 hv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = (int)(int8_t)(((i < 4 ? qo.c0 : qo.c1) >> (8 * (i & 3))) & 0xffu);
+            hv[i] = e < 0 ? (_Float16)0.0f : (_Float16)__builtin_ldexpf((float)c, sh);
+        }
+        *reinterpret_cast<u32x4 *>(xh + 32 * b + 8 * q) = __builtin_bit_cast(u32x4, hv);
+        if (o.xmin && q == 0) {
+            const int X = qo.s32;
+            const int hq = (X >= 0 ? X : X - 63) / 64;  // floor(X / 64)
+            _Float16 *m = o.xmin + ((size_t)tok * (o.kpad / 256) + b / 8) * 16;
+            m[b % 8] = e < 0 ? (_Float16)0.0f : (_Float16)__builtin_ldexpf((float)(64 * hq), sh);
+            m[8 + b % 8] = e < 0 ? (_Float16)0.0f : (_Float16)__builtin_ldexpf((float)(X - 64 * hq), sh);
+        }
+    }
+}
+
 // Device-side f16 scale scan of a payload: flags any Inf/NaN d / dmin word.
 __global__ void scan_scales_kernel(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes,
                                    uint32_t off0, uint32_t off1, int *bad) {
@@ -660,8 +769,8 @@ __global__ void __launch_bounds__(kSThreads)
 
     // Prologue.  Every wave's activation loads go out before any tile load of the workgroup (the
     // barrier orders issue, not completion), tile 0 follows at once, and the quantizer runs from
-    // registers while tile 0 streams in; then tile 0 is staged and tile 1 requested before the
-    // barrier that publishes the activation, so the stream does not stall on the prologue.
+    // registers while tile 0 streams in.  After the barrier that publishes the activation each
+    // wave stages its own tile 0 and requests tile 1, so no wave waits for another's tile.
     const uint32_t nbp = kpad / 32, QB = kSThreads / 4;
     const uint32_t passes = (nbp + QB - 1) / QB;
     const ActRsrc xr = act_rsrc(P.x, P.scales, P.src, P.n_in);
@@ -689,8 +798,8 @@ __global__ void __launch_bounds__(kSThreads)
         for (uint32_t i = 0; i < kChunks; ++i) reinterpret_cast<u32x4 *>(tl)[lane + 64 * i] = chunk[i];
         load_tile(t + 1);
     };
-    stage(0);  // unconditional, like every tile load: a wave without rows stages zeros
-    ah_lds_barrier();
+    ah_lds_barrier();  // the activation is published; tiles are wave-private, so each wave
+    stage(0);          // stages its own tile 0 (unconditionally: a wave without rows stages zeros)
 
     // Row sums leave through a buffer store that every lane issues (lanes that own no row store
     // out of range, which writes nothing): a store behind a branch would make the compiler wait for
@@ -853,6 +962,13 @@ hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart 
     default:
         return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream) {
+    if (o.n_tok == 0) return hipSuccess;
+    const uint32_t grid = (o.n_tok + kThreads / 64 - 1) / (kThreads / 64);
+    hipLaunchKernelGGL(gemm_operand_kernel, dim3(grid), dim3(kThreads), 0, stream, o);
     return hipGetLastError();
 }
 

@@ -178,10 +178,11 @@ struct QuantArgs {
 // when e_b - E_tok >= -24), tok_scale[tok] = 2^(E_tok - 32), and for Q4_K the min-term operand
 // xmin[tok][kpad/256][16] (split sub-block code sums, see ah_gemm.hip).
 struct OperandArgs {
-    const int8_t *codes;
-    const int64_t *scales;
-    _Float16 *xh;
-    float *tok_scale;
-    _Float16 *xmin;        // nullptr unless Q4_K
-    uint32_t n_tok, n_in, nb32, kpad;
+    const void *x;         // f32 / Q32.32 int64 [n_tok][n_in], or int8 codes with `scales`
+    const int64_t *scales; // [n_tok][nb32] with AH_SRC_CODES
+    _Float16 *xh;          // [n_tok][kpad]
+    float *tok_scale;      // [n_tok]
+    _Float16 *xmin;        // [n_tok][kpad/256][16] for Q4_K, else nullptr
+    unsigned long long *status;
+    uint32_t n_tok, n_in, nb32, kpad, src;
 };

@@ -33,7 +33,8 @@ hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uin
                           uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t kpad,
                           const _Float16 *xh, const _Float16 *xmin, const float *tok_scale,
                           float *y, float *partials, uint32_t splits, hipStream_t stream);
-uint32_t ah_gemm_splits_used(uint32_t type, uint32_t n_in, uint32_t splits);
+uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
+                             uint32_t cus);
 hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream);
 
 struct ah_ctx {
@@ -283,13 +284,7 @@ int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     if (w->n_out > (0xFFFFFF00ull / (128 * 4))) return AH_ERR_INVALID_ARG;
     const uint32_t n_in = (uint32_t)w->n_in, n_out = (uint32_t)w->n_out, N = (uint32_t)n_tok;
     const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
-    // split-K so the grid covers the chip about twice
-    const uint32_t tiles = ((n_out + 127) / 128) * ((N + 127) / 128);
-    uint32_t want = tiles >= 2u * (uint32_t)ctx->cu_count ? 1u : (2u * (uint32_t)ctx->cu_count + tiles - 1) / tiles;
-    const uint32_t max_splits = w->type == AH_GGML_Q8_0 ? (n_in + 63) / 64 : nsb;
-    if (want > max_splits) want = max_splits;
-    if (want < 1) want = 1;
-    const uint32_t splits = ah_gemm_splits_used(w->type, n_in, want);
+    const uint32_t splits = ah_gemm_pick_splits(w->type, n_out, n_in, N, (uint32_t)ctx->cu_count);
 
     size_t off = 0;
     const size_t o_xh = off; off = align256(off + (size_t)N * kpad * 2);

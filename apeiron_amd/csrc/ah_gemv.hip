@@ -577,7 +577,7 @@ AH_DEV uint32_t wave_max_u(uint32_t v) {
     return v;
 }
 
-// GEMM activation operand straight from the input, one wave per token.  The token's largest
+// GEMM activation operand straight from the input, one workgroup per token.  The token's largest
 // block exponent E is the exponent of its largest magnitude (act_scale is monotone in absmax,
 // kern/pow2.rs:11-39), so a first pass reduces |x|; a second quantizes every 32-block bit-exactly
 // (quant_act, chart/mod.rs:258-334, refusals recorded as quant_kernel does) and writes
@@ -587,9 +587,9 @@ AH_DEV uint32_t wave_max_u(uint32_t v) {
 //        laid out per super-block as [hi 0..7, lo 0..7].
 // With codes input (AH_SRC_CODES) the block exponents come from the power-of-two scales.
 __global__ void __launch_bounds__(kThreads) gemm_operand_kernel(OperandArgs o) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t tok = blockIdx.x * (kThreads / 64) + wave;
-    if (tok >= o.n_tok) return;  // wave-uniform
+    __shared__ uint32_t red[2][kThreads / 64];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tok = blockIdx.x;
     const size_t row = (size_t)tok * o.n_in;
     const uint32_t esz = o.src == AH_SRC_F32 ? 4u : o.src == AH_SRC_Q32 ? 8u : 1u;
     const ActRsrc r = act_rsrc(static_cast<const uint8_t *>(o.x) + row * esz,
@@ -599,7 +599,7 @@ __global__ void __launch_bounds__(kThreads) gemm_operand_kernel(OperandArgs o) {
     int E = -1;
     if (o.src == AH_SRC_F32) {
         uint32_t mb = 0;
-        for (uint32_t c = lane; 4 * c < o.n_in; c += 64) {
+        for (uint32_t c = tid; 4 * c < o.n_in; c += kThreads) {
             const u32x4 v = ah_ld128(r.x, 16 * c);
             const uint32_t a = (v.x & 0x7fffffffu) > (v.y & 0x7fffffffu) ? (v.x & 0x7fffffffu) : (v.y & 0x7fffffffu);
             const uint32_t b = (v.z & 0x7fffffffu) > (v.w & 0x7fffffffu) ? (v.z & 0x7fffffffu) : (v.w & 0x7fffffffu);
@@ -607,37 +607,54 @@ __global__ void __launch_bounds__(kThreads) gemm_operand_kernel(OperandArgs o) {
             mb = m > mb ? m : mb;
         }
         mb = wave_max_u(mb);
+        if (lane == 0) red[0][wave] = mb;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) mb = red[0][w] > mb ? red[0][w] : mb;
         uint64_t mag;
         bool neg;
         if (ah_to_q32_mag(mb, mag, neg) == 0) E = ah_act_scale_exp(mag);  // else refused below
     } else if (o.src == AH_SRC_Q32) {
         uint64_t mm = 0;
-        for (uint32_t c = lane; 2 * c < o.n_in; c += 64) {
+        for (uint32_t c = tid; 2 * c < o.n_in; c += kThreads) {
             const u32x4 v = ah_ld128(r.x, 16 * c);
             const int64_t a = (int64_t)(((uint64_t)v.y << 32) | v.x), b = (int64_t)(((uint64_t)v.w << 32) | v.z);
             const uint64_t ma = a < 0 ? 0ull - (uint64_t)a : (uint64_t)a, mbb = b < 0 ? 0ull - (uint64_t)b : (uint64_t)b;
             const uint64_t m = ma > mbb ? ma : mbb;
             mm = m > mm ? m : mm;
         }
-        const uint32_t hi = wave_max_u((uint32_t)(mm >> 32));
-        const uint32_t lo = wave_max_u((uint32_t)(mm >> 32) == hi ? (uint32_t)mm : 0u);
+        // 64-bit max: the high words first, then the low words among the lanes that hold it
+        uint32_t hi = wave_max_u((uint32_t)(mm >> 32));
+        if (lane == 0) red[0][wave] = hi;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) hi = red[0][w] > hi ? red[0][w] : hi;
+        uint32_t lo = wave_max_u((uint32_t)(mm >> 32) == hi ? (uint32_t)mm : 0u);
+        if (lane == 0) red[1][wave] = lo;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) lo = red[1][w] > lo ? red[1][w] : lo;
         E = ah_act_scale_exp(((uint64_t)hi << 32) | lo);
     } else {
-        for (uint32_t b = lane; b < o.nb32; b += 64) {
+        for (uint32_t b = tid; b < o.nb32; b += kThreads) {
             const u32x2 sv = ah_ld64(r.s, 8 * b);
             const uint64_t S = ((uint64_t)sv.y << 32) | sv.x;
             const int e = (int64_t)S > 0 ? 63 - __builtin_clzll(S) : -1;
             E = e > E ? e : E;
         }
         E = wave_max(E);
+        if (lane == 0) red[0][wave] = (uint32_t)(E + 1);
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) E = (int)red[0][w] - 1 > E ? (int)red[0][w] - 1 : E;
     }
     if (E > 62) E = 62;  // a block without a Q32.32 scale: the call is refused anyway
-    if (lane == 0) o.tok_scale[tok] = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
+    if (tid == 0) o.tok_scale[tok] = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
     // pass 2: codes -> operand
     const uint32_t nbp = o.kpad / 32, q = lane & 3;
     _Float16 *xh = o.xh + (size_t)tok * o.kpad;
-    for (uint32_t base = 0; base < nbp; base += 16) {
-        const uint32_t b = base + lane / 4;
+    for (uint32_t base = 0; base < nbp; base += kThreads / 4) {
+        const uint32_t b = base + tid / 4;
         // codes rows start at tok * n_in bytes, not always a dword boundary: bytewise loads there
         const QuadIn in = o.src == AH_SRC_CODES
                               ? quad_load(o.x, o.scales + (size_t)tok * o.nb32, o.src, o.n_in, row, b, b < o.nb32)
@@ -967,8 +984,7 @@ hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart 
 
 hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream) {
     if (o.n_tok == 0) return hipSuccess;
-    const uint32_t grid = (o.n_tok + kThreads / 64 - 1) / (kThreads / 64);
-    hipLaunchKernelGGL(gemm_operand_kernel, dim3(grid), dim3(kThreads), 0, stream, o);
+    hipLaunchKernelGGL(gemm_operand_kernel, dim3(o.n_tok), dim3(kThreads), 0, stream, o);
     return hipGetLastError();
 }
 

@@ -387,22 +387,24 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
 
 // ---- register-blocked kernel (Q8_0, Q4_K) ---------------------------------------------------
 //
-// A workgroup is 4 waves over 256 weight rows x 64 tokens.  Wave w owns rows [64w, 64w+64) as
-// two 32-row MFMA column tiles (n) and the workgroup's 64 tokens as two 32-token row tiles (m), so
-// every activation fragment read from LDS feeds two MFMAs and every dequantized weight fragment
-// feeds two (a 32-row x 128-token wave tile reads 1 KB of LDS per MFMA, the LDS port's whole
-// bandwidth at the MFMA rate).  The loop body is U stages of 64 (Q8_0: U = 2, Q4_K: U = 4 = one
-// super-block), so the LDS buffer, the weight register set and the super-block position of each
-// stage are compile-time: no runtime register indexing, no copies between register sets.
+// A workgroup is 4 waves.  Wave w owns NN 32-row MFMA column tiles (n) of weight rows and all NM
+// 32-token row tiles (m) of the workgroup's tokens, so every activation fragment read from LDS
+// feeds NN MFMAs and every dequantized weight fragment feeds NM.  The VALU work per MFMA (weight
+// dequantization over NM, plus the scale folds) is what bounds this kernel, so NM = 4 by default;
+// LDS sustains the resulting 1 KB of fragment reads per MFMA.  The loop body is U stages of 64
+// (Q8_0: U = 2, Q4_K: U = 4 = one super-block), so the LDS buffer, the weight register set and the
+// super-block position of each stage are compile-time: no runtime register indexing, no copies
+// between register sets.
 namespace rb {
-constexpr int kTok = 64;                        // tokens per workgroup
-constexpr int kRows = 256;                      // weight rows per workgroup
+constexpr int kNN = 1, kNM = 4;                 // column / row tiles per wave
+constexpr int kTok = 32 * kNM;                  // tokens per workgroup
+constexpr int kRows = 4 * 32 * kNN;             // weight rows per workgroup
 constexpr int kActBytes = kTok * kPitch;        // f16 activation slice of one stage
 constexpr int kBufBytes = kActBytes + kTok * 32; // + Q4_K split code sums of the super-block
 template <int TYPE> constexpr int unroll() { return TYPE == AH_GGML_Q8_0 ? 2 : 4; }
 }  // namespace rb
 
-// Weight bytes of one stage for the lane's two rows, fetched a stage ahead.  Ordinary (not
+// Weight bytes of one stage for the lane's NN rows, fetched a stage ahead.  Ordinary (not
 // non-temporal) loads: the workgroups of the other token tiles read the same bytes from L2.
 //   Q8_0: per row n and block bb, v[2n+bb] = the 16 codes of the lane half (4-aligned window),
 //         s[4n+2bb] = the dword after the window, s[4n+2bb+1] = the dword holding d.
@@ -413,16 +415,20 @@ struct WRb {
     uint32_t s[8];
 };
 
-template <int TYPE, int P>
-AH_DEV WRb fetch_rb(__amdgpu_buffer_rsrc_t rs, const uint32_t (&rb)[2], const bool (&rl)[2],
+template <int TYPE, int P, int NN>
+AH_DEV WRb fetch_rb(__amdgpu_buffer_rsrc_t rs, const uint32_t (&rb)[NN], const bool (&rl)[NN],
                     uint32_t st, uint32_t n_in, int h, bool live) {
     WRb w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w.v[i] = (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w.s[i] = 0u;
     const uint32_t k0 = st * kKS;
     if constexpr (TYPE == AH_GGML_Q8_0) {
         const uint32_t b = k0 / 32;
         const bool l0 = live && b * 32 < n_in, l1 = live && (b + 1) * 32 < n_in;
 #pragma unroll
-        for (int n = 0; n < 2; ++n) {
+        for (int n = 0; n < NN; ++n) {
             const uint32_t blk0 = rb[n] + 34 * b, blk1 = blk0 + 34;
             const bool m0 = l0 && rl[n], m1 = l1 && rl[n];
             const uint32_t c0 = (blk0 + 2 + 16 * h) & ~3u, c1 = (blk1 + 2 + 16 * h) & ~3u;
@@ -435,15 +441,13 @@ AH_DEV WRb fetch_rb(__amdgpu_buffer_rsrc_t rs, const uint32_t (&rb)[2], const bo
         }
     } else {
 #pragma unroll
-        for (int n = 0; n < 2; ++n) {
+        for (int n = 0; n < NN; ++n) {
             const uint32_t sb = rb[n] + 144 * (k0 / 256);
             const bool m = live && rl[n];
             if constexpr (P == 0) w.v[2 * n] = ah_ld128(rs, m ? sb : kOob);
             else w.v[2 * n] = (u32x4){0u, 0u, 0u, 0u};
             w.v[2 * n + 1] = ah_ld128(rs, m ? sb + 16 + 32 * P + 16 * h : kOob);
         }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) w.s[i] = 0u;
     }
     return w;
 }
@@ -463,7 +467,7 @@ AH_DEV uint32_t q4k_scale(uint32_t s0, uint32_t s1, uint32_t s2) {
 
 template <int TYPE>
 __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
-    constexpr int U = rb::unroll<TYPE>();
+    constexpr int U = rb::unroll<TYPE>(), NN = rb::kNN, NM = rb::kNM;
     __shared__ __align__(16) uint8_t lds[2][rb::kBufBytes];
     // XCD-aware order: dispatch i goes to XCD i % 8, so XCD x takes logical ids
     // [x * per, (x + 1) * per).  Consecutive logical ids share a weight row tile and split, so the
@@ -476,11 +480,11 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
-    const uint32_t row_w = rtile * rb::kRows + wave * 64;
-    uint32_t rbase[2];
-    bool rl[2];
+    const uint32_t row_w = rtile * rb::kRows + wave * 32 * NN;
+    uint32_t rbase[NN];
+    bool rl[NN];
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
+    for (int n = 0; n < NN; ++n) {
         const uint32_t r = row_w + 32 * n + j;
         rl[n] = r < a.n_out;
         rbase[n] = (rl[n] ? r : 0u) * a.row_bytes;
@@ -500,29 +504,30 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
     uint32_t st_end = st_begin + a.stages_per_split;
     if (st_end > nstages) st_end = nstages;
 
-    // activation slice of a stage: 64 tokens x 128 B = two 16-B chunks per thread (+ Q4_K: the
-    // 32-B split code sums of the stage's super-block, one 16-B chunk per thread of waves 0-1)
-    u32x4 areg[2], mreg;
+    // activation slice of a stage: 32*NM tokens x 128 B = NM 16-B chunks per thread (+ Q4_K: the
+    // 32-B split code sums of the stage's super-block, one 16-B chunk per thread of the first NM
+    // waves)
+    u32x4 areg[NM], mreg;
     auto act_load = [&](uint32_t st) {
         const bool live = st < st_end;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NM; ++i) {
             const uint32_t c = tid + kThreads * i, t = c >> 3, kc = c & 7;
             areg[i] = ah_ld128(rx, live && t < ntile ? (t * a.kpad + st * kKS + 8 * kc) * 2u : kOob);
         }
         if constexpr (TYPE == AH_GGML_Q4_K) {
-            const uint32_t t = (tid >> 1) & 63, hc = tid & 1;
-            mreg = ah_ld128(rm, live && tid < 128 && t < ntile ? ((t * nsb + st / 4) * 16 + 8 * hc) * 2u : kOob);
+            const uint32_t t = (tid >> 1) & (rb::kTok - 1), hc = tid & 1;
+            mreg = ah_ld128(rm, live && tid < 2 * rb::kTok && t < ntile ? ((t * nsb + st / 4) * 16 + 8 * hc) * 2u : kOob);
         }
     };
     auto act_store = [&](uint8_t *buf) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NM; ++i) {
             const uint32_t c = tid + kThreads * i, t = c >> 3, kc = c & 7;
             *reinterpret_cast<u32x4 *>(buf + t * kPitch + 16 * kc) = areg[i];
         }
         if constexpr (TYPE == AH_GGML_Q4_K) {
-            if (tid < 128)  // waves 0 and 1
+            if (tid < 2 * rb::kTok)  // whole waves
                 *reinterpret_cast<u32x4 *>(buf + rb::kActBytes + (tid >> 1) * 32 + 16 * (tid & 1)) = mreg;
         }
     };
@@ -530,38 +535,43 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
         return *reinterpret_cast<const f16x8 *>(buf + (m * 32 + j) * kPitch + 2 * kk);
     };
 
-    f32x16 acc[2][2], P[2][2];
+    f32x16 acc[NM][NN], P[NM][NN];
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int n = 0; n < 2; ++n) acc[m][n] = P[m][n] = (f32x16){};
-    float fd[2] = {0.0f, 0.0f}, fdm[2] = {0.0f, 0.0f};
-    uint32_t s0[2] = {0u, 0u}, s1[2] = {0u, 0u}, s2[2] = {0u, 0u};
+        for (int n = 0; n < NN; ++n) acc[m][n] = P[m][n] = (f32x16){};
+    float fd[NN], fdm[NN];
+    uint32_t s0[NN], s1[NN], s2[NN];
+#pragma unroll
+    for (int n = 0; n < NN; ++n) {
+        fd[n] = fdm[n] = 0.0f;
+        s0[n] = s1[n] = s2[n] = 0u;
+    }
 
     act_load(st_begin);
     act_store(lds[0]);
     act_load(st_begin + 1);
     WRb W[2];
-    W[0] = fetch_rb<TYPE, 0>(rs, rbase, rl, st_begin, a.n_in, h, st_begin < st_end);
+    W[0] = fetch_rb<TYPE, 0, NN>(rs, rbase, rl, st_begin, a.n_in, h, st_begin < st_end);
 
     auto stage = [&](auto uc, uint32_t st) {
         constexpr int u = decltype(uc)::value;
         const uint8_t *cur = lds[u & 1];
         ah_lds_barrier();  // buffer `cur` is written; every wave is done with the other one
-        W[(u + 1) & 1] = fetch_rb<TYPE, (u + 1) % U>(rs, rbase, rl, st + 1, a.n_in, h, st + 1 < st_end);
+        W[(u + 1) & 1] = fetch_rb<TYPE, (u + 1) % U, NN>(rs, rbase, rl, st + 1, a.n_in, h, st + 1 < st_end);
         __builtin_amdgcn_sched_barrier(0);  // the next stage's weight requests stay a stage ahead
         const WRb &wc = W[u & 1];
         if constexpr (TYPE == AH_GGML_Q8_0) {
-            // Eight MFMA chains per stage (block bb, token tile m, row tile n), each two MFMAs
+            // 2*NM*NN MFMA chains per stage (block bb, token tile m, row tile n), each two MFMAs
             // into a fresh accumulator that is folded with the block's d.  The fold of chain c-1
             // is issued after chain c's MFMAs, so the VALU fold overlaps the matrix core.
             // A block past n_in has zero codes and d = 0 against zero activations.
-            float d[2][2];
-            f16x8 bq[2][2][2];
+            float d[2][NN];
+            f16x8 bq[2][NN][2];
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-                for (int n = 0; n < 2; ++n) {
+                for (int n = 0; n < NN; ++n) {
                     const uint32_t blk = rbase[n] + 34 * (st * 2 + bb);
                     const uint32_t shc = (blk + 2 + 16 * h) & 3u;  // 0 or 2
                     const u32x4 v = wc.v[2 * n + bb];
@@ -574,17 +584,18 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
                     bq[bb][n][0] = pack8(f[0], f[1], f[2], f[3]);
                     bq[bb][n][1] = pack8(f[4], f[5], f[6], f[7]);
                 }
+            constexpr int NC = 2 * NM * NN;
             f32x16 pq[2];
 #pragma unroll
-            for (int c = 0; c <= 8; ++c) {
-                if (c < 8) {
-                    const int bb = c >> 2, m = (c >> 1) & 1, n = c & 1;
+            for (int c = 0; c <= NC; ++c) {
+                if (c < NC) {
+                    const int bb = c / (NM * NN), m = (c / NN) % NM, n = c % NN;
                     const f16x8 a0 = frag(cur, m, 32 * bb + 16 * h), a1 = frag(cur, m, 32 * bb + 16 * h + 8);
                     pq[c & 1] = mfma(a0, bq[bb][n][0], (f32x16){});
                     pq[c & 1] = mfma(a1, bq[bb][n][1], pq[c & 1]);
                 }
                 if (c > 0) {
-                    const int pc = c - 1, bb = pc >> 2, m = (pc >> 1) & 1, n = pc & 1;
+                    const int pc = c - 1, bb = pc / (NM * NN), m = (pc / NN) % NM, n = pc % NN;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[m][n][r] = __builtin_fmaf(d[bb][n], pq[pc & 1][r], acc[m][n][r]);
                 }
@@ -592,7 +603,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
         } else {  // Q4_K, stage u of the super-block: qs chunk u = sub-blocks 2u (low), 2u+1 (high)
             if constexpr (u == 0) {
 #pragma unroll
-                for (int n = 0; n < 2; ++n) {
+                for (int n = 0; n < NN; ++n) {
                     const u32x4 hd = wc.v[2 * n];
                     fd[n] = ah_f16_bits_to_f32(hd.x & 0xffffu);
                     fdm[n] = ah_f16_bits_to_f32(hd.x >> 16);
@@ -603,9 +614,9 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
             }
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb) {
-                f16x8 bq[2][2];
+                f16x8 bq[NN][2];
 #pragma unroll
-                for (int n = 0; n < 2; ++n) {
+                for (int n = 0; n < NN; ++n) {
                     const uint32_t scv = hb ? q4k_scale<2 * u + 1, false>(s0[n], s1[n], s2[n])
                                             : q4k_scale<2 * u, false>(s0[n], s1[n], s2[n]);
                     const _Float16 sc = (_Float16)(float)scv;
@@ -624,10 +635,10 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
 #pragma unroll
                 for (int m8 = 0; m8 < 2; ++m8)
 #pragma unroll
-                    for (int m = 0; m < 2; ++m) {
+                    for (int m = 0; m < NM; ++m) {
                         const f16x8 av = frag(cur, m, 32 * hb + 16 * h + 8 * m8);
 #pragma unroll
-                        for (int n = 0; n < 2; ++n) P[m][n] = mfma(av, bq[n][m8], P[m][n]);
+                        for (int n = 0; n < NN; ++n) P[m][n] = mfma(av, bq[n][m8], P[m][n]);
                     }
             }
             if constexpr (u == 3) {
@@ -635,7 +646,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
                 // A'[tok][8h+e] = split code sum of sub-block e (hi piece h = 0, lo piece h = 1),
                 // B'[8h+e][row] = m_e.
 #pragma unroll
-                for (int n = 0; n < 2; ++n) {
+                for (int n = 0; n < NN; ++n) {
                     const f16x2 m01 = {(_Float16)(float)q4k_scale<0, true>(s0[n], s1[n], s2[n]),
                                        (_Float16)(float)q4k_scale<1, true>(s0[n], s1[n], s2[n])};
                     const f16x2 m23 = {(_Float16)(float)q4k_scale<2, true>(s0[n], s1[n], s2[n]),
@@ -646,7 +657,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
                                        (_Float16)(float)q4k_scale<7, true>(s0[n], s1[n], s2[n])};
                     const f16x8 bm = pack8(as_u(m01), as_u(m23), as_u(m45), as_u(m67));
 #pragma unroll
-                    for (int m = 0; m < 2; ++m) {
+                    for (int m = 0; m < NM; ++m) {
                         const f16x8 am = *reinterpret_cast<const f16x8 *>(cur + rb::kActBytes + (32 * m + j) * 32 + 16 * h);
                         const f32x16 pm = mfma(am, bm, (f32x16){});
 #pragma unroll
@@ -679,12 +690,12 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t rt = ah_rsrc(a.tok_scale + tok0, ntile * 4u);
     const bool scaled = a.splits == 1;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
+    for (int m = 0; m < NM; ++m) {
         uint32_t sc[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] = ah_ld32(rt, 4 * (32 * m + 8 * (r / 4) + 4 * h + (r % 4)));
 #pragma unroll
-        for (int n = 0; n < 2; ++n) {
+        for (int n = 0; n < NN; ++n) {
             const uint32_t row = row_w + 32 * n + j;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {

@@ -568,115 +568,88 @@ AH_DEV int wave_max(int v) {
     }
     return v;
 }
-AH_DEV uint32_t wave_max_u(uint32_t v) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = (uint32_t)__shfl_xor((int)v, o, 64);
-        v = t > v ? t : v;
-    }
-    return v;
-}
-
-// GEMM activation operand straight from the input, one workgroup per token.  The token's largest
-// block exponent E is the exponent of its largest magnitude (act_scale is monotone in absmax,
-// kern/pow2.rs:11-39), so a first pass reduces |x|; a second quantizes every 32-block bit-exactly
-// (quant_act, chart/mod.rs:258-334, refusals recorded as quant_kernel does) and writes
+// GEMM activation operand straight from the input, one workgroup per token.  Every 32-block is
+// quantized once, bit-exactly (quant_act, chart/mod.rs:258-334; refusals recorded as quant_kernel
+// does), into LDS.  The token's largest block exponent E is then the max of the block exponents
+// (act_scale is monotone in absmax, kern/pow2.rs:11-39), and a second pass over LDS writes
 //   xh   = xq * 2^(e_b - E) in f16 (exact whenever e_b - E >= -24),
 //   tok_scale = 2^(E - 32),
 //   xmin (Q4_K) = per 32-block code sum X split exactly as [64*floor(X/64), X mod 64] * 2^(e_b - E),
 //        laid out per super-block as [hi 0..7, lo 0..7].
 // With codes input (AH_SRC_CODES) the block exponents come from the power-of-two scales.
+// The source kind is a template parameter: the three quantizer paths do not share one body.
+constexpr uint32_t kOpMaxBlocks = AH_MAX_N_IN / 32;
+template <uint32_t SRC>
 __global__ void __launch_bounds__(kThreads) gemm_operand_kernel(OperandArgs o) {
-    __shared__ uint32_t red[2][kThreads / 64];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ uint32_t red[kThreads / 64];
+    __shared__ u32x2 lcodes[kOpMaxBlocks * 4];  // 8 codes per quad lane
+    __shared__ int lexp[kOpMaxBlocks], lsum[kOpMaxBlocks];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = tid & 3;
     const uint32_t tok = blockIdx.x;
     const size_t row = (size_t)tok * o.n_in;
-    const uint32_t esz = o.src == AH_SRC_F32 ? 4u : o.src == AH_SRC_Q32 ? 8u : 1u;
-    const ActRsrc r = act_rsrc(static_cast<const uint8_t *>(o.x) + row * esz,
-                               o.src == AH_SRC_CODES ? o.scales + (size_t)tok * o.nb32 : nullptr, o.src,
-                               o.n_in);
-    // pass 1: E
-    int E = -1;
-    if (o.src == AH_SRC_F32) {
-        uint32_t mb = 0;
-        for (uint32_t c = tid; 4 * c < o.n_in; c += kThreads) {
-            const u32x4 v = ah_ld128(r.x, 16 * c);
-            const uint32_t a = (v.x & 0x7fffffffu) > (v.y & 0x7fffffffu) ? (v.x & 0x7fffffffu) : (v.y & 0x7fffffffu);
-            const uint32_t b = (v.z & 0x7fffffffu) > (v.w & 0x7fffffffu) ? (v.z & 0x7fffffffu) : (v.w & 0x7fffffffu);
-            const uint32_t m = a > b ? a : b;
-            mb = m > mb ? m : mb;
+    const uint32_t esz = SRC == AH_SRC_F32 ? 4u : SRC == AH_SRC_Q32 ? 8u : 1u;
+    const int64_t *srow = SRC == AH_SRC_CODES ? o.scales + (size_t)tok * o.nb32 : nullptr;
+    const ActRsrc r = act_rsrc(static_cast<const uint8_t *>(o.x) + row * esz, srow, SRC, o.n_in);
+    const uint32_t nbp = o.kpad / 32;
+    // pass 1: quantize every block into LDS; E = the largest block exponent.  Four rounds of
+    // blocks are requested before any is quantized, so their loads are in flight together.
+    constexpr uint32_t kRounds = 4, kPer = kThreads / 4;
+    int emax = -1;
+    for (uint32_t base = 0; base < nbp; base += kRounds * kPer) {
+        QuadIn in[kRounds];
+#pragma unroll
+        for (uint32_t u = 0; u < kRounds; ++u) {
+            const uint32_t b = base + u * kPer + tid / 4;
+            // codes rows start at tok * n_in bytes, not always a dword boundary: bytewise loads
+            in[u] = SRC == AH_SRC_CODES ? quad_load(o.x, srow, SRC, o.n_in, row, b, b < o.nb32)
+                                          : quad_load_row(r, SRC, o.n_in, b);
         }
-        mb = wave_max_u(mb);
-        if (lane == 0) red[0][wave] = mb;
-        __syncthreads();
 #pragma unroll
-        for (int w = 0; w < kThreads / 64; ++w) mb = red[0][w] > mb ? red[0][w] : mb;
-        uint64_t mag;
-        bool neg;
-        if (ah_to_q32_mag(mb, mag, neg) == 0) E = ah_act_scale_exp(mag);  // else refused below
-    } else if (o.src == AH_SRC_Q32) {
-        uint64_t mm = 0;
-        for (uint32_t c = tid; 2 * c < o.n_in; c += kThreads) {
-            const u32x4 v = ah_ld128(r.x, 16 * c);
-            const int64_t a = (int64_t)(((uint64_t)v.y << 32) | v.x), b = (int64_t)(((uint64_t)v.w << 32) | v.z);
-            const uint64_t ma = a < 0 ? 0ull - (uint64_t)a : (uint64_t)a, mbb = b < 0 ? 0ull - (uint64_t)b : (uint64_t)b;
-            const uint64_t m = ma > mbb ? ma : mbb;
-            mm = m > mm ? m : mm;
+        for (uint32_t u = 0; u < kRounds; ++u) {
+            if (base + u * kPer >= nbp) break;  // uniform: rounds past the padded row
+            const uint32_t b = base + u * kPer + tid / 4;
+            const QuadOut qo = quad_quant(in[u], SRC, b, o.status, (unsigned long long)row);
+            int e = qo.e;
+            if (SRC == AH_SRC_CODES) {
+                const u32x2 sv = ah_ld64(r.s, 8 * b);
+                const uint64_t S = ((uint64_t)sv.y << 32) | sv.x;
+                e = (int64_t)S > 0 ? 63 - __builtin_clzll(S) : -1;
+            }
+            if (b < nbp) {
+                lcodes[4 * b + q] = (u32x2){qo.c0, qo.c1};
+                if (q == 0) {
+                    lexp[b] = e;
+                    lsum[b] = qo.s32;
+                }
+                emax = e > emax ? e : emax;
+            }
         }
-        // 64-bit max: the high words first, then the low words among the lanes that hold it
-        uint32_t hi = wave_max_u((uint32_t)(mm >> 32));
-        if (lane == 0) red[0][wave] = hi;
-        __syncthreads();
-#pragma unroll
-        for (int w = 0; w < kThreads / 64; ++w) hi = red[0][w] > hi ? red[0][w] : hi;
-        uint32_t lo = wave_max_u((uint32_t)(mm >> 32) == hi ? (uint32_t)mm : 0u);
-        if (lane == 0) red[1][wave] = lo;
-        __syncthreads();
-#pragma unroll
-        for (int w = 0; w < kThreads / 64; ++w) lo = red[1][w] > lo ? red[1][w] : lo;
-        E = ah_act_scale_exp(((uint64_t)hi << 32) | lo);
-    } else {
-        for (uint32_t b = tid; b < o.nb32; b += kThreads) {
-            const u32x2 sv = ah_ld64(r.s, 8 * b);
-            const uint64_t S = ((uint64_t)sv.y << 32) | sv.x;
-            const int e = (int64_t)S > 0 ? 63 - __builtin_clzll(S) : -1;
-            E = e > E ? e : E;
-        }
-        E = wave_max(E);
-        if (lane == 0) red[0][wave] = (uint32_t)(E + 1);
-        __syncthreads();
-#pragma unroll
-        for (int w = 0; w < kThreads / 64; ++w) E = (int)red[0][w] - 1 > E ? (int)red[0][w] - 1 : E;
     }
+    emax = wave_max(emax);
+    if (lane == 0) red[wave] = (uint32_t)(emax + 1);
+    __syncthreads();
+    int E = -1;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) E = (int)red[w] - 1 > E ? (int)red[w] - 1 : E;
     if (E > 62) E = 62;  // a block without a Q32.32 scale: the call is refused anyway
     if (tid == 0) o.tok_scale[tok] = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
-    // pass 2: codes -> operand
-    const uint32_t nbp = o.kpad / 32, q = lane & 3;
+    // pass 2: LDS -> f16 operand
     _Float16 *xh = o.xh + (size_t)tok * o.kpad;
     for (uint32_t base = 0; base < nbp; base += kThreads / 4) {
         const uint32_t b = base + tid / 4;
-        // codes rows start at tok * n_in bytes, not always a dword boundary: bytewise loads there
-        const QuadIn in = o.src == AH_SRC_CODES
-                              ? quad_load(o.x, o.scales + (size_t)tok * o.nb32, o.src, o.n_in, row, b, b < o.nb32)
-                              : quad_load_row(r, o.src, o.n_in, b);
-        const QuadOut qo = quad_quant(in, o.src, b, o.status, (unsigned long long)row);
-        int e = qo.e;
-        if (o.src == AH_SRC_CODES) {
-            const u32x2 sv = ah_ld64(r.s, 8 * b);
-            const uint64_t S = ((uint64_t)sv.y << 32) | sv.x;
-            e = (int64_t)S > 0 ? 63 - __builtin_clzll(S) : -1;
-        }
-        if (b >= nbp) continue;
+        if (b >= nbp) break;
+        const u32x2 cw = lcodes[4 * b + q];
+        const int e = lexp[b];
         const int sh = e - E;
         _Float16 hv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int c = (int)(int8_t)(((i < 4 ? qo.c0 : qo.c1) >> (8 * (i & 3))) & 0xffu);
+            const int c = (int)(int8_t)(((i < 4 ? cw.x : cw.y) >> (8 * (i & 3))) & 0xffu);
             hv[i] = e < 0 ? (_Float16)0.0f : (_Float16)__builtin_ldexpf((float)c, sh);
         }
         *reinterpret_cast<u32x4 *>(xh + 32 * b + 8 * q) = __builtin_bit_cast(u32x4, hv);
         if (o.xmin && q == 0) {
-            const int X = qo.s32;
+            const int X = lsum[b];
             const int hq = (X >= 0 ? X : X - 63) / 64;  // floor(X / 64)
             _Float16 *m = o.xmin + ((size_t)tok * (o.kpad / 256) + b / 8) * 16;
             m[b % 8] = e < 0 ? (_Float16)0.0f : (_Float16)__builtin_ldexpf((float)(64 * hq), sh);
@@ -984,7 +957,12 @@ hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart 
 
 hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream) {
     if (o.n_tok == 0) return hipSuccess;
-    hipLaunchKernelGGL(gemm_operand_kernel, dim3(o.n_tok), dim3(kThreads), 0, stream, o);
+    switch (o.src) {
+    case AH_SRC_F32: hipLaunchKernelGGL(gemm_operand_kernel<AH_SRC_F32>, dim3(o.n_tok), dim3(kThreads), 0, stream, o); break;
+    case AH_SRC_Q32: hipLaunchKernelGGL(gemm_operand_kernel<AH_SRC_Q32>, dim3(o.n_tok), dim3(kThreads), 0, stream, o); break;
+    case AH_SRC_CODES: hipLaunchKernelGGL(gemm_operand_kernel<AH_SRC_CODES>, dim3(o.n_tok), dim3(kThreads), 0, stream, o); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -402,14 +402,36 @@ int32_t ah_upload_weight(ah_ctx *ctx, uint32_t type, const void *raw, size_t raw
         const uint16_t h1 = (uint16_t)(b[off + o1] | (b[off + o1 + 1] << 8));
         if (f16_nonfinite(h0) || f16_nonfinite(h1)) return AH_ERR_NONFINITE_SCALE;
     }
+    // A Q4_K row whose K is not a multiple of 256 ends in a partial super-block whose trailing qs
+    // chunks the product never reads; the device copy keeps each row's leading `stride` bytes only
+    // (16-byte aligned).  The last unit of a row then reads into the next row, or past the tensor,
+    // against zero activations: the kernels' LDS tiles carry the slack for it.
+    size_t stride = row_bytes;
+    if (type == AH_GGML_Q4_K && n_in % 256 && n_in <= 8192)
+        stride = 144 * (n_in / 256) + 16 + 32 * ((n_in % 256 + 63) / 64);
+    const size_t dev_bytes = n_out * stride;
+    const void *src = raw;
+    uint8_t *packed = nullptr;
+    if (stride != row_bytes) {
+        packed = static_cast<uint8_t *>(std::malloc(dev_bytes ? dev_bytes : 1));
+        if (!packed) return AH_ERR_OUT_OF_MEMORY;
+        for (size_t r = 0; r < n_out; ++r) std::memcpy(packed + r * stride, b + r * row_bytes, stride);
+        src = packed;
+    }
     ah_tensor *t = new (std::nothrow) ah_tensor();
-    if (!t) return AH_ERR_OUT_OF_MEMORY;
+    if (!t) {
+        std::free(packed);
+        return AH_ERR_OUT_OF_MEMORY;
+    }
     AH_HIP(ctx, hipSetDevice(ctx->device));
-    if (hipMalloc(&t->d, need + 256) != hipSuccess) {
+    if (hipMalloc(&t->d, dev_bytes + 256) != hipSuccess) {
+        std::free(packed);
         delete t;
         return AH_ERR_OUT_OF_MEMORY;
     }
-    if (hipMemcpy(t->d, raw, need, hipMemcpyHostToDevice) != hipSuccess) {
+    const hipError_t ce = hipMemcpy(t->d, src, dev_bytes, hipMemcpyHostToDevice);
+    std::free(packed);
+    if (ce != hipSuccess) {
         hipFree(t->d);
         delete t;
         return AH_ERR_HIP;
@@ -417,8 +439,8 @@ int32_t ah_upload_weight(ah_ctx *ctx, uint32_t type, const void *raw, size_t raw
     t->type = type;
     t->n_out = n_out;
     t->n_in = n_in;
-    t->row_bytes = row_bytes;
-    t->bytes = need;
+    t->row_bytes = stride;
+    t->bytes = dev_bytes;
     t->owned = true;
     *out = t;
     return AH_OK;

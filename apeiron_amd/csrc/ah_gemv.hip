@@ -322,6 +322,9 @@ AH_DEV GemvPart load_part(const GemvPart &single, const GemvPart *__restrict__ p
 
 // Q8_0 block at byte `off` of the tile (format/quant.rs:238-250): f16 d at byte 0, 32 int8 codes
 // at 2..33.  Blocks are 2-byte aligned: 9 dwords from the 4-aligned address below are realigned.
+// DOTS: the debug entry point's exact group dots are stored (a runtime null check); without it the
+// code has no store and no ragged-row case (blocks past n_in meet zero activations and add 0).
+template <bool DOTS>
 AH_DEV float unit_q8(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &A, int32_t *dots) {
     const uint32_t sh = off & 3u;
     const uint32_t *p = reinterpret_cast<const uint32_t *>(tl + (off & ~3u));
@@ -338,7 +341,7 @@ AH_DEV float unit_q8(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &
         const uint32_t c = sh ? w[i + 1] : ah_alignbyte(w[i + 1], w[i], 2);
         D = ah_sdot4(c, xw[i], D);
     }
-    if (dots) dots[b] = D;
+    if (DOTS && dots) dots[b] = D;
     return ah_f16_bits_to_f32(d16) * A.fsc[b] * (float)D;
 }
 
@@ -361,9 +364,10 @@ AH_DEV void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &m
 // Q4_K super-block s (format/quant.rs:481-510): d, dmin, 12 packed 6-bit (scale, min) pairs,
 // 128 bytes of nibbles; sub-block j takes the low (j even) / high (j odd) nibbles of
 // qs[32*(j/2) + l].  Term per sub-block: S_j * (d*sc_j*D_j - dmin*m_j*X_j).
-template <int P>
+template <int P, bool DOTS>
 AH_DEV float q4k_pair(const u32x4 *sb, uint32_t s0, uint32_t s1, uint32_t s2, float fd, float fdm,
-                      uint32_t g0, uint32_t nb32, const ActLds &A, int32_t *dots) {
+                      uint32_t g0, uint32_t nb32, const ActLds &A, int32_t *dots, float flo, float fhi,
+                      int32_t xlo, int32_t xhi) {
     const u32x4 qa = sb[1 + 2 * P], qb = sb[2 + 2 * P];
     const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
     const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g0));
@@ -379,26 +383,36 @@ AH_DEV float q4k_pair(const u32x4 *sb, uint32_t s0, uint32_t s1, uint32_t s2, fl
     int sl, ml, shh, mh;
     q4k_scale_min<2 * P>(s0, s1, s2, sl, ml);
     q4k_scale_min<2 * P + 1>(s0, s1, s2, shh, mh);
-    if (dots) {
+    if (DOTS && dots) {
         dots[g0] = Dlo;
         if (g0 + 1 < nb32) dots[g0 + 1] = Dhi;  // a ragged row ends on an odd sub-block
     }
-    const float tlo = fd * (float)(sl * Dlo) - fdm * (float)(ml * A.xs32[g0]);
-    const float thi = fd * (float)(shh * Dhi) - fdm * (float)(mh * A.xs32[g0 + 1]);
-    return A.fsc[g0] * tlo + A.fsc[g0 + 1] * thi;
+    const float tlo = fd * (float)(sl * Dlo) - fdm * (float)(ml * xlo);
+    const float thi = fd * (float)(shh * Dhi) - fdm * (float)(mh * xhi);
+    return flo * tlo + fhi * thi;
 }
+template <bool DOTS>
 AH_DEV float unit_q4(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in, const ActLds &A,
                      int32_t *dots) {
     const u32x4 *sb = reinterpret_cast<const u32x4 *>(tl + off);  // 16-byte aligned
     const u32x4 h = sb[0];
+    // the super-block's eight activation scales and code sums, read ahead of the pairs
+    float fs[8];
+    int32_t xs[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        fs[i] = A.fsc[8 * s + i];
+        xs[i] = A.xs32[8 * s + i];
+    }
     const float fd = ah_f16_bits_to_f32(h.x & 0xffffu), fdm = ah_f16_bits_to_f32(h.x >> 16);
     const uint32_t nb32 = (n_in + 31) / 32, rem = n_in - 256 * s;
-    const uint32_t npairs = rem >= 256 ? 4u : (rem + 63) / 64;  // a ragged row uses fewer pairs
+    // a ragged row's last super-block uses fewer pairs; without DOTS the rest meet zero activations
+    const uint32_t npairs = !DOTS || rem >= 256 ? 4u : (rem + 63) / 64;
     const uint32_t g = 8 * s;
-    float acc = q4k_pair<0>(sb, h.y, h.z, h.w, fd, fdm, g, nb32, A, dots);
-    if (npairs > 1) acc += q4k_pair<1>(sb, h.y, h.z, h.w, fd, fdm, g + 2, nb32, A, dots);
-    if (npairs > 2) acc += q4k_pair<2>(sb, h.y, h.z, h.w, fd, fdm, g + 4, nb32, A, dots);
-    if (npairs > 3) acc += q4k_pair<3>(sb, h.y, h.z, h.w, fd, fdm, g + 6, nb32, A, dots);
+    float acc = q4k_pair<0, DOTS>(sb, h.y, h.z, h.w, fd, fdm, g, nb32, A, dots, fs[0], fs[1], xs[0], xs[1]);
+    if (npairs > 1) acc += q4k_pair<1, DOTS>(sb, h.y, h.z, h.w, fd, fdm, g + 2, nb32, A, dots, fs[2], fs[3], xs[2], xs[3]);
+    if (npairs > 2) acc += q4k_pair<2, DOTS>(sb, h.y, h.z, h.w, fd, fdm, g + 4, nb32, A, dots, fs[4], fs[5], xs[4], xs[5]);
+    if (npairs > 3) acc += q4k_pair<3, DOTS>(sb, h.y, h.z, h.w, fd, fdm, g + 6, nb32, A, dots, fs[6], fs[7], xs[6], xs[7]);
     return acc;
 }
 
@@ -406,6 +420,7 @@ AH_DEV float unit_q4(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
 // f16 d @208.  Element 128n + 32t + l = (nibble t/2 of ql[64n + 32(t&1) + l]
 // | ((qh[32n + l] >> 2t) & 3) << 4) - 32.  Super-blocks are 2-byte aligned: 54 dwords from the
 // 4-aligned address below are realigned.
+template <bool DOTS>
 AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in, const ActLds &A,
                      int32_t *dots16) {
     const uint32_t sh = off & 3u;
@@ -416,7 +431,7 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
     float acc = 0.0f;
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
-        if (8 * s + 4 * n >= nb32) break;  // a ragged row may end after the first half
+        if (DOTS && 8 * s + 4 * n >= nb32) break;  // a ragged row may end after the first half
         uint32_t qh[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) qh[i] = V(32 + 8 * n + i);
@@ -424,7 +439,7 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const uint32_t g = 8 * s + 4 * n + t;
-            if (g >= nb32) break;
+            if (DOTS && g >= nb32) break;
             const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g));
             const u32x4 x0 = xv[0], x1 = xv[1];
             const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -444,7 +459,7 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
             const uint32_t scw = (t >> 1) ? scw1 : scw0;
             const int sclo = (int)(int8_t)((scw >> (16 * (t & 1))) & 0xffu);
             const int schi = (int)(int8_t)((scw >> (16 * (t & 1) + 8)) & 0xffu);
-            if (dots16) {
+            if (DOTS && dots16) {
                 dots16[2 * g] = Dlo;
                 if (2 * g + 1 < nb16) dots16[2 * g + 1] = Dhi;  // ragged row ends on a 16-group
             }
@@ -454,24 +469,24 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
     return acc;
 }
 
-template <int TYPE>
+template <int TYPE, bool DOTS>
 AH_DEV float comp_unit(const GemvPart &P, const uint8_t *tl, uint32_t off, uint32_t row, uint32_t u,
                        const ActLds &A) {
     if constexpr (TYPE == AH_GGML_Q8_0) {
         const uint32_t nb32 = (P.n_in + 31) / 32;
-        return unit_q8(tl, off, u, A, P.dots ? P.dots + (size_t)row * nb32 : nullptr);
+        return unit_q8<DOTS>(tl, off, u, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
     } else if constexpr (TYPE == AH_GGML_Q4_K) {
         const uint32_t nb32 = (P.n_in + 31) / 32;
-        return unit_q4(tl, off, u, P.n_in, A, P.dots ? P.dots + (size_t)row * nb32 : nullptr);
+        return unit_q4<DOTS>(tl, off, u, P.n_in, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
     } else {
         const uint32_t nb16 = (P.n_in + 15) / 16;
-        return unit_q6(tl, off, u, P.n_in, A, P.dots ? P.dots + (size_t)row * nb16 : nullptr);
+        return unit_q6<DOTS>(tl, off, u, P.n_in, A, DOTS && P.dots ? P.dots + (size_t)row * nb16 : nullptr);
     }
 }
 
 constexpr uint32_t kUnitBytes(int type) { return type == AH_GGML_Q8_0 ? 34u : type == AH_GGML_Q4_K ? 144u : 210u; }
 constexpr uint32_t kRedSlots = 1024;  // unit partials of one tile
-constexpr uint32_t kTileSlack = 64;   // bytes past a tile that realigned unit reads may touch
+constexpr uint32_t kTileSlack = 128;  // bytes past a tile that realigned or compact-row unit reads may touch
 
 // One workgroup streams whole-row tiles of a part.  A tile's bytes are loaded with 16-byte
 // buffer loads in which consecutive lanes take consecutive chunks (each wave instruction reads
@@ -521,7 +536,7 @@ __global__ void __launch_bounds__(kThreads)
         for (uint32_t f = threadIdx.x; f < TU; f += kThreads) {
             const uint32_t r = f / U, u = f - r * U, row = tile * R + r;
             float v = 0.0f;
-            if (row < P.n_out) v = comp_unit<TYPE>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
+            if (row < P.n_out) v = comp_unit<TYPE, true>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
             A.red[f] = v;
         }
         ah_lds_barrier();
@@ -713,12 +728,13 @@ constexpr uint32_t kSThreads = 512;                // threads of a streaming wor
 constexpr uint32_t kSWaves = kSThreads / 64;
 constexpr uint32_t kChunks = 8;                    // 16-byte loads per lane per tile
 constexpr uint32_t kStreamTile = kChunks * 1024;   // bytes per tile
-constexpr uint32_t kSlotBytes = kStreamTile + 32;  // + what realigned unit reads touch past a tile
+constexpr uint32_t kSlotBytes = kStreamTile + 128; // + what realigned or compact-row unit reads touch past a tile
 constexpr uint32_t kOob = 0xFFFFFFF0u;             // past any payload (payloads stay below 4 GiB - 256)
 
 // PLAN: the workgroup's part comes from a plan's table (else the launch argument); either way the
 // descriptor is read with scalar loads, which do not queue behind the vector memory stream.
-template <int TYPE, bool PLAN>
+// DOTS: the debug form that also stores exact group dots (single launches only).
+template <int TYPE, bool PLAN, bool DOTS>
 __global__ void __launch_bounds__(kSThreads)
     gemv_stream_kernel(GemvPart single, const GemvPart *__restrict__ parts,
                        const uint32_t *__restrict__ wg_part, uint32_t kpad_max,
@@ -806,7 +822,7 @@ __global__ void __launch_bounds__(kSThreads)
         float acc = 0.0f;
         if (owns) {
             for (uint32_t u = g; u < U; u += G)
-                acc += comp_unit<TYPE>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
+                acc += comp_unit<TYPE, DOTS>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
         }
         acc = group_sum(acc, G);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), ry,
@@ -838,9 +854,10 @@ size_t ah_gemv_stream_lds_bytes(uint32_t kpad_max) {
 
 uint32_t ah_gemv_stream_threads() { return kSThreads; }
 
-static const void *stream_fn(uint32_t type, bool plan) {
-#define AH_SFN(T) return plan ? reinterpret_cast<const void *>(&gemv_stream_kernel<T, true>)            \
-                              : reinterpret_cast<const void *>(&gemv_stream_kernel<T, false>);
+static const void *stream_fn(uint32_t type, bool plan, bool dots = false) {
+#define AH_SFN(T) return plan ? reinterpret_cast<const void *>(&gemv_stream_kernel<T, true, false>)     \
+                      : dots ? reinterpret_cast<const void *>(&gemv_stream_kernel<T, false, true>)     \
+                             : reinterpret_cast<const void *>(&gemv_stream_kernel<T, false, false>);
     switch (type) {
     case AH_GGML_Q8_0: AH_SFN(AH_GGML_Q8_0)
     case AH_GGML_Q4_K: AH_SFN(AH_GGML_Q4_K)
@@ -865,10 +882,13 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const Ge
     const size_t lds = ah_gemv_stream_lds_bytes(kpad_max);
 #define AH_SLAUNCH(T)                                                                              \
     if (d_parts)                                                                                   \
-        hipLaunchKernelGGL((gemv_stream_kernel<T, true>), dim3(grid), dim3(kSThreads), lds, stream, \
-                           single, d_parts, d_wg_part, kpad_max, status);                         \
+        hipLaunchKernelGGL((gemv_stream_kernel<T, true, false>), dim3(grid), dim3(kSThreads), lds,  \
+                           stream, single, d_parts, d_wg_part, kpad_max, status);                 \
+    else if (single.dots)                                                                          \
+        hipLaunchKernelGGL((gemv_stream_kernel<T, false, true>), dim3(grid), dim3(kSThreads), lds,  \
+                           stream, single, d_parts, d_wg_part, kpad_max, status);                 \
     else                                                                                           \
-        hipLaunchKernelGGL((gemv_stream_kernel<T, false>), dim3(grid), dim3(kSThreads), lds,       \
+        hipLaunchKernelGGL((gemv_stream_kernel<T, false, false>), dim3(grid), dim3(kSThreads), lds, \
                            stream, single, d_parts, d_wg_part, kpad_max, status);
     switch (type) {
     case AH_GGML_Q8_0: AH_SLAUNCH(AH_GGML_Q8_0) break;
@@ -930,8 +950,9 @@ hipError_t ah_gemv_init_attrs() {
     AH_ATTR(AH_GGML_Q6_K, 4) AH_ATTR(AH_GGML_Q6_K, 8) AH_ATTR(AH_GGML_Q6_K, 12)
 #undef AH_ATTR
     for (uint32_t t : {AH_GGML_Q8_0, AH_GGML_Q4_K, AH_GGML_Q6_K})
-        for (bool plan : {false, true})
-            if (e == hipSuccess) e = hipFuncSetAttribute(stream_fn(t, plan), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+        for (int v = 0; v < 3; ++v)
+            if (e == hipSuccess)
+                e = hipFuncSetAttribute(stream_fn(t, v == 1, v == 2), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     return e;
 }
 

@@ -157,7 +157,7 @@ def test_gemv_golden_fixtures(dev):
 
 @pytest.mark.parametrize("t", [8, 12, 14])
 @pytest.mark.parametrize("n_out,n_in", [(4864, 896), (896, 4864), (128, 896), (333, 1536), (37, 8960), (5, 100),
-                                         (7, 32768), (9, 20000)])
+                                         (301, 300), (2001, 576), (7, 32768), (9, 20000)])
 def test_gemv_config_shapes(dev, t, n_out, n_in):
     rng = synth.rng_for(1, t * 1000 + n_in)
     raw = synth.payload(t, rng, n_out, n_in)

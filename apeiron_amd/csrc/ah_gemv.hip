@@ -345,29 +345,40 @@ AH_DEV float unit_q8(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &
     return ah_f16_bits_to_f32(d16) * A.fsc[b] * (float)D;
 }
 
-// get_scale_min_k4 (format/quant.rs:482-491) on the 12 packed bytes held in three dwords.
-AH_DEV uint32_t sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
-    const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
-    return (w >> (8 * (i & 3))) & 0xffu;
-}
-template <int J>
-AH_DEV void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &m) {
-    if (J < 4) {
-        sc = sbyte(s0, s1, s2, J) & 63;
-        m = sbyte(s0, s1, s2, J + 4) & 63;
-    } else {
-        sc = (sbyte(s0, s1, s2, J + 4) & 0xF) | ((sbyte(s0, s1, s2, J - 4) >> 6) << 4);
-        m = (sbyte(s0, s1, s2, J + 4) >> 4) | ((sbyte(s0, s1, s2, J) >> 6) << 4);
-    }
-}
-
 // Q4_K super-block s (format/quant.rs:481-510): d, dmin, 12 packed 6-bit (scale, min) pairs,
 // 128 bytes of nibbles; sub-block j takes the low (j even) / high (j odd) nibbles of
 // qs[32*(j/2) + l].  Term per sub-block: S_j * (d*sc_j*D_j - dmin*m_j*X_j).
+//
+// The eight (sc, m) pairs of get_scale_min_k4 (format/quant.rs:482-491) unpack as four words of
+// four bytes each: sc 0-3 = b[0..3] & 63, m 0-3 = b[4..7] & 63, sc 4-7 = (b[8..11] & 15) |
+// (b[0..3] >> 6) << 4, m 4-7 = (b[8..11] >> 4) | (b[4..7] >> 6) << 4.  d*sc_j and dmin*m_j are
+// formed once per super-block; the per-sub-block arithmetic is f32 (no integer multiplies).
+struct Q4kScales {
+    float dsc[8], dm[8];
+};
+AH_DEV Q4kScales q4k_scales(uint32_t s0, uint32_t s1, uint32_t s2, float fd, float fdm) {
+    const uint32_t sc03 = s0 & 0x3F3F3F3Fu, m03 = s1 & 0x3F3F3F3Fu;
+    const uint32_t sc47 = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t m47 = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+    Q4kScales q;
+    const uint32_t w[4] = {sc03, sc47, m03, m47};
+    float b[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) b[4 * i + k] = (float)((w[i] >> (8 * k)) & 0xffu);  // v_cvt_f32_ubyteN
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        q.dsc[j] = fd * b[j];
+        q.dm[j] = fdm * b[8 + j];
+    }
+    return q;
+}
+
 template <int P, bool DOTS>
-AH_DEV float q4k_pair(const u32x4 *sb, uint32_t s0, uint32_t s1, uint32_t s2, float fd, float fdm,
-                      uint32_t g0, uint32_t nb32, const ActLds &A, int32_t *dots, float flo, float fhi,
-                      int32_t xlo, int32_t xhi) {
+AH_DEV float q4k_pair(const u32x4 *sb, const Q4kScales &q4, uint32_t g0, uint32_t nb32, const ActLds &A,
+                      int32_t *dots, float flo, float fhi, float xlo, float xhi) {
     const u32x4 qa = sb[1 + 2 * P], qb = sb[2 + 2 * P];
     const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
     const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g0));
@@ -380,15 +391,12 @@ AH_DEV float q4k_pair(const u32x4 *sb, uint32_t s0, uint32_t s1, uint32_t s2, fl
         Dlo = ah_sdot4(q[i] & 0x0F0F0F0Fu, xl[i], Dlo);
         Dhi = ah_sdot4((q[i] >> 4) & 0x0F0F0F0Fu, xh[i], Dhi);
     }
-    int sl, ml, shh, mh;
-    q4k_scale_min<2 * P>(s0, s1, s2, sl, ml);
-    q4k_scale_min<2 * P + 1>(s0, s1, s2, shh, mh);
     if (DOTS && dots) {
         dots[g0] = Dlo;
         if (g0 + 1 < nb32) dots[g0 + 1] = Dhi;  // a ragged row ends on an odd sub-block
     }
-    const float tlo = fd * (float)(sl * Dlo) - fdm * (float)(ml * xlo);
-    const float thi = fd * (float)(shh * Dhi) - fdm * (float)(mh * xhi);
+    const float tlo = q4.dsc[2 * P] * (float)Dlo - q4.dm[2 * P] * xlo;
+    const float thi = q4.dsc[2 * P + 1] * (float)Dhi - q4.dm[2 * P + 1] * xhi;
     return flo * tlo + fhi * thi;
 }
 template <bool DOTS>
@@ -397,22 +405,22 @@ AH_DEV float unit_q4(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
     const u32x4 *sb = reinterpret_cast<const u32x4 *>(tl + off);  // 16-byte aligned
     const u32x4 h = sb[0];
     // the super-block's eight activation scales and code sums, read ahead of the pairs
-    float fs[8];
-    int32_t xs[8];
+    float fs[8], xs[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         fs[i] = A.fsc[8 * s + i];
-        xs[i] = A.xs32[8 * s + i];
+        xs[i] = (float)A.xs32[8 * s + i];  // |X| <= 32 * 128: exact
     }
     const float fd = ah_f16_bits_to_f32(h.x & 0xffffu), fdm = ah_f16_bits_to_f32(h.x >> 16);
+    const Q4kScales q4 = q4k_scales(h.y, h.z, h.w, fd, fdm);
     const uint32_t nb32 = (n_in + 31) / 32, rem = n_in - 256 * s;
     // a ragged row's last super-block uses fewer pairs; without DOTS the rest meet zero activations
     const uint32_t npairs = !DOTS || rem >= 256 ? 4u : (rem + 63) / 64;
     const uint32_t g = 8 * s;
-    float acc = q4k_pair<0, DOTS>(sb, h.y, h.z, h.w, fd, fdm, g, nb32, A, dots, fs[0], fs[1], xs[0], xs[1]);
-    if (npairs > 1) acc += q4k_pair<1, DOTS>(sb, h.y, h.z, h.w, fd, fdm, g + 2, nb32, A, dots, fs[2], fs[3], xs[2], xs[3]);
-    if (npairs > 2) acc += q4k_pair<2, DOTS>(sb, h.y, h.z, h.w, fd, fdm, g + 4, nb32, A, dots, fs[4], fs[5], xs[4], xs[5]);
-    if (npairs > 3) acc += q4k_pair<3, DOTS>(sb, h.y, h.z, h.w, fd, fdm, g + 6, nb32, A, dots, fs[6], fs[7], xs[6], xs[7]);
+    float acc = q4k_pair<0, DOTS>(sb, q4, g, nb32, A, dots, fs[0], fs[1], xs[0], xs[1]);
+    if (npairs > 1) acc += q4k_pair<1, DOTS>(sb, q4, g + 2, nb32, A, dots, fs[2], fs[3], xs[2], xs[3]);
+    if (npairs > 2) acc += q4k_pair<2, DOTS>(sb, q4, g + 4, nb32, A, dots, fs[4], fs[5], xs[4], xs[5]);
+    if (npairs > 3) acc += q4k_pair<3, DOTS>(sb, q4, g + 6, nb32, A, dots, fs[6], fs[7], xs[6], xs[7]);
     return acc;
 }
 

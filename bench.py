@@ -44,6 +44,20 @@ LAYERS = 24
 SHAPES = [("q", 896, 896), ("k", 128, 896), ("v", 128, 896), ("o", 896, 896),
           ("gate", 4864, 896), ("up", 4864, 896), ("down", 896, 4864)]
 GEMM_SHAPES = [(4864, 896), (896, 4864), (8960, 1536), (1536, 8960)]
+# Qwen2.5-1.5B architecture, Q4_K_M-style mix (Q6_K for attn_v, for ffn_down on
+# llama.cpp's use_more_bits layers, and for the output head)
+CFG4_LAYERS = 28
+CFG4_Q6K_DOWN = {0, 1, 2, 5, 8, 11, 14, 17, 20, 23, 24, 25, 26, 27}
+
+
+def cfg4_projections(synth):
+    out = []
+    for l in range(CFG4_LAYERS):
+        out += [(synth.Q4_K, 1536, 1536), (synth.Q4_K, 256, 1536), (synth.Q6_K, 256, 1536),
+                (synth.Q4_K, 1536, 1536), (synth.Q4_K, 8960, 1536), (synth.Q4_K, 8960, 1536),
+                (synth.Q6_K if l in CFG4_Q6K_DOWN else synth.Q4_K, 1536, 8960)]
+    out.append((synth.Q6_K, 151936, 1536))  # output head
+    return out
 
 
 def log(*a):
@@ -81,7 +95,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--cpu-threads", type=int, default=8)
-    ap.add_argument("--only", choices=["gemv", "gemm", "copy"], default=None)
+    ap.add_argument("--only", choices=["gemv", "gemm", "copy", "config4"], default=None)
+    ap.add_argument("--no-config4", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
@@ -293,6 +308,80 @@ def main() -> int:
                 w.free()
         result["gemm"] = gemm
 
+    # ---- config 4: the 197 projections of a Qwen2.5-1.5B token (Q4_K + Q6_K), N = 1 and N = 512 ----
+    if not args.no_config4 and args.only in (None, "config4"):
+        projs = cfg4_projections(synth)
+        host = {}
+        for (gt, n_out, n_in) in set(projs):
+            host[(gt, n_out, n_in)] = synth.payload(gt, synth.rng_for(4, gt * 100000 + n_out + n_in), n_out, n_in)
+        ws = [dev.upload(gt, host[(gt, n_out, n_in)], n_out, n_in) for gt, n_out, n_in in projs]
+        del host
+        tok_bytes = sum(proj_bytes(synth, gt, n_out, n_in) for gt, n_out, n_in in projs)
+        rng = synth.rng_for(4, 1)
+        x1 = {k: torch.from_numpy(synth.activations(rng, k)).cuda() for k in (1536, 8960)}
+        y1 = {}
+        for gt, n_out, n_in in projs:
+            y1.setdefault(n_out, torch.zeros(n_out, dtype=torch.float32, device="cuda"))
+        # N = 1: one grouped launch per quant type (the projections of a token are independent here,
+        # as in configs[1]); the 0.98 GB of weights per token is past the 256 MB Infinity Cache
+        cplans = []
+        for gt in (synth.Q4_K, synth.Q6_K):
+            idx = [i for i, p in enumerate(projs) if p[0] == gt]
+            cplans.append(chart.GemvPlan(dev, [ws[i] for i in idx], [ptr(x1[projs[i][2]]) for i in idx],
+                                         [ptr(y1[projs[i][1]]) for i in idx]))
+
+        def tok():
+            for p in cplans:
+                p.run(sh)
+        for _ in range(3):
+            tok()
+        torch.cuda.synchronize()
+        assert dev.sync_status(sh) == 0
+        reps = 20
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            tok()
+        b.record(stream)
+        torch.cuda.synchronize()
+        us_tok = a.elapsed_time(b) * 1e3 / reps
+        gbs = tok_bytes / us_tok / 1e3
+        log(f"[bench] config4 N=1: {us_tok:.1f} us/token ({len(projs)} projections, 2 launches), "
+            f"{gbs:.0f} GB/s = {100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
+        for p in cplans:
+            p.free()
+        # N = 512: one GEMM per projection, f32 inputs quantized in the operand pass
+        n_tok = 512
+        xs = {k: torch.from_numpy(synth.activations(rng, k, n_tok).reshape(n_tok, k)).cuda() for k in (1536, 8960)}
+        ys = {}
+        for gt, n_out, n_in in projs:
+            ys.setdefault(n_out, torch.empty((n_tok, n_out), dtype=torch.float32, device="cuda"))
+
+        def prefill():
+            for w, (gt, n_out, n_in) in zip(ws, projs):
+                w.gemm_f32_dev(ptr(xs[n_in]), n_tok, ptr(ys[n_out]), sh)
+        prefill()
+        torch.cuda.synchronize()
+        assert dev.sync_status(sh) == 0
+        a.record(stream)
+        for _ in range(2):
+            prefill()
+        b.record(stream)
+        torch.cuda.synchronize()
+        ms_pre = a.elapsed_time(b) / 2
+        ops = sum(2.0 * n_tok * n_out * n_in for _, n_out, n_in in projs)
+        tops = ops / ms_pre / 1e9
+        log(f"[bench] config4 N=512: {ms_pre:.2f} ms/prefill ({len(projs)} GEMMs), {tops:.0f} TOPS = "
+            f"{100 * tops / INT8_PEAK_TOPS:.1f}% int8 peak")
+        result["config4"] = {"projections": len(projs), "n1_us_per_token": round(us_tok, 1),
+                             "n1_bytes_per_token": tok_bytes, "n1_gbs": round(gbs, 1),
+                             "n1_frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                             "n512_ms": round(ms_pre, 3), "n512_tops": round(tops, 1),
+                             "n512_frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        for w in ws:
+            w.free()
+        del xs, ys, x1, y1
+
     # ---- CPU baseline: the same config-1 step on the host (restated reference fast path) ----------
     if not args.no_cpu and args.only in (None, "gemv"):
         import oracle
@@ -364,6 +453,7 @@ def main() -> int:
         "cpu_baseline": result.get("cpu_baseline"),
         "gemv": result["gemv"],
         "gemm": result.get("gemm"),
+        "config4": result.get("config4"),
     }
     print(json.dumps(line))
     dev.close()

@@ -18,11 +18,12 @@
 // weight-scale change: per 32-block (Q8_0 d), per 16-group (Q6_K d*sc), per 256-super-block
 // (Q4_K d, plus one FMA for the dmin*m*X term, which rides on one extra MFMA per super-block).
 //
-// Tiling: a workgroup is 4 waves; wave w owns 32 weight rows (the MFMA N/column dimension, so
-// the weight scale is one value per lane) and all TN = 32*NT tokens of the workgroup (the MFMA M
-// dimension).  The f16 activation tile of each 64-deep K stage is staged in LDS and shared by the
-// 4 waves; each wave reads its own weight rows straight from the GGUF bytes and converts them in
-// registers.  Split-K over grid.z writes partials that a second pass reduces in fixed order.
+// Tiling (gemm_rb_kernel below): a workgroup is 4 waves over 128 weight rows x 128 tokens; wave w
+// owns 32 weight rows (the MFMA N/column dimension, so the weight scale is one value per lane) and
+// the workgroup's 128 tokens as four 32-token MFMA row tiles.  The f16 activation slice of each
+// 64-deep K stage is staged in LDS (double-buffered) and shared by the 4 waves; each wave reads its
+// own weight rows straight from the GGUF bytes a stage ahead and converts them in registers.
+// Split-K writes partials that a second pass reduces in fixed order.
 #include "ah_internal.h"
 
 namespace {
@@ -32,8 +33,6 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
-constexpr int kNT = 4;                 // token tiles (of 32) per workgroup
-constexpr int kTN = 32 * kNT;          // tokens per workgroup
 constexpr int kKS = 64;                // K depth of one LDS stage
 constexpr int kPitch = kKS * 2 + 16;   // bytes per token row in LDS (padding breaks bank aliasing)
 
@@ -85,314 +84,16 @@ struct GemmArgs {
     uint32_t tok_tiles, n_wg;  // register-blocked grid: token tiles, real workgroup count
 };
 
-// The A operand of token tile `tile` for k-offset `kk` (elements) within the stage.
-AH_DEV f16x8 act_frag(const uint8_t *lds, int tile, int kk) {
-    const int lane = threadIdx.x & 63;
-    return *reinterpret_cast<const f16x8 *>(lds + (tile * 32 + (lane & 31)) * kPitch + 2 * kk);
-}
-
 constexpr uint32_t kOob = 0xFFFFFFF0u;  // a buffer offset past any operand: reads zeros
 
-// Weight bytes one lane needs for one 64-deep stage, fetched a stage ahead.
-//   Q8_0: per block, the lane half's 16 codes (the 4-aligned 20 bytes around them, realigned at
-//         use with a register shift -- no per-lane register indexing) and the dword holding d.
-//   Q4_K: the super-block header (d, dmin, 12 packed scales) and the lane half's 16 nibble bytes.
-struct WStage {
-    u32x4 a0, a1, b0, b1;
-    uint32_t a2, a3, b2, b3;
-};
-
-template <int TYPE>
-AH_DEV WStage fetch_w(__amdgpu_buffer_rsrc_t rs, uint32_t rbase, uint32_t st, uint32_t n_in, int h,
-                      bool live) {
-    WStage w;
-    const uint32_t k0 = st * kKS;
-    if constexpr (TYPE == AH_GGML_Q8_0) {
-        const uint32_t b = k0 / 32;
-        const uint32_t blk0 = rbase + 34 * b, blk1 = blk0 + 34;
-        const bool l0 = live && b * 32 < n_in, l1 = live && (b + 1) * 32 < n_in;
-        const uint32_t c0 = (blk0 + 2 + 16 * h) & ~3u, c1 = (blk1 + 2 + 16 * h) & ~3u;
-        w.a0 = ah_ld128_nt(rs, l0 ? c0 : kOob);
-        w.a2 = ah_ld32(rs, l0 ? c0 + 16 : kOob);
-        w.a3 = ah_ld32(rs, l0 ? (blk0 & ~3u) : kOob);
-        w.b0 = ah_ld128_nt(rs, l1 ? c1 : kOob);
-        w.b2 = ah_ld32(rs, l1 ? c1 + 16 : kOob);
-        w.b3 = ah_ld32(rs, l1 ? (blk1 & ~3u) : kOob);
-        w.a1 = w.b1 = (u32x4){0u, 0u, 0u, 0u};
-    } else if constexpr (TYPE == AH_GGML_Q4_K) {
-        const uint32_t sb = rbase + 144 * (k0 / 256), p = (k0 / 64) & 3;
-        w.a0 = ah_ld128(rs, live ? sb : kOob);
-        w.a1 = ah_ld128_nt(rs, live ? sb + 16 + 32 * p + 16 * h : kOob);
-        w.b0 = w.b1 = (u32x4){0u, 0u, 0u, 0u};
-        w.a2 = w.a3 = w.b2 = w.b3 = 0u;
-    } else {
-        w.a0 = w.a1 = w.b0 = w.b1 = (u32x4){0u, 0u, 0u, 0u};
-        w.a2 = w.a3 = w.b2 = w.b3 = 0u;
-    }
-    return w;
-}
-
-// Pipelined K loop.  The [kTN tokens][64 k] f16 activation slice of a stage is shared by the 4
-// waves through one of two LDS buffers: while the waves compute stage s from buffer s&1, every
-// thread holds stage s+1's slice in registers (loaded during stage s-1) and writes it to the other
-// buffer after its MFMAs, then requests stage s+2.  Weight bytes are fetched a stage ahead into
-// registers.  One LDS-only barrier per stage; every load is issued unconditionally (out-of-range
-// offsets read zeros), so the compiler's load counting never drains the prefetches.
-template <int TYPE>
-__global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
-    __shared__ __align__(16) uint8_t lds[2][kTN * kPitch];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int j = lane & 31, h = lane >> 5;
-    const uint32_t row0 = blockIdx.x * 128 + wave * 32;
-    const uint32_t tok0 = blockIdx.y * kTN;
-    const uint32_t my_row = row0 + j;
-    const bool row_ok = my_row < a.n_out;
-    const uint32_t rbase = (row_ok ? my_row : 0) * a.row_bytes;
-    const __amdgpu_buffer_rsrc_t rs = ah_rsrc(a.w, a.w_bytes);
-    // this workgroup's token rows of the operand (at most kTN * 32768 * 2 bytes)
-    const uint32_t ntile = a.n_tok - tok0 < (uint32_t)kTN ? a.n_tok - tok0 : (uint32_t)kTN;
-    const __amdgpu_buffer_rsrc_t rx = ah_rsrc(a.xh + (size_t)tok0 * a.kpad, ntile * a.kpad * 2u);
-
-    const uint32_t nstages = (a.n_in + kKS - 1) / kKS;
-    const uint32_t st_begin = blockIdx.z * a.stages_per_split;
-    uint32_t st_end = st_begin + a.stages_per_split;
-    if (st_end > nstages) st_end = nstages;
-
-    u32x4 areg[kTN * 8 / kThreads];
-    auto act_load = [&](uint32_t st) {
-        const bool live = st < st_end;
-#pragma unroll
-        for (int i = 0; i < kTN * 8 / kThreads; ++i) {
-            const uint32_t c = threadIdx.x + kThreads * i, t = c >> 3, kc = c & 7;
-            const uint32_t off = (t * a.kpad + st * kKS + 8 * kc) * 2u;
-            areg[i] = ah_ld128(rx, live && t < ntile ? off : kOob);
-        }
-    };
-    auto act_store = [&](uint8_t *buf) {
-#pragma unroll
-        for (int i = 0; i < kTN * 8 / kThreads; ++i) {
-            const uint32_t c = threadIdx.x + kThreads * i, t = c >> 3, kc = c & 7;
-            *reinterpret_cast<u32x4 *>(buf + t * kPitch + 16 * kc) = areg[i];
-        }
-    };
-
-    f32x16 acc[kNT];
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) acc[t] = (f32x16){};
-
-    // per-super-block state (K-quants)
-    f32x16 P[kNT];
-    float fd = 0.0f, fdm = 0.0f;
-    uint32_t s0 = 0, s1 = 0, s2 = 0;   // Q4_K packed scales
-    uint32_t w6[54];                   // Q6_K super-block window
-    uint32_t sh6 = 0;
-
-    act_load(st_begin);
-    act_store(lds[0]);
-    act_load(st_begin + 1);
-    WStage wc = fetch_w<TYPE>(rs, rbase, st_begin, a.n_in, h, st_begin < st_end);
-
-    for (uint32_t st = st_begin; st < st_end; ++st) {
-        const uint32_t k0 = st * kKS;
-        const uint8_t *cur = lds[(st - st_begin) & 1];
-        ah_lds_barrier();  // buffer `cur` is written; every wave is done with the other one
-        const WStage wn = fetch_w<TYPE>(rs, rbase, st + 1, a.n_in, h, st + 1 < st_end);
-        // keep the next stage's weight requests here, a whole stage ahead of their use (the
-        // scheduler would otherwise sink them to the end of the iteration)
-        __builtin_amdgcn_sched_barrier(0);
-
-        if (TYPE == AH_GGML_Q8_0) {
-            // two 32-blocks per stage; lane half h owns codes [16h, 16h+16) of each block
-#pragma unroll
-            for (int bb = 0; bb < 2; ++bb) {
-                // a block past n_in has zero codes and d = 0 (fetch_w) against zero activations
-                const uint32_t b = k0 / 32 + bb;
-                const uint32_t blk = rbase + 34 * b;
-                const uint32_t shc = (blk + 2 + 16 * h) & 3u;  // 0 or 2
-                const u32x4 v = bb ? wc.b0 : wc.a0;
-                const uint32_t w[5] = {v.x, v.y, v.z, v.w, bb ? wc.b2 : wc.a2};
-                const uint32_t dw = bb ? wc.b3 : wc.a3;
-                const float d = ah_f16_bits_to_f32((dw >> (8 * (blk & 3u))) & 0xffffu);
-                uint32_t c[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) c[i] = ah_alignbyte(w[i + 1], w[i], shc);
-                uint32_t f[8];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) i8x4_to_f16(c[i], f[2 * i], f[2 * i + 1]);
-                const f16x8 b0 = pack8(f[0], f[1], f[2], f[3]), b1 = pack8(f[4], f[5], f[6], f[7]);
-#pragma unroll
-                for (int t = 0; t < kNT; ++t) {
-                    f32x16 p = mfma(act_frag(cur, t, 32 * bb + 16 * h), b0, (f32x16){});
-                    p = mfma(act_frag(cur, t, 32 * bb + 16 * h + 8), b1, p);
-                    acc[t] += d * p;
-                }
-            }
-        } else if (TYPE == AH_GGML_Q4_K) {
-            const uint32_t s = k0 / 256, p = (k0 / 64) & 3;
-            if (p == 0) {
-                const u32x4 hd = wc.a0;
-                fd = ah_f16_bits_to_f32(hd.x & 0xffffu);
-                fdm = ah_f16_bits_to_f32(hd.x >> 16);
-                s0 = hd.y;
-                s1 = hd.z;
-                s2 = hd.w;
-#pragma unroll
-                for (int t = 0; t < kNT; ++t) P[t] = (f32x16){};
-            }
-            // qs window p: lane half h takes bytes [16h, 16h+16) -> sub-block 2p (low nibbles)
-            // and 2p+1 (high nibbles), k = 16h + 8m + e.
-            const u32x4 q = wc.a1;
-            const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-            int scv[2];
-            {
-                auto byte = [&](int i) -> uint32_t {
-                    const uint32_t wv = i < 4 ? s0 : (i < 8 ? s1 : s2);
-                    return (wv >> (8 * (i & 3))) & 0xffu;
-                };
-#pragma unroll
-                for (int hb = 0; hb < 2; ++hb) {
-                    const int jj = 2 * (int)p + hb;
-                    scv[hb] = jj < 4 ? (int)(byte(jj) & 63)
-                                     : (int)((byte(jj + 4) & 0xF) | ((byte(jj - 4) >> 6) << 4));
-                }
-            }
-#pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                const _Float16 sc = (_Float16)(float)scv[hb];
-                const f16x2 sc2 = {sc, sc}, off2 = {(_Float16)(-1024.0f) * sc, (_Float16)(-1024.0f) * sc};
-                uint32_t f[8];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t n = hb ? ((qw[i] >> 4) & 0x0F0F0F0Fu) : (qw[i] & 0x0F0F0F0Fu);
-                    nib4_times(n, sc2, off2, f[2 * i], f[2 * i + 1]);
-                }
-                const f16x8 b0 = pack8(f[0], f[1], f[2], f[3]), b1 = pack8(f[4], f[5], f[6], f[7]);
-#pragma unroll
-                for (int t = 0; t < kNT; ++t) {
-                    P[t] = mfma(act_frag(cur, t, 32 * hb + 16 * h), b0, P[t]);
-                    P[t] = mfma(act_frag(cur, t, 32 * hb + 16 * h + 8), b1, P[t]);
-                }
-            }
-            if (p == 3 || k0 + kKS >= a.n_in) {
-                // min term: sum_j m_j * X_j over the super-block, one MFMA with K' = 16:
-                // A'[tok][8h+e] = split code sum of sub-block e (hi piece h=0, lo piece h=1),
-                // B'[8h+e][row] = m_e.
-                auto byte = [&](int i) -> uint32_t {
-                    const uint32_t wv = i < 4 ? s0 : (i < 8 ? s1 : s2);
-                    return (wv >> (8 * (i & 3))) & 0xffu;
-                };
-                uint32_t mf[4];
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const int m0 = e < 4 ? (int)(byte(e + 4) & 63)
-                                         : (int)((byte(e + 4) >> 4) | ((byte(e) >> 6) << 4));
-                    const int m1 = e + 1 < 4 ? (int)(byte(e + 5) & 63)
-                                             : (int)((byte(e + 5) >> 4) | ((byte(e + 1) >> 6) << 4));
-                    const f16x2 mm = {(_Float16)(float)m0, (_Float16)(float)m1};
-                    mf[e / 2] = as_u(mm);
-                }
-                const f16x8 bm = pack8(mf[0], mf[1], mf[2], mf[3]);
-                const uint32_t nsb = a.kpad / 256;
-#pragma unroll
-                for (int t = 0; t < kNT; ++t) {
-                    const uint32_t tok = tok0 + 32 * t + j;
-                    f16x8 am = {};
-                    if (tok < a.n_tok)
-                        am = *reinterpret_cast<const f16x8 *>(a.xmin + ((size_t)tok * nsb + s) * 16 + 8 * h);
-                    const f32x16 pm = mfma(am, bm, (f32x16){});
-                    acc[t] += fd * P[t] - fdm * pm;
-                }
-            }
-        } else {  // Q6_K
-            const uint32_t s = k0 / 256, stq = (k0 / 64) & 3;
-            if (stq == 0) {
-                const uint32_t addr = rbase + 210 * s;
-                const uint32_t base = addr & ~3u;
-                sh6 = addr & 3u;
-#pragma unroll
-                for (int i = 0; i < 13; ++i) {
-                    const u32x4 t = ah_ld128(rs, base + 16 * i);
-                    w6[4 * i] = t.x;
-                    w6[4 * i + 1] = t.y;
-                    w6[4 * i + 2] = t.z;
-                    w6[4 * i + 3] = t.w;
-                }
-                w6[52] = ah_ld32(rs, base + 208);
-                w6[53] = ah_ld32(rs, base + 212);
-                fd = ah_f16_bits_to_f32(ah_alignbyte(w6[53], w6[52], sh6) & 0xffffu);
-            }
-            auto V = [&](int i) -> uint32_t { return ah_alignbyte(w6[i + 1], w6[i], sh6); };
-            // stage stq covers elements 64*stq .. +64: half n = stq/2, nibble = stq&1,
-            // group G = 4*stq + gg: ql bytes 64n + 16gg + 8h + e, qh bytes 32n + 16(gg&1) + 8h + e,
-            // qh shift 2t with t = 2*(stq&1) + gg/2.
-            const int n = stq >> 1, nib = stq & 1;
-#pragma unroll
-            for (int gg = 0; gg < 4; ++gg) {
-                // a group past n_in meets zero activations (the operand is zero up to kpad)
-                const int G = 4 * (int)stq + gg;
-                const int t = 2 * nib + (gg >> 1);
-                const int qlb = 64 * n + 16 * gg + 8 * h;          // byte offset, multiple of 8
-                const int qhb = 128 + 32 * n + 16 * (gg & 1) + 8 * h;
-                uint32_t u[2];
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const uint32_t qlw = V(qlb / 4 + i), qhw = V(qhb / 4 + i);
-                    const uint32_t lo4 = nib ? ((qlw >> 4) & 0x0F0F0F0Fu) : (qlw & 0x0F0F0F0Fu);
-                    u[i] = lo4 | (((qhw >> (2 * t)) & 0x03030303u) << 4);
-                }
-                uint32_t f[4];
-                u6x4_to_f16(u[0], f[0], f[1]);
-                u6x4_to_f16(u[1], f[2], f[3]);
-                const f16x8 bq = pack8(f[0], f[1], f[2], f[3]);
-                const uint32_t scw = V(48 + G / 4);
-                const float coef = fd * (float)(int)(int8_t)((scw >> (8 * (G & 3))) & 0xffu);
-#pragma unroll
-                for (int tt = 0; tt < kNT; ++tt) {
-                    const f32x16 p = mfma(act_frag(cur, tt, 16 * gg + 8 * h), bq, (f32x16){});
-                    acc[tt] += coef * p;
-                }
-            }
-        }
-
-        act_store(lds[((st - st_begin) & 1) ^ 1]);  // stage st+1 (zeros past the split)
-        act_load(st + 2);
-        wc = wn;
-    }
-
-    // D layout of a 32x32 MFMA: lane (j, h), register r -> row i = 8*(r/4) + 4*h + (r%4), col j.
-    // Buffer stores relative to this workgroup's token rows; a lane past n_out or a token past
-    // n_tok stores out of range (nothing is written), so there is no branch per element.
-    float *ybase = a.splits == 1 ? a.y + (size_t)tok0 * a.n_out
-                                 : a.y + ((size_t)blockIdx.z * a.n_tok + tok0) * a.n_out;
-    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(ybase, ntile * a.n_out * 4u);
-    // the token scales of the lane's 16 tokens per tile (1.0 for partials), loaded up front
-    const __amdgpu_buffer_rsrc_t rt = ah_rsrc(a.tok_scale + tok0, ntile * 4u);
-    const bool scaled = a.splits == 1;
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-        uint32_t sc[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[r] = ah_ld32(rt, 4 * (32 * t + 8 * (r / 4) + 4 * h + (r % 4)));
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t tl = 32 * t + 8 * (r / 4) + 4 * h + (r % 4);
-            const bool ok = row_ok && tl < ntile;
-            const float v = acc[t][r] * (scaled ? __builtin_bit_cast(float, sc[r]) : 1.0f);
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
-                                                  ok ? (tl * a.n_out + my_row) * 4u : kOob, 0, 0);
-        }
-    }
-}
-
-
-// ---- register-blocked kernel (Q8_0, Q4_K) ---------------------------------------------------
+// ---- register-blocked kernel ----------------------------------------------------------------
 //
 // A workgroup is 4 waves.  Wave w owns NN 32-row MFMA column tiles (n) of weight rows and all NM
 // 32-token row tiles (m) of the workgroup's tokens, so every activation fragment read from LDS
 // feeds NN MFMAs and every dequantized weight fragment feeds NM.  The VALU work per MFMA (weight
 // dequantization over NM, plus the scale folds) is what bounds this kernel, so NM = 4 by default;
 // LDS sustains the resulting 1 KB of fragment reads per MFMA.  The loop body is U stages of 64
-// (Q8_0: U = 2, Q4_K: U = 4 = one super-block), so the LDS buffer, the weight register set and the
+// (Q8_0: U = 2, K-quants: U = 4 = one super-block), so the LDS buffer, the weight register set and the
 // super-block position of each stage are compile-time: no runtime register indexing, no copies
 // between register sets.
 namespace rb {
@@ -410,8 +111,12 @@ template <int TYPE> constexpr int unroll() { return TYPE == AH_GGML_Q8_0 ? 2 : 4
 //         s[4n+2bb] = the dword after the window, s[4n+2bb+1] = the dword holding d.
 //   Q4_K: v[2n] = super-block header (read at the super-block's first stage only),
 //         v[2n+1] = the lane half's 16 bytes of qs chunk P.
+//   Q6_K (one row per lane): stage P of a super-block covers half n = P/2, low (P even) or high
+//         nibbles: v[0..3] = 64 bytes from ql[64n + 8h], v[4..5] = 32 bytes from qh[32n + 8h],
+//         s[0..1] = 8 bytes from sc[4P], s[2] = the dword holding d (all from 4-aligned
+//         addresses below, realigned by the super-block's offset mod 4).
 struct WRb {
-    u32x4 v[4];
+    u32x4 v[6];
     uint32_t s[8];
 };
 
@@ -420,7 +125,7 @@ AH_DEV WRb fetch_rb(__amdgpu_buffer_rsrc_t rs, const uint32_t (&rb)[NN], const b
                     uint32_t st, uint32_t n_in, int h, bool live) {
     WRb w;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w.v[i] = (u32x4){0u, 0u, 0u, 0u};
+    for (int i = 0; i < 6; ++i) w.v[i] = (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < 8; ++i) w.s[i] = 0u;
     const uint32_t k0 = st * kKS;
@@ -439,6 +144,19 @@ AH_DEV WRb fetch_rb(__amdgpu_buffer_rsrc_t rs, const uint32_t (&rb)[NN], const b
             w.s[4 * n + 2] = ah_ld32(rs, m1 ? c1 + 16 : kOob);
             w.s[4 * n + 3] = ah_ld32(rs, m1 ? (blk1 & ~3u) : kOob);
         }
+    } else if constexpr (TYPE == AH_GGML_Q6_K) {
+        static_assert(NN == 1, "Q6_K stages one row per lane");
+        const uint32_t sb = rb[0] + 210 * (k0 / 256), nh = P / 2;
+        const bool m = live && rl[0];
+        const uint32_t aql = (sb + 64 * nh + 8 * h) & ~3u, aqh = (sb + 128 + 32 * nh + 8 * h) & ~3u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w.v[i] = ah_ld128(rs, m ? aql + 16 * i : kOob);
+        w.v[4] = ah_ld128(rs, m ? aqh : kOob);
+        w.v[5] = ah_ld128(rs, m ? aqh + 16 : kOob);
+        const uint32_t asc = (sb + 192 + 4 * P) & ~3u;
+        w.s[0] = ah_ld32(rs, m ? asc : kOob);
+        w.s[1] = ah_ld32(rs, m ? asc + 4 : kOob);
+        w.s[2] = ah_ld32(rs, m ? (sb + 208) & ~3u : kOob);
     } else {
 #pragma unroll
         for (int n = 0; n < NN; ++n) {
@@ -600,6 +318,53 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
                     for (int r = 0; r < 16; ++r) acc[m][n][r] = __builtin_fmaf(d[bb][n], pq[pc & 1][r], acc[m][n][r]);
                 }
             }
+        } else if constexpr (TYPE == AH_GGML_Q6_K) {
+            // Stage u of the super-block: half n = u/2, nibble u&1.  k-step gg is the 16-group
+            // G = 4u + gg (one int8 scale); lane half h takes its elements 8h..8h+7, i.e. ql bytes
+            // 64n + 16gg + 8h + e, qh bytes 32n + 16(gg&1) + 8h + e at bit 2(2(u&1) + gg/2)
+            // (format/quant.rs:556-599).  B = u - 32 is exact in f16; every group's MFMA goes to a
+            // fresh accumulator folded with d*sc_G, the fold of chain c-1 issued after chain c.
+            const uint32_t sh = (rbase[0] + 210 * (st / 4)) & 3u;  // 0 or 2
+            const uint32_t scw = ah_alignbyte(wc.s[1], wc.s[0], sh);
+            const float fd6 = ah_f16_bits_to_f32((wc.s[2] >> (8 * sh)) & 0xffffu);
+            const uint32_t ql[16] = {wc.v[0].x, wc.v[0].y, wc.v[0].z, wc.v[0].w, wc.v[1].x, wc.v[1].y,
+                                     wc.v[1].z, wc.v[1].w, wc.v[2].x, wc.v[2].y, wc.v[2].z, wc.v[2].w,
+                                     wc.v[3].x, wc.v[3].y, wc.v[3].z, wc.v[3].w};
+            const uint32_t qh[8] = {wc.v[4].x, wc.v[4].y, wc.v[4].z, wc.v[4].w,
+                                    wc.v[5].x, wc.v[5].y, wc.v[5].z, wc.v[5].w};
+            constexpr int nib = u & 1;
+            f16x8 bq[4];
+            float coef[4];
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) {
+                uint32_t uu[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint32_t lw = ah_alignbyte(ql[4 * gg + i + 1], ql[4 * gg + i], sh);
+                    const uint32_t hw = ah_alignbyte(qh[4 * (gg & 1) + i + 1], qh[4 * (gg & 1) + i], sh);
+                    const uint32_t lo4 = nib ? ((lw >> 4) & 0x0F0F0F0Fu) : (lw & 0x0F0F0F0Fu);
+                    uu[i] = lo4 | (((hw >> (2 * (2 * nib + gg / 2))) & 0x03030303u) << 4);
+                }
+                uint32_t f[4];
+                u6x4_to_f16(uu[0], f[0], f[1]);
+                u6x4_to_f16(uu[1], f[2], f[3]);
+                bq[gg] = pack8(f[0], f[1], f[2], f[3]);
+                coef[gg] = fd6 * (float)(int)(int8_t)((scw >> (8 * gg)) & 0xffu);
+            }
+            constexpr int NC = 4 * NM;
+            f32x16 pq[2];
+#pragma unroll
+            for (int c = 0; c <= NC; ++c) {
+                if (c < NC) {
+                    const int gg = c / NM, m = c % NM;
+                    pq[c & 1] = mfma(frag(cur, m, 16 * gg + 8 * h), bq[gg], (f32x16){});
+                }
+                if (c > 0) {
+                    const int pc = c - 1, gg = pc / NM, m = pc % NM;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[m][0][r] = __builtin_fmaf(coef[gg], pq[pc & 1][r], acc[m][0][r]);
+                }
+            }
         } else {  // Q4_K, stage u of the super-block: qs chunk u = sub-blocks 2u (low), 2u+1 (high)
             if constexpr (u == 0) {
 #pragma unroll
@@ -731,8 +496,7 @@ struct GemmGeom {
 };
 GemmGeom geom_of(uint32_t type, uint32_t n_in, uint32_t kpad) {
     if (type == AH_GGML_Q8_0) return {(n_in + 2 * kKS - 1) / (2 * kKS) * 2, 2, rb::kRows, rb::kTok};
-    if (type == AH_GGML_Q4_K) return {kpad / kKS, 4, rb::kRows, rb::kTok};
-    return {(n_in + kKS - 1) / kKS, 4, 128, kTN};
+    return {kpad / kKS, 4, rb::kRows, rb::kTok};  // K-quants: whole super-blocks
 }
 
 // Stages per split for a requested split count: a multiple of the unroll.
@@ -791,11 +555,10 @@ hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uin
     const uint32_t row_tiles = (n_out + g.rows - 1) / g.rows;
     a.n_wg = row_tiles * a.tok_tiles * a.splits;
     const dim3 rb_grid((a.n_wg + 7) / 8 * 8);
-    const dim3 grid(row_tiles, a.tok_tiles, a.splits);
     switch (type) {
     case AH_GGML_Q8_0: hipLaunchKernelGGL(gemm_rb_kernel<AH_GGML_Q8_0>, rb_grid, dim3(kThreads), 0, stream, a); break;
     case AH_GGML_Q4_K: hipLaunchKernelGGL(gemm_rb_kernel<AH_GGML_Q4_K>, rb_grid, dim3(kThreads), 0, stream, a); break;
-    case AH_GGML_Q6_K: hipLaunchKernelGGL(gemm_kernel<AH_GGML_Q6_K>, grid, dim3(kThreads), 0, stream, a); break;
+    case AH_GGML_Q6_K: hipLaunchKernelGGL(gemm_rb_kernel<AH_GGML_Q6_K>, rb_grid, dim3(kThreads), 0, stream, a); break;
     default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();

@@ -426,8 +426,10 @@ AH_DEV float unit_q4(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
 
 // Q6_K super-block s (format/quant.rs:556-599): ql[128] @0, qh[64] @128, int8 sc[16] @192,
 // f16 d @208.  Element 128n + 32t + l = (nibble t/2 of ql[64n + 32(t&1) + l]
-// | ((qh[32n + l] >> 2t) & 3) << 4) - 32.  Super-blocks are 2-byte aligned: 54 dwords from the
-// 4-aligned address below are realigned.
+// | ((qh[32n + l] >> 2t) & 3) << 4) - 32.  Super-blocks are 2-byte aligned: the dwords of each half
+// are read from the 4-aligned address below and realigned, one half at a time.  The 6-bit value is
+// built with one and-or per word (the high bits are moved into place by one shift and mask), and
+// the group terms are f32 (no integer multiplies).
 template <bool DOTS>
 AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in, const ActLds &A,
                      int32_t *dots16) {
@@ -437,13 +439,13 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
     auto V = [&](int i) -> uint32_t { return ah_alignbyte(p[i + 1], p[i], sh); };
     const float fd = ah_f16_bits_to_f32(V(52) & 0xffffu);
     float acc = 0.0f;
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
+#pragma unroll 1
+    for (int n = 0; n < 2; ++n) {  // one half at a time keeps the realigned words' live range short
         if (DOTS && 8 * s + 4 * n >= nb32) break;  // a ragged row may end after the first half
         uint32_t qh[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) qh[i] = V(32 + 8 * n + i);
-        const uint32_t scw0 = V(48 + 2 * n), scw1 = V(49 + 2 * n);
+        const uint32_t scw[2] = {V(48 + 2 * n), V(49 + 2 * n)};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const uint32_t g = 8 * s + 4 * n + t;
@@ -455,8 +457,9 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const uint32_t qlw = V(16 * n + 8 * (t & 1) + i);
-                const uint32_t lo4 = t < 2 ? (qlw & 0x0F0F0F0Fu) : ((qlw >> 4) & 0x0F0F0F0Fu);
-                const uint32_t uu = lo4 | (((qh[i] >> (2 * t)) & 0x03030303u) << 4);
+                // bits 4-5 of each byte: qh bits 2t, 2t+1
+                const uint32_t hi = (2 * t <= 4 ? (qh[i] << (4 - 2 * t)) : (qh[i] >> (2 * t - 4))) & 0x30303030u;
+                const uint32_t uu = ((t < 2 ? qlw : (qlw >> 4)) & 0x0F0F0F0Fu) | hi;
                 if (i < 4)
                     Dlo = ah_sdot4(uu, xw[i], Dlo);
                 else
@@ -464,14 +467,13 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
             }
             Dlo -= 32 * A.xs16[2 * g];
             Dhi -= 32 * A.xs16[2 * g + 1];
-            const uint32_t scw = (t >> 1) ? scw1 : scw0;
-            const int sclo = (int)(int8_t)((scw >> (16 * (t & 1))) & 0xffu);
-            const int schi = (int)(int8_t)((scw >> (16 * (t & 1) + 8)) & 0xffu);
             if (DOTS && dots16) {
                 dots16[2 * g] = Dlo;
                 if (2 * g + 1 < nb16) dots16[2 * g + 1] = Dhi;  // ragged row ends on a 16-group
             }
-            acc += A.fsc[g] * fd * (float)(sclo * Dlo + schi * Dhi);
+            const uint32_t sw = scw[t >> 1] >> (16 * (t & 1));
+            const float sclo = (float)(int)(int8_t)(sw & 0xffu), schi = (float)(int)(int8_t)((sw >> 8) & 0xffu);
+            acc += A.fsc[g] * fd * (sclo * (float)Dlo + schi * (float)Dhi);
         }
     }
     return acc;
@@ -743,7 +745,7 @@ constexpr uint32_t kOob = 0xFFFFFFF0u;             // past any payload (payloads
 // descriptor is read with scalar loads, which do not queue behind the vector memory stream.
 // DOTS: the debug form that also stores exact group dots (single launches only).
 template <int TYPE, bool PLAN, bool DOTS>
-__global__ void __launch_bounds__(kSThreads)
+__global__ void __launch_bounds__(kSThreads, 4)
     gemv_stream_kernel(GemvPart single, const GemvPart *__restrict__ parts,
                        const uint32_t *__restrict__ wg_part, uint32_t kpad_max,
                        unsigned long long *status) {

@@ -21,11 +21,13 @@ uint32_t ah_gemv_rows_per_tile(uint32_t row_bytes, uint32_t units);
 hipError_t ah_gemv_init_attrs();
 bool ah_gemv_stream_geometry(uint32_t row_bytes, uint32_t units, uint32_t &rows, uint32_t &lanes);
 size_t ah_gemv_stream_lds_bytes(uint32_t kpad_max);
+size_t ah_gemv_act_bytes(uint32_t kpad);
+size_t ah_gemv_stream_slot_bytes();
 uint32_t ah_gemv_stream_threads();
 int ah_gemv_stream_occupancy(uint32_t type, size_t lds);
-hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single,
-                                 const GemvPart *d_parts, const uint32_t *d_wg_part, uint32_t grid,
-                                 uint32_t kpad_max, unsigned long long *status, hipStream_t stream);
+hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const GemvPart *d_parts,
+                                 const StreamWG *d_wgd, uint32_t grid, uint32_t act_bytes,
+                                 unsigned long long *status, hipStream_t stream);
 hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream);
 hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes, uint32_t off0,
                           uint32_t off1, int *d_bad, hipStream_t stream);
@@ -57,8 +59,10 @@ struct ah_tensor {
 struct ah_gemv_plan {
     uint32_t type = 0, n_parts = 0, grid = 0, kpad_max = 0, nc = 4;
     bool stream = false;  // streaming kernel (else the workgroup-tile kernel)
+    uint32_t act_bytes = 0;        // streaming: LDS activation region of a workgroup
     GemvPart *d_parts = nullptr;   // part descriptors
-    uint32_t *d_wg_part = nullptr; // workgroup -> part index (one load per workgroup)
+    uint32_t *d_wg_part = nullptr; // workgroup-tile kernel: workgroup -> part index
+    StreamWG *d_wgd = nullptr;     // streaming kernel: per-workgroup wave assignment
 };
 
 #define AH_HIP(ctx, call)                                                                       \
@@ -244,6 +248,101 @@ uint32_t deal_wgs(GemvPart *parts, size_t n, uint64_t target, bool stream) {
     return wg;
 }
 
+// Streaming plan: deal the waves of `n_wg` resident workgroups over the parts so that the most
+// tiles any wave streams is as small as it can be (every part gets at least one wave; a part
+// never gets more waves than tiles), then lay the waves out in part order, eight per workgroup.
+// A workgroup quantizes the activation of every part its waves use into its own LDS region, so
+// a workgroup takes at most 8 parts and `act_budget` bytes of activations: a part that would
+// overflow it starts the next workgroup (the waves skipped are idle).  Wave k of a part with n
+// waves streams tiles [T*k/n, T*(k+1)/n).  Returns the workgroup count (0: does not fit).
+uint32_t deal_waves(const GemvPart *parts, size_t n, uint32_t n_wg, size_t act_budget, StreamWG *out) {
+    const uint64_t W = (uint64_t)n_wg * 8;
+    if (n > W) return 0;
+    uint32_t *nw = static_cast<uint32_t *>(std::malloc(n * sizeof(uint32_t)));
+    if (!nw) return 0;
+    auto tiles = [&](size_t p) { return (parts[p].n_out + parts[p].rows_per_tile - 1) / parts[p].rows_per_tile; };
+    auto actb = [&](size_t p) { return ah_gemv_act_bytes(kpad_of(parts[p].n_in)); };
+    uint64_t target = W;
+    uint32_t used_wg = 0;
+    for (int attempt = 0; attempt < 8 && target >= n; ++attempt) {
+        // waves per part: greedy on the largest ceil(tiles / waves)
+        uint64_t total = n;
+        for (size_t p = 0; p < n; ++p) nw[p] = 1;
+        while (total < target) {
+            size_t best = n;
+            uint32_t bl = 1;
+            for (size_t p = 0; p < n; ++p) {
+                if (nw[p] >= tiles(p)) continue;
+                const uint32_t l = (tiles(p) + nw[p] - 1) / nw[p];
+                if (l > bl) {
+                    bl = l;
+                    best = p;
+                }
+            }
+            if (best == n) break;  // every part has a wave per tile
+            ++nw[best];
+            ++total;
+        }
+        // lay out, eight waves per workgroup
+        uint64_t c = 0;
+        size_t cur_bytes = 0;
+        uint32_t cur_nact = 0;
+        bool fits = true;
+        for (size_t p = 0; p < n && fits; ++p) {
+            const size_t a = actb(p);
+            for (uint32_t k = 0; k < nw[p]; ++k) {
+                if (c % 8 == 0) {  // a new workgroup starts with this part
+                    cur_bytes = 0;
+                    cur_nact = 0;
+                }
+                if (k == 0 || c % 8 == 0) {
+                    if (c % 8 != 0 && (cur_bytes + a > act_budget || cur_nact == 8)) {
+                        c = (c / 8 + 1) * 8;  // pad: this part starts the next workgroup
+                        cur_bytes = 0;
+                        cur_nact = 0;
+                    }
+                    if (a > act_budget) {
+                        fits = false;
+                        break;
+                    }
+                    cur_bytes += a;
+                    ++cur_nact;
+                }
+                const uint64_t wg = c / 8, wi = c % 8;
+                if (wg >= n_wg) {
+                    fits = false;
+                    break;
+                }
+                StreamWG &D = out[wg];
+                if (wi == 0 || k == 0) {
+                    if (wi == 0) {
+                        std::memset(&D, 0, sizeof(D));
+                        for (int i = 0; i < 8; ++i) D.wave_part[i] = kIdleWave;
+                    }
+                    D.act_part[D.n_act] = (uint32_t)p;
+                    D.act_off[D.n_act] = D.n_act ? D.act_off[D.n_act - 1] + (uint32_t)actb(D.act_part[D.n_act - 1]) : 0u;
+                    ++D.n_act;
+                }
+                const uint32_t T = tiles(p), RW = parts[p].rows_per_tile;
+                const uint32_t tb = (uint32_t)((uint64_t)T * k / nw[p]), te = (uint32_t)((uint64_t)T * (k + 1) / nw[p]);
+                D.wave_part[wi] = (uint32_t)p;
+                D.wave_act[wi] = D.n_act - 1;
+                D.r_begin[wi] = tb * RW < parts[p].n_out ? tb * RW : parts[p].n_out;
+                D.r_end[wi] = te * RW < parts[p].n_out ? te * RW : parts[p].n_out;
+                ++c;
+            }
+        }
+        if (fits) {
+            used_wg = (uint32_t)((c + 7) / 8);
+            // workgroups whose tail waves were skipped by padding: those waves stay idle
+            break;
+        }
+        target -= target / 16 + 1;  // padding overflowed the grid: fewer waves, try again
+    }
+    std::free(nw);
+    return used_wg;
+}
+
 int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
                     const int64_t *scales, float *y, int32_t *dots, void *stream) {
     if (!ctx || !w || (!x && w->n_in) || (!y && w->n_out)) return AH_ERR_INVALID_ARG;
@@ -260,8 +359,8 @@ int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     const uint32_t grid = deal_wgs(&P, 1, resident_wgs(ctx, w->type, st, kp), st);
     if (grid == 0) return AH_ERR_OUT_OF_MEMORY;
     if (st)
-        AH_HIP(ctx, ah_launch_gemv_stream(w->type, P, nullptr, nullptr, grid, kp, ctx->d_status,
-                                          pick(ctx, stream)));
+        AH_HIP(ctx, ah_launch_gemv_stream(w->type, P, nullptr, nullptr, grid, (uint32_t)ah_gemv_act_bytes(kp),
+                                          ctx->d_status, pick(ctx, stream)));
     else
         AH_HIP(ctx, ah_launch_gemv(w->type, P, nullptr, nullptr, grid, kp, ah_gemv_nc(P.row_bytes),
                                    ctx->d_status, pick(ctx, stream)));
@@ -572,14 +671,62 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
         const uint32_t nci = ah_gemv_nc(parts[i].row_bytes);
         nc = nci > nc ? nci : nc;
     }
-    if (!all_stream)  // one kernel serves the plan: every part as workgroup tiles
-        for (size_t i = 0; i < n_parts; ++i) recut_wg_tiles(parts[i]);
     hipError_t e0 = hipSetDevice(ctx->device);
     if (e0 != hipSuccess) {
         std::free(parts);
         ctx->last_hip = (int)e0;
         return AH_ERR_HIP;
     }
+    // Streaming plan: waves dealt over the parts, activations sharing a workgroup's LDS region of
+    // at most `budget` bytes (15 KB keeps two workgroups per CU; a larger activation raises it).
+    if (all_stream) {
+        size_t budget = 15360;
+        for (size_t i = 0; i < n_parts; ++i) {
+            const size_t a = ah_gemv_act_bytes(kpad_of(parts[i].n_in));
+            budget = a > budget ? a : budget;
+        }
+        int occ = ah_gemv_stream_occupancy(type, budget + ah_gemv_stream_slot_bytes());
+        if (occ < 1) occ = 1;
+        const uint32_t n_res = (uint32_t)occ * (uint32_t)ctx->cu_count;
+        StreamWG *wgd = static_cast<StreamWG *>(std::calloc(n_res, sizeof(StreamWG)));
+        if (!wgd) {
+            std::free(parts);
+            return AH_ERR_OUT_OF_MEMORY;
+        }
+        const uint32_t nwg = deal_waves(parts, n_parts, n_res, budget, wgd);
+        if (nwg) {
+            ah_gemv_plan *p = new (std::nothrow) ah_gemv_plan();
+            hipError_t e = p ? hipSuccess : hipErrorOutOfMemory;
+            if (e == hipSuccess) e = hipMalloc(&p->d_parts, n_parts * sizeof(GemvPart));
+            if (e == hipSuccess) e = hipMalloc(&p->d_wgd, (size_t)nwg * sizeof(StreamWG));
+            if (e == hipSuccess) e = hipMemcpy(p->d_parts, parts, n_parts * sizeof(GemvPart), hipMemcpyHostToDevice);
+            if (e == hipSuccess) e = hipMemcpy(p->d_wgd, wgd, (size_t)nwg * sizeof(StreamWG), hipMemcpyHostToDevice);
+            std::free(parts);
+            std::free(wgd);
+            if (e != hipSuccess) {
+                if (p) {
+                    if (p->d_parts) (void)hipFree(p->d_parts);
+                    if (p->d_wgd) (void)hipFree(p->d_wgd);
+                    delete p;
+                }
+                ctx->last_hip = (int)e;
+                return p ? AH_ERR_HIP : AH_ERR_OUT_OF_MEMORY;
+            }
+            p->type = type;
+            p->n_parts = (uint32_t)n_parts;
+            p->grid = nwg;
+            p->kpad_max = kpad_max;
+            p->nc = nc;
+            p->stream = true;
+            p->act_bytes = (uint32_t)budget;
+            *out = p;
+            return AH_OK;
+        }
+        std::free(wgd);
+        all_stream = false;  // more parts than the resident waves: the workgroup-tile kernel
+    }
+    // one kernel serves the plan: every part as workgroup tiles
+    for (size_t i = 0; i < n_parts; ++i) recut_wg_tiles(parts[i]);
     const uint32_t wg = deal_wgs(parts, n_parts, resident_wgs(ctx, type, all_stream, kpad_max), all_stream);
     if (wg == 0) {
         std::free(parts);
@@ -628,8 +775,8 @@ int32_t ah_gemv_plan_run(ah_ctx *ctx, const ah_gemv_plan *plan, void *stream) {
     std::memset(&none, 0, sizeof(none));
     AH_HIP(ctx, hipSetDevice(ctx->device));
     if (plan->stream)
-        AH_HIP(ctx, ah_launch_gemv_stream(plan->type, none, plan->d_parts, plan->d_wg_part,
-                                          plan->grid, plan->kpad_max, ctx->d_status, pick(ctx, stream)));
+        AH_HIP(ctx, ah_launch_gemv_stream(plan->type, none, plan->d_parts, plan->d_wgd, plan->grid,
+                                          plan->act_bytes, ctx->d_status, pick(ctx, stream)));
     else
         AH_HIP(ctx, ah_launch_gemv(plan->type, none, plan->d_parts, plan->d_wg_part, plan->grid,
                                    plan->kpad_max, plan->nc, ctx->d_status, pick(ctx, stream)));
@@ -641,7 +788,8 @@ int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan) {
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     (void)hipFree(plan->d_parts);
-    (void)hipFree(plan->d_wg_part);
+    if (plan->d_wg_part) (void)hipFree(plan->d_wg_part);
+    if (plan->d_wgd) (void)hipFree(plan->d_wgd);
     delete plan;
     return AH_OK;
 }

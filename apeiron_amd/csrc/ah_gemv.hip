@@ -741,30 +741,53 @@ constexpr uint32_t kStreamTile = kChunks * 1024;   // bytes per tile
 constexpr uint32_t kSlotBytes = kStreamTile + 128; // + what realigned or compact-row unit reads touch past a tile
 constexpr uint32_t kOob = 0xFFFFFFF0u;             // past any payload (payloads stay below 4 GiB - 256)
 
-// PLAN: the workgroup's part comes from a plan's table (else the launch argument); either way the
-// descriptor is read with scalar loads, which do not queue behind the vector memory stream.
+// Part descriptor `i` of a plan's table, every word in a scalar register.
+AH_DEV GemvPart part_at(const GemvPart *__restrict__ parts, uint32_t i) {
+    GemvPart P = parts[i];
+    uint32_t w[sizeof(GemvPart) / 4];
+    __builtin_memcpy(w, &P, sizeof(P));
+#pragma unroll
+    for (uint32_t k = 0; k < sizeof(GemvPart) / 4; ++k) w[k] = __builtin_amdgcn_readfirstlane(w[k]);
+    __builtin_memcpy(&P, w, sizeof(P));
+    return P;
+}
+
+// PLAN: each wave's part and rows come from the workgroup's StreamWG entry (read with scalar
+// loads, which do not queue behind the vector memory stream), and the workgroup first quantizes
+// the activations of all its waves' parts.  Otherwise every wave serves the launch argument's
+// part, its rows split evenly over the grid's waves.
 // DOTS: the debug form that also stores exact group dots (single launches only).
+// LDS: [activation region: act_bytes][one tile slot per wave].
 template <int TYPE, bool PLAN, bool DOTS>
 __global__ void __launch_bounds__(kSThreads, 4)
     gemv_stream_kernel(GemvPart single, const GemvPart *__restrict__ parts,
-                       const uint32_t *__restrict__ wg_part, uint32_t kpad_max,
+                       const StreamWG *__restrict__ wgd, uint32_t act_bytes,
                        unsigned long long *status) {
     extern __shared__ __align__(16) uint8_t smem[];
-    GemvPart P;
-    if constexpr (PLAN)
-        P = parts[__builtin_amdgcn_readfirstlane(wg_part[blockIdx.x])];
-    else
-        P = single;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    GemvPart P;
+    uint32_t r_begin, r_end, aoff = 0;
+    if constexpr (PLAN) {
+        const StreamWG *D = wgd + blockIdx.x;
+        const uint32_t pi = D->wave_part[wv];
+        const bool idle = pi == kIdleWave;
+        P = part_at(parts, idle ? D->act_part[0] : pi);  // an idle wave streams no rows
+        r_begin = D->r_begin[wv];
+        r_end = idle ? r_begin : D->r_end[wv];
+        aoff = D->act_off[D->wave_act[wv]];
+    } else {
+        P = single;
+        const uint32_t n_waves = P.wg_count * kSWaves;
+        const uint32_t wl = (blockIdx.x - P.wg_begin) * kSWaves + wave;
+        r_begin = (uint32_t)((uint64_t)P.n_out * wl / n_waves);
+        r_end = (uint32_t)((uint64_t)P.n_out * (wl + 1) / n_waves);
+    }
     const uint32_t kpad = (P.n_in + 255) / 256 * 256;
-    const ActLds A = carve(smem, kpad_max);
-    uint8_t *tl = reinterpret_cast<uint8_t *>(A.xs16 + kpad_max / 16) + wave * kSlotBytes;
+    const ActLds A = carve(smem + aoff, kpad);
+    uint8_t *tl = smem + act_bytes + wave * kSlotBytes;
     const __amdgpu_buffer_rsrc_t rs = ah_rsrc(P.w, (uint32_t)P.w_bytes);
     const uint32_t U = P.units, RW = P.rows_per_tile, RB = P.row_bytes, G = P.lanes;
-    const uint32_t n_waves = P.wg_count * kSWaves;
-    const uint32_t wl = (blockIdx.x - P.wg_begin) * kSWaves + wave;
-    const uint32_t r_begin = (uint32_t)((uint64_t)P.n_out * wl / n_waves);
-    const uint32_t r_end = (uint32_t)((uint64_t)P.n_out * (wl + 1) / n_waves);
     const uint32_t n_t = (r_end - r_begin + RW - 1) / RW;
 
     // Tile t's loads.  Issued unconditionally (a tile past the wave's rows loads nothing) so that
@@ -783,31 +806,52 @@ __global__ void __launch_bounds__(kSThreads, 4)
         }
     };
 
-    // Prologue.  Every wave's activation loads go out before any tile load of the workgroup (the
-    // barrier orders issue, not completion), tile 0 follows at once, and the quantizer runs from
-    // registers while tile 0 streams in.  After the barrier that publishes the activation each
-    // wave stages its own tile 0 and requests tile 1, so no wave waits for another's tile.
-    const uint32_t nbp = kpad / 32, QB = kSThreads / 4;
-    const uint32_t passes = (nbp + QB - 1) / QB;
-    const ActRsrc xr = act_rsrc(P.x, P.scales, P.src, P.n_in);
-    const QuadIn x0 = quad_load_row(xr, P.src, P.n_in, threadIdx.x / 4);
-    const QuadIn x1 = quad_load_row(xr, P.src, P.n_in, QB + threadIdx.x / 4);  // past the row: zeros
-    ah_lds_barrier();
-    load_tile(0);
-    // a wave whose 16 blocks all lie past the activation has nothing to quantize
+    // Prologue.  Single part: every wave's activation loads go out before any tile load of the
+    // workgroup (the barrier orders issue, not completion), tile 0 follows at once, and the
+    // quantizer runs from registers while tile 0 streams in.  Plan: each wave requests its own
+    // tile 0 first, then the workgroup quantizes its activations one after another.  After the
+    // barrier that publishes the activations each wave stages its own tile 0 and requests tile 1,
+    // so no wave waits for another's tile.
+    constexpr uint32_t QB = kSThreads / 4;
+    if constexpr (PLAN) {
+        load_tile(0);
+        const StreamWG *D = wgd + blockIdx.x;
+        const uint32_t n_act = D->n_act;
+        for (uint32_t a = 0; a < n_act; ++a) {
+            const GemvPart Pa = part_at(parts, D->act_part[a]);
+            const uint32_t nbpa = (Pa.n_in + 255) / 256 * 8;
+            const ActLds Aa = carve(smem + D->act_off[a], nbpa * 32);
+            const ActRsrc xra = act_rsrc(Pa.x, Pa.scales, Pa.src, Pa.n_in);
+            for (uint32_t base = 0; base < nbpa; base += QB) {
+                if (base + wave * 16 >= nbpa) break;  // this wave's 16 blocks lie past the activation
+                const uint32_t b = base + threadIdx.x / 4;
+                const QuadOut o = quad_quant(quad_load_row(xra, Pa.src, Pa.n_in, b), Pa.src, b, status, 0);
+                if (b < nbpa) store_quad(Aa, b, o);
+            }
+        }
+    } else {
+        const uint32_t nbp = kpad / 32;
+        const uint32_t passes = (nbp + QB - 1) / QB;
+        const ActRsrc xr = act_rsrc(P.x, P.scales, P.src, P.n_in);
+        const QuadIn x0 = quad_load_row(xr, P.src, P.n_in, threadIdx.x / 4);
+        const QuadIn x1 = quad_load_row(xr, P.src, P.n_in, QB + threadIdx.x / 4);  // past the row: zeros
+        ah_lds_barrier();
+        load_tile(0);
+        // a wave whose 16 blocks all lie past the activation has nothing to quantize
 #pragma unroll
-    for (uint32_t p = 0; p < 2; ++p) {
-        const uint32_t b = p * QB + threadIdx.x / 4;
-        if (p < passes && p * QB + wave * 16 < nbp) {
-            const QuadOut o = quad_quant(p ? x1 : x0, P.src, b, status, 0);
+        for (uint32_t p = 0; p < 2; ++p) {
+            const uint32_t b = p * QB + threadIdx.x / 4;
+            if (p < passes && p * QB + wave * 16 < nbp) {
+                const QuadOut o = quad_quant(p ? x1 : x0, P.src, b, status, 0);
+                if (b < nbp) store_quad(A, b, o);
+            }
+        }
+        for (uint32_t p = 2; p < passes; ++p) {  // activations past 2 * 128 blocks (K > 8192)
+            const uint32_t b = p * QB + threadIdx.x / 4;
+            if (p * QB + wave * 16 >= nbp) break;
+            const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, 0);
             if (b < nbp) store_quad(A, b, o);
         }
-    }
-    for (uint32_t p = 2; p < passes; ++p) {  // activations past 2 * 128 blocks (K > 8192)
-        const uint32_t b = p * QB + threadIdx.x / 4;
-        if (p * QB + wave * 16 >= nbp) break;
-        const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, 0);
-        if (b < nbp) store_quad(A, b, o);
     }
     auto stage = [&](uint32_t t) {  // tile t (in registers) to the slot; request tile t + 1
 #pragma unroll
@@ -857,10 +901,13 @@ bool ah_gemv_stream_geometry(uint32_t row_bytes, uint32_t units, uint32_t &rows,
     return true;
 }
 
-size_t ah_gemv_stream_lds_bytes(uint32_t kpad_max) {
-    return kpad_max + kpad_max / 16 + (size_t)kpad_max / 32 * 8 + (size_t)kpad_max / 16 * 4 +
-           (size_t)kSWaves * kSlotBytes;
+// LDS bytes of one part's quantized activation (codes with padding, fsc, xs32, xs16): a multiple
+// of 16 for any kpad that is a multiple of 256.
+size_t ah_gemv_act_bytes(uint32_t kpad) {
+    return kpad + kpad / 16 + (size_t)kpad / 32 * 8 + (size_t)kpad / 16 * 4;
 }
+size_t ah_gemv_stream_slot_bytes() { return (size_t)kSWaves * kSlotBytes; }
+size_t ah_gemv_stream_lds_bytes(uint32_t kpad_max) { return ah_gemv_act_bytes(kpad_max) + ah_gemv_stream_slot_bytes(); }
 
 uint32_t ah_gemv_stream_threads() { return kSThreads; }
 
@@ -886,20 +933,21 @@ int ah_gemv_stream_occupancy(uint32_t type, size_t lds) {
     return n0 < n1 ? n0 : n1;
 }
 
+// act_bytes: the activation region (a plan's budget; for a single part ah_gemv_act_bytes of its kpad).
 hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const GemvPart *d_parts,
-                                 const uint32_t *d_wg_part, uint32_t grid, uint32_t kpad_max,
+                                 const StreamWG *d_wgd, uint32_t grid, uint32_t act_bytes,
                                  unsigned long long *status, hipStream_t stream) {
-    const size_t lds = ah_gemv_stream_lds_bytes(kpad_max);
+    const size_t lds = act_bytes + ah_gemv_stream_slot_bytes();
 #define AH_SLAUNCH(T)                                                                              \
     if (d_parts)                                                                                   \
         hipLaunchKernelGGL((gemv_stream_kernel<T, true, false>), dim3(grid), dim3(kSThreads), lds,  \
-                           stream, single, d_parts, d_wg_part, kpad_max, status);                 \
+                           stream, single, d_parts, d_wgd, act_bytes, status);                    \
     else if (single.dots)                                                                          \
         hipLaunchKernelGGL((gemv_stream_kernel<T, false, true>), dim3(grid), dim3(kSThreads), lds,  \
-                           stream, single, d_parts, d_wg_part, kpad_max, status);                 \
+                           stream, single, d_parts, d_wgd, act_bytes, status);                    \
     else                                                                                           \
         hipLaunchKernelGGL((gemv_stream_kernel<T, false, false>), dim3(grid), dim3(kSThreads), lds, \
-                           stream, single, d_parts, d_wg_part, kpad_max, status);
+                           stream, single, d_parts, d_wgd, act_bytes, status);
     switch (type) {
     case AH_GGML_Q8_0: AH_SLAUNCH(AH_GGML_Q8_0) break;
     case AH_GGML_Q4_K: AH_SLAUNCH(AH_GGML_Q4_K) break;

@@ -165,6 +165,19 @@ struct GemvPart {
     uint32_t src;          // AH_SRC_*
 };
 
+// Streaming GEMV plan: what one workgroup serves.  Each of its 8 waves streams a row range of one
+// part; the workgroup quantizes the activation of every part its waves use into its own LDS
+// region first.
+constexpr uint32_t kIdleWave = 0xFFFFFFFFu;  // wave_part of a wave with no rows
+struct StreamWG {
+    uint32_t n_act;        // distinct parts (activations) of the workgroup
+    uint32_t act_part[8];  // their part indices
+    uint32_t act_off[8];   // LDS byte offsets of their activations
+    uint32_t wave_part[8]; // per wave: part index, or kIdleWave
+    uint32_t wave_act[8];  // per wave: index into act_*
+    uint32_t r_begin[8], r_end[8];
+};
+
 struct QuantArgs {
     const void *x;         // f32 or int64 [n_tok][n_in]
     int8_t *codes;         // [n_tok][n_in]

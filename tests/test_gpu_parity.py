@@ -245,6 +245,46 @@ def test_grouped_plan_matches_single_launches(dev):
         w.free()
 
 
+def _plan_vs_singles(dev, t, shapes, seed):
+    rng = synth.rng_for(5, seed)
+    ws, xs, ys, singles = [], [], [], []
+    for n_out, n_in in shapes:
+        raw = synth.payload(t, rng, n_out, n_in)
+        w = dev.upload(t, raw, n_out, n_in)
+        x = to_dev(synth.activations(rng, n_in))
+        y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+        ys1 = torch.zeros(n_out, dtype=torch.float32, device="cuda")
+        w.gemv_f32_dev(ptr(x), ptr(ys1), stream())
+        ws.append(w), xs.append(x), ys.append(y), singles.append(ys1)
+    plan = chart.GemvPlan(dev, ws, [ptr(x) for x in xs], [ptr(y) for y in ys])
+    for _ in range(2):
+        plan.run(stream())
+    assert dev.sync_status(stream()) == 0
+    for i, (y, s1) in enumerate(zip(ys, singles)):
+        assert torch.equal(y, s1), (t, i, shapes[i])
+    plan.free()
+    for w in ws:
+        w.free()
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+def test_plan_many_small_parts(dev, t):
+    # one-tile parts get one wave each: workgroups serve up to 8 parts (8 activations in LDS),
+    # mixed K, ragged rows, and trailing idle waves in the last workgroup
+    shapes = [(3 + i % 5, (96, 300, 896, 1024)[i % 4]) for i in range(61)]
+    _plan_vs_singles(dev, t, shapes, 10 + t)
+
+
+@pytest.mark.parametrize("t", [8, 12])
+def test_plan_activation_budget_padding(dev, t):
+    # consecutive one-wave parts with K = 4864 overflow a workgroup's activation budget after two:
+    # the next part starts a new workgroup and the skipped waves stay idle
+    shapes = []
+    for i in range(12):
+        shapes += [(2, 4864), (5, 896)] if i % 3 == 0 else [(2, 4864)]
+    _plan_vs_singles(dev, t, shapes, 30 + t)
+
+
 def test_upload_refusals(dev):
     raw = synth.payload(8, synth.rng_for(0, 1), 4, 64)
     with pytest.raises(chart.MatvecError) as e:

@@ -8,8 +8,11 @@
  * status.  No exceptions cross the ABI.  All paths cited below are in the apeiron tree.
  *
  * Conventions
- *   - Weights live on the device in their unchanged GGUF byte layout: n_out rows of
- *     ceil(n_in/qk) whole blocks (ops/matvec.rs:164-175).
+ *   - Weights live on the device in their GGUF block layout: n_out rows of ceil(n_in/qk) whole
+ *     blocks (ops/matvec.rs:164-175).  One exception, made by ah_upload_weight only: a Q4_K row
+ *     whose n_in is not a multiple of 256 (n_in <= 8192) is stored without the trailing qs
+ *     chunks of its last super-block, which the product never reads (ah_tensor_info reports the
+ *     device row stride).  Results are identical either way.
  *   - Activations are f32 (converted exactly as F32::to_q32, num/fp.rs:186-230) or
  *     Q32.32 int64 (the engine's own type, engine/mod.rs:58-80), or already quantized
  *     (codes int8 + scales int64, the QuantAct of chart/mod.rs:67-81).
@@ -77,7 +80,8 @@ int32_t ah_last_hip_error(const ah_ctx *ctx);
 
 /* ---- weights -------------------------------------------------------------------------------- */
 
-/* Copy an n_out x n_in GGUF payload (host bytes, unchanged layout) to the device.
+/* Copy an n_out x n_in GGUF payload (host bytes) to the device (ragged Q4_K rows compacted, see
+ * Conventions).
  * Validates geometry like matvec_fixed (ops/matvec.rs:160-175: UNSUPPORTED_QUANT,
  * LENGTH_OVERFLOW, SHORT_PAYLOAD) and scans every f16 block scale (d, dmin) for Inf/NaN:
  * a non-finite tensor is refused with AH_ERR_NONFINITE_SCALE, the refusal the reference's
@@ -90,7 +94,7 @@ int32_t ah_upload_weight(ah_ctx *ctx, uint32_t ggml_type, const void *raw, size_
 int32_t ah_wrap_weight_dev(ah_ctx *ctx, uint32_t ggml_type, const void *d_raw, size_t raw_len,
                            size_t n_out, size_t n_in, ah_tensor **out);
 int32_t ah_free_tensor(ah_ctx *ctx, ah_tensor *t);
-/* Geometry of a tensor: ggml type, n_out, n_in, row stride in bytes, device pointer. */
+/* Geometry of a tensor: ggml type, n_out, n_in, device row stride in bytes, device pointer. */
 int32_t ah_tensor_info(const ah_tensor *t, uint32_t *ggml_type, size_t *n_out, size_t *n_in,
                        size_t *row_bytes, const void **d_raw);
 
@@ -117,7 +121,8 @@ int32_t ah_gemv_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
 /* Grouped GEMV: n_parts independent projections in ONE launch, each with its own weight,
  * f32 input and output (chart/ffn.rs:925 projections_q8act shares one dispatch for q/k/v;
  * here every part may have its own input).  All parts share one ggml type.  A plan fixes the
- * device pointers once (descriptors are uploaded at creation), so running it is one launch
+ * device pointers once (descriptors and the waves' assignment, dealt over the parts by tiles,
+ * are uploaded at creation), so running it is one launch
  * with no host-device traffic -- the form a per-token projection sequence replays. */
 typedef struct ah_gemv_plan ah_gemv_plan;
 int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w,

@@ -25,7 +25,7 @@ EXPORTS = [
     "ah_quant_act_q32_dev", "ah_gemv_f32_dev", "ah_gemv_q8_dev", "ah_gemv_plan_create",
     "ah_gemv_plan_run", "ah_gemv_plan_free", "ah_gemm_f32_dev", "ah_gemm_q8_dev",
     "ah_gemv_q8_dots_dev", "ah_sync_status", "ah_matvec_q8act", "ah_matmat_q8act",
-    "ah_quant_act",
+    "ah_quant_act", "ah_probe_mfma_peak",
 ]
 
 _lib = None
@@ -69,6 +69,7 @@ def load() -> ctypes.CDLL:
         "ah_matvec_q8act": (I32, [P, P, P, P, S, P]),
         "ah_matmat_q8act": (I32, [P, P, P, P, S, P]),
         "ah_quant_act": (I32, [P, P, S, P, P]),
+        "ah_probe_mfma_peak": (I32, [P, U32, ctypes.POINTER(ctypes.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -88,6 +88,12 @@ class Device:
     def sync_status(self, stream: int | None = None) -> int:
         return self.lib.ah_sync_status(self.h, stream)
 
+    def probe_mfma_peak(self, kind: int) -> float:
+        """Measured MFMA-only rate in tera-ops/s (kind 0: int8 32x32x32, 1: f16 32x32x16)."""
+        out = ctypes.c_double(0.0)
+        _check(self.lib.ah_probe_mfma_peak(self.h, kind, ctypes.byref(out)), "probe_mfma_peak")
+        return out.value
+
     # device-pointer forms (enqueue only) -------------------------------------------------
     def quant_act_f32_dev(self, x_ptr: int, n_tok: int, n_in: int, codes_ptr: int,
                           scales_ptr: int, stream: int | None = None) -> None:

@@ -38,6 +38,8 @@ hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uin
 uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
                              uint32_t cus);
 hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream);
+hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, uint32_t *d_sink,
+                         hipStream_t stream, double *tops);
 
 struct ah_ctx {
     int device = -1;
@@ -815,6 +817,23 @@ int32_t ah_sync_status(ah_ctx *ctx, void *stream) {
     int32_t r = reset_status(ctx);
     if (r) return r;
     return (int32_t)(key & 0xffu);
+}
+
+// ---- diagnostics ----
+
+int32_t ah_probe_mfma_peak(ah_ctx *ctx, uint32_t kind, double *tera_ops) {
+    if (!ctx || !tera_ops || kind > 1) return AH_ERR_INVALID_ARG;
+    const size_t o_sink = 256, sink_bytes = (size_t)2 * ctx->cu_count * 256 * 4;
+    int32_t st = ensure_scratch(ctx, o_sink + sink_bytes);
+    if (st) return st;
+    uint8_t *S = static_cast<uint8_t *>(ctx->scratch);
+    const uint32_t seed[8] = {0x9e3779b9u, 0x7f4a7c15u, 0x85ebca6bu, 0xc2b2ae35u,
+                              0x27d4eb2fu, 0x165667b1u, 0xd3a2646cu, 0xfd7046c5u};
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, hipMemcpy(S, seed, sizeof(seed), hipMemcpyHostToDevice));
+    AH_HIP(ctx, ah_probe_mfma(kind, (uint32_t)ctx->cu_count, reinterpret_cast<const uint32_t *>(S),
+                              reinterpret_cast<uint32_t *>(S + o_sink), ctx->stream, tera_ops));
+    return AH_OK;
 }
 
 // ---- host convenience forms ----

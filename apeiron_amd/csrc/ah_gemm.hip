@@ -531,6 +531,101 @@ uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint3
     return best;
 }
 
+// ---- MFMA peak probe ---------------------------------------------------------------------------
+//
+// The instruction's own ceiling, measured rather than quoted: a loop with no memory traffic that
+// issues nothing but the MFMA (KIND 0: v_mfma_i32_32x32x32_i8, KIND 1: v_mfma_f32_32x32x16_f16)
+// into 8 independent accumulators whose operands come from memory (so nothing is a compile-time
+// constant) and differ per accumulator; every accumulator is folded into a per-thread sink, so
+// no MFMA can be dropped (the emitted loop is 8 back-to-back MFMAs and a counter).  Each iteration depends on the last through its accumulator.
+namespace {
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+constexpr int kProbeAcc = 8;
+
+template <int KIND>
+__global__ void __launch_bounds__(256) mfma_probe_kernel(const uint32_t *__restrict__ seed, uint32_t iters,
+                                                         uint32_t *__restrict__ sink) {
+    const uint32_t t = threadIdx.x & 63;
+    uint32_t acc_x = 0;
+    if constexpr (KIND == 0) {
+        v4i a[kProbeAcc], b;
+#pragma unroll
+        for (int i = 0; i < kProbeAcc; ++i)
+            a[i] = (v4i){(int)(seed[0] ^ t ^ i), (int)seed[1], (int)(seed[2] + i), (int)seed[3]};
+        b = (v4i){(int)seed[4], (int)(seed[5] ^ t), (int)seed[6], (int)seed[7]};
+        v16i c[kProbeAcc];
+#pragma unroll
+        for (int i = 0; i < kProbeAcc; ++i) c[i] = (v16i){};
+        for (uint32_t it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int i = 0; i < kProbeAcc; ++i) c[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b, c[i], 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < kProbeAcc; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc_x ^= (uint32_t)c[i][r];
+    } else {
+        f16x8 a[kProbeAcc], b;
+#pragma unroll
+        for (int i = 0; i < kProbeAcc; ++i) {
+            const u32x4 v = {seed[0] ^ t, seed[1] + (uint32_t)i, seed[2], seed[3]};
+            a[i] = __builtin_bit_cast(f16x8, v & (u32x4){0x3bff3bffu, 0x3bff3bffu, 0x3bff3bffu, 0x3bff3bffu});
+        }
+        const u32x4 vb = {seed[4], seed[5] ^ t, seed[6], seed[7]};
+        b = __builtin_bit_cast(f16x8, vb & (u32x4){0x3bff3bffu, 0x3bff3bffu, 0x3bff3bffu, 0x3bff3bffu});
+        f32x16 c[kProbeAcc];
+#pragma unroll
+        for (int i = 0; i < kProbeAcc; ++i) c[i] = (f32x16){};
+        for (uint32_t it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int i = 0; i < kProbeAcc; ++i) c[i] = mfma(a[i], b, c[i]);
+        }
+        float fsum = 0.0f;  // a float sum: this compiler folded an XOR of the bit patterns to zero
+#pragma unroll
+        for (int i = 0; i < kProbeAcc; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) fsum += c[i][r];
+        acc_x = __builtin_bit_cast(uint32_t, fsum);
+    }
+    sink[blockIdx.x * blockDim.x + threadIdx.x] = acc_x;
+}
+}  // namespace
+
+// Runs the probe on `stream` (two 256-thread workgroups per CU: 2 waves per SIMD, which the 128
+// accumulator registers of each wave allow) and returns the rate in tera-ops per second (int8:
+// 2*32*32*32 ops per MFMA; f16: 2*32*32*16 flops), timed with HIP events.
+hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, uint32_t *d_sink,
+                         hipStream_t stream, double *tops) {
+    const uint32_t grid = 2 * cus, iters = 8192;
+    hipEvent_t e0, e1;
+    hipError_t e = hipEventCreate(&e0);
+    if (e != hipSuccess) return e;
+    e = hipEventCreate(&e1);
+    if (e != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return e;
+    }
+    float ms = 0.0f;
+    for (int rep = 0; rep < 2 && e == hipSuccess; ++rep) {  // the first run warms up the clocks
+        e = hipEventRecord(e0, stream);
+        if (e != hipSuccess) break;
+        if (kind == 0) hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(grid), dim3(256), 0, stream, d_seed, iters, d_sink);
+        else hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(grid), dim3(256), 0, stream, d_seed, iters, d_sink);
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipEventRecord(e1, stream);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (e != hipSuccess) return e;
+    const double per = kind == 0 ? 2.0 * 32 * 32 * 32 : 2.0 * 32 * 32 * 16;
+    const double ops = per * kProbeAcc * iters * ((double)grid * 4);  // 4 waves per workgroup
+    *tops = ms > 0.0f ? ops / (ms * 1e-3) / 1e12 : 0.0;
+    return hipSuccess;
+}
+
 hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes,
                           uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t kpad,
                           const _Float16 *xh, const _Float16 *xmin, const float *tok_scale,

@@ -40,6 +40,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+F16_PEAK_TFLOPS = 2500.0  # dense f16 MFMA peak (the instruction the GEMM computes with)
 LAYERS = 24
 SHAPES = [("q", 896, 896), ("k", 128, 896), ("v", 128, 896), ("o", 896, 896),
           ("gate", 4864, 896), ("up", 4864, 896), ("down", 896, 4864)]
@@ -268,6 +269,14 @@ def main() -> int:
 
     # ---- config 3: N = 512 GEMMs ---------------------------------------------------------------
     if not args.no_gemm and args.only in (None, "gemm"):
+        # The matrix-core ceiling measured on this device: MFMA-only loops on every CU.
+        probe = {"int8_tops": round(dev.probe_mfma_peak(0), 1),
+                 "f16_tflops": round(dev.probe_mfma_peak(1), 1)}
+        log(f"[bench] MFMA-only probe: int8 32x32x32 {probe['int8_tops']:.0f} TOPS "
+            f"({100 * probe['int8_tops'] / INT8_PEAK_TOPS:.1f}% of {INT8_PEAK_TOPS:.0f}), "
+            f"f16 32x32x16 {probe['f16_tflops']:.0f} TFLOPS "
+            f"({100 * probe['f16_tflops'] / F16_PEAK_TFLOPS:.1f}% of {F16_PEAK_TFLOPS:.0f})")
+        result["mfma_probe"] = probe
         gemm = []
         n_tok = 512
         for gt in (synth.Q8_0, synth.Q4_K):
@@ -300,6 +309,7 @@ def main() -> int:
                 gemm.append({"type": synth.NAMES[gt], "shape": [n_out, n_in], "n_tok": n_tok,
                              "us": round(us, 2), "tops": round(tops, 1),
                              "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                             "frac_f16_probe": round(tops / probe["f16_tflops"], 4),
                              "attainable_tops": round(attain, 1),
                              "frac_attainable": round(tops / attain, 4)})
                 log(f"[bench] gemm {synth.NAMES[gt]} {n_out}x{n_in} N{n_tok}: {us:.1f} us "
@@ -453,6 +463,7 @@ def main() -> int:
         "cpu_baseline": result.get("cpu_baseline"),
         "gemv": result["gemv"],
         "gemm": result.get("gemm"),
+        "mfma_probe": result.get("mfma_probe"),
         "config4": result.get("config4"),
     }
     print(json.dumps(line))

@@ -149,6 +149,15 @@ int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
 int32_t ah_gemv_q8_dots_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
                             const int64_t *d_scales, float *d_y, int32_t *d_dots, void *stream);
 
+/* ---- diagnostics ---- */
+
+/* Measures the matrix-core ceiling that bounds the prefill GEMM: a kernel issuing nothing but
+ * back-to-back MFMAs (kind 0: v_mfma_i32_32x32x32_i8, kind 1: v_mfma_f32_32x32x16_f16, the
+ * instruction the GEMM uses) on every CU, timed with HIP events on the context's stream.
+ * Returns tera-ops per second in *tera_ops.  Plays the part of the reference's DP4A ceiling
+ * probe (gpu/simt/dp4a.rs:1421-1443), which measures the int8 dot rate of its own device. */
+int32_t ah_probe_mfma_peak(ah_ctx *ctx, uint32_t kind, double *tera_ops);
+
 /* ---- status ---- */
 
 /* Synchronize `stream` and return (then clear) the first data-dependent refusal recorded by

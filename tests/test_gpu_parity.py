@@ -387,3 +387,14 @@ def test_gemm_n1_equals_gemv_within_tolerance(dev):
         st2, absdot = oracle.row_absdot(t, raw, 300, 896, codes, scales)
         assert_close(y.cpu().numpy()[0], yref, absdot, f"gemm N=1 t{t}")
         w.free()
+
+
+def test_mfma_probe_within_published_peaks(dev):
+    """The MFMA-only probe must report a positive rate no higher than the dense peak of its
+    instruction (a rate above the peak would mean the compiler dropped MFMAs from the loop)."""
+    i8 = dev.probe_mfma_peak(0)
+    f16 = dev.probe_mfma_peak(1)
+    assert 0.0 < i8 <= 5000.0 * 1.05, i8
+    assert 0.0 < f16 <= 2500.0 * 1.05, f16
+    with pytest.raises(chart.MatvecError):
+        dev.probe_mfma_peak(2)

@@ -97,12 +97,18 @@ constexpr uint32_t kOob = 0xFFFFFFF0u;  // a buffer offset past any operand: rea
 // super-block position of each stage are compile-time: no runtime register indexing, no copies
 // between register sets.
 namespace rb {
-constexpr int kNN = 1, kNM = 4;                 // column / row tiles per wave
-constexpr int kTok = 32 * kNM;                  // tokens per workgroup
+constexpr int kNN = 1;                          // column tiles per wave
 constexpr int kRows = 4 * 32 * kNN;             // weight rows per workgroup
-constexpr int kActBytes = kTok * kPitch;        // f16 activation slice of one stage
-constexpr int kBufBytes = kActBytes + kTok * 32; // + Q4_K split code sums of the super-block
+// Row (token) tiles per wave.  Q8_0 and Q6_K are bound by VALU work per MFMA (the per-block
+// folds), so each dequantized weight fragment feeds 4 token tiles.  Q4_K folds once per
+// super-block and is bound by stalls of its single wave per SIMD instead: 2 token tiles halve
+// the registers and the tile, so two workgroups share a CU at prefill sizes.
+template <int TYPE> constexpr int nm() { return TYPE == AH_GGML_Q4_K ? 2 : 4; }
+template <int TYPE> constexpr int tok() { return 32 * nm<TYPE>(); }              // tokens per workgroup
+template <int TYPE> constexpr int act_bytes() { return tok<TYPE>() * kPitch; }   // f16 slice of a stage
+template <int TYPE> constexpr int buf_bytes() { return act_bytes<TYPE>() + tok<TYPE>() * 32; }  // + Q4_K sums
 template <int TYPE> constexpr int unroll() { return TYPE == AH_GGML_Q8_0 ? 2 : 4; }
+inline uint32_t tok_of(uint32_t type) { return type == AH_GGML_Q4_K ? tok<AH_GGML_Q4_K>() : tok<AH_GGML_Q8_0>(); }
 }  // namespace rb
 
 // Weight bytes of one stage for the lane's NN rows, fetched a stage ahead.  Ordinary (not
@@ -185,8 +191,9 @@ AH_DEV uint32_t q4k_scale(uint32_t s0, uint32_t s1, uint32_t s2) {
 
 template <int TYPE>
 __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
-    constexpr int U = rb::unroll<TYPE>(), NN = rb::kNN, NM = rb::kNM;
-    __shared__ __align__(16) uint8_t lds[2][rb::kBufBytes];
+    constexpr int U = rb::unroll<TYPE>(), NN = rb::kNN, NM = rb::nm<TYPE>();
+    constexpr int kTok = rb::tok<TYPE>(), kActBytes = rb::act_bytes<TYPE>();
+    __shared__ __align__(16) uint8_t lds[2][rb::buf_bytes<TYPE>()];
     // XCD-aware order: dispatch i goes to XCD i % 8, so XCD x takes logical ids
     // [x * per, (x + 1) * per).  Consecutive logical ids share a weight row tile and split, so the
     // workgroups reading the same weights share one XCD's L2.  The grid is a multiple of 8.
@@ -207,8 +214,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
         rl[n] = r < a.n_out;
         rbase[n] = (rl[n] ? r : 0u) * a.row_bytes;
     }
-    const uint32_t tok0 = tt * rb::kTok;
-    const uint32_t ntile = a.n_tok - tok0 < (uint32_t)rb::kTok ? a.n_tok - tok0 : (uint32_t)rb::kTok;
+    const uint32_t tok0 = tt * kTok;
+    const uint32_t ntile = a.n_tok - tok0 < (uint32_t)kTok ? a.n_tok - tok0 : (uint32_t)kTok;
     const __amdgpu_buffer_rsrc_t rs = ah_rsrc(a.w, a.w_bytes);
     const __amdgpu_buffer_rsrc_t rx = ah_rsrc(a.xh + (size_t)tok0 * a.kpad, ntile * a.kpad * 2u);
     const uint32_t nsb = a.kpad / 256;
@@ -234,8 +241,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
             areg[i] = ah_ld128(rx, live && t < ntile ? (t * a.kpad + st * kKS + 8 * kc) * 2u : kOob);
         }
         if constexpr (TYPE == AH_GGML_Q4_K) {
-            const uint32_t t = (tid >> 1) & (rb::kTok - 1), hc = tid & 1;
-            mreg = ah_ld128(rm, live && tid < 2 * rb::kTok && t < ntile ? ((t * nsb + st / 4) * 16 + 8 * hc) * 2u : kOob);
+            const uint32_t t = (tid >> 1) & (kTok - 1), hc = tid & 1;
+            mreg = ah_ld128(rm, live && tid < 2 * kTok && t < ntile ? ((t * nsb + st / 4) * 16 + 8 * hc) * 2u : kOob);
         }
     };
     auto act_store = [&](uint8_t *buf) {
@@ -245,8 +252,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
             *reinterpret_cast<u32x4 *>(buf + t * kPitch + 16 * kc) = areg[i];
         }
         if constexpr (TYPE == AH_GGML_Q4_K) {
-            if (tid < 2 * rb::kTok)  // whole waves
-                *reinterpret_cast<u32x4 *>(buf + rb::kActBytes + (tid >> 1) * 32 + 16 * (tid & 1)) = mreg;
+            if (tid < 2 * kTok)  // whole waves
+                *reinterpret_cast<u32x4 *>(buf + kActBytes + (tid >> 1) * 32 + 16 * (tid & 1)) = mreg;
         }
     };
     auto frag = [&](const uint8_t *buf, int m, int kk) -> f16x8 {
@@ -423,7 +430,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
                     const f16x8 bm = pack8(as_u(m01), as_u(m23), as_u(m45), as_u(m67));
 #pragma unroll
                     for (int m = 0; m < NM; ++m) {
-                        const f16x8 am = *reinterpret_cast<const f16x8 *>(cur + rb::kActBytes + (32 * m + j) * 32 + 16 * h);
+                        const f16x8 am = *reinterpret_cast<const f16x8 *>(cur + kActBytes + (32 * m + j) * 32 + 16 * h);
                         const f32x16 pm = mfma(am, bm, (f32x16){});
 #pragma unroll
                         for (int r = 0; r < 16; ++r)
@@ -495,8 +502,8 @@ struct GemmGeom {
     uint32_t nstages, unroll, rows, toks;
 };
 GemmGeom geom_of(uint32_t type, uint32_t n_in, uint32_t kpad) {
-    if (type == AH_GGML_Q8_0) return {(n_in + 2 * kKS - 1) / (2 * kKS) * 2, 2, rb::kRows, rb::kTok};
-    return {kpad / kKS, 4, rb::kRows, rb::kTok};  // K-quants: whole super-blocks
+    if (type == AH_GGML_Q8_0) return {(n_in + 2 * kKS - 1) / (2 * kKS) * 2, 2, rb::kRows, rb::tok_of(type)};
+    return {kpad / kKS, 4, rb::kRows, rb::tok_of(type)};  // K-quants: whole super-blocks
 }
 
 // Stages per split for a requested split count: a multiple of the unroll.
@@ -520,7 +527,9 @@ uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint3
         const uint32_t per = per_split(g, want);
         const uint32_t used = (g.nstages + per - 1) / per;
         if (used != want) continue;
-        const double waves = (double)((tiles * used + cus - 1) / cus);
+        // workgroups resident per CU: two of the Q4_K kernel's 64-token tiles, one otherwise
+        const uint64_t slots = (uint64_t)cus * (type == AH_GGML_Q4_K ? 2 : 1);
+        const double waves = (double)((tiles * used + slots - 1) / slots);
         double cost = waves * per * 0.25;
         if (used > 1) cost += (double)(used + 1) * n_tok * n_out * 4.0 / 4.0e6;
         if (cost < best_cost) {
@@ -537,7 +546,8 @@ uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint3
 // issues nothing but the MFMA (KIND 0: v_mfma_i32_32x32x32_i8, KIND 1: v_mfma_f32_32x32x16_f16)
 // into 8 independent accumulators whose operands come from memory (so nothing is a compile-time
 // constant) and differ per accumulator; every accumulator is folded into a per-thread sink, so
-// no MFMA can be dropped (the emitted loop is 8 back-to-back MFMAs and a counter).  Each iteration depends on the last through its accumulator.
+// no MFMA can be dropped (the emitted loop is 8 back-to-back MFMAs and a counter).  Each
+// iteration depends on the last through its accumulator.
 namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));

@@ -595,60 +595,82 @@ AH_DEV int wave_max(int v) {
 }
 // GEMM activation operand straight from the input, one workgroup per token.  Every 32-block is
 // quantized once, bit-exactly (quant_act, chart/mod.rs:258-334; refusals recorded as quant_kernel
-// does), into LDS.  The token's largest block exponent E is then the max of the block exponents
-// (act_scale is monotone in absmax, kern/pow2.rs:11-39), and a second pass over LDS writes
+// does).  The token's largest block exponent E is the max of the block exponents (act_scale is
+// monotone in absmax, kern/pow2.rs:11-39); with it the kernel writes
 //   xh   = xq * 2^(e_b - E) in f16 (exact whenever e_b - E >= -24),
 //   tok_scale = 2^(E - 32),
 //   xmin (Q4_K) = per 32-block code sum X split exactly as [64*floor(X/64), X mod 64] * 2^(e_b - E),
 //        laid out per super-block as [hi 0..7, lo 0..7].
 // With codes input (AH_SRC_CODES) the block exponents come from the power-of-two scales.
-// The source kind is a template parameter: the three quantizer paths do not share one body.
-constexpr uint32_t kOpMaxBlocks = AH_MAX_N_IN / 32;
+// A quad of lanes owns a block per round and R rounds cover the padded row, so every input load
+// of the token is issued before the first is used and the quantized blocks stay in registers: one
+// memory round trip, one reduction of E, then the stores.
+constexpr uint32_t kOpBlocks = kThreads / 4;  // blocks per round
+
+// One quad lane's inputs for block b, issuing only the loads its source kind needs: two 16-byte
+// loads of f32, or 8 code bytes plus the block scale (dword loads: the row must start on a 4-byte
+// boundary, i.e. n_in % 4 == 0).  Past n_in the resource reads zeros.
 template <uint32_t SRC>
+AH_DEV QuadIn operand_load(const ActRsrc &r, uint32_t n_in, uint32_t b) {
+    QuadIn in;
+    const uint32_t k0 = b * 32 + 8 * (threadIdx.x & 3);
+    in.take = n_in > k0 ? (n_in - k0 < 8 ? n_in - k0 : 8) : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) in.w[i] = 0;
+    in.s0 = in.s1 = 0;
+    if constexpr (SRC == AH_SRC_F32) {
+        const u32x4 l0 = ah_ld128(r.x, 4 * k0), l1 = ah_ld128(r.x, 4 * k0 + 16);
+        in.w[0] = l0.x; in.w[1] = l0.y; in.w[2] = l0.z; in.w[3] = l0.w;
+        in.w[4] = l1.x; in.w[5] = l1.y; in.w[6] = l1.z; in.w[7] = l1.w;
+    } else {
+        const u32x2 c = ah_ld64(r.x, k0), sc = ah_ld64(r.s, 8 * b);
+        in.w[0] = c.x;
+        in.w[1] = c.y;
+        in.s0 = sc.x;
+        in.s1 = sc.y;
+    }
+    return in;
+}
+
+template <uint32_t SRC, uint32_t R>
 __global__ void __launch_bounds__(kThreads) gemm_operand_kernel(OperandArgs o) {
+    static_assert(SRC == AH_SRC_F32 || SRC == AH_SRC_CODES, "the GEMM takes f32 or code inputs");
     __shared__ uint32_t red[kThreads / 64];
-    __shared__ u32x2 lcodes[kOpMaxBlocks * 4];  // 8 codes per quad lane
-    __shared__ int lexp[kOpMaxBlocks], lsum[kOpMaxBlocks];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = tid & 3;
     const uint32_t tok = blockIdx.x;
     const size_t row = (size_t)tok * o.n_in;
-    const uint32_t esz = SRC == AH_SRC_F32 ? 4u : SRC == AH_SRC_Q32 ? 8u : 1u;
+    const uint32_t esz = SRC == AH_SRC_F32 ? 4u : 1u;
     const int64_t *srow = SRC == AH_SRC_CODES ? o.scales + (size_t)tok * o.nb32 : nullptr;
     const ActRsrc r = act_rsrc(static_cast<const uint8_t *>(o.x) + row * esz, srow, SRC, o.n_in);
     const uint32_t nbp = o.kpad / 32;
-    // pass 1: quantize every block into LDS; E = the largest block exponent.  Four rounds of
-    // blocks are requested before any is quantized, so their loads are in flight together.
-    constexpr uint32_t kRounds = 4, kPer = kThreads / 4;
+    // codes rows start at tok * n_in bytes: bytewise loads unless that is a dword boundary
+    const bool bytewise = SRC == AH_SRC_CODES && (o.n_in & 3u) != 0;
+    QuadIn in[R];
+#pragma unroll
+    for (uint32_t u = 0; u < R; ++u) {
+        if (u * kOpBlocks >= nbp) break;  // uniform: rounds past the padded row
+        const uint32_t b = u * kOpBlocks + tid / 4;
+        in[u] = bytewise ? quad_load(o.x, srow, SRC, o.n_in, row, b, b < o.nb32) : operand_load<SRC>(r, o.n_in, b);
+    }
+    uint32_t c0[R], c1[R];
+    int ex[R], sum[R];
     int emax = -1;
-    for (uint32_t base = 0; base < nbp; base += kRounds * kPer) {
-        QuadIn in[kRounds];
 #pragma unroll
-        for (uint32_t u = 0; u < kRounds; ++u) {
-            const uint32_t b = base + u * kPer + tid / 4;
-            // codes rows start at tok * n_in bytes, not always a dword boundary: bytewise loads
-            in[u] = SRC == AH_SRC_CODES ? quad_load(o.x, srow, SRC, o.n_in, row, b, b < o.nb32)
-                                          : quad_load_row(r, SRC, o.n_in, b);
+    for (uint32_t u = 0; u < R; ++u) {
+        if (u * kOpBlocks >= nbp) break;
+        const uint32_t b = u * kOpBlocks + tid / 4;
+        const QuadOut qo = quad_quant(in[u], SRC, b, o.status, (unsigned long long)row);
+        int e = qo.e;
+        if (SRC == AH_SRC_CODES) {
+            const uint64_t S = ((uint64_t)in[u].s1 << 32) | in[u].s0;
+            e = (int64_t)S > 0 ? 63 - __builtin_clzll(S) : -1;
         }
-#pragma unroll
-        for (uint32_t u = 0; u < kRounds; ++u) {
-            if (base + u * kPer >= nbp) break;  // uniform: rounds past the padded row
-            const uint32_t b = base + u * kPer + tid / 4;
-            const QuadOut qo = quad_quant(in[u], SRC, b, o.status, (unsigned long long)row);
-            int e = qo.e;
-            if (SRC == AH_SRC_CODES) {
-                const u32x2 sv = ah_ld64(r.s, 8 * b);
-                const uint64_t S = ((uint64_t)sv.y << 32) | sv.x;
-                e = (int64_t)S > 0 ? 63 - __builtin_clzll(S) : -1;
-            }
-            if (b < nbp) {
-                lcodes[4 * b + q] = (u32x2){qo.c0, qo.c1};
-                if (q == 0) {
-                    lexp[b] = e;
-                    lsum[b] = qo.s32;
-                }
-                emax = e > emax ? e : emax;
-            }
-        }
+        if (b >= nbp) e = -1;
+        c0[u] = qo.c0;
+        c1[u] = qo.c1;
+        ex[u] = e;
+        sum[u] = qo.s32;
+        emax = e > emax ? e : emax;
     }
     emax = wave_max(emax);
     if (lane == 0) red[wave] = (uint32_t)(emax + 1);
@@ -658,23 +680,22 @@ __global__ void __launch_bounds__(kThreads) gemm_operand_kernel(OperandArgs o) {
     for (int w = 0; w < kThreads / 64; ++w) E = (int)red[w] - 1 > E ? (int)red[w] - 1 : E;
     if (E > 62) E = 62;  // a block without a Q32.32 scale: the call is refused anyway
     if (tid == 0) o.tok_scale[tok] = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
-    // pass 2: LDS -> f16 operand
     _Float16 *xh = o.xh + (size_t)tok * o.kpad;
-    for (uint32_t base = 0; base < nbp; base += kThreads / 4) {
-        const uint32_t b = base + tid / 4;
-        if (b >= nbp) break;
-        const u32x2 cw = lcodes[4 * b + q];
-        const int e = lexp[b];
-        const int sh = e - E;
+#pragma unroll
+    for (uint32_t u = 0; u < R; ++u) {
+        if (u * kOpBlocks >= nbp) break;
+        const uint32_t b = u * kOpBlocks + tid / 4;
+        if (b >= nbp) continue;
+        const int e = ex[u], sh = e - E;
         _Float16 hv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int c = (int)(int8_t)(((i < 4 ? cw.x : cw.y) >> (8 * (i & 3))) & 0xffu);
+            const int c = (int)(int8_t)(((i < 4 ? c0[u] : c1[u]) >> (8 * (i & 3))) & 0xffu);
             hv[i] = e < 0 ? (_Float16)0.0f : (_Float16)__builtin_ldexpf((float)c, sh);
         }
         *reinterpret_cast<u32x4 *>(xh + 32 * b + 8 * q) = __builtin_bit_cast(u32x4, hv);
         if (o.xmin && q == 0) {
-            const int X = lsum[b];
+            const int X = sum[u];
             const int hq = (X >= 0 ? X : X - 63) / 64;  // floor(X / 64)
             _Float16 *m = o.xmin + ((size_t)tok * (o.kpad / 256) + b / 8) * 16;
             m[b % 8] = e < 0 ? (_Float16)0.0f : (_Float16)__builtin_ldexpf((float)(64 * hq), sh);
@@ -1034,15 +1055,26 @@ hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart 
     return hipGetLastError();
 }
 
+template <uint32_t SRC>
+static hipError_t launch_operand(const OperandArgs &o, hipStream_t stream) {
+    const uint32_t rounds = (o.kpad / 32 + kOpBlocks - 1) / kOpBlocks;  // kpad <= AH_MAX_N_IN: <= 16
+    const dim3 grid(o.n_tok), block(kThreads);
+    if (rounds <= 1) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 1>), grid, block, 0, stream, o);
+    else if (rounds <= 2) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 2>), grid, block, 0, stream, o);
+    else if (rounds <= 4) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 4>), grid, block, 0, stream, o);
+    else if (rounds <= 8) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 8>), grid, block, 0, stream, o);
+    else if (rounds <= 16) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 16>), grid, block, 0, stream, o);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream) {
     if (o.n_tok == 0) return hipSuccess;
     switch (o.src) {
-    case AH_SRC_F32: hipLaunchKernelGGL(gemm_operand_kernel<AH_SRC_F32>, dim3(o.n_tok), dim3(kThreads), 0, stream, o); break;
-    case AH_SRC_Q32: hipLaunchKernelGGL(gemm_operand_kernel<AH_SRC_Q32>, dim3(o.n_tok), dim3(kThreads), 0, stream, o); break;
-    case AH_SRC_CODES: hipLaunchKernelGGL(gemm_operand_kernel<AH_SRC_CODES>, dim3(o.n_tok), dim3(kThreads), 0, stream, o); break;
+    case AH_SRC_F32: return launch_operand<AH_SRC_F32>(o, stream);
+    case AH_SRC_CODES: return launch_operand<AH_SRC_CODES>(o, stream);
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream) {

@@ -398,3 +398,34 @@ def test_mfma_probe_within_published_peaks(dev):
     assert 0.0 < f16 <= 2500.0 * 1.05, f16
     with pytest.raises(chart.MatvecError):
         dev.probe_mfma_peak(2)
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(96, 301, 5), (130, 8960, 70), (64, 20000, 3), (256, 1536, 129)])
+def test_gemm_codes_input_equals_f32_input(dev, t, n_out, n_in, n_tok):
+    """The codes-input GEMM (quantizer output handed over) equals the f32-input GEMM bit for bit:
+    both build the same f16 operand from the same codes.  Covers bytewise code rows (n_in % 4 != 0),
+    and operand passes of 1, 8 and 16 register rounds; a few columns are checked against the oracle."""
+    rng = synth.rng_for(3, 4000 + t + n_in)
+    raw = synth.payload(t, rng, n_out, n_in)
+    x = synth.activations(rng, n_in, n_tok).reshape(n_tok, n_in)
+    w = dev.upload(t, raw, n_out, n_in)
+    dx = to_dev(x)
+    codes = torch.empty((n_tok, n_in), dtype=torch.int8, device="cuda")
+    scales = torch.empty((n_tok, -(-n_in // 32)), dtype=torch.int64, device="cuda")
+    dev.quant_act_f32_dev(ptr(dx), n_tok, n_in, ptr(codes), ptr(scales), stream())
+    y1 = torch.full((n_tok, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    y2 = torch.full((n_tok, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    w.gemm_f32_dev(ptr(dx), n_tok, ptr(y1), stream())
+    w.gemm_q8_dev(ptr(codes), ptr(scales), n_tok, ptr(y2), stream())
+    assert dev.sync_status(stream()) == 0
+    assert torch.isfinite(y1).all()
+    assert torch.equal(y1, y2)
+    Y = y2.cpu().numpy()
+    for c in sorted({0, n_tok - 1}):
+        st, cq, sq = oracle.quant_act_f32(x[c])
+        st, yref = oracle.matvec_q8act(t, raw, n_out, n_in, cq, sq)
+        st2, absdot = oracle.row_absdot(t, raw, n_out, n_in, cq, sq)
+        assert st == 0 and st2 == 0
+        assert_close(Y[c], yref, absdot, f"gemm codes t{t} {n_out}x{n_in} col {c}")
+    w.free()

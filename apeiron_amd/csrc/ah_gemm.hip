@@ -34,7 +34,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
 constexpr int kKS = 64;                // K depth of one LDS stage
-constexpr int kPitch = kKS * 2 + 16;   // bytes per token row in LDS (padding breaks bank aliasing)
+
 
 AH_DEV f32x16 mfma(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -105,9 +105,33 @@ constexpr int kRows = 4 * 32 * kNN;             // weight rows per workgroup
 // the registers and the tile, so two workgroups share a CU at prefill sizes.
 template <int TYPE> constexpr int nm() { return TYPE == AH_GGML_Q4_K ? 2 : 4; }
 template <int TYPE> constexpr int tok() { return 32 * nm<TYPE>(); }              // tokens per workgroup
-template <int TYPE> constexpr int act_bytes() { return tok<TYPE>() * kPitch; }   // f16 slice of a stage
-template <int TYPE> constexpr int buf_bytes() { return act_bytes<TYPE>() + tok<TYPE>() * 32; }  // + Q4_K sums
+template <int TYPE> constexpr int act_bytes() { return tok<TYPE>() * kKS * 2; }   // f16 slice of a stage
+template <int TYPE> constexpr int buf_bytes() {                                    // + Q4_K split sums
+    return act_bytes<TYPE>() + (TYPE == AH_GGML_Q4_K ? tok<TYPE>() * 32 : 0);
+}
+// Split granularity in stages (Q8_0 pairs, K-quant super-blocks); the loop body is 4 stages.
 template <int TYPE> constexpr int unroll() { return TYPE == AH_GGML_Q8_0 ? 2 : 4; }
+constexpr int kRing = 4;  // LDS slots: the stage being read and three in flight
+// Weight register sets and how many stages ahead they are fetched (Q6_K's 27-register set
+// allows only two sets within the 256-register budget).
+template <int TYPE> constexpr int nw() { return TYPE == AH_GGML_Q6_K ? 2 : 4; }
+template <int TYPE> constexpr int dw() { return TYPE == AH_GGML_Q6_K ? 1 : 2; }
+// Per-wave vector memory instructions a stage issues: activation slice (16-byte direct-to-LDS
+// loads, 1 KB per instruction), Q4_K split sums (4-byte direct-to-LDS loads, 256 B each), and the
+// weight fetch of super-block position P.
+template <int TYPE> constexpr int an() { return tok<TYPE>() * kKS * 2 / 1024 / 4; }
+template <int TYPE> constexpr int xn() { return TYPE == AH_GGML_Q4_K ? tok<TYPE>() * 32 / 256 / 4 : 0; }
+template <int TYPE> constexpr int wn(int P) {
+    return TYPE == AH_GGML_Q8_0 ? 6 : TYPE == AH_GGML_Q6_K ? 9 : (P == 0 ? 2 : 1);
+}
+// At the top of stage slot u, the loads issued after that stage's activation slice: the weight
+// fetch of the stage that issued it and the slices and fetches of the two stages after.  Waiting
+// for vmcnt <= this count completes the slice (vector memory loads complete in issue order).
+template <int TYPE> constexpr int wait_count(int u) {
+    constexpr int D = dw<TYPE>();
+    return wn<TYPE>((u + 1 + D) % 4) + wn<TYPE>((u + 2 + D) % 4) + wn<TYPE>((u + 3 + D) % 4) +
+           2 * (xn<TYPE>() + an<TYPE>());
+}
 inline uint32_t tok_of(uint32_t type) { return type == AH_GGML_Q4_K ? tok<AH_GGML_Q4_K>() : tok<AH_GGML_Q8_0>(); }
 }  // namespace rb
 
@@ -191,9 +215,10 @@ AH_DEV uint32_t q4k_scale(uint32_t s0, uint32_t s1, uint32_t s2) {
 
 template <int TYPE>
 __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
-    constexpr int U = rb::unroll<TYPE>(), NN = rb::kNN, NM = rb::nm<TYPE>();
+    constexpr int NN = rb::kNN, NM = rb::nm<TYPE>(), NW = rb::nw<TYPE>(), DW = rb::dw<TYPE>();
     constexpr int kTok = rb::tok<TYPE>(), kActBytes = rb::act_bytes<TYPE>();
-    __shared__ __align__(16) uint8_t lds[2][rb::buf_bytes<TYPE>()];
+    constexpr int kAN = rb::an<TYPE>(), kXN = rb::xn<TYPE>();
+    __shared__ __align__(16) uint8_t lds[rb::kRing][rb::buf_bytes<TYPE>()];
     // XCD-aware order: dispatch i goes to XCD i % 8, so XCD x takes logical ids
     // [x * per, (x + 1) * per).  Consecutive logical ids share a weight row tile and split, so the
     // workgroups reading the same weights share one XCD's L2.  The grid is a multiple of 8.
@@ -229,35 +254,36 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
     uint32_t st_end = st_begin + a.stages_per_split;
     if (st_end > nstages) st_end = nstages;
 
-    // activation slice of a stage: 32*NM tokens x 128 B = NM 16-B chunks per thread (+ Q4_K: the
-    // 32-B split code sums of the stage's super-block, one 16-B chunk per thread of the first NM
-    // waves)
-    u32x4 areg[NM], mreg;
-    auto act_load = [&](uint32_t st) {
+    // The f16 activation slice of a stage (kTok tokens x 64 K) goes global -> LDS directly (no
+    // registers), three stages ahead.  Wave w's instruction i fills bytes [(w*kAN + i) KB, +1 KB) of
+    // the slot, lane l at +16*l: token t = o / 128 at LDS chunk c' = (o / 16) % 8, which holds the
+    // token's K chunk c' ^ ((t >> 1) & 7).  The XOR spreads the 32 token rows an MFMA fragment read
+    // touches over all 64 banks.  Stages past the split and tokens past the tile read zeros.
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    auto act_dma = [&](uint8_t *buf, uint32_t st) {
         const bool live = st < st_end;
 #pragma unroll
-        for (int i = 0; i < NM; ++i) {
-            const uint32_t c = tid + kThreads * i, t = c >> 3, kc = c & 7;
-            areg[i] = ah_ld128(rx, live && t < ntile ? (t * a.kpad + st * kKS + 8 * kc) * 2u : kOob);
+        for (int i = 0; i < kAN; ++i) {
+            const uint32_t o = (wv * kAN + i) * 1024u + lane * 16u;
+            const uint32_t t = o >> 7, c = ((o >> 4) & 7u) ^ ((t >> 1) & 7u);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rx, (__attribute__((address_space(3))) void *)(buf + (wv * kAN + i) * 1024u), 16,
+                live && t < ntile ? (t * a.kpad + st * kKS + 8 * c) * 2u : kOob, 0, 0, 0);
         }
         if constexpr (TYPE == AH_GGML_Q4_K) {
-            const uint32_t t = (tid >> 1) & (kTok - 1), hc = tid & 1;
-            mreg = ah_ld128(rm, live && tid < 2 * kTok && t < ntile ? ((t * nsb + st / 4) * 16 + 8 * hc) * 2u : kOob);
-        }
-    };
-    auto act_store = [&](uint8_t *buf) {
+            // the 32-byte split code sums of the stage's super-block, [token][32 B] after the slice
 #pragma unroll
-        for (int i = 0; i < NM; ++i) {
-            const uint32_t c = tid + kThreads * i, t = c >> 3, kc = c & 7;
-            *reinterpret_cast<u32x4 *>(buf + t * kPitch + 16 * kc) = areg[i];
-        }
-        if constexpr (TYPE == AH_GGML_Q4_K) {
-            if (tid < 2 * kTok)  // whole waves
-                *reinterpret_cast<u32x4 *>(buf + kActBytes + (tid >> 1) * 32 + 16 * (tid & 1)) = mreg;
+            for (int i = 0; i < kXN; ++i) {
+                const uint32_t o = (wv * kXN + i) * 256u + lane * 4u, t = o >> 5;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rm, (__attribute__((address_space(3))) void *)(buf + kActBytes + (wv * kXN + i) * 256u), 4,
+                    live && t < ntile ? (t * nsb + st / 4) * 32u + (o & 31u) : kOob, 0, 0, 0);
+            }
         }
     };
+    const uint32_t sw = (uint32_t)(j >> 1) & 7u;
     auto frag = [&](const uint8_t *buf, int m, int kk) -> f16x8 {
-        return *reinterpret_cast<const f16x8 *>(buf + (m * 32 + j) * kPitch + 2 * kk);
+        return *reinterpret_cast<const f16x8 *>(buf + (m * 32 + j) * (kKS * 2) + 16 * (((uint32_t)kk >> 3) ^ sw));
     };
 
     f32x16 acc[NM][NN], P[NM][NN];
@@ -273,19 +299,30 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
         s0[n] = s1[n] = s2[n] = 0u;
     }
 
-    act_load(st_begin);
-    act_store(lds[0]);
-    act_load(st_begin + 1);
-    WRb W[2];
-    W[0] = fetch_rb<TYPE, 0, NN>(rs, rbase, rl, st_begin, a.n_in, h, st_begin < st_end);
+    // Prologue: the loads of three notional stages before st_begin, in the loop's own order (slice,
+    // then the weight fetch DW stages ahead of the notional stage; fetches before st_begin are
+    // out-of-range dummies), so every stage's wait count is the same compile-time number.
+    WRb W[NW];
+    auto prologue = [&](auto kc) {
+        constexpr int k = decltype(kc)::value, rel = k - 3 + DW;  // fetched stage - st_begin
+        act_dma(lds[k], st_begin + k);
+        constexpr int wi = ((rel % NW) + NW) % NW, P = ((rel % 4) + 4) % 4;
+        W[wi] = fetch_rb<TYPE, P, NN>(rs, rbase, rl, rel >= 0 ? st_begin + rel : st_begin, a.n_in, h,
+                                      rel >= 0 && st_begin + rel < st_end);
+    };
+    prologue(std::integral_constant<int, 0>{});
+    prologue(std::integral_constant<int, 1>{});
+    prologue(std::integral_constant<int, 2>{});
 
     auto stage = [&](auto uc, uint32_t st) {
         constexpr int u = decltype(uc)::value;
-        const uint8_t *cur = lds[u & 1];
-        ah_lds_barrier();  // buffer `cur` is written; every wave is done with the other one
-        W[(u + 1) & 1] = fetch_rb<TYPE, (u + 1) % U, NN>(rs, rbase, rl, st + 1, a.n_in, h, st + 1 < st_end);
-        __builtin_amdgcn_sched_barrier(0);  // the next stage's weight requests stay a stage ahead
-        const WRb &wc = W[u & 1];
+        // the slice of this stage is complete in every wave, and every wave is done with slot u+3
+        ah_vm_lds_barrier<rb::wait_count<TYPE>(u)>();
+        act_dma(lds[(u + 3) & 3], st + 3);
+        W[(u + DW) % NW] = fetch_rb<TYPE, (u + DW) % 4, NN>(rs, rbase, rl, st + DW, a.n_in, h, st + DW < st_end);
+        __builtin_amdgcn_sched_barrier(0);  // the requests above stay ahead of this stage's work
+        const uint8_t *cur = lds[u];
+        const WRb &wc = W[u % NW];
         if constexpr (TYPE == AH_GGML_Q8_0) {
             // 2*NM*NN MFMA chains per stage (block bb, token tile m, row tile n), each two MFMAs
             // into a fresh accumulator that is folded with the block's d.  The fold of chain c-1
@@ -440,18 +477,17 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
                 }
             }
         }
-        act_store(lds[(u + 1) & 1]);  // stage st+1 (zeros past the split)
-        act_load(st + 2);
     };
 
-    for (uint32_t st = st_begin; st < st_end; st += U) {
+    for (uint32_t st = st_begin; st < st_end; st += 4) {
         stage(std::integral_constant<int, 0>{}, st);
         stage(std::integral_constant<int, 1>{}, st + 1);
-        if constexpr (U == 4) {
-            stage(std::integral_constant<int, 2>{}, st + 2);
-            stage(std::integral_constant<int, 3>{}, st + 3);
-        }
+        if (TYPE == AH_GGML_Q8_0 && st + 2 >= st_end) break;  // Q8_0 splits are whole pairs
+        stage(std::integral_constant<int, 2>{}, st + 2);
+        stage(std::integral_constant<int, 3>{}, st + 3);
     }
+    // the slices requested past the split must land before this workgroup's LDS is released
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // D layout of a 32x32 MFMA: lane (j, h), register r -> row i = 8*(r/4) + 4*h + (r%4), col j.
     // Token scales (1.0 for partials) are loaded up front; lanes past n_out and tokens past n_tok

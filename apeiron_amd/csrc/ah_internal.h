@@ -55,6 +55,12 @@ AH_DEV uint32_t ah_ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 // load, which would drain a prefetch).  The memory clobber keeps the compiler from moving memory
 // operations across it.
 AH_DEV void ah_lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// The same after this wave's vector memory loads have come down to at most N outstanding (they
+// complete in issue order), for direct-to-LDS loads that the compiler does not wait for.
+template <int N> AH_DEV void ah_vm_lds_barrier() {
+    static_assert(N >= 0 && N <= 63, "vmcnt is a 6-bit count");
+    __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 
 // ---- exact integer helpers ----
 

@@ -99,10 +99,11 @@ constexpr uint32_t kOob = 0xFFFFFFF0u;  // a buffer offset past any operand: rea
 namespace rb {
 constexpr int kNN = 1;                          // column tiles per wave
 constexpr int kRows = 4 * 32 * kNN;             // weight rows per workgroup
-// Row (token) tiles per wave.  Q8_0 and Q6_K are bound by VALU work per MFMA (the per-block
-// folds), so each dequantized weight fragment feeds 4 token tiles.  Q4_K folds once per
-// super-block and is bound by stalls of its single wave per SIMD instead: 2 token tiles halve
-// the registers and the tile, so two workgroups share a CU at prefill sizes.
+// Row (token) tiles per wave.  Q8_0 (a fold per block) and Q6_K (two operands per weight, see
+// the Q6_K stage) are bound by VALU work per MFMA, so each dequantized weight fragment feeds 4
+// token tiles.  Q4_K's dequantization is cheap and it is bound by the stalls of a single wave per
+// SIMD instead: 2 token tiles halve the registers and the tile, so two of its workgroups share a
+// CU at prefill sizes.  (Measured each way round: the other choice is 7-11% slower per type.)
 template <int TYPE> constexpr int nm() { return TYPE == AH_GGML_Q4_K ? 2 : 4; }
 template <int TYPE> constexpr int tok() { return 32 * nm<TYPE>(); }              // tokens per workgroup
 template <int TYPE> constexpr int act_bytes() { return tok<TYPE>() * kKS * 2; }   // f16 slice of a stage
@@ -248,8 +249,9 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
         ah_rsrc(TYPE == AH_GGML_Q4_K ? a.xmin + (size_t)tok0 * nsb * 16 : a.xh,
                 TYPE == AH_GGML_Q4_K ? ntile * nsb * 32u : 0u);
 
-    // stages: whole super-blocks for Q4_K (zero activations past n_in), pairs for Q8_0
-    const uint32_t nstages = TYPE == AH_GGML_Q4_K ? a.kpad / kKS : ((a.n_in + 2 * kKS - 1) / (2 * kKS)) * 2;
+    // stages: whole super-blocks for the K-quants (zero activations past n_in; their folds are
+    // per super-block, at its last stage), pairs for Q8_0
+    const uint32_t nstages = TYPE != AH_GGML_Q8_0 ? a.kpad / kKS : ((a.n_in + 2 * kKS - 1) / (2 * kKS)) * 2;
     const uint32_t st_begin = split * a.stages_per_split;
     uint32_t st_end = st_begin + a.stages_per_split;
     if (st_end > nstages) st_end = nstages;
@@ -366,19 +368,21 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
             // Stage u of the super-block: half n = u/2, nibble u&1.  k-step gg is the 16-group
             // G = 4u + gg (one int8 scale); lane half h takes its elements 8h..8h+7, i.e. ql bytes
             // 64n + 16gg + 8h + e, qh bytes 32n + 16(gg&1) + 8h + e at bit 2(2(u&1) + gg/2)
-            // (format/quant.rs:556-599).  B = u - 32 is exact in f16; every group's MFMA goes to a
-            // fresh accumulator folded with d*sc_G, the fold of chain c-1 issued after chain c.
+            // (format/quant.rs:556-599).  The group scale splits as sc = 16a + b (a = sc >> 4 in
+            // -8..7, b = sc & 15), so a weight's sc*(u-32) is the sum of two exact f16 operands,
+            // 16a*(u-32) (a multiple of 16 below 2^12 with at most 9 significant bits) and
+            // b*(u-32) (|.| <= 480).  Both go to MFMAs into the super-block accumulator P, and d
+            // is folded once per super-block: twice the MFMAs of one operand per group, a
+            // sixteenth of the folds.
             const uint32_t sh = (rbase[0] + 210 * (st / 4)) & 3u;  // 0 or 2
             const uint32_t scw = ah_alignbyte(wc.s[1], wc.s[0], sh);
-            const float fd6 = ah_f16_bits_to_f32((wc.s[2] >> (8 * sh)) & 0xffffu);
             const uint32_t ql[16] = {wc.v[0].x, wc.v[0].y, wc.v[0].z, wc.v[0].w, wc.v[1].x, wc.v[1].y,
                                      wc.v[1].z, wc.v[1].w, wc.v[2].x, wc.v[2].y, wc.v[2].z, wc.v[2].w,
                                      wc.v[3].x, wc.v[3].y, wc.v[3].z, wc.v[3].w};
             const uint32_t qh[8] = {wc.v[4].x, wc.v[4].y, wc.v[4].z, wc.v[4].w,
                                     wc.v[5].x, wc.v[5].y, wc.v[5].z, wc.v[5].w};
             constexpr int nib = u & 1;
-            f16x8 bq[4];
-            float coef[4];
+            f16x8 bhi[4], blo[4];
 #pragma unroll
             for (int gg = 0; gg < 4; ++gg) {
                 uint32_t uu[2];
@@ -392,21 +396,29 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
                 uint32_t f[4];
                 u6x4_to_f16(uu[0], f[0], f[1]);
                 u6x4_to_f16(uu[1], f[2], f[3]);
-                bq[gg] = pack8(f[0], f[1], f[2], f[3]);
-                coef[gg] = fd6 * (float)(int)(int8_t)((scw >> (8 * gg)) & 0xffu);
+                const int sc = (int)(int8_t)((scw >> (8 * gg)) & 0xffu);
+                const _Float16 ha = (_Float16)(float)(16 * (sc >> 4)), hb = (_Float16)(float)(sc & 15);
+                const f16x2 a2 = {ha, ha}, b2 = {hb, hb};
+                bhi[gg] = pack8(as_u(as_h2(f[0]) * a2), as_u(as_h2(f[1]) * a2), as_u(as_h2(f[2]) * a2),
+                                as_u(as_h2(f[3]) * a2));
+                blo[gg] = pack8(as_u(as_h2(f[0]) * b2), as_u(as_h2(f[1]) * b2), as_u(as_h2(f[2]) * b2),
+                                as_u(as_h2(f[3]) * b2));
             }
-            constexpr int NC = 4 * NM;
-            f32x16 pq[2];
 #pragma unroll
-            for (int c = 0; c <= NC; ++c) {
-                if (c < NC) {
-                    const int gg = c / NM, m = c % NM;
-                    pq[c & 1] = mfma(frag(cur, m, 16 * gg + 8 * h), bq[gg], (f32x16){});
+            for (int gg = 0; gg < 4; ++gg)
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {
+                    const f16x8 av = frag(cur, m, 16 * gg + 8 * h);
+                    P[m][0] = mfma(av, bhi[gg], P[m][0]);
+                    P[m][0] = mfma(av, blo[gg], P[m][0]);
                 }
-                if (c > 0) {
-                    const int pc = c - 1, gg = pc / NM, m = pc % NM;
+            if constexpr (u == 3) {
+                const float fd6 = ah_f16_bits_to_f32((wc.s[2] >> (8 * sh)) & 0xffffu);
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[m][0][r] = __builtin_fmaf(coef[gg], pq[pc & 1][r], acc[m][0][r]);
+                for (int m = 0; m < NM; ++m) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[m][0][r] = __builtin_fmaf(fd6, P[m][0][r], acc[m][0][r]);
+                    P[m][0] = (f32x16){};
                 }
             }
         } else {  // Q4_K, stage u of the super-block: qs chunk u = sub-blocks 2u (low), 2u+1 (high)

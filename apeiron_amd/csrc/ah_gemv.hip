@@ -604,8 +604,9 @@ AH_DEV int wave_max(int v) {
 // With codes input (AH_SRC_CODES) the block exponents come from the power-of-two scales.
 // A quad of lanes owns a block per round and R rounds cover the padded row, so every input load
 // of the token is issued before the first is used and the quantized blocks stay in registers: one
-// memory round trip, one reduction of E, then the stores.
-constexpr uint32_t kOpBlocks = kThreads / 4;  // blocks per round
+// memory round trip, one reduction of E, then the stores.  Rows past 64 blocks (K > 2048) take
+// 1024-thread workgroups: 16 waves per token keep a CU's 32 wave slots full at prefill sizes,
+// where 4 waves per token left the exact quantizer's VALU work and the load latency exposed.
 
 // One quad lane's inputs for block b, issuing only the loads its source kind needs: two 16-byte
 // loads of f32, or 8 code bytes plus the block scale (dword loads: the row must start on a 4-byte
@@ -632,10 +633,11 @@ AH_DEV QuadIn operand_load(const ActRsrc &r, uint32_t n_in, uint32_t b) {
     return in;
 }
 
-template <uint32_t SRC, uint32_t R>
-__global__ void __launch_bounds__(kThreads) gemm_operand_kernel(OperandArgs o) {
+template <uint32_t SRC, uint32_t R, uint32_t T>
+__global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
     static_assert(SRC == AH_SRC_F32 || SRC == AH_SRC_CODES, "the GEMM takes f32 or code inputs");
-    __shared__ uint32_t red[kThreads / 64];
+    constexpr uint32_t kOpBlocks = T / 4;  // blocks per round
+    __shared__ uint32_t red[T / 64];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = tid & 3;
     const uint32_t tok = blockIdx.x;
     const size_t row = (size_t)tok * o.n_in;
@@ -677,7 +679,7 @@ __global__ void __launch_bounds__(kThreads) gemm_operand_kernel(OperandArgs o) {
     __syncthreads();
     int E = -1;
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) E = (int)red[w] - 1 > E ? (int)red[w] - 1 : E;
+    for (uint32_t w = 0; w < T / 64; ++w) E = (int)red[w] - 1 > E ? (int)red[w] - 1 : E;
     if (E > 62) E = 62;  // a block without a Q32.32 scale: the call is refused anyway
     if (tid == 0) o.tok_scale[tok] = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
     _Float16 *xh = o.xh + (size_t)tok * o.kpad;
@@ -1057,13 +1059,12 @@ hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart 
 
 template <uint32_t SRC>
 static hipError_t launch_operand(const OperandArgs &o, hipStream_t stream) {
-    const uint32_t rounds = (o.kpad / 32 + kOpBlocks - 1) / kOpBlocks;  // kpad <= AH_MAX_N_IN: <= 16
-    const dim3 grid(o.n_tok), block(kThreads);
-    if (rounds <= 1) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 1>), grid, block, 0, stream, o);
-    else if (rounds <= 2) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 2>), grid, block, 0, stream, o);
-    else if (rounds <= 4) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 4>), grid, block, 0, stream, o);
-    else if (rounds <= 8) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 8>), grid, block, 0, stream, o);
-    else if (rounds <= 16) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 16>), grid, block, 0, stream, o);
+    const uint32_t nbp = o.kpad / 32;  // kpad <= AH_MAX_N_IN: <= 1024 blocks
+    const dim3 grid(o.n_tok);
+    if (nbp <= 64) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 1, 256>), grid, dim3(256), 0, stream, o);
+    else if (nbp <= 256) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 1, 1024>), grid, dim3(1024), 0, stream, o);
+    else if (nbp <= 512) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 2, 1024>), grid, dim3(1024), 0, stream, o);
+    else if (nbp <= 1024) hipLaunchKernelGGL((gemm_operand_kernel<SRC, 4, 1024>), grid, dim3(1024), 0, stream, o);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

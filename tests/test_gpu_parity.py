@@ -405,7 +405,8 @@ def test_mfma_probe_within_published_peaks(dev):
 def test_gemm_codes_input_equals_f32_input(dev, t, n_out, n_in, n_tok):
     """The codes-input GEMM (quantizer output handed over) equals the f32-input GEMM bit for bit:
     both build the same f16 operand from the same codes.  Covers bytewise code rows (n_in % 4 != 0),
-    and operand passes of 1, 8 and 16 register rounds; a few columns are checked against the oracle."""
+    and the operand pass's 256-thread form and its 1024-thread forms of 2 and 4 register rounds
+    (K = 8960, 20000); a few columns are checked against the oracle."""
     rng = synth.rng_for(3, 4000 + t + n_in)
     raw = synth.payload(t, rng, n_out, n_in)
     x = synth.activations(rng, n_in, n_tok).reshape(n_tok, n_in)

@@ -167,6 +167,7 @@ GemvPart make_part(const ah_tensor *w, uint32_t src, const void *x, const int64_
         P.lanes = 0;
     }
     P.src = src;
+    P.type = w->type;
     return P;
 }
 
@@ -264,18 +265,22 @@ uint32_t deal_waves(const GemvPart *parts, size_t n, uint32_t n_wg, size_t act_b
     if (!nw) return 0;
     auto tiles = [&](size_t p) { return (parts[p].n_out + parts[p].rows_per_tile - 1) / parts[p].rows_per_tile; };
     auto actb = [&](size_t p) { return ah_gemv_act_bytes(kpad_of(parts[p].n_in)); };
+    // Relative time of a wave tile: a Q6_K tile (heavier unpacking) takes ~9/8 of the others
+    // (measured on separate Q4_K and Q6_K plans: ~6.1 against ~5.4 us per tile and wave).  In a
+    // single-type plan the weight cancels.
+    auto tile_w = [&](size_t p) -> uint64_t { return parts[p].type == AH_GGML_Q6_K ? 9u : 8u; };
     uint64_t target = W;
     uint32_t used_wg = 0;
     for (int attempt = 0; attempt < 8 && target >= n; ++attempt) {
-        // waves per part: greedy on the largest ceil(tiles / waves)
+        // waves per part: greedy on the largest weighted ceil(tiles / waves)
         uint64_t total = n;
         for (size_t p = 0; p < n; ++p) nw[p] = 1;
         while (total < target) {
             size_t best = n;
-            uint32_t bl = 1;
+            uint64_t bl = 0;
             for (size_t p = 0; p < n; ++p) {
                 if (nw[p] >= tiles(p)) continue;
-                const uint32_t l = (tiles(p) + nw[p] - 1) / nw[p];
+                const uint64_t l = (uint64_t)((tiles(p) + nw[p] - 1) / nw[p]) * tile_w(p);
                 if (l > bl) {
                     bl = l;
                     best = p;
@@ -654,17 +659,17 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
                             const float *const *d_x, float *const *d_y, ah_gemv_plan **out) {
     if (!ctx || !out || !w || !d_x || !d_y || n_parts == 0 || n_parts > 65536) return AH_ERR_INVALID_ARG;
     *out = nullptr;
-    const uint32_t type = w[0]->type;
+    if (!w[0]) return AH_ERR_INVALID_ARG;
     GemvPart *parts = static_cast<GemvPart *>(std::calloc(n_parts, sizeof(GemvPart)));
     if (!parts) return AH_ERR_OUT_OF_MEMORY;
     uint32_t kpad_max = 0, nc = 4;
-    bool all_stream = true;
+    bool all_stream = true, mixed = false;
     for (size_t i = 0; i < n_parts; ++i) {
-        if (!w[i] || w[i]->type != type || !d_x[i] || !d_y[i] || w[i]->n_out == 0 ||
-            reinterpret_cast<uintptr_t>(d_x[i]) % 4) {
+        if (!w[i] || !d_x[i] || !d_y[i] || w[i]->n_out == 0 || reinterpret_cast<uintptr_t>(d_x[i]) % 4) {
             std::free(parts);
             return AH_ERR_INVALID_ARG;
         }
+        mixed = mixed || w[i]->type != w[0]->type;
         bool st = false;
         parts[i] = make_part(w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr, st);
         all_stream = all_stream && st;
@@ -673,6 +678,13 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
         const uint32_t nci = ah_gemv_nc(parts[i].row_bytes);
         nc = nci > nc ? nci : nc;
     }
+    // Parts of different GGUF types share one launch of the mixed-type streaming kernel, which
+    // serves only parts whose rows fit its 8 KB wave tiles.
+    if (mixed && !all_stream) {
+        std::free(parts);
+        return AH_ERR_INVALID_ARG;
+    }
+    const uint32_t type = mixed ? (uint32_t)kMixedType : w[0]->type;
     hipError_t e0 = hipSetDevice(ctx->device);
     if (e0 != hipSuccess) {
         std::free(parts);
@@ -725,6 +737,10 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
             return AH_OK;
         }
         std::free(wgd);
+        if (mixed) {  // more parts than the resident waves: no single-type kernel can take them
+            std::free(parts);
+            return AH_ERR_INVALID_ARG;
+        }
         all_stream = false;  // more parts than the resident waves: the workgroup-tile kernel
     }
     // one kernel serves the plan: every part as workgroup tiles

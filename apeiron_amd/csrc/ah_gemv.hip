@@ -779,6 +779,9 @@ AH_DEV GemvPart part_at(const GemvPart *__restrict__ parts, uint32_t i) {
 // loads, which do not queue behind the vector memory stream), and the workgroup first quantizes
 // the activations of all its waves' parts.  Otherwise every wave serves the launch argument's
 // part, its rows split evenly over the grid's waves.
+// TYPE kMixedType (plans only): the parts may be of different GGUF types; each wave's units are
+// computed by the loop of its part's type, a branch that is uniform over the wave and taken once
+// per tile outside the unit loop.  The activation layout is the same for every type.
 // DOTS: the debug form that also stores exact group dots (single launches only).
 // LDS: [activation region: act_bytes][one tile slot per wave].
 template <int TYPE, bool PLAN, bool DOTS>
@@ -898,8 +901,21 @@ __global__ void __launch_bounds__(kSThreads, 4)
         const bool owns = r < RW && row < r_end;
         float acc = 0.0f;
         if (owns) {
-            for (uint32_t u = g; u < U; u += G)
-                acc += comp_unit<TYPE, DOTS>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
+            if constexpr (TYPE == kMixedType) {
+                if (P.type == AH_GGML_Q4_K) {
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q4_K, DOTS>(P, tl, toff + r * RB + u * kUnitBytes(AH_GGML_Q4_K), row, u, A);
+                } else if (P.type == AH_GGML_Q6_K) {
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q6_K, DOTS>(P, tl, toff + r * RB + u * kUnitBytes(AH_GGML_Q6_K), row, u, A);
+                } else {
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q8_0, DOTS>(P, tl, toff + r * RB + u * kUnitBytes(AH_GGML_Q8_0), row, u, A);
+                }
+            } else {
+                for (uint32_t u = g; u < U; u += G)
+                    acc += comp_unit<TYPE, DOTS>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
+            }
         }
         acc = group_sum(acc, G);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), ry,
@@ -938,6 +954,8 @@ static const void *stream_fn(uint32_t type, bool plan, bool dots = false) {
 #define AH_SFN(T) return plan ? reinterpret_cast<const void *>(&gemv_stream_kernel<T, true, false>)     \
                       : dots ? reinterpret_cast<const void *>(&gemv_stream_kernel<T, false, true>)     \
                              : reinterpret_cast<const void *>(&gemv_stream_kernel<T, false, false>);
+    if (type == kMixedType)  // plans only
+        return plan ? reinterpret_cast<const void *>(&gemv_stream_kernel<kMixedType, true, false>) : nullptr;
     switch (type) {
     case AH_GGML_Q8_0: AH_SFN(AH_GGML_Q8_0)
     case AH_GGML_Q4_K: AH_SFN(AH_GGML_Q4_K)
@@ -947,10 +965,12 @@ static const void *stream_fn(uint32_t type, bool plan, bool dots = false) {
 #undef AH_SFN
 }
 
-// Workgroups of the streaming kernel that fit one CU at once with `lds` bytes of LDS each.
+// Workgroups of the streaming kernel that fit one CU at once with `lds` bytes of LDS each
+// (type kMixedType: the mixed-type plan kernel).
 int ah_gemv_stream_occupancy(uint32_t type, size_t lds) {
     int n0 = 0, n1 = 0;
-    const void *f0 = stream_fn(type, false), *f1 = stream_fn(type, true);
+    const void *f1 = stream_fn(type, true);
+    const void *f0 = type == kMixedType ? f1 : stream_fn(type, false);
     if (!f0 || hipOccupancyMaxActiveBlocksPerMultiprocessor(&n0, f0, kSThreads, lds) != hipSuccess) return 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n1, f1, kSThreads, lds) != hipSuccess) return 0;
     return n0 < n1 ? n0 : n1;
@@ -975,6 +995,11 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const Ge
     case AH_GGML_Q8_0: AH_SLAUNCH(AH_GGML_Q8_0) break;
     case AH_GGML_Q4_K: AH_SLAUNCH(AH_GGML_Q4_K) break;
     case AH_GGML_Q6_K: AH_SLAUNCH(AH_GGML_Q6_K) break;
+    case kMixedType:
+        if (!d_parts) return hipErrorInvalidValue;  // mixed types exist only in plans
+        hipLaunchKernelGGL((gemv_stream_kernel<kMixedType, true, false>), dim3(grid), dim3(kSThreads), lds,
+                           stream, single, d_parts, d_wgd, act_bytes, status);
+        break;
     default: return hipErrorInvalidValue;
     }
 #undef AH_SLAUNCH
@@ -1034,6 +1059,8 @@ hipError_t ah_gemv_init_attrs() {
         for (int v = 0; v < 3; ++v)
             if (e == hipSuccess)
                 e = hipFuncSetAttribute(stream_fn(t, v == 1, v == 2), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(stream_fn(kMixedType, true), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     return e;
 }
 

@@ -169,7 +169,12 @@ struct GemvPart {
     uint32_t wg_begin;     // first workgroup of this part in a grouped launch
     uint32_t wg_count;     // workgroups of this part
     uint32_t src;          // AH_SRC_*
+    uint32_t type;         // GGUF type (AH_GGML_*): read by the mixed-type streaming plan
 };
+
+// The streaming kernel instantiation whose plan mixes GGUF types (each wave dispatches on its
+// part's type).
+constexpr int kMixedType = 0;
 
 // Streaming GEMV plan: what one workgroup serves.  Each of its 8 waves streams a row range of one
 // part; the workgroup quantizes the activation of every part its waves use into its own LDS

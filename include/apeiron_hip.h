@@ -120,8 +120,11 @@ int32_t ah_gemv_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
 
 /* Grouped GEMV: n_parts independent projections in ONE launch, each with its own weight,
  * f32 input and output (chart/ffn.rs:925 projections_q8act shares one dispatch for q/k/v;
- * here every part may have its own input).  All parts share one ggml type.  A plan fixes the
- * device pointers once (descriptors and the waves' assignment, dealt over the parts by tiles,
+ * here every part may have its own input).  Parts may mix ggml types (a Q4_K_M model's Q4_K and
+ * Q6_K projections in one launch) when every part's rows fit the streaming kernel's 8 KB tiles
+ * (Q8_0 K <= 7680, Q4_K K <= 14336, Q6_K K <= 9728); otherwise a mixed plan is refused with
+ * AH_ERR_INVALID_ARG and a single-type plan falls back to the workgroup-tile kernel.  A plan fixes
+ * the device pointers once (descriptors and the waves' assignment, dealt over the parts by tiles,
  * are uploaded at creation), so running it is one launch
  * with no host-device traffic -- the form a per-token projection sequence replays. */
 typedef struct ah_gemv_plan ah_gemv_plan;

@@ -246,9 +246,12 @@ def test_grouped_plan_matches_single_launches(dev):
 
 
 def _plan_vs_singles(dev, t, shapes, seed):
+    """A plan's outputs equal single launches bit for bit.  t is one ggml type for every part, or a
+    list with one type per shape (a mixed-type plan)."""
     rng = synth.rng_for(5, seed)
+    types = t if isinstance(t, list) else [t] * len(shapes)
     ws, xs, ys, singles = [], [], [], []
-    for n_out, n_in in shapes:
+    for (n_out, n_in), t in zip(shapes, types):
         raw = synth.payload(t, rng, n_out, n_in)
         w = dev.upload(t, raw, n_out, n_in)
         x = to_dev(synth.activations(rng, n_in))
@@ -430,3 +433,27 @@ def test_gemm_codes_input_equals_f32_input(dev, t, n_out, n_in, n_tok):
         assert st == 0 and st2 == 0
         assert_close(Y[c], yref, absdot, f"gemm codes t{t} {n_out}x{n_in} col {c}")
     w.free()
+
+
+def test_mixed_type_plan_matches_single_launches(dev):
+    """A Q4_K_M-style token (Q4_K and Q6_K projections, plus Q8_0 parts) in one mixed-type launch:
+    every part's output is bit-identical to its own single-type launch."""
+    parts = [(12, 1536, 1536), (12, 256, 1536), (14, 256, 1536), (12, 1536, 1536), (12, 8960, 1536),
+             (14, 1536, 8960), (12, 1536, 8960), (8, 300, 896), (14, 5000, 1536), (8, 77, 7680),
+             (12, 129, 300), (14, 33, 256)]
+    _plan_vs_singles(dev, [t for t, _, _ in parts], [(n, k) for _, n, k in parts], 91)
+
+
+def test_mixed_type_plan_refuses_rows_past_the_stream_tile(dev):
+    """Mixed types need the streaming kernel: a Q8_0 part with K = 8192 (8704-byte rows) is refused."""
+    rng = synth.rng_for(5, 92)
+    w1 = dev.upload(12, synth.payload(12, rng, 64, 1536), 64, 1536)
+    w2 = dev.upload(8, synth.payload(8, rng, 64, 8192), 64, 8192)
+    x1, x2 = to_dev(synth.activations(rng, 1536)), to_dev(synth.activations(rng, 8192))
+    y1 = torch.zeros(64, dtype=torch.float32, device="cuda")
+    y2 = torch.zeros(64, dtype=torch.float32, device="cuda")
+    with pytest.raises(chart.MatvecError) as ei:
+        chart.GemvPlan(dev, [w1, w2], [ptr(x1), ptr(x2)], [ptr(y1), ptr(y2)])
+    assert ei.value.status == 21  # AH_ERR_INVALID_ARG
+    w1.free()
+    w2.free()

@@ -17,6 +17,9 @@ Dispatch modes (``--mode``):
           down -- 4 dependent launches per layer, captured in a HIP graph per step window.  This
           is latency-bound (96 serialized kernels per token) and is reported beside the value.
 
+Timing: the hot path first runs untimed for 150 ms (clock ramp-up of an idle GPU), then the W
+warm-up steps, then the K timed steps between two synchronizations.
+
 value = algorithmic bytes per step * steps / wall time (GB/s).  Algorithmic bytes per
 projection = n_out * (weight bytes a correct kernel must read per row) + 4*n_in (f32 input)
 + 4*n_out (f32 output).
@@ -39,6 +42,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+CLOCK_WARMUP_S = 0.15  # untimed hot-path load before the warm-up steps (clock ramp-up)
 INT8_PEAK_TOPS = 5000.0
 F16_PEAK_TFLOPS = 2500.0  # dense f16 MFMA peak (the instruction the GEMM computes with)
 LAYERS = 24
@@ -193,6 +197,17 @@ def main() -> int:
         launches_per_step = 1
 
     if args.only in (None, "gemv"):
+        # Clock warm-up, untimed and before the W warm-up steps: an idle MI355X needs tens of ms of
+        # load to reach its sustained clocks (20 steps ~ 1 ms left the timed region 15% slow), so
+        # the hot path runs until CLOCK_WARMUP_S have passed.  Steady-state throughput is what a
+        # busy serving GPU sees; the JSON line records the warm-up.
+        t_w = time.perf_counter()
+        n_clock = 0
+        while time.perf_counter() - t_w < CLOCK_WARMUP_S:
+            for _ in range(100):
+                step(n_clock)
+                n_clock += 1
+            torch.cuda.synchronize()
         for i in range(args.warmup):
             step(i)
         torch.cuda.synchronize()
@@ -289,9 +304,11 @@ def main() -> int:
                 scales = torch.empty((n_tok, -(-n_in // 32)), dtype=torch.int64, device="cuda")
                 dev.quant_act_f32_dev(ptr(x), n_tok, n_in, ptr(codes), ptr(scales), sh)
                 y = torch.empty((n_tok, n_out), dtype=torch.float32, device="cuda")
-                for _ in range(5):
-                    w.gemm_q8_dev(ptr(codes), ptr(scales), n_tok, ptr(y), sh)
-                torch.cuda.synchronize()
+                t_w = time.perf_counter()  # clocks back up after the upload (untimed)
+                while time.perf_counter() - t_w < 0.03:
+                    for _ in range(5):
+                        w.gemm_q8_dev(ptr(codes), ptr(scales), n_tok, ptr(y), sh)
+                    torch.cuda.synchronize()
                 assert dev.sync_status(sh) == 0
                 reps = 50
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -454,6 +471,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_warmup_ms": round(CLOCK_WARMUP_S * 1e3),
         "ms_per_step": round(result["_ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -133,8 +133,9 @@ int32_t ensure_scratch(ah_ctx *ctx, size_t bytes) {
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Work units of a row: Q8_0 blocks, Q4_K super-blocks, Q6_K half super-blocks (128 elements).
 uint32_t units_per_row(uint32_t t, uint32_t n_in) {
-    return t == AH_GGML_Q8_0 ? (n_in + 31) / 32 : (n_in + 255) / 256;
+    return t == AH_GGML_Q8_0 ? (n_in + 31) / 32 : t == AH_GGML_Q4_K ? (n_in + 255) / 256 : (n_in + 127) / 128;
 }
 
 uint32_t kpad_of(size_t n_in) { return (uint32_t)((n_in + 255) / 256 * 256); }

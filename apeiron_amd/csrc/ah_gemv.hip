@@ -426,55 +426,55 @@ AH_DEV float unit_q4(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
 
 // Q6_K super-block s (format/quant.rs:556-599): ql[128] @0, qh[64] @128, int8 sc[16] @192,
 // f16 d @208.  Element 128n + 32t + l = (nibble t/2 of ql[64n + 32(t&1) + l]
-// | ((qh[32n + l] >> 2t) & 3) << 4) - 32.  Super-blocks are 2-byte aligned: the dwords of each half
-// are read from the 4-aligned address below and realigned, one half at a time.  The 6-bit value is
-// built with one and-or per word (the high bits are moved into place by one shift and mask), and
-// the group terms are f32 (no integer multiplies).
+// | ((qh[32n + l] >> 2t) & 3) << 4) - 32.  The unit is one half n (128 elements: ql[64n..],
+// qh[32n..], sc[8n..], d), so a row of K elements has ceil(K/128) units and a lane's work per
+// unit is half a super-block.  Super-blocks are 2-byte aligned: the half's dwords are read from the
+// 4-aligned address below and realigned.  The 6-bit value is built with one and-or per word (the
+// high bits are moved into place by one shift and mask), and the group terms are f32 (no integer
+// multiplies).
 template <bool DOTS>
-AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in, const ActLds &A,
-                     int32_t *dots16) {
+AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, uint32_t n_in,
+                     const ActLds &A, int32_t *dots16) {
     const uint32_t sh = off & 3u;
     const uint32_t *p = reinterpret_cast<const uint32_t *>(tl + (off & ~3u));
+    // the half's three regions as their own bases, so every read below has a constant offset
+    const uint32_t *pl = p + 16 * n, *ph = p + 32 + 8 * n, *ps = p + 48 + 2 * n;
     const uint32_t nb32 = (n_in + 31) / 32, nb16 = (n_in + 15) / 16;
-    auto V = [&](int i) -> uint32_t { return ah_alignbyte(p[i + 1], p[i], sh); };
-    const float fd = ah_f16_bits_to_f32(V(52) & 0xffffu);
+    auto V = [&](const uint32_t *b, int i) -> uint32_t { return ah_alignbyte(b[i + 1], b[i], sh); };
+    const float fd = ah_f16_bits_to_f32(V(p, 52) & 0xffffu);
     float acc = 0.0f;
-#pragma unroll 1
-    for (int n = 0; n < 2; ++n) {  // one half at a time keeps the realigned words' live range short
-        if (DOTS && 8 * s + 4 * n >= nb32) break;  // a ragged row may end after the first half
-        uint32_t qh[8];
+    uint32_t qh[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qh[i] = V(32 + 8 * n + i);
-        const uint32_t scw[2] = {V(48 + 2 * n), V(49 + 2 * n)};
+    for (int i = 0; i < 8; ++i) qh[i] = V(ph, i);
+    const uint32_t scw[2] = {V(ps, 0), V(ps, 1)};
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t g = 8 * s + 4 * n + t;
-            if (DOTS && g >= nb32) break;
-            const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g));
-            const u32x4 x0 = xv[0], x1 = xv[1];
-            const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            int32_t Dlo = 0, Dhi = 0;
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t g = 8 * s + 4 * n + t;
+        if (DOTS && g >= nb32) break;
+        const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g));
+        const u32x4 x0 = xv[0], x1 = xv[1];
+        const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        int32_t Dlo = 0, Dhi = 0;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t qlw = V(16 * n + 8 * (t & 1) + i);
-                // bits 4-5 of each byte: qh bits 2t, 2t+1
-                const uint32_t hi = (2 * t <= 4 ? (qh[i] << (4 - 2 * t)) : (qh[i] >> (2 * t - 4))) & 0x30303030u;
-                const uint32_t uu = ((t < 2 ? qlw : (qlw >> 4)) & 0x0F0F0F0Fu) | hi;
-                if (i < 4)
-                    Dlo = ah_sdot4(uu, xw[i], Dlo);
-                else
-                    Dhi = ah_sdot4(uu, xw[i], Dhi);
-            }
-            Dlo -= 32 * A.xs16[2 * g];
-            Dhi -= 32 * A.xs16[2 * g + 1];
-            if (DOTS && dots16) {
-                dots16[2 * g] = Dlo;
-                if (2 * g + 1 < nb16) dots16[2 * g + 1] = Dhi;  // ragged row ends on a 16-group
-            }
-            const uint32_t sw = scw[t >> 1] >> (16 * (t & 1));
-            const float sclo = (float)(int)(int8_t)(sw & 0xffu), schi = (float)(int)(int8_t)((sw >> 8) & 0xffu);
-            acc += A.fsc[g] * fd * (sclo * (float)Dlo + schi * (float)Dhi);
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t qlw = V(pl, 8 * (t & 1) + i);
+            // bits 4-5 of each byte: qh bits 2t, 2t+1
+            const uint32_t hi = (2 * t <= 4 ? (qh[i] << (4 - 2 * t)) : (qh[i] >> (2 * t - 4))) & 0x30303030u;
+            const uint32_t uu = ((t < 2 ? qlw : (qlw >> 4)) & 0x0F0F0F0Fu) | hi;
+            if (i < 4)
+                Dlo = ah_sdot4(uu, xw[i], Dlo);
+            else
+                Dhi = ah_sdot4(uu, xw[i], Dhi);
         }
+        Dlo -= 32 * A.xs16[2 * g];
+        Dhi -= 32 * A.xs16[2 * g + 1];
+        if (DOTS && dots16) {
+            dots16[2 * g] = Dlo;
+            if (2 * g + 1 < nb16) dots16[2 * g + 1] = Dhi;  // ragged row ends on a 16-group
+        }
+        const uint32_t sw = scw[t >> 1] >> (16 * (t & 1));
+        const float sclo = (float)(int)(int8_t)(sw & 0xffu), schi = (float)(int)(int8_t)((sw >> 8) & 0xffu);
+        acc += A.fsc[g] * fd * (sclo * (float)Dlo + schi * (float)Dhi);
     }
     return acc;
 }
@@ -490,11 +490,15 @@ AH_DEV float comp_unit(const GemvPart &P, const uint8_t *tl, uint32_t off, uint3
         return unit_q4<DOTS>(tl, off, u, P.n_in, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
     } else {
         const uint32_t nb16 = (P.n_in + 15) / 16;
-        return unit_q6<DOTS>(tl, off, u, P.n_in, A, DOTS && P.dots ? P.dots + (size_t)row * nb16 : nullptr);
+        return unit_q6<DOTS>(tl, off, u >> 1, u & 1u, P.n_in, A, DOTS && P.dots ? P.dots + (size_t)row * nb16 : nullptr);
     }
 }
 
-constexpr uint32_t kUnitBytes(int type) { return type == AH_GGML_Q8_0 ? 34u : type == AH_GGML_Q4_K ? 144u : 210u; }
+// Byte offset of unit u within a row: Q8_0 blocks, Q4_K super-blocks, Q6_K half super-blocks
+// (both halves of a super-block start at its first byte).
+constexpr uint32_t unit_off(int type, uint32_t u) {
+    return type == AH_GGML_Q8_0 ? 34u * u : type == AH_GGML_Q4_K ? 144u * u : 210u * (u >> 1);
+}
 constexpr uint32_t kRedSlots = 1024;  // unit partials of one tile
 constexpr uint32_t kTileSlack = 128;  // bytes past a tile that realigned or compact-row unit reads may touch
 
@@ -546,7 +550,7 @@ __global__ void __launch_bounds__(kThreads)
         for (uint32_t f = threadIdx.x; f < TU; f += kThreads) {
             const uint32_t r = f / U, u = f - r * U, row = tile * R + r;
             float v = 0.0f;
-            if (row < P.n_out) v = comp_unit<TYPE, true>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
+            if (row < P.n_out) v = comp_unit<TYPE, true>(P, tl, toff + r * RB + unit_off(TYPE, u), row, u, A);
             A.red[f] = v;
         }
         ah_lds_barrier();
@@ -903,18 +907,22 @@ __global__ void __launch_bounds__(kSThreads, 4)
         if (owns) {
             if constexpr (TYPE == kMixedType) {
                 if (P.type == AH_GGML_Q4_K) {
+#pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q4_K, DOTS>(P, tl, toff + r * RB + u * kUnitBytes(AH_GGML_Q4_K), row, u, A);
+                        acc += comp_unit<AH_GGML_Q4_K, DOTS>(P, tl, toff + r * RB + unit_off(AH_GGML_Q4_K, u), row, u, A);
                 } else if (P.type == AH_GGML_Q6_K) {
+#pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q6_K, DOTS>(P, tl, toff + r * RB + u * kUnitBytes(AH_GGML_Q6_K), row, u, A);
+                        acc += comp_unit<AH_GGML_Q6_K, DOTS>(P, tl, toff + r * RB + unit_off(AH_GGML_Q6_K, u), row, u, A);
                 } else {
+#pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q8_0, DOTS>(P, tl, toff + r * RB + u * kUnitBytes(AH_GGML_Q8_0), row, u, A);
+                        acc += comp_unit<AH_GGML_Q8_0, DOTS>(P, tl, toff + r * RB + unit_off(AH_GGML_Q8_0, u), row, u, A);
                 }
             } else {
+#pragma unroll 1
                 for (uint32_t u = g; u < U; u += G)
-                    acc += comp_unit<TYPE, DOTS>(P, tl, toff + r * RB + u * kUnitBytes(TYPE), row, u, A);
+                    acc += comp_unit<TYPE, DOTS>(P, tl, toff + r * RB + unit_off(TYPE, u), row, u, A);
             }
         }
         acc = group_sum(acc, G);
@@ -927,16 +935,25 @@ __global__ void __launch_bounds__(kSThreads, 4)
 
 // Stream geometry for a row of RB bytes and U units: whole rows per tile and lanes per row.
 // Returns false when a row does not fit one tile (the workgroup-tile kernel then serves the part).
+// A lane computes ceil(units / G) units of its row per tile, so (rows, G) is chosen for the most
+// row bytes per round of unit work (ties to more rows): e.g. Q4_K at K = 1536 takes 8 rows of 8
+// lanes (one super-block each) rather than 9 rows of 4 (two each).
 bool ah_gemv_stream_geometry(uint32_t row_bytes, uint32_t units, uint32_t &rows, uint32_t &lanes) {
     if (row_bytes == 0 || row_bytes + 16 > kStreamTile) return false;
     const uint32_t fit = (kStreamTile - 16) / row_bytes;
-    uint32_t G = 64;
-    while (G > 1 && G * fit > 64) G >>= 1;      // lanes so that the tile's rows cover the wave
-    uint32_t cap = 1;
-    while (cap < units && cap < 64) cap <<= 1;  // no more lanes than units
-    if (G > cap) G = cap;
-    lanes = G;
-    rows = fit < 64 / G ? fit : 64 / G;
+    uint64_t best = 0;
+    rows = 1;
+    lanes = 64;
+    for (uint32_t G = 1; G <= 64; G <<= 1) {
+        const uint32_t r = fit < 64 / G ? fit : 64 / G;
+        const uint32_t rounds = units > G ? (units + G - 1) / G : 1u;
+        const uint64_t score = (uint64_t)r * row_bytes * 64 / rounds;
+        if (score > best) {
+            best = score;
+            rows = r;
+            lanes = G;
+        }
+    }
     return true;
 }
 

@@ -97,10 +97,11 @@ def main() -> int:
     ap.add_argument("--mode", choices=["engine", "token"], default="token")
     ap.add_argument("--pool-gib", type=float, default=1.1)
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-heads", action="store_true", help="skip configs[0] and configs[2]")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--cpu-threads", type=int, default=8)
-    ap.add_argument("--only", choices=["gemv", "gemm", "copy", "config4"], default=None)
+    ap.add_argument("--only", choices=["gemv", "gemm", "copy", "config4", "heads"], default=None)
     ap.add_argument("--no-config4", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -336,6 +337,45 @@ def main() -> int:
         result["gemm"] = gemm
 
     # ---- config 4: the 197 projections of a Qwen2.5-1.5B token (Q4_K + Q6_K), N = 1 and N = 512 ----
+    # ---- configs[0] (Q8_0 4864x896) and configs[2] (151936x896 vocab head, Q6_K and Q8_0) ------
+    # Single GEMV launches back to back over rotating weight copies of >= 1.1 GiB in all (the
+    # 256 MB Infinity Cache cannot serve them), f32 N(0,1) input quantized in the kernel.
+    if not args.no_heads and args.only in (None, "heads"):
+        singles = []
+        for cfg, gt, n_out, n_in in ((0, synth.Q8_0, 4864, 896), (2, synth.Q6_K, 151936, 896),
+                                     (2, synth.Q8_0, 151936, 896)):
+            raw = synth.payload(gt, synth.rng_for(cfg, gt), n_out, n_in)
+            copies = max(2, -(-int(1.1 * 2 ** 30) // raw.nbytes))
+            wc = [dev.upload(gt, raw, n_out, n_in) for _ in range(copies)]
+            del raw
+            x = torch.from_numpy(synth.activations(synth.rng_for(cfg, 99), n_in)).cuda()
+            y = torch.empty(n_out, dtype=torch.float32, device="cuda")
+            t_w = time.perf_counter()
+            while time.perf_counter() - t_w < 0.05:  # clocks up after the uploads (untimed)
+                for i in range(copies):
+                    wc[i].gemv_f32_dev(ptr(x), ptr(y), sh)
+                torch.cuda.synchronize()
+            assert dev.sync_status(sh) == 0
+            reps = 400 if n_out < 100000 else 60
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for i in range(reps):
+                wc[i % copies].gemv_f32_dev(ptr(x), ptr(y), sh)
+            b.record(stream)
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / reps
+            nbytes = proj_bytes(synth, gt, n_out, n_in)
+            gbs = nbytes / us / 1e3
+            singles.append({"config": cfg, "type": synth.NAMES[gt], "shape": [n_out, n_in],
+                            "copies": copies, "us": round(us, 2), "bytes": nbytes,
+                            "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+            log(f"[bench] config{cfg} {synth.NAMES[gt]} {n_out}x{n_in}: {us:.2f} us/launch, {gbs:.0f} GB/s "
+                f"= {100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s ({copies} rotating copies)")
+            for w in wc:
+                w.free()
+            del wc
+        result["heads"] = singles
+
     if not args.no_config4 and args.only in (None, "config4"):
         projs = cfg4_projections(synth)
         host = {}
@@ -488,6 +528,7 @@ def main() -> int:
         "gemm": result.get("gemm"),
         "mfma_probe": result.get("mfma_probe"),
         "config4": result.get("config4"),
+        "config0_config2": result.get("heads"),
     }
     print(json.dumps(line))
     dev.close()

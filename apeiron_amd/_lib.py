@@ -25,7 +25,7 @@ EXPORTS = [
     "ah_quant_act_q32_dev", "ah_gemv_f32_dev", "ah_gemv_q8_dev", "ah_gemv_plan_create",
     "ah_gemv_plan_run", "ah_gemv_plan_free", "ah_gemm_f32_dev", "ah_gemm_q8_dev",
     "ah_gemv_q8_dots_dev", "ah_sync_status", "ah_matvec_q8act", "ah_matmat_q8act",
-    "ah_quant_act", "ah_probe_mfma_peak",
+    "ah_quant_act", "ah_probe_mfma_peak", "ah_gemm_group_f32_dev", "ah_gemm_group_q8_dev",
 ]
 
 _lib = None
@@ -70,6 +70,8 @@ def load() -> ctypes.CDLL:
         "ah_matmat_q8act": (I32, [P, P, P, P, S, P]),
         "ah_quant_act": (I32, [P, P, S, P, P]),
         "ah_probe_mfma_peak": (I32, [P, U32, ctypes.POINTER(ctypes.c_double)]),
+        "ah_gemm_group_f32_dev": (I32, [P, S, P, P, S, P, P]),
+        "ah_gemm_group_q8_dev": (I32, [P, S, P, P, P, S, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -161,6 +161,25 @@ class Tensor:
                                            stream), "gemm_q8")
 
 
+def gemm_group_f32_dev(dev: "Device", tensors: list["Tensor"], x_ptr: int, n_tok: int,
+                       y_ptrs: list[int], stream: int | None = None) -> None:
+    """Prefill over projections of one f32 input [n_tok][n_in] (ah_gemm_group_f32_dev)."""
+    n = len(tensors)
+    W = (ctypes.c_void_p * n)(*[t.h.value for t in tensors])
+    Y = (ctypes.c_void_p * n)(*y_ptrs)
+    _check(dev.lib.ah_gemm_group_f32_dev(dev.h, n, W, x_ptr, n_tok, Y, stream), "gemm_group_f32")
+
+
+def gemm_group_q8_dev(dev: "Device", tensors: list["Tensor"], codes_ptr: int, scales_ptr: int,
+                      n_tok: int, y_ptrs: list[int], stream: int | None = None) -> None:
+    """Prefill over projections of one quantized input (ah_gemm_group_q8_dev)."""
+    n = len(tensors)
+    W = (ctypes.c_void_p * n)(*[t.h.value for t in tensors])
+    Y = (ctypes.c_void_p * n)(*y_ptrs)
+    _check(dev.lib.ah_gemm_group_q8_dev(dev.h, n, W, codes_ptr, scales_ptr, n_tok, Y, stream),
+           "gemm_group_q8")
+
+
 class GemvPlan:
     """A grouped GEMV launch over fixed device pointers (ah_gemv_plan_*)."""
 

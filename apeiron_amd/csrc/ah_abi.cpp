@@ -382,22 +382,40 @@ int32_t reset_status(ah_ctx *ctx) {
 }
 
 // GEMM operand preparation + launch.  src = AH_SRC_F32 (x = f32 [n_tok][n_in]) or AH_SRC_CODES.
-int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
-                    const int64_t *scales_in, size_t n_tok, float *y, void *stream) {
-    if (!ctx || !w || !y || (!x && n_tok && w->n_in)) return AH_ERR_INVALID_ARG;
-    if (n_tok == 0 || w->n_out == 0) return AH_OK;
+// Prefill over n_parts projections of one input: one operand pass (shared by every part, as the
+// reference's grouped GEMM shares one activation pack, kern/gemm.rs:799-818), then each part's
+// GEMM (and split-K reduction) in order on the stream.  All parts share n_in; types and n_out
+// may differ.  A single projection is the group of one.
+int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w, uint32_t src,
+                          const void *x, const int64_t *scales_in, size_t n_tok, float *const *y,
+                          void *stream) {
+    if (!ctx || !w || !y || n_parts == 0 || n_parts > 65536 || !w[0]) return AH_ERR_INVALID_ARG;
+    const size_t n_in_sz = w[0]->n_in;
+    bool any_q4k = false;
+    for (size_t i = 0; i < n_parts; ++i) {
+        if (!w[i] || (!y[i] && w[i]->n_out) || w[i]->n_in != n_in_sz) return AH_ERR_INVALID_ARG;
+        // a workgroup's output rows (128 tokens x n_out f32) are addressed with 32-bit offsets
+        if (w[i]->n_out > (0xFFFFFF00ull / (128 * 4))) return AH_ERR_INVALID_ARG;
+        any_q4k = any_q4k || w[i]->type == AH_GGML_Q4_K;
+    }
+    if (!x && n_tok && n_in_sz) return AH_ERR_INVALID_ARG;
+    if (n_tok == 0) return AH_OK;
     if (n_tok >= (1ull << 24)) return AH_ERR_INVALID_ARG;
-    // a workgroup's output rows (128 tokens x n_out f32) are addressed with 32-bit offsets
-    if (w->n_out > (0xFFFFFF00ull / (128 * 4))) return AH_ERR_INVALID_ARG;
-    const uint32_t n_in = (uint32_t)w->n_in, n_out = (uint32_t)w->n_out, N = (uint32_t)n_tok;
+    const uint32_t n_in = (uint32_t)n_in_sz, N = (uint32_t)n_tok;
     const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
-    const uint32_t splits = ah_gemm_pick_splits(w->type, n_out, n_in, N, (uint32_t)ctx->cu_count);
+    // the parts run one after another on the stream, so they share one partials region
+    size_t part_bytes = 0;
+    for (size_t i = 0; i < n_parts; ++i) {
+        const uint32_t sp = ah_gemm_pick_splits(w[i]->type, (uint32_t)w[i]->n_out, n_in, N, (uint32_t)ctx->cu_count);
+        const size_t b = sp > 1 ? (size_t)sp * N * w[i]->n_out * 4 : 0;
+        part_bytes = b > part_bytes ? b : part_bytes;
+    }
 
     size_t off = 0;
     const size_t o_xh = off; off = align256(off + (size_t)N * kpad * 2);
     const size_t o_ts = off; off = align256(off + (size_t)N * 4);
-    const size_t o_xmin = off; off = align256(off + (w->type == AH_GGML_Q4_K ? (size_t)N * nsb * 32 : 0));
-    const size_t o_part = off; off = align256(off + (splits > 1 ? (size_t)splits * N * n_out * 4 : 0));
+    const size_t o_xmin = off; off = align256(off + (any_q4k ? (size_t)N * nsb * 32 : 0));
+    const size_t o_part = off; off = align256(off + part_bytes);
     int32_t st = ensure_scratch(ctx, off);
     if (st) return st;
     uint8_t *S = static_cast<uint8_t *>(ctx->scratch);
@@ -414,7 +432,7 @@ int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     o.scales = scales_in;
     o.xh = xh;
     o.tok_scale = ts;
-    o.xmin = w->type == AH_GGML_Q4_K ? xmin : nullptr;
+    o.xmin = any_q4k ? xmin : nullptr;
     o.status = ctx->d_status;
     o.n_tok = N;
     o.n_in = n_in;
@@ -422,9 +440,21 @@ int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     o.kpad = kpad;
     o.src = src;
     AH_HIP(ctx, ah_launch_gemm_operand(o, s));
-    AH_HIP(ctx, ah_launch_gemm(w->type, w->d, (uint32_t)w->bytes, (uint32_t)w->row_bytes, n_out, n_in, N,
-                               kpad, xh, xmin, ts, y, part, splits, s));
+    for (size_t i = 0; i < n_parts; ++i) {
+        const uint32_t n_out = (uint32_t)w[i]->n_out;
+        if (n_out == 0) continue;
+        const uint32_t splits = ah_gemm_pick_splits(w[i]->type, n_out, n_in, N, (uint32_t)ctx->cu_count);
+        AH_HIP(ctx, ah_launch_gemm(w[i]->type, w[i]->d, (uint32_t)w[i]->bytes, (uint32_t)w[i]->row_bytes, n_out,
+                                   n_in, N, kpad, xh, xmin, ts, y[i], part, splits, s));
+    }
     return AH_OK;
+}
+
+int32_t gemm_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
+                    const int64_t *scales_in, size_t n_tok, float *y, void *stream) {
+    if (!ctx || !w || !y || (!x && n_tok && w->n_in)) return AH_ERR_INVALID_ARG;
+    if (n_tok == 0 || w->n_out == 0) return AH_OK;
+    return gemm_group_launch(ctx, 1, &w, src, x, scales_in, n_tok, &y, stream);
 }
 
 }  // namespace
@@ -822,6 +852,17 @@ int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes, c
                        size_t n_tok, float *d_y, void *stream) {
     if (!d_scales && n_tok) return AH_ERR_INVALID_ARG;
     return gemm_launch(ctx, w, AH_SRC_CODES, d_codes, d_scales, n_tok, d_y, stream);
+}
+
+int32_t ah_gemm_group_f32_dev(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w, const float *d_x,
+                              size_t n_tok, float *const *d_y, void *stream) {
+    return gemm_group_launch(ctx, n_parts, w, AH_SRC_F32, d_x, nullptr, n_tok, d_y, stream);
+}
+
+int32_t ah_gemm_group_q8_dev(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w, const int8_t *d_codes,
+                             const int64_t *d_scales, size_t n_tok, float *const *d_y, void *stream) {
+    if (!d_scales && n_tok) return AH_ERR_INVALID_ARG;
+    return gemm_group_launch(ctx, n_parts, w, AH_SRC_CODES, d_codes, d_scales, n_tok, d_y, stream);
 }
 
 int32_t ah_sync_status(ah_ctx *ctx, void *stream) {

@@ -143,6 +143,17 @@ int32_t ah_gemm_f32_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, size_
 int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
                        const int64_t *d_scales, size_t n_tok, float *d_y, void *stream);
 
+/* Grouped prefill: n_parts projections of ONE input (q/k/v, gate/up).  gemm_q8_0_group
+ * (kern/gemm.rs:799-818) shares one activation pack over its parts; here one operand pass
+ * serves every part, then each part's GEMM runs in order on the stream.  All parts share n_in
+ * (AH_ERR_INVALID_ARG otherwise); ggml types and n_out may differ.  d_y[i] is part i's
+ * [n_tok][n_out_i] output; each equals what the single-projection call produces for that part. */
+int32_t ah_gemm_group_f32_dev(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w,
+                              const float *d_x, size_t n_tok, float *const *d_y, void *stream);
+int32_t ah_gemm_group_q8_dev(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w,
+                             const int8_t *d_codes, const int64_t *d_scales, size_t n_tok,
+                             float *const *d_y, void *stream);
+
 /* ---- debug: exact integer group dots (the bit-exact quantity of the contract) ---- */
 
 /* ah_gemv_q8_dev that ALSO stores, from inside the same production kernel, the exact integer

@@ -457,3 +457,44 @@ def test_mixed_type_plan_refuses_rows_past_the_stream_tile(dev):
     assert ei.value.status == 21  # AH_ERR_INVALID_ARG
     w1.free()
     w2.free()
+
+
+@pytest.mark.parametrize("codes_input", [False, True])
+def test_gemm_group_equals_single_projections(dev, codes_input):
+    """One operand pass shared by q/k/v-like parts of mixed types (gemm_q8_0_group's shared pack,
+    kern/gemm.rs:799-818): each part's output is bit-identical to its single-projection GEMM."""
+    n_in, n_tok = 1536, 129
+    shapes = [(12, 1536), (12, 256), (14, 256), (8, 300), (12, 0), (14, 4000)]
+    rng = synth.rng_for(6, 31 + codes_input)
+    x = to_dev(synth.activations(rng, n_in, n_tok).reshape(n_tok, n_in))
+    codes = torch.empty((n_tok, n_in), dtype=torch.int8, device="cuda")
+    scales = torch.empty((n_tok, n_in // 32), dtype=torch.int64, device="cuda")
+    dev.quant_act_f32_dev(ptr(x), n_tok, n_in, ptr(codes), ptr(scales), stream())
+    ws, ys, singles = [], [], []
+    for t, n_out in shapes:
+        w = dev.upload(t, synth.payload(t, rng, n_out, n_in), n_out, n_in)
+        y = torch.full((n_tok, max(n_out, 1)), float("nan"), dtype=torch.float32, device="cuda")
+        y1 = torch.full((n_tok, max(n_out, 1)), float("nan"), dtype=torch.float32, device="cuda")
+        if codes_input:
+            w.gemm_q8_dev(ptr(codes), ptr(scales), n_tok, ptr(y1), stream())
+        else:
+            w.gemm_f32_dev(ptr(x), n_tok, ptr(y1), stream())
+        ws.append(w), ys.append(y), singles.append(y1)
+    if codes_input:
+        chart.gemm_group_q8_dev(dev, ws, ptr(codes), ptr(scales), n_tok, [ptr(y) for y in ys], stream())
+    else:
+        chart.gemm_group_f32_dev(dev, ws, ptr(x), n_tok, [ptr(y) for y in ys], stream())
+    assert dev.sync_status(stream()) == 0
+    for (t, n_out), y, y1 in zip(shapes, ys, singles):
+        if n_out:
+            assert torch.isfinite(y).all(), (t, n_out)
+            assert torch.equal(y, y1), (t, n_out)
+        else:  # a part without rows writes nothing
+            assert torch.isnan(y).all() and torch.isnan(y1).all()
+    # parts must share n_in
+    w_bad = dev.upload(12, synth.payload(12, rng, 64, 896), 64, 896)
+    with pytest.raises(chart.MatvecError) as ei:
+        chart.gemm_group_f32_dev(dev, [ws[0], w_bad], ptr(x), n_tok, [ptr(ys[0]), ptr(ys[1])], stream())
+    assert ei.value.status == 21
+    for w in ws + [w_bad]:
+        w.free()

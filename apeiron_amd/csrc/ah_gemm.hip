@@ -98,7 +98,11 @@ constexpr uint32_t kOob = 0xFFFFFFF0u;  // a buffer offset past any operand: rea
 // between register sets.
 namespace rb {
 constexpr int kNN = 1;                          // column tiles per wave
-constexpr int kRows = 4 * 32 * kNN;             // weight rows per workgroup
+// W waves per workgroup (each owns 32 weight rows): 4, with a 4-slot LDS ring; or 2, with a
+// 2-slot ring, so that four workgroups (two waves per SIMD) share a CU -- the host takes it when
+// the 4-wave grid would put between one and two workgroups on a CU (see ah_gemm_pick_shape).
+template <int W> constexpr int ring() { return W == 2 ? 2 : 4; }
+template <int W> constexpr int rows() { return W * 32 * kNN; }  // rows per workgroup
 // Row (token) tiles per wave.  Q8_0 (a fold per block) and Q6_K (two operands per weight, see
 // the Q6_K stage) are bound by VALU work per MFMA, so each dequantized weight fragment feeds 4
 // token tiles.  Q4_K's dequantization is cheap and it is bound by the stalls of a single wave per
@@ -112,28 +116,33 @@ template <int TYPE> constexpr int buf_bytes() {                                 
 }
 // Split granularity in stages (Q8_0 pairs, K-quant super-blocks); the loop body is 4 stages.
 template <int TYPE> constexpr int unroll() { return TYPE == AH_GGML_Q8_0 ? 2 : 4; }
-constexpr int kRing = 4;  // LDS slots: the stage being read and three in flight
 // Weight register sets and how many stages ahead they are fetched (Q6_K's 27-register set
 // allows only two sets within the 256-register budget).
-template <int TYPE> constexpr int nw() { return TYPE == AH_GGML_Q6_K ? 2 : 4; }
-template <int TYPE> constexpr int dw() { return TYPE == AH_GGML_Q6_K ? 1 : 2; }
+// The prologue replays ring - 1 notional stages, so a fetch is at most ring - 1 stages ahead.
+template <int TYPE, int W> constexpr int dw() { return TYPE == AH_GGML_Q6_K || ring<W>() < 3 ? 1 : 2; }
+template <int TYPE, int W> constexpr int nw() { return dw<TYPE, W>() == 1 ? 2 : 4; }
 // Per-wave vector memory instructions a stage issues: activation slice (16-byte direct-to-LDS
 // loads, 1 KB per instruction), Q4_K split sums (4-byte direct-to-LDS loads, 256 B each), and the
 // weight fetch of super-block position P.
-template <int TYPE> constexpr int an() { return tok<TYPE>() * kKS * 2 / 1024 / 4; }
-template <int TYPE> constexpr int xn() { return TYPE == AH_GGML_Q4_K ? tok<TYPE>() * 32 / 256 / 4 : 0; }
+template <int TYPE, int W> constexpr int an() { return tok<TYPE>() * kKS * 2 / 1024 / W; }
+template <int TYPE, int W> constexpr int xn() { return TYPE == AH_GGML_Q4_K ? tok<TYPE>() * 32 / 256 / W : 0; }
 template <int TYPE> constexpr int wn(int P) {
     return TYPE == AH_GGML_Q8_0 ? 6 : TYPE == AH_GGML_Q6_K ? 9 : (P == 0 ? 2 : 1);
 }
-// At the top of stage slot u, the loads issued after that stage's activation slice: the weight
-// fetch of the stage that issued it and the slices and fetches of the two stages after.  Waiting
-// for vmcnt <= this count completes the slice (vector memory loads complete in issue order).
-template <int TYPE> constexpr int wait_count(int u) {
-    constexpr int D = dw<TYPE>();
-    return wn<TYPE>((u + 1 + D) % 4) + wn<TYPE>((u + 2 + D) % 4) + wn<TYPE>((u + 3 + D) % 4) +
-           2 * (xn<TYPE>() + an<TYPE>());
+// At the top of stage slot u, the loads issued after that stage's activation slice (issued R - 1
+// stages earlier, R the ring's slots): the weight fetch of the stage that issued it and the
+// slices and fetches of the R - 2 stages after.  Waiting for vmcnt <= this count completes the
+// slice (vector memory loads complete in issue order).
+template <int TYPE, int W> constexpr int wait_count(int u) {
+    constexpr int D = dw<TYPE, W>(), R = ring<W>();
+    int c = (R - 2) * (xn<TYPE, W>() + an<TYPE, W>());
+    for (int j = 1; j <= R - 1; ++j) c += wn<TYPE>((u - j + D + 8) % 4);
+    return c;
 }
-inline uint32_t tok_of(uint32_t type) { return type == AH_GGML_Q4_K ? tok<AH_GGML_Q4_K>() : tok<AH_GGML_Q8_0>(); }
+inline uint32_t tok_of(uint32_t type) {
+    return type == AH_GGML_Q4_K ? tok<AH_GGML_Q4_K>() : type == AH_GGML_Q6_K ? tok<AH_GGML_Q6_K>() : tok<AH_GGML_Q8_0>();
+}
+
 }  // namespace rb
 
 // Weight bytes of one stage for the lane's NN rows, fetched a stage ahead.  Ordinary (not
@@ -214,12 +223,13 @@ AH_DEV uint32_t q4k_scale(uint32_t s0, uint32_t s1, uint32_t s2) {
     else return (byte(J + 4) >> 4) | ((byte(J) >> 6) << 4);
 }
 
-template <int TYPE>
-__global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
-    constexpr int NN = rb::kNN, NM = rb::nm<TYPE>(), NW = rb::nw<TYPE>(), DW = rb::dw<TYPE>();
+template <int TYPE, int WV>
+__global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
+    constexpr int NN = rb::kNN, NM = rb::nm<TYPE>(), NW = rb::nw<TYPE, WV>(), DW = rb::dw<TYPE, WV>();
     constexpr int kTok = rb::tok<TYPE>(), kActBytes = rb::act_bytes<TYPE>();
-    constexpr int kAN = rb::an<TYPE>(), kXN = rb::xn<TYPE>();
-    __shared__ __align__(16) uint8_t lds[rb::kRing][rb::buf_bytes<TYPE>()];
+    constexpr int kAN = rb::an<TYPE, WV>(), kXN = rb::xn<TYPE, WV>();
+    constexpr int kR = rb::ring<WV>();
+    __shared__ __align__(16) uint8_t lds[kR][rb::buf_bytes<TYPE>()];
     // XCD-aware order: dispatch i goes to XCD i % 8, so XCD x takes logical ids
     // [x * per, (x + 1) * per).  Consecutive logical ids share a weight row tile and split, so the
     // workgroups reading the same weights share one XCD's L2.  The grid is a multiple of 8.
@@ -231,7 +241,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
-    const uint32_t row_w = rtile * rb::kRows + wave * 32 * NN;
+    const uint32_t row_w = rtile * rb::rows<WV>() + wave * 32 * NN;
     uint32_t rbase[NN];
     bool rl[NN];
 #pragma unroll
@@ -306,24 +316,24 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_rb_kernel(GemmArgs a) {
     // out-of-range dummies), so every stage's wait count is the same compile-time number.
     WRb W[NW];
     auto prologue = [&](auto kc) {
-        constexpr int k = decltype(kc)::value, rel = k - 3 + DW;  // fetched stage - st_begin
+        constexpr int k = decltype(kc)::value, rel = k - (kR - 1) + DW;  // fetched stage - st_begin
         act_dma(lds[k], st_begin + k);
         constexpr int wi = ((rel % NW) + NW) % NW, P = ((rel % 4) + 4) % 4;
         W[wi] = fetch_rb<TYPE, P, NN>(rs, rbase, rl, rel >= 0 ? st_begin + rel : st_begin, a.n_in, h,
                                       rel >= 0 && st_begin + rel < st_end);
     };
     prologue(std::integral_constant<int, 0>{});
-    prologue(std::integral_constant<int, 1>{});
-    prologue(std::integral_constant<int, 2>{});
+    if constexpr (kR > 2) prologue(std::integral_constant<int, 1>{});
+    if constexpr (kR > 3) prologue(std::integral_constant<int, 2>{});
 
     auto stage = [&](auto uc, uint32_t st) {
         constexpr int u = decltype(uc)::value;
         // the slice of this stage is complete in every wave, and every wave is done with slot u+3
-        ah_vm_lds_barrier<rb::wait_count<TYPE>(u)>();
-        act_dma(lds[(u + 3) & 3], st + 3);
+        ah_vm_lds_barrier<rb::wait_count<TYPE, WV>(u)>();
+        act_dma(lds[(u + kR - 1) % kR], st + kR - 1);
         W[(u + DW) % NW] = fetch_rb<TYPE, (u + DW) % 4, NN>(rs, rbase, rl, st + DW, a.n_in, h, st + DW < st_end);
         __builtin_amdgcn_sched_barrier(0);  // the requests above stay ahead of this stage's work
-        const uint8_t *cur = lds[u];
+        const uint8_t *cur = lds[u % kR];
         const WRb &wc = W[u % NW];
         if constexpr (TYPE == AH_GGML_Q8_0) {
             // 2*NM*NN MFMA chains per stage (block bb, token tile m, row tile n), each two MFMAs
@@ -549,9 +559,10 @@ namespace {
 struct GemmGeom {
     uint32_t nstages, unroll, rows, toks;
 };
-GemmGeom geom_of(uint32_t type, uint32_t n_in, uint32_t kpad) {
-    if (type == AH_GGML_Q8_0) return {(n_in + 2 * kKS - 1) / (2 * kKS) * 2, 2, rb::kRows, rb::tok_of(type)};
-    return {kpad / kKS, 4, rb::kRows, rb::tok_of(type)};  // K-quants: whole super-blocks
+GemmGeom geom_of(uint32_t type, uint32_t n_in, uint32_t kpad, uint32_t waves = 4) {
+    const uint32_t rows = 32u * rb::kNN * waves;
+    if (type == AH_GGML_Q8_0) return {(n_in + 2 * kKS - 1) / (2 * kKS) * 2, 2, rows, rb::tok_of(type)};
+    return {kpad / kKS, 4, rows, rb::tok_of(type)};  // K-quants: whole super-blocks
 }
 
 // Stages per split for a requested split count: a multiple of the unroll.
@@ -586,6 +597,19 @@ uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint3
         }
     }
     return best;
+}
+
+// Waves per workgroup for a GEMM planned with `splits` (4-wave tiles): Q8_0 and Q6_K take the
+// 2-wave kernel when the 4-wave grid holds more workgroups than CUs but at most two per CU
+// (one resident workgroup per CU, the rest a second round on a few CUs); twice as many 2-wave
+// workgroups keep two waves per SIMD on every CU instead.  Measured at N = 512: 8960x1536 Q8_0
+// 48.8 -> 43.3 us, Q6_K 54.4 -> 47.7; shapes outside the band run 7-14% slower on it.
+uint32_t ah_gemm_pick_waves(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits,
+                            uint32_t cus) {
+    if (type == AH_GGML_Q4_K) return 4;
+    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4);
+    const uint64_t n_wg = (uint64_t)((n_out + g.rows - 1) / g.rows) * ((n_tok + g.toks - 1) / g.toks) * splits;
+    return n_wg > cus && n_wg <= 2ull * cus ? 2u : 4u;
 }
 
 // ---- MFMA peak probe ---------------------------------------------------------------------------
@@ -687,7 +711,8 @@ hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, ui
 hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes,
                           uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t kpad,
                           const _Float16 *xh, const _Float16 *xmin, const float *tok_scale,
-                          float *y, float *partials, uint32_t splits, hipStream_t stream) {
+                          float *y, float *partials, uint32_t splits, uint32_t waves, hipStream_t stream) {
+    if (type == AH_GGML_Q4_K || (waves != 2 && waves != 4)) waves = 4;
     GemmArgs a;
     a.w = w;
     a.w_bytes = w_bytes;
@@ -699,7 +724,7 @@ hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uin
     a.xh = xh;
     a.xmin = xmin;
     a.tok_scale = tok_scale;
-    const GemmGeom g = geom_of(type, n_in, kpad);
+    const GemmGeom g = geom_of(type, n_in, kpad, waves);
     const uint32_t per = per_split(g, splits ? splits : 1);
     a.stages_per_split = per;
     a.splits = (g.nstages + per - 1) / per;
@@ -708,10 +733,17 @@ hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uin
     const uint32_t row_tiles = (n_out + g.rows - 1) / g.rows;
     a.n_wg = row_tiles * a.tok_tiles * a.splits;
     const dim3 rb_grid((a.n_wg + 7) / 8 * 8);
+    const dim3 blk(64 * waves);
     switch (type) {
-    case AH_GGML_Q8_0: hipLaunchKernelGGL(gemm_rb_kernel<AH_GGML_Q8_0>, rb_grid, dim3(kThreads), 0, stream, a); break;
-    case AH_GGML_Q4_K: hipLaunchKernelGGL(gemm_rb_kernel<AH_GGML_Q4_K>, rb_grid, dim3(kThreads), 0, stream, a); break;
-    case AH_GGML_Q6_K: hipLaunchKernelGGL(gemm_rb_kernel<AH_GGML_Q6_K>, rb_grid, dim3(kThreads), 0, stream, a); break;
+    case AH_GGML_Q8_0:
+        if (waves == 2) hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q8_0, 2>), rb_grid, blk, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q8_0, 4>), rb_grid, blk, 0, stream, a);
+        break;
+    case AH_GGML_Q4_K: hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q4_K, 4>), rb_grid, blk, 0, stream, a); break;
+    case AH_GGML_Q6_K:
+        if (waves == 2) hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q6_K, 2>), rb_grid, blk, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q6_K, 4>), rb_grid, blk, 0, stream, a);
+        break;
     default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();

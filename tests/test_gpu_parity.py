@@ -373,6 +373,8 @@ def test_gemm_config3_shapes(dev, t, n_out, n_in):
 def test_gemm_q6_k_config4_shapes(dev):
     gemm_check(dev, 14, 256, 1536, 512, sample_cols=[0, 200, 511])
     gemm_check(dev, 14, 1536, 8960, 512, sample_cols=[0, 511])
+    # 280 four-wave tiles on 256 CUs: served by the 2-wave kernel
+    gemm_check(dev, 14, 8960, 1536, 512, sample_cols=[0, 300, 511])
 
 
 def test_gemm_n1_equals_gemv_within_tolerance(dev):

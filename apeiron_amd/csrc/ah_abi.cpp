@@ -34,7 +34,7 @@ hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_by
 hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes,
                           uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t kpad,
                           const _Float16 *xh, const _Float16 *xmin, const float *tok_scale,
-                          float *y, float *partials, uint32_t splits, uint32_t waves, hipStream_t stream);
+                          float *y, float *partials, uint32_t splits, uint32_t form, hipStream_t stream);
 uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
                              uint32_t cus);
 uint32_t ah_gemm_pick_waves(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits,
@@ -447,9 +447,9 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         if (n_out == 0) continue;
         const uint32_t cus = (uint32_t)ctx->cu_count;
         const uint32_t splits = ah_gemm_pick_splits(w[i]->type, n_out, n_in, N, cus);
-        const uint32_t waves = ah_gemm_pick_waves(w[i]->type, n_out, n_in, N, splits, cus);
+        const uint32_t form = ah_gemm_pick_waves(w[i]->type, n_out, n_in, N, splits, cus);
         AH_HIP(ctx, ah_launch_gemm(w[i]->type, w[i]->d, (uint32_t)w[i]->bytes, (uint32_t)w[i]->row_bytes, n_out,
-                                   n_in, N, kpad, xh, xmin, ts, y[i], part, splits, waves, s));
+                                   n_in, N, kpad, xh, xmin, ts, y[i], part, splits, form, s));
     }
     return AH_OK;
 }

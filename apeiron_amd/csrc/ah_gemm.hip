@@ -98,10 +98,8 @@ constexpr uint32_t kOob = 0xFFFFFFF0u;  // a buffer offset past any operand: rea
 // between register sets.
 namespace rb {
 constexpr int kNN = 1;                          // column tiles per wave
-// W waves per workgroup (each owns 32 weight rows): 4, with a 4-slot LDS ring; or 2, with a
-// 2-slot ring, so that four workgroups (two waves per SIMD) share a CU -- the host takes it when
-// the 4-wave grid would put between one and two workgroups on a CU (see ah_gemm_pick_shape).
-template <int W> constexpr int ring() { return W == 2 ? 2 : 4; }
+// A workgroup is W waves (each owns 32 weight rows) with an R-slot LDS ring; the host picks the
+// form per GEMM shape (ah_gemm_pick_waves).
 template <int W> constexpr int rows() { return W * 32 * kNN; }  // rows per workgroup
 // Row (token) tiles per wave.  Q8_0 (a fold per block) and Q6_K (two operands per weight, see
 // the Q6_K stage) are bound by VALU work per MFMA, so each dequantized weight fragment feeds 4
@@ -119,8 +117,8 @@ template <int TYPE> constexpr int unroll() { return TYPE == AH_GGML_Q8_0 ? 2 : 4
 // Weight register sets and how many stages ahead they are fetched (Q6_K's 27-register set
 // allows only two sets within the 256-register budget).
 // The prologue replays ring - 1 notional stages, so a fetch is at most ring - 1 stages ahead.
-template <int TYPE, int W> constexpr int dw() { return TYPE == AH_GGML_Q6_K || ring<W>() < 3 ? 1 : 2; }
-template <int TYPE, int W> constexpr int nw() { return dw<TYPE, W>() == 1 ? 2 : 4; }
+template <int TYPE, int R> constexpr int dw() { return TYPE == AH_GGML_Q6_K || R < 3 ? 1 : 2; }
+template <int TYPE, int R> constexpr int nw() { return dw<TYPE, R>() == 1 ? 2 : 4; }
 // Per-wave vector memory instructions a stage issues: activation slice (16-byte direct-to-LDS
 // loads, 1 KB per instruction), Q4_K split sums (4-byte direct-to-LDS loads, 256 B each), and the
 // weight fetch of super-block position P.
@@ -133,8 +131,8 @@ template <int TYPE> constexpr int wn(int P) {
 // stages earlier, R the ring's slots): the weight fetch of the stage that issued it and the
 // slices and fetches of the R - 2 stages after.  Waiting for vmcnt <= this count completes the
 // slice (vector memory loads complete in issue order).
-template <int TYPE, int W> constexpr int wait_count(int u) {
-    constexpr int D = dw<TYPE, W>(), R = ring<W>();
+template <int TYPE, int W, int R> constexpr int wait_count(int u) {
+    constexpr int D = dw<TYPE, R>();
     int c = (R - 2) * (xn<TYPE, W>() + an<TYPE, W>());
     for (int j = 1; j <= R - 1; ++j) c += wn<TYPE>((u - j + D + 8) % 4);
     return c;
@@ -223,12 +221,12 @@ AH_DEV uint32_t q4k_scale(uint32_t s0, uint32_t s1, uint32_t s2) {
     else return (byte(J + 4) >> 4) | ((byte(J) >> 6) << 4);
 }
 
-template <int TYPE, int WV>
+template <int TYPE, int WV, int RG>
 __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
-    constexpr int NN = rb::kNN, NM = rb::nm<TYPE>(), NW = rb::nw<TYPE, WV>(), DW = rb::dw<TYPE, WV>();
+    constexpr int NN = rb::kNN, NM = rb::nm<TYPE>(), NW = rb::nw<TYPE, RG>(), DW = rb::dw<TYPE, RG>();
     constexpr int kTok = rb::tok<TYPE>(), kActBytes = rb::act_bytes<TYPE>();
     constexpr int kAN = rb::an<TYPE, WV>(), kXN = rb::xn<TYPE, WV>();
-    constexpr int kR = rb::ring<WV>();
+    constexpr int kR = RG;
     __shared__ __align__(16) uint8_t lds[kR][rb::buf_bytes<TYPE>()];
     // XCD-aware order: dispatch i goes to XCD i % 8, so XCD x takes logical ids
     // [x * per, (x + 1) * per).  Consecutive logical ids share a weight row tile and split, so the
@@ -329,7 +327,7 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
     auto stage = [&](auto uc, uint32_t st) {
         constexpr int u = decltype(uc)::value;
         // the slice of this stage is complete in every wave, and every wave is done with slot u+3
-        ah_vm_lds_barrier<rb::wait_count<TYPE, WV>(u)>();
+        ah_vm_lds_barrier<rb::wait_count<TYPE, WV, RG>(u)>();
         act_dma(lds[(u + kR - 1) % kR], st + kR - 1);
         W[(u + DW) % NW] = fetch_rb<TYPE, (u + DW) % 4, NN>(rs, rbase, rl, st + DW, a.n_in, h, st + DW < st_end);
         __builtin_amdgcn_sched_barrier(0);  // the requests above stay ahead of this stage's work
@@ -599,17 +597,21 @@ uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint3
     return best;
 }
 
-// Waves per workgroup for a GEMM planned with `splits` (4-wave tiles): Q8_0 and Q6_K take the
-// 2-wave kernel when the 4-wave grid holds more workgroups than CUs but at most two per CU
-// (one resident workgroup per CU, the rest a second round on a few CUs); twice as many 2-wave
-// workgroups keep two waves per SIMD on every CU instead.  Measured at N = 512: 8960x1536 Q8_0
-// 48.8 -> 43.3 us, Q6_K 54.4 -> 47.7; shapes outside the band run 7-14% slower on it.
+// Workgroup form for a GEMM planned with `splits` on 4-wave tiles (Q8_0 and Q6_K; Q4_K's 64-token
+// tiles already put two workgroups on a CU):
+//   kForm4x4: 4 waves, 4-slot ring (64 KB), when the 4-wave grid is past two workgroups per CU;
+//   kForm2x2: 2 waves, 2-slot ring (32 KB, four per CU), when it holds more workgroups than CUs
+//             but at most two per CU -- a few CUs would run a second round after the rest;
+//   kForm2x4: 2 waves, 4-slot ring, when it fits one workgroup per CU -- the same busy SIMDs
+//             spread over every CU, halving each CU's load on its texture unit and LDS.
+// Measured at N = 512 (A/B in one run): 8960x1536 Q8_0 48.8 -> 43.3 us, Q6_K 54.4 -> 47.7 on
+// kForm2x2; 4864x896 23.5 -> 22.6, 1536x8960 46.6 -> 45.7 (Q6_K 55.3 -> 51.8) on kForm2x4.
 uint32_t ah_gemm_pick_waves(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits,
                             uint32_t cus) {
-    if (type == AH_GGML_Q4_K) return 4;
+    if (type == AH_GGML_Q4_K) return kForm4x4;
     const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4);
     const uint64_t n_wg = (uint64_t)((n_out + g.rows - 1) / g.rows) * ((n_tok + g.toks - 1) / g.toks) * splits;
-    return n_wg > cus && n_wg <= 2ull * cus ? 2u : 4u;
+    return n_wg <= cus ? kForm2x4 : n_wg <= 2ull * cus ? kForm2x2 : kForm4x4;
 }
 
 // ---- MFMA peak probe ---------------------------------------------------------------------------
@@ -711,8 +713,9 @@ hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, ui
 hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes,
                           uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t kpad,
                           const _Float16 *xh, const _Float16 *xmin, const float *tok_scale,
-                          float *y, float *partials, uint32_t splits, uint32_t waves, hipStream_t stream) {
-    if (type == AH_GGML_Q4_K || (waves != 2 && waves != 4)) waves = 4;
+                          float *y, float *partials, uint32_t splits, uint32_t form, hipStream_t stream) {
+    if (type == AH_GGML_Q4_K || form > kForm2x4) form = kForm4x4;
+    const uint32_t waves = form == kForm4x4 ? 4u : 2u;
     GemmArgs a;
     a.w = w;
     a.w_bytes = w_bytes;
@@ -734,18 +737,17 @@ hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uin
     a.n_wg = row_tiles * a.tok_tiles * a.splits;
     const dim3 rb_grid((a.n_wg + 7) / 8 * 8);
     const dim3 blk(64 * waves);
+#define AH_GFORMS(T)                                                                                    \
+    if (form == kForm2x2) hipLaunchKernelGGL((gemm_rb_kernel<T, 2, 2>), rb_grid, blk, 0, stream, a);    \
+    else if (form == kForm2x4) hipLaunchKernelGGL((gemm_rb_kernel<T, 2, 4>), rb_grid, blk, 0, stream, a); \
+    else hipLaunchKernelGGL((gemm_rb_kernel<T, 4, 4>), rb_grid, blk, 0, stream, a);
     switch (type) {
-    case AH_GGML_Q8_0:
-        if (waves == 2) hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q8_0, 2>), rb_grid, blk, 0, stream, a);
-        else hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q8_0, 4>), rb_grid, blk, 0, stream, a);
-        break;
-    case AH_GGML_Q4_K: hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q4_K, 4>), rb_grid, blk, 0, stream, a); break;
-    case AH_GGML_Q6_K:
-        if (waves == 2) hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q6_K, 2>), rb_grid, blk, 0, stream, a);
-        else hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q6_K, 4>), rb_grid, blk, 0, stream, a);
-        break;
+    case AH_GGML_Q8_0: AH_GFORMS(AH_GGML_Q8_0) break;
+    case AH_GGML_Q4_K: hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q4_K, 4, 4>), rb_grid, blk, 0, stream, a); break;
+    case AH_GGML_Q6_K: AH_GFORMS(AH_GGML_Q6_K) break;
     default: return hipErrorInvalidValue;
     }
+#undef AH_GFORMS
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.splits == 1) return e;
     const size_t n = (size_t)n_tok * n_out;

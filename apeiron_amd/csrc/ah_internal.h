@@ -172,6 +172,9 @@ struct GemvPart {
     uint32_t type;         // GGUF type (AH_GGML_*): read by the mixed-type streaming plan
 };
 
+// GEMM workgroup forms (waves x LDS ring slots), chosen per shape by ah_gemm_pick_waves.
+enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2 };
+
 // The streaming kernel instantiation whose plan mixes GGUF types (each wave dispatches on its
 // part's type).
 constexpr int kMixedType = 0;

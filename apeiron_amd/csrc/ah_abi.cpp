@@ -11,6 +11,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <new>
+#include <vector>
 
 // launchers (ah_gemv.hip, ah_gemm.hip)
 hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart *d_parts,
@@ -31,14 +32,16 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const Ge
 hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream);
 hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes, uint32_t off0,
                           uint32_t off1, int *d_bad, hipStream_t stream);
-hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes,
-                          uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t kpad,
-                          const _Float16 *xh, const _Float16 *xmin, const float *tok_scale,
-                          float *y, float *partials, uint32_t splits, uint32_t form, hipStream_t stream);
+hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_in,
+                          uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xmin,
+                          const float *tok_scale, uint32_t form, hipStream_t stream);
+hipError_t ah_launch_splitk_reduce(uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_tok,
+                                   const float *tok_scale, hipStream_t stream);
 uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
                              uint32_t cus);
-uint32_t ah_gemm_pick_waves(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits,
-                            uint32_t cus);
+uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits);
+uint32_t ah_gemm_max_parts(uint32_t type);
+uint32_t ah_gemm_pick_waves(uint32_t type, uint64_t n_wg4, uint32_t cus);
 hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream);
 hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, uint32_t *d_sink,
                          hipStream_t stream, double *tops);
@@ -385,9 +388,11 @@ int32_t reset_status(ah_ctx *ctx) {
 
 // GEMM operand preparation + launch.  src = AH_SRC_F32 (x = f32 [n_tok][n_in]) or AH_SRC_CODES.
 // Prefill over n_parts projections of one input: one operand pass (shared by every part, as the
-// reference's grouped GEMM shares one activation pack, kern/gemm.rs:799-818), then each part's
-// GEMM (and split-K reduction) in order on the stream.  All parts share n_in; types and n_out
-// may differ.  A single projection is the group of one.
+// reference's grouped GEMM shares one activation pack, kern/gemm.rs:799-818), then one GEMM launch
+// per run of consecutive parts of one GGUF type (up to kGemmMaxParts; Q8_0 one), then one split-K reduction
+// for every part that splits.  Each part keeps the split count it would get alone, so its outputs
+// are those of its single-projection call bit for bit.  All parts share n_in; types and n_out may
+// differ.  A single projection is the group of one.
 int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w, uint32_t src,
                           const void *x, const int64_t *scales_in, size_t n_tok, float *const *y,
                           void *stream) {
@@ -405,12 +410,25 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     if (n_tok >= (1ull << 24)) return AH_ERR_INVALID_ARG;
     const uint32_t n_in = (uint32_t)n_in_sz, N = (uint32_t)n_tok;
     const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
-    // the parts run one after another on the stream, so they share one partials region
+    const uint32_t cus = (uint32_t)ctx->cu_count;
+    // every split part has its own partials region: the parts of a launch run together and the
+    // reduction reads them all at the end
+    std::vector<GemmPartDesc> pd(n_parts);
+    std::vector<size_t> part_off(n_parts, 0);
     size_t part_bytes = 0;
     for (size_t i = 0; i < n_parts; ++i) {
-        const uint32_t sp = ah_gemm_pick_splits(w[i]->type, (uint32_t)w[i]->n_out, n_in, N, (uint32_t)ctx->cu_count);
-        const size_t b = sp > 1 ? (size_t)sp * N * w[i]->n_out * 4 : 0;
-        part_bytes = b > part_bytes ? b : part_bytes;
+        GemmPartDesc &d = pd[i];
+        d.w = w[i]->d;
+        d.w_bytes = (uint32_t)w[i]->bytes;
+        d.row_bytes = (uint32_t)w[i]->row_bytes;
+        d.n_out = (uint32_t)w[i]->n_out;
+        d.splits = d.n_out ? ah_gemm_pick_splits(w[i]->type, d.n_out, n_in, N, cus) : 1;
+        d.y = y[i];
+        d.partials = nullptr;
+        if (d.splits > 1) {
+            part_off[i] = part_bytes;
+            part_bytes = align256(part_bytes + (size_t)d.splits * N * d.n_out * 4);
+        }
     }
 
     size_t off = 0;
@@ -424,7 +442,8 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     _Float16 *xh = reinterpret_cast<_Float16 *>(S + o_xh);
     float *ts = reinterpret_cast<float *>(S + o_ts);
     _Float16 *xmin = reinterpret_cast<_Float16 *>(S + o_xmin);
-    float *part = reinterpret_cast<float *>(S + o_part);
+    for (size_t i = 0; i < n_parts; ++i)
+        if (pd[i].splits > 1) pd[i].partials = reinterpret_cast<float *>(S + o_part + part_off[i]);
     hipStream_t s = pick(ctx, stream);
     AH_HIP(ctx, hipSetDevice(ctx->device));
 
@@ -442,15 +461,28 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     o.kpad = kpad;
     o.src = src;
     AH_HIP(ctx, ah_launch_gemm_operand(o, s));
-    for (size_t i = 0; i < n_parts; ++i) {
-        const uint32_t n_out = (uint32_t)w[i]->n_out;
-        if (n_out == 0) continue;
-        const uint32_t cus = (uint32_t)ctx->cu_count;
-        const uint32_t splits = ah_gemm_pick_splits(w[i]->type, n_out, n_in, N, cus);
-        const uint32_t form = ah_gemm_pick_waves(w[i]->type, n_out, n_in, N, splits, cus);
-        AH_HIP(ctx, ah_launch_gemm(w[i]->type, w[i]->d, (uint32_t)w[i]->bytes, (uint32_t)w[i]->row_bytes, n_out,
-                                   n_in, N, kpad, xh, xmin, ts, y[i], part, splits, form, s));
+    // runs of consecutive parts of one type (parts with no rows skipped)
+    bool any_split = false;
+    for (size_t i = 0; i < n_parts;) {
+        if (pd[i].n_out == 0) {
+            ++i;
+            continue;
+        }
+        const uint32_t type = w[i]->type, max_run = ah_gemm_max_parts(type);
+        GemmPartDesc run[kGemmMaxParts];
+        uint32_t nr = 0;
+        uint64_t wg4 = 0;
+        for (; i < n_parts && nr < max_run; ++i) {
+            if (pd[i].n_out == 0) continue;
+            if (w[i]->type != type) break;
+            run[nr++] = pd[i];
+            wg4 += ah_gemm_part_wg4(type, pd[i].n_out, n_in, N, pd[i].splits);
+            any_split = any_split || pd[i].splits > 1;
+        }
+        const uint32_t form = ah_gemm_pick_waves(type, wg4, cus);
+        AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xmin, ts, form, s));
     }
+    if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd.data(), N, ts, s));
     return AH_OK;
 }
 

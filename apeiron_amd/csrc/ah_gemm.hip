@@ -71,17 +71,21 @@ AH_DEV f16x8 pack8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(f16x8, v);
 }
 
-struct GemmArgs {
+// A part of the launch: logical workgroups [wg_begin, next part's wg_begin) are its tiles x splits.
+struct GemmPartArgs {
     const uint8_t *w;
-    uint32_t w_bytes, row_bytes;
-    uint32_t n_out, n_in, n_tok, kpad;
+    float *y;                  // [n_tok][n_out] (splits == 1) or partials [splits][n_tok][n_out]
+    uint32_t w_bytes, row_bytes, n_out;
+    uint32_t stages_per_split; // K stages of 64 per split (multiple of the kernel's unroll)
+    uint32_t splits, wg_begin;
+};
+struct GemmArgs {
+    GemmPartArgs p[kGemmMaxParts];
+    uint32_t n_parts, n_in, n_tok, kpad;
     const _Float16 *xh;        // [n_tok][kpad]
     const _Float16 *xmin;      // Q4_K: [n_tok][kpad/256][16] split code sums (see quant pass)
     const float *tok_scale;    // [n_tok]
-    float *y;                  // [n_tok][n_out] (splits == 1) or partials [splits][n_tok][n_out]
-    uint32_t stages_per_split; // K stages of 64 per split (multiple of the kernel's unroll)
-    uint32_t splits;
-    uint32_t tok_tiles, n_wg;  // register-blocked grid: token tiles, real workgroup count
+    uint32_t tok_tiles, n_wg;  // token tiles, real workgroup count over all parts
 };
 
 constexpr uint32_t kOob = 0xFFFFFFF0u;  // a buffer offset past any operand: reads zeros
@@ -107,6 +111,9 @@ template <int W> constexpr int rows() { return W * 32 * kNN; }  // rows per work
 // SIMD instead: 2 token tiles halve the registers and the tile, so two of its workgroups share a
 // CU at prefill sizes.  (Measured each way round: the other choice is 7-11% slower per type.)
 template <int TYPE> constexpr int nm() { return TYPE == AH_GGML_Q4_K ? 2 : 4; }
+// Parts one launch may hold (see the part lookup in the kernel).
+template <int TYPE> constexpr uint32_t max_parts() { return TYPE == AH_GGML_Q8_0 ? 1u : kGemmMaxParts; }
+uint32_t max_parts_of(uint32_t type) { return type == AH_GGML_Q8_0 ? 1u : kGemmMaxParts; }
 template <int TYPE> constexpr int tok() { return 32 * nm<TYPE>(); }              // tokens per workgroup
 template <int TYPE> constexpr int act_bytes() { return tok<TYPE>() * kKS * 2; }   // f16 slice of a stage
 template <int TYPE> constexpr int buf_bytes() {                                    // + Q4_K split sums
@@ -234,8 +241,17 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
     const uint32_t per = gridDim.x >> 3;
     const uint32_t L = (blockIdx.x & 7u) * per + (blockIdx.x >> 3);
     if (L >= a.n_wg) return;  // whole workgroup, before any barrier
-    const uint32_t tt = L % a.tok_tiles, rest = L / a.tok_tiles;
-    const uint32_t split = rest % a.splits, rtile = rest / a.splits;
+    // The part owning L.  Q8_0 launches take one part (rb::max_parts): with a runtime part index
+    // the compiler turns the slice loads' bounds selects into branches and the Q8_0 kernel grows
+    // from 207 to 256 VGPRs and spills.
+    uint32_t pi = 0;
+#pragma unroll
+    for (uint32_t i = 1; i < rb::max_parts<TYPE>(); ++i)
+        if (i < a.n_parts && L >= a.p[i].wg_begin) pi = i;
+    const GemmPartArgs &pa = a.p[pi];
+    const uint32_t Lp = L - pa.wg_begin;
+    const uint32_t tt = Lp % a.tok_tiles, rest = Lp / a.tok_tiles;
+    const uint32_t split = rest % pa.splits, rtile = rest / pa.splits;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
@@ -245,12 +261,12 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
 #pragma unroll
     for (int n = 0; n < NN; ++n) {
         const uint32_t r = row_w + 32 * n + j;
-        rl[n] = r < a.n_out;
-        rbase[n] = (rl[n] ? r : 0u) * a.row_bytes;
+        rl[n] = r < pa.n_out;
+        rbase[n] = (rl[n] ? r : 0u) * pa.row_bytes;
     }
     const uint32_t tok0 = tt * kTok;
     const uint32_t ntile = a.n_tok - tok0 < (uint32_t)kTok ? a.n_tok - tok0 : (uint32_t)kTok;
-    const __amdgpu_buffer_rsrc_t rs = ah_rsrc(a.w, a.w_bytes);
+    const __amdgpu_buffer_rsrc_t rs = ah_rsrc(pa.w, pa.w_bytes);
     const __amdgpu_buffer_rsrc_t rx = ah_rsrc(a.xh + (size_t)tok0 * a.kpad, ntile * a.kpad * 2u);
     const uint32_t nsb = a.kpad / 256;
     const __amdgpu_buffer_rsrc_t rm =
@@ -260,8 +276,8 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
     // stages: whole super-blocks for the K-quants (zero activations past n_in; their folds are
     // per super-block, at its last stage), pairs for Q8_0
     const uint32_t nstages = TYPE != AH_GGML_Q8_0 ? a.kpad / kKS : ((a.n_in + 2 * kKS - 1) / (2 * kKS)) * 2;
-    const uint32_t st_begin = split * a.stages_per_split;
-    uint32_t st_end = st_begin + a.stages_per_split;
+    const uint32_t st_begin = split * pa.stages_per_split;
+    uint32_t st_end = st_begin + pa.stages_per_split;
     if (st_end > nstages) st_end = nstages;
 
     // The f16 activation slice of a stage (kTok tokens x 64 K) goes global -> LDS directly (no
@@ -512,11 +528,11 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
     // D layout of a 32x32 MFMA: lane (j, h), register r -> row i = 8*(r/4) + 4*h + (r%4), col j.
     // Token scales (1.0 for partials) are loaded up front; lanes past n_out and tokens past n_tok
     // store out of range, so there is no branch per element.
-    float *ybase = a.splits == 1 ? a.y + (size_t)tok0 * a.n_out
-                                 : a.y + ((size_t)split * a.n_tok + tok0) * a.n_out;
-    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(ybase, ntile * a.n_out * 4u);
+    float *ybase = pa.splits == 1 ? pa.y + (size_t)tok0 * pa.n_out
+                                  : pa.y + ((size_t)split * a.n_tok + tok0) * pa.n_out;
+    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(ybase, ntile * pa.n_out * 4u);
     const __amdgpu_buffer_rsrc_t rt = ah_rsrc(a.tok_scale + tok0, ntile * 4u);
-    const bool scaled = a.splits == 1;
+    const bool scaled = pa.splits == 1;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
         uint32_t sc[16];
@@ -531,21 +547,74 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
                 const bool ok = rl[n] && tl < ntile;
                 const float v = acc[m][n][r] * (scaled ? __builtin_bit_cast(float, sc[r]) : 1.0f);
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
-                                                      ok ? (tl * a.n_out + row) * 4u : kOob, 0, 0);
+                                                      ok ? (tl * pa.n_out + row) * 4u : kOob, 0, 0);
             }
         }
     }
 }
 
-// y[tok][row] = tok_scale[tok] * sum_s partial[s][tok][row], fixed summation order.
-__global__ void splitk_reduce(const float *part, uint32_t splits, uint32_t n_tok, uint32_t n_out,
-                              const float *tok_scale, float *y) {
-    const size_t n = (size_t)n_tok * n_out;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * blockDim.x) {
-        float s = 0.0f;
-        for (uint32_t z = 0; z < splits; ++z) s += part[z * n + i];
-        y[i] = s * tok_scale[i / n_out];
+// y[tok][row] = tok_scale[tok] * sum_s partial[s][tok][row], summed in split order from 0, for
+// every split part of a grouped call in one launch.  A work item is 4 consecutive outputs (VEC:
+// every part has n % 4 == 0 and 16-byte aligned planes) or one; a thread issues the loads of 8
+// splits before the first add.
+constexpr uint32_t kReduceBatch = 8;
+constexpr uint32_t kReduceMaxParts = 8;
+struct ReducePart {
+    const float *part;
+    float *y;
+    uint64_t begin;  // first work item of the part
+    uint32_t n_out, splits;
+};
+struct ReduceArgs {
+    ReducePart p[kReduceMaxParts];
+    const float *tok_scale;
+    uint64_t total;  // work items over all parts
+    uint32_t n_parts, n_tok;
+};
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <bool VEC>
+__global__ void splitk_reduce(ReduceArgs r) {
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < r.total;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        ReducePart P = r.p[0];
+#pragma unroll
+        for (uint32_t k = 1; k < kReduceMaxParts; ++k)
+            if (k < r.n_parts && i >= r.p[k].begin) P = r.p[k];
+        const uint64_t li = i - P.begin;
+        const size_t n = (size_t)r.n_tok * P.n_out;
+        if constexpr (VEC) {
+            const size_t n4 = n / 4;
+            const f32x4 *p = reinterpret_cast<const f32x4 *>(P.part) + li;
+            f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (uint32_t z = 0; z < P.splits; z += kReduceBatch) {
+                f32x4 v[kReduceBatch];
+#pragma unroll
+                for (uint32_t j = 0; j < kReduceBatch; ++j)
+                    if (z + j < P.splits) v[j] = __builtin_nontemporal_load(p + (z + j) * n4);
+#pragma unroll
+                for (uint32_t j = 0; j < kReduceBatch; ++j)
+                    if (z + j < P.splits) s += v[j];
+            }
+            const size_t e = 4 * li;
+            f32x4 o;
+            o.x = s.x * r.tok_scale[e / P.n_out];
+            o.y = s.y * r.tok_scale[(e + 1) / P.n_out];
+            o.z = s.z * r.tok_scale[(e + 2) / P.n_out];
+            o.w = s.w * r.tok_scale[(e + 3) / P.n_out];
+            reinterpret_cast<f32x4 *>(P.y)[li] = o;
+        } else {
+            float s = 0.0f;
+            for (uint32_t z = 0; z < P.splits; z += kReduceBatch) {
+                float v[kReduceBatch];
+#pragma unroll
+                for (uint32_t j = 0; j < kReduceBatch; ++j)
+                    if (z + j < P.splits) v[j] = __builtin_nontemporal_load(P.part + (z + j) * n + li);
+#pragma unroll
+                for (uint32_t j = 0; j < kReduceBatch; ++j)
+                    if (z + j < P.splits) s += v[j];
+            }
+            P.y[li] = s * r.tok_scale[li / P.n_out];
+        }
     }
 }
 
@@ -597,8 +666,17 @@ uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint3
     return best;
 }
 
-// Workgroup form for a GEMM planned with `splits` on 4-wave tiles (Q8_0 and Q6_K; Q4_K's 64-token
-// tiles already put two workgroups on a CU):
+// Parts one GEMM launch of `type` may hold.
+uint32_t ah_gemm_max_parts(uint32_t type) { return rb::max_parts_of(type); }
+
+// 4-wave workgroups (tiles x splits) of one part.
+uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits) {
+    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4);
+    return ((n_out + g.rows - 1) / g.rows) * ((n_tok + g.toks - 1) / g.toks) * splits;
+}
+
+// Workgroup form for a launch whose parts take n_wg4 workgroups on 4-wave tiles (Q8_0 and Q6_K;
+// Q4_K's 64-token tiles already put two workgroups on a CU):
 //   kForm4x4: 4 waves, 4-slot ring (64 KB), when the 4-wave grid is past two workgroups per CU;
 //   kForm2x2: 2 waves, 2-slot ring (32 KB, four per CU), when it holds more workgroups than CUs
 //             but at most two per CU -- a few CUs would run a second round after the rest;
@@ -606,12 +684,9 @@ uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint3
 //             spread over every CU, halving each CU's load on its texture unit and LDS.
 // Measured at N = 512 (A/B in one run): 8960x1536 Q8_0 48.8 -> 43.3 us, Q6_K 54.4 -> 47.7 on
 // kForm2x2; 4864x896 23.5 -> 22.6, 1536x8960 46.6 -> 45.7 (Q6_K 55.3 -> 51.8) on kForm2x4.
-uint32_t ah_gemm_pick_waves(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits,
-                            uint32_t cus) {
+uint32_t ah_gemm_pick_waves(uint32_t type, uint64_t n_wg4, uint32_t cus) {
     if (type == AH_GGML_Q4_K) return kForm4x4;
-    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4);
-    const uint64_t n_wg = (uint64_t)((n_out + g.rows - 1) / g.rows) * ((n_tok + g.toks - 1) / g.toks) * splits;
-    return n_wg <= cus ? kForm2x4 : n_wg <= 2ull * cus ? kForm2x2 : kForm4x4;
+    return n_wg4 <= cus ? kForm2x4 : n_wg4 <= 2ull * cus ? kForm2x2 : kForm4x4;
 }
 
 // ---- MFMA peak probe ---------------------------------------------------------------------------
@@ -710,31 +785,45 @@ hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, ui
     return hipSuccess;
 }
 
-hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes,
-                          uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t kpad,
-                          const _Float16 *xh, const _Float16 *xmin, const float *tok_scale,
-                          float *y, float *partials, uint32_t splits, uint32_t form, hipStream_t stream) {
+hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_in,
+                          uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xmin,
+                          const float *tok_scale, uint32_t form, hipStream_t stream) {
+    if (n_parts == 0 || n_parts > rb::max_parts_of(type)) return hipErrorInvalidValue;
     if (type == AH_GGML_Q4_K || form > kForm2x4) form = kForm4x4;
     const uint32_t waves = form == kForm4x4 ? 4u : 2u;
+    const GemmGeom g = geom_of(type, n_in, kpad, waves);
     GemmArgs a;
-    a.w = w;
-    a.w_bytes = w_bytes;
-    a.row_bytes = row_bytes;
-    a.n_out = n_out;
+    a.n_parts = n_parts;
     a.n_in = n_in;
     a.n_tok = n_tok;
     a.kpad = kpad;
     a.xh = xh;
     a.xmin = xmin;
     a.tok_scale = tok_scale;
-    const GemmGeom g = geom_of(type, n_in, kpad, waves);
-    const uint32_t per = per_split(g, splits ? splits : 1);
-    a.stages_per_split = per;
-    a.splits = (g.nstages + per - 1) / per;
-    a.y = a.splits == 1 ? y : partials;
     a.tok_tiles = (n_tok + g.toks - 1) / g.toks;
-    const uint32_t row_tiles = (n_out + g.rows - 1) / g.rows;
-    a.n_wg = row_tiles * a.tok_tiles * a.splits;
+    uint32_t wg = 0;
+    for (uint32_t i = 0; i < kGemmMaxParts; ++i) {
+        GemmPartArgs &P = a.p[i];
+        if (i >= n_parts) {
+            P = a.p[0];
+            P.wg_begin = 0xFFFFFFFFu;
+            continue;
+        }
+        const GemmPartDesc &d = parts[i];
+        const uint32_t per = per_split(g, d.splits ? d.splits : 1);
+        P.w = d.w;
+        P.w_bytes = d.w_bytes;
+        P.row_bytes = d.row_bytes;
+        P.n_out = d.n_out;
+        P.stages_per_split = per;
+        P.splits = (g.nstages + per - 1) / per;
+        if (P.splits != (d.splits ? d.splits : 1)) return hipErrorInvalidValue;  // planned with per_split
+        P.y = P.splits == 1 ? d.y : d.partials;
+        P.wg_begin = wg;
+        wg += ((d.n_out + g.rows - 1) / g.rows) * a.tok_tiles * P.splits;
+    }
+    a.n_wg = wg;
+    if (wg == 0) return hipSuccess;
     const dim3 rb_grid((a.n_wg + 7) / 8 * 8);
     const dim3 blk(64 * waves);
 #define AH_GFORMS(T)                                                                                    \
@@ -748,12 +837,49 @@ hipError_t ah_launch_gemm(uint32_t type, const uint8_t *w, uint32_t w_bytes, uin
     default: return hipErrorInvalidValue;
     }
 #undef AH_GFORMS
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.splits == 1) return e;
-    const size_t n = (size_t)n_tok * n_out;
-    uint32_t rg = (uint32_t)((n + 255) / 256);
-    if (rg > 8192) rg = 8192;
-    hipLaunchKernelGGL(splitk_reduce, dim3(rg), dim3(256), 0, stream, partials, a.splits, n_tok, n_out,
-                       tok_scale, y);
     return hipGetLastError();
+}
+
+// One reduction launch for every part with splits > 1 (kReduceMaxParts per launch).
+hipError_t ah_launch_splitk_reduce(uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_tok,
+                                   const float *tok_scale, hipStream_t stream) {
+    uint32_t i = 0;
+    while (i < n_parts) {
+        ReduceArgs r;
+        r.tok_scale = tok_scale;
+        r.n_tok = n_tok;
+        r.n_parts = 0;
+        bool vec = true;
+        for (; i < n_parts && r.n_parts < kReduceMaxParts; ++i) {
+            const GemmPartDesc &d = parts[i];
+            if (d.splits <= 1 || d.n_out == 0) continue;
+            const size_t n = (size_t)n_tok * d.n_out;
+            vec = vec && n % 4 == 0 && (reinterpret_cast<uintptr_t>(d.partials) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(d.y) & 15u) == 0;
+            ReducePart &P = r.p[r.n_parts++];
+            P.part = d.partials;
+            P.y = d.y;
+            P.n_out = d.n_out;
+            P.splits = d.splits;
+        }
+        if (r.n_parts == 0) continue;
+        uint64_t total = 0;
+        for (uint32_t k = 0; k < r.n_parts; ++k) {
+            r.p[k].begin = total;
+            const uint64_t n = (uint64_t)n_tok * r.p[k].n_out;
+            total += vec ? n / 4 : n;
+        }
+        for (uint32_t k = r.n_parts; k < kReduceMaxParts; ++k) {
+            r.p[k] = r.p[0];
+            r.p[k].begin = ~0ull;
+        }
+        r.total = total;
+        uint64_t rg = (total + 255) / 256;
+        if (rg > 8192) rg = 8192;
+        if (vec) hipLaunchKernelGGL(splitk_reduce<true>, dim3((uint32_t)rg), dim3(256), 0, stream, r);
+        else hipLaunchKernelGGL(splitk_reduce<false>, dim3((uint32_t)rg), dim3(256), 0, stream, r);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }

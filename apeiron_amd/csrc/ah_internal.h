@@ -172,8 +172,19 @@ struct GemvPart {
     uint32_t type;         // GGUF type (AH_GGML_*): read by the mixed-type streaming plan
 };
 
-// GEMM workgroup forms (waves x LDS ring slots), chosen per shape by ah_gemm_pick_waves.
+// GEMM workgroup forms (waves x LDS ring slots), chosen per launch by ah_gemm_pick_waves.
 enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2 };
+
+// One projection of a GEMM launch: the parts of a launch share the GGUF type, the input and its
+// operand (n_in, n_tok), and run in one grid.  `splits` is the part's own split-K count (its
+// partials, [splits][n_tok][n_out] f32, are summed by ah_launch_splitk_reduce afterwards).
+constexpr uint32_t kGemmMaxParts = 4;
+struct GemmPartDesc {
+    const uint8_t *w;
+    uint32_t w_bytes, row_bytes, n_out, splits;
+    float *y;         // [n_tok][n_out]
+    float *partials;  // with splits > 1
+};
 
 // The streaming kernel instantiation whose plan mixes GGUF types (each wave dispatches on its
 // part's type).

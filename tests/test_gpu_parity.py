@@ -500,3 +500,42 @@ def test_gemm_group_equals_single_projections(dev, codes_input):
     assert ei.value.status == 21
     for w in ws + [w_bad]:
         w.free()
+
+
+GROUP_LAYOUTS = [
+    # configs[4] q/k/v at prefill size: two Q4_K parts in one launch, both split, then Q6_K
+    (1536, 512, [(12, 1536), (12, 256), (14, 256)]),
+    # configs[4] gate/up: two 280-tile Q4_K parts in one launch
+    (1536, 512, [(12, 8960), (12, 8960)]),
+    # a run of six Q4_K parts (two launches), an empty part inside it, ragged n_out whose
+    # n_tok * n_out is odd (the scalar reduction path for the whole group)
+    (896, 201, [(12, 100), (12, 0), (12, 257), (12, 64), (12, 896), (12, 33), (12, 128)]),
+    # consecutive Q6_K parts of different split counts, then Q8_0 parts (one per launch)
+    (2048, 300, [(14, 2048), (14, 96), (14, 520), (8, 700), (8, 64)]),
+]
+
+
+@pytest.mark.parametrize("layout", range(len(GROUP_LAYOUTS)))
+def test_gemm_group_runs_equal_single_projections(dev, layout):
+    """Grouped prefill launches several parts of one type in one grid and reduces every split part
+    in one pass; each part's output equals its single-projection GEMM bit for bit."""
+    n_in, n_tok, shapes = GROUP_LAYOUTS[layout]
+    rng = synth.rng_for(7, 50 + layout)
+    x = to_dev(synth.activations(rng, n_in, n_tok).reshape(n_tok, n_in))
+    ws, ys, singles = [], [], []
+    for t, n_out in shapes:
+        w = dev.upload(t, synth.payload(t, rng, n_out, n_in), n_out, n_in)
+        y = torch.full((n_tok, max(n_out, 1)), float("nan"), dtype=torch.float32, device="cuda")
+        y1 = torch.full((n_tok, max(n_out, 1)), float("nan"), dtype=torch.float32, device="cuda")
+        w.gemm_f32_dev(ptr(x), n_tok, ptr(y1), stream())
+        ws.append(w), ys.append(y), singles.append(y1)
+    chart.gemm_group_f32_dev(dev, ws, ptr(x), n_tok, [ptr(y) for y in ys], stream())
+    assert dev.sync_status(stream()) == 0
+    for (t, n_out), y, y1 in zip(shapes, ys, singles):
+        if n_out:
+            assert torch.isfinite(y).all(), (t, n_out)
+            assert torch.equal(y, y1), (t, n_out)
+        else:
+            assert torch.isnan(y).all() and torch.isnan(y1).all()
+    for w in ws:
+        w.free()

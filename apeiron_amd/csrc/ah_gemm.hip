@@ -640,24 +640,27 @@ uint32_t per_split(const GemmGeom &g, uint32_t splits) {
 
 }  // namespace
 
-// Split-K count for an n_tok x n_out GEMM on `cus` compute units.  Cost model (microseconds):
-// the busiest CU runs ceil(workgroups / cus) workgroups of `per` stages each (~0.25 us a stage),
-// and every split beyond the first costs its partials' write and read-back at ~4 TB/s.
+// Split-K count for an n_tok x n_out GEMM on `cus` compute units.  Cost model (microseconds),
+// fitted to a sweep of every valid split count over the configs[3] and configs[4] prefill shapes
+// at N = 512 on MI355X (it picks the measured best for all 13):
+//   the busiest CU runs ceil(workgroups / cus) workgroups of `per` stages, c_type us a stage
+//   (a second resident Q4_K workgroup shares the CU's throughput rather than adding to it);
+//   a split GEMM adds the reduction: 4.8 us fixed plus the partials' write and read-back,
+//   (splits + 1) * n_tok * n_out * 4 bytes at 0.253 us per MB.
 uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
                              uint32_t cus) {
     const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256);
     const uint64_t tiles = (uint64_t)((n_out + g.rows - 1) / g.rows) * ((n_tok + g.toks - 1) / g.toks);
+    const double c = type == AH_GGML_Q8_0 ? 0.806 : type == AH_GGML_Q4_K ? 0.400 : 1.081;
     uint32_t best = 1;
     double best_cost = 1e30;
     for (uint32_t want = 1; want <= 64 && want <= g.nstages; ++want) {
         const uint32_t per = per_split(g, want);
         const uint32_t used = (g.nstages + per - 1) / per;
         if (used != want) continue;
-        // workgroups resident per CU: two of the Q4_K kernel's 64-token tiles, one otherwise
-        const uint64_t slots = (uint64_t)cus * (type == AH_GGML_Q4_K ? 2 : 1);
-        const double waves = (double)((tiles * used + slots - 1) / slots);
-        double cost = waves * per * 0.25;
-        if (used > 1) cost += (double)(used + 1) * n_tok * n_out * 4.0 / 4.0e6;
+        const double waves = (double)((tiles * used + cus - 1) / cus);
+        double cost = waves * per * c;
+        if (used > 1) cost += 4.8 + (double)(used + 1) * n_tok * n_out * 4.0 * 0.253e-6;
         if (cost < best_cost) {
             best_cost = cost;
             best = used;

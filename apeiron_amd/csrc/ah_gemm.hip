@@ -126,24 +126,18 @@ template <int TYPE> constexpr int unroll() { return TYPE == AH_GGML_Q8_0 ? 2 : 4
 // The prologue replays ring - 1 notional stages, so a fetch is at most ring - 1 stages ahead.
 template <int TYPE, int R> constexpr int dw() { return TYPE == AH_GGML_Q6_K || R < 3 ? 1 : 2; }
 template <int TYPE, int R> constexpr int nw() { return dw<TYPE, R>() == 1 ? 2 : 4; }
-// Per-wave vector memory instructions a stage issues: activation slice (16-byte direct-to-LDS
-// loads, 1 KB per instruction), Q4_K split sums (4-byte direct-to-LDS loads, 256 B each), and the
-// weight fetch of super-block position P.
+// Per-wave direct-to-LDS instructions of one stage's slice: activation (16-byte loads, 1 KB per
+// instruction) and Q4_K split sums (4-byte loads, 256 B each).
 template <int TYPE, int W> constexpr int an() { return tok<TYPE>() * kKS * 2 / 1024 / W; }
 template <int TYPE, int W> constexpr int xn() { return TYPE == AH_GGML_Q4_K ? tok<TYPE>() * 32 / 256 / W : 0; }
-template <int TYPE> constexpr int wn(int P) {
-    return TYPE == AH_GGML_Q8_0 ? 6 : TYPE == AH_GGML_Q6_K ? 9 : (P == 0 ? 2 : 1);
-}
-// At the top of stage slot u, the loads issued after that stage's activation slice (issued R - 1
-// stages earlier, R the ring's slots): the weight fetch of the stage that issued it and the
-// slices and fetches of the R - 2 stages after.  Waiting for vmcnt <= this count completes the
-// slice (vector memory loads complete in issue order).
-template <int TYPE, int W, int R> constexpr int wait_count(int u) {
-    constexpr int D = dw<TYPE, R>();
-    int c = (R - 2) * (xn<TYPE, W>() + an<TYPE, W>());
-    for (int j = 1; j <= R - 1; ++j) c += wn<TYPE>((u - j + D + 8) % 4);
-    return c;
-}
+// The vmcnt the top of a stage waits for.  The stage's slice was issued R - 1 stages earlier (R
+// ring slots); after it came the slices of the R - 2 stages that follow and the weight fetches.
+// Only the slices are counted: the compiler merges or drops weight loads that coincide across
+// the unrolled stages (the Q6_K d dword is one address for a whole super-block), so their number
+// per stage is not fixed, while every slice instruction is issued.  Vector memory loads complete
+// in issue order, so vmcnt <= the slice instructions issued since makes the stage's slice (and
+// any weight fetch older than those) complete, whatever the weight loads' count.
+template <int TYPE, int W, int R> constexpr int wait_count() { return (R - 2) * (xn<TYPE, W>() + an<TYPE, W>()); }
 inline uint32_t tok_of(uint32_t type) {
     return type == AH_GGML_Q4_K ? tok<AH_GGML_Q4_K>() : type == AH_GGML_Q6_K ? tok<AH_GGML_Q6_K>() : tok<AH_GGML_Q8_0>();
 }
@@ -342,8 +336,9 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
 
     auto stage = [&](auto uc, uint32_t st) {
         constexpr int u = decltype(uc)::value;
-        // the slice of this stage is complete in every wave, and every wave is done with slot u+3
-        ah_vm_lds_barrier<rb::wait_count<TYPE, WV, RG>(u)>();
+        // the slice of this stage is complete in every wave, and every wave is done with the slot
+        // the next slice goes to (read by the previous stage)
+        ah_vm_lds_barrier<rb::wait_count<TYPE, WV, RG>()>();
         act_dma(lds[(u + kR - 1) % kR], st + kR - 1);
         W[(u + DW) % NW] = fetch_rb<TYPE, (u + DW) % 4, NN>(rs, rbase, rl, st + DW, a.n_in, h, st + DW < st_end);
         __builtin_amdgcn_sched_barrier(0);  // the requests above stay ahead of this stage's work

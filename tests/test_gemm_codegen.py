@@ -1,0 +1,81 @@
+"""Properties of the compiled GEMM kernel that its LDS ring depends on (CPU: hipcc cross-compiles).
+
+The ring's barrier waits for `vmcnt <= (slots - 2) * slice instructions`: vector memory loads
+complete in issue order, so every slice instruction issued before the last (slots - 2) stages'
+slices has landed.  That holds only if each slice instruction is issued on every path, so no
+direct-to-LDS load may sit where an `s_cbranch_execz` can jump over it, and every barrier must use
+the count of its instantiation.
+"""
+from __future__ import annotations
+
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from apeiron_amd import build
+
+HIPCC = build.HIPCC
+KS = 64  # K depth of one stage
+TYPES = {8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}
+
+
+def expected_vmcnt(t: int, waves: int, slots: int) -> int:
+    tok = 64 if t == 12 else 128
+    an = tok * KS * 2 // 1024 // waves
+    xn = tok * 32 // 256 // waves if t == 12 else 0
+    return (slots - 2) * (an + xn)
+
+
+@pytest.fixture(scope="module")
+def gemm_asm(tmp_path_factory):
+    if not (os.path.exists(HIPCC) or shutil.which(HIPCC)):
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("asm") / "ah_gemm.s"
+    flags = [f for f in build.FLAGS if f not in ("-shared", "-fPIC")]
+    cmd = [HIPCC, *flags, "--cuda-device-only", "-S", "-x", "hip",
+           os.path.join(build.CSRC, "ah_gemm.hip"), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return out.read_text().split("\n")
+
+
+def kernels(lines):
+    for i, l in enumerate(lines):
+        m = re.match(r"^(_ZN12_GLOBAL__N_114gemm_rb_kernelILi(\d+)ELi(\d+)ELi(\d+)E\S*):", l)
+        if m:
+            end = next(j for j in range(i, len(lines)) if "s_endpgm" in lines[j])
+            yield (int(m.group(2)), int(m.group(3)), int(m.group(4))), [x.strip() for x in lines[i:end]]
+
+
+def test_every_form_is_compiled(gemm_asm):
+    forms = {k for k, _ in kernels(gemm_asm)}
+    assert {(8, 4, 4), (8, 2, 2), (8, 2, 4), (12, 4, 4), (14, 4, 4), (14, 2, 2), (14, 2, 4)} <= forms
+
+
+def test_ring_barriers_wait_for_the_slice_count(gemm_asm):
+    for (t, waves, slots), body in kernels(gemm_asm):
+        want = expected_vmcnt(t, waves, slots)
+        bars = [i for i, l in enumerate(body) if l.startswith("s_barrier")]
+        assert bars, (t, waves, slots)
+        for i in bars:
+            m = re.match(r"s_waitcnt vmcnt\((\d+)\) lgkmcnt\(0\)", body[i - 1])
+            assert m and int(m.group(1)) == want, (TYPES[t], waves, slots, body[i - 1], want)
+
+
+def test_no_slice_load_can_be_skipped(gemm_asm):
+    def is_slice(l):
+        return l.startswith("buffer_load") and l.endswith(" lds")
+
+    for (t, waves, slots), body in kernels(gemm_asm):
+        assert any(is_slice(l) for l in body), (t, waves, slots)
+        for i, l in enumerate(body):
+            m = re.match(r"s_cbranch_execz\s+(\S+)", l)
+            if not m:
+                continue
+            for j in range(i + 1, len(body)):
+                if body[j].startswith(m.group(1) + ":"):
+                    break
+                assert not is_slice(body[j]), (TYPES[t], waves, slots, j, body[j])

@@ -377,6 +377,43 @@ def test_gemm_q6_k_config4_shapes(dev):
     gemm_check(dev, 14, 8960, 1536, 512, sample_cols=[0, 300, 511])
 
 
+@pytest.mark.parametrize("t,n_out,n_in", [(14, 8960, 1536), (8, 8960, 1536), (14, 1536, 8960),
+                                          (8, 4864, 896), (12, 8960, 1536), (14, 256, 1536)])
+def test_gemm_first_call_after_other_kernels(dev, t, n_out, n_in):
+    """Every LDS ring slot holds this stage's slice before any wave reads it, whatever the CUs ran
+    before: right after GEMMs of another type and shape (their data left in LDS), the first call
+    equals the next calls bit for bit and the oracle.  Covers the three workgroup forms at N = 512
+    (2 waves x 2 slots for 280-tile grids, 2 x 4 for small grids, 4 x 4 otherwise)."""
+    n_tok = 512
+    rng = synth.rng_for(8, t * 7 + n_out)
+    ot = 12 if t != 12 else 14
+    w_o = dev.upload(ot, synth.payload(ot, rng, 2048, 2048), 2048, 2048)
+    x_o = torch.randn(n_tok, 2048, device="cuda")
+    y_o = torch.empty((n_tok, 2048), dtype=torch.float32, device="cuda")
+    raw = synth.payload(t, rng, n_out, n_in)
+    x = synth.activations(rng, n_in, n_tok).reshape(n_tok, n_in)
+    w = dev.upload(t, raw, n_out, n_in)
+    dx = to_dev(x)
+    ys = [torch.full((n_tok, n_out), float("nan"), dtype=torch.float32, device="cuda") for _ in range(3)]
+    for _ in range(3):
+        w_o.gemm_f32_dev(ptr(x_o), n_tok, ptr(y_o), stream())
+    for y in ys:  # queued right behind the other GEMMs, no synchronisation in between
+        w.gemm_f32_dev(ptr(dx), n_tok, ptr(y), stream())
+    assert dev.sync_status(stream()) == 0
+    assert torch.equal(ys[0], ys[1]) and torch.equal(ys[1], ys[2])
+    Y = ys[0].cpu().numpy()
+    rows = np.unique(rng.integers(0, n_out, 128))
+    rb = synth.row_bytes(t, n_in)
+    sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in rows])
+    for c in (0, 77, 300, 511):
+        st, codes, scales = oracle.quant_act_f32(x[c])
+        st, yref = oracle.matvec_q8act(t, sub, len(rows), n_in, codes, scales)
+        st2, absdot = oracle.row_absdot(t, sub, len(rows), n_in, codes, scales)
+        assert_close(Y[c, rows], yref, absdot, f"first call t{t} {n_out}x{n_in} col {c}")
+    w.free()
+    w_o.free()
+
+
 def test_gemm_n1_equals_gemv_within_tolerance(dev):
     rng = synth.rng_for(3, 77)
     for t in (8, 12, 14):

@@ -18,12 +18,13 @@
 // weight-scale change: per 32-block (Q8_0 d), per 16-group (Q6_K d*sc), per 256-super-block
 // (Q4_K d, plus one FMA for the dmin*m*X term, which rides on one extra MFMA per super-block).
 //
-// Tiling (gemm_rb_kernel below): a workgroup is 4 waves over 128 weight rows x 128 tokens; wave w
-// owns 32 weight rows (the MFMA N/column dimension, so the weight scale is one value per lane) and
-// the workgroup's 128 tokens as four 32-token MFMA row tiles.  The f16 activation slice of each
-// 64-deep K stage is staged in LDS (double-buffered) and shared by the 4 waves; each wave reads its
-// own weight rows straight from the GGUF bytes a stage ahead and converts them in registers.
-// Split-K writes partials that a second pass reduces in fixed order.
+// Tiling (gemm_rb_kernel below): a workgroup is 4 (or 2) waves; wave w owns 32 weight rows (the
+// MFMA N/column dimension, so the weight scale is one value per lane) and the workgroup's 128
+// tokens (64 for Q4_K) as 32-token MFMA row tiles.  The f16 activation slice of each 64-deep K
+// stage goes global -> LDS into a ring of 4 (or 2) slots shared by the waves; each wave reads its
+// own weight rows straight from the GGUF bytes ahead of use and converts them in registers.  One
+// launch may cover several projections of one input (parts).  Split-K writes partials that one
+// pass per grouped call reduces in fixed order.
 #include "ah_internal.h"
 
 namespace {

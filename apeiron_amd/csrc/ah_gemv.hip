@@ -651,10 +651,13 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
     const uint32_t nbp = o.kpad / 32;
     // codes rows start at tok * n_in bytes: bytewise loads unless that is a dword boundary
     const bool bytewise = SRC == AH_SRC_CODES && (o.n_in & 3u) != 0;
+    // a wave whose first block of round u is past the padded row skips the round (and the later
+    // ones): every lane's block would read zeros
+    const uint32_t wb0 = __builtin_amdgcn_readfirstlane(wave) * 16u;
     QuadIn in[R];
 #pragma unroll
     for (uint32_t u = 0; u < R; ++u) {
-        if (u * kOpBlocks >= nbp) break;  // uniform: rounds past the padded row
+        if (u * kOpBlocks + wb0 >= nbp) break;
         const uint32_t b = u * kOpBlocks + tid / 4;
         in[u] = bytewise ? quad_load(o.x, srow, SRC, o.n_in, row, b, b < o.nb32) : operand_load<SRC>(r, o.n_in, b);
     }
@@ -663,7 +666,7 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
     int emax = -1;
 #pragma unroll
     for (uint32_t u = 0; u < R; ++u) {
-        if (u * kOpBlocks >= nbp) break;
+        if (u * kOpBlocks + wb0 >= nbp) break;
         const uint32_t b = u * kOpBlocks + tid / 4;
         const QuadOut qo = quad_quant(in[u], SRC, b, o.status, (unsigned long long)row);
         int e = qo.e;
@@ -689,7 +692,7 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
     _Float16 *xh = o.xh + (size_t)tok * o.kpad;
 #pragma unroll
     for (uint32_t u = 0; u < R; ++u) {
-        if (u * kOpBlocks >= nbp) break;
+        if (u * kOpBlocks + wb0 >= nbp) break;
         const uint32_t b = u * kOpBlocks + tid / 4;
         if (b >= nbp) continue;
         const int e = ex[u], sh = e - E;

@@ -132,17 +132,17 @@ AH_DEV int ah_act_code_f32(uint32_t bits, int e, bool &bad) {
     const uint32_t eb = (bits >> 23) & 0xffu;
     const uint32_t ee = eb ? eb : 1u;
     const uint32_t m = (bits & 0x7fffffu) | (eb ? 0x800000u : 0u);
-    uint32_t c;
-    if (ee >= 118u) {
-        const int sh = e + 118 - (int)ee;
-        const uint32_t k = sh < 1 ? 0u : (sh - 1 > 25 ? 25u : (uint32_t)(sh - 1));
-        c = ((m >> k) + 1u) >> 1;
-    } else {
-        const uint32_t k1 = 117u - ee > 25u ? 25u : 117u - ee;
-        const uint32_t mag = ((m >> k1) + 1u) >> 1;
-        const uint32_t k = e < 1 ? 0u : (e - 1 > 25 ? 25u : (uint32_t)(e - 1));
-        c = e == 0 ? mag : ((mag >> k) + 1u) >> 1;
-    }
+    // Both cases are evaluated (shift counts clamped to [0, 25]) and one is selected, so a wave
+    // whose lanes straddle ee = 118 does not run two branches.
+    const int sh = e + 118 - (int)ee;
+    const uint32_t ka = sh < 1 ? 0u : (sh - 1 > 25 ? 25u : (uint32_t)(sh - 1));
+    const uint32_t ca = ((m >> ka) + 1u) >> 1;
+    const int d1 = 117 - (int)ee;
+    const uint32_t k1 = d1 < 0 ? 0u : (d1 > 25 ? 25u : (uint32_t)d1);
+    const uint32_t mag = ((m >> k1) + 1u) >> 1;
+    const uint32_t kb = e < 1 ? 0u : (e - 1 > 25 ? 25u : (uint32_t)(e - 1));
+    const uint32_t cb = e == 0 ? mag : ((mag >> kb) + 1u) >> 1;
+    const uint32_t c = ee >= 118u ? ca : cb;
     const bool neg = (bits >> 31) != 0;
     if (e >= 56) {
         const uint32_t lim = 1u << (63 - e);

@@ -54,6 +54,12 @@ struct ah_ctx {
     int cu_count = 256;
     void *scratch = nullptr;  // device scratch for GEMM operands / host-form staging
     size_t scratch_bytes = 0;
+    // streaming-GEMV occupancy by (type, LDS bytes): a runtime query per launch costs more host
+    // time than a small GEMV takes on the device
+    static constexpr int kOccSlots = 16;
+    uint32_t occ_key[kOccSlots] = {};
+    int occ_val[kOccSlots] = {};
+    int occ_n = 0;
 };
 
 struct ah_tensor {
@@ -185,8 +191,22 @@ void recut_wg_tiles(GemvPart &P) {
 
 // Workgroups that are resident on the whole device at once for the kernel serving these parts:
 // a launch never asks for more, so no workgroup waits for another to finish before it starts.
-uint64_t resident_wgs(const ah_ctx *ctx, uint32_t type, bool stream, uint32_t kpad_max) {
-    int occ = stream ? ah_gemv_stream_occupancy(type, ah_gemv_stream_lds_bytes(kpad_max)) : 4;
+uint64_t resident_wgs(ah_ctx *ctx, uint32_t type, bool stream, uint32_t kpad_max) {
+    int occ = 4;
+    if (stream) {
+        const size_t lds = ah_gemv_stream_lds_bytes(kpad_max);
+        const uint32_t key = (type << 24) | (uint32_t)lds | 0x800000u;  // lds < 2^23
+        occ = -1;
+        for (int i = 0; i < ctx->occ_n; ++i)
+            if (ctx->occ_key[i] == key) occ = ctx->occ_val[i];
+        if (occ < 0) {
+            occ = ah_gemv_stream_occupancy(type, lds);
+            if (occ > 0 && ctx->occ_n < ah_ctx::kOccSlots) {
+                ctx->occ_key[ctx->occ_n] = key;
+                ctx->occ_val[ctx->occ_n++] = occ;
+            }
+        }
+    }
     if (occ < 1) occ = 1;
     return (uint64_t)occ * (uint64_t)ctx->cu_count;
 }

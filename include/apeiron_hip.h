@@ -145,7 +145,8 @@ int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
 
 /* Grouped prefill: n_parts projections of ONE input (q/k/v, gate/up).  gemm_q8_0_group
  * (kern/gemm.rs:799-818) shares one activation pack over its parts; here one operand pass
- * serves every part, then each part's GEMM runs in order on the stream.  All parts share n_in
+ * serves every part, then one GEMM launch per run of same-type parts and one split-K
+ * reduction for the parts that split, in order on the stream.  All parts share n_in
  * (AH_ERR_INVALID_ARG otherwise); ggml types and n_out may differ.  d_y[i] is part i's
  * [n_tok][n_out_i] output; each equals what the single-projection call produces for that part. */
 int32_t ah_gemm_group_f32_dev(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w,

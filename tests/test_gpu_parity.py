@@ -549,6 +549,9 @@ GROUP_LAYOUTS = [
     (896, 201, [(12, 100), (12, 0), (12, 257), (12, 64), (12, 896), (12, 33), (12, 128)]),
     # consecutive Q6_K parts of different split counts, then Q8_0 parts (one per launch)
     (2048, 300, [(14, 2048), (14, 96), (14, 520), (8, 700), (8, 64)]),
+    # ten one-tile Q4_K parts, all split: three GEMM launches (4 + 4 + 2 parts) and two
+    # reduction launches (8 + 2 parts)
+    (2048, 64, [(12, 64 + 32 * i) for i in range(10)]),
 ]
 
 

@@ -136,7 +136,9 @@ int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan);
 /* ---- prefill GEMM, N = n_tok > 1 (kern/matmat.rs:134 matmat_q8act) ---- */
 
 /* y[n_tok][n_out] (token-major) = X W^T for X[n_tok][n_in] f32; quantization is a separate
- * in-stream pass into context scratch (grown on demand, never shrunk). */
+ * in-stream pass into context scratch (grown on demand, never shrunk), which also holds split-K
+ * partials.  GEMM calls on one context share that scratch: calls on different streams of the same
+ * context must not overlap (use one context per stream for concurrent prefills). */
 int32_t ah_gemm_f32_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, size_t n_tok,
                         float *d_y, void *stream);
 /* Same from pre-quantized codes[n_tok][n_in] + scales[n_tok][ceil(n_in/32)]. */

@@ -59,7 +59,8 @@ AH_DEV void u6x4_to_f16(uint32_t u, uint32_t &lo, uint32_t &hi) {
     hi = as_u(as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
 }
 
-// 4 nibble bytes (values 0..15 in the low nibble of each byte) times sc -> 4 exact f16 sc*q.
+// 4 bytes b (the nibble q as q or 16 q) -> 4 f16 (1024 + b) * sc2 + off2 (exact sc*q for the
+// scale pairs the Q4_K stage passes).
 AH_DEV void nib4_times(uint32_t n, f16x2 sc2, f16x2 off2, uint32_t &lo, uint32_t &hi) {
     const uint32_t a = __builtin_amdgcn_perm(0x64646464u, n, 0x04010400u);
     const uint32_t b = __builtin_amdgcn_perm(0x64646464u, n, 0x04030402u);
@@ -460,14 +461,20 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
                 for (int n = 0; n < NN; ++n) {
                     const uint32_t scv = hb ? q4k_scale<2 * u + 1, false>(s0[n], s1[n], s2[n])
                                             : q4k_scale<2 * u, false>(s0[n], s1[n], s2[n]);
-                    const _Float16 sc = (_Float16)(float)scv;
-                    const f16x2 sc2 = {sc, sc}, off2 = {(_Float16)(-1024.0f) * sc, (_Float16)(-1024.0f) * sc};
+                    // Low nibbles (hb = 0): the byte q -> f16 1024 + q, times sc minus 1024 sc.
+                    // High nibbles: the byte masked in place is 16 q -> f16 1024 + 16 q, times
+                    // sc / 16 minus 64 sc.  Both products are exact: sc / 16 and 64 sc are exact
+                    // in f16 and q sc <= 945 is representable, so the fused rounding is exact.
+                    const _Float16 sc = (_Float16)(uint16_t)scv;
+                    const _Float16 scm = hb ? sc * (_Float16)0.0625f : sc;
+                    const _Float16 off = sc * (hb ? (_Float16)(-64.0f) : (_Float16)(-1024.0f));
+                    const f16x2 sc2 = {scm, scm}, off2 = {off, off};
                     const u32x4 q = wc.v[2 * n + 1];
                     const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
                     uint32_t f[8];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const uint32_t nb = hb ? ((qw[i] >> 4) & 0x0F0F0F0Fu) : (qw[i] & 0x0F0F0F0Fu);
+                        const uint32_t nb = qw[i] & (hb ? 0xF0F0F0F0u : 0x0F0F0F0Fu);
                         nib4_times(nb, sc2, off2, f[2 * i], f[2 * i + 1]);
                     }
                     bq[n][0] = pack8(f[0], f[1], f[2], f[3]);

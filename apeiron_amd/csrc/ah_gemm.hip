@@ -277,7 +277,7 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
     if (st_end > nstages) st_end = nstages;
 
     // The f16 activation slice of a stage (kTok tokens x 64 K) goes global -> LDS directly (no
-    // registers), three stages ahead.  Wave w's instruction i fills bytes [(w*kAN + i) KB, +1 KB) of
+    // registers), slots - 1 stages ahead.  Wave w's instruction i fills bytes [(w*kAN + i) KB, +1 KB) of
     // the slot, lane l at +16*l: token t = o / 128 at LDS chunk c' = (o / 16) % 8, which holds the
     // token's K chunk c' ^ ((t >> 1) & 7).  The XOR spreads the 32 token rows an MFMA fragment read
     // touches over all 64 banks.  Stages past the split and tokens past the tile read zeros.

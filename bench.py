@@ -106,7 +106,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
-              "multi-GPU path; see DESIGN.md for how the projections would shard.", file=sys.stderr)
+              "multi-GPU path (a projection would shard by output rows, one row range per GPU, "
+              "with no collective on the GEMV or GEMM itself).", file=sys.stderr)
         return 2
 
     import torch

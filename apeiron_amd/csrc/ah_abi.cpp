@@ -439,6 +439,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     for (size_t i = 0; i < n_parts; ++i) {
         GemmPartDesc &d = pd[i];
         d.w = w[i]->d;
+        d.type = w[i]->type;
         d.w_bytes = (uint32_t)w[i]->bytes;
         d.row_bytes = (uint32_t)w[i]->row_bytes;
         d.n_out = (uint32_t)w[i]->n_out;
@@ -488,18 +489,37 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
             ++i;
             continue;
         }
-        const uint32_t type = w[i]->type, max_run = ah_gemm_max_parts(type);
+        uint32_t type = w[i]->type;
         GemmPartDesc run[kGemmMaxParts];
         uint32_t nr = 0;
         uint64_t wg4 = 0;
+        // K-quant parts of both types (q/k beside v) share one grid when together they leave CUs
+        // idle: one run of consecutive Q4_K/Q6_K parts, if it holds both types and its 4-wave
+        // grid is at most two workgroups per CU; otherwise runs of one type
+        if (type == AH_GGML_Q4_K || type == AH_GGML_Q6_K) {
+            uint32_t k = 0, types = 0;
+            uint64_t g4 = 0;
+            for (size_t j = i; j < n_parts && k < kGemmMaxParts; ++j) {
+                if (pd[j].n_out == 0) continue;
+                if (w[j]->type != AH_GGML_Q4_K && w[j]->type != AH_GGML_Q6_K) break;
+                types |= w[j]->type == AH_GGML_Q4_K ? 1u : 2u;
+                g4 += ah_gemm_part_wg4(w[j]->type, pd[j].n_out, n_in, N, pd[j].splits);
+                ++k;
+            }
+            if (types == 3u && g4 <= 2ull * cus) type = kGemmMixedKQuant;
+        }
+        const uint32_t max_run = type == kGemmMixedKQuant ? kGemmMaxParts : ah_gemm_max_parts(type);
         for (; i < n_parts && nr < max_run; ++i) {
             if (pd[i].n_out == 0) continue;
-            if (w[i]->type != type) break;
+            const bool fits = type == kGemmMixedKQuant
+                                  ? (w[i]->type == AH_GGML_Q4_K || w[i]->type == AH_GGML_Q6_K)
+                                  : w[i]->type == type;
+            if (!fits) break;
             run[nr++] = pd[i];
-            wg4 += ah_gemm_part_wg4(type, pd[i].n_out, n_in, N, pd[i].splits);
+            wg4 += ah_gemm_part_wg4(w[i]->type, pd[i].n_out, n_in, N, pd[i].splits);
             any_split = any_split || pd[i].splits > 1;
         }
-        const uint32_t form = ah_gemm_pick_waves(type, wg4, cus);
+        const uint32_t form = type == kGemmMixedKQuant ? kForm4x4 : ah_gemm_pick_waves(type, wg4, cus);
         AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xmin, ts, form, s));
     }
     if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd.data(), N, ts, s));

@@ -80,6 +80,8 @@ struct GemmPartArgs {
     uint32_t w_bytes, row_bytes, n_out;
     uint32_t stages_per_split; // K stages of 64 per split (multiple of the kernel's unroll)
     uint32_t splits, wg_begin;
+    uint32_t tok_tiles;        // token tiles of the part's type
+    uint32_t type;             // GGUF type (read by the mixed K-quant kernel)
 };
 struct GemmArgs {
     GemmPartArgs p[kGemmMaxParts];
@@ -87,7 +89,7 @@ struct GemmArgs {
     const _Float16 *xh;        // [n_tok][kpad]
     const _Float16 *xmin;      // Q4_K: [n_tok][kpad/256][16] split code sums (see quant pass)
     const float *tok_scale;    // [n_tok]
-    uint32_t tok_tiles, n_wg;  // token tiles, real workgroup count over all parts
+    uint32_t n_wg;             // real workgroup count over all parts
 };
 
 constexpr uint32_t kOob = 0xFFFFFFF0u;  // a buffer offset past any operand: reads zeros
@@ -224,13 +226,16 @@ AH_DEV uint32_t q4k_scale(uint32_t s0, uint32_t s1, uint32_t s2) {
     else return (byte(J + 4) >> 4) | ((byte(J) >> 6) << 4);
 }
 
+// The kernel body, on an LDS ring of RG slots of buf_bytes<TYPE> at `lds`.
 template <int TYPE, int WV, int RG>
-__global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
+// (by value: with a reference to the kernel argument the Q8_0 kernel grows from 207 to 256 VGPRs)
+AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds_base) {
     constexpr int NN = rb::kNN, NM = rb::nm<TYPE>(), NW = rb::nw<TYPE, RG>(), DW = rb::dw<TYPE, RG>();
     constexpr int kTok = rb::tok<TYPE>(), kActBytes = rb::act_bytes<TYPE>();
     constexpr int kAN = rb::an<TYPE, WV>(), kXN = rb::xn<TYPE, WV>();
     constexpr int kR = RG;
-    __shared__ __align__(16) uint8_t lds[kR][rb::buf_bytes<TYPE>()];
+    constexpr uint32_t kBuf = rb::buf_bytes<TYPE>();
+    auto lds = [&](int k) -> uint8_t * { return lds_base + k * kBuf; };
     // XCD-aware order: dispatch i goes to XCD i % 8, so XCD x takes logical ids
     // [x * per, (x + 1) * per).  Consecutive logical ids share a weight row tile and split, so the
     // workgroups reading the same weights share one XCD's L2.  The grid is a multiple of 8.
@@ -246,7 +251,7 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
         if (i < a.n_parts && L >= a.p[i].wg_begin) pi = i;
     const GemmPartArgs &pa = a.p[pi];
     const uint32_t Lp = L - pa.wg_begin;
-    const uint32_t tt = Lp % a.tok_tiles, rest = Lp / a.tok_tiles;
+    const uint32_t tt = Lp % pa.tok_tiles, rest = Lp / pa.tok_tiles;
     const uint32_t split = rest % pa.splits, rtile = rest / pa.splits;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -327,7 +332,7 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
     WRb W[NW];
     auto prologue = [&](auto kc) {
         constexpr int k = decltype(kc)::value, rel = k - (kR - 1) + DW;  // fetched stage - st_begin
-        act_dma(lds[k], st_begin + k);
+        act_dma(lds(k), st_begin + k);
         constexpr int wi = ((rel % NW) + NW) % NW, P = ((rel % 4) + 4) % 4;
         W[wi] = fetch_rb<TYPE, P, NN>(rs, rbase, rl, rel >= 0 ? st_begin + rel : st_begin, a.n_in, h,
                                       rel >= 0 && st_begin + rel < st_end);
@@ -341,10 +346,10 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
         // the slice of this stage is complete in every wave, and every wave is done with the slot
         // the next slice goes to (read by the previous stage)
         ah_vm_lds_barrier<rb::wait_count<TYPE, WV, RG>()>();
-        act_dma(lds[(u + kR - 1) % kR], st + kR - 1);
+        act_dma(lds((u + kR - 1) % kR), st + kR - 1);
         W[(u + DW) % NW] = fetch_rb<TYPE, (u + DW) % 4, NN>(rs, rbase, rl, st + DW, a.n_in, h, st + DW < st_end);
         __builtin_amdgcn_sched_barrier(0);  // the requests above stay ahead of this stage's work
-        const uint8_t *cur = lds[u % kR];
+        const uint8_t *cur = lds(u % kR);
         const WRb &wc = W[u % NW];
         if constexpr (TYPE == AH_GGML_Q8_0) {
             // 2*NM*NN MFMA chains per stage (block bb, token tile m, row tile n), each two MFMAs
@@ -554,6 +559,30 @@ __global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
             }
         }
     }
+}
+
+template <int TYPE, int WV, int RG>
+__global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
+    __shared__ __align__(16) uint8_t lds[RG * rb::buf_bytes<TYPE>()];
+    gemm_rb_body<TYPE, WV, RG>(a, lds);
+}
+
+// Q4_K and Q6_K parts of one input in one grid (4 waves, 4 slots sized for the larger type):
+// each workgroup runs its part's body, a branch uniform over the workgroup.  A group's runs of
+// the two types (q/k beside v) then share the CUs one run alone leaves idle.
+__global__ void __launch_bounds__(256, 2) gemm_rb_kquant_kernel(GemmArgs a) {
+    constexpr uint32_t kB = rb::buf_bytes<AH_GGML_Q4_K>() > rb::buf_bytes<AH_GGML_Q6_K>()
+                                ? rb::buf_bytes<AH_GGML_Q4_K>() : rb::buf_bytes<AH_GGML_Q6_K>();
+    __shared__ __align__(16) uint8_t lds[4 * kB];
+    const uint32_t per = gridDim.x >> 3;
+    const uint32_t L = (blockIdx.x & 7u) * per + (blockIdx.x >> 3);
+    if (L >= a.n_wg) return;
+    uint32_t pi = 0;
+#pragma unroll
+    for (uint32_t i = 1; i < kGemmMaxParts; ++i)
+        if (i < a.n_parts && L >= a.p[i].wg_begin) pi = i;
+    if (a.p[pi].type == AH_GGML_Q4_K) gemm_rb_body<AH_GGML_Q4_K, 4, 4>(a, lds);
+    else gemm_rb_body<AH_GGML_Q6_K, 4, 4>(a, lds);
 }
 
 // y[tok][row] = tok_scale[tok] * sum_s partial[s][tok][row], summed in split order from 0, for
@@ -794,10 +823,10 @@ hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, ui
 hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_in,
                           uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xmin,
                           const float *tok_scale, uint32_t form, hipStream_t stream) {
-    if (n_parts == 0 || n_parts > rb::max_parts_of(type)) return hipErrorInvalidValue;
-    if (type == AH_GGML_Q4_K || form > kForm2x4) form = kForm4x4;
+    const bool mixed = type == kGemmMixedKQuant;  // Q4_K and Q6_K parts, 4-wave form
+    if (n_parts == 0 || n_parts > (mixed ? kGemmMaxParts : rb::max_parts_of(type))) return hipErrorInvalidValue;
+    if (mixed || type == AH_GGML_Q4_K || form > kForm2x4) form = kForm4x4;
     const uint32_t waves = form == kForm4x4 ? 4u : 2u;
-    const GemmGeom g = geom_of(type, n_in, kpad, waves);
     GemmArgs a;
     a.n_parts = n_parts;
     a.n_in = n_in;
@@ -806,7 +835,6 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     a.xh = xh;
     a.xmin = xmin;
     a.tok_scale = tok_scale;
-    a.tok_tiles = (n_tok + g.toks - 1) / g.toks;
     uint32_t wg = 0;
     for (uint32_t i = 0; i < kGemmMaxParts; ++i) {
         GemmPartArgs &P = a.p[i];
@@ -816,6 +844,9 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
             continue;
         }
         const GemmPartDesc &d = parts[i];
+        const uint32_t pt = mixed ? d.type : type;
+        if (mixed && pt != AH_GGML_Q4_K && pt != AH_GGML_Q6_K) return hipErrorInvalidValue;
+        const GemmGeom g = geom_of(pt, n_in, kpad, waves);
         const uint32_t per = per_split(g, d.splits ? d.splits : 1);
         P.w = d.w;
         P.w_bytes = d.w_bytes;
@@ -826,7 +857,9 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
         if (P.splits != (d.splits ? d.splits : 1)) return hipErrorInvalidValue;  // planned with per_split
         P.y = P.splits == 1 ? d.y : d.partials;
         P.wg_begin = wg;
-        wg += ((d.n_out + g.rows - 1) / g.rows) * a.tok_tiles * P.splits;
+        P.tok_tiles = (n_tok + g.toks - 1) / g.toks;
+        P.type = pt;
+        wg += ((d.n_out + g.rows - 1) / g.rows) * P.tok_tiles * P.splits;
     }
     a.n_wg = wg;
     if (wg == 0) return hipSuccess;
@@ -837,6 +870,7 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     else if (form == kForm2x4) hipLaunchKernelGGL((gemm_rb_kernel<T, 2, 4>), rb_grid, blk, 0, stream, a); \
     else hipLaunchKernelGGL((gemm_rb_kernel<T, 4, 4>), rb_grid, blk, 0, stream, a);
     switch (type) {
+    case kGemmMixedKQuant: hipLaunchKernelGGL(gemm_rb_kquant_kernel, rb_grid, blk, 0, stream, a); break;
     case AH_GGML_Q8_0: AH_GFORMS(AH_GGML_Q8_0) break;
     case AH_GGML_Q4_K: hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q4_K, 4, 4>), rb_grid, blk, 0, stream, a); break;
     case AH_GGML_Q6_K: AH_GFORMS(AH_GGML_Q6_K) break;

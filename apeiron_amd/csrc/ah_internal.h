@@ -179,8 +179,11 @@ enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2 };
 // operand (n_in, n_tok), and run in one grid.  `splits` is the part's own split-K count (its
 // partials, [splits][n_tok][n_out] f32, are summed by ah_launch_splitk_reduce afterwards).
 constexpr uint32_t kGemmMaxParts = 4;
+// ah_launch_gemm's `type` for one grid of Q4_K and Q6_K parts (each part's own type applies).
+constexpr uint32_t kGemmMixedKQuant = 0xFFFFu;
 struct GemmPartDesc {
     const uint8_t *w;
+    uint32_t type;    // the part's GGUF type
     uint32_t w_bytes, row_bytes, n_out, splits;
     float *y;         // [n_tok][n_out]
     float *partials;  // with splits > 1

@@ -65,6 +65,31 @@ def test_ring_barriers_wait_for_the_slice_count(gemm_asm):
             assert m and int(m.group(1)) == want, (TYPES[t], waves, slots, body[i - 1], want)
 
 
+def test_mixed_kquant_kernel_barriers(gemm_asm):
+    """The grid of Q4_K and Q6_K parts holds both bodies on a 4-slot ring of 4 waves; both wait
+    for 8 slice instructions and no slice load sits behind an execz branch."""
+    starts = [i for i, l in enumerate(gemm_asm) if re.match(r"^_ZN12_GLOBAL__N_121gemm_rb_kquant_kernel\S*:", l)]
+    assert starts
+    end = next(j for j in range(starts[0], len(gemm_asm)) if "s_endpgm" in gemm_asm[j])
+    body = [x.strip() for x in gemm_asm[starts[0]:end]]
+    want = expected_vmcnt(12, 4, 4)
+    assert want == expected_vmcnt(14, 4, 4)
+    ring = 0
+    for i, l in enumerate(body):
+        if l.startswith("s_barrier"):
+            m = re.match(r"s_waitcnt vmcnt\((\d+)\) lgkmcnt\(0\)$", body[i - 1])
+            if m:
+                ring += 1
+                assert int(m.group(1)) == want, body[i - 1]
+        m = re.match(r"s_cbranch_execz\s+(\S+)", l)
+        if m:
+            for j in range(i + 1, len(body)):
+                if body[j].startswith(m.group(1) + ":"):
+                    break
+                assert not (body[j].startswith("buffer_load") and body[j].endswith(" lds")), body[j]
+    assert ring >= 8, ring  # four stages in each body
+
+
 def test_no_slice_load_can_be_skipped(gemm_asm):
     def is_slice(l):
         return l.startswith("buffer_load") and l.endswith(" lds")

@@ -578,8 +578,8 @@ int32_t ah_init(int32_t device, ah_ctx **out) {
         return AH_ERR_HIP;
     }
     if (reset_status(ctx) != AH_OK) {
-        hipFree(ctx->d_status);
-        hipStreamDestroy(ctx->stream);
+        (void)hipFree(ctx->d_status);
+        (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return AH_ERR_HIP;
     }
@@ -589,11 +589,11 @@ int32_t ah_init(int32_t device, ah_ctx **out) {
 
 int32_t ah_destroy(ah_ctx *ctx) {
     if (!ctx) return AH_ERR_INVALID_ARG;
-    hipSetDevice(ctx->device);
-    hipStreamSynchronize(ctx->stream);
-    if (ctx->scratch) hipFree(ctx->scratch);
-    hipFree(ctx->d_status);
-    hipStreamDestroy(ctx->stream);
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    (void)hipFree(ctx->d_status);
+    (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return AH_OK;
 }
@@ -645,7 +645,7 @@ int32_t ah_upload_weight(ah_ctx *ctx, uint32_t type, const void *raw, size_t raw
     const hipError_t ce = hipMemcpy(t->d, src, dev_bytes, hipMemcpyHostToDevice);
     std::free(packed);
     if (ce != hipSuccess) {
-        hipFree(t->d);
+        (void)hipFree(t->d);
         delete t;
         return AH_ERR_HIP;
     }
@@ -677,7 +677,7 @@ int32_t ah_wrap_weight_dev(ah_ctx *ctx, uint32_t type, const void *d_raw, size_t
         e = ah_launch_scan(static_cast<const uint8_t *>(d_raw), need / bb, bb, o0, o1, d_bad, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e == hipSuccess) e = hipMemcpy(&bad, d_bad, sizeof(int), hipMemcpyDeviceToHost);
-    hipFree(d_bad);
+    (void)hipFree(d_bad);
     if (e != hipSuccess) {
         ctx->last_hip = (int)e;
         return AH_ERR_HIP;
@@ -699,9 +699,9 @@ int32_t ah_wrap_weight_dev(ah_ctx *ctx, uint32_t type, const void *d_raw, size_t
 int32_t ah_free_tensor(ah_ctx *ctx, ah_tensor *t) {
     if (!ctx || !t) return AH_ERR_INVALID_ARG;
     if (t->owned && t->d) {
-        hipSetDevice(ctx->device);
-        hipStreamSynchronize(ctx->stream);
-        hipFree(t->d);
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(t->d);
     }
     delete t;
     return AH_OK;
@@ -910,8 +910,8 @@ int32_t ah_gemv_plan_run(ah_ctx *ctx, const ah_gemv_plan *plan, void *stream) {
 
 int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan) {
     if (!ctx || !plan) return AH_ERR_INVALID_ARG;
-    hipSetDevice(ctx->device);
-    hipStreamSynchronize(ctx->stream);
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
     (void)hipFree(plan->d_parts);
     if (plan->d_wg_part) (void)hipFree(plan->d_wg_part);
     if (plan->d_wgd) (void)hipFree(plan->d_wgd);
@@ -1016,7 +1016,7 @@ int32_t ah_matmat_q8act(ah_ctx *ctx, const ah_tensor *w, const int8_t *codes, co
     int32_t st = e == hipSuccess ? gemm_launch(ctx, w, AH_SRC_CODES, dc, ds, n_tok, dy, nullptr) : AH_ERR_HIP;
     if (st == AH_OK) st = ah_sync_status(ctx, nullptr);
     if (st == AH_OK && hipMemcpy(y, dy, n_tok * w->n_out * 4, hipMemcpyDeviceToHost) != hipSuccess) st = AH_ERR_HIP;
-    hipFree(buf);
+    (void)hipFree(buf);
     if (e != hipSuccess) ctx->last_hip = (int)e;
     return st;
 }

@@ -552,6 +552,8 @@ GROUP_LAYOUTS = [
     # ten one-tile Q4_K parts, all split: three GEMM launches (4 + 4 + 2 parts) and two
     # reduction launches (8 + 2 parts)
     (2048, 64, [(12, 64 + 32 * i) for i in range(10)]),
+    # alternating Q6_K / Q4_K parts in one mixed K-quant grid, ragged widths, then a fifth part
+    (1536, 200, [(14, 300), (12, 700), (14, 64), (12, 1000), (14, 129)]),
 ]
 
 

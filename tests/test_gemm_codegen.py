@@ -104,3 +104,27 @@ def test_no_slice_load_can_be_skipped(gemm_asm):
                 if body[j].startswith(m.group(1) + ":"):
                     break
                 assert not is_slice(body[j]), (TYPES[t], waves, slots, j, body[j])
+
+
+@pytest.fixture(scope="module")
+def gemv_asm(tmp_path_factory):
+    if not (os.path.exists(HIPCC) or shutil.which(HIPCC)):
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("asm") / "ah_gemv.s"
+    flags = [f for f in build.FLAGS if f not in ("-shared", "-fPIC")]
+    cmd = [HIPCC, *flags, "--cuda-device-only", "-S", "-x", "hip",
+           os.path.join(build.CSRC, "ah_gemv.hip"), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return out.read_text().split("\n")
+
+
+def test_no_packed_fp32_instructions(gemm_asm, gemv_asm):
+    """Every HIP translation unit is built with packed FP32 disabled, and no kernel contains
+    v_pk_add_f32 / v_pk_mul_f32 / v_pk_fma_f32 (some of their forms have given wrong results on
+    these devices without an error)."""
+    i = build.FLAGS.index("-packed-fp32-ops")
+    assert build.FLAGS[i - 1] == "-Xclang" and build.FLAGS[i - 2] == "-target-feature"
+    for asm in (gemm_asm, gemv_asm):
+        bad = [l.strip() for l in asm if re.match(r"\s*v_pk_(add|mul|fma)_f32\b", l)]
+        assert not bad, bad[:5]

@@ -26,6 +26,7 @@ EXPORTS = [
     "ah_gemv_plan_run", "ah_gemv_plan_free", "ah_gemm_f32_dev", "ah_gemm_q8_dev",
     "ah_gemv_q8_dots_dev", "ah_sync_status", "ah_matvec_q8act", "ah_matmat_q8act",
     "ah_quant_act", "ah_probe_mfma_peak", "ah_gemm_group_f32_dev", "ah_gemm_group_q8_dev",
+    "ah_last_refusal_bits",
 ]
 
 _lib = None
@@ -50,6 +51,7 @@ def load() -> ctypes.CDLL:
         "ah_destroy": (I32, [P]),
         "ah_status_str": (ctypes.c_char_p, [I32]),
         "ah_last_hip_error": (I32, [P]),
+        "ah_last_refusal_bits": (I32, [P, ctypes.POINTER(U32)]),
         "ah_upload_weight": (I32, [P, U32, P, S, S, S, ctypes.POINTER(P)]),
         "ah_wrap_weight_dev": (I32, [P, U32, P, S, S, S, ctypes.POINTER(P)]),
         "ah_free_tensor": (I32, [P, P]),

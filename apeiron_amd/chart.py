@@ -88,6 +88,12 @@ class Device:
     def sync_status(self, stream: int | None = None) -> int:
         return self.lib.ah_sync_status(self.h, stream)
 
+    def last_refusal_bits(self) -> int:
+        """f16 bits of the scale behind the last NonFiniteScale refusal (NonFiniteScale { bits })."""
+        b = ctypes.c_uint32(0)
+        _check(self.lib.ah_last_refusal_bits(self.h, ctypes.byref(b)), "last_refusal_bits")
+        return b.value
+
     def probe_mfma_peak(self, kind: int) -> float:
         """Measured MFMA-only rate in tera-ops/s (kind 0: int8 32x32x32, 1: f16 32x32x16)."""
         out = ctypes.c_double(0.0)

@@ -31,12 +31,13 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const Ge
                                  unsigned long long *status, hipStream_t stream);
 hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream);
 hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes, uint32_t off0,
-                          uint32_t off1, int *d_bad, hipStream_t stream);
+                          uint32_t off1, unsigned long long *d_bad, hipStream_t stream);
 hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_in,
                           uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xmin,
-                          const float *tok_scale, uint32_t form, hipStream_t stream);
+                          const float *tok_scale, const int8_t *fcodes, const int64_t *fscales,
+                          unsigned long long *status, uint32_t form, hipStream_t stream);
 hipError_t ah_launch_splitk_reduce(uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_tok,
-                                   const float *tok_scale, hipStream_t stream);
+                                   const float *tok_scale, unsigned long long *status, hipStream_t stream);
 uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
                              uint32_t cus);
 uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits);
@@ -51,6 +52,7 @@ struct ah_ctx {
     hipStream_t stream = nullptr;
     unsigned long long *d_status = nullptr;
     int last_hip = 0;
+    uint32_t last_bad_bits = 0;  // f16 bits behind the last AH_ERR_NONFINITE_SCALE
     int cu_count = 256;
     void *scratch = nullptr;  // device scratch for GEMM operands / host-form staging
     size_t scratch_bytes = 0;
@@ -456,6 +458,10 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     const size_t o_xh = off; off = align256(off + (size_t)N * kpad * 2);
     const size_t o_ts = off; off = align256(off + (size_t)N * 4);
     const size_t o_xmin = off; off = align256(off + (any_q4k ? (size_t)N * nsb * 32 : 0));
+    // flagged tokens' QuantAct (f32 input; codes input is read in place)
+    const bool keep = src == AH_SRC_F32;
+    const size_t o_fc = off; off = align256(off + (keep ? (size_t)N * n_in : 0));
+    const size_t o_fs = off; off = align256(off + (keep ? (size_t)N * nb32 * 8 : 0));
     const size_t o_part = off; off = align256(off + part_bytes);
     int32_t st = ensure_scratch(ctx, off);
     if (st) return st;
@@ -463,6 +469,8 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     _Float16 *xh = reinterpret_cast<_Float16 *>(S + o_xh);
     float *ts = reinterpret_cast<float *>(S + o_ts);
     _Float16 *xmin = reinterpret_cast<_Float16 *>(S + o_xmin);
+    int8_t *fcodes = keep ? reinterpret_cast<int8_t *>(S + o_fc) : static_cast<int8_t *>(const_cast<void *>(x));
+    int64_t *fscales = keep ? reinterpret_cast<int64_t *>(S + o_fs) : const_cast<int64_t *>(scales_in);
     for (size_t i = 0; i < n_parts; ++i)
         if (pd[i].splits > 1) pd[i].partials = reinterpret_cast<float *>(S + o_part + part_off[i]);
     hipStream_t s = pick(ctx, stream);
@@ -475,6 +483,8 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     o.xh = xh;
     o.tok_scale = ts;
     o.xmin = any_q4k ? xmin : nullptr;
+    o.fcodes = keep ? fcodes : nullptr;
+    o.fscales = keep ? fscales : nullptr;
     o.status = ctx->d_status;
     o.n_tok = N;
     o.n_in = n_in;
@@ -520,9 +530,9 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
             any_split = any_split || pd[i].splits > 1;
         }
         const uint32_t form = type == kGemmMixedKQuant ? kForm4x4 : ah_gemm_pick_waves(type, wg4, cus);
-        AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xmin, ts, form, s));
+        AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xmin, ts, fcodes, fscales, ctx->d_status, form, s));
     }
-    if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd.data(), N, ts, s));
+    if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd.data(), N, ts, ctx->d_status, s));
     return AH_OK;
 }
 
@@ -600,6 +610,12 @@ int32_t ah_destroy(ah_ctx *ctx) {
 
 int32_t ah_last_hip_error(const ah_ctx *ctx) { return ctx ? ctx->last_hip : 0; }
 
+int32_t ah_last_refusal_bits(const ah_ctx *ctx, uint32_t *bits) {
+    if (!ctx || !bits) return AH_ERR_INVALID_ARG;
+    *bits = ctx->last_bad_bits;
+    return AH_OK;
+}
+
 int32_t ah_upload_weight(ah_ctx *ctx, uint32_t type, const void *raw, size_t raw_len, size_t n_out,
                          size_t n_in, ah_tensor **out) {
     if (!ctx || !out || (!raw && raw_len)) return AH_ERR_INVALID_ARG;
@@ -613,7 +629,10 @@ int32_t ah_upload_weight(ah_ctx *ctx, uint32_t type, const void *raw, size_t raw
     for (size_t off = 0; off < need; off += bb) {
         const uint16_t h0 = (uint16_t)(b[off + o0] | (b[off + o0 + 1] << 8));
         const uint16_t h1 = (uint16_t)(b[off + o1] | (b[off + o1 + 1] << 8));
-        if (f16_nonfinite(h0) || f16_nonfinite(h1)) return AH_ERR_NONFINITE_SCALE;
+        if (f16_nonfinite(h0) || f16_nonfinite(h1)) {
+            ctx->last_bad_bits = f16_nonfinite(h0) ? h0 : h1;
+            return AH_ERR_NONFINITE_SCALE;
+        }
     }
     // A Q4_K row whose K is not a multiple of 256 ends in a partial super-block whose trailing qs
     // chunks the product never reads; the device copy keeps each row's leading `stride` bytes only
@@ -669,20 +688,23 @@ int32_t ah_wrap_weight_dev(ah_ctx *ctx, uint32_t type, const void *d_raw, size_t
     uint32_t o0, o1, bb;
     scale_offsets(type, o0, o1, bb);
     AH_HIP(ctx, hipSetDevice(ctx->device));
-    int *d_bad = nullptr;
-    AH_HIP(ctx, hipMalloc(&d_bad, sizeof(int)));
-    int bad = 0;
-    hipError_t e = hipMemcpy(d_bad, &bad, sizeof(int), hipMemcpyHostToDevice);
+    unsigned long long *d_bad = nullptr;
+    AH_HIP(ctx, hipMalloc(&d_bad, sizeof(*d_bad)));
+    unsigned long long bad = ~0ull;  // earliest non-finite scale: (block << 17) | (dmin << 16) | bits
+    hipError_t e = hipMemcpy(d_bad, &bad, sizeof(bad), hipMemcpyHostToDevice);
     if (e == hipSuccess)
         e = ah_launch_scan(static_cast<const uint8_t *>(d_raw), need / bb, bb, o0, o1, d_bad, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    if (e == hipSuccess) e = hipMemcpy(&bad, d_bad, sizeof(int), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(&bad, d_bad, sizeof(bad), hipMemcpyDeviceToHost);
     (void)hipFree(d_bad);
     if (e != hipSuccess) {
         ctx->last_hip = (int)e;
         return AH_ERR_HIP;
     }
-    if (bad) return AH_ERR_NONFINITE_SCALE;
+    if (bad != ~0ull) {
+        ctx->last_bad_bits = (uint32_t)(bad & 0xffffu);
+        return AH_ERR_NONFINITE_SCALE;
+    }
     ah_tensor *t = new (std::nothrow) ah_tensor();
     if (!t) return AH_ERR_OUT_OF_MEMORY;
     t->type = type;

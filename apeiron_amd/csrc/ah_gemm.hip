@@ -88,7 +88,10 @@ struct GemmArgs {
     uint32_t n_parts, n_in, n_tok, kpad;
     const _Float16 *xh;        // [n_tok][kpad]
     const _Float16 *xmin;      // Q4_K: [n_tok][kpad/256][16] split code sums (see quant pass)
-    const float *tok_scale;    // [n_tok]
+    const float *tok_scale;    // [n_tok]; bit 0 set: the token is served by the exact path
+    unsigned long long *status;
+    const int8_t *fcodes;      // [n_tok][n_in] codes of flagged tokens
+    const int64_t *fscales;    // [n_tok][nb32] their scales
     uint32_t n_wg;             // real workgroup count over all parts
 };
 
@@ -224,6 +227,74 @@ AH_DEV uint32_t q4k_scale(uint32_t s0, uint32_t s1, uint32_t s2) {
     if constexpr (J < 4) return byte(J + (MIN ? 4 : 0)) & 63;
     else if constexpr (!MIN) return (byte(J + 4) & 0xF) | ((byte(J - 4) >> 6) << 4);
     else return (byte(J + 4) >> 4) | ((byte(J) >> 6) << 4);
+}
+
+// ---- exact path for tokens the f16 operand cannot carry ----------------------------------------
+//
+// A token flagged by the operand pass (a nonzero block more than kF16Band binades below its largest)
+// is recomputed per row from its codes and power-of-two scales, like the GEMV: exact integer group
+// dots, folded in f32 with the block scale S_b * 2^-32 (an exact f32 power of two for every S_b a
+// QuantAct can hold).  Units are Q8_0 blocks / K-quant super-blocks in [u_lo, u_hi), every second
+// one from `first`.  Byte loads throughout: this path serves rare, pathological activations.
+AH_DEV float s_of(const int64_t *sc, uint32_t b) { return (float)sc[b] * 0x1p-32f; }  // exact for 2^e
+AH_DEV uint32_t byte_at(const uint8_t *p, uint32_t i) { return p[i]; }
+AH_DEV float f16_at(const uint8_t *p) { return ah_f16_bits_to_f32(byte_at(p, 0) | (byte_at(p, 1) << 8)); }
+
+template <int TYPE>
+AH_DEV float exact_row(const uint8_t *row, const int8_t *xq, const int64_t *sc, uint32_t n_in,
+                       uint32_t u_lo, uint32_t u_hi, uint32_t first) {
+    float acc = 0.0f;
+    for (uint32_t u = u_lo + first; u < u_hi; u += 2) {
+        if constexpr (TYPE == AH_GGML_Q8_0) {
+            const uint8_t *blk = row + 34 * u;
+            int D = 0;
+            for (uint32_t l = 0; l < 32 && 32 * u + l < n_in; ++l)
+                D += (int)(int8_t)byte_at(blk, 2 + l) * (int)xq[32 * u + l];
+            acc += s_of(sc, u) * (f16_at(blk) * (float)D);
+        } else if constexpr (TYPE == AH_GGML_Q4_K) {
+            const uint8_t *sb = row + 144 * u;
+            const float d = f16_at(sb), dmin = f16_at(sb + 2);
+            for (uint32_t j = 0; j < 8 && 256 * u + 32 * j < n_in; ++j) {
+                // get_scale_min_k4 (format/quant.rs:200-213)
+                const uint8_t *s12 = sb + 4;
+                uint32_t scj, mj;
+                if (j < 4) {
+                    scj = byte_at(s12, j) & 63;
+                    mj = byte_at(s12, j + 4) & 63;
+                } else {
+                    scj = (byte_at(s12, j + 4) & 15) | ((byte_at(s12, j - 4) >> 6) << 4);
+                    mj = (byte_at(s12, j + 4) >> 4) | ((byte_at(s12, j) >> 6) << 4);
+                }
+                int D = 0, X = 0;
+                for (uint32_t l = 0; l < 32; ++l) {
+                    const uint32_t k = 256 * u + 32 * j + l;
+                    if (k >= n_in) break;
+                    const int q = (int)((byte_at(sb + 16, 32 * (j / 2) + l) >> (4 * (j & 1))) & 15);
+                    D += q * (int)xq[k];
+                    X += (int)xq[k];
+                }
+                acc += s_of(sc, 8 * u + j) * ((d * (float)scj) * (float)D - (dmin * (float)mj) * (float)X);
+            }
+        } else {  // Q6_K: element 128n + 32t + l (format/quant.rs:556-599), 16-groups g
+            const uint8_t *sb = row + 210 * u;
+            const float d = f16_at(sb + 208);
+            for (uint32_t g = 0; g < 16 && 256 * u + 16 * g < n_in; ++g) {
+                int D = 0;
+                for (uint32_t i = 0; i < 16; ++i) {
+                    const uint32_t e = 16 * g + i, k = 256 * u + e;
+                    if (k >= n_in) break;
+                    const uint32_t n = e / 128, t = (e % 128) / 32, l = e % 32;
+                    const uint32_t lb = byte_at(sb, 64 * n + l + 32 * (t & 1));
+                    const uint32_t hb = byte_at(sb + 128, 32 * n + l);
+                    const int uq = (int)(((t < 2 ? lb : lb >> 4) & 15) | (((hb >> (2 * t)) & 3) << 4));
+                    D += (uq - 32) * (int)xq[k];
+                }
+                const int scg = (int)(int8_t)byte_at(sb + 192, g);
+                acc += s_of(sc, (256 * u + 16 * g) / 32) * ((d * (float)scg) * (float)D);
+            }
+        }
+    }
+    return acc;
 }
 
 // The kernel body, on an LDS ring of RG slots of buf_bytes<TYPE> at `lds`.
@@ -534,35 +605,87 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // D layout of a 32x32 MFMA: lane (j, h), register r -> row i = 8*(r/4) + 4*h + (r%4), col j.
-    // Token scales (1.0 for partials) are loaded up front; lanes past n_out and tokens past n_tok
-    // store out of range, so there is no branch per element.
+    // Token scales (1.0 for partials) are loaded up front; lanes past n_out, tokens past n_tok and
+    // flagged tokens (bit 0 of their scale) store out of range, so there is no branch per element.
+    // fm[0..1] collect the tile's flagged tokens (bit tl) for the exact path after the stores.
+    uint64_t fm[2] = {0ull, 0ull};
     float *ybase = pa.splits == 1 ? pa.y + (size_t)tok0 * pa.n_out
                                   : pa.y + ((size_t)split * a.n_tok + tok0) * pa.n_out;
     const __amdgpu_buffer_rsrc_t ry = ah_rsrc(ybase, ntile * pa.n_out * 4u);
     const __amdgpu_buffer_rsrc_t rt = ah_rsrc(a.tok_scale + tok0, ntile * 4u);
     const bool scaled = pa.splits == 1;
+    // outputs the contract refuses (unsplit parts; a split part's reduction checks its sums): the
+    // store loop only ORs the compare masks (scalar registers); a rare second pass reads this
+    // lane's own stores back (once they are complete, bypassing L1) and records them
+    uint64_t obad = 0ull;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
         uint32_t sc[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] = ah_ld32(rt, 4 * (32 * m + 8 * (r / 4) + 4 * h + (r % 4)));
 #pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            // lanes of half h hold token 32m + 8(r/4) + 4h + r%4
+            const uint64_t b = __builtin_amdgcn_ballot_w64(ah_ts_flagged(sc[r]));
+            const uint32_t tl0 = 32 * m + 8 * (r / 4) + (r % 4);
+            fm[tl0 >> 6] |= (b & 1ull) << (tl0 & 63);
+            fm[(tl0 + 4) >> 6] |= ((b >> 32) & 1ull) << ((tl0 + 4) & 63);
+        }
+#pragma unroll
         for (int n = 0; n < NN; ++n) {
             const uint32_t row = row_w + 32 * n + j;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t tl = 32 * m + 8 * (r / 4) + 4 * h + (r % 4);
-                const bool ok = rl[n] && tl < ntile;
-                const float v = acc[m][n][r] * (scaled ? __builtin_bit_cast(float, sc[r]) : 1.0f);
+                const bool ok = rl[n] && tl < ntile && !ah_ts_flagged(sc[r]);
+                const float v = acc[m][n][r] * (scaled ? ah_ts_value(sc[r]) : 1.0f);
+                obad |= __builtin_amdgcn_ballot_w64(ok && !(__builtin_fabsf(v) < 0x1p31f));
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
                                                       ok ? (tl * pa.n_out + row) * 4u : kOob, 0, 0);
+            }
+        }
+    }
+    if (scaled && obad != 0ull) {
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (uint32_t e = 0; e < 16u * NM * NN; ++e) {
+            const uint32_t m = e / (16 * NN), n = (e / 16) % NN, r = e % 16;
+            const uint32_t tl = 32 * m + 8 * (r / 4) + 4 * h + (r % 4), row = row_w + 32 * n + j;
+            if (!rl[n] || tl >= ntile || ah_ts_flagged(ah_ld32(rt, 4 * tl))) continue;
+            const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, (tl * pa.n_out + row) * 4u, 0, 1));
+            if (const uint32_t oc = ah_out_code(v)) ah_record(a.status, ah_out_key((uint64_t)(tok0 + tl) * pa.n_out + row, oc));
+        }
+    }
+    if ((fm[0] | fm[1]) != 0ull) {
+        // Flagged tokens: this wave's 32 rows, the split's K range, the lane halves taking
+        // alternate units; split partials are stored in the reduction's units (divided by the
+        // token scale, an exact power of two).
+        const uint32_t nb32 = (a.n_in + 31) / 32;
+        const uint32_t u_lo = TYPE == AH_GGML_Q8_0 ? 2 * st_begin : st_begin / 4;
+        uint32_t u_hi = TYPE == AH_GGML_Q8_0 ? 2 * st_end : st_end / 4;
+        if (TYPE == AH_GGML_Q8_0 && u_hi > nb32) u_hi = nb32;
+        const uint32_t row = row_w + j;
+        for (int half = 0; half < 2; ++half) {
+            uint64_t mk = fm[half];
+            while (mk) {
+                const uint32_t tl = 64 * half + (uint32_t)__builtin_ctzll(mk);
+                mk &= mk - 1;
+                const size_t t = (size_t)tok0 + tl;
+                float v = rl[0] ? exact_row<TYPE>(pa.w + rbase[0], a.fcodes + t * a.n_in, a.fscales + t * nb32,
+                                                  a.n_in, u_lo, u_hi, (uint32_t)h)
+                                : 0.0f;
+                v += __shfl_xor(v, 32, 64);
+                const float ts = ah_ts_value(__builtin_bit_cast(uint32_t, a.tok_scale[t]));
+                if (h == 0 && rl[0]) {
+                    ybase[(size_t)tl * pa.n_out + row] = scaled ? v : v / ts;
+                    if (const uint32_t oc = scaled ? ah_out_code(v) : 0u) ah_record(a.status, ah_out_key((uint64_t)t * pa.n_out + row, oc));
+                }
             }
         }
     }
 }
 
 template <int TYPE, int WV, int RG>
-__global__ void __launch_bounds__(64 * WV, 2) gemm_rb_kernel(GemmArgs a) {
+__global__ void __launch_bounds__(64 * WV, TYPE == AH_GGML_Q4_K ? 4 : 2) gemm_rb_kernel(GemmArgs a) {
     __shared__ __align__(16) uint8_t lds[RG * rb::buf_bytes<TYPE>()];
     gemm_rb_body<TYPE, WV, RG>(a, lds);
 }
@@ -600,10 +723,12 @@ struct ReducePart {
 struct ReduceArgs {
     ReducePart p[kReduceMaxParts];
     const float *tok_scale;
+    unsigned long long *status;
     uint64_t total;  // work items over all parts
     uint32_t n_parts, n_tok;
 };
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+AH_DEV float ts_at(const float *ts, size_t i) { return ah_ts_value(__builtin_bit_cast(uint32_t, ts[i])); }
 template <bool VEC>
 __global__ void splitk_reduce(ReduceArgs r) {
     for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < r.total;
@@ -629,11 +754,15 @@ __global__ void splitk_reduce(ReduceArgs r) {
             }
             const size_t e = 4 * li;
             f32x4 o;
-            o.x = s.x * r.tok_scale[e / P.n_out];
-            o.y = s.y * r.tok_scale[(e + 1) / P.n_out];
-            o.z = s.z * r.tok_scale[(e + 2) / P.n_out];
-            o.w = s.w * r.tok_scale[(e + 3) / P.n_out];
+            o.x = s.x * ts_at(r.tok_scale, e / P.n_out);
+            o.y = s.y * ts_at(r.tok_scale, (e + 1) / P.n_out);
+            o.z = s.z * ts_at(r.tok_scale, (e + 2) / P.n_out);
+            o.w = s.w * ts_at(r.tok_scale, (e + 3) / P.n_out);
             reinterpret_cast<f32x4 *>(P.y)[li] = o;
+            const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (const uint32_t oc = ah_out_code(ov[c])) { ah_record(r.status, ah_out_key(e + c, oc)); break; }
         } else {
             float s = 0.0f;
             for (uint32_t z = 0; z < P.splits; z += kReduceBatch) {
@@ -645,7 +774,8 @@ __global__ void splitk_reduce(ReduceArgs r) {
                 for (uint32_t j = 0; j < kReduceBatch; ++j)
                     if (z + j < P.splits) s += v[j];
             }
-            P.y[li] = s * r.tok_scale[li / P.n_out];
+            P.y[li] = s * ts_at(r.tok_scale, li / P.n_out);
+            if (const uint32_t oc = ah_out_code(P.y[li])) ah_record(r.status, ah_out_key(li, oc));
         }
     }
 }
@@ -822,7 +952,8 @@ hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, ui
 
 hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_in,
                           uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xmin,
-                          const float *tok_scale, uint32_t form, hipStream_t stream) {
+                          const float *tok_scale, const int8_t *fcodes, const int64_t *fscales,
+                          unsigned long long *status, uint32_t form, hipStream_t stream) {
     const bool mixed = type == kGemmMixedKQuant;  // Q4_K and Q6_K parts, 4-wave form
     if (n_parts == 0 || n_parts > (mixed ? kGemmMaxParts : rb::max_parts_of(type))) return hipErrorInvalidValue;
     if (mixed || type == AH_GGML_Q4_K || form > kForm2x4) form = kForm4x4;
@@ -835,6 +966,9 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     a.xh = xh;
     a.xmin = xmin;
     a.tok_scale = tok_scale;
+    a.fcodes = fcodes;
+    a.status = status;
+    a.fscales = fscales;
     uint32_t wg = 0;
     for (uint32_t i = 0; i < kGemmMaxParts; ++i) {
         GemmPartArgs &P = a.p[i];
@@ -882,11 +1016,12 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
 
 // One reduction launch for every part with splits > 1 (kReduceMaxParts per launch).
 hipError_t ah_launch_splitk_reduce(uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_tok,
-                                   const float *tok_scale, hipStream_t stream) {
+                                   const float *tok_scale, unsigned long long *status, hipStream_t stream) {
     uint32_t i = 0;
     while (i < n_parts) {
         ReduceArgs r;
         r.tok_scale = tok_scale;
+        r.status = status;
         r.n_tok = n_tok;
         r.n_parts = 0;
         bool vec = true;

@@ -177,7 +177,19 @@ AH_DEV QuadOut quad_quant(const QuadIn &in, uint32_t src, uint32_t b, unsigned l
         o.s16 = s8 + (int)quad_xor1((uint32_t)s8);
         o.s32 = o.s16 + (int)quad_xor2((uint32_t)o.s16);
         o.e = 0;
-        o.fsc = (float)(int64_t)(((uint64_t)in.s1 << 32) | in.s0) * 0x1p-32f;
+        const int64_t S = (int64_t)(((uint64_t)in.s1 << 32) | in.s0);
+        o.fsc = (float)S * 0x1p-32f;
+        // QuantAct::dequantizes (chart/mod.rs:128-134): every S * code must be an i64, else the
+        // call refuses with Dequant(FixedOverflow) before it projects
+        bool bad = false;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            int64_t prod;
+            bad |= __builtin_mul_overflow(S, (int64_t)(int8_t)((((i < 4) ? o.c0 : o.c1) >> (8 * (i & 3))) & 0xffu), &prod);
+        }
+        const uint32_t badq = (uint32_t)bad | quad_xor1((uint32_t)bad);
+        if ((badq | quad_xor2(badq)) != 0 && q == 0)
+            ah_record(status, AH_QUANT_ORDER_BASE + (((key_base >> 5) + b) << 8) + 7u);
         return o;
     }
     uint32_t bits[8];
@@ -563,7 +575,11 @@ __global__ void __launch_bounds__(kThreads)
             for (uint32_t i = gl; i < U; i += G) sum += A.red[r * U + i];
         for (uint32_t o = 1; o < G; o <<= 1) sum += __shfl_xor(sum, (int)o, 64);
         const uint32_t row = tile * R + r;
-        if (r < R && gl == 0 && row < P.n_out) P.y[row] = sum;
+        if (r < R && gl == 0 && row < P.n_out) {
+            P.y[row] = sum;
+            const uint32_t oc = ah_out_code(sum);
+            if (oc) ah_record(status, ah_out_key(row, oc));
+        }
     }
 }
 
@@ -594,6 +610,14 @@ AH_DEV int wave_max(int v) {
     for (int o = 1; o < 64; o <<= 1) {
         const int t = __shfl_xor(v, o, 64);
         v = t > v ? t : v;
+    }
+    return v;
+}
+AH_DEV int wave_min(int v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_xor(v, o, 64);
+        v = t < v ? t : v;
     }
     return v;
 }
@@ -641,7 +665,7 @@ template <uint32_t SRC, uint32_t R, uint32_t T>
 __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
     static_assert(SRC == AH_SRC_F32 || SRC == AH_SRC_CODES, "the GEMM takes f32 or code inputs");
     constexpr uint32_t kOpBlocks = T / 4;  // blocks per round
-    __shared__ uint32_t red[T / 64];
+    __shared__ uint32_t red[T / 64], redn[T / 64];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = tid & 3;
     const uint32_t tok = blockIdx.x;
     const size_t row = (size_t)tok * o.n_in;
@@ -663,7 +687,8 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
     }
     uint32_t c0[R], c1[R];
     int ex[R], sum[R];
-    int emax = -1;
+    int emax = -1, emin = 64;  // largest block exponent, smallest of a nonzero block
+    bool odd = false;          // a codes scale that is not a power of two
 #pragma unroll
     for (uint32_t u = 0; u < R; ++u) {
         if (u * kOpBlocks + wb0 >= nbp) break;
@@ -673,6 +698,9 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
         if (SRC == AH_SRC_CODES) {
             const uint64_t S = ((uint64_t)in[u].s1 << 32) | in[u].s0;
             e = (int64_t)S > 0 ? 63 - __builtin_clzll(S) : -1;
+            // a QuantAct built by hand may hold any i64 scale: one that is not 0 or a power of
+            // two has no exact f16 operand, so the token takes the exact path
+            if (S != 0 && ((int64_t)S < 0 || (S & (S - 1)) != 0)) { e = 0; odd = true; }
         }
         if (b >= nbp) e = -1;
         c0[u] = qo.c0;
@@ -680,15 +708,44 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
         ex[u] = e;
         sum[u] = qo.s32;
         emax = e > emax ? e : emax;
+        emin = e >= 0 && e < emin ? e : emin;
     }
     emax = wave_max(emax);
-    if (lane == 0) red[wave] = (uint32_t)(emax + 1);
+    emin = wave_min(odd ? -1000 : emin);  // below any band: the token is flagged
+    if (lane == 0) {
+        red[wave] = (uint32_t)(emax + 1);
+        redn[wave] = (uint32_t)emin;
+    }
     __syncthreads();
-    int E = -1;
+    int E = -1, Emin = 64;
 #pragma unroll
-    for (uint32_t w = 0; w < T / 64; ++w) E = (int)red[w] - 1 > E ? (int)red[w] - 1 : E;
+    for (uint32_t w = 0; w < T / 64; ++w) {
+        E = (int)red[w] - 1 > E ? (int)red[w] - 1 : E;
+        Emin = (int)redn[w] < Emin ? (int)redn[w] : Emin;
+    }
     if (E > 62) E = 62;  // a block without a Q32.32 scale: the call is refused anyway
-    if (tid == 0) o.tok_scale[tok] = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
+    // a nonzero block below the f16 band: the GEMM serves this token exactly from its codes
+    const bool flagged = Emin < E - kF16Band;
+    if (tid == 0) {
+        const float ts = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
+        o.tok_scale[tok] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, ts) | (flagged ? 1u : 0u));
+    }
+    if (SRC == AH_SRC_F32 && flagged) {
+        // keep the token's QuantAct for the exact path (uniform branch: one workgroup per token)
+        int8_t *fc = o.fcodes + row;
+        int64_t *fs = o.fscales + (size_t)tok * o.nb32;
+#pragma unroll
+        for (uint32_t u = 0; u < R; ++u) {
+            if (u * kOpBlocks + wb0 >= nbp) break;
+            const uint32_t b = u * kOpBlocks + tid / 4;
+            if (b >= o.nb32) continue;
+            const uint32_t k0 = 32 * b + 8 * q;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (k0 + i < o.n_in) fc[k0 + i] = (int8_t)(((i < 4 ? c0[u] : c1[u]) >> (8 * (i & 3))) & 0xffu);
+            if (q == 0) fs[b] = ex[u] < 0 ? 0 : (int64_t)(1ull << ex[u]);
+        }
+    }
     _Float16 *xh = o.xh + (size_t)tok * o.kpad;
 #pragma unroll
     for (uint32_t u = 0; u < R; ++u) {
@@ -713,19 +770,17 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
     }
 }
 
-// Device-side f16 scale scan of a payload: flags any Inf/NaN d / dmin word.
+// Device-side f16 scale scan of a payload: records the earliest Inf/NaN d / dmin word as
+// (block << 17) | (dmin << 16) | bits.
 __global__ void scan_scales_kernel(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes,
-                                   uint32_t off0, uint32_t off1, int *bad) {
+                                   uint32_t off0, uint32_t off1, unsigned long long *bad) {
     for (uint64_t b = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; b < n_blocks;
          b += (uint64_t)gridDim.x * blockDim.x) {
         const uint8_t *p = w + b * block_bytes;
-        uint32_t h0 = p[off0] | (p[off0 + 1] << 8);
-        bool nf = ((h0 >> 10) & 0x1f) == 0x1f;
-        if (off1 != off0) {
-            uint32_t h1 = p[off1] | (p[off1 + 1] << 8);
-            nf |= ((h1 >> 10) & 0x1f) == 0x1f;
-        }
-        if (nf) atomicOr(bad, 1);
+        const uint32_t h0 = p[off0] | (p[off0 + 1] << 8);
+        const uint32_t h1 = off1 != off0 ? (uint32_t)(p[off1] | (p[off1 + 1] << 8)) : 0u;
+        if (((h0 >> 10) & 0x1f) == 0x1f) atomicMin(bad, (b << 17) | h0);
+        else if (((h1 >> 10) & 0x1f) == 0x1f) atomicMin(bad, (b << 17) | (1ull << 16) | h1);
     }
 }
 
@@ -899,6 +954,9 @@ __global__ void __launch_bounds__(kSThreads, 4)
     // its completion before the next tile is staged.
     const __amdgpu_buffer_rsrc_t ry = ah_rsrc(P.y, P.n_out * 4u);
     const uint32_t r = lane / G, g = lane & (G - 1);
+    // earliest refused output row of the wave, (row << 1) | (code == 9), kept in a scalar register
+    // (a ballot, no memory operation in the loop); recorded once after the last tile
+    uint32_t obad = 0xFFFFFFFFu;
     for (uint32_t t = 0; t < n_t; ++t) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS stores have landed
         __builtin_amdgcn_wave_barrier();
@@ -931,9 +989,16 @@ __global__ void __launch_bounds__(kSThreads, 4)
         acc = group_sum(acc, G);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), ry,
                                               (g == 0 && owns) ? row * 4u : kOob, 0, 0);
+        const uint32_t oc = ah_out_code(acc);
+        const uint64_t ob = __builtin_amdgcn_ballot_w64(g == 0 && owns && oc != 0u);
+        if (ob) {  // uniform: lanes own rows in lane order, so the lowest lane is the earliest row
+            const uint32_t k = __builtin_amdgcn_readlane((row << 1) | (oc == 9u ? 1u : 0u), (int)__builtin_ctzll(ob));
+            obad = k < obad ? k : obad;
+        }
         __builtin_amdgcn_wave_barrier();  // all lanes are done reading the slot before it is refilled
         stage(t + 1);
     }
+    if (obad != 0xFFFFFFFFu && lane == 0) ah_record(status, ah_out_key(obad >> 1, (obad & 1u) ? 9u : 8u));
 }
 
 // Stream geometry for a row of RB bytes and U units: whole rows per tile and lanes per row.
@@ -1135,7 +1200,7 @@ hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream) {
 }
 
 hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes,
-                          uint32_t off0, uint32_t off1, int *d_bad, hipStream_t stream) {
+                          uint32_t off0, uint32_t off1, unsigned long long *d_bad, hipStream_t stream) {
     if (n_blocks == 0) return hipSuccess;
     uint64_t grid = (n_blocks + 255) / 256;
     if (grid > 4096) grid = 4096;

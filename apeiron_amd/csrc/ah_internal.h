@@ -22,9 +22,27 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 // f32 vector before quant_act runs.
 #define AH_ST_NONE 0xFFFFFFFFFFFFFFFFull
 #define AH_QUANT_ORDER_BASE (1ull << 48)
+// Output refusals come after every input refusal of the call (the reference converts and
+// quantizes before it projects) and are ordered by output index (token-major for the GEMM, as
+// matmat_q8act reports its first failing column).
+#define AH_OUTPUT_ORDER_BASE (1ull << 56)
 
 AH_DEV void ah_record(unsigned long long *st, unsigned long long key) {
     if (st) atomicMin(st, key);
+}
+
+// The refusal the exact contract makes for an output of real value y (ops/matvec.rs:35-37,
+// 113-115): the i128 sum of Q32.32 products is y * 2^64, so |y| >= 2^63 leaves i128
+// (AccumulatorOverflow, 8); round_shift_32 of it is y * 2^32, so |y| >= 2^31 leaves i64
+// (OutputOverflow, 9).  A NaN (an f32 fold that overflowed both ways) counts as the former.
+// Values within the f32 fold's tolerance of either bound may be classed either way.
+AH_DEV uint32_t ah_out_code(float y) {
+    const float a = __builtin_fabsf(y);
+    return !(a < 0x1p63f) ? 8u : a >= 0x1p31f ? 9u : 0u;
+}
+AH_DEV unsigned long long ah_out_key(uint64_t index, uint32_t code) {
+    const uint64_t i = index < (1ull << 47) ? index : (1ull << 47) - 1;
+    return AH_OUTPUT_ORDER_BASE + (i << 8) + code;
 }
 
 // ---- buffer resources: range-checked loads (out-of-range lanes read 0, never fault) ----
@@ -216,14 +234,26 @@ struct QuantArgs {
 };
 
 // GEMM activation operand built from a QuantAct: xh[tok][kpad] f16 = xq * 2^(e_b - E_tok) (exact
-// when e_b - E_tok >= -24), tok_scale[tok] = 2^(E_tok - 32), and for Q4_K the min-term operand
-// xmin[tok][kpad/256][16] (split sub-block code sums, see ah_gemm.hip).
+// when e_b - E_tok >= -kF16Band), tok_scale[tok] = 2^(E_tok - 32), and for Q4_K the min-term
+// operand xmin[tok][kpad/256][16] (split sub-block code sums, see ah_gemm.hip).
+//
+// A token with a nonzero block below the band (e_b - E_tok < -kF16Band) cannot be carried exactly
+// by the f16 operand.  The pass flags it in the lowest mantissa bit of its tok_scale (a power of
+// two, so that bit is otherwise 0; readers take the value with ah_ts_value) and, for f32 input,
+// keeps its codes and scales (fcodes / fscales rows, written for flagged tokens only).  The GEMM
+// then serves flagged tokens from those with exact integer group dots and f32 power-of-two scales,
+// as the GEMV does, instead of the MFMA.
+constexpr int kF16Band = 24;
+AH_DEV float ah_ts_value(uint32_t bits) { return __builtin_bit_cast(float, bits & ~1u); }
+AH_DEV bool ah_ts_flagged(uint32_t bits) { return (bits & 1u) != 0; }
 struct OperandArgs {
     const void *x;         // f32 / Q32.32 int64 [n_tok][n_in], or int8 codes with `scales`
     const int64_t *scales; // [n_tok][nb32] with AH_SRC_CODES
     _Float16 *xh;          // [n_tok][kpad]
-    float *tok_scale;      // [n_tok]
+    float *tok_scale;      // [n_tok] (bit 0: flagged)
     _Float16 *xmin;        // [n_tok][kpad/256][16] for Q4_K, else nullptr
+    int8_t *fcodes;        // [n_tok][n_in] (f32 input only; flagged rows written)
+    int64_t *fscales;      // [n_tok][nb32] (f32 input only; flagged rows written)
     unsigned long long *status;
     uint32_t n_tok, n_in, nb32, kpad, src;
 };

@@ -77,6 +77,10 @@ int32_t ah_destroy(ah_ctx *ctx);
 const char *ah_status_str(int32_t status);
 /* The last HIP error the context saw (hipError_t as int), for diagnostics. */
 int32_t ah_last_hip_error(const ah_ctx *ctx);
+/* The f16 bit pattern of the first non-finite block scale (row order; d before dmin) behind the
+ * context's most recent AH_ERR_NONFINITE_SCALE: the `bits` of the reference's
+ * EngineError::NonFiniteScale { bits } (num/dequant.rs:25-41). */
+int32_t ah_last_refusal_bits(const ah_ctx *ctx, uint32_t *bits);
 
 /* ---- weights -------------------------------------------------------------------------------- */
 
@@ -178,8 +182,16 @@ int32_t ah_probe_mfma_peak(ah_ctx *ctx, uint32_t kind, double *tera_ops);
 /* ---- status ---- */
 
 /* Synchronize `stream` and return (then clear) the first data-dependent refusal recorded by
- * kernels since the last call: AH_ERR_NONFINITE_INPUT, AH_ERR_INPUT_RANGE or
- * AH_ERR_FIXED_OVERFLOW, else AH_OK (or AH_ERR_HIP if the stream faulted). */
+ * kernels since the last call, else AH_OK (or AH_ERR_HIP if the stream faulted).  In the
+ * reference's order: input conversion (AH_ERR_NONFINITE_INPUT, AH_ERR_INPUT_RANGE, earliest
+ * element), then quantization (AH_ERR_FIXED_OVERFLOW: quant_act's None, or a pre-quantized
+ * QuantAct that fails dequantizes, chart/mod.rs:128-134), then the outputs (earliest token, then
+ * row): AH_ERR_ACCUMULATOR_OVERFLOW where |y| >= 2^63 (the exact sum y * 2^64 leaves i128,
+ * ops/matvec.rs:35-37) and AH_ERR_OUTPUT_OVERFLOW where |y| >= 2^31 (round_shift_32 leaves i64,
+ * ops/matvec.rs:113-115).  Outputs are classified from the f32 result, so a value within the
+ * f32 fold's tolerance of either bound may be classed either way; and an i128 partial sum that
+ * overflows and cancels back into range (a refusal of the reference's sequential checked sum)
+ * is not seen. */
 int32_t ah_sync_status(ah_ctx *ctx, void *stream);
 
 /* ---- host convenience forms (synchronous; copy in and out) ---- */

@@ -42,6 +42,16 @@ def gemm_asm(tmp_path_factory):
     return out.read_text().split("\n")
 
 
+def skipped_by_execz(body, i, label):
+    """Instructions a forward `s_cbranch_execz label` at body[i] jumps over (none for a backward
+    branch: a loop's back edge skips nothing after it)."""
+    labels = {l[:-1]: j for j, l in enumerate(body) if l.endswith(":") and not l.startswith(";")}
+    tgt = labels.get(label)
+    if tgt is None or tgt < i:
+        return []
+    return body[i + 1:tgt]
+
+
 def kernels(lines):
     for i, l in enumerate(lines):
         m = re.match(r"^(_ZN12_GLOBAL__N_114gemm_rb_kernelILi(\d+)ELi(\d+)ELi(\d+)E\S*):", l)
@@ -83,10 +93,8 @@ def test_mixed_kquant_kernel_barriers(gemm_asm):
                 assert int(m.group(1)) == want, body[i - 1]
         m = re.match(r"s_cbranch_execz\s+(\S+)", l)
         if m:
-            for j in range(i + 1, len(body)):
-                if body[j].startswith(m.group(1) + ":"):
-                    break
-                assert not (body[j].startswith("buffer_load") and body[j].endswith(" lds")), body[j]
+            for x in skipped_by_execz(body, i, m.group(1)):
+                assert not (x.startswith("buffer_load") and x.endswith(" lds")), x
     assert ring >= 8, ring  # four stages in each body
 
 
@@ -100,10 +108,8 @@ def test_no_slice_load_can_be_skipped(gemm_asm):
             m = re.match(r"s_cbranch_execz\s+(\S+)", l)
             if not m:
                 continue
-            for j in range(i + 1, len(body)):
-                if body[j].startswith(m.group(1) + ":"):
-                    break
-                assert not is_slice(body[j]), (TYPES[t], waves, slots, j, body[j])
+            for x in skipped_by_execz(body, i, m.group(1)):
+                assert not is_slice(x), (TYPES[t], waves, slots, i, x)
 
 
 @pytest.fixture(scope="module")

@@ -15,7 +15,7 @@ STATUS = {
     0: "ok", 1: "ShapeMismatch", 2: "RowLength", 3: "ShortPayload", 4: "LengthOverflow",
     5: "UnsupportedQuant", 6: "NonFiniteScale", 7: "FixedOverflow", 8: "AccumulatorOverflow",
     9: "OutputOverflow", 10: "NonFiniteInput", 11: "InputRange", 20: "NoDevice",
-    21: "InvalidArg", 22: "Hip", 23: "OutOfMemory",
+    21: "InvalidArg", 22: "Hip", 23: "OutOfMemory", 24: "ScratchLimit",
 }
 
 # Every symbol include/apeiron_hip.h declares.
@@ -26,7 +26,7 @@ EXPORTS = [
     "ah_gemv_plan_run", "ah_gemv_plan_free", "ah_gemm_f32_dev", "ah_gemm_q8_dev",
     "ah_gemv_q8_dots_dev", "ah_sync_status", "ah_matvec_q8act", "ah_matmat_q8act",
     "ah_quant_act", "ah_probe_mfma_peak", "ah_gemm_group_f32_dev", "ah_gemm_group_q8_dev",
-    "ah_last_refusal_bits",
+    "ah_last_refusal_bits", "ah_gemm_f32_noalloc_dev", "ah_gemm_noalloc_scratch_bytes",
 ]
 
 _lib = None
@@ -66,6 +66,8 @@ def load() -> ctypes.CDLL:
         "ah_gemv_plan_run": (I32, [P, P, P]),
         "ah_gemv_plan_free": (I32, [P, P]),
         "ah_gemm_f32_dev": (I32, [P, P, P, S, P, P]),
+        "ah_gemm_f32_noalloc_dev": (I32, [P, P, P, S, P, P]),
+        "ah_gemm_noalloc_scratch_bytes": (I32, [ctypes.POINTER(S)]),
         "ah_gemm_q8_dev": (I32, [P, P, P, P, S, P, P]),
         "ah_sync_status": (I32, [P, P]),
         "ah_matvec_q8act": (I32, [P, P, P, P, S, P]),

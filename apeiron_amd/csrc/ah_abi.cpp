@@ -47,8 +47,16 @@ hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream);
 hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, uint32_t *d_sink,
                          hipStream_t stream, double *tops);
 
+// Scratch of ah_gemm_f32_noalloc_dev: device memory the library holds on every GPU it runs on
+// until the process ends (a static device array: no allocation per call).  In host code
+// `scratch` only names the symbol; its device address is resolved once per context by ah_init
+// (hipGetSymbolAddress with the context's device current) and kept in ah_ctx::noalloc.
+constexpr size_t kNoAllocScratchBytes = 64ull << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 struct ah_ctx {
     int device = -1;
+    uint8_t *noalloc = nullptr;  // this device's copy of `scratch`
     hipStream_t stream = nullptr;
     unsigned long long *d_status = nullptr;
     int last_hip = 0;
@@ -415,9 +423,13 @@ int32_t reset_status(ah_ctx *ctx) {
 // for every part that splits.  Each part keeps the split count it would get alone, so its outputs
 // are those of its single-projection call bit for bit.  All parts share n_in; types and n_out may
 // differ.  A single projection is the group of one.
+// `fixed` (with `fixed_cap` bytes) replaces the context's growable scratch: the call then neither
+// allocates nor frees anything (device or host, for up to kStackParts parts), and refuses with
+// AH_ERR_SCRATCH_LIMIT when its operands and partials need more than `fixed_cap`.
+constexpr size_t kStackParts = 16;
 int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w, uint32_t src,
                           const void *x, const int64_t *scales_in, size_t n_tok, float *const *y,
-                          void *stream) {
+                          void *stream, uint8_t *fixed = nullptr, size_t fixed_cap = 0) {
     if (!ctx || !w || !y || n_parts == 0 || n_parts > 65536 || !w[0]) return AH_ERR_INVALID_ARG;
     const size_t n_in_sz = w[0]->n_in;
     bool any_q4k = false;
@@ -435,8 +447,17 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     const uint32_t cus = (uint32_t)ctx->cu_count;
     // every split part has its own partials region: the parts of a launch run together and the
     // reduction reads them all at the end
-    std::vector<GemmPartDesc> pd(n_parts);
-    std::vector<size_t> part_off(n_parts, 0);
+    GemmPartDesc pd_stack[kStackParts];
+    size_t off_stack[kStackParts] = {};
+    std::vector<GemmPartDesc> pd_heap;
+    std::vector<size_t> off_heap;
+    if (n_parts > kStackParts) {
+        if (fixed) return AH_ERR_INVALID_ARG;
+        pd_heap.resize(n_parts);
+        off_heap.assign(n_parts, 0);
+    }
+    GemmPartDesc *pd = n_parts > kStackParts ? pd_heap.data() : pd_stack;
+    size_t *part_off = n_parts > kStackParts ? off_heap.data() : off_stack;
     size_t part_bytes = 0;
     for (size_t i = 0; i < n_parts; ++i) {
         GemmPartDesc &d = pd[i];
@@ -463,9 +484,14 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     const size_t o_fc = off; off = align256(off + (keep ? (size_t)N * n_in : 0));
     const size_t o_fs = off; off = align256(off + (keep ? (size_t)N * nb32 * 8 : 0));
     const size_t o_part = off; off = align256(off + part_bytes);
-    int32_t st = ensure_scratch(ctx, off);
-    if (st) return st;
-    uint8_t *S = static_cast<uint8_t *>(ctx->scratch);
+    uint8_t *S = fixed;
+    if (fixed) {
+        if (off > fixed_cap) return AH_ERR_SCRATCH_LIMIT;
+    } else {
+        const int32_t st = ensure_scratch(ctx, off);
+        if (st) return st;
+        S = static_cast<uint8_t *>(ctx->scratch);
+    }
     _Float16 *xh = reinterpret_cast<_Float16 *>(S + o_xh);
     float *ts = reinterpret_cast<float *>(S + o_ts);
     _Float16 *xmin = reinterpret_cast<_Float16 *>(S + o_xmin);
@@ -532,7 +558,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         const uint32_t form = type == kGemmMixedKQuant ? kForm4x4 : ah_gemm_pick_waves(type, wg4, cus);
         AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xmin, ts, fcodes, fscales, ctx->d_status, form, s));
     }
-    if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd.data(), N, ts, ctx->d_status, s));
+    if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd, N, ts, ctx->d_status, s));
     return AH_OK;
 }
 
@@ -565,6 +591,7 @@ const char *ah_status_str(int32_t s) {
     case AH_ERR_INVALID_ARG: return "invalid argument";
     case AH_ERR_HIP: return "hip error";
     case AH_ERR_OUT_OF_MEMORY: return "out of device memory";
+    case AH_ERR_SCRATCH_LIMIT: return "call needs more than the fixed scratch of the no-alloc entry point";
     default: return "unknown status";
     }
 }
@@ -587,12 +614,16 @@ int32_t ah_init(int32_t device, ah_ctx **out) {
         delete ctx;
         return AH_ERR_HIP;
     }
-    if (reset_status(ctx) != AH_OK) {
+    void *sp = nullptr;
+    const hipError_t se = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));  // this device's copy
+    if (se != hipSuccess || !sp || reset_status(ctx) != AH_OK) {
+        ctx->last_hip = (int)se;
         (void)hipFree(ctx->d_status);
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return AH_ERR_HIP;
     }
+    ctx->noalloc = static_cast<uint8_t *>(sp);
     *out = ctx;
     return AH_OK;
 }
@@ -944,6 +975,21 @@ int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan) {
 int32_t ah_gemm_f32_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, size_t n_tok, float *d_y,
                         void *stream) {
     return gemm_launch(ctx, w, AH_SRC_F32, d_x, nullptr, n_tok, d_y, stream);
+}
+
+int32_t ah_gemm_f32_noalloc_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, size_t n_tok,
+                                float *d_y, void *stream) {
+    if (!ctx || !w || !d_y || (!d_x && n_tok && w->n_in)) return AH_ERR_INVALID_ARG;
+    if (n_tok == 0 || w->n_out == 0) return AH_OK;
+    if (!ctx->noalloc) return AH_ERR_HIP;
+    return gemm_group_launch(ctx, 1, &w, AH_SRC_F32, d_x, nullptr, n_tok, &d_y, stream, ctx->noalloc,
+                             kNoAllocScratchBytes);
+}
+
+int32_t ah_gemm_noalloc_scratch_bytes(size_t *bytes) {
+    if (!bytes) return AH_ERR_INVALID_ARG;
+    *bytes = kNoAllocScratchBytes;
+    return AH_OK;
 }
 
 int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes, const int64_t *d_scales,

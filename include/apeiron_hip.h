@@ -55,6 +55,7 @@ extern "C" {
 #define AH_ERR_INVALID_ARG 21         /* null pointer / bad handle / limits exceeded       */
 #define AH_ERR_HIP 22                 /* a HIP runtime call failed                         */
 #define AH_ERR_OUT_OF_MEMORY 23
+#define AH_ERR_SCRATCH_LIMIT 24       /* a no-alloc call needs more than its fixed scratch  */
 
 /* ggml type ids (format/quant.rs:20-49) */
 #define AH_GGML_Q8_0 8
@@ -145,6 +146,19 @@ int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan);
  * context must not overlap (use one context per stream for concurrent prefills). */
 int32_t ah_gemm_f32_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, size_t n_tok,
                         float *d_y, void *stream);
+/* ah_gemm_f32_dev that allocates nothing.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The call calls no hipMalloc/hipFree or other allocating
+ * routine; its operand and split-K scratch is a 64 MiB static device array the library holds on
+ * each GPU until the process ends (ah_gemm_noalloc_scratch_bytes reports the size), and a call
+ * that needs more refuses with AH_ERR_SCRATCH_LIMIT before it enqueues anything (at K = 8960,
+ * N = 512 it needs about 40 MiB).  Every call on one GPU shares that array and each call writes
+ * every scratch byte it reads, so nothing carries over between calls; calls that overlap on one
+ * GPU (other streams, other contexts, other threads) race on it and must be serialised by the
+ * caller.  Results equal ah_gemm_f32_dev's bit for bit. */
+int32_t ah_gemm_f32_noalloc_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, size_t n_tok,
+                                float *d_y, void *stream);
+int32_t ah_gemm_noalloc_scratch_bytes(size_t *bytes);
 /* Same from pre-quantized codes[n_tok][n_in] + scales[n_tok][ceil(n_in/32)]. */
 int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
                        const int64_t *d_scales, size_t n_tok, float *d_y, void *stream);

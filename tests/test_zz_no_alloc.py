@@ -1,0 +1,66 @@
+"""ah_gemm_f32_noalloc_dev (the GEMM entry point that allocates nothing) against ah_gemm_f32_dev,
+through the C ABI: bit-identical outputs on two calls in a row, the second with a smaller input
+(its fixed scratch keeps the first call's contents), and a clear refusal past its scratch."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from apeiron_amd import chart, synth
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    d = chart.Device(0)
+    yield d
+    d.close()
+
+
+def run(dev, fn, w, x):
+    n_tok = x.shape[0]
+    y = torch.full((n_tok, w.n_out), float("nan"), dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    st = fn(dev.h, w.h, x.data_ptr(), n_tok, y.data_ptr(), s)
+    assert st == 0, chart._lib.STATUS.get(st, st)
+    assert dev.sync_status(s) == 0
+    return y
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+def test_noalloc_gemm_equals_gemm(dev, t):
+    L = dev.lib
+    cap = ctypes.c_size_t(0)
+    assert L.ah_gemm_noalloc_scratch_bytes(ctypes.byref(cap)) == 0 and cap.value == 64 << 20
+    rng = synth.rng_for(7, t)
+    # a split-K shape at N = 512 (partials in the scratch), then a smaller call on another weight
+    shapes = [(1536, 8960, 512), (300, 896, 37)]
+    outs = []
+    for n_out, n_in, n_tok in shapes:
+        raw = synth.payload(t, rng, n_out, n_in)
+        w = dev.upload(t, raw, n_out, n_in)
+        x = torch.from_numpy(synth.activations(rng, n_in, n_tok).reshape(n_tok, n_in)).cuda()
+        x[n_tok // 2] *= torch.exp2(torch.arange(n_in, device="cuda") // 32 * 40.0 / (n_in // 32) - 20)
+        y_na = run(dev, L.ah_gemm_f32_noalloc_dev, w, x)
+        y_ref = run(dev, L.ah_gemm_f32_dev, w, x)
+        assert torch.equal(y_na, y_ref), (t, n_out, n_in, n_tok)
+        outs.append((w, x, y_na))
+    # the first shape again after the smaller call: same result
+    w, x, y0 = outs[0]
+    assert torch.equal(run(dev, L.ah_gemm_f32_noalloc_dev, w, x), y0)
+    for w, _, _ in outs:
+        w.free()
+
+
+def test_noalloc_gemm_refuses_past_its_scratch(dev):
+    rng = synth.rng_for(7, 99)
+    n_out, n_in, n_tok = 64, 8960, 4096  # operands alone: 4096 * 8960 * 3 bytes > 64 MiB
+    w = dev.upload(8, synth.payload(8, rng, n_out, n_in), n_out, n_in)
+    x = torch.zeros((n_tok, n_in), dtype=torch.float32, device="cuda")
+    y = torch.zeros((n_tok, n_out), dtype=torch.float32, device="cuda")
+    st = dev.lib.ah_gemm_f32_noalloc_dev(dev.h, w.h, x.data_ptr(), n_tok, y.data_ptr(), None)
+    assert st == 24  # AH_ERR_SCRATCH_LIMIT, before anything is enqueued
+    w.free()

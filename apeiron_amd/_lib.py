@@ -15,7 +15,8 @@ STATUS = {
     0: "ok", 1: "ShapeMismatch", 2: "RowLength", 3: "ShortPayload", 4: "LengthOverflow",
     5: "UnsupportedQuant", 6: "NonFiniteScale", 7: "FixedOverflow", 8: "AccumulatorOverflow",
     9: "OutputOverflow", 10: "NonFiniteInput", 11: "InputRange", 20: "NoDevice",
-    21: "InvalidArg", 22: "Hip", 23: "OutOfMemory", 24: "ScratchLimit",
+    12: "FfnOverflow", 13: "ExpOutOfRange", 14: "ZeroDenominator",
+    21: "InvalidArg", 22: "Hip", 23: "OutOfMemory", 24: "ScratchLimit", 25: "SeqTimeout",
 }
 
 # Every symbol include/apeiron_hip.h declares.
@@ -27,11 +28,21 @@ EXPORTS = [
     "ah_gemv_q8_dots_dev", "ah_sync_status", "ah_matvec_q8act", "ah_matmat_q8act",
     "ah_quant_act", "ah_probe_mfma_peak", "ah_gemm_group_f32_dev", "ah_gemm_group_q8_dev",
     "ah_last_refusal_bits", "ah_gemm_f32_noalloc_dev", "ah_gemm_noalloc_scratch_bytes",
+    "ah_seq_create", "ah_seq_run", "ah_seq_sync_status", "ah_seq_free", "ah_seq_info",
 ]
 
 _lib = None
 
 P = ctypes.c_void_p
+
+
+class SeqStage(ctypes.Structure):
+    """struct ah_seq_stage of include/apeiron_hip.h."""
+    _fields_ = [("kind", ctypes.c_uint32), ("n_parts", ctypes.c_size_t), ("w", ctypes.c_void_p),
+                ("x", ctypes.c_void_p), ("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("y", ctypes.c_void_p), ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p),
+                ("n", ctypes.c_size_t), ("h_codes", ctypes.c_void_p), ("h_scales", ctypes.c_void_p)]
+
 S = ctypes.c_size_t
 I32 = ctypes.c_int32
 U32 = ctypes.c_uint32
@@ -76,6 +87,11 @@ def load() -> ctypes.CDLL:
         "ah_probe_mfma_peak": (I32, [P, U32, ctypes.POINTER(ctypes.c_double)]),
         "ah_gemm_group_f32_dev": (I32, [P, S, P, P, S, P, P]),
         "ah_gemm_group_q8_dev": (I32, [P, S, P, P, P, S, P, P]),
+        "ah_seq_create": (I32, [P, S, P, ctypes.POINTER(P)]),
+        "ah_seq_run": (I32, [P, P, P]),
+        "ah_seq_sync_status": (I32, [P, P, P, ctypes.POINTER(U32)]),
+        "ah_seq_free": (I32, [P, P]),
+        "ah_seq_info": (I32, [P, ctypes.POINTER(U32), ctypes.POINTER(U32)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

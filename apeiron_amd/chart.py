@@ -207,6 +207,58 @@ class GemvPlan:
             self.h = None
 
 
+class Seq:
+    """A persistent decode sequence (ah_seq_*): stages run in order in ONE launch, each reading
+    outputs of the stages before it.  A stage is ``("gemv", parts)`` with parts a list of
+    ``(tensor, x_ptr, y_ptr)`` (f32 input) or ``(tensor, (codes_ptr, scales_ptr), y_ptr)``
+    (a QuantAct, e.g. a SwiGLU stage's output), or ``("swiglu", gate_ptr, up_ptr, n, codes_ptr,
+    scales_ptr)``: the fused FFN's hidden activation (chart/ffn.rs:1532-1594)."""
+
+    def __init__(self, dev: Device, stages: list):
+        n = len(stages)
+        arr = (_lib.SeqStage * n)()
+        self.keep = []
+        for i, st in enumerate(stages):
+            S = arr[i]
+            if st[0] == "swiglu":
+                _, gate, up, width, codes, scales = st
+                S.kind, S.gate, S.up, S.n, S.h_codes, S.h_scales = 1, gate, up, width, codes, scales
+                continue
+            parts = st[1]
+            k = len(parts)
+            W = (ctypes.c_void_p * k)(*[p[0].h.value for p in parts])
+            X = (ctypes.c_void_p * k)(*[p[1] if isinstance(p[1], int) else None for p in parts])
+            C = (ctypes.c_void_p * k)(*[p[1][0] if not isinstance(p[1], int) else None for p in parts])
+            Sc = (ctypes.c_void_p * k)(*[p[1][1] if not isinstance(p[1], int) else None for p in parts])
+            Y = (ctypes.c_void_p * k)(*[p[2] for p in parts])
+            self.keep += [W, X, C, Sc, Y, [p[0] for p in parts]]
+            S.kind, S.n_parts = 0, k
+            S.w, S.x, S.codes, S.scales, S.y = (ctypes.cast(a, ctypes.c_void_p) for a in (W, X, C, Sc, Y))
+        h = ctypes.c_void_p()
+        _check(dev.lib.ah_seq_create(dev.h, n, ctypes.cast(arr, ctypes.c_void_p), ctypes.byref(h)), "seq_create")
+        self.dev, self.h = dev, h
+
+    def run(self, stream: int | None = None) -> None:
+        _check(self.dev.lib.ah_seq_run(self.dev.h, self.h, stream), "seq_run")
+
+    def sync_status(self, stream: int | None = None) -> tuple[int, int]:
+        """(status, stage) of the first refusal since the last call, in stage order."""
+        stage = ctypes.c_uint32(0)
+        st = self.dev.lib.ah_seq_sync_status(self.dev.h, self.h, stream, ctypes.byref(stage))
+        return st, stage.value
+
+    def info(self) -> tuple[int, int]:
+        """(resident grid, activation LDS bytes per workgroup)."""
+        g, a = ctypes.c_uint32(0), ctypes.c_uint32(0)
+        _check(self.dev.lib.ah_seq_info(self.h, ctypes.byref(g), ctypes.byref(a)), "seq_info")
+        return g.value, a.value
+
+    def free(self) -> None:
+        if self.h:
+            self.dev.lib.ah_seq_free(self.dev.h, self.h)
+            self.h = None
+
+
 _default: Device | None = None
 
 

@@ -30,6 +30,8 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const Ge
                                  const StreamWG *d_wgd, uint32_t grid, uint32_t act_bytes,
                                  unsigned long long *status, hipStream_t stream);
 hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream);
+int ah_gemv_seq_occupancy(uint32_t type, size_t act_bytes);
+hipError_t ah_launch_gemv_seq(uint32_t type, const SeqArgs &a, uint32_t grid, hipStream_t stream);
 hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes, uint32_t off0,
                           uint32_t off1, unsigned long long *d_bad, hipStream_t stream);
 hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_in,
@@ -86,6 +88,17 @@ struct ah_gemv_plan {
     GemvPart *d_parts = nullptr;   // part descriptors
     uint32_t *d_wg_part = nullptr; // workgroup-tile kernel: workgroup -> part index
     StreamWG *d_wgd = nullptr;     // streaming kernel: per-workgroup wave assignment
+};
+
+struct ah_seq {
+    uint32_t type = 0, grid = 0, n_stages = 0, act_bytes = 0;
+    SeqStage *d_stages = nullptr;
+    GemvPart *d_parts = nullptr;
+    StreamWG *d_wgd = nullptr;
+    uint32_t *d_prod = nullptr;   // per stage, producer workgroups of each group
+    unsigned *d_done = nullptr;   // per stage and group, a completion counter (128-byte lines)
+    unsigned *d_runs = nullptr;   // per workgroup, completed launches
+    unsigned long long *d_status = nullptr;
 };
 
 #define AH_HIP(ctx, call)                                                                       \
@@ -592,6 +605,10 @@ const char *ah_status_str(int32_t s) {
     case AH_ERR_HIP: return "hip error";
     case AH_ERR_OUT_OF_MEMORY: return "out of device memory";
     case AH_ERR_SCRATCH_LIMIT: return "call needs more than the fixed scratch of the no-alloc entry point";
+    case AH_ERR_SEQ_TIMEOUT: return "sequence barrier timed out";
+    case AH_ERR_FFN_OVERFLOW: return "FFN overflow";
+    case AH_ERR_EXP_RANGE: return "exp out of range";
+    case AH_ERR_ZERO_DENOMINATOR: return "zero denominator";
     default: return "unknown status";
     }
 }
@@ -969,6 +986,189 @@ int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan) {
     if (plan->d_wg_part) (void)hipFree(plan->d_wg_part);
     if (plan->d_wgd) (void)hipFree(plan->d_wgd);
     delete plan;
+    return AH_OK;
+}
+
+// ---- persistent decode sequence ----
+
+static void seq_release(ah_seq *q) {
+    if (!q) return;
+    if (q->d_stages) (void)hipFree(q->d_stages);
+    if (q->d_parts) (void)hipFree(q->d_parts);
+    if (q->d_wgd) (void)hipFree(q->d_wgd);
+    if (q->d_prod) (void)hipFree(q->d_prod);
+    if (q->d_done) (void)hipFree(q->d_done);
+    if (q->d_runs) (void)hipFree(q->d_runs);
+    if (q->d_status) (void)hipFree(q->d_status);
+    delete q;
+}
+
+int32_t ah_seq_create(ah_ctx *ctx, size_t n_stages, const ah_seq_stage *stages, ah_seq **out) {
+    if (!ctx || !out || !stages || n_stages == 0 || n_stages > 65536) return AH_ERR_INVALID_ARG;
+    *out = nullptr;
+    // every GEMV part of every stage, stage by stage
+    std::vector<GemvPart> parts;
+    std::vector<size_t> first(n_stages, 0);
+    uint32_t type = 0xFFFFFFFFu;
+    bool mixed = false;
+    size_t budget = 15360;
+    for (size_t s = 0; s < n_stages; ++s) {
+        const ah_seq_stage &S = stages[s];
+        first[s] = parts.size();
+        if (S.kind == AH_SEQ_SWIGLU) {
+            if (!S.gate || !S.up || !S.h_codes || !S.h_scales || S.n == 0 || S.n > AH_MAX_N_IN ||
+                reinterpret_cast<uintptr_t>(S.h_scales) % 8 || reinterpret_cast<uintptr_t>(S.h_codes) % 8)
+                return AH_ERR_INVALID_ARG;
+            continue;
+        }
+        if (S.kind != AH_SEQ_GEMV || S.n_parts == 0 || S.n_parts > 4096 || !S.w || !S.y) return AH_ERR_INVALID_ARG;
+        for (size_t i = 0; i < S.n_parts; ++i) {
+            const ah_tensor *w = S.w[i];
+            const float *x = S.x ? S.x[i] : nullptr;
+            const int8_t *c = S.codes ? S.codes[i] : nullptr;
+            const int64_t *sc = S.scales ? S.scales[i] : nullptr;
+            if (!w || w->n_out == 0 || !S.y[i]) return AH_ERR_INVALID_ARG;
+            if (x ? reinterpret_cast<uintptr_t>(x) % 4 != 0
+                  : (!c || !sc || reinterpret_cast<uintptr_t>(c) % 4 || reinterpret_cast<uintptr_t>(sc) % 8))
+                return AH_ERR_INVALID_ARG;
+            bool st = false;
+            parts.push_back(make_part(w, x ? AH_SRC_F32 : AH_SRC_CODES, x ? static_cast<const void *>(x) : c,
+                                      x ? nullptr : sc, S.y[i], nullptr, st));
+            if (!st) return AH_ERR_INVALID_ARG;  // rows past the 8 KB streaming tile
+            if (type != 0xFFFFFFFFu && type != w->type) mixed = true;
+            type = w->type;
+            const size_t a = ah_gemv_act_bytes(kpad_of(w->n_in));
+            budget = a > budget ? a : budget;
+        }
+    }
+    if (type == 0xFFFFFFFFu) type = AH_GGML_Q4_K;  // SwiGLU stages only
+    if (mixed) type = kMixedType;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    const int occ = ah_gemv_seq_occupancy(type, budget);
+    if (occ < 1) return AH_ERR_INVALID_ARG;
+    const uint32_t grid = (uint32_t)occ * (uint32_t)ctx->cu_count;
+    if (grid > kSeqGroup * kSeqMaxGroups) return AH_ERR_INVALID_ARG;
+    // one StreamWG table of `grid` entries per GEMV stage; workgroups past the dealt ones idle;
+    // each stage's producers (workgroups with work) counted per group of kSeqGroup
+    std::vector<SeqStage> dst(n_stages);
+    std::vector<StreamWG> wgd;
+    std::vector<uint32_t> prod(n_stages * kSeqMaxGroups, 0u);
+    for (size_t s = 0; s < n_stages; ++s) {
+        const ah_seq_stage &S = stages[s];
+        SeqStage &D = dst[s];
+        std::memset(&D, 0, sizeof(D));
+        D.prod_off = (uint32_t)(s * kSeqMaxGroups);
+        if (S.kind == AH_SEQ_SWIGLU) {
+            const uint64_t nb = (S.n + 31) / 32;
+            for (uint32_t g = 0; g < grid; ++g)
+                if (nb * g / grid != nb * (g + 1) / grid) ++prod[s * kSeqMaxGroups + g / kSeqGroup];
+            D.kind = kSeqSwiglu;
+            D.n = (uint32_t)S.n;
+            D.gate = S.gate;
+            D.up = S.up;
+            D.codes = S.h_codes;
+            D.scales = S.h_scales;
+            continue;
+        }
+        D.kind = kSeqGemv;
+        D.wgd_off = (uint32_t)wgd.size();
+        const size_t base = first[s];
+        std::vector<StreamWG> tab(grid);
+        const uint32_t nwg = deal_waves(parts.data() + base, S.n_parts, grid, budget, tab.data());
+        if (nwg == 0) return AH_ERR_INVALID_ARG;
+        for (uint32_t g = 0; g < grid; ++g) {
+            StreamWG &T = tab[g];
+            if (g >= nwg) {
+                std::memset(&T, 0, sizeof(T));
+                for (int v = 0; v < 8; ++v) T.wave_part[v] = kIdleWave;
+            }
+            if (T.n_act) ++prod[s * kSeqMaxGroups + g / kSeqGroup];
+            for (int a = 0; a < 8; ++a) T.act_part[a] += (uint32_t)base;
+            for (int v = 0; v < 8; ++v)
+                if (T.wave_part[v] != kIdleWave) T.wave_part[v] += (uint32_t)base;
+        }
+        wgd.insert(wgd.end(), tab.begin(), tab.end());
+    }
+    ah_seq *q = new (std::nothrow) ah_seq();
+    if (!q) return AH_ERR_OUT_OF_MEMORY;
+    q->type = type;
+    q->grid = grid;
+    q->n_stages = (uint32_t)n_stages;
+    q->act_bytes = (uint32_t)budget;
+    std::vector<unsigned long long> none(n_stages, AH_ST_NONE);
+    const size_t done_words = n_stages * kSeqMaxGroups * kSeqLine;
+    hipError_t e = hipMalloc(&q->d_stages, n_stages * sizeof(SeqStage));
+    if (e == hipSuccess && !parts.empty()) e = hipMalloc(&q->d_parts, parts.size() * sizeof(GemvPart));
+    if (e == hipSuccess && !wgd.empty()) e = hipMalloc(&q->d_wgd, wgd.size() * sizeof(StreamWG));
+    if (e == hipSuccess) e = hipMalloc(&q->d_prod, prod.size() * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&q->d_done, done_words * sizeof(unsigned));
+    if (e == hipSuccess) e = hipMalloc(&q->d_runs, grid * sizeof(unsigned));
+    if (e == hipSuccess) e = hipMalloc(&q->d_status, n_stages * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMemcpy(q->d_stages, dst.data(), n_stages * sizeof(SeqStage), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !parts.empty())
+        e = hipMemcpy(q->d_parts, parts.data(), parts.size() * sizeof(GemvPart), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !wgd.empty())
+        e = hipMemcpy(q->d_wgd, wgd.data(), wgd.size() * sizeof(StreamWG), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(q->d_prod, prod.data(), prod.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(q->d_done, 0, done_words * sizeof(unsigned));
+    if (e == hipSuccess) e = hipMemset(q->d_runs, 0, grid * sizeof(unsigned));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(q->d_status, none.data(), n_stages * sizeof(unsigned long long), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        seq_release(q);
+        ctx->last_hip = (int)e;
+        return AH_ERR_HIP;
+    }
+    *out = q;
+    return AH_OK;
+}
+
+int32_t ah_seq_run(ah_ctx *ctx, const ah_seq *seq, void *stream) {
+    if (!ctx || !seq) return AH_ERR_INVALID_ARG;
+    SeqArgs a;
+    a.stages = seq->d_stages;
+    a.parts = seq->d_parts;
+    a.wgd = seq->d_wgd;
+    a.producers = seq->d_prod;
+    a.done = seq->d_done;
+    a.runs = seq->d_runs;
+    a.status = seq->d_status;
+    a.n_stages = seq->n_stages;
+    a.act_bytes = seq->act_bytes;
+    a.spin_limit = 1u << 21;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, ah_launch_gemv_seq(seq->type, a, seq->grid, pick(ctx, stream)));
+    return AH_OK;
+}
+
+int32_t ah_seq_sync_status(ah_ctx *ctx, const ah_seq *seq, void *stream, uint32_t *stage) {
+    if (!ctx || !seq) return AH_ERR_INVALID_ARG;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, hipStreamSynchronize(pick(ctx, stream)));
+    std::vector<unsigned long long> st(seq->n_stages);
+    AH_HIP(ctx, hipMemcpy(st.data(), seq->d_status, st.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+    for (uint32_t s = 0; s < seq->n_stages; ++s) {
+        if (st[s] == AH_ST_NONE) continue;
+        std::vector<unsigned long long> none(seq->n_stages, AH_ST_NONE);
+        AH_HIP(ctx, hipMemcpy(seq->d_status, none.data(), none.size() * sizeof(unsigned long long), hipMemcpyHostToDevice));
+        if (stage) *stage = s;
+        return (int32_t)(st[s] & 0xffu);
+    }
+    return AH_OK;
+}
+
+int32_t ah_seq_info(const ah_seq *seq, uint32_t *grid, uint32_t *act_bytes) {
+    if (!seq) return AH_ERR_INVALID_ARG;
+    if (grid) *grid = seq->grid;
+    if (act_bytes) *act_bytes = seq->act_bytes;
+    return AH_OK;
+}
+
+int32_t ah_seq_free(ah_ctx *ctx, ah_seq *seq) {
+    if (!ctx || !seq) return AH_ERR_INVALID_ARG;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    seq_release(seq);
     return AH_OK;
 }
 

@@ -26,8 +26,16 @@ constexpr uint32_t kThreads = 256;
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// CP: cache policy of the load.  0 for inputs written before the launch; kCoherent (sc1, device
+// scope) for inputs another workgroup of the same persistent launch wrote (gemv_seq_kernel).
+constexpr int kCoherent = 16;
+template <int CP = 0>
 AH_DEV u32x2 ah_ld64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, CP));
+}
+template <int CP = 0>
+AH_DEV u32x4 ah_ld128p(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CP));
 }
 
 struct ActLds {
@@ -141,17 +149,18 @@ AH_DEV ActRsrc act_rsrc(const void *x, const int64_t *scales, uint32_t src, uint
     return r;
 }
 constexpr uint32_t kActOob = 0xFFFFFFF0u;  // past any activation resource
+template <int CP = 0>
 AH_DEV QuadIn quad_load_row(const ActRsrc &r, uint32_t src, uint32_t n_in, uint32_t b) {
     QuadIn in;
     const uint32_t k0 = b * 32 + 8 * (threadIdx.x & 3);
     in.take = n_in > k0 ? (n_in - k0 < 8 ? n_in - k0 : 8) : 0;
     const bool f = src == AH_SRC_F32, q = src == AH_SRC_Q32;
     const uint32_t base = f ? 4 * k0 : q ? 8 * k0 : k0;
-    const u32x4 l0 = ah_ld128(r.x, base);
-    const u32x4 l1 = ah_ld128(r.x, f || q ? base + 16 : kActOob);
-    const u32x4 l2 = ah_ld128(r.x, q ? base + 32 : kActOob);
-    const u32x4 l3 = ah_ld128(r.x, q ? base + 48 : kActOob);
-    const u32x2 sc = ah_ld64(r.s, f || q ? kActOob : 8 * b);
+    const u32x4 l0 = ah_ld128p<CP>(r.x, base);
+    const u32x4 l1 = ah_ld128p<CP>(r.x, f || q ? base + 16 : kActOob);
+    const u32x4 l2 = ah_ld128p<CP>(r.x, q ? base + 32 : kActOob);
+    const u32x4 l3 = ah_ld128p<CP>(r.x, q ? base + 48 : kActOob);
+    const u32x2 sc = ah_ld64<CP>(r.s, f || q ? kActOob : 8 * b);
     in.w[0] = l0.x; in.w[1] = l0.y; in.w[2] = l0.z; in.w[3] = l0.w;
     in.w[4] = l1.x; in.w[5] = l1.y; in.w[6] = l1.z; in.w[7] = l1.w;
     in.w[8] = l2.x; in.w[9] = l2.y; in.w[10] = l2.z; in.w[11] = l2.w;
@@ -1001,6 +1010,347 @@ __global__ void __launch_bounds__(kSThreads, 4)
     if (obad != 0xFFFFFFFFu && lane == 0) ah_record(status, ah_out_key(obad >> 1, (obad & 1u) ? 9u : 8u));
 }
 
+// ---- persistent decode sequence ---------------------------------------------------------------
+//
+// A token's projections form a chain of stages (q/k/v -> o -> gate/up -> SwiGLU -> down per layer,
+// then the head): each stage reads an earlier stage's output.  One kernel launch per stage pays a
+// dispatch, the grid's fill and the activation prologue in series for every stage.  Here one
+// resident grid runs the whole chain as a dataflow: a workgroup takes part in a stage only if the
+// stage's plan gives it work; when its outputs are stored (device-scope sc1 stores, complete before
+// it signals) it counts itself into its group's completion counter for that stage.  A workgroup
+// with work in stage s+1 first requests its weight tiles (they do not depend on stage s), then
+// waits until every group counter of stage s has reached this launch's target (run number x the
+// group's producers), then reads stage s's outputs (sc1 loads).  Waiting for stage s implies every
+// earlier stage (each producer of s waited for s-1), so stages cannot overtake one another, and no
+// workgroup rewrites a buffer an earlier stage still reads.  Workgroups idle in a stage skip it.
+//
+// Counters: one per group of kSeqGroup workgroups and stage, each on its own 128-byte line, so a
+// stage's increments spread over up to kSeqMaxGroups addresses (one counter for a whole 512-wide
+// grid serializes its atomics: 7.2 us a barrier measured, against 2.7 us for groups of 16-32).
+// Lane g of wave 0 polls group g's counter, so one load instruction checks every group; polls are
+// bounded (past spin_limit the stage records AH_ERR_SEQ_TIMEOUT and waits no more in this launch).
+// A workgroup's run number is its own device counter, read at start and bumped at the end.  The
+// grid is launched cooperatively, which guarantees that every workgroup is resident.
+
+typedef __int128 i128;
+constexpr int64_t kOneQ32 = (int64_t)1 << 32;
+
+// round(v / 2^32), ties away from zero (numeric/fixed_exp.rs round_div_2p32)
+AH_DEV i128 round_div_2p32(i128 v) {
+    const i128 half = (i128)1 << 31;
+    return v >= 0 ? (v + half) >> 32 : -((-v + half) >> 32);
+}
+// exp(x) in Q32.32 for x in [-16, 21] (numeric/fixed_exp.rs:40-131): k = round(x / ln 2),
+// r = x - k ln 2, the degree-7 Taylor sum of exp(r) by Horner with round_div_2p32, then 2^k.
+AH_DEV int fx_exp(int64_t x, int64_t &out) {
+    if (x < -16 * kOneQ32 || x > 21 * kOneQ32) return AH_ERR_EXP_RANGE;
+    const int64_t k = (int64_t)(((i128)x * 6196328019LL + ((i128)1 << 63)) >> 64);
+    const int64_t r = x - k * 2977044472LL;
+    i128 acc = 852176;
+    acc = round_div_2p32(acc * r) + 5965232;
+    acc = round_div_2p32(acc * r) + 35791394;
+    acc = round_div_2p32(acc * r) + 178956971;
+    acc = round_div_2p32(acc * r) + 715827883;
+    acc = round_div_2p32(acc * r) + 2147483648LL;
+    acc = round_div_2p32(acc * r) + 4294967296LL;
+    acc = round_div_2p32(acc * r) + 4294967296LL;
+    i128 v;
+    if (k >= 0) {
+        if (k >= 64) return AH_ERR_EXP_RANGE;
+        v = acc << k;
+    } else {
+        const int64_t n = -k;
+        if (n >= 64) {
+            out = 0;
+            return 0;
+        }
+        v = (acc + ((i128)1 << (n - 1))) >> n;
+    }
+    if (v > (i128)INT64_MAX || v < (i128)INT64_MIN) return AH_ERR_EXP_RANGE;
+    out = (int64_t)v;
+    return 0;
+}
+// silu(v) = round(|v| * 2^32 / (2^32 + exp(-v))) with v's sign on -21 < v < 16, v above, 0 below
+// (engine/ops/silu.rs:18-60).  The quotient is below 2^37: a double estimate of the i128 division,
+// then exact correction against the remainder (the hardware has no i128 divide).
+AH_DEV int silu_fx(int64_t v, int64_t &out) {
+    if (v >= 16 * kOneQ32) {
+        out = v;
+        return 0;
+    }
+    if (v <= -21 * kOneQ32) {
+        out = 0;
+        return 0;
+    }
+    int64_t e;
+    if (fx_exp(-v, e)) return AH_ERR_EXP_RANGE;
+    if (e > INT64_MAX - kOneQ32) return AH_ERR_FFN_OVERFLOW;
+    const int64_t den = kOneQ32 + e;
+    if (den <= 0) return AH_ERR_ZERO_DENOMINATOR;
+    const uint64_t mag = v < 0 ? 0ull - (uint64_t)v : (uint64_t)v;
+    const i128 n2 = (i128)mag * kOneQ32 + (den >> 1);  // div_round_nearest's num + den / 2
+    const double nd = (double)(uint64_t)(n2 >> 32) * 4294967296.0 + (double)(uint64_t)(n2 & 0xFFFFFFFFu);
+    int64_t q = (int64_t)(nd / (double)den);
+    i128 rem = n2 - (i128)q * den;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (rem < 0) {
+            --q;
+            rem += den;
+        } else if (rem >= den) {
+            ++q;
+            rem -= den;
+        }
+    }
+    out = v < 0 ? -q : q;
+    return 0;
+}
+// h = round_shift_32(silu(gate) * up) (engine/chart/ffn.rs:246-252)
+AH_DEV int swiglu_fx(int64_t g, int64_t u, int64_t &h) {
+    int64_t s;
+    const int st = silu_fx(g, s);
+    if (st) return st;
+    const i128 r = ((i128)s * u + ((i128)1 << 31)) >> 32;
+    if (r > (i128)INT64_MAX || r < (i128)INT64_MIN) return AH_ERR_FFN_OVERFLOW;
+    h = (int64_t)r;
+    return 0;
+}
+
+// The SwiGLU stage: the hidden activation's 32-blocks are dealt to the workgroups, 16 blocks per
+// round (one element per thread): gate and up from f32 to Q32.32 (to_q32), h = swiglu into LDS,
+// then a quad of lanes per block quantizes it (quant_act) into the hidden QuantAct the down stage
+// reads.  Refusals in element order (conversion or SwiGLU), then the quantizer's, as the
+// reference FFN orders them (chart/ffn.rs:1712-1720).  `hl` is 512 int64 of LDS.
+AH_DEV void swiglu_stage(const SeqStage &S, unsigned long long *st, int64_t *hl) {
+    constexpr uint32_t kRound = kSThreads / 32;  // blocks per round
+    const uint32_t nb = (S.n + 31) / 32;
+    const uint32_t b0 = (uint32_t)((uint64_t)nb * blockIdx.x / gridDim.x);
+    const uint32_t b1 = (uint32_t)((uint64_t)nb * (blockIdx.x + 1) / gridDim.x);
+    const __amdgpu_buffer_rsrc_t rg = ah_rsrc(S.gate, S.n * 4u), ru = ah_rsrc(S.up, S.n * 4u);
+    const __amdgpu_buffer_rsrc_t rc = ah_rsrc(S.codes, S.n), rs = ah_rsrc(S.scales, nb * 8u);
+    const uint32_t q = threadIdx.x & 3;
+    for (uint32_t base = b0; base < b1; base += kRound) {  // a uniform trip count
+        const uint32_t k = 32 * base + threadIdx.x;
+        const bool live = k < 32 * b1 && k < S.n;
+        const uint32_t gb = __builtin_amdgcn_raw_buffer_load_b32(rg, live ? 4 * k : kActOob, 0, kCoherent);
+        const uint32_t ub = __builtin_amdgcn_raw_buffer_load_b32(ru, live ? 4 * k : kActOob, 0, kCoherent);
+        int64_t h = 0;
+        if (live) {
+            uint64_t mg, mu;
+            bool ng, nu;
+            int e = ah_to_q32_mag(gb, mg, ng);
+            if (!e) e = ah_to_q32_mag(ub, mu, nu);
+            if (!e) e = swiglu_fx(ng ? (int64_t)(0ull - mg) : (int64_t)mg, nu ? (int64_t)(0ull - mu) : (int64_t)mu, h);
+            if (e) {
+                ah_record(st, ((unsigned long long)k << 8) | (unsigned)e);
+                h = 0;
+            }
+        }
+        hl[threadIdx.x] = h;
+        ah_lds_barrier();
+        // quads: lane q of the quad for block base + j (j < 16, 4 * 16 = 64 lanes of wave 0 .. 1)
+        if (threadIdx.x < 4 * kRound) {
+            const uint32_t j = threadIdx.x / 4, b = base + j, k0 = 32 * b + 8 * q;
+            QuadIn in;
+            in.take = b < b1 && S.n > k0 ? (S.n - k0 < 8 ? S.n - k0 : 8) : 0;
+            in.s0 = in.s1 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint64_t v = (uint32_t)i < in.take ? (uint64_t)hl[32 * j + 8 * q + i] : 0ull;
+                in.w[2 * i] = (uint32_t)v;
+                in.w[2 * i + 1] = (uint32_t)(v >> 32);
+            }
+            const QuadOut o = quad_quant(in, AH_SRC_Q32, b, st, 0);
+            if (b < b1) {
+                if (in.take == 8) {
+                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, (u32x2){o.c0, o.c1}), rc, k0, 0, kCoherent);
+                } else {
+#pragma unroll
+                    for (uint32_t i = 0; i < 8; ++i)
+                        if (i < in.take)
+                            __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(((i < 4 ? o.c0 : o.c1) >> (8 * (i & 3))) & 0xffu), rc,
+                                                                 k0 + i, 0, kCoherent);
+                }
+                if (q == 0) {
+                    const uint64_t S64 = o.e < 0 ? 0ull : (1ull << o.e);
+                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, (u32x2){(uint32_t)S64, (uint32_t)(S64 >> 32)}),
+                                                          rs, 8 * b, 0, kCoherent);
+                }
+            }
+        }
+        ah_lds_barrier();  // hl is reused by the next round
+    }
+}
+
+// Wave 0 of a workgroup waits until stage `sp`'s counters reach run r's targets.
+AH_DEV void seq_wait(const SeqArgs &a, uint32_t sp, uint32_t r, unsigned long long *st, bool &broken) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t ngrp = (gridDim.x + kSeqGroup - 1) / kSeqGroup;
+    const uint32_t need = lane < ngrp ? a.producers[a.stages[sp].prod_off + lane] * r : 0u;
+    const unsigned *cnt = a.done + (size_t)(sp * kSeqMaxGroups + (lane < ngrp ? lane : 0)) * kSeqLine;
+    uint32_t polls = 0;
+    while (!broken) {
+        const unsigned v = lane < ngrp ? __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        if (__builtin_amdgcn_ballot_w64(v < need) == 0) break;
+        if (++polls >= a.spin_limit) {  // every later wait of this launch is skipped
+            if (lane == 0) ah_record(st, AH_ERR_SEQ_TIMEOUT);
+            broken = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+// Thread 0 counts the workgroup into stage s's group counter (after every wave's stores are done).
+AH_DEV void seq_signal(const SeqArgs &a, uint32_t s) {
+    if (threadIdx.x == 0)
+        (void)__hip_atomic_fetch_add(a.done + (size_t)(s * kSeqMaxGroups + blockIdx.x / kSeqGroup) * kSeqLine, 1u,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One GEMV stage of the sequence: the workgroup's waves stream their rows of the stage's parts
+// (the PLAN form of gemv_stream_kernel) with device-scope output stores.
+template <int TYPE>
+AH_DEV void seq_gemv_stage(const SeqArgs &a, uint32_t s, uint32_t r, bool &broken) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const SeqStage &S = a.stages[s];
+    const StreamWG *D = a.wgd + S.wgd_off + blockIdx.x;
+    const uint32_t n_act = D->n_act;
+    if (n_act == 0) return;  // no work for this workgroup in this stage
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    uint8_t *tl = smem + a.act_bytes + wave * kSlotBytes;
+    constexpr uint32_t QB = kSThreads / 4;
+    unsigned long long *st = a.status + s;
+    const uint32_t pi = D->wave_part[wv];
+    const bool idle = pi == kIdleWave;
+    const GemvPart P = part_at(a.parts, idle ? D->act_part[0] : pi);  // an idle wave streams no rows
+    const uint32_t r_begin = D->r_begin[wv], r_end = idle ? r_begin : D->r_end[wv];
+    const ActLds A = carve(smem + D->act_off[D->wave_act[wv]], (P.n_in + 255) / 256 * 256);
+    const __amdgpu_buffer_rsrc_t rsw = ah_rsrc(P.w, (uint32_t)P.w_bytes);
+    const uint32_t U = P.units, RW = P.rows_per_tile, RB = P.row_bytes, G = P.lanes;
+    const uint32_t n_t = (r_end - r_begin + RW - 1) / RW;
+    u32x4 chunk[kChunks];
+    auto load_tile = [&](uint32_t t) {
+        const uint32_t r0 = r_begin + t * RW;
+        const uint32_t rows = t >= n_t ? 0u : (r_end - r0 < RW ? r_end - r0 : RW);
+        const uint32_t start = rows ? r0 * RB : 0u, a0 = start & ~15u;
+        const uint32_t nch = rows ? (rows * RB + (start - a0) + 15) / 16 : 0u;
+#pragma unroll
+        for (uint32_t i = 0; i < kChunks; ++i) {
+            const uint32_t c = lane + 64 * i;
+            chunk[i] = ah_ld128_nt(rsw, c < nch ? a0 + 16 * c : kOob);
+        }
+    };
+    // Weights do not depend on the previous stage: waves 1-7 request their tile 0 at once; wave 0
+    // first waits for the previous stage (its loads would hold up its polls: vector memory
+    // operations complete in order), then requests its own.
+    ah_lds_barrier();  // the previous stage's LDS readers are done
+    if (s) {
+        if (wv != 0) load_tile(0);
+        else seq_wait(a, s - 1, r, st, broken);
+        ah_lds_barrier();
+        if (wv == 0) load_tile(0);
+    } else {
+        load_tile(0);
+    }
+    for (uint32_t ai = 0; ai < n_act; ++ai) {
+        const GemvPart Pa = part_at(a.parts, D->act_part[ai]);
+        const uint32_t nbpa = (Pa.n_in + 255) / 256 * 8;
+        const ActLds Aa = carve(smem + D->act_off[ai], nbpa * 32);
+        const ActRsrc xra = act_rsrc(Pa.x, Pa.scales, Pa.src, Pa.n_in);
+        for (uint32_t base = 0; base < nbpa; base += QB) {
+            if (base + wave * 16 >= nbpa) break;
+            const uint32_t b = base + threadIdx.x / 4;
+            const QuadOut o = quad_quant(quad_load_row<kCoherent>(xra, Pa.src, Pa.n_in, b), Pa.src, b, st, 0);
+            if (b < nbpa) store_quad(Aa, b, o);
+        }
+    }
+    auto stage = [&](uint32_t t) {
+#pragma unroll
+        for (uint32_t i = 0; i < kChunks; ++i) reinterpret_cast<u32x4 *>(tl)[lane + 64 * i] = chunk[i];
+        load_tile(t + 1);
+    };
+    ah_lds_barrier();
+    stage(0);
+    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(P.y, P.n_out * 4u);
+    const uint32_t rr = lane / G, g = lane & (G - 1);
+    uint32_t obad = 0xFFFFFFFFu;
+    for (uint32_t t = 0; t < n_t; ++t) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS stores have landed
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t r0 = r_begin + t * RW;
+        const uint32_t toff = (r0 * RB) & 15u;
+        const uint32_t row = r0 + rr;
+        const bool owns = rr < RW && row < r_end;
+        float acc = 0.0f;
+        if (owns) {
+            if constexpr (TYPE == kMixedType) {
+                if (P.type == AH_GGML_Q4_K) {
+#pragma unroll 1
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q4_K, false>(P, tl, toff + rr * RB + unit_off(AH_GGML_Q4_K, u), row, u, A);
+                } else if (P.type == AH_GGML_Q6_K) {
+#pragma unroll 1
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q6_K, false>(P, tl, toff + rr * RB + unit_off(AH_GGML_Q6_K, u), row, u, A);
+                } else {
+#pragma unroll 1
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q8_0, false>(P, tl, toff + rr * RB + unit_off(AH_GGML_Q8_0, u), row, u, A);
+                }
+            } else {
+#pragma unroll 1
+                for (uint32_t u = g; u < U; u += G)
+                    acc += comp_unit<TYPE, false>(P, tl, toff + rr * RB + unit_off(TYPE, u), row, u, A);
+            }
+        }
+        acc = group_sum(acc, G);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), ry,
+                                              (g == 0 && owns) ? row * 4u : kOob, 0, kCoherent);
+        const uint32_t oc = ah_out_code(acc);
+        const uint64_t ob = __builtin_amdgcn_ballot_w64(g == 0 && owns && oc != 0u);
+        if (ob) {
+            const uint32_t k = __builtin_amdgcn_readlane((row << 1) | (oc == 9u ? 1u : 0u), (int)__builtin_ctzll(ob));
+            obad = k < obad ? k : obad;
+        }
+        __builtin_amdgcn_wave_barrier();
+        stage(t + 1);
+    }
+    if (obad != 0xFFFFFFFFu && lane == 0) ah_record(st, ah_out_key(obad >> 1, (obad & 1u) ? 9u : 8u));
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's outputs are complete
+    ah_lds_barrier();
+    seq_signal(a, s);
+}
+
+AH_DEV void seq_swiglu_stage(const SeqArgs &a, uint32_t s, uint32_t r, bool &broken) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const SeqStage &S = a.stages[s];
+    const uint32_t nb = (S.n + 31) / 32;
+    if ((uint64_t)nb * blockIdx.x / gridDim.x == (uint64_t)nb * (blockIdx.x + 1) / gridDim.x) return;  // no blocks
+    unsigned long long *st = a.status + s;
+    ah_lds_barrier();
+    if (s && __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == 0) seq_wait(a, s - 1, r, st, broken);
+    ah_lds_barrier();
+    swiglu_stage(S, st, reinterpret_cast<int64_t *>(smem));
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    ah_lds_barrier();
+    seq_signal(a, s);
+}
+
+template <int TYPE>
+__global__ void __launch_bounds__(kSThreads, 4) gemv_seq_kernel(SeqArgs a) {
+    // this launch's run number (nothing writes the counter until the workgroup ends)
+    const uint32_t r = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(a.runs + blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1);
+    bool broken = false;  // (wave 0) a wait timed out: the launch's results are refused
+    for (uint32_t s = 0; s < a.n_stages; ++s) {
+        if (a.stages[s].kind == kSeqSwiglu) seq_swiglu_stage(a, s, r, broken);
+        else seq_gemv_stage<TYPE>(a, s, r, broken);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.runs + blockIdx.x, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Stream geometry for a row of RB bytes and U units: whole rows per tile and lanes per row.
 // Returns false when a row does not fit one tile (the workgroup-tile kernel then serves the part).
 // A lane computes ceil(units / G) units of its row per tile, so (rows, G) is chosen for the most
@@ -1048,6 +1398,36 @@ static const void *stream_fn(uint32_t type, bool plan, bool dots = false) {
     default: return nullptr;
     }
 #undef AH_SFN
+}
+
+static const void *seq_fn(uint32_t type) {
+    switch (type) {
+    case kMixedType: return reinterpret_cast<const void *>(&gemv_seq_kernel<kMixedType>);
+    case AH_GGML_Q8_0: return reinterpret_cast<const void *>(&gemv_seq_kernel<AH_GGML_Q8_0>);
+    case AH_GGML_Q4_K: return reinterpret_cast<const void *>(&gemv_seq_kernel<AH_GGML_Q4_K>);
+    case AH_GGML_Q6_K: return reinterpret_cast<const void *>(&gemv_seq_kernel<AH_GGML_Q6_K>);
+    default: return nullptr;
+    }
+}
+
+// Workgroups of the sequence kernel that fit one CU at once with `act_bytes` of activation LDS.
+int ah_gemv_seq_occupancy(uint32_t type, size_t act_bytes) {
+    int n = 0;
+    const void *f = seq_fn(type);
+    if (!f || hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, kSThreads, act_bytes + ah_gemv_stream_slot_bytes()) != hipSuccess)
+        return 0;
+    return n;
+}
+
+// One cooperative launch runs the whole sequence: every workgroup is resident, which the grid
+// barriers between stages require (the launch fails rather than run a grid that does not fit).
+hipError_t ah_launch_gemv_seq(uint32_t type, const SeqArgs &a, uint32_t grid, hipStream_t stream) {
+    const void *f = seq_fn(type);
+    if (!f) return hipErrorInvalidValue;
+    SeqArgs arg = a;
+    void *args[] = {&arg};
+    return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kSThreads), args,
+                                      (unsigned)(a.act_bytes + ah_gemv_stream_slot_bytes()), stream);
 }
 
 // Workgroups of the streaming kernel that fit one CU at once with `lds` bytes of LDS each
@@ -1146,6 +1526,8 @@ hipError_t ah_gemv_init_attrs() {
                 e = hipFuncSetAttribute(stream_fn(t, v == 1, v == 2), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     if (e == hipSuccess)
         e = hipFuncSetAttribute(stream_fn(kMixedType, true), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+    for (uint32_t t : {(uint32_t)kMixedType, (uint32_t)AH_GGML_Q8_0, (uint32_t)AH_GGML_Q4_K, (uint32_t)AH_GGML_Q6_K})
+        if (e == hipSuccess) e = hipFuncSetAttribute(seq_fn(t), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     return e;
 }
 

@@ -224,6 +224,34 @@ struct StreamWG {
     uint32_t r_begin[8], r_end[8];
 };
 
+// Persistent decode sequence (gemv_seq_kernel): stages run in order on one resident grid, each
+// waiting at a grid barrier for the previous stage's outputs.
+enum : uint32_t { kSeqGemv = 0, kSeqSwiglu = 1 };
+constexpr uint32_t kSeqGroup = 16;   // workgroups per completion counter
+constexpr uint32_t kSeqMaxGroups = 64; // one counter per lane of the polling wave: grid <= 1024
+constexpr uint32_t kSeqLine = 32;      // u32 words per 128-byte line (one counter per line)
+struct SeqStage {
+    uint32_t kind;        // kSeqGemv / kSeqSwiglu
+    uint32_t wgd_off;     // GEMV: this stage's StreamWG table starts at wgd[wgd_off] (grid entries)
+    uint32_t n;           // SwiGLU: hidden width
+    uint32_t prod_off;    // producers[prod_off + g]: workgroups of group g with work in this stage
+    const float *gate;    // SwiGLU: f32 gate / up outputs of an earlier stage
+    const float *up;
+    int8_t *codes;        // SwiGLU: the hidden QuantAct (codes [n], scales [ceil(n/32)])
+    int64_t *scales;
+};
+struct SeqArgs {
+    const SeqStage *stages;
+    const GemvPart *parts;
+    const StreamWG *wgd;
+    const uint32_t *producers;     // per stage, kSeqMaxGroups producer counts
+    unsigned *done;                // per stage and group, a completion counter on its own line
+    unsigned *runs;                // per workgroup: launches it has completed
+    unsigned long long *status;    // [n_stages]: each stage's first refusal
+    uint32_t n_stages, act_bytes;  // LDS activation region of a workgroup (largest stage)
+    uint32_t spin_limit;           // polls before a wait gives up (AH_ERR_SEQ_TIMEOUT)
+};
+
 struct QuantArgs {
     const void *x;         // f32 or int64 [n_tok][n_in]
     int8_t *codes;         // [n_tok][n_in]

@@ -50,12 +50,16 @@ extern "C" {
 #define AH_ERR_OUTPUT_OVERFLOW 9      /* MatvecError::OutputOverflow                      */
 #define AH_ERR_NONFINITE_INPUT 10     /* F32Error::NonFinite (num/f32_convert.rs:44-49)   */
 #define AH_ERR_INPUT_RANGE 11         /* F32Error::OutOfRange                             */
+#define AH_ERR_FFN_OVERFLOW 12        /* FfnError::Overflow (ops/ffn.rs:11-27)            */
+#define AH_ERR_EXP_RANGE 13           /* FfnError::ExpOutOfRange                          */
+#define AH_ERR_ZERO_DENOMINATOR 14    /* FfnError::ZeroDenominator                        */
 #define AH_ERR_NO_DEVICE 20           /* no usable gfx950 device (the honest skip of       */
                                       /* Vk::load, gpu/vulkan.rs:1097-1106)               */
 #define AH_ERR_INVALID_ARG 21         /* null pointer / bad handle / limits exceeded       */
 #define AH_ERR_HIP 22                 /* a HIP runtime call failed                         */
 #define AH_ERR_OUT_OF_MEMORY 23
 #define AH_ERR_SCRATCH_LIMIT 24       /* a no-alloc call needs more than its fixed scratch  */
+#define AH_ERR_SEQ_TIMEOUT 25         /* a sequence's grid barrier waited past its limit    */
 
 /* ggml type ids (format/quant.rs:20-49) */
 #define AH_GGML_Q8_0 8
@@ -137,6 +141,52 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
                             const float *const *d_x, float *const *d_y, ah_gemv_plan **out);
 int32_t ah_gemv_plan_run(ah_ctx *ctx, const ah_gemv_plan *plan, void *stream);
 int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan);
+
+/* Persistent decode sequence: a token's chain of projection stages in ONE launch.  Stage s may
+ * read outputs of stages before it (q/k/v -> o -> gate/up -> SwiGLU -> down per layer, then the
+ * head): every workgroup of a resident grid finishes its share of stage s, then all meet at a
+ * grid barrier before stage s+1 reads its inputs; each wave requests its first stage-(s+1) weight
+ * tile before it waits, so the weight stream runs on through the barriers.  Replaces the
+ * engine's per-projection dispatches of a decode step (projections_q8act, chart/ffn.rs:905-1098;
+ * Vulkan's one command buffer per token, gpu/decode/model.rs:1-12).  A SwiGLU stage is the
+ * reference's fused FFN step (fused_ffn_task, chart/ffn.rs:1532-1594): for each hidden index
+ * h = round_shift_32(silu_fixed(to_q32(gate)) * to_q32(up)) exactly (ops/silu.rs:18-60,
+ * chart/ffn.rs:246-252), quantized (quant_act) into a QuantAct that a later GEMV stage takes as
+ * pre-quantized input, so gate/up -> SwiGLU -> down runs without leaving the launch.
+ * Limits: every GEMV part's rows fit the streaming kernel's 8 KB tiles (Q8_0 K <= 7680, Q4_K
+ * K <= 14336, Q6_K K <= 9728), at most 8 parts per stage per workgroup's activation budget
+ * (as ah_gemv_plan_create), at most 65536 stages. */
+#define AH_SEQ_GEMV 0
+#define AH_SEQ_SWIGLU 1
+typedef struct ah_seq ah_seq;
+typedef struct ah_seq_stage {
+    uint32_t kind;                 /* AH_SEQ_GEMV or AH_SEQ_SWIGLU */
+    /* AH_SEQ_GEMV: n_parts projections, each from an f32 input x[i] or, when x[i] is NULL, from a
+     * QuantAct codes[i] / scales[i] (e.g. a SwiGLU stage's output; codes 4-byte aligned) */
+    size_t n_parts;
+    const ah_tensor *const *w;
+    const float *const *x;
+    const int8_t *const *codes;    /* may be NULL when every x[i] is given */
+    const int64_t *const *scales;
+    float *const *y;
+    /* AH_SEQ_SWIGLU: n hidden values from f32 gate[n] / up[n] into h_codes[n] / h_scales[ceil(n/32)] */
+    const float *gate;
+    const float *up;
+    size_t n;
+    int8_t *h_codes;
+    int64_t *h_scales;
+} ah_seq_stage;
+/* Plans the sequence (every device pointer is fixed here) and uploads its tables. */
+int32_t ah_seq_create(ah_ctx *ctx, size_t n_stages, const ah_seq_stage *stages, ah_seq **out);
+/* Enqueues the whole sequence as one cooperative launch on `stream`. */
+int32_t ah_seq_run(ah_ctx *ctx, const ah_seq *seq, void *stream);
+/* Synchronizes `stream`, then returns (and clears) the first refusal of the sequence's last runs
+ * in stage order, as ah_sync_status does per call; *stage (optional) receives its stage index.
+ * AH_ERR_SEQ_TIMEOUT: a grid barrier waited past its limit (the run's outputs are not valid). */
+int32_t ah_seq_sync_status(ah_ctx *ctx, const ah_seq *seq, void *stream, uint32_t *stage);
+int32_t ah_seq_free(ah_ctx *ctx, ah_seq *seq);
+/* The sequence's resident grid (workgroups of 512 threads) and its per-workgroup activation LDS. */
+int32_t ah_seq_info(const ah_seq *seq, uint32_t *grid, uint32_t *act_bytes);
 
 /* ---- prefill GEMM, N = n_tok > 1 (kern/matmat.rs:134 matmat_q8act) ---- */
 

@@ -45,6 +45,10 @@ def lib():
         L.aho_matvec_q8act_fast.argtypes = [ctypes.c_uint32, c_ptr, c_size, c_size, c_size, c_ptr, c_ptr, c_ptr, ctypes.c_int]
         L.aho_matmat_q8act_fast.argtypes = [ctypes.c_uint32, c_ptr, c_size, c_size, c_size, c_size, c_ptr, c_ptr, c_ptr, ctypes.c_int]
         L.aho_row_bytes.argtypes = [ctypes.c_uint32, c_size, ctypes.POINTER(c_size)]
+        L.aho_fixed_exp.argtypes = [ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]
+        L.aho_silu_fixed.argtypes = [ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]
+        L.aho_swiglu.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]
+        L.aho_swiglu_quant_f32.argtypes = [c_ptr, c_ptr, c_size, c_ptr, c_ptr, c_ptr]
         _lib = L
     return _lib
 
@@ -173,6 +177,36 @@ def row_absdot(t: int, raw, n_out: int, n_in: int, codes, scales) -> tuple[int, 
     out = np.zeros(max(n_out, 1), dtype=np.float64)
     st = lib().aho_row_absdot(t, _p(raw), raw.shape[0], n_out, n_in, _p(codes), _p(scales), _p(out))
     return st, out[:n_out]
+
+
+def fixed_exp(x: int):
+    v = ctypes.c_int64(0)
+    st = lib().aho_fixed_exp(int(x), ctypes.byref(v))
+    return st, v.value
+
+
+def silu_fixed(x: int):
+    v = ctypes.c_int64(0)
+    st = lib().aho_silu_fixed(int(x), ctypes.byref(v))
+    return st, v.value
+
+
+def swiglu(gate: int, up: int):
+    v = ctypes.c_int64(0)
+    st = lib().aho_swiglu(int(gate), int(up), ctypes.byref(v))
+    return st, v.value
+
+
+def swiglu_quant_f32(gate, up):
+    """to_q32 + SwiGLU + quant_act of f32 gate/up: (status, codes, scales, hidden Q32.32)."""
+    gate = np.ascontiguousarray(gate, dtype=np.float32)
+    up = np.ascontiguousarray(up, dtype=np.float32)
+    n = gate.shape[0]
+    codes = np.zeros(max(n, 1), dtype=np.int8)
+    scales = np.zeros(max(-(-n // 32), 1), dtype=np.int64)
+    h = np.zeros(max(n, 1), dtype=np.int64)
+    st = lib().aho_swiglu_quant_f32(_p(gate), _p(up), n, _p(codes), _p(scales), _p(h))
+    return st, codes[:n], scales[: -(-n // 32)], h[:n]
 
 
 def q32_to_real(y: np.ndarray) -> np.ndarray:

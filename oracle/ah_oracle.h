@@ -18,6 +18,11 @@
  *   aho_matvec_fixed      reference 2x2 KAT (engine/tests.rs:389-407) + big-int brute force
  *   aho_block_dots        big-int brute force on the same payloads
  *   aho_matvec_q8act_fast bit-equal to aho_matvec_fixed on every tested payload
+ *   aho_fixed_exp         reference KATs (fixed_exp.rs zero_and_boundaries), accuracy against
+ *                         exp on a dense grid and monotonicity (fixed_exp.rs tests)
+ *   aho_silu_fixed        reference KATs (engine/tests.rs:949-963) + the closed form
+ *                         v / (1 + e^-v) within the exp tolerance + saturation bounds
+ *   aho_swiglu            exact big-int product rounding on random operands
  */
 #ifndef AH_ORACLE_H
 #define AH_ORACLE_H
@@ -42,7 +47,10 @@ enum {
     AHO_ERR_ACCUMULATOR_OVERFLOW = 8,/* MatvecError::AccumulatorOverflow           */
     AHO_ERR_OUTPUT_OVERFLOW = 9,     /* MatvecError::OutputOverflow                */
     AHO_ERR_NONFINITE_INPUT = 10,    /* F32Error::NonFinite (f32 boundary)         */
-    AHO_ERR_INPUT_RANGE = 11         /* F32Error::OutOfRange (f32 boundary)        */
+    AHO_ERR_INPUT_RANGE = 11,        /* F32Error::OutOfRange (f32 boundary)        */
+    AHO_ERR_FFN_OVERFLOW = 12,       /* FfnError::Overflow                         */
+    AHO_ERR_EXP_RANGE = 13,          /* FfnError::ExpOutOfRange (ExpError)         */
+    AHO_ERR_ZERO_DENOMINATOR = 14         /* FfnError::ZeroDenominator                  */
 };
 
 enum { AHO_Q8_0 = 8, AHO_Q4_K = 12, AHO_Q6_K = 14 };
@@ -107,6 +115,18 @@ int aho_matvec_q8act_fast(uint32_t ggml_type, const uint8_t *raw, size_t raw_len
 int aho_matmat_q8act_fast(uint32_t ggml_type, const uint8_t *raw, size_t raw_len, size_t n_out,
                           size_t n_in, size_t n_tok, const int8_t *codes, const int64_t *scales,
                           int64_t *y, int n_threads);
+
+/* The FFN's SwiGLU step (ah_oracle_ffn.c). */
+/* numeric/fixed_exp.rs:120-131: exp(x) in Q32.32, x in [-16, 21] * 2^32, else AHO_ERR_EXP_RANGE. */
+int aho_fixed_exp(int64_t x, int64_t *out);
+/* engine/ops/silu.rs:18-60 */
+int aho_silu_fixed(int64_t v, int64_t *out);
+/* engine/chart/ffn.rs:246-252: h = round_shift_32(silu_fixed(gate) * up) */
+int aho_swiglu(int64_t gate, int64_t up, int64_t *h);
+/* to_q32 of f32 gate/up, aho_swiglu, then aho_quant_act: the down projection's QuantAct.
+ * h (optional, n entries) receives the hidden Q32.32 values. */
+int aho_swiglu_quant_f32(const float *gate, const float *up, size_t n, int8_t *codes,
+                         int64_t *scales, int64_t *h);
 
 /* 1 when the host has AVX2 (the fast cores), else 0 (portable loops are used). */
 int aho_has_avx2(void);

@@ -1,32 +1,37 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized linear-layer path on one MI355X.
 
-Headline: Q4_K GEMV decode, N = 1, over the Qwen2.5-0.5B
-projection shapes.  One step is one token through a 24-layer stack of the seven projections
-(q 896x896, k/v 128x896, o 896x896, gate/up 4864x896, down 896x4864), each an f32 N(0,1) input
-quantized inside the kernel.  The weights of consecutive steps come from a rotating pool of
-layer copies larger than 1 GiB, so every step streams its weights from HBM (the 256 MB
-Infinity Cache is defeated), and the inputs are already resident in HBM.
+Headline (the largest single-GPU configuration): one decode token (N = 1)
+through every linear layer of a random-init Qwen2.5-1.5B-architecture model in the Q4_K_M-style mix
+(hidden 1536, 28 layers, KV width 256, FFN 8960, vocab 151936; Q4_K everywhere except Q6_K for
+attn_v, ffn_down on llama.cpp's use_more_bits layers and the output head).  One step is one token,
+run as a dependency-respecting sequence: per layer q/k/v (one grouped launch: they share their
+input) -> o -> gate/up (one grouped launch) -> down, then the head -- 113 dependent stage launches,
+each waiting for the previous one (stream order), replayed as one HIP graph per token.  The engine's
+own operations between stages (attention, RMSNorm, SwiGLU, residuals) are not on this path; each
+stage reads its own HBM-resident f32 input.  The 0.99 GB of weights per token is past the 256 MB
+Infinity Cache, so every token streams its weights from HBM.
 
-Dispatch modes (``--mode``):
-  token   (default) all 168 projections of a step in one grouped launch: the path's streaming
-          rate.  The projections of a token are independent here because their callers
-          (RMSNorm, attention, SwiGLU) are outside this path;
-  engine  the reference engine's dispatch shape per layer: one grouped launch for q/k/v
-          (shared input, chart/ffn.rs:925), o, one grouped launch for gate/up (shared input),
-          down -- 4 dependent launches per layer, captured in a HIP graph per step window.  This
-          is latency-bound (96 serialized kernels per token) and is reported beside the value.
+value = algorithmic bytes per token * steps / wall time (GB/s).  Algorithmic bytes per projection
+= n_out * (weight bytes a correct kernel must read per row) + 4*n_in (f32 input) + 4*n_out (f32
+output).
 
 Timing: the hot path first runs untimed for 150 ms (clock ramp-up of an idle GPU), then the W
 warm-up steps, then the K timed steps between two synchronizations.
 
-value = algorithmic bytes per step * steps / wall time (GB/s).  Algorithmic bytes per
-projection = n_out * (weight bytes a correct kernel must read per row) + 4*n_in (f32 input)
-+ 4*n_out (f32 output).
-
-Also reported: the dominant kernel against the 8 TB/s HBM roofline (HIP events on the launch
-stream), the N = 512 GEMMs of configs[3] against the 5.0 POPS dense int8 MFMA peak, and the
-CPU baseline (the restated reference fast path, oracle/ah_cpu_fast.c, on this host's cores).
+Also reported, beside the value:
+  roofline      the token's dominant kernel (the Q4_K stage launches, o / gate-up / Q4_K down:
+                most of a token's time) against the 8 TB/s HBM peak, HIP events on the launch
+                stream over those launches back to back;
+  decode        the same token as one persistent launch (ah_seq_*, with and without the fused
+                FFN's SwiGLU stage), as eager launches, and with its 197 projections batched as
+                independent parts (two launches: not a dependency-respecting token);
+  config1       BASELINE configs[1] (Qwen2.5-0.5B, 24 layers, Q4_K) as one batched launch;
+  gemm          configs[3] N = 512 GEMMs against the 5.0 POPS int8 MFMA peak, the MFMA-only probe,
+                and the configs[4] N = 512 prefill;
+  heads         configs[0] (Q8_0 4864x896) and configs[2] (151936x896 head, Q6_K and Q8_0);
+  cpu_baseline  the restated reference fast path (oracle/ah_cpu_fast.c) on the same token's
+                projections, on this host's cores; cpu_baseline_gemm the same for N = 512.
 """
 from __future__ import annotations
 
@@ -45,24 +50,26 @@ HBM_PEAK_GBS = 8000.0
 CLOCK_WARMUP_S = 0.15  # untimed hot-path load before the warm-up steps (clock ramp-up)
 INT8_PEAK_TOPS = 5000.0
 F16_PEAK_TFLOPS = 2500.0  # dense f16 MFMA peak (the instruction the GEMM computes with)
-LAYERS = 24
-SHAPES = [("q", 896, 896), ("k", 128, 896), ("v", 128, 896), ("o", 896, 896),
-          ("gate", 4864, 896), ("up", 4864, 896), ("down", 896, 4864)]
+# Qwen2.5-0.5B projections
+CFG1_LAYERS = 24
+CFG1_SHAPES = [("q", 896, 896), ("k", 128, 896), ("v", 128, 896), ("o", 896, 896),
+               ("gate", 4864, 896), ("up", 4864, 896), ("down", 896, 4864)]
 GEMM_SHAPES = [(4864, 896), (896, 4864), (8960, 1536), (1536, 8960)]
 # Qwen2.5-1.5B architecture, Q4_K_M-style mix (Q6_K for attn_v, for ffn_down on
 # llama.cpp's use_more_bits layers, and for the output head)
 CFG4_LAYERS = 28
 CFG4_Q6K_DOWN = {0, 1, 2, 5, 8, 11, 14, 17, 20, 23, 24, 25, 26, 27}
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_config4_token.md")
 
 
-def cfg4_projections(synth):
-    out = []
-    for l in range(CFG4_LAYERS):
-        out += [(synth.Q4_K, 1536, 1536), (synth.Q4_K, 256, 1536), (synth.Q6_K, 256, 1536),
-                (synth.Q4_K, 1536, 1536), (synth.Q4_K, 8960, 1536), (synth.Q4_K, 8960, 1536),
-                (synth.Q6_K if l in CFG4_Q6K_DOWN else synth.Q4_K, 1536, 8960)]
-    out.append((synth.Q6_K, 151936, 1536))  # output head
-    return out
+def cfg4_layer(synth, l):
+    """configs[4] layer l: (name, ggml type, n_out, n_in) in the engine's projection order."""
+    return [("q", synth.Q4_K, 1536, 1536), ("k", synth.Q4_K, 256, 1536), ("v", synth.Q6_K, 256, 1536),
+            ("o", synth.Q4_K, 1536, 1536), ("gate", synth.Q4_K, 8960, 1536), ("up", synth.Q4_K, 8960, 1536),
+            ("down", synth.Q6_K if l in CFG4_Q6K_DOWN else synth.Q4_K, 1536, 8960)]
+
+
+CFG4_STAGES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
 
 
 def log(*a):
@@ -73,20 +80,40 @@ def proj_bytes(synth, t, n_out, n_in):
     return n_out * synth.needed_row_bytes(t, n_in) + 4 * n_in + 4 * n_out
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_stream_q4k_config1_token.md")
-
-
-def measured_traffic():
-    """HBM bytes per token-plan launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs
-    (copy-calibrated; the counters cannot be read from inside this process), or None."""
+def profile_value(key, cast=float):
+    """A figure of the roofline kernel from the committed rocprofv3 summary: the HBM bytes per
+    launch from its FETCH_SIZE / WRITE_SIZE runs (copy-calibrated; the counters cannot be read from
+    inside this process) or its kernel-only average duration; None when not committed."""
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1])
+                if line.startswith(key + ":"):
+                    return cast(line.split(":", 1)[1])
     except OSError:
         pass
     return None
+
+
+def cpu_flags():
+    try:
+        for l in open("/proc/cpuinfo"):
+            if l.startswith("flags"):
+                f = set(l.split(":", 1)[1].split())
+                return {"avx2": "avx2" in f, "avx_vnni": "avx_vnni" in f, "avx512f": "avx512f" in f,
+                        "avx512_vnni": "avx512_vnni" in f}
+    except OSError:
+        pass
+    return {}
+
+
+def _cpu_name() -> str:
+    try:
+        for l in open("/proc/cpuinfo"):
+            if l.startswith("model name"):
+                return l.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main() -> int:
@@ -94,15 +121,13 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--mode", choices=["engine", "token"], default="token")
-    ap.add_argument("--pool-gib", type=float, default=1.1)
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-heads", action="store_true", help="skip configs[0] and configs[2]")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--no-extras", action="store_true", help="headline only (decode token + roofline)")
+    ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--cpu-threads", type=int, default=8)
-    ap.add_argument("--only", choices=["gemv", "gemm", "copy", "config4", "heads"], default=None)
-    ap.add_argument("--no-config4", action="store_true")
+    ap.add_argument("--only", choices=["decode", "gemm", "config1", "heads", "copy"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
@@ -117,8 +142,10 @@ def main() -> int:
     dev = chart.Device(0)
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
-    t = synth.Q4_K
     result: dict = {}
+
+    def ptr(x):
+        return x.data_ptr()
 
     if args.only == "copy":
         # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain 256 MiB copy
@@ -130,218 +157,291 @@ def main() -> int:
         print(json.dumps({"copy_bytes": a.numel()}))
         return 0
 
-    # ---- config 1: weight pool ------------------------------------------------------------
-    layer_bytes_stored = sum(n * synth.row_bytes(t, k) for _, n, k in SHAPES)
-    n_sets = max(LAYERS + 8, int(args.pool_gib * (1 << 30) // layer_bytes_stored) + 1)
-    n_unique = 4
-    log(f"[bench] pool: {n_sets} layer copies x {layer_bytes_stored / 1e6:.2f} MB = "
-        f"{n_sets * layer_bytes_stored / 2**30:.2f} GiB")
-    host_layers = []
-    for u in range(n_unique):
-        rng = synth.rng_for(1, 100 + u)
-        host_layers.append({name: synth.payload(t, rng, n, k) for name, n, k in SHAPES})
-    rng = synth.rng_for(1, 1)
-    xin = {name: torch.from_numpy(synth.activations(rng, k)).cuda() for name, _, k in SHAPES}
-    layers = []
-    for i in range(n_sets):
-        src = host_layers[i % n_unique]
-        layers.append({name: dev.upload(t, src[name], n, k) for name, n, k in SHAPES})
-    outs = {name: torch.zeros(n, dtype=torch.float32, device="cuda") for name, n, _ in SHAPES}
-    step_bytes = LAYERS * sum(proj_bytes(synth, t, n, k) for _, n, k in SHAPES)
-    x_attn, x_ffn = xin["q"], xin["gate"]
-
-    def ptr(x):
-        return x.data_ptr()
-
-    # ---- config 1: dispatch ---------------------------------------------------------------
-    plans = []
-    if args.mode == "engine":
-        qkv = [chart.GemvPlan(dev, [L["q"], L["k"], L["v"]], [ptr(x_attn)] * 3,
-                              [ptr(outs["q"]), ptr(outs["k"]), ptr(outs["v"])]) for L in layers]
-        gu = [chart.GemvPlan(dev, [L["gate"], L["up"]], [ptr(x_ffn)] * 2,
-                             [ptr(outs["gate"]), ptr(outs["up"])]) for L in layers]
-        plans = qkv + gu
-
-        def layer_launch(i, s):
-            L = layers[i]
-            qkv[i].run(s)
-            L["o"].gemv_f32_dev(ptr(xin["o"]), ptr(outs["o"]), s)
-            gu[i].run(s)
-            L["down"].gemv_f32_dev(ptr(xin["down"]), ptr(outs["down"]), s)
-
-        n_windows = -(-n_sets // LAYERS)
-        graphs = []
-        cap = torch.cuda.Stream()
-        for wdx in range(n_windows):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=cap):
-                s = torch.cuda.current_stream().cuda_stream
-                for l in range(LAYERS):
-                    layer_launch((wdx * LAYERS + l) % n_sets, s)
-            graphs.append(g)
-        torch.cuda.synchronize()
-
-        def step(i):
-            graphs[i % n_windows].replay()
-        launches_per_step = 4 * LAYERS
-    else:
-        n_windows = -(-n_sets // LAYERS)
-        for wdx in range(n_windows):
-            ws, xs, ys = [], [], []
-            for l in range(LAYERS):
-                L = layers[(wdx * LAYERS + l) % n_sets]
-                for name, _, _ in SHAPES:
-                    ws.append(L[name]), xs.append(ptr(xin[name])), ys.append(ptr(outs[name]))
-            plans.append(chart.GemvPlan(dev, ws, xs, ys))
-
-        def step(i):
-            plans[i % n_windows].run(sh)
-        launches_per_step = 1
-
-    if args.only in (None, "gemv"):
-        # Clock warm-up, untimed and before the W warm-up steps: an idle MI355X needs tens of ms of
-        # load to reach its sustained clocks (20 steps ~ 1 ms left the timed region 15% slow), so
-        # the hot path runs until CLOCK_WARMUP_S have passed.  Steady-state throughput is what a
-        # busy serving GPU sees; the JSON line records the warm-up.
+    def clock_up(fn, seconds=CLOCK_WARMUP_S):
         t_w = time.perf_counter()
-        n_clock = 0
-        while time.perf_counter() - t_w < CLOCK_WARMUP_S:
-            for _ in range(100):
-                step(n_clock)
-                n_clock += 1
+        while time.perf_counter() - t_w < seconds:
+            for _ in range(10):
+                fn()
             torch.cuda.synchronize()
-        for i in range(args.warmup):
-            step(i)
+
+    def event_us(fn, reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / reps
+
+    # ---- weights (one device copy per projection, 0.99 GB) --------------------------
+    run_decode = args.only in (None, "decode")
+    run_prefill = args.only in (None, "gemm") and not args.no_gemm and not args.no_extras
+    if run_decode or run_prefill:
+        host = {}
+        spec = [cfg4_layer(synth, l) for l in range(CFG4_LAYERS)]
+        for layer in spec:
+            for _, gt, n_out, n_in in layer:
+                if (gt, n_out, n_in) not in host:
+                    host[(gt, n_out, n_in)] = synth.payload(gt, synth.rng_for(4, gt * 100000 + n_out + n_in), n_out, n_in)
+        head_key = (synth.Q6_K, 151936, 1536)
+        host[head_key] = synth.payload(synth.Q6_K, synth.rng_for(4, 7), 151936, 1536)
+        W = [{nm: (gt, n_out, n_in, dev.upload(gt, host[(gt, n_out, n_in)], n_out, n_in))
+              for nm, gt, n_out, n_in in layer} for layer in spec]
+        head = dev.upload(synth.Q6_K, host[head_key], 151936, 1536)
+        tok_bytes = sum(proj_bytes(synth, gt, n_out, n_in) for layer in spec for _, gt, n_out, n_in in layer)
+        tok_bytes += proj_bytes(synth, *head_key)
+        rng = synth.rng_for(4, 1)
+        X = {nm: torch.from_numpy(synth.activations(rng, k)).cuda()
+             for nm, k in (("attn", 1536), ("o", 1536), ("ffn", 1536), ("down", 8960), ("head", 1536))}
+        Y = {nm: torch.zeros(n, dtype=torch.float32, device="cuda")
+             for nm, n in (("q", 1536), ("k", 256), ("v", 256), ("o", 1536), ("gate", 8960), ("up", 8960),
+                           ("down", 1536), ("head", 151936))}
+        src = {"q": "attn", "k": "attn", "v": "attn", "o": "o", "gate": "ffn", "up": "ffn", "down": "down"}
+
+    if run_decode:
+        # the token's 113 dependent stages, one plan (one launch) each
+        plans, kinds = [], []
+        for L in W:
+            for kind, names in CFG4_STAGES:
+                plans.append(chart.GemvPlan(dev, [L[n][3] for n in names], [ptr(X[src[n]]) for n in names],
+                                            [ptr(Y[n]) for n in names]))
+                kinds.append((kind, sum(proj_bytes(synth, *L[n][:3]) for n in names),
+                              tuple(sorted({L[n][0] for n in names}))))
+        plans.append(chart.GemvPlan(dev, [head], [ptr(X["head"])], [ptr(Y["head"])]))
+        kinds.append(("head", proj_bytes(synth, *head_key), (synth.Q6_K,)))
+
+        def token_eager():
+            for p in plans:
+                p.run(sh)
+
+        token_eager()
+        torch.cuda.synchronize()
+        assert dev.sync_status(sh) == 0
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        with torch.cuda.graph(graph, stream=cap):
+            s_cap = torch.cuda.current_stream().cuda_stream
+            for p in plans:
+                p.run(s_cap)
+        torch.cuda.synchronize()
+        step = graph.replay
+
+        clock_up(step)
+        for _ in range(args.warmup):
+            step()
         torch.cuda.synchronize()
         assert dev.sync_status(sh) == 0
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         ev0.record(stream)
-        for i in range(args.steps):
-            step(i)
+        for _ in range(args.steps):
+            step()
         ev1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         ev_ms = ev0.elapsed_time(ev1)
+        assert dev.sync_status(sh) == 0
         ms_per_step = wall * 1e3 / args.steps
-        value = step_bytes * args.steps / wall / 1e9
-        log(f"[bench] config1 {args.mode}: {ms_per_step * 1e3:.1f} us/step, {value:.0f} GB/s wall, "
-            f"{step_bytes * args.steps / (ev_ms / 1e3) / 1e9:.0f} GB/s events")
+        value = tok_bytes * args.steps / wall / 1e9
+        log(f"[bench] configs[4] decode token (graph of {len(plans)} dependent stage launches): "
+            f"{ms_per_step * 1e3:.1f} us/token, {value:.0f} GB/s wall, "
+            f"{tok_bytes * args.steps / (ev_ms / 1e3) / 1e9:.0f} GB/s events")
 
-        # dominant kernel.  token: the plan launch, one per step, timed by the events over the timed
-        # region.  engine: the per-layer launch with the most time, HIP events around each launch
-        # on the launch stream (eager launches, rotating layers).
-        kinds = {}
-        if args.mode == "engine":
-            kinds = {
-                "qkv": (lambda i, s: qkv[i].run(s),
-                        sum(proj_bytes(synth, t, n, k) for nm, n, k in SHAPES if nm in ("q", "k", "v"))),
-                "o": (lambda i, s: layers[i]["o"].gemv_f32_dev(ptr(xin["o"]), ptr(outs["o"]), s),
-                      proj_bytes(synth, t, 896, 896)),
-                "gate_up": (lambda i, s: gu[i].run(s), 2 * proj_bytes(synth, t, 4864, 896)),
-                "down": (lambda i, s: layers[i]["down"].gemv_f32_dev(ptr(xin["down"]), ptr(outs["down"]), s),
-                         proj_bytes(synth, t, 896, 4864)),
-            }
+        # Per stage kind: the kind's launches back to back in token order (eager, HIP events on the
+        # launch stream over 4 passes).  The roofline kernel is gemv_stream_kernel<Q4_K> (plan form):
+        # the o, gate/up and Q4_K down launches, which take most of a token.
         per_kind = {}
-        if args.mode == "token":
-            # one launch per step: the timed region's events give the launch duration directly
-            us = ev_ms * 1e3 / args.steps
-            per_kind["token_plan"] = {"us": us, "bytes": step_bytes, "gbs": step_bytes / us / 1e3}
-        reps = 64
-        for name, (fn, nbytes) in kinds.items():
-            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for _ in range(reps)]
-            for i in range(8):
-                fn(i % n_sets, sh)
-            torch.cuda.synchronize()
-            for i, (a, b) in enumerate(evs):
-                a.record(stream)
-                fn((i * 7) % n_sets if args.mode == "engine" else i, sh)
-                b.record(stream)
-            torch.cuda.synchronize()
-            us = float(np.mean([a.elapsed_time(b) for a, b in evs[4:]])) * 1e3
-            per_kind[name] = {"us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3}
-        dom = max(per_kind, key=lambda k: per_kind[k]["us"])
-        d = per_kind[dom]
-        result["gemv"] = {
-            "mode": args.mode, "launches_per_step": launches_per_step,
-            "step_bytes": step_bytes, "ms_per_step": ms_per_step, "gbs_wall": value,
-            "gbs_events": step_bytes * args.steps / (ev_ms / 1e3) / 1e9,
-            "pool_gib": n_sets * layer_bytes_stored / 2**30,
-            "kernels": per_kind,
-        }
-        result["_value"] = value
-        result["_ms"] = ms_per_step
-        traffic = measured_traffic() if args.mode == "token" else None
-        result["roofline"] = {"bound": "hbm",
-                              "kernel": ("gemv_stream_kernel<Q4_K> (token plan: 168 projections per launch)"
-                                         if args.mode == "token" else f"gemv_stream_kernel<Q4_K> ({dom})"),
-                              "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                              "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                              "bytes_per_launch": d["bytes"], "us_per_launch": round(d["us"], 3)}
+        for kind in ("qkv", "o", "gate_up", "down", "head"):
+            idx = [i for i, k in enumerate(kinds) if k[0] == kind]
+            reps = 4 if kind != "head" else 40
+            us = event_us(lambda: [plans[i].run(sh) for i in idx], reps) / len(idx)
+            nbytes = sum(kinds[i][1] for i in idx) / len(idx)
+            per_kind[kind] = {"launches_per_token": len(idx), "us_per_launch": round(us, 2),
+                              "bytes_per_launch": int(nbytes), "gbs": round(nbytes / us / 1e3, 1),
+                              "us_per_token": round(us * len(idx), 1)}
+        q4 = [i for i, k in enumerate(kinds) if k[2] == (synth.Q4_K,)]
+        us_q4 = event_us(lambda: [plans[i].run(sh) for i in q4], 4) / len(q4)
+        b_q4 = sum(kinds[i][1] for i in q4) / len(q4)
+        assert dev.sync_status(sh) == 0
+        traffic = profile_value("traffic_bytes_per_launch", int)
+        result["roofline"] = {
+            "bound": "hbm",
+            "kernel": f"gemv_stream_kernel<Q4_K> plan launches of the token ({len(q4)} per token: "
+                      "o, gate/up and the Q4_K down projections)",
+            "achieved": round(b_q4 / us_q4 / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(b_q4 / us_q4 / 1e3 / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "bytes_per_launch": int(b_q4), "us_per_launch": round(us_q4, 3),
+            "note": "us_per_launch: HIP events over the launches back to back, dispatch gaps between "
+                    "dependent launches included; traffic and kernel_us_profile: the committed rocprofv3 "
+                    "summary (profiles/decode_config4_token.md)",
+            "kernel_us_profile": profile_value("kernel_us_per_launch")}
+        result["_value"], result["_ms"] = value, ms_per_step
+        decode = {"stages": len(plans), "bytes_per_token": tok_bytes, "us_per_token_graph": round(ms_per_step * 1e3, 1),
+                  "gbs_graph": round(value, 1), "gbs_events": round(tok_bytes * args.steps / (ev_ms / 1e3) / 1e9, 1),
+                  "per_stage_kind": per_kind}
 
-    for p in plans:
-        p.free()
+        if not args.no_extras:
+            reps = 20
+            decode["us_per_token_eager"] = round(event_us(token_eager, reps), 1)
+            # one persistent launch per token (ah_seq_*): the same stages; and with the fused FFN's
+            # SwiGLU stage between gate/up and down (down then reads the hidden QuantAct)
+            hc = torch.zeros(8960, dtype=torch.int8, device="cuda")
+            hs = torch.zeros(280, dtype=torch.int64, device="cuda")
+            for fused in (False, True):
+                stages = []
+                for L in W:
+                    part = lambda n, x=None: (L[n][3], x if x is not None else ptr(X[src[n]]), ptr(Y[n]))
+                    stages += [("gemv", [part("q"), part("k"), part("v")]), ("gemv", [part("o")]),
+                               ("gemv", [part("gate"), part("up")])]
+                    if fused:
+                        stages += [("swiglu", ptr(Y["gate"]), ptr(Y["up"]), 8960, ptr(hc), ptr(hs)),
+                                   ("gemv", [part("down", (ptr(hc), ptr(hs)))])]
+                    else:
+                        stages += [("gemv", [part("down")])]
+                stages.append(("gemv", [(head, ptr(X["head"]), ptr(Y["head"]))]))
+                seq = chart.Seq(dev, stages)
+                clock_up(lambda: seq.run(sh), 0.05)
+                us = event_us(lambda: seq.run(sh), reps)
+                st = seq.sync_status(sh)
+                assert st == (0, 0), st
+                decode["us_per_token_persistent" + ("_fused_ffn" if fused else "")] = round(us, 1)
+                seq.free()
+            # the 197 projections batched as independent parts, one launch per quant type (not a
+            # dependency-respecting token: the rate of the streaming kernel alone)
+            flat = [(L[n], n) for L in W for n in ("q", "k", "v", "o", "gate", "up", "down")]
+            by_type = []
+            for gt in (synth.Q4_K, synth.Q6_K):
+                sel = [(w, n) for w, n in flat if w[0] == gt]
+                ws = [w[3] for w, _ in sel] + ([head] if gt == synth.Q6_K else [])
+                xs = [ptr(X[src[n]]) for _, n in sel] + ([ptr(X["head"])] if gt == synth.Q6_K else [])
+                ys = [ptr(Y[n]) for _, n in sel] + ([ptr(Y["head"])] if gt == synth.Q6_K else [])
+                by_type.append(chart.GemvPlan(dev, ws, xs, ys))
+            clock_up(lambda: [p.run(sh) for p in by_type], 0.05)
+            us_b = event_us(lambda: [p.run(sh) for p in by_type], reps)
+            decode["us_per_token_independent_parts"] = round(us_b, 1)
+            decode["gbs_independent_parts"] = round(tok_bytes / us_b / 1e3, 1)
+            for p in by_type:
+                p.free()
+            assert dev.sync_status(sh) == 0
+            log(f"[bench] decode token: eager {decode['us_per_token_eager']} us, persistent "
+                f"{decode['us_per_token_persistent']} us, persistent with fused FFN "
+                f"{decode['us_per_token_persistent_fused_ffn']} us, independent parts {us_b:.1f} us")
+        result["decode"] = decode
+        for p in plans:
+            p.free()
 
-    # ---- config 3: N = 512 GEMMs ---------------------------------------------------------------
-    if not args.no_gemm and args.only in (None, "gemm"):
-        # The matrix-core ceiling measured on this device: MFMA-only loops on every CU.
-        probe = {"int8_tops": round(dev.probe_mfma_peak(0), 1),
-                 "f16_tflops": round(dev.probe_mfma_peak(1), 1)}
-        log(f"[bench] MFMA-only probe: int8 32x32x32 {probe['int8_tops']:.0f} TOPS "
-            f"({100 * probe['int8_tops'] / INT8_PEAK_TOPS:.1f}% of {INT8_PEAK_TOPS:.0f}), "
-            f"f16 32x32x16 {probe['f16_tflops']:.0f} TFLOPS "
-            f"({100 * probe['f16_tflops'] / F16_PEAK_TFLOPS:.1f}% of {F16_PEAK_TFLOPS:.0f})")
+    # ---- configs[4] prefill, N = 512: grouped GEMMs as a layer feeds them -------------------------
+    if run_prefill:
+        n_tok = 512
+        xs = {k: torch.from_numpy(synth.activations(rng, k, n_tok).reshape(n_tok, k)).cuda() for k in (1536, 8960)}
+        ys = {nm: torch.empty((n_tok, n), dtype=torch.float32, device="cuda")
+              for nm, n in (("q", 1536), ("k", 256), ("v", 256), ("o", 1536), ("gate", 8960), ("up", 8960),
+                            ("down", 1536), ("head", 151936))}
+        groups = []
+        for L in W:
+            for _, names in CFG4_STAGES:
+                groups.append(([L[n][3] for n in names], names[0] == "down", list(names)))
+        groups.append(([head], False, ["head"]))
+
+        def prefill():
+            for ws, is_down, outs in groups:
+                chart.gemm_group_f32_dev(dev, ws, ptr(xs[8960 if is_down else 1536]), n_tok,
+                                         [ptr(ys[n]) for n in outs], sh)
+        prefill()
+        torch.cuda.synchronize()
+        assert dev.sync_status(sh) == 0
+        ms_pre = event_us(prefill, 2) / 1e3
+        ops = sum(2.0 * n_tok * w[1] * w[2] for L in W for w in L.values()) + 2.0 * n_tok * 151936 * 1536
+        tops = ops / ms_pre / 1e9
+        log(f"[bench] configs[4] N=512 prefill: {ms_pre:.2f} ms ({len(groups)} grouped calls), {tops:.0f} TOPS "
+            f"= {100 * tops / INT8_PEAK_TOPS:.1f}% int8 peak")
+        result["config4_prefill"] = {"n_tok": n_tok, "ms": round(ms_pre, 3), "tops": round(tops, 1),
+                                     "grouped_calls": len(groups), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        del xs, ys
+    if run_decode or run_prefill:
+        for L in W:
+            for w in L.values():
+                w[3].free()
+        head.free()
+
+    # ---- N = 512 GEMMs ------------------------------------------------------------------
+    if args.only in (None, "gemm") and not args.no_gemm and not args.no_extras:
+        probe = {"int8_tops": round(dev.probe_mfma_peak(0), 1), "f16_tflops": round(dev.probe_mfma_peak(1), 1)}
+        log(f"[bench] MFMA-only probe: int8 32x32x32 {probe['int8_tops']:.0f} TOPS, "
+            f"f16 32x32x16 {probe['f16_tflops']:.0f} TFLOPS")
         result["mfma_probe"] = probe
         gemm = []
         n_tok = 512
         for gt in (synth.Q8_0, synth.Q4_K):
             for n_out, n_in in GEMM_SHAPES:
-                rng = synth.rng_for(3, gt * 10 + n_in)
-                raw = synth.payload(gt, rng, n_out, n_in)
-                w = dev.upload(gt, raw, n_out, n_in)
-                x = torch.from_numpy(synth.activations(rng, n_in, n_tok).reshape(n_tok, n_in)).cuda()
+                rng3 = synth.rng_for(3, gt * 10 + n_in)
+                w = dev.upload(gt, synth.payload(gt, rng3, n_out, n_in), n_out, n_in)
+                x = torch.from_numpy(synth.activations(rng3, n_in, n_tok).reshape(n_tok, n_in)).cuda()
                 codes = torch.empty((n_tok, n_in), dtype=torch.int8, device="cuda")
                 scales = torch.empty((n_tok, -(-n_in // 32)), dtype=torch.int64, device="cuda")
                 dev.quant_act_f32_dev(ptr(x), n_tok, n_in, ptr(codes), ptr(scales), sh)
                 y = torch.empty((n_tok, n_out), dtype=torch.float32, device="cuda")
-                t_w = time.perf_counter()  # clocks back up after the upload (untimed)
-                while time.perf_counter() - t_w < 0.03:
-                    for _ in range(5):
-                        w.gemm_q8_dev(ptr(codes), ptr(scales), n_tok, ptr(y), sh)
-                    torch.cuda.synchronize()
+                run = lambda: w.gemm_q8_dev(ptr(codes), ptr(scales), n_tok, ptr(y), sh)
+                clock_up(run, 0.03)
                 assert dev.sync_status(sh) == 0
-                reps = 50
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record(stream)
-                for _ in range(reps):
-                    w.gemm_q8_dev(ptr(codes), ptr(scales), n_tok, ptr(y), sh)
-                b.record(stream)
-                torch.cuda.synchronize()
-                us = a.elapsed_time(b) * 1e3 / reps
+                us = event_us(run, 50)
                 ops = 2.0 * n_tok * n_out * n_in
                 tops = ops / us / 1e6
-                wbytes = n_out * synth.needed_row_bytes(gt, n_in)
-                traffic = wbytes + 4.0 * n_tok * n_out + n_tok * n_in  # weights + f32 out + int8 codes
+                traffic = n_out * synth.needed_row_bytes(gt, n_in) + 4.0 * n_tok * n_out + n_tok * n_in
                 attain = min(INT8_PEAK_TOPS, ops / traffic * HBM_PEAK_GBS / 1e3)
-                gemm.append({"type": synth.NAMES[gt], "shape": [n_out, n_in], "n_tok": n_tok,
-                             "us": round(us, 2), "tops": round(tops, 1),
-                             "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                gemm.append({"type": synth.NAMES[gt], "shape": [n_out, n_in], "n_tok": n_tok, "us": round(us, 2),
+                             "tops": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                              "frac_f16_probe": round(tops / probe["f16_tflops"], 4),
-                             "attainable_tops": round(attain, 1),
-                             "frac_attainable": round(tops / attain, 4)})
-                log(f"[bench] gemm {synth.NAMES[gt]} {n_out}x{n_in} N{n_tok}: {us:.1f} us "
-                    f"{tops:.0f} TOPS ({100 * tops / INT8_PEAK_TOPS:.1f}% int8 peak, "
-                    f"{100 * tops / attain:.1f}% attainable)")
+                             "attainable_tops": round(attain, 1), "frac_attainable": round(tops / attain, 4)})
+                log(f"[bench] gemm {synth.NAMES[gt]} {n_out}x{n_in} N{n_tok}: {us:.1f} us {tops:.0f} TOPS "
+                    f"({100 * tops / INT8_PEAK_TOPS:.1f}% int8 peak)")
                 w.free()
         result["gemm"] = gemm
 
-    # ---- config 4: the 197 projections of a Qwen2.5-1.5B token (Q4_K + Q6_K), N = 1 and N = 512 ----
-    # ---- configs[0] (Q8_0 4864x896) and configs[2] (151936x896 vocab head, Q6_K and Q8_0) ------
-    # Single GEMV launches back to back over rotating weight copies of >= 1.1 GiB in all (the
-    # 256 MB Infinity Cache cannot serve them), f32 N(0,1) input quantized in the kernel.
-    if not args.no_heads and args.only in (None, "heads"):
+    # ---- the 168 projections of a Qwen2.5-0.5B token batched in one launch ------------
+    if args.only in (None, "config1") and not args.no_extras:
+        t = synth.Q4_K
+        layer_stored = sum(n * synth.row_bytes(t, k) for _, n, k in CFG1_SHAPES)
+        n_sets = max(CFG1_LAYERS + 8, int(1.1 * (1 << 30) // layer_stored) + 1)
+        host1 = [{nm: synth.payload(t, synth.rng_for(1, 100 + u), n, k) for nm, n, k in CFG1_SHAPES}
+                 for u in range(4)]
+        rng1 = synth.rng_for(1, 1)
+        xin = {nm: torch.from_numpy(synth.activations(rng1, k)).cuda() for nm, _, k in CFG1_SHAPES}
+        outs = {nm: torch.zeros(n, dtype=torch.float32, device="cuda") for nm, n, _ in CFG1_SHAPES}
+        L1 = [{nm: dev.upload(t, host1[i % 4][nm], n, k) for nm, n, k in CFG1_SHAPES} for i in range(n_sets)]
+        step1_bytes = CFG1_LAYERS * sum(proj_bytes(synth, t, n, k) for _, n, k in CFG1_SHAPES)
+        windows = []
+        for wdx in range(-(-n_sets // CFG1_LAYERS)):
+            ws, xs1, ys1 = [], [], []
+            for l in range(CFG1_LAYERS):
+                L = L1[(wdx * CFG1_LAYERS + l) % n_sets]
+                for nm, _, _ in CFG1_SHAPES:
+                    ws.append(L[nm]), xs1.append(ptr(xin[nm])), ys1.append(ptr(outs[nm]))
+            windows.append(chart.GemvPlan(dev, ws, xs1, ys1))
+        ctr = [0]
+
+        def step1():
+            windows[ctr[0] % len(windows)].run(sh)
+            ctr[0] += 1
+        clock_up(step1)
+        us1 = event_us(step1, 200)
+        assert dev.sync_status(sh) == 0
+        result["config1"] = {"us_per_token": round(us1, 2), "bytes_per_token": step1_bytes,
+                             "gbs": round(step1_bytes / us1 / 1e3, 1),
+                             "frac_hbm": round(step1_bytes / us1 / 1e3 / HBM_PEAK_GBS, 4),
+                             "launches_per_token": 1, "pool_gib": round(n_sets * layer_stored / 2 ** 30, 2),
+                             "note": "168 projections batched as independent parts in one launch"}
+        log(f"[bench] configs[1] batched token: {us1:.1f} us, {step1_bytes / us1 / 1e3:.0f} GB/s")
+        for p in windows:
+            p.free()
+        for L in L1:
+            for w in L.values():
+                w.free()
+        del L1
+
+    # ---- single GEMV launches over rotating copies --------------------
+    if args.only in (None, "heads") and not args.no_heads and not args.no_extras:
         singles = []
         for cfg, gt, n_out, n_in in ((0, synth.Q8_0, 4864, 896), (2, synth.Q6_K, 151936, 896),
                                      (2, synth.Q8_0, 151936, 896)):
@@ -351,170 +451,92 @@ def main() -> int:
             del raw
             x = torch.from_numpy(synth.activations(synth.rng_for(cfg, 99), n_in)).cuda()
             y = torch.empty(n_out, dtype=torch.float32, device="cuda")
-            t_w = time.perf_counter()
-            while time.perf_counter() - t_w < 0.05:  # clocks up after the uploads (untimed)
-                for i in range(copies):
-                    wc[i].gemv_f32_dev(ptr(x), ptr(y), sh)
-                torch.cuda.synchronize()
+            ctr = [0]
+
+            def one():
+                wc[ctr[0] % copies].gemv_f32_dev(ptr(x), ptr(y), sh)
+                ctr[0] += 1
+            clock_up(one, 0.05)
             assert dev.sync_status(sh) == 0
-            reps = 400 if n_out < 100000 else 60
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for i in range(reps):
-                wc[i % copies].gemv_f32_dev(ptr(x), ptr(y), sh)
-            b.record(stream)
-            torch.cuda.synchronize()
-            us = a.elapsed_time(b) * 1e3 / reps
+            us = event_us(one, 400 if n_out < 100000 else 60)
             nbytes = proj_bytes(synth, gt, n_out, n_in)
             gbs = nbytes / us / 1e3
-            singles.append({"config": cfg, "type": synth.NAMES[gt], "shape": [n_out, n_in],
-                            "copies": copies, "us": round(us, 2), "bytes": nbytes,
-                            "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
-            log(f"[bench] config{cfg} {synth.NAMES[gt]} {n_out}x{n_in}: {us:.2f} us/launch, {gbs:.0f} GB/s "
-                f"= {100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s ({copies} rotating copies)")
+            singles.append({"config": cfg, "type": synth.NAMES[gt], "shape": [n_out, n_in], "copies": copies,
+                            "us": round(us, 2), "bytes": nbytes, "gbs": round(gbs, 1),
+                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+            log(f"[bench] configs[{cfg}] {synth.NAMES[gt]} {n_out}x{n_in}: {us:.2f} us/launch, {gbs:.0f} GB/s")
             for w in wc:
                 w.free()
             del wc
         result["heads"] = singles
 
-    if not args.no_config4 and args.only in (None, "config4"):
-        projs = cfg4_projections(synth)
-        host = {}
-        for (gt, n_out, n_in) in set(projs):
-            host[(gt, n_out, n_in)] = synth.payload(gt, synth.rng_for(4, gt * 100000 + n_out + n_in), n_out, n_in)
-        ws = [dev.upload(gt, host[(gt, n_out, n_in)], n_out, n_in) for gt, n_out, n_in in projs]
-        del host
-        tok_bytes = sum(proj_bytes(synth, gt, n_out, n_in) for gt, n_out, n_in in projs)
-        rng = synth.rng_for(4, 1)
-        x1 = {k: torch.from_numpy(synth.activations(rng, k)).cuda() for k in (1536, 8960)}
-        y1 = {}
-        for gt, n_out, n_in in projs:
-            y1.setdefault(n_out, torch.zeros(n_out, dtype=torch.float32, device="cuda"))
-        # N = 1: the token's 197 projections as one launch per quant type (the projections of a
-        # token are independent here, as in configs[1]), and for comparison as one mixed-type
-        # launch; the 0.98 GB of weights per token is past the 256 MB Infinity Cache
-        mixed = [chart.GemvPlan(dev, ws, [ptr(x1[p[2]]) for p in projs], [ptr(y1[p[1]]) for p in projs])]
-        by_type = []
-        for gt in (synth.Q4_K, synth.Q6_K):
-            idx = [i for i, p in enumerate(projs) if p[0] == gt]
-            by_type.append(chart.GemvPlan(dev, [ws[i] for i in idx], [ptr(x1[projs[i][2]]) for i in idx],
-                                          [ptr(y1[projs[i][1]]) for i in idx]))
-
-        def tok_us(plans, reps=20):
-            for _ in range(3):
-                for p in plans:
-                    p.run(sh)
-            torch.cuda.synchronize()
-            assert dev.sync_status(sh) == 0
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for _ in range(reps):
-                for p in plans:
-                    p.run(sh)
-            b.record(stream)
-            torch.cuda.synchronize()
-            return a.elapsed_time(b) * 1e3 / reps
-        tok_us(by_type)  # clocks up
-        us_mixed = min(tok_us(mixed), tok_us(mixed))
-        us_tok = min(tok_us(by_type), tok_us(by_type))
-        gbs = tok_bytes / us_tok / 1e3
-        log(f"[bench] config4 N=1: {us_tok:.1f} us/token ({len(projs)} projections, one launch per type), "
-            f"{gbs:.0f} GB/s = {100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s; one mixed-type launch: {us_mixed:.1f} us")
-        for p in mixed + by_type:
-            p.free()
-        # N = 512: one GEMM per projection, f32 inputs quantized in the operand pass
-        n_tok = 512
-        xs = {k: torch.from_numpy(synth.activations(rng, k, n_tok).reshape(n_tok, k)).cuda() for k in (1536, 8960)}
-        ys = {}
-        for gt, n_out, n_in in projs:
-            ys.setdefault(n_out, torch.empty((n_tok, n_out), dtype=torch.float32, device="cuda"))
-
-        # one grouped call per shared input, as a layer feeds them: q/k/v (the attention input),
-        # o, gate/up (the FFN input), down; the head alone.  7 projections -> 4 operand passes.
-        groups, i = [], 0
-        while i < len(projs):
-            n = 3 if i % 7 == 0 and i + 3 <= len(projs) - 1 else 2 if i % 7 == 4 else 1
-            groups.append(list(range(i, i + n)))
-            i += n
-
-        def prefill():
-            for g in groups:
-                n_in = projs[g[0]][2]
-                chart.gemm_group_f32_dev(dev, [ws[j] for j in g], ptr(xs[n_in]), n_tok,
-                                         [ptr(ys[projs[j][1]]) for j in g], sh)
-        prefill()
-        torch.cuda.synchronize()
-        assert dev.sync_status(sh) == 0
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(2):
-            prefill()
-        b.record(stream)
-        torch.cuda.synchronize()
-        ms_pre = a.elapsed_time(b) / 2
-        ops = sum(2.0 * n_tok * n_out * n_in for _, n_out, n_in in projs)
-        tops = ops / ms_pre / 1e9
-        log(f"[bench] config4 N=512: {ms_pre:.2f} ms/prefill ({len(projs)} GEMMs in {len(groups)} grouped "
-            f"calls, one operand pass each), {tops:.0f} TOPS = "
-            f"{100 * tops / INT8_PEAK_TOPS:.1f}% int8 peak")
-        result["config4"] = {"projections": len(projs), "n1_us_per_token": round(us_tok, 1),
-                             "n1_bytes_per_token": tok_bytes, "n1_gbs": round(gbs, 1),
-                             "n1_frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "n1_launches": 2,
-                             "n1_us_one_mixed_launch": round(us_mixed, 1),
-                             "n512_ms": round(ms_pre, 3), "n512_tops": round(tops, 1),
-                             "n512_grouped_calls": len(groups),
-                             "n512_frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
-        for w in ws:
-            w.free()
-        del xs, ys, x1, y1
-
-    # ---- CPU baseline: the same config-1 step on the host (restated reference fast path) ----------
-    if not args.no_cpu and args.only in (None, "gemv"):
+    # ---- CPU baselines: the same token (and N = 512 sample) on the host ---------------------------
+    if run_decode and not args.no_cpu:
         import oracle
 
-        threads = max(1, min(args.cpu_threads, os.cpu_count() or 1))
-        xq = {}
-        for name, _, k in SHAPES:
-            xq[name] = xin[name].cpu().numpy()
+        # distinct host copies of the layer payloads past the host LLC, rotated, plus the head
+        n_copies = 8  # one host copy per projection of layers 0..7, rotated (~230 MB)
+        copies = [{nm: host[(gt, n_out, n_in)].copy() for nm, gt, n_out, n_in in spec[i]} for i in range(n_copies)]
+        xa = synth.activations(synth.rng_for(4, 2), 1536)
+        xd = synth.activations(synth.rng_for(4, 3), 8960)
+        st, ca, sa = oracle.quant_act_f32(xa)
+        st, cd, sd = oracle.quant_act_f32(xd)
 
-        def cpu_step(li):
-            src = host_layers[li % n_unique]
-            st, c_attn, s_attn = oracle.quant_act_f32(xq["q"])
-            for name in ("q", "k", "v"):
-                n, k = next((n, k) for nm, n, k in SHAPES if nm == name)
-                oracle.matvec_q8act_fast(t, src[name], n, k, c_attn, s_attn, threads)
-            st, c, s = oracle.quant_act_f32(xq["o"])
-            oracle.matvec_q8act_fast(t, src["o"], 896, 896, c, s, threads)
-            st, c, s = oracle.quant_act_f32(xq["gate"])
-            oracle.matvec_q8act_fast(t, src["gate"], 4864, 896, c, s, threads)
-            oracle.matvec_q8act_fast(t, src["up"], 4864, 896, c, s, threads)
-            st, c, s = oracle.quant_act_f32(xq["down"])
-            oracle.matvec_q8act_fast(t, src["down"], 896, 4864, c, s, threads)
+        def cpu_layer(li, threads):
+            P = copies[li % n_copies]
+            nbytes = 0
+            for nm, gt, n_out, n_in in spec[li % n_copies]:
+                c, s = (cd, sd) if n_in == 8960 else (ca, sa)
+                oracle.matvec_q8act_fast(gt, P[nm], n_out, n_in, c, s, threads)
+                nbytes += proj_bytes(synth, gt, n_out, n_in)
+            return nbytes
 
-        # host pool: distinct copies past the host LLC, like the GPU pool
-        host_pool = [{nm: host_layers[i % n_unique][nm].copy() for nm, _, _ in SHAPES}
-                     for i in range(48)]
-        host_layers = host_pool
-        n_unique = len(host_pool)
-        cpu_step(0)
-        layers_done = 0
-        t0 = time.perf_counter()
-        while time.perf_counter() - t0 < args.cpu_seconds:
-            cpu_step(layers_done)
-            layers_done += 1
-        el = time.perf_counter() - t0
-        layer_bytes = step_bytes / LAYERS
-        cpu_gbs = layers_done * layer_bytes / el / 1e9
+        def cpu_head(threads):
+            oracle.matvec_q8act_fast(synth.Q6_K, host[head_key], 151936, 1536, ca, sa, threads)
+            return proj_bytes(synth, *head_key)
+
+        runs = []
+        for threads in sorted({max(1, min(args.cpu_threads, os.cpu_count() or 1)), os.cpu_count() or 1}):
+            cpu_layer(0, threads)
+            t0, nbytes, nl = time.perf_counter(), 0, 0
+            while time.perf_counter() - t0 < args.cpu_seconds:
+                nbytes += cpu_layer(nl, threads)
+                nl += 1
+                if nl % CFG4_LAYERS == 0:
+                    nbytes += cpu_head(threads)
+            el = time.perf_counter() - t0
+            runs.append({"threads": threads, "gbs": round(nbytes / el / 1e9, 2), "layers": nl, "seconds": round(el, 1)})
+            log(f"[bench] cpu baseline: {nbytes / el / 1e9:.1f} GB/s on {threads} threads ({nl} layers)")
+        best = runs[0]
         result["cpu_baseline"] = {
-            "value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{layers_done} layers ({layers_done / LAYERS:.1f} config-1 steps) of the 7 Q4_K "
-                      f"projections, f32 input quantized per call, {el:.1f} s on {threads} threads, "
-                      f"48 rotating layer copies ({48 * layer_bytes_stored / 2**30:.2f} GiB)",
-            "cpu": _cpu_name(), "host_cpus": os.cpu_count(),
-        }
-        log(f"[bench] cpu baseline: {cpu_gbs:.1f} GB/s on {threads} threads")
+            "value": best["gbs"], "unit": "GB/s", "cores": best["threads"], "kind": "port",
+            "sample": f"{best['layers']} configs[4] layers ({best['layers'] / CFG4_LAYERS:.1f} tokens, the head "
+                      f"once per 28 layers), f32 input quantized once per input width, {best['seconds']} s, "
+                      f"{n_copies} rotating host copies of the layer payloads",
+            "cpu": _cpu_name(), "host_cpus": os.cpu_count(), "cpu_flags": cpu_flags(), "runs": runs}
+        del copies
+    if args.only in (None, "gemm") and not args.no_cpu and not args.no_gemm and not args.no_extras:
+        import oracle
 
-    if args.only not in (None, "gemv"):
+        cg = []
+        for gt in (synth.Q8_0, synth.Q4_K):
+            for n_out, n_in in ((4864, 896), (8960, 1536)):
+                raw = synth.payload(gt, synth.rng_for(3, gt * 10 + n_in), n_out, n_in)
+                k = 32  # a bounded sample of the N = 512 token columns
+                x = synth.activations(synth.rng_for(3, 5), n_in, k).reshape(k, n_in)
+                st, codes, scales = oracle.quant_act_f32_batch(x)
+                threads = max(1, min(args.cpu_threads, os.cpu_count() or 1))
+                oracle.matmat_q8act_fast(gt, raw, n_out, n_in, codes[:2], scales[:2], threads)
+                t0 = time.perf_counter()
+                oracle.matmat_q8act_fast(gt, raw, n_out, n_in, codes, scales, threads)
+                el = time.perf_counter() - t0
+                gops = 2.0 * k * n_out * n_in / el / 1e9
+                cg.append({"type": synth.NAMES[gt], "shape": [n_out, n_in], "columns": k, "threads": threads,
+                           "seconds": round(el, 3), "gops": round(gops, 1)})
+        result["cpu_baseline_gemm"] = cg
+        log(f"[bench] cpu gemm baseline: {[c['gops'] for c in cg]} GOPS")
+
+    if not run_decode:
         print(json.dumps(result))
         return 0
 
@@ -530,33 +552,25 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8xQ4_K (exact int32 group dots, f32 fold)",
-        "data": "synthetic (BASELINE.json configs[1] distributions, seeded)",
-        "config": {"workload": "configs[1]: Q4_K GEMV decode N=1, Qwen2.5-0.5B projections "
-                               "(q,k,v,o,gate,up,down) x 24 layers per step, weights rotated "
-                               f"through a {result['gemv']['pool_gib']:.2f} GiB pool",
-                   "mode": args.mode, "parallelism": "single GPU"},
+        "dtype": "int8 x Q4_K/Q6_K (exact int32 group dots, f32 fold)",
+        "data": "synthetic (BASELINE.json configs[4] distributions, random-init weights, seeded)",
+        "config": {"workload": "configs[4]: one decode token (N=1) of a Qwen2.5-1.5B-architecture Q4_K_M-style "
+                               "model, 197 projections as 113 dependent stages (q/k/v -> o -> gate/up -> down "
+                               "per layer, then the Q6_K vocab head), one HIP graph per token",
+                   "parallelism": "single GPU"},
         "roofline": result["roofline"],
         "cpu_baseline": result.get("cpu_baseline"),
-        "gemv": result["gemv"],
+        "decode": result.get("decode"),
+        "config4_prefill": result.get("config4_prefill"),
         "gemm": result.get("gemm"),
         "mfma_probe": result.get("mfma_probe"),
-        "config4": result.get("config4"),
+        "config1": result.get("config1"),
         "config0_config2": result.get("heads"),
+        "cpu_baseline_gemm": result.get("cpu_baseline_gemm"),
     }
     print(json.dumps(line))
     dev.close()
     return 0
-
-
-def _cpu_name() -> str:
-    try:
-        for l in open("/proc/cpuinfo"):
-            if l.startswith("model name"):
-                return l.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
 
 
 if __name__ == "__main__":

@@ -26,7 +26,7 @@ size_t ah_gemv_act_bytes(uint32_t kpad);
 size_t ah_gemv_stream_slot_bytes();
 uint32_t ah_gemv_stream_threads();
 int ah_gemv_stream_occupancy(uint32_t type, size_t lds);
-hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const GemvPart *d_parts,
+hipError_t ah_launch_gemv_stream(uint32_t type, const StreamParts &sp, const GemvPart *d_parts,
                                  const StreamWG *d_wgd, uint32_t grid, uint32_t act_bytes,
                                  unsigned long long *status, hipStream_t stream);
 hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream);
@@ -84,6 +84,8 @@ struct ah_tensor {
 struct ah_gemv_plan {
     uint32_t type = 0, n_parts = 0, grid = 0, kpad_max = 0, nc = 4;
     bool stream = false;  // streaming kernel (else the workgroup-tile kernel)
+    bool arg_parts = false;        // streaming, parts in the kernel arguments (sp; no tables)
+    StreamParts sp = {};
     uint32_t act_bytes = 0;        // streaming: LDS activation region of a workgroup
     GemvPart *d_parts = nullptr;   // part descriptors
     uint32_t *d_wg_part = nullptr; // workgroup-tile kernel: workgroup -> part index
@@ -409,13 +411,16 @@ int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
         return AH_ERR_INVALID_ARG;
     if (w->n_out == 0) return AH_OK;
     bool st = false;
-    GemvPart P = make_part(w, src, x, scales, y, dots, st);
+    StreamParts sp = {};
+    sp.n = 1;
+    GemvPart &P = sp.p[0];
+    P = make_part(w, src, x, scales, y, dots, st);
     const uint32_t kp = kpad_of(w->n_in);
     AH_HIP(ctx, hipSetDevice(ctx->device));
     const uint32_t grid = deal_wgs(&P, 1, resident_wgs(ctx, w->type, st, kp), st);
     if (grid == 0) return AH_ERR_OUT_OF_MEMORY;
     if (st)
-        AH_HIP(ctx, ah_launch_gemv_stream(w->type, P, nullptr, nullptr, grid, (uint32_t)ah_gemv_act_bytes(kp),
+        AH_HIP(ctx, ah_launch_gemv_stream(w->type, sp, nullptr, nullptr, grid, (uint32_t)ah_gemv_act_bytes(kp),
                                           ctx->d_status, pick(ctx, stream)));
     else
         AH_HIP(ctx, ah_launch_gemv(w->type, P, nullptr, nullptr, grid, kp, ah_gemv_nc(P.row_bytes),
@@ -868,6 +873,36 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
         ctx->last_hip = (int)e0;
         return AH_ERR_HIP;
     }
+    // A small streaming plan (every decode stage: q/k/v, o, gate/up, down, head) passes its parts
+    // in the kernel arguments with whole workgroups per part, as a single projection does: a
+    // workgroup then reaches its rows without the descriptor loads of the table plan, whose chain
+    // (workgroup entry, then part, then activation) sits on the critical path of a stage that
+    // streams one tile per wave.
+    if (all_stream && n_parts <= kStreamArgParts) {
+        ah_gemv_plan *p = new (std::nothrow) ah_gemv_plan();
+        if (!p) {
+            std::free(parts);
+            return AH_ERR_OUT_OF_MEMORY;
+        }
+        const uint32_t wg = deal_wgs(parts, n_parts, resident_wgs(ctx, type, true, kpad_max), true);
+        for (size_t i = 0; i < n_parts; ++i) p->sp.p[i] = parts[i];
+        std::free(parts);
+        if (wg == 0) {
+            delete p;
+            return AH_ERR_OUT_OF_MEMORY;
+        }
+        p->sp.n = (uint32_t)n_parts;
+        p->type = type;
+        p->n_parts = (uint32_t)n_parts;
+        p->grid = wg;
+        p->kpad_max = kpad_max;
+        p->nc = nc;
+        p->stream = true;
+        p->arg_parts = true;
+        p->act_bytes = (uint32_t)ah_gemv_act_bytes(kpad_max);
+        *out = p;
+        return AH_OK;
+    }
     // Streaming plan: waves dealt over the parts, activations sharing a workgroup's LDS region of
     // at most `budget` bytes (15 KB keeps two workgroups per CU; a larger activation raises it).
     if (all_stream) {
@@ -969,8 +1004,11 @@ int32_t ah_gemv_plan_run(ah_ctx *ctx, const ah_gemv_plan *plan, void *stream) {
     GemvPart none;
     std::memset(&none, 0, sizeof(none));
     AH_HIP(ctx, hipSetDevice(ctx->device));
-    if (plan->stream)
-        AH_HIP(ctx, ah_launch_gemv_stream(plan->type, none, plan->d_parts, plan->d_wgd, plan->grid,
+    if (plan->arg_parts)
+        AH_HIP(ctx, ah_launch_gemv_stream(plan->type, plan->sp, nullptr, nullptr, plan->grid,
+                                          plan->act_bytes, ctx->d_status, pick(ctx, stream)));
+    else if (plan->stream)
+        AH_HIP(ctx, ah_launch_gemv_stream(plan->type, plan->sp, plan->d_parts, plan->d_wgd, plan->grid,
                                           plan->act_bytes, ctx->d_status, pick(ctx, stream)));
     else
         AH_HIP(ctx, ah_launch_gemv(plan->type, none, plan->d_parts, plan->d_wg_part, plan->grid,
@@ -982,7 +1020,7 @@ int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan) {
     if (!ctx || !plan) return AH_ERR_INVALID_ARG;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(plan->d_parts);
+    if (plan->d_parts) (void)hipFree(plan->d_parts);
     if (plan->d_wg_part) (void)hipFree(plan->d_wg_part);
     if (plan->d_wgd) (void)hipFree(plan->d_wgd);
     delete plan;

@@ -849,15 +849,23 @@ AH_DEV GemvPart part_at(const GemvPart *__restrict__ parts, uint32_t i) {
 // PLAN: each wave's part and rows come from the workgroup's StreamWG entry (read with scalar
 // loads, which do not queue behind the vector memory stream), and the workgroup first quantizes
 // the activations of all its waves' parts.  Otherwise every wave serves the launch argument's
-// part, its rows split evenly over the grid's waves.
-// TYPE kMixedType (plans only): the parts may be of different GGUF types; each wave's units are
+// part, its rows split evenly over the grid's waves.  Otherwise each workgroup serves one of the
+// argument parts (whole workgroups per part), its rows split evenly over that part's waves.
+// TYPE kMixedType: the parts may be of different GGUF types; each wave's units are
 // computed by the loop of its part's type, a branch that is uniform over the wave and taken once
 // per tile outside the unit loop.  The activation layout is the same for every type.
 // DOTS: the debug form that also stores exact group dots (single launches only).
 // LDS: [activation region: act_bytes][one tile slot per wave].
+// Single-type kernels run 4 waves per SIMD (two workgroups per CU, <= 128 VGPRs).  The mixed-type
+// kernel holds every type's unit loop and spilled at that budget (1.1 MB of scratch writes per
+// configs[4] q/k/v launch); its plans are small (36 workgroups for q/k/v), so it is built for 2
+// waves per SIMD (one workgroup per CU, <= 256 VGPRs), which costs those plans nothing.
+template <int TYPE>
+constexpr int stream_waves_per_simd() { return TYPE == kMixedType ? 2 : 4; }
+
 template <int TYPE, bool PLAN, bool DOTS>
-__global__ void __launch_bounds__(kSThreads, 4)
-    gemv_stream_kernel(GemvPart single, const GemvPart *__restrict__ parts,
+__global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
+    gemv_stream_kernel(StreamParts sp, const GemvPart *__restrict__ parts,
                        const StreamWG *__restrict__ wgd, uint32_t act_bytes,
                        unsigned long long *status) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -874,7 +882,11 @@ __global__ void __launch_bounds__(kSThreads, 4)
         r_end = idle ? r_begin : D->r_end[wv];
         aoff = D->act_off[D->wave_act[wv]];
     } else {
-        P = single;
+        // the workgroup's part: uniform compares and selects (no run-time index into the arguments)
+        P = sp.p[0];
+#pragma unroll
+        for (uint32_t i = 1; i < kStreamArgParts; ++i)
+            if (i < sp.n && blockIdx.x >= sp.p[i].wg_begin) P = sp.p[i];
         const uint32_t n_waves = P.wg_count * kSWaves;
         const uint32_t wl = (blockIdx.x - P.wg_begin) * kSWaves + wave;
         r_begin = (uint32_t)((uint64_t)P.n_out * wl / n_waves);
@@ -1339,7 +1351,7 @@ AH_DEV void seq_swiglu_stage(const SeqArgs &a, uint32_t s, uint32_t r, bool &bro
 }
 
 template <int TYPE>
-__global__ void __launch_bounds__(kSThreads, 4) gemv_seq_kernel(SeqArgs a) {
+__global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>()) gemv_seq_kernel(SeqArgs a) {
     // this launch's run number (nothing writes the counter until the workgroup ends)
     const uint32_t r = __builtin_amdgcn_readfirstlane(
         __hip_atomic_load(a.runs + blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1);
@@ -1389,8 +1401,9 @@ static const void *stream_fn(uint32_t type, bool plan, bool dots = false) {
 #define AH_SFN(T) return plan ? reinterpret_cast<const void *>(&gemv_stream_kernel<T, true, false>)     \
                       : dots ? reinterpret_cast<const void *>(&gemv_stream_kernel<T, false, true>)     \
                              : reinterpret_cast<const void *>(&gemv_stream_kernel<T, false, false>);
-    if (type == kMixedType)  // plans only
-        return plan ? reinterpret_cast<const void *>(&gemv_stream_kernel<kMixedType, true, false>) : nullptr;
+    if (type == kMixedType)  // a table plan or argument parts (no debug form)
+        return plan ? reinterpret_cast<const void *>(&gemv_stream_kernel<kMixedType, true, false>)
+                    : dots ? nullptr : reinterpret_cast<const void *>(&gemv_stream_kernel<kMixedType, false, false>);
     switch (type) {
     case AH_GGML_Q8_0: AH_SFN(AH_GGML_Q8_0)
     case AH_GGML_Q4_K: AH_SFN(AH_GGML_Q4_K)
@@ -1435,35 +1448,39 @@ hipError_t ah_launch_gemv_seq(uint32_t type, const SeqArgs &a, uint32_t grid, hi
 int ah_gemv_stream_occupancy(uint32_t type, size_t lds) {
     int n0 = 0, n1 = 0;
     const void *f1 = stream_fn(type, true);
-    const void *f0 = type == kMixedType ? f1 : stream_fn(type, false);
+    const void *f0 = stream_fn(type, false);
     if (!f0 || hipOccupancyMaxActiveBlocksPerMultiprocessor(&n0, f0, kSThreads, lds) != hipSuccess) return 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n1, f1, kSThreads, lds) != hipSuccess) return 0;
     return n0 < n1 ? n0 : n1;
 }
 
-// act_bytes: the activation region (a plan's budget; for a single part ah_gemv_act_bytes of its kpad).
-hipError_t ah_launch_gemv_stream(uint32_t type, const GemvPart &single, const GemvPart *d_parts,
+// act_bytes: the activation region (a plan's budget; for argument parts ah_gemv_act_bytes of the
+// largest kpad).  d_parts: a plan with a workgroup table, else the parts in `sp`.
+hipError_t ah_launch_gemv_stream(uint32_t type, const StreamParts &sp, const GemvPart *d_parts,
                                  const StreamWG *d_wgd, uint32_t grid, uint32_t act_bytes,
                                  unsigned long long *status, hipStream_t stream) {
     const size_t lds = act_bytes + ah_gemv_stream_slot_bytes();
 #define AH_SLAUNCH(T)                                                                              \
     if (d_parts)                                                                                   \
         hipLaunchKernelGGL((gemv_stream_kernel<T, true, false>), dim3(grid), dim3(kSThreads), lds,  \
-                           stream, single, d_parts, d_wgd, act_bytes, status);                    \
-    else if (single.dots)                                                                          \
+                           stream, sp, d_parts, d_wgd, act_bytes, status);                        \
+    else if (sp.p[0].dots)                                                                         \
         hipLaunchKernelGGL((gemv_stream_kernel<T, false, true>), dim3(grid), dim3(kSThreads), lds,  \
-                           stream, single, d_parts, d_wgd, act_bytes, status);                    \
+                           stream, sp, d_parts, d_wgd, act_bytes, status);                        \
     else                                                                                           \
         hipLaunchKernelGGL((gemv_stream_kernel<T, false, false>), dim3(grid), dim3(kSThreads), lds, \
-                           stream, single, d_parts, d_wgd, act_bytes, status);
+                           stream, sp, d_parts, d_wgd, act_bytes, status);
     switch (type) {
     case AH_GGML_Q8_0: AH_SLAUNCH(AH_GGML_Q8_0) break;
     case AH_GGML_Q4_K: AH_SLAUNCH(AH_GGML_Q4_K) break;
     case AH_GGML_Q6_K: AH_SLAUNCH(AH_GGML_Q6_K) break;
     case kMixedType:
-        if (!d_parts) return hipErrorInvalidValue;  // mixed types exist only in plans
-        hipLaunchKernelGGL((gemv_stream_kernel<kMixedType, true, false>), dim3(grid), dim3(kSThreads), lds,
-                           stream, single, d_parts, d_wgd, act_bytes, status);
+        if (d_parts)
+            hipLaunchKernelGGL((gemv_stream_kernel<kMixedType, true, false>), dim3(grid), dim3(kSThreads), lds,
+                               stream, sp, d_parts, d_wgd, act_bytes, status);
+        else
+            hipLaunchKernelGGL((gemv_stream_kernel<kMixedType, false, false>), dim3(grid), dim3(kSThreads), lds,
+                               stream, sp, d_parts, d_wgd, act_bytes, status);
         break;
     default: return hipErrorInvalidValue;
     }
@@ -1524,8 +1541,9 @@ hipError_t ah_gemv_init_attrs() {
         for (int v = 0; v < 3; ++v)
             if (e == hipSuccess)
                 e = hipFuncSetAttribute(stream_fn(t, v == 1, v == 2), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute(stream_fn(kMixedType, true), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+    for (int v = 0; v < 2; ++v)
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(stream_fn(kMixedType, v == 1), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     for (uint32_t t : {(uint32_t)kMixedType, (uint32_t)AH_GGML_Q8_0, (uint32_t)AH_GGML_Q4_K, (uint32_t)AH_GGML_Q6_K})
         if (e == hipSuccess) e = hipFuncSetAttribute(seq_fn(t), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     return e;

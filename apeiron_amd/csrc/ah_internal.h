@@ -190,6 +190,16 @@ struct GemvPart {
     uint32_t type;         // GGUF type (AH_GGML_*): read by the mixed-type streaming plan
 };
 
+// The parts of a streaming launch without a workgroup table: a single projection, or a plan of at
+// most kStreamArgParts parts (whole workgroups per part, p[i].wg_begin / wg_count), passed in the
+// kernel arguments so that a workgroup reaches its part, its weights and its activation without a
+// dependent descriptor load.
+constexpr uint32_t kStreamArgParts = 4;
+struct StreamParts {
+    GemvPart p[kStreamArgParts];
+    uint32_t n;
+};
+
 // GEMM workgroup forms (waves x LDS ring slots), chosen per launch by ah_gemm_pick_waves.
 enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2 };
 

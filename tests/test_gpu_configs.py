@@ -106,6 +106,25 @@ def test_config4_layer_mixed_plan_vs_oracle(dev, layer):
 
 
 @pytest.mark.parametrize("layer", [0, 3])
+def test_config4_decode_stage_plans_vs_oracle(dev, layer):
+    """The configs[4] decode stages as a token issues them: q/k/v (Q4_K, Q4_K, Q6_K: one mixed
+    launch), o, gate/up, down.  Plans of at most 4 parts carry their descriptors in the kernel
+    arguments (whole workgroups per part); every part against the oracle."""
+    proj = cfg4_layer(layer)
+    for g in ([0, 1, 2], [3], [4, 5], [6]):
+        plan_vs_oracle(dev, [proj[i] for i in g], 20 + 10 * layer + g[0])
+
+
+def test_argument_plan_limits_vs_oracle(dev):
+    """Four parts (the most the kernel arguments carry) and five (the workgroup-table plan), mixed
+    types and ragged shapes, every part against the oracle."""
+    four = [("a", Q6_K, 300, 512), ("b", Q4_K, 7, 768), ("c", Q8_0, 1000, 96), ("d", Q4_K, 129, 256)]
+    plan_vs_oracle(dev, four, 40)
+    plan_vs_oracle(dev, four + [("e", Q6_K, 33, 1024)], 41)
+    plan_vs_oracle(dev, [("s", Q8_0, 1, 32)], 42)
+
+
+@pytest.mark.parametrize("layer", [0, 3])
 def test_config4_layer_prefill_groups_vs_oracle(dev, layer):
     """One configs[4] layer at N = 512 as the engine issues it: q/k/v grouped on one input, o,
     gate/up grouped, down; sampled rows x columns of every part against the oracle."""

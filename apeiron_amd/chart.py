@@ -94,6 +94,13 @@ class Device:
         _check(self.lib.ah_last_refusal_bits(self.h, ctypes.byref(b)), "last_refusal_bits")
         return b.value
 
+    GEMM_AUTO, GEMM_F16, GEMM_INT8 = 0, 1, 2
+
+    def set_gemm_design(self, ggml_type: int, design: int) -> None:
+        """The prefill GEMM design of `ggml_type` on this context (ah_set_gemm_design; F16 is the
+        default and the K-quants' only design, INT8 exists for Q8_0)."""
+        _check(self.lib.ah_set_gemm_design(self.h, ggml_type, design), "set_gemm_design")
+
     def probe_mfma_peak(self, kind: int) -> float:
         """Measured MFMA-only rate in tera-ops/s (kind 0: int8 32x32x32, 1: f16 32x32x16)."""
         out = ctypes.c_double(0.0)

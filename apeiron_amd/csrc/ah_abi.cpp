@@ -37,14 +37,16 @@ hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_by
 hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_in,
                           uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xmin,
                           const float *tok_scale, const int8_t *fcodes, const int64_t *fscales,
+                          const int8_t *xc, const uint32_t *xsp,
                           unsigned long long *status, uint32_t form, hipStream_t stream);
 hipError_t ah_launch_splitk_reduce(uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_tok,
                                    const float *tok_scale, unsigned long long *status, hipStream_t stream);
 uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
-                             uint32_t cus);
-uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits);
+                             uint32_t cus, bool int8);
+uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits,
+                          bool int8);
 uint32_t ah_gemm_max_parts(uint32_t type);
-uint32_t ah_gemm_pick_waves(uint32_t type, uint64_t n_wg4, uint32_t cus);
+uint32_t ah_gemm_pick_waves(uint32_t type, uint64_t n_wg4, uint32_t cus, bool int8);
 hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream);
 hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, uint32_t *d_sink,
                          hipStream_t stream, double *tops);
@@ -64,6 +66,7 @@ struct ah_ctx {
     int last_hip = 0;
     uint32_t last_bad_bits = 0;  // f16 bits behind the last AH_ERR_NONFINITE_SCALE
     int cu_count = 256;
+    uint32_t q8_design = AH_GEMM_DESIGN_AUTO;  // Q8_0 GEMM design (ah_set_gemm_design)
     void *scratch = nullptr;  // device scratch for GEMM operands / host-form staging
     size_t scratch_bytes = 0;
     // streaming-GEMV occupancy by (type, LDS bytes): a runtime query per launch costs more host
@@ -463,6 +466,16 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     const uint32_t n_in = (uint32_t)n_in_sz, N = (uint32_t)n_tok;
     const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
     const uint32_t cus = (uint32_t)ctx->cu_count;
+    // Q8_0 parts take the int8-MFMA design when it is selected (the f16 design, the faster one
+    // measured, is the default); the operand pass then writes int8 codes and block factors, and
+    // the f16 operand only if another part needs it
+    const bool q8_int8 = ctx->q8_design == AH_GEMM_DESIGN_INT8;
+    bool any_int8 = false, any_f16 = false;
+    for (size_t i = 0; i < n_parts; ++i) {
+        const bool i8p = q8_int8 && w[i]->type == AH_GGML_Q8_0;
+        any_int8 = any_int8 || i8p;
+        any_f16 = any_f16 || !i8p;
+    }
     // every split part has its own partials region: the parts of a launch run together and the
     // reduction reads them all at the end
     GemmPartDesc pd_stack[kStackParts];
@@ -484,7 +497,9 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         d.w_bytes = (uint32_t)w[i]->bytes;
         d.row_bytes = (uint32_t)w[i]->row_bytes;
         d.n_out = (uint32_t)w[i]->n_out;
-        d.splits = d.n_out ? ah_gemm_pick_splits(w[i]->type, d.n_out, n_in, N, cus) : 1;
+        d.splits = d.n_out ? ah_gemm_pick_splits(w[i]->type, d.n_out, n_in, N, cus,
+                                                 q8_int8 && w[i]->type == AH_GGML_Q8_0)
+                           : 1;
         d.y = y[i];
         d.partials = nullptr;
         if (d.splits > 1) {
@@ -494,7 +509,9 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     }
 
     size_t off = 0;
-    const size_t o_xh = off; off = align256(off + (size_t)N * kpad * 2);
+    const size_t o_xh = off; off = align256(off + (any_f16 ? (size_t)N * kpad * 2 : 0));
+    const size_t o_xc = off; off = align256(off + (any_int8 ? (size_t)N * kpad : 0));
+    const size_t o_xsp = off; off = align256(off + (any_int8 ? (size_t)N * (kpad / 32) * 4 : 0));
     const size_t o_ts = off; off = align256(off + (size_t)N * 4);
     const size_t o_xmin = off; off = align256(off + (any_q4k ? (size_t)N * nsb * 32 : 0));
     // flagged tokens' QuantAct (f32 input; codes input is read in place)
@@ -510,7 +527,9 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         if (st) return st;
         S = static_cast<uint8_t *>(ctx->scratch);
     }
-    _Float16 *xh = reinterpret_cast<_Float16 *>(S + o_xh);
+    _Float16 *xh = any_f16 ? reinterpret_cast<_Float16 *>(S + o_xh) : nullptr;
+    int8_t *xc = any_int8 ? reinterpret_cast<int8_t *>(S + o_xc) : nullptr;
+    uint32_t *xsp = any_int8 ? reinterpret_cast<uint32_t *>(S + o_xsp) : nullptr;
     float *ts = reinterpret_cast<float *>(S + o_ts);
     _Float16 *xmin = reinterpret_cast<_Float16 *>(S + o_xmin);
     int8_t *fcodes = keep ? reinterpret_cast<int8_t *>(S + o_fc) : static_cast<int8_t *>(const_cast<void *>(x));
@@ -529,6 +548,8 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     o.xmin = any_q4k ? xmin : nullptr;
     o.fcodes = keep ? fcodes : nullptr;
     o.fscales = keep ? fscales : nullptr;
+    o.xc = xc;
+    o.xsp = xsp;
     o.status = ctx->d_status;
     o.n_tok = N;
     o.n_in = n_in;
@@ -557,7 +578,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                 if (pd[j].n_out == 0) continue;
                 if (w[j]->type != AH_GGML_Q4_K && w[j]->type != AH_GGML_Q6_K) break;
                 types |= w[j]->type == AH_GGML_Q4_K ? 1u : 2u;
-                g4 += ah_gemm_part_wg4(w[j]->type, pd[j].n_out, n_in, N, pd[j].splits);
+                g4 += ah_gemm_part_wg4(w[j]->type, pd[j].n_out, n_in, N, pd[j].splits, false);
                 ++k;
             }
             if (types == 3u && g4 <= 2ull * cus) type = kGemmMixedKQuant;
@@ -570,11 +591,15 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                                   : w[i]->type == type;
             if (!fits) break;
             run[nr++] = pd[i];
-            wg4 += ah_gemm_part_wg4(w[i]->type, pd[i].n_out, n_in, N, pd[i].splits);
+            wg4 += ah_gemm_part_wg4(w[i]->type, pd[i].n_out, n_in, N, pd[i].splits,
+                                    q8_int8 && w[i]->type == AH_GGML_Q8_0);
             any_split = any_split || pd[i].splits > 1;
         }
-        const uint32_t form = type == kGemmMixedKQuant ? kForm4x4 : ah_gemm_pick_waves(type, wg4, cus);
-        AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xmin, ts, fcodes, fscales, ctx->d_status, form, s));
+        const uint32_t form = type == kGemmMixedKQuant
+                                  ? kForm4x4
+                                  : ah_gemm_pick_waves(type, wg4, cus, q8_int8 && type == AH_GGML_Q8_0);
+        AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xmin, ts, fcodes, fscales, xc, xsp,
+                                   ctx->d_status, form, s));
     }
     if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd, N, ts, ctx->d_status, s));
     return AH_OK;
@@ -1222,6 +1247,15 @@ int32_t ah_gemm_f32_noalloc_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_
     if (!ctx->noalloc) return AH_ERR_HIP;
     return gemm_group_launch(ctx, 1, &w, AH_SRC_F32, d_x, nullptr, n_tok, &d_y, stream, ctx->noalloc,
                              kNoAllocScratchBytes);
+}
+
+int32_t ah_set_gemm_design(ah_ctx *ctx, uint32_t ggml_type, uint32_t design) {
+    if (!ctx || design > AH_GEMM_DESIGN_INT8) return AH_ERR_INVALID_ARG;
+    size_t qk = 0, bb = 0;
+    if (!geom(ggml_type, qk, bb)) return AH_ERR_UNSUPPORTED_QUANT;
+    if (ggml_type != AH_GGML_Q8_0) return design == AH_GEMM_DESIGN_INT8 ? AH_ERR_UNSUPPORTED_QUANT : AH_OK;
+    ctx->q8_design = design;
+    return AH_OK;
 }
 
 int32_t ah_gemm_noalloc_scratch_bytes(size_t *bytes) {

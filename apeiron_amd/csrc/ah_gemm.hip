@@ -4,19 +4,23 @@
 // the reference's GEMMs (kern/gemm.rs:488-580 Q8_0, chart/kcols.rs:1399-1518 Q4_K / Q6_K) fold
 // sum_b d_rb * S_cb * D_rcb with exact integer group dots D.
 //
-// MI355X design.  A per-32-block f32 epilogue after an int8 MFMA costs ~3 VALU ops per output
-// element per block (convert, scale, accumulate), six times the VALU slots a 32x32x32 i8 MFMA
-// leaves free.  Instead both operands are fed to v_mfma_f32_32x32x16_f16 as exact small
-// integers:
+// MI355X design (the f16 design; an int8-MFMA design for Q8_0 follows gemm_rb_kernel).  After an
+// int8 MFMA every 32-block needs an f32 fold per output element (convert, scale, accumulate).
+// Instead both operands are fed to v_mfma_f32_32x32x16_f16 as exact small integers:
 //   * the activation operand is xq * 2^(e_b - E_tok) in f16 (the quantizer's power-of-two block
 //     scale S_b = 2^e_b folded in exactly; E_tok is the token's largest block exponent, applied
 //     once at the end), so the MFMA itself applies the activation scale;
 //   * the weight operand is the integer code (Q8_0 q, Q6_K u-32) or, for Q4_K, sc_j * q (<= 945),
 //     exact in f16.
-// Every product is exact and every partial sum below 2^24 is exact in the f32 accumulator, so a
-// Q8_0 block result is exactly 2^(e_b-E) * D_b.  What remains per output element is one FMA per
-// weight-scale change: per 32-block (Q8_0 d), per 16-group (Q6_K d*sc), per 256-super-block
-// (Q4_K d, plus one FMA for the dmin*m*X term, which rides on one extra MFMA per super-block).
+// Every product is exact.  For Q8_0 a block's partial sums stay below 2^24 units of its smallest
+// term (|q * xq| <= 127 * 127, 32 terms), so a Q8_0 block result is exactly 2^(e_b-E) * D_b.  The
+// K-quants accumulate a whole super-block (Q6_K) or its sc-weighted sub-blocks (Q4_K) in one MFMA
+// accumulator, whose sums pass 2^24 (up to ~1.2e5 per Q4_K product, ~5.2e5 per Q6_K element) and
+// round: each accumulation step rounds at 2^-24 relative, so a super-block's sum is off by at most
+// ~256 * 2^-24 ~= 1.5e-5 of the sum of its terms' magnitudes, inside the contract's 1e-4 *
+// sum|w * xhat| tolerance.  What remains per output element is one FMA per weight-scale change:
+// per 32-block (Q8_0 d), per 256-super-block (Q6_K d; Q4_K d, plus one FMA for the dmin*m*X term,
+// which rides on one extra MFMA per super-block).
 //
 // Tiling (gemm_rb_kernel below): a workgroup is 4 (or 2) waves; wave w owns 32 weight rows (the
 // MFMA N/column dimension, so the weight scale is one value per lane) and the workgroup's 128
@@ -32,6 +36,7 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kKS = 64;                // K depth of one LDS stage
@@ -92,6 +97,8 @@ struct GemmArgs {
     unsigned long long *status;
     const int8_t *fcodes;      // [n_tok][n_in] codes of flagged tokens
     const int64_t *fscales;    // [n_tok][nb32] their scales
+    const int8_t *xc;          // int8 design: codes [n_tok][kpad] (zero past n_in)
+    const uint32_t *xsp;       // int8 design: [n_tok][kpad/32] block factors 2^(e_b - E_tok), bf16 x2
     uint32_t n_wg;             // real workgroup count over all parts
 };
 
@@ -295,6 +302,94 @@ AH_DEV float exact_row(const uint8_t *row, const int8_t *xq, const int64_t *sc, 
         }
     }
     return acc;
+}
+
+// The epilogue of both GEMM designs.  acc[m][n] holds the wave's sums in the 32x32 MFMA D layout
+// (token tiles m, 32-row tiles n from row_w); units [u_lo, u_hi) (Q8_0 blocks, K-quant
+// super-blocks) are the split's K range, which the exact path of flagged tokens recomputes.
+template <int TYPE, int NM, int NN>
+AH_DEV __attribute__((always_inline)) void gemm_store(const GemmArgs &a, const GemmPartArgs &pa,
+                                                      const f32x16 (&acc)[NM][NN], uint32_t row_w,
+                                                      const bool (&rl)[NN], const uint32_t (&rbase)[NN],
+                                                      uint32_t tok0, uint32_t ntile, uint32_t split,
+                                                      uint32_t u_lo, uint32_t u_hi) {
+    const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+    // D layout of a 32x32 MFMA: lane (j, h), register r -> row i = 8*(r/4) + 4*h + (r%4), col j.
+    // Token scales (1.0 for partials) are loaded up front; lanes past n_out, tokens past n_tok and
+    // flagged tokens (bit 0 of their scale) store out of range, so there is no branch per element.
+    // fm[0..1] collect the tile's flagged tokens (bit tl) for the exact path after the stores.
+    uint64_t fm[2] = {0ull, 0ull};
+    float *ybase = pa.splits == 1 ? pa.y + (size_t)tok0 * pa.n_out
+                                  : pa.y + ((size_t)split * a.n_tok + tok0) * pa.n_out;
+    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(ybase, ntile * pa.n_out * 4u);
+    const __amdgpu_buffer_rsrc_t rt = ah_rsrc(a.tok_scale + tok0, ntile * 4u);
+    const bool scaled = pa.splits == 1;
+    // outputs the contract refuses (unsplit parts; a split part's reduction checks its sums): the
+    // store loop only ORs the compare masks (scalar registers); a rare second pass reads this
+    // lane's own stores back (once they are complete, bypassing L1) and records them
+    uint64_t obad = 0ull;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        uint32_t sc[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[r] = ah_ld32(rt, 4 * (32 * m + 8 * (r / 4) + 4 * h + (r % 4)));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            // lanes of half h hold token 32m + 8(r/4) + 4h + r%4
+            const uint64_t b = __builtin_amdgcn_ballot_w64(ah_ts_flagged(sc[r]));
+            const uint32_t tl0 = 32 * m + 8 * (r / 4) + (r % 4);
+            fm[tl0 >> 6] |= (b & 1ull) << (tl0 & 63);
+            fm[(tl0 + 4) >> 6] |= ((b >> 32) & 1ull) << ((tl0 + 4) & 63);
+        }
+#pragma unroll
+        for (int n = 0; n < NN; ++n) {
+            const uint32_t row = row_w + 32 * n + j;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t tl = 32 * m + 8 * (r / 4) + 4 * h + (r % 4);
+                const bool ok = rl[n] && tl < ntile && !ah_ts_flagged(sc[r]);
+                const float v = acc[m][n][r] * (scaled ? ah_ts_value(sc[r]) : 1.0f);
+                obad |= __builtin_amdgcn_ballot_w64(ok && !(__builtin_fabsf(v) < 0x1p31f));
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
+                                                      ok ? (tl * pa.n_out + row) * 4u : kOob, 0, 0);
+            }
+        }
+    }
+    if (scaled && obad != 0ull) {
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (uint32_t e = 0; e < 16u * NM * NN; ++e) {
+            const uint32_t m = e / (16 * NN), n = (e / 16) % NN, r = e % 16;
+            const uint32_t tl = 32 * m + 8 * (r / 4) + 4 * h + (r % 4), row = row_w + 32 * n + j;
+            if (!rl[n] || tl >= ntile || ah_ts_flagged(ah_ld32(rt, 4 * tl))) continue;
+            const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, (tl * pa.n_out + row) * 4u, 0, 1));
+            if (const uint32_t oc = ah_out_code(v)) ah_record(a.status, ah_out_key((uint64_t)(tok0 + tl) * pa.n_out + row, oc));
+        }
+    }
+    if ((fm[0] | fm[1]) != 0ull) {
+        // Flagged tokens: this wave's 32 rows, the split's K range, the lane halves taking
+        // alternate units; split partials are stored in the reduction's units (divided by the
+        // token scale, an exact power of two).
+        const uint32_t nb32 = (a.n_in + 31) / 32;
+        if (TYPE == AH_GGML_Q8_0 && u_hi > nb32) u_hi = nb32;
+        const uint32_t row = row_w + j;
+        for (int half = 0; half < 2; ++half) {
+            uint64_t mk = fm[half];
+            while (mk) {
+                const uint32_t tl = 64 * half + (uint32_t)__builtin_ctzll(mk);
+                mk &= mk - 1;
+                const size_t t = (size_t)tok0 + tl;
+                float v = rl[0] ? exact_row<TYPE>(pa.w + rbase[0], a.fcodes + t * a.n_in, a.fscales + t * nb32,
+                                                  a.n_in, u_lo, u_hi, (uint32_t)h)
+                                : 0.0f;
+                v += __shfl_xor(v, 32, 64);
+                const float ts = ah_ts_value(__builtin_bit_cast(uint32_t, a.tok_scale[t]));
+                if (h == 0 && rl[0]) {
+                    ybase[(size_t)tl * pa.n_out + row] = scaled ? v : v / ts;
+                    if (const uint32_t oc = scaled ? ah_out_code(v) : 0u) ah_record(a.status, ah_out_key((uint64_t)t * pa.n_out + row, oc));
+                }
+            }
+        }
+    }
 }
 
 // The kernel body, on an LDS ring of RG slots of buf_bytes<TYPE> at `lds`.
@@ -604,90 +699,189 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
     // the slices requested past the split must land before this workgroup's LDS is released
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // D layout of a 32x32 MFMA: lane (j, h), register r -> row i = 8*(r/4) + 4*h + (r%4), col j.
-    // Token scales (1.0 for partials) are loaded up front; lanes past n_out, tokens past n_tok and
-    // flagged tokens (bit 0 of their scale) store out of range, so there is no branch per element.
-    // fm[0..1] collect the tile's flagged tokens (bit tl) for the exact path after the stores.
-    uint64_t fm[2] = {0ull, 0ull};
-    float *ybase = pa.splits == 1 ? pa.y + (size_t)tok0 * pa.n_out
-                                  : pa.y + ((size_t)split * a.n_tok + tok0) * pa.n_out;
-    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(ybase, ntile * pa.n_out * 4u);
-    const __amdgpu_buffer_rsrc_t rt = ah_rsrc(a.tok_scale + tok0, ntile * 4u);
-    const bool scaled = pa.splits == 1;
-    // outputs the contract refuses (unsplit parts; a split part's reduction checks its sums): the
-    // store loop only ORs the compare masks (scalar registers); a rare second pass reads this
-    // lane's own stores back (once they are complete, bypassing L1) and records them
-    uint64_t obad = 0ull;
-#pragma unroll
-    for (int m = 0; m < NM; ++m) {
-        uint32_t sc[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[r] = ah_ld32(rt, 4 * (32 * m + 8 * (r / 4) + 4 * h + (r % 4)));
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            // lanes of half h hold token 32m + 8(r/4) + 4h + r%4
-            const uint64_t b = __builtin_amdgcn_ballot_w64(ah_ts_flagged(sc[r]));
-            const uint32_t tl0 = 32 * m + 8 * (r / 4) + (r % 4);
-            fm[tl0 >> 6] |= (b & 1ull) << (tl0 & 63);
-            fm[(tl0 + 4) >> 6] |= ((b >> 32) & 1ull) << ((tl0 + 4) & 63);
-        }
-#pragma unroll
-        for (int n = 0; n < NN; ++n) {
-            const uint32_t row = row_w + 32 * n + j;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t tl = 32 * m + 8 * (r / 4) + 4 * h + (r % 4);
-                const bool ok = rl[n] && tl < ntile && !ah_ts_flagged(sc[r]);
-                const float v = acc[m][n][r] * (scaled ? ah_ts_value(sc[r]) : 1.0f);
-                obad |= __builtin_amdgcn_ballot_w64(ok && !(__builtin_fabsf(v) < 0x1p31f));
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
-                                                      ok ? (tl * pa.n_out + row) * 4u : kOob, 0, 0);
-            }
-        }
-    }
-    if (scaled && obad != 0ull) {
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        for (uint32_t e = 0; e < 16u * NM * NN; ++e) {
-            const uint32_t m = e / (16 * NN), n = (e / 16) % NN, r = e % 16;
-            const uint32_t tl = 32 * m + 8 * (r / 4) + 4 * h + (r % 4), row = row_w + 32 * n + j;
-            if (!rl[n] || tl >= ntile || ah_ts_flagged(ah_ld32(rt, 4 * tl))) continue;
-            const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, (tl * pa.n_out + row) * 4u, 0, 1));
-            if (const uint32_t oc = ah_out_code(v)) ah_record(a.status, ah_out_key((uint64_t)(tok0 + tl) * pa.n_out + row, oc));
-        }
-    }
-    if ((fm[0] | fm[1]) != 0ull) {
-        // Flagged tokens: this wave's 32 rows, the split's K range, the lane halves taking
-        // alternate units; split partials are stored in the reduction's units (divided by the
-        // token scale, an exact power of two).
-        const uint32_t nb32 = (a.n_in + 31) / 32;
-        const uint32_t u_lo = TYPE == AH_GGML_Q8_0 ? 2 * st_begin : st_begin / 4;
-        uint32_t u_hi = TYPE == AH_GGML_Q8_0 ? 2 * st_end : st_end / 4;
-        if (TYPE == AH_GGML_Q8_0 && u_hi > nb32) u_hi = nb32;
-        const uint32_t row = row_w + j;
-        for (int half = 0; half < 2; ++half) {
-            uint64_t mk = fm[half];
-            while (mk) {
-                const uint32_t tl = 64 * half + (uint32_t)__builtin_ctzll(mk);
-                mk &= mk - 1;
-                const size_t t = (size_t)tok0 + tl;
-                float v = rl[0] ? exact_row<TYPE>(pa.w + rbase[0], a.fcodes + t * a.n_in, a.fscales + t * nb32,
-                                                  a.n_in, u_lo, u_hi, (uint32_t)h)
-                                : 0.0f;
-                v += __shfl_xor(v, 32, 64);
-                const float ts = ah_ts_value(__builtin_bit_cast(uint32_t, a.tok_scale[t]));
-                if (h == 0 && rl[0]) {
-                    ybase[(size_t)tl * pa.n_out + row] = scaled ? v : v / ts;
-                    if (const uint32_t oc = scaled ? ah_out_code(v) : 0u) ah_record(a.status, ah_out_key((uint64_t)t * pa.n_out + row, oc));
-                }
-            }
-        }
-    }
+    const uint32_t u_lo = TYPE == AH_GGML_Q8_0 ? 2 * st_begin : st_begin / 4;
+    const uint32_t u_hi = TYPE == AH_GGML_Q8_0 ? 2 * st_end : st_end / 4;
+    gemm_store<TYPE, NM, NN>(a, pa, acc, row_w, rl, rbase, tok0, ntile, split, u_lo, u_hi);
 }
 
 template <int TYPE, int WV, int RG>
 __global__ void __launch_bounds__(64 * WV, TYPE == AH_GGML_Q4_K ? 4 : 2) gemm_rb_kernel(GemmArgs a) {
     __shared__ __align__(16) uint8_t lds[RG * rb::buf_bytes<TYPE>()];
     gemm_rb_body<TYPE, WV, RG>(a, lds);
+}
+
+// ---- int8-MFMA design (Q8_0) ------------------------------------------------------------------
+//
+// v_mfma_i32_32x32x32_i8 takes one whole 32-block per MFMA: the activation codes (A, M = 32
+// tokens) from LDS, the weight codes (B, N = 32 rows) straight from the GGUF bytes, and gives the
+// exact int32 block dot D[tok][row] (|D| <= 32 * 127 * 127 < 2^19).  Each block then needs
+// y += D * d_rb * S'_tb per element, where S' = 2^(e_b - E_tok) is the block's power-of-two
+// activation factor relative to the token's largest block (the token scale 2^(E_tok - 32) is
+// applied once at the end, as in the f16 design).  A VALU multiply per element would make that
+// fold three VALU operations per element and block.  Instead a second MFMA forms the product
+// table as an outer product: v_mfma_f32_32x32x8_bf16 with A'[tok] = (S', S') and B'[row] =
+// (d_hi, d_lo), the f16 d split exactly into two bf16 (its top 8 and low 3 significant bits).  S'
+// is an exact bf16 whatever the exponent gap (bf16 has the f32 exponent range, so this design has
+// no f16 band and flags no token for it).  P = d_hi S' + d_lo S' = d * S' exactly in f32, in the
+// same D layout as the int32 dots, and the fold is one convert and one FMA per element and block.
+//
+// Bounds per 32-block and 32x32 tile: two MFMAs on the matrix core (the int8 one at twice the f16
+// rate) against 32 VALU instructions of 64 lanes (4 cycles each): the VALU bounds this design at
+// about 128 cycles per 65536 int8 operations a SIMD, a quarter of the int8 MFMA peak.
+//
+// Tiling: W waves, each owning 32 weight rows and the workgroup's 128 tokens (4 token tiles); a
+// stage is 4 blocks (K = 128).  The stage's activation codes (128 tokens x 128 B, chunk-XOR
+// swizzled like the f16 slice) and block factors (128 tokens x 16 B) go global -> LDS into a ring
+// of 3 slots, two stages ahead; each wave reads its rows' weight bytes a stage ahead into
+// registers.  Every stage issues its weight loads, then its slice: the top of a stage waits for
+// vmcnt <= one stage's slice instructions, which completes the stage's slice and its weights.
+namespace i8 {
+constexpr uint32_t kTok = 128, kKS = 128, kR = 3;
+constexpr uint32_t kAct = kTok * kKS;       // activation codes of a slot
+constexpr uint32_t kSlot = kAct + 4096;     // + block factors (one 1 KB load per wave)
+template <int W> constexpr int an() { return (int)(kAct / 1024) / W; }
+template <int W> constexpr int wait_count() { return (int)(kR - 2) * (an<W>() + 1); }
+constexpr uint32_t stages(uint32_t n_in) { return ((n_in + 31) / 32 + 3) / 4; }
+}  // namespace i8
+
+typedef int v4i8x4 __attribute__((ext_vector_type(4)));     // 16 int8 codes
+typedef int v16i32 __attribute__((ext_vector_type(16)));
+typedef short v4bf16 __attribute__((ext_vector_type(4)));   // 4 bf16 bit patterns
+
+template <int W>
+__global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
+    constexpr int NM = 4, AN = i8::an<W>();
+    constexpr uint32_t TPW = i8::kTok / W;  // tokens whose block factors one wave loads
+    __shared__ __align__(16) uint8_t lds[i8::kR * i8::kSlot];
+    const uint32_t per = gridDim.x >> 3;  // XCD-aware order, as gemm_rb_body
+    const uint32_t L = (blockIdx.x & 7u) * per + (blockIdx.x >> 3);
+    if (L >= a.n_wg) return;
+    const GemmPartArgs &pa = a.p[0];  // one part per launch
+    const uint32_t tt = L % pa.tok_tiles, rest = L / pa.tok_tiles;
+    const uint32_t split = rest % pa.splits, rtile = rest / pa.splits;
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t row_w = rtile * 32u * W + wv * 32u;
+    bool rl[1];
+    uint32_t rbase[1];
+    rl[0] = row_w + j < pa.n_out;
+    rbase[0] = (rl[0] ? row_w + j : 0u) * pa.row_bytes;
+    const uint32_t tok0 = tt * i8::kTok;
+    const uint32_t ntile = a.n_tok - tok0 < i8::kTok ? a.n_tok - tok0 : i8::kTok;
+    const uint32_t nbp = a.kpad / 32, nb32 = (a.n_in + 31) / 32;
+    const __amdgpu_buffer_rsrc_t rs = ah_rsrc(pa.w, pa.w_bytes);
+    const __amdgpu_buffer_rsrc_t rx = ah_rsrc(a.xc + (size_t)tok0 * a.kpad, ntile * a.kpad);
+    const __amdgpu_buffer_rsrc_t rp = ah_rsrc(a.xsp + (size_t)tok0 * nbp, ntile * nbp * 4u);
+    const uint32_t nstages = i8::stages(a.n_in);
+    const uint32_t st_begin = split * pa.stages_per_split;
+    const uint32_t st_end = st_begin + pa.stages_per_split < nstages ? st_begin + pa.stages_per_split : nstages;
+
+    auto slot = [&](uint32_t k) -> uint8_t * { return lds + k * i8::kSlot; };
+    // slice of stage st: wave w's instruction i fills slot bytes [(w*AN + i) KB, +1 KB), lane l at
+    // +16 l: token t = o / 128 at LDS chunk (o / 16) % 8, which holds the token's K chunk
+    // ((o / 16) % 8) ^ ((t >> 1) & 7); then its block factors, lanes < TPW taking tokens w*TPW + l
+    auto dma = [&](uint8_t *buf, uint32_t st) {
+        const bool live = st < st_end;
+#pragma unroll
+        for (int i = 0; i < AN; ++i) {
+            const uint32_t o = (wv * AN + i) * 1024u + lane * 16u;
+            const uint32_t t = o >> 7, c = ((o >> 4) & 7u) ^ ((t >> 1) & 7u);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rx, (__attribute__((address_space(3))) void *)(buf + (wv * AN + i) * 1024u), 16,
+                live && t < ntile ? t * a.kpad + st * i8::kKS + 16 * c : kOob, 0, 0, 0);
+        }
+        const uint32_t t = wv * TPW + lane;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rp, (__attribute__((address_space(3))) void *)(buf + i8::kAct + wv * 1024u), 16,
+            live && lane < TPW && t < ntile ? (t * nbp + 4 * st) * 4u : kOob, 0, 0, 0);
+    };
+    // weight bytes of stage st for row j: per block the lane half's 16 codes (4-aligned window
+    // plus the dword after it) and, for half 0, the dword holding d
+    struct Wt {
+        u32x4 v[4];
+        uint32_t s[4], d[4];
+    };
+    auto fetch = [&](uint32_t st) -> Wt {
+        Wt f;
+        const bool live = st < st_end && rl[0];
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+            const uint32_t b = 4 * st + bb;
+            const bool m = live && b < nb32;
+            const uint32_t blk = rbase[0] + 34 * b, c = (blk + 2 + 16 * h) & ~3u;
+            f.v[bb] = ah_ld128(rs, m ? c : kOob);
+            f.s[bb] = ah_ld32(rs, m ? c + 16 : kOob);
+            f.d[bb] = ah_ld32(rs, m && h == 0 ? blk & ~3u : kOob);
+        }
+        return f;
+    };
+
+    f32x16 acc[NM][1];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) acc[m][0] = (f32x16){};
+    const uint32_t sw = (uint32_t)(j >> 1) & 7u;
+    auto compute = [&](const uint8_t *buf, const Wt &f, uint32_t st) {
+        v4i8x4 A[4];
+        v4bf16 Dp[4];
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+            const uint32_t blk = rbase[0] + 34 * (4 * st + bb);
+            const uint32_t shc = (blk + 2 + 16 * h) & 3u;  // 0 or 2
+            const uint32_t w5[5] = {f.v[bb].x, f.v[bb].y, f.v[bb].z, f.v[bb].w, f.s[bb]};
+            A[bb] = (v4i8x4){(int)ah_alignbyte(w5[1], w5[0], shc), (int)ah_alignbyte(w5[2], w5[1], shc),
+                             (int)ah_alignbyte(w5[3], w5[2], shc), (int)ah_alignbyte(w5[4], w5[3], shc)};
+            // d = d_hi + d_lo exactly: d_hi keeps the top 8 significant bits (an f32 with a zero
+            // low half is a bf16), d_lo the other 3 (half 1 loaded d = 0: a zero operand)
+            const float d = ah_f16_bits_to_f32((f.d[bb] >> (8 * (blk & 3u))) & 0xffffu);
+            const uint32_t hi = __builtin_bit_cast(uint32_t, d) & 0xffff0000u;
+            const uint32_t lo = __builtin_bit_cast(uint32_t, d - __builtin_bit_cast(float, hi));
+            const u32x2 pr = {(hi >> 16) | (lo & 0xffff0000u), 0u};
+            Dp[bb] = __builtin_bit_cast(v4bf16, pr);
+        }
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const uint32_t t = 32 * m + j;
+            const u32x4 sv = *reinterpret_cast<const u32x4 *>(buf + i8::kAct + (t / TPW) * 1024u + (t % TPW) * 16u);
+            const uint32_t s4[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                const v4i8x4 B = *reinterpret_cast<const v4i8x4 *>(buf + t * i8::kKS + 16 * ((uint32_t)(2 * bb + h) ^ sw));
+                // tokens on the MFMA's M side, rows on N: the D layout gemm_store reads
+                const v16i32 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(B, A[bb], (v16i32){}, 0, 0, 0);
+                const u32x2 sp = {h ? 0u : s4[bb], 0u};
+                const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(v4bf16, sp), Dp[bb], (f32x16){}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[m][0][r] = __builtin_fmaf((float)D[r], P[r], acc[m][0][r]);
+            }
+        }
+    };
+
+    Wt F0 = fetch(st_begin), F1;
+    __builtin_amdgcn_sched_barrier(0);
+    dma(slot(0), st_begin);
+    dma(slot(1), st_begin + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t k = 0;  // slot of the current stage
+    for (uint32_t st = st_begin; st < st_end; st += 2) {
+        ah_vm_lds_barrier<i8::wait_count<W>()>();  // slice st (and weights st) landed; slot k+2 free
+        F1 = fetch(st + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        dma(slot(k == 0 ? 2u : k - 1), st + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(slot(k), F0, st);
+        k = k == 2 ? 0u : k + 1;
+        if (st + 1 >= st_end) break;
+        ah_vm_lds_barrier<i8::wait_count<W>()>();
+        F0 = fetch(st + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        dma(slot(k == 0 ? 2u : k - 1), st + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(slot(k), F1, st + 1);
+        k = k == 2 ? 0u : k + 1;
+    }
+    // the slices requested past the split must land before this workgroup's LDS is released
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    gemm_store<AH_GGML_Q8_0, NM, 1>(a, pa, acc, row_w, rl, rbase, tok0, ntile, split, 4 * st_begin, 4 * st_end);
 }
 
 // Q4_K and Q6_K parts of one input in one grid (4 waves, 4 slots sized for the larger type):
@@ -788,8 +982,9 @@ namespace {
 struct GemmGeom {
     uint32_t nstages, unroll, rows, toks;
 };
-GemmGeom geom_of(uint32_t type, uint32_t n_in, uint32_t kpad, uint32_t waves = 4) {
+GemmGeom geom_of(uint32_t type, uint32_t n_in, uint32_t kpad, uint32_t waves = 4, bool int8 = false) {
     const uint32_t rows = 32u * rb::kNN * waves;
+    if (int8) return {i8::stages(n_in), 1, rows, i8::kTok};  // stages of 4 blocks
     if (type == AH_GGML_Q8_0) return {(n_in + 2 * kKS - 1) / (2 * kKS) * 2, 2, rows, rb::tok_of(type)};
     return {kpad / kKS, 4, rows, rb::tok_of(type)};  // K-quants: whole super-blocks
 }
@@ -810,10 +1005,10 @@ uint32_t per_split(const GemmGeom &g, uint32_t splits) {
 //   a split GEMM adds the reduction: 4.8 us fixed plus the partials' write and read-back,
 //   (splits + 1) * n_tok * n_out * 4 bytes at 0.253 us per MB.
 uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
-                             uint32_t cus) {
-    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256);
+                             uint32_t cus, bool int8) {
+    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4, int8);
     const uint64_t tiles = (uint64_t)((n_out + g.rows - 1) / g.rows) * ((n_tok + g.toks - 1) / g.toks);
-    const double c = type == AH_GGML_Q8_0 ? 0.806 : type == AH_GGML_Q4_K ? 0.400 : 1.081;
+    const double c = int8 ? 1.0 : type == AH_GGML_Q8_0 ? 0.806 : type == AH_GGML_Q4_K ? 0.400 : 1.081;
     uint32_t best = 1;
     double best_cost = 1e30;
     for (uint32_t want = 1; want <= 64 && want <= g.nstages; ++want) {
@@ -835,8 +1030,9 @@ uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint3
 uint32_t ah_gemm_max_parts(uint32_t type) { return rb::max_parts_of(type); }
 
 // 4-wave workgroups (tiles x splits) of one part.
-uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits) {
-    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4);
+uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits,
+                          bool int8) {
+    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4, int8);
     return ((n_out + g.rows - 1) / g.rows) * ((n_tok + g.toks - 1) / g.toks) * splits;
 }
 
@@ -849,7 +1045,8 @@ uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t
 //             spread over every CU, halving each CU's load on its texture unit and LDS.
 // Measured at N = 512 (A/B in one run): 8960x1536 Q8_0 48.8 -> 43.3 us, Q6_K 54.4 -> 47.7 on
 // kForm2x2; 4864x896 23.5 -> 22.6, 1536x8960 46.6 -> 45.7 (Q6_K 55.3 -> 51.8) on kForm2x4.
-uint32_t ah_gemm_pick_waves(uint32_t type, uint64_t n_wg4, uint32_t cus) {
+uint32_t ah_gemm_pick_waves(uint32_t type, uint64_t n_wg4, uint32_t cus, bool int8) {
+    if (int8) return n_wg4 <= cus ? kFormI8x2 : kFormI8x4;
     if (type == AH_GGML_Q4_K) return kForm4x4;
     return n_wg4 <= cus ? kForm2x4 : n_wg4 <= 2ull * cus ? kForm2x2 : kForm4x4;
 }
@@ -953,11 +1150,14 @@ hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, ui
 hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_in,
                           uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xmin,
                           const float *tok_scale, const int8_t *fcodes, const int64_t *fscales,
+                          const int8_t *xc, const uint32_t *xsp,
                           unsigned long long *status, uint32_t form, hipStream_t stream) {
     const bool mixed = type == kGemmMixedKQuant;  // Q4_K and Q6_K parts, 4-wave form
+    const bool int8 = form == kFormI8x4 || form == kFormI8x2;
     if (n_parts == 0 || n_parts > (mixed ? kGemmMaxParts : rb::max_parts_of(type))) return hipErrorInvalidValue;
-    if (mixed || type == AH_GGML_Q4_K || form > kForm2x4) form = kForm4x4;
-    const uint32_t waves = form == kForm4x4 ? 4u : 2u;
+    if (int8 && (type != AH_GGML_Q8_0 || !xc || !xsp)) return hipErrorInvalidValue;
+    if (!int8 && (mixed || type == AH_GGML_Q4_K || form > kForm2x4)) form = kForm4x4;
+    const uint32_t waves = form == kForm4x4 || form == kFormI8x4 ? 4u : 2u;
     GemmArgs a;
     a.n_parts = n_parts;
     a.n_in = n_in;
@@ -969,6 +1169,8 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     a.fcodes = fcodes;
     a.status = status;
     a.fscales = fscales;
+    a.xc = xc;
+    a.xsp = xsp;
     uint32_t wg = 0;
     for (uint32_t i = 0; i < kGemmMaxParts; ++i) {
         GemmPartArgs &P = a.p[i];
@@ -980,7 +1182,7 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
         const GemmPartDesc &d = parts[i];
         const uint32_t pt = mixed ? d.type : type;
         if (mixed && pt != AH_GGML_Q4_K && pt != AH_GGML_Q6_K) return hipErrorInvalidValue;
-        const GemmGeom g = geom_of(pt, n_in, kpad, waves);
+        const GemmGeom g = geom_of(pt, n_in, kpad, waves, int8);
         const uint32_t per = per_split(g, d.splits ? d.splits : 1);
         P.w = d.w;
         P.w_bytes = d.w_bytes;
@@ -1003,6 +1205,14 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     if (form == kForm2x2) hipLaunchKernelGGL((gemm_rb_kernel<T, 2, 2>), rb_grid, blk, 0, stream, a);    \
     else if (form == kForm2x4) hipLaunchKernelGGL((gemm_rb_kernel<T, 2, 4>), rb_grid, blk, 0, stream, a); \
     else hipLaunchKernelGGL((gemm_rb_kernel<T, 4, 4>), rb_grid, blk, 0, stream, a);
+    if (form == kFormI8x4) {
+        hipLaunchKernelGGL(gemm_i8_kernel<4>, rb_grid, blk, 0, stream, a);
+        return hipGetLastError();
+    }
+    if (form == kFormI8x2) {
+        hipLaunchKernelGGL(gemm_i8_kernel<2>, rb_grid, blk, 0, stream, a);
+        return hipGetLastError();
+    }
     switch (type) {
     case kGemmMixedKQuant: hipLaunchKernelGGL(gemm_rb_kquant_kernel, rb_grid, blk, 0, stream, a); break;
     case AH_GGML_Q8_0: AH_GFORMS(AH_GGML_Q8_0) break;

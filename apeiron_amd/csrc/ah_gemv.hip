@@ -733,8 +733,10 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
         Emin = (int)redn[w] < Emin ? (int)redn[w] : Emin;
     }
     if (E > 62) E = 62;  // a block without a Q32.32 scale: the call is refused anyway
-    // a nonzero block below the f16 band: the GEMM serves this token exactly from its codes
-    const bool flagged = Emin < E - kF16Band;
+    // a nonzero block below the f16 band (when the f16 operand is written; the int8 design's
+    // bf16 block factors carry any gap), or a scale that is not a power of two: the GEMM serves
+    // this token exactly from its codes
+    const bool flagged = o.xh ? Emin < E - kF16Band : Emin < -500;
     if (tid == 0) {
         const float ts = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
         o.tok_scale[tok] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, ts) | (flagged ? 1u : 0u));
@@ -755,6 +757,24 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
             if (q == 0) fs[b] = ex[u] < 0 ? 0 : (int64_t)(1ull << ex[u]);
         }
     }
+    if (o.xc) {
+        // int8 design: the codes (zero past n_in) and the block factor 2^(e_b - E) as a bf16 pair
+        int8_t *xc = o.xc + (size_t)tok * o.kpad;
+        uint32_t *xsp = o.xsp + (size_t)tok * nbp;
+#pragma unroll
+        for (uint32_t u = 0; u < R; ++u) {
+            if (u * kOpBlocks + wb0 >= nbp) break;
+            const uint32_t b = u * kOpBlocks + tid / 4;
+            if (b >= nbp) continue;
+            const u32x2 cv = {c0[u], c1[u]};
+            *reinterpret_cast<u32x2 *>(xc + 32 * b + 8 * q) = cv;
+            if (q == 0) {
+                const uint32_t bf = ex[u] < 0 ? 0u : (uint32_t)(ex[u] - E + 127) << 7;  // 2^(e-E) >= 2^-63
+                xsp[b] = bf | (bf << 16);
+            }
+        }
+    }
+    if (!o.xh) return;
     _Float16 *xh = o.xh + (size_t)tok * o.kpad;
 #pragma unroll
     for (uint32_t u = 0; u < R; ++u) {

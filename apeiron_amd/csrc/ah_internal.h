@@ -201,7 +201,8 @@ struct StreamParts {
 };
 
 // GEMM workgroup forms (waves x LDS ring slots), chosen per launch by ah_gemm_pick_waves.
-enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2 };
+// kFormI8x4 / kFormI8x2: the int8-MFMA design (Q8_0), 4 or 2 waves.
+enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2, kFormI8x4 = 3, kFormI8x2 = 4 };
 
 // One projection of a GEMM launch: the parts of a launch share the GGUF type, the input and its
 // operand (n_in, n_tok), and run in one grid.  `splits` is the part's own split-K count (its
@@ -292,6 +293,8 @@ struct OperandArgs {
     _Float16 *xmin;        // [n_tok][kpad/256][16] for Q4_K, else nullptr
     int8_t *fcodes;        // [n_tok][n_in] (f32 input only; flagged rows written)
     int64_t *fscales;      // [n_tok][nb32] (f32 input only; flagged rows written)
+    int8_t *xc;            // int8 design: codes [n_tok][kpad] (zero past n_in), or nullptr
+    uint32_t *xsp;         // int8 design: [n_tok][kpad/32] bf16 pairs of 2^(e_b - E_tok), or nullptr
     unsigned long long *status;
     uint32_t n_tok, n_in, nb32, kpad, src;
 };

@@ -27,8 +27,9 @@ Also reported, beside the value:
                 FFN's SwiGLU stage), as eager launches, and with its 197 projections batched as
                 independent parts (two launches: not a dependency-respecting token);
   config1       BASELINE configs[1] (Qwen2.5-0.5B, 24 layers, Q4_K) as one batched launch;
-  gemm          configs[3] N = 512 GEMMs against the 5.0 POPS int8 MFMA peak, the MFMA-only probe,
-                and the configs[4] N = 512 prefill;
+  gemm          configs[3] N = 512 GEMMs against the 5.0 POPS int8 MFMA peak (Q8_0 on both MFMA
+                designs, int8 and f16), the MFMA-only probe, and the configs[4] N = 512 prefill
+                (--only gemm3: the configs[3] GEMMs alone, for profiling);
   heads         configs[0] (Q8_0 4864x896) and configs[2] (151936x896 head, Q6_K and Q8_0);
   cpu_baseline  the restated reference fast path (oracle/ah_cpu_fast.c) on the same token's
                 projections, on this host's cores; cpu_baseline_gemm the same for N = 512.
@@ -127,7 +128,7 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true", help="headline only (decode token + roofline)")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--cpu-threads", type=int, default=8)
-    ap.add_argument("--only", choices=["decode", "gemm", "config1", "heads", "copy"], default=None)
+    ap.add_argument("--only", choices=["decode", "gemm", "gemm3", "config1", "heads", "copy"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
@@ -366,14 +367,21 @@ def main() -> int:
         head.free()
 
     # ---- N = 512 GEMMs ------------------------------------------------------------------
-    if args.only in (None, "gemm") and not args.no_gemm and not args.no_extras:
-        probe = {"int8_tops": round(dev.probe_mfma_peak(0), 1), "f16_tflops": round(dev.probe_mfma_peak(1), 1)}
-        log(f"[bench] MFMA-only probe: int8 32x32x32 {probe['int8_tops']:.0f} TOPS, "
-            f"f16 32x32x16 {probe['f16_tflops']:.0f} TFLOPS")
-        result["mfma_probe"] = probe
+    if args.only in (None, "gemm", "gemm3") and not args.no_gemm and not args.no_extras:
+        if args.only == "gemm3":
+            probe = {"int8_tops": INT8_PEAK_TOPS, "f16_tflops": INT8_PEAK_TOPS / 2}  # published peaks
+        else:
+            probe = {"int8_tops": round(dev.probe_mfma_peak(0), 1), "f16_tflops": round(dev.probe_mfma_peak(1), 1)}
+            log(f"[bench] MFMA-only probe: int8 32x32x32 {probe['int8_tops']:.0f} TOPS, "
+                f"f16 32x32x16 {probe['f16_tflops']:.0f} TFLOPS")
+            result["mfma_probe"] = probe
         gemm = []
         n_tok = 512
-        for gt in (synth.Q8_0, synth.Q4_K):
+        # Q8_0 on both MFMA designs (int8, the default, and f16); the K-quants have the f16 design
+        for gt, design in ((synth.Q8_0, chart.Device.GEMM_INT8), (synth.Q8_0, chart.Device.GEMM_F16),
+                           (synth.Q4_K, chart.Device.GEMM_F16)):
+            dname = "int8" if design == chart.Device.GEMM_INT8 else "f16"
+            dev.set_gemm_design(gt, design)
             for n_out, n_in in GEMM_SHAPES:
                 rng3 = synth.rng_for(3, gt * 10 + n_in)
                 w = dev.upload(gt, synth.payload(gt, rng3, n_out, n_in), n_out, n_in)
@@ -390,13 +398,15 @@ def main() -> int:
                 tops = ops / us / 1e6
                 traffic = n_out * synth.needed_row_bytes(gt, n_in) + 4.0 * n_tok * n_out + n_tok * n_in
                 attain = min(INT8_PEAK_TOPS, ops / traffic * HBM_PEAK_GBS / 1e3)
-                gemm.append({"type": synth.NAMES[gt], "shape": [n_out, n_in], "n_tok": n_tok, "us": round(us, 2),
-                             "tops": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                gemm.append({"type": synth.NAMES[gt], "design": dname, "shape": [n_out, n_in], "n_tok": n_tok,
+                             "us": round(us, 2), "tops": round(tops, 1),
+                             "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                              "frac_f16_probe": round(tops / probe["f16_tflops"], 4),
                              "attainable_tops": round(attain, 1), "frac_attainable": round(tops / attain, 4)})
-                log(f"[bench] gemm {synth.NAMES[gt]} {n_out}x{n_in} N{n_tok}: {us:.1f} us {tops:.0f} TOPS "
-                    f"({100 * tops / INT8_PEAK_TOPS:.1f}% int8 peak)")
+                log(f"[bench] gemm {synth.NAMES[gt]} ({dname} MFMA) {n_out}x{n_in} N{n_tok}: {us:.1f} us "
+                    f"{tops:.0f} TOPS ({100 * tops / INT8_PEAK_TOPS:.1f}% int8 peak)")
                 w.free()
+            dev.set_gemm_design(gt, chart.Device.GEMM_AUTO)
         result["gemm"] = gemm
 
     # ---- the 168 projections of a Qwen2.5-0.5B token batched in one launch ------------

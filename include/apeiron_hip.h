@@ -213,6 +213,20 @@ int32_t ah_gemm_noalloc_scratch_bytes(size_t *bytes);
 int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
                        const int64_t *d_scales, size_t n_tok, float *d_y, void *stream);
 
+/* Design of the Q8_0 prefill GEMM.  The reference has one CPU kernel per type (gemm_q8_0,
+ * kern/gemm.rs:488-580); here two MFMA designs meet the same contract, selectable per context for
+ * comparison (results agree within the tolerance, not bit for bit):
+ *   AH_GEMM_DESIGN_INT8: v_mfma_i32_32x32x32_i8 exact block dots of the int8 codes, folded with
+ *     d * 2^(e_b - E) formed exactly by a bf16 outer-product MFMA (no exponent band);
+ *   AH_GEMM_DESIGN_F16: v_mfma_f32_32x32x16_f16 on exact f16 operands (the K-quants' design);
+ *   AH_GEMM_DESIGN_AUTO (the default): the F16 design, measured 17-25% faster on MI355X at the
+ *     configs[3] shapes (N = 512).
+ * Only Q8_0 has an INT8 design (other types: AH_ERR_UNSUPPORTED_QUANT). */
+#define AH_GEMM_DESIGN_AUTO 0u
+#define AH_GEMM_DESIGN_F16 1u
+#define AH_GEMM_DESIGN_INT8 2u
+int32_t ah_set_gemm_design(ah_ctx *ctx, uint32_t ggml_type, uint32_t design);
+
 /* Grouped prefill: n_parts projections of ONE input (q/k/v, gate/up).  gemm_q8_0_group
  * (kern/gemm.rs:799-818) shares one activation pack over its parts; here one operand pass
  * serves every part, then one GEMM launch per run of same-type parts and one split-K

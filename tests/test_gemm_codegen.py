@@ -112,6 +112,36 @@ def test_no_slice_load_can_be_skipped(gemm_asm):
                 assert not is_slice(x), (TYPES[t], waves, slots, i, x)
 
 
+def test_int8_design_ring(gemm_asm):
+    """The int8 Q8_0 kernel (W waves, 3-slot ring, stages of 4 blocks): each wave issues 16/W
+    activation loads and one block-factor load per stage, every ring barrier waits for one stage's
+    slice (the weights of the stage are issued before its slice, so they complete too), and no
+    slice load sits behind an execz branch."""
+    seen = set()
+    for i, l in enumerate(gemm_asm):
+        m = re.match(r"^(_ZN12_GLOBAL__N_114gemm_i8_kernelILi(\d+)E\S*):", l)
+        if not m:
+            continue
+        w = int(m.group(2))
+        seen.add(w)
+        end = next(j for j in range(i, len(gemm_asm)) if "s_endpgm" in gemm_asm[j])
+        body = [x.strip() for x in gemm_asm[i:end]]
+        want = 16 // w + 1
+        bars = [k for k, x in enumerate(body) if x.startswith("s_barrier")]
+        assert len(bars) == 2, (w, len(bars))  # the loop body runs two stages
+        for k in bars:
+            mm = re.match(r"s_waitcnt vmcnt\((\d+)\) lgkmcnt\(0\)$", body[k - 1])
+            assert mm and int(mm.group(1)) == want, (w, body[k - 1], want)
+        slices = [x for x in body if x.startswith("buffer_load") and x.endswith(" lds")]
+        assert len(slices) == 4 * want, (w, len(slices))  # prologue 2 stages + 2 in the loop
+        for k, x in enumerate(body):
+            mm = re.match(r"s_cbranch_execz\s+(\S+)", x)
+            if mm:
+                for y in skipped_by_execz(body, k, mm.group(1)):
+                    assert not (y.startswith("buffer_load") and y.endswith(" lds")), (w, y)
+    assert seen == {2, 4}, seen
+
+
 @pytest.fixture(scope="module")
 def gemv_asm(tmp_path_factory):
     if not (os.path.exists(HIPCC) or shutil.which(HIPCC)):

@@ -120,6 +120,7 @@ namespace {
 bool geom(uint32_t t, size_t &qk, size_t &bb) {
     switch (t) {
     case AH_GGML_Q8_0: qk = 32; bb = 34; return true;
+    case AH_GGML_Q5_0: qk = 32; bb = 22; return true;
     case AH_GGML_Q4_K: qk = 256; bb = 144; return true;
     case AH_GGML_Q6_K: qk = 256; bb = 210; return true;
     default: return false;
@@ -142,6 +143,7 @@ int32_t validate(uint32_t t, size_t raw_len, size_t n_out, size_t n_in, size_t &
 
 void scale_offsets(uint32_t t, uint32_t &o0, uint32_t &o1, uint32_t &bb) {
     if (t == AH_GGML_Q8_0) { o0 = o1 = 0; bb = 34; }
+    else if (t == AH_GGML_Q5_0) { o0 = o1 = 0; bb = 22; }
     else if (t == AH_GGML_Q4_K) { o0 = 0; o1 = 2; bb = 144; }
     else { o0 = o1 = 208; bb = 210; }
 }
@@ -172,9 +174,9 @@ int32_t ensure_scratch(ah_ctx *ctx, size_t bytes) {
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Work units of a row: Q8_0 blocks, Q4_K super-blocks, Q6_K half super-blocks (128 elements).
+// Work units of a row: Q8_0 / Q5_0 blocks, Q4_K super-blocks, Q6_K half super-blocks (128 elements).
 uint32_t units_per_row(uint32_t t, uint32_t n_in) {
-    return t == AH_GGML_Q8_0 ? (n_in + 31) / 32 : t == AH_GGML_Q4_K ? (n_in + 255) / 256 : (n_in + 127) / 128;
+    return ah_blk32((int)t) ? (n_in + 31) / 32 : t == AH_GGML_Q4_K ? (n_in + 255) / 256 : (n_in + 127) / 128;
 }
 
 uint32_t kpad_of(size_t n_in) { return (uint32_t)((n_in + 255) / 256 * 256); }

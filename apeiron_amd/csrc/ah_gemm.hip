@@ -57,6 +57,13 @@ AH_DEV void i8x4_to_f16(uint32_t c, uint32_t &lo, uint32_t &hi) {
     hi = as_u(as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
 }
 
+// 4 unsigned 5-bit values (bytes) -> 4 exact f16 of (u - 16).
+AH_DEV void u5x4_to_f16(uint32_t u, uint32_t &lo, uint32_t &hi) {
+    const f16x2 bias = {(_Float16)1040.0f, (_Float16)1040.0f};
+    lo = as_u(as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
+    hi = as_u(as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
+}
+
 // 4 unsigned 6-bit values (bytes) -> 4 exact f16 of (u - 32).
 AH_DEV void u6x4_to_f16(uint32_t u, uint32_t &lo, uint32_t &hi) {
     const f16x2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};
@@ -126,15 +133,15 @@ template <int W> constexpr int rows() { return W * 32 * kNN; }  // rows per work
 // CU at prefill sizes.  (Measured each way round: the other choice is 7-11% slower per type.)
 template <int TYPE> constexpr int nm() { return TYPE == AH_GGML_Q4_K ? 2 : 4; }
 // Parts one launch may hold (see the part lookup in the kernel).
-template <int TYPE> constexpr uint32_t max_parts() { return TYPE == AH_GGML_Q8_0 ? 1u : kGemmMaxParts; }
-uint32_t max_parts_of(uint32_t type) { return type == AH_GGML_Q8_0 ? 1u : kGemmMaxParts; }
+template <int TYPE> constexpr uint32_t max_parts() { return ah_blk32(TYPE) ? 1u : kGemmMaxParts; }
+uint32_t max_parts_of(uint32_t type) { return ah_blk32((int)type) ? 1u : kGemmMaxParts; }
 template <int TYPE> constexpr int tok() { return 32 * nm<TYPE>(); }              // tokens per workgroup
 template <int TYPE> constexpr int act_bytes() { return tok<TYPE>() * kKS * 2; }   // f16 slice of a stage
 template <int TYPE> constexpr int buf_bytes() {                                    // + Q4_K split sums
     return act_bytes<TYPE>() + (TYPE == AH_GGML_Q4_K ? tok<TYPE>() * 32 : 0);
 }
 // Split granularity in stages (Q8_0 pairs, K-quant super-blocks); the loop body is 4 stages.
-template <int TYPE> constexpr int unroll() { return TYPE == AH_GGML_Q8_0 ? 2 : 4; }
+template <int TYPE> constexpr int unroll() { return ah_blk32(TYPE) ? 2 : 4; }
 // Weight register sets and how many stages ahead they are fetched (Q6_K's 27-register set
 // allows only two sets within the 256-register budget).
 // The prologue replays ring - 1 notional stages, so a fetch is at most ring - 1 stages ahead.
@@ -197,6 +204,22 @@ AH_DEV WRb fetch_rb(__amdgpu_buffer_rsrc_t rs, const uint32_t (&rb)[NN], const b
             w.s[4 * n + 2] = ah_ld32(rs, m1 ? c1 + 16 : kOob);
             w.s[4 * n + 3] = ah_ld32(rs, m1 ? (blk1 & ~3u) : kOob);
         }
+    } else if constexpr (TYPE == AH_GGML_Q5_0) {
+        // per block the 6 dwords from its 4-aligned start: d, qh and all 16 qs bytes (both lane
+        // halves need every qs byte: half 0 the low nibbles, half 1 the high ones)
+        const uint32_t b = k0 / 32;
+        const bool l0 = live && b * 32 < n_in, l1 = live && (b + 1) * 32 < n_in;
+#pragma unroll
+        for (int n = 0; n < NN; ++n) {
+            const uint32_t c0 = (rb[n] + 22 * b) & ~3u, c1 = (rb[n] + 22 * (b + 1)) & ~3u;
+            const bool m0 = l0 && rl[n], m1 = l1 && rl[n];
+            w.v[2 * n] = ah_ld128(rs, m0 ? c0 : kOob);
+            w.s[4 * n] = ah_ld32(rs, m0 ? c0 + 16 : kOob);
+            w.s[4 * n + 1] = ah_ld32(rs, m0 ? c0 + 20 : kOob);
+            w.v[2 * n + 1] = ah_ld128(rs, m1 ? c1 : kOob);
+            w.s[4 * n + 2] = ah_ld32(rs, m1 ? c1 + 16 : kOob);
+            w.s[4 * n + 3] = ah_ld32(rs, m1 ? c1 + 20 : kOob);
+        }
     } else if constexpr (TYPE == AH_GGML_Q6_K) {
         static_assert(NN == 1, "Q6_K stages one row per lane");
         const uint32_t sb = rb[0] + 210 * (k0 / 256), nh = P / 2;
@@ -257,6 +280,15 @@ AH_DEV float exact_row(const uint8_t *row, const int8_t *xq, const int64_t *sc, 
             int D = 0;
             for (uint32_t l = 0; l < 32 && 32 * u + l < n_in; ++l)
                 D += (int)(int8_t)byte_at(blk, 2 + l) * (int)xq[32 * u + l];
+            acc += s_of(sc, u) * (f16_at(blk) * (float)D);
+        } else if constexpr (TYPE == AH_GGML_Q5_0) {  // format/quant.rs:263-297
+            const uint8_t *blk = row + 22 * u;
+            const uint32_t qh = byte_at(blk, 2) | (byte_at(blk, 3) << 8) | (byte_at(blk, 4) << 16) | (byte_at(blk, 5) << 24);
+            int D = 0;
+            for (uint32_t l = 0; l < 32 && 32 * u + l < n_in; ++l) {
+                const uint32_t j = l & 15u, nib = (byte_at(blk, 6 + j) >> (l < 16 ? 0 : 4)) & 15u;
+                D += ((int)(nib | (((qh >> l) & 1u) << 4)) - 16) * (int)xq[32 * u + l];
+            }
             acc += s_of(sc, u) * (f16_at(blk) * (float)D);
         } else if constexpr (TYPE == AH_GGML_Q4_K) {
             const uint8_t *sb = row + 144 * u;
@@ -370,7 +402,7 @@ AH_DEV __attribute__((always_inline)) void gemm_store(const GemmArgs &a, const G
         // alternate units; split partials are stored in the reduction's units (divided by the
         // token scale, an exact power of two).
         const uint32_t nb32 = (a.n_in + 31) / 32;
-        if (TYPE == AH_GGML_Q8_0 && u_hi > nb32) u_hi = nb32;
+        if (ah_blk32(TYPE) && u_hi > nb32) u_hi = nb32;
         const uint32_t row = row_w + j;
         for (int half = 0; half < 2; ++half) {
             uint64_t mk = fm[half];
@@ -442,7 +474,7 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
 
     // stages: whole super-blocks for the K-quants (zero activations past n_in; their folds are
     // per super-block, at its last stage), pairs for Q8_0
-    const uint32_t nstages = TYPE != AH_GGML_Q8_0 ? a.kpad / kKS : ((a.n_in + 2 * kKS - 1) / (2 * kKS)) * 2;
+    const uint32_t nstages = !ah_blk32(TYPE) ? a.kpad / kKS : ((a.n_in + 2 * kKS - 1) / (2 * kKS)) * 2;
     const uint32_t st_begin = split * pa.stages_per_split;
     uint32_t st_end = st_begin + pa.stages_per_split;
     if (st_end > nstages) st_end = nstages;
@@ -517,7 +549,7 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
         __builtin_amdgcn_sched_barrier(0);  // the requests above stay ahead of this stage's work
         const uint8_t *cur = lds(u % kR);
         const WRb &wc = W[u % NW];
-        if constexpr (TYPE == AH_GGML_Q8_0) {
+        if constexpr (ah_blk32(TYPE)) {
             // 2*NM*NN MFMA chains per stage (block bb, token tile m, row tile n), each two MFMAs
             // into a fresh accumulator that is folded with the block's d.  The fold of chain c-1
             // is issued after chain c's MFMAs, so the VALU fold overlaps the matrix core.
@@ -528,15 +560,33 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
             for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
                 for (int n = 0; n < NN; ++n) {
-                    const uint32_t blk = rbase[n] + 34 * (st * 2 + bb);
-                    const uint32_t shc = (blk + 2 + 16 * h) & 3u;  // 0 or 2
                     const u32x4 v = wc.v[2 * n + bb];
-                    const uint32_t w5[5] = {v.x, v.y, v.z, v.w, wc.s[4 * n + 2 * bb]};
-                    const uint32_t dw = wc.s[4 * n + 2 * bb + 1];
-                    d[bb][n] = ah_f16_bits_to_f32((dw >> (8 * (blk & 3u))) & 0xffffu);
                     uint32_t f[8];
+                    if constexpr (TYPE == AH_GGML_Q8_0) {
+                        const uint32_t blk = rbase[n] + 34 * (st * 2 + bb);
+                        const uint32_t shc = (blk + 2 + 16 * h) & 3u;  // 0 or 2
+                        const uint32_t w5[5] = {v.x, v.y, v.z, v.w, wc.s[4 * n + 2 * bb]};
+                        const uint32_t dw = wc.s[4 * n + 2 * bb + 1];
+                        d[bb][n] = ah_f16_bits_to_f32((dw >> (8 * (blk & 3u))) & 0xffffu);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) i8x4_to_f16(ah_alignbyte(w5[i + 1], w5[i], shc), f[2 * i], f[2 * i + 1]);
+                        for (int i = 0; i < 4; ++i) i8x4_to_f16(ah_alignbyte(w5[i + 1], w5[i], shc), f[2 * i], f[2 * i + 1]);
+                    } else {
+                        // Q5_0 (format/quant.rs:263-297): lane half h takes outputs 16h..16h+15,
+                        // the low (h = 0) or high nibbles of qs[0..15] with qh bits 16h.. as the
+                        // fifth bit; u - 16 is exact in f16
+                        const uint32_t blk = rbase[n] + 22 * (st * 2 + bb);
+                        const bool odd = (blk & 3u) != 0;  // the block starts 2 bytes into its first dword
+                        const uint32_t w6[6] = {v.x, v.y, v.z, v.w, wc.s[4 * n + 2 * bb], wc.s[4 * n + 2 * bb + 1]};
+                        d[bb][n] = ah_f16_bits_to_f32((odd ? w6[0] >> 16 : w6[0]) & 0xffffu);
+                        const uint32_t qh = odd ? w6[1] : ah_alignbyte(w6[1], w6[0], 2);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const uint32_t qs = odd ? w6[i + 2] : ah_alignbyte(w6[i + 2], w6[i + 1], 2);
+                            const uint32_t nib = (h ? qs >> 4 : qs) & 0x0F0F0F0Fu;
+                            const uint32_t hb = (qh >> (16 * h + 4 * i)) & 0xFu;
+                            u5x4_to_f16(nib | (((hb * 0x00204081u) & 0x01010101u) << 4), f[2 * i], f[2 * i + 1]);
+                        }
+                    }
                     bq[bb][n][0] = pack8(f[0], f[1], f[2], f[3]);
                     bq[bb][n][1] = pack8(f[4], f[5], f[6], f[7]);
                 }
@@ -692,15 +742,15 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
     for (uint32_t st = st_begin; st < st_end; st += 4) {
         stage(std::integral_constant<int, 0>{}, st);
         stage(std::integral_constant<int, 1>{}, st + 1);
-        if (TYPE == AH_GGML_Q8_0 && st + 2 >= st_end) break;  // Q8_0 splits are whole pairs
+        if (ah_blk32(TYPE) && st + 2 >= st_end) break;  // Q8_0 / Q5_0 splits are whole pairs
         stage(std::integral_constant<int, 2>{}, st + 2);
         stage(std::integral_constant<int, 3>{}, st + 3);
     }
     // the slices requested past the split must land before this workgroup's LDS is released
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    const uint32_t u_lo = TYPE == AH_GGML_Q8_0 ? 2 * st_begin : st_begin / 4;
-    const uint32_t u_hi = TYPE == AH_GGML_Q8_0 ? 2 * st_end : st_end / 4;
+    const uint32_t u_lo = ah_blk32(TYPE) ? 2 * st_begin : st_begin / 4;
+    const uint32_t u_hi = ah_blk32(TYPE) ? 2 * st_end : st_end / 4;
     gemm_store<TYPE, NM, NN>(a, pa, acc, row_w, rl, rbase, tok0, ntile, split, u_lo, u_hi);
 }
 
@@ -985,7 +1035,7 @@ struct GemmGeom {
 GemmGeom geom_of(uint32_t type, uint32_t n_in, uint32_t kpad, uint32_t waves = 4, bool int8 = false) {
     const uint32_t rows = 32u * rb::kNN * waves;
     if (int8) return {i8::stages(n_in), 1, rows, i8::kTok};  // stages of 4 blocks
-    if (type == AH_GGML_Q8_0) return {(n_in + 2 * kKS - 1) / (2 * kKS) * 2, 2, rows, rb::tok_of(type)};
+    if (ah_blk32((int)type)) return {(n_in + 2 * kKS - 1) / (2 * kKS) * 2, 2, rows, rb::tok_of(type)};
     return {kpad / kKS, 4, rows, rb::tok_of(type)};  // K-quants: whole super-blocks
 }
 
@@ -1008,7 +1058,7 @@ uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint3
                              uint32_t cus, bool int8) {
     const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4, int8);
     const uint64_t tiles = (uint64_t)((n_out + g.rows - 1) / g.rows) * ((n_tok + g.toks - 1) / g.toks);
-    const double c = int8 ? 1.0 : type == AH_GGML_Q8_0 ? 0.806 : type == AH_GGML_Q4_K ? 0.400 : 1.081;
+    const double c = int8 ? 1.0 : ah_blk32((int)type) ? 0.806 : type == AH_GGML_Q4_K ? 0.400 : 1.081;
     uint32_t best = 1;
     double best_cost = 1e30;
     for (uint32_t want = 1; want <= 64 && want <= g.nstages; ++want) {
@@ -1216,6 +1266,7 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     switch (type) {
     case kGemmMixedKQuant: hipLaunchKernelGGL(gemm_rb_kquant_kernel, rb_grid, blk, 0, stream, a); break;
     case AH_GGML_Q8_0: AH_GFORMS(AH_GGML_Q8_0) break;
+    case AH_GGML_Q5_0: AH_GFORMS(AH_GGML_Q5_0) break;
     case AH_GGML_Q4_K: hipLaunchKernelGGL((gemm_rb_kernel<AH_GGML_Q4_K, 4, 4>), rb_grid, blk, 0, stream, a); break;
     case AH_GGML_Q6_K: AH_GFORMS(AH_GGML_Q6_K) break;
     default: return hipErrorInvalidValue;

@@ -366,6 +366,37 @@ AH_DEV float unit_q8(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &
     return ah_f16_bits_to_f32(d16) * A.fsc[b] * (float)D;
 }
 
+// Q5_0 block at byte `off` of the tile (format/quant.rs:261-297): f16 d at byte 0, the fifth bits
+// qh (a little-endian u32) at 2..5, 16 bytes of nibbles at 6..21.  Output j < 16 is qs[j] & 15 with
+// qh bit j as its fifth bit, output 16 + j is qs[j] >> 4 with qh bit 16 + j, each minus 16.  The
+// five-bit values u (0..31) go to v_dot4 as bytes (four qh bits spread to bit 4 of four bytes by
+// one multiply), and the -16 offset is folded through the block's code sum: D = sum u*xq - 16*X.
+template <bool DOTS>
+AH_DEV float unit_q5(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &A, int32_t *dots) {
+    const bool odd = (off & 3u) != 0;  // 2-byte aligned blocks: 6 dwords from the 4-aligned start
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(tl + (off & ~3u));
+    uint32_t w[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) w[i] = p[i];
+    const uint32_t d16 = (odd ? (w[0] >> 16) : w[0]) & 0xffffu;
+    const uint32_t qh = odd ? w[1] : ah_alignbyte(w[1], w[0], 2);
+    const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * b));
+    const u32x4 x0 = xv[0], x1 = xv[1];
+    const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    int32_t D = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t qs = odd ? w[i + 2] : ah_alignbyte(w[i + 2], w[i + 1], 2);
+        const uint32_t blo = ((((qh >> (4 * i)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+        const uint32_t bhi = ((((qh >> (16 + 4 * i)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+        D = ah_sdot4((qs & 0x0F0F0F0Fu) | blo, xw[i], D);
+        D = ah_sdot4(((qs >> 4) & 0x0F0F0F0Fu) | bhi, xw[4 + i], D);
+    }
+    D -= 16 * A.xs32[b];
+    if (DOTS && dots) dots[b] = D;
+    return ah_f16_bits_to_f32(d16) * A.fsc[b] * (float)D;
+}
+
 // Q4_K super-block s (format/quant.rs:481-510): d, dmin, 12 packed 6-bit (scale, min) pairs,
 // 128 bytes of nibbles; sub-block j takes the low (j even) / high (j odd) nibbles of
 // qs[32*(j/2) + l].  Term per sub-block: S_j * (d*sc_j*D_j - dmin*m_j*X_j).
@@ -506,6 +537,9 @@ AH_DEV float comp_unit(const GemvPart &P, const uint8_t *tl, uint32_t off, uint3
     if constexpr (TYPE == AH_GGML_Q8_0) {
         const uint32_t nb32 = (P.n_in + 31) / 32;
         return unit_q8<DOTS>(tl, off, u, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
+    } else if constexpr (TYPE == AH_GGML_Q5_0) {
+        const uint32_t nb32 = (P.n_in + 31) / 32;
+        return unit_q5<DOTS>(tl, off, u, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
     } else if constexpr (TYPE == AH_GGML_Q4_K) {
         const uint32_t nb32 = (P.n_in + 31) / 32;
         return unit_q4<DOTS>(tl, off, u, P.n_in, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
@@ -515,10 +549,11 @@ AH_DEV float comp_unit(const GemvPart &P, const uint8_t *tl, uint32_t off, uint3
     }
 }
 
-// Byte offset of unit u within a row: Q8_0 blocks, Q4_K super-blocks, Q6_K half super-blocks
-// (both halves of a super-block start at its first byte).
+// Byte offset of unit u within a row: Q8_0 / Q5_0 blocks, Q4_K super-blocks, Q6_K half
+// super-blocks (both halves of a super-block start at its first byte).
 constexpr uint32_t unit_off(int type, uint32_t u) {
-    return type == AH_GGML_Q8_0 ? 34u * u : type == AH_GGML_Q4_K ? 144u * u : 210u * (u >> 1);
+    return type == AH_GGML_Q8_0 ? 34u * u : type == AH_GGML_Q5_0 ? 22u * u
+         : type == AH_GGML_Q4_K ? 144u * u : 210u * (u >> 1);
 }
 constexpr uint32_t kRedSlots = 1024;  // unit partials of one tile
 constexpr uint32_t kTileSlack = 128;  // bytes past a tile that realigned or compact-row unit reads may touch
@@ -1016,6 +1051,10 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
                         acc += comp_unit<AH_GGML_Q6_K, DOTS>(P, tl, toff + r * RB + unit_off(AH_GGML_Q6_K, u), row, u, A);
+                } else if (P.type == AH_GGML_Q5_0) {
+#pragma unroll 1
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q5_0, DOTS>(P, tl, toff + r * RB + unit_off(AH_GGML_Q5_0, u), row, u, A);
                 } else {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
@@ -1326,6 +1365,10 @@ AH_DEV void seq_gemv_stage(const SeqArgs &a, uint32_t s, uint32_t r, bool &broke
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
                         acc += comp_unit<AH_GGML_Q6_K, false>(P, tl, toff + rr * RB + unit_off(AH_GGML_Q6_K, u), row, u, A);
+                } else if (P.type == AH_GGML_Q5_0) {
+#pragma unroll 1
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q5_0, false>(P, tl, toff + rr * RB + unit_off(AH_GGML_Q5_0, u), row, u, A);
                 } else {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
@@ -1426,6 +1469,7 @@ static const void *stream_fn(uint32_t type, bool plan, bool dots = false) {
                     : dots ? nullptr : reinterpret_cast<const void *>(&gemv_stream_kernel<kMixedType, false, false>);
     switch (type) {
     case AH_GGML_Q8_0: AH_SFN(AH_GGML_Q8_0)
+    case AH_GGML_Q5_0: AH_SFN(AH_GGML_Q5_0)
     case AH_GGML_Q4_K: AH_SFN(AH_GGML_Q4_K)
     case AH_GGML_Q6_K: AH_SFN(AH_GGML_Q6_K)
     default: return nullptr;
@@ -1437,6 +1481,7 @@ static const void *seq_fn(uint32_t type) {
     switch (type) {
     case kMixedType: return reinterpret_cast<const void *>(&gemv_seq_kernel<kMixedType>);
     case AH_GGML_Q8_0: return reinterpret_cast<const void *>(&gemv_seq_kernel<AH_GGML_Q8_0>);
+    case AH_GGML_Q5_0: return reinterpret_cast<const void *>(&gemv_seq_kernel<kMixedType>);  // rare: no own form
     case AH_GGML_Q4_K: return reinterpret_cast<const void *>(&gemv_seq_kernel<AH_GGML_Q4_K>);
     case AH_GGML_Q6_K: return reinterpret_cast<const void *>(&gemv_seq_kernel<AH_GGML_Q6_K>);
     default: return nullptr;
@@ -1492,6 +1537,7 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const StreamParts &sp, const Gem
                            stream, sp, d_parts, d_wgd, act_bytes, status);
     switch (type) {
     case AH_GGML_Q8_0: AH_SLAUNCH(AH_GGML_Q8_0) break;
+    case AH_GGML_Q5_0: AH_SLAUNCH(AH_GGML_Q5_0) break;
     case AH_GGML_Q4_K: AH_SLAUNCH(AH_GGML_Q4_K) break;
     case AH_GGML_Q6_K: AH_SLAUNCH(AH_GGML_Q6_K) break;
     case kMixedType:
@@ -1554,10 +1600,11 @@ hipError_t ah_gemv_init_attrs() {
         e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_kernel<T, N>),                \
                                 hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     AH_ATTR(AH_GGML_Q8_0, 4) AH_ATTR(AH_GGML_Q8_0, 8) AH_ATTR(AH_GGML_Q8_0, 12)
+    AH_ATTR(AH_GGML_Q5_0, 4) AH_ATTR(AH_GGML_Q5_0, 8) AH_ATTR(AH_GGML_Q5_0, 12)
     AH_ATTR(AH_GGML_Q4_K, 4) AH_ATTR(AH_GGML_Q4_K, 8) AH_ATTR(AH_GGML_Q4_K, 12)
     AH_ATTR(AH_GGML_Q6_K, 4) AH_ATTR(AH_GGML_Q6_K, 8) AH_ATTR(AH_GGML_Q6_K, 12)
 #undef AH_ATTR
-    for (uint32_t t : {AH_GGML_Q8_0, AH_GGML_Q4_K, AH_GGML_Q6_K})
+    for (uint32_t t : {AH_GGML_Q8_0, AH_GGML_Q5_0, AH_GGML_Q4_K, AH_GGML_Q6_K})
         for (int v = 0; v < 3; ++v)
             if (e == hipSuccess)
                 e = hipFuncSetAttribute(stream_fn(t, v == 1, v == 2), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
@@ -1576,6 +1623,9 @@ hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart 
     switch (type) {
     case AH_GGML_Q8_0:
         launch_type<AH_GGML_Q8_0>(nc, dim3(grid), lds, stream, single, d_parts, d_wg_part, kpad_max, status);
+        break;
+    case AH_GGML_Q5_0:
+        launch_type<AH_GGML_Q5_0>(nc, dim3(grid), lds, stream, single, d_parts, d_wg_part, kpad_max, status);
         break;
     case AH_GGML_Q4_K:
         launch_type<AH_GGML_Q4_K>(nc, dim3(grid), lds, stream, single, d_parts, d_wg_part, kpad_max, status);

@@ -19,9 +19,9 @@ from __future__ import annotations
 
 import numpy as np
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
-GEOM = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
-NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+Q5_0, Q8_0, Q4_K, Q6_K = 6, 8, 12, 14
+GEOM = {Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+NAMES = {Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
 
 
 def row_bytes(ggml_type: int, n_in: int) -> int:
@@ -31,8 +31,8 @@ def row_bytes(ggml_type: int, n_in: int) -> int:
 
 def needed_row_bytes(ggml_type: int, n_in: int) -> int:
     """Bytes of one row a correct kernel must read (the algorithmic traffic per row)."""
-    if ggml_type == Q8_0:
-        return 34 * (-(-n_in // 32))
+    if ggml_type in (Q8_0, Q5_0):
+        return GEOM[ggml_type][1] * (-(-n_in // 32))
     full, rem = divmod(n_in, 256)
     if ggml_type == Q4_K:
         # header 16 B + the qs bytes of the used sub-block pairs
@@ -61,6 +61,18 @@ def q8_0_payload(rng: np.random.Generator, rows: int, n_in: int, sigma: float = 
     blk[:, 0] = d & 0xFF
     blk[:, 1] = d >> 8
     blk[:, 2:] = rng.integers(-127, 128, size=(rows * nb, 32), dtype=np.int16).astype(np.int8).view(np.uint8)
+    return blk.reshape(-1)
+
+
+def q5_0_payload(rng: np.random.Generator, rows: int, n_in: int, sigma: float = 0.02) -> np.ndarray:
+    """Q5_0 blocks (format/quant.rs:261-297): f16 d = |N(0, sigma)| / 16, random qh and qs bytes
+    (every five-bit code 0..31 equally likely)."""
+    nb = -(-n_in // 32)
+    blk = np.empty((rows * nb, 22), dtype=np.uint8)
+    d = _f16_abs_normal(rng, rows * nb, sigma, 16.0)
+    blk[:, 0] = d & 0xFF
+    blk[:, 1] = d >> 8
+    blk[:, 2:] = rng.integers(0, 256, size=(rows * nb, 20), dtype=np.uint8)
     return blk.reshape(-1)
 
 
@@ -124,6 +136,8 @@ def q6_k_payload(rng: np.random.Generator, rows: int, n_in: int, sigma: float = 
 def payload(ggml_type: int, rng: np.random.Generator, rows: int, n_in: int) -> np.ndarray:
     if ggml_type == Q8_0:
         return q8_0_payload(rng, rows, n_in)
+    if ggml_type == Q5_0:
+        return q5_0_payload(rng, rows, n_in)
     if ggml_type == Q4_K:
         return q4_k_payload(rng, rows, n_in)
     if ggml_type == Q6_K:
@@ -137,7 +151,7 @@ def random_bytes_payload(rng: np.random.Generator, ggml_type: int, rows: int, n_
     qk, bb = GEOM[ggml_type]
     nblk = rows * (-(-n_in // qk))
     raw = rng.integers(0, 256, size=(nblk, bb), dtype=np.uint8)
-    if ggml_type == Q8_0:
+    if ggml_type in (Q8_0, Q5_0):
         raw[:, 0], raw[:, 1] = d & 0xFF, d >> 8
     elif ggml_type == Q4_K:
         raw[:, 0], raw[:, 1] = d & 0xFF, d >> 8

@@ -62,6 +62,7 @@ extern "C" {
 #define AH_ERR_SEQ_TIMEOUT 25         /* a sequence's grid barrier waited past its limit    */
 
 /* ggml type ids (format/quant.rs:20-49) */
+#define AH_GGML_Q5_0 6   /* format/quant.rs:28-29, :261-297 */
 #define AH_GGML_Q8_0 8
 #define AH_GGML_Q4_K 12
 #define AH_GGML_Q6_K 14

@@ -87,6 +87,21 @@ static int decode_row(uint32_t t, const uint8_t *row, size_t nb32, int8_t *codes
             cf[b].cmin = 0;
             memcpy(codes + 32 * b, blk + 2, 32);
         }
+    } else if (t == AHO_Q5_0) {
+        /* format/quant.rs:263-297 (the five-bit codes minus 16) */
+        for (size_t b = 0; b < nb32; b++) {
+            const uint8_t *blk = row + 22 * b;
+            int64_t d = f16_fixed_or_marker(rd16(blk));
+            bad |= d;
+            cf[b].clo = cf[b].chi = d;
+            cf[b].cmin = 0;
+            const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                                ((uint32_t)blk[5] << 24);
+            for (int j = 0; j < 16; j++) {
+                codes[32 * b + j] = (int8_t)((int)((blk[6 + j] & 0xF) | (((qh >> j) & 1) << 4)) - 16);
+                codes[32 * b + 16 + j] = (int8_t)((int)((blk[6 + j] >> 4) | (((qh >> (16 + j)) & 1) << 4)) - 16);
+            }
+        }
     } else if (t == AHO_Q4_K) {
         size_t nsb = (nb32 + 7) / 8;
         for (size_t s = 0; s < nsb; s++) {
@@ -139,16 +154,16 @@ static int decode_row(uint32_t t, const uint8_t *row, size_t nb32, int8_t *codes
     return (bad & 1) != 0;
 }
 
-/* The call-level fast bound, chart/mod.rs:336-383 (narrow form for Q8_0). */
+/* The call-level fast bound, chart/mod.rs:336-383 (narrow form for Q8_0 and Q5_0). */
 static int fast_bound_ok(uint32_t t, size_t n_in, const int64_t *scales, size_t nb32) {
-    i128 top = t == AHO_Q8_0 ? 128 : t == AHO_Q4_K ? 1008 : 4096;
+    i128 top = t == AHO_Q8_0 ? 128 : t == AHO_Q5_0 ? 16 : t == AHO_Q4_K ? 1008 : 4096;
     i128 smax = 0;
     for (size_t b = 0; b < nb32; b++) {
         i128 a = scales[b] < 0 ? -(i128)scales[b] : (i128)scales[b];
         if (a > smax) smax = a;
     }
     const i128 imax = (i128)(((unsigned __int128)1 << 127) - 1);
-    if (t == AHO_Q8_0) {
+    if (t == AHO_Q8_0 || t == AHO_Q5_0) {
         i128 p;
         if (__builtin_mul_overflow(smax, 32 * top * 127, &p) || p > (i128)INT64_MAX) return 0;
     }
@@ -357,7 +372,7 @@ int aho_matvec_q8act_fast(uint32_t t, const uint8_t *raw, size_t raw_len, size_t
         size_t lo = task * per, hi = lo + per < n_out ? lo + per : n_out;
         int8_t *wc = NULL;
         grp_coef *cf = NULL;
-        if (!avx2) {
+        if (!avx2 || t == AHO_Q5_0) {
             wc = (int8_t *)malloc(nb32 * 32 + 32);
             cf = (grp_coef *)malloc((nb32 + 8) * sizeof(grp_coef));
         }
@@ -365,7 +380,10 @@ int aho_matvec_q8act_fast(uint32_t t, const uint8_t *raw, size_t raw_len, size_t
             const uint8_t *row = raw + r * row_bytes;
             i128 acc = 0;
             int bad;
-            if (avx2) {
+            if (avx2 && t == AHO_Q5_0) {  /* decoded row, then the shared AVX2 accumulator */
+                bad = decode_row(t, row, nb32, wc, cf);
+                if (!bad) acc = row_acc_avx2(wc, cf, nb32, pa.codes, scales, pa.xs32);
+            } else if (avx2) {
                 if (t == AHO_Q8_0) bad = q8_0_row_direct(row, nb32, pa.codes, scales, &acc);
                 else if (t == AHO_Q4_K) bad = q4_k_row_direct(row, nb32, pa.codes, scales, pa.xs32, &acc);
                 else bad = q6_k_row_direct(row, nb32, pa.codes, scales, pa.xs16, &acc);

@@ -15,6 +15,7 @@ typedef unsigned __int128 u128;
 
 #define QK_K 256
 #define Q8_0_BYTES 34
+#define Q5_0_BYTES 22
 #define Q4_K_BYTES 144
 #define Q6_K_BYTES 210
 
@@ -22,6 +23,7 @@ typedef unsigned __int128 u128;
 int aho_block_geom(uint32_t t, size_t *qk, size_t *bb) {
     switch (t) {
     case AHO_Q8_0: *qk = 32; *bb = Q8_0_BYTES; return 1;
+    case AHO_Q5_0: *qk = 32; *bb = Q5_0_BYTES; return 1;
     case AHO_Q4_K: *qk = QK_K; *bb = Q4_K_BYTES; return 1;
     case AHO_Q6_K: *qk = QK_K; *bb = Q6_K_BYTES; return 1;
     default: return 0;
@@ -195,6 +197,18 @@ static void q6k_codes(const uint8_t *blk, int8_t *out) {
         }
 }
 
+/* format/quant.rs:263-297: the 32 Q5_0 codes in output order, already minus 16.  qs[j]'s low
+ * nibble is output j, its high nibble output 16 + j; the fifth bit of output j is bit j of qh read
+ * as a little-endian u32, that of output 16 + j is bit 16 + j. */
+static void q50_codes(const uint8_t *blk, int8_t *out) {
+    const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24);
+    const uint8_t *qs = blk + 6;
+    for (int j = 0; j < 16; j++) {
+        out[j] = (int8_t)((int)((qs[j] & 0xF) | (((qh >> j) & 1) << 4)) - 16);
+        out[16 + j] = (int8_t)((int)((qs[j] >> 4) | (((qh >> (16 + j)) & 1) << 4)) - 16);
+    }
+}
+
 /* The integer codes of one super-block / block in output order (Q4_K: nibbles 0..15). */
 static void q4k_codes(const uint8_t *blk, uint8_t *out) {
     const uint8_t *qs = blk + 16;
@@ -221,6 +235,13 @@ int aho_dequant_row(uint32_t t, const uint8_t *row, size_t row_len, size_t n, in
             int64_t d;
             if ((st = aho_f16_to_fixed(rd16(blk), &d))) return st;
             for (size_t l = 0; l < take; l++) out[b * qk + l] = d * (int64_t)(int8_t)blk[2 + l];
+        } else if (t == AHO_Q5_0) {
+            /* num/dequant.rs:353-380: w = d * (q - 16) */
+            int64_t d;
+            if ((st = aho_f16_to_fixed(rd16(blk), &d))) return st;
+            int8_t c[32];
+            q50_codes(blk, c);
+            for (size_t l = 0; l < take; l++) out[b * qk + l] = d * (int64_t)c[l];
         } else if (t == AHO_Q4_K) {
             int64_t d, dmin;
             if ((st = aho_f16_to_fixed(rd16(blk), &d))) return st;
@@ -320,6 +341,15 @@ int aho_block_dots(uint32_t t, const uint8_t *row, size_t row_len, size_t n_in,
             int32_t s = 0;
             for (size_t l = 0; l < 32 && b * 32 + l < n_in; l++)
                 s += (int32_t)(int8_t)row[b * 34 + 2 + l] * codes[b * 32 + l];
+            dots[b] = s;
+        }
+    } else if (t == AHO_Q5_0) {
+        /* chart/mod.rs:630-712: one group per block, dot = sum (q - 16) * xq */
+        for (size_t b = 0; b < nb32; b++) {
+            int8_t c[32];
+            q50_codes(row + b * Q5_0_BYTES, c);
+            int32_t s = 0;
+            for (size_t l = 0; l < 32 && b * 32 + l < n_in; l++) s += (int32_t)c[l] * codes[b * 32 + l];
             dots[b] = s;
         }
     } else if (t == AHO_Q4_K) {

@@ -53,7 +53,7 @@ enum {
     AHO_ERR_ZERO_DENOMINATOR = 14         /* FfnError::ZeroDenominator                  */
 };
 
-enum { AHO_Q8_0 = 8, AHO_Q4_K = 12, AHO_Q6_K = 14 };
+enum { AHO_Q5_0 = 6, AHO_Q8_0 = 8, AHO_Q4_K = 12, AHO_Q6_K = 14 };
 
 /* (weights per block, bytes per block) -- format/quant.rs:129-147.  0 on unknown type. */
 int aho_block_geom(uint32_t ggml_type, size_t *qk, size_t *block_bytes);

@@ -98,6 +98,16 @@ def q4k_pairs(sc12: bytes) -> list[tuple[int, int]]:
     return out
 
 
+def q5_0_codes(blk: bytes) -> list[int]:
+    """A Q5_0 block's 32 codes minus 16: element e < 16 is qs[e] & 15 with the fifth bit from bit e of
+    the little-endian word qh = blk[2:6]; element 16 + e is qs[e] >> 4 with bit 16 + e."""
+    qh = int.from_bytes(blk[2:6], "little")
+    qs = blk[6:22]
+    lo = [(qs[e] & 15) + 16 * ((qh >> e) & 1) - 16 for e in range(16)]
+    hi = [(qs[e] >> 4) + 16 * ((qh >> (16 + e)) & 1) - 16 for e in range(16)]
+    return lo + hi
+
+
 def weights_row(ggml_type: int, row: bytes, n: int) -> list[int] | None:
     """Exact Q32.32 weights of one row, or None for a non-finite scale."""
     w: list[int] = []
@@ -108,6 +118,13 @@ def weights_row(ggml_type: int, row: bytes, n: int) -> list[int] | None:
             if d is None:
                 return None
             w += [d * (c - 256 if c > 127 else c) for c in blk[2:34]]
+    elif ggml_type == 6:
+        for b in range(-(-n // 32)):
+            blk = row[22 * b:22 * b + 22]
+            d = f16_q32(blk[0] | (blk[1] << 8))
+            if d is None:
+                return None
+            w += [d * c for c in q5_0_codes(blk)]
     elif ggml_type == 12:
         for s in range(-(-n // 256)):
             blk = row[144 * s:144 * s + 144]
@@ -147,7 +164,8 @@ def weights_row(ggml_type: int, row: bytes, n: int) -> list[int] | None:
 
 def matvec(ggml_type: int, raw: bytes, n_out: int, n_in: int, xhat: list[int]):
     """floor((sum w*xhat + 2^31) / 2^32) per row, or None on a refusal."""
-    rb = {8: 34 * -(-n_in // 32), 12: 144 * -(-n_in // 256), 14: 210 * -(-n_in // 256)}[ggml_type]
+    rb = {6: 22 * -(-n_in // 32), 8: 34 * -(-n_in // 32), 12: 144 * -(-n_in // 256),
+          14: 210 * -(-n_in // 256)}[ggml_type]
     ys = []
     for o in range(n_out):
         w = weights_row(ggml_type, raw[o * rb:(o + 1) * rb], n_in)
@@ -159,11 +177,15 @@ def matvec(ggml_type: int, raw: bytes, n_out: int, n_in: int, xhat: list[int]):
 
 
 def block_dots(ggml_type: int, row: bytes, n_in: int, codes: list[int]):
-    """Exact integer group dots: per-32 (Q8_0 codes, Q4_K nibbles), per-16 (Q6_K u-32)."""
+    """Exact integer group dots: per-32 (Q8_0 codes, Q5_0 q-16, Q4_K nibbles), per-16 (Q6_K u-32)."""
     w_codes: list[int] = []
     if ggml_type == 8:
         for b in range(-(-n_in // 32)):
             w_codes += [c - 256 if c > 127 else c for c in row[34 * b + 2:34 * b + 34]]
+        g = 32
+    elif ggml_type == 6:
+        for b in range(-(-n_in // 32)):
+            w_codes += q5_0_codes(row[22 * b:22 * b + 22])
         g = 32
     elif ggml_type == 12:
         for s in range(-(-n_in // 256)):

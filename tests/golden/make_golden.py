@@ -71,6 +71,23 @@ def main() -> None:
             c = case_from_q32(8, raw, 4, 96, x)
             if all(-(1 << 63) <= v < (1 << 63) for v in c["y"]):
                 cases.append(("scaleset", c))
+    # Q5_0 (format/quant.rs:261-297), appended with a stream of its own so the cases above keep
+    # their bytes: the same shape families, random qh/qs bytes, BASELINE-style payloads with f32
+    # N(0,1) input, the largest finite scale against +-127 codes, zero activation blocks
+    rng5 = np.random.default_rng(0x60DE50)
+    for rows, n_in in shapes + [(2, w) for w in (47, 65, 257, 271)]:
+        raw = synth.random_bytes_payload(rng5, 6, rows, n_in, 0x3800, 0x3800)
+        x = rng5.integers(-2048, 2048, size=n_in)
+        cases.append(("random", case_from_q32(6, raw, rows, n_in, x)))
+    raw = synth.payload(6, rng5, 3, 896)
+    xf = rng5.standard_normal(896).astype(np.float32)
+    c = case_from_q32(6, raw, 3, 896, [bf.f32_q32(int(w)) for w in xf.view(np.uint32)])
+    c["xf"] = xf
+    cases.append(("f32", c))
+    raw = synth.random_bytes_payload(rng5, 6, 2, 256, 0x7BFF, 0x7BFF)
+    cases.append(("extreme", case_from_q32(6, raw, 2, 256, [127 if j % 2 == 0 else -127 for j in range(256)])))
+    raw = synth.random_bytes_payload(rng5, 6, 1, 96, 0x3800, 0x3800)
+    cases.append(("zeroblk", case_from_q32(6, raw, 1, 96, [0] * 64 + [1000 - 100 * j for j in range(64, 96)])))
     out = {}
     for i, (kind, c) in enumerate(cases):
         p = f"c{i:03d}_"

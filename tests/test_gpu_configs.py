@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
 Q32 = 2.0 ** -32
-Q8_0, Q4_K, Q6_K = 8, 12, 14
+Q5_0, Q8_0, Q4_K, Q6_K = 6, 8, 12, 14
 CFG4_Q6K_DOWN = {0, 1, 2, 5, 8, 11, 14, 17, 20, 23, 24, 25, 26, 27}
 
 
@@ -122,6 +122,38 @@ def test_argument_plan_limits_vs_oracle(dev):
     plan_vs_oracle(dev, four, 40)
     plan_vs_oracle(dev, four + [("e", Q6_K, 33, 1024)], 41)
     plan_vs_oracle(dev, [("s", Q8_0, 1, 32)], 42)
+    # Q5_0 parts through the mixed-type kernel (argument and table plans) and alone
+    q5 = [("q5a", Q5_0, 640, 896), ("q4", Q4_K, 100, 896), ("q5b", Q5_0, 33, 300), ("q6", Q6_K, 64, 512)]
+    plan_vs_oracle(dev, q5, 43)
+    plan_vs_oracle(dev, q5 + [("q5c", Q5_0, 5, 4864)], 44)
+    plan_vs_oracle(dev, [("q5", Q5_0, 896, 896), ("q5k", Q5_0, 128, 896)], 45)
+
+
+def test_qwen05b_q4_k_m_layer_with_q5_0_tensors(dev):
+    """A Qwen2.5-0.5B layer in a mixed-quant checkpoint's style (its ffn_gate and attn_output are
+    Q5_0 there, tests/gpu_gemv_match.rs:252-275; here every K = 896 tensor is Q5_0 and ffn_down
+    Q6_K): one mixed plan at N = 1 and the grouped prefill at N = 300, every part against the
+    oracle."""
+    layer = [("q", Q5_0, 896, 896), ("k", Q5_0, 128, 896), ("v", Q5_0, 128, 896), ("o", Q5_0, 896, 896),
+             ("gate", Q5_0, 4864, 896), ("up", Q5_0, 4864, 896), ("down", Q6_K, 896, 4864)]
+    plan_vs_oracle(dev, layer, 46)
+    rng = synth.rng_for(1, 4600)
+    n_tok = 300
+    x = synth.activations(rng, 896, n_tok)
+    dx = to_dev(x)
+    parts = [p for p in layer if p[3] == 896]
+    raws = [synth.payload(t, rng, n, k) for _, t, n, k in parts]
+    W = [dev.upload(t, r, n, k) for (_, t, n, k), r in zip(parts, raws)]
+    ys = [torch.full((n_tok, n), float("nan"), dtype=torch.float32, device="cuda") for _, _, n, _ in parts]
+    chart.gemm_group_f32_dev(dev, W, dx.data_ptr(), n_tok, [y.data_ptr() for y in ys], stream())
+    assert dev.sync_status(stream()) == 0
+    for (name, t, n, k), raw, y in zip(parts, raws, ys):
+        Y = y.cpu().numpy()
+        rows = sample_rows(rng, n, 64)
+        for c in (0, 150, 299):
+            check_rows(t, raw, k, rows, x[c], Y[c, rows], f"q5_0 layer {name} col {c}")
+    for w in W:
+        w.free()
 
 
 @pytest.mark.parametrize("layer", [0, 3])

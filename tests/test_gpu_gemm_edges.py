@@ -195,7 +195,7 @@ def test_gemm_reference_equality_inputs(dev, n_out, n_in):
         assert refusals > 0  # the largest scale word drives some calls past 2^31
 
 
-@pytest.mark.parametrize("t", [12, 14, 8])
+@pytest.mark.parametrize("t", [12, 14, 8, 6])
 @pytest.mark.parametrize("n_in", [256, 1024])
 def test_gemm_spread_columns(dev, t, n_in):
     """chart/tests.rs:1080-1110 (29 binades across a column) through the GEMM, n_out = 7."""
@@ -246,9 +246,10 @@ def cliff_case(t, n_in, gap, rng):
     rb = synth.row_bytes(t, n_in)
     R = raw.reshape(16, rb)
     half = n_in // 2
-    if t == 8:
+    if t in (8, 6):
+        bb = 34 if t == 8 else 22
         for b in range(half // 32):
-            R[:, 34 * b:34 * b + 2] = 0
+            R[:, bb * b:bb * b + 2] = 0
     else:
         for sb in range(half // 256):
             off = (210 * sb + 208) if t == 14 else 144 * sb
@@ -259,7 +260,7 @@ def cliff_case(t, n_in, gap, rng):
     return R.reshape(-1), x
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 12, 14])
 @pytest.mark.parametrize("gap", [27, 24, 20, 12])
 def test_gemm_zero_weight_heavy_blocks(dev, t, gap):
     """Heavy blocks against zero weights, the rest 2^gap lower.  gap 27 is past the f16 band
@@ -281,7 +282,7 @@ def test_gemm_zero_weight_heavy_blocks(dev, t, gap):
     w.free()
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 12, 14])
 def test_gemm_f32_input_wide_spread_tokens(dev, t):
     """f32 input whose blocks span ~40 binades (flagged by the operand pass, whose quantized codes
     it keeps for the exact path) mixed with ordinary tokens, at a split-K shape and a small one."""

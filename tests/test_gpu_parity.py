@@ -155,7 +155,7 @@ def test_gemv_golden_fixtures(dev):
     assert n >= 40
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 12, 14])
 @pytest.mark.parametrize("n_out,n_in", [(4864, 896), (896, 4864), (128, 896), (333, 1536), (37, 8960), (5, 100),
                                          (301, 300), (2001, 576), (7, 32768), (9, 20000)])
 def test_gemv_config_shapes(dev, t, n_out, n_in):
@@ -296,7 +296,7 @@ def test_upload_refusals(dev):
     with pytest.raises(chart.MatvecError) as e:
         dev.upload(3, raw, 4, 64)
     assert e.value.kind == "UnsupportedQuant"
-    for t, off in ((8, 34), (12, 146), (14, 210 + 208)):
+    for t, off in ((8, 34), (6, 22), (12, 146), (14, 210 + 208)):
         raw = synth.payload(t, synth.rng_for(0, t), 3, 256)
         raw[off:off + 2] = [0x00, 0x7C]  # +inf scale in a later block
         with pytest.raises(chart.MatvecError) as e:
@@ -358,13 +358,13 @@ def gemm_check(dev, t, n_out, n_in, n_tok, sample_cols=None, seed=0):
     return Y
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 12, 14])
 @pytest.mark.parametrize("n_out,n_in,n_tok", [(64, 256, 8), (96, 300, 33), (200, 896, 130), (33, 64, 2)])
 def test_gemm_small_shapes(dev, t, n_out, n_in, n_tok):
     gemm_check(dev, t, n_out, n_in, n_tok)
 
 
-@pytest.mark.parametrize("t", [8, 12])
+@pytest.mark.parametrize("t", [6, 8, 12])
 @pytest.mark.parametrize("n_out,n_in", [(4864, 896), (896, 4864), (8960, 1536), (1536, 8960)])
 def test_gemm_config3_shapes(dev, t, n_out, n_in):
     gemm_check(dev, t, n_out, n_in, 512, sample_cols=[0, 1, 127, 128, 255, 300, 511])
@@ -442,7 +442,7 @@ def test_mfma_probe_within_published_peaks(dev):
         dev.probe_mfma_peak(2)
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 12, 14])
 @pytest.mark.parametrize("n_out,n_in,n_tok", [(96, 301, 5), (130, 8960, 70), (64, 20000, 3), (256, 1536, 129)])
 def test_gemm_codes_input_equals_f32_input(dev, t, n_out, n_in, n_tok):
     """The codes-input GEMM (quantizer output handed over) equals the f32-input GEMM bit for bit:

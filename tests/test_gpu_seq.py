@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
 Q32 = 2.0 ** -32
-Q8_0, Q4_K, Q6_K = 8, 12, 14
+Q5_0, Q8_0, Q4_K, Q6_K = 6, 8, 12, 14
 ONE = 1 << 32
 
 
@@ -117,7 +117,8 @@ def ffn_case(dev, rng, n_embd, n_ff, down_type, sigma=1.0 / 32):
     return raws, W
 
 
-@pytest.mark.parametrize("n_embd,n_ff,down_type", [(1536, 8960, Q6_K), (896, 4864, Q4_K), (256, 300, Q8_0)])
+@pytest.mark.parametrize("n_embd,n_ff,down_type", [(1536, 8960, Q6_K), (896, 4864, Q4_K), (256, 300, Q8_0),
+                                                    (896, 4864, Q5_0)])
 def test_seq_fused_ffn_vs_oracle(dev, n_embd, n_ff, down_type):
     rng = synth.rng_for(9, n_ff)
     raws, W = ffn_case(dev, rng, n_embd, n_ff, down_type)

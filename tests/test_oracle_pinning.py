@@ -156,6 +156,25 @@ def test_format_unpack_kats():
     b8[2], b8[3] = 2, 0xFE
     st, w = oracle.dequant_row(8, b8, 32)
     assert st == 0 and w[0] == ONE and w[1] == -ONE
+    # Q5_0 (format/quant.rs:836-857): d = 0.5; qh[0] = 0b101 sets the fifth bit of outputs 0 and 2,
+    # qh[2] = 1 that of output 16; qs[0] = 0xFF, qs[1] = 0, qs[2] = 0x10
+    b5 = np.zeros(22, np.uint8)
+    b5[0:2] = [0x00, 0x38]
+    b5[2], b5[4] = 0b101, 1
+    b5[6], b5[7], b5[8] = 0xFF, 0x00, 0x10
+    st, w = oracle.dequant_row(6, b5, 32)
+    assert st == 0
+    got = {i: int(w[i]) // (ONE // 2) for i in (0, 1, 2, 3, 16, 17, 18)}
+    assert got == {0: 15, 1: -16, 2: 0, 3: -16, 16: 15, 17: -16, 18: -15}
+    assert bf.q5_0_codes(bytes(b5))[:4] == [15, -16, 0, -16]
+    # engine/tests.rs:60-72: d = 1.0, qh[2] = 1, qs[0] = 0x21 -> w[0] = -15, w[1] = -16,
+    # w[16] = (2 | 16) - 16 = 2, w[17] = -16
+    b5 = np.zeros(22, np.uint8)
+    b5[0:2] = [0x00, 0x3C]
+    b5[4], b5[6] = 0x01, 0x21
+    st, w = oracle.dequant_row(6, b5, 32)
+    assert st == 0 and len(w) == 32
+    assert (w[0], w[1], w[16], w[17]) == (-15 * ONE, -16 * ONE, 2 * ONE, -16 * ONE)
 
 
 def test_matvec_fixed_reference_kats():
@@ -182,7 +201,7 @@ def test_matvec_fixed_reference_kats():
 SHAPES = [(4, 32), (3, 48), (2, 33), (2, 300), (1, 64), (5, 0), (1, 256), (2, 512), (2, 256)]
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 12, 14])
 def test_matvec_random_payloads_vs_bruteforce(t):
     # chart/tests.rs:222-267 shapes, random block bytes with d = dmin = 0x3800.
     rng = np.random.default_rng(0x12345678 + t)
@@ -212,7 +231,7 @@ def test_matvec_random_payloads_vs_bruteforce(t):
             assert xs.tolist() == [int(codes[b:b + 32].astype(np.int64).sum()) for b in range(0, n_in, 32)]
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 12, 14])
 def test_extreme_scales_and_codes(t):
     # chart/tests.rs:269-307: largest finite scale 0x7BFF, codes +-127 at unit scale.
     rng = np.random.default_rng(0x51FF0000 + t)
@@ -285,7 +304,8 @@ def test_zero_activation_blocks():
 def test_matmat_fast_equals_per_column_contract():
     # kern/matmat.rs:973-1149 shape: every column equals the per-column contract.
     rng = np.random.default_rng(21)
-    for t, n_out, n_in in [(8, 17, 64), (12, 9, 512), (14, 7, 256), (12, 5, 896), (8, 3, 96)]:
+    for t, n_out, n_in in [(8, 17, 64), (12, 9, 512), (14, 7, 256), (12, 5, 896), (8, 3, 96), (6, 11, 96),
+                           (6, 4, 896)]:
         raw = synth.payload(t, rng, n_out, n_in)
         x = synth.activations(rng, n_in, 9)
         st, codes, scales = oracle.quant_act_f32_batch(x)
@@ -294,6 +314,24 @@ def test_matmat_fast_equals_per_column_contract():
         assert st == 0
         for c in range(9):
             assert y[c].tolist() == oracle.matvec_q8act(t, raw, n_out, n_in, codes[c], scales[c])[1].tolist()
+
+
+def test_q5_0_every_code_and_bit_position():
+    # Each of the 32 outputs takes its nibble and its qh bit from the position the layout fixes:
+    # a block whose only nonzero field is one nibble or one qh bit changes exactly one output.
+    for e in range(32):
+        for field in ("nib", "bit"):
+            b5 = np.zeros(22, np.uint8)
+            b5[0:2] = [0x00, 0x3C]  # d = 1
+            if field == "nib":
+                b5[6 + e % 16] = 0x0F if e < 16 else 0xF0
+            else:
+                b5[2 + e // 8] = 1 << (e % 8)
+            w = oracle.dequant_row(6, b5, 32)[1] // ONE
+            want = [-16] * 32
+            want[e] = -1 if field == "nib" else 0
+            assert w.tolist() == want, (e, field)
+            assert bf.q5_0_codes(bytes(b5)) == want
 
 
 def test_synth_generators_roundtrip():

@@ -27,6 +27,23 @@ FLAGS = [
 ]
 
 
+DRIVER_SRC = os.path.join(ROOT, "tests", "cpp", "abi_driver.cpp")
+DRIVER = os.path.join(ROOT, "tests", "cpp", "abi_driver")
+
+
+def build_driver(out: str = DRIVER, verbose: bool = False) -> str:
+    """The C++ ABI driver (tests/cpp/abi_driver.cpp): plain g++, dlopen at run time, no HIP."""
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"),
+           DRIVER_SRC, "-ldl", "-o", out + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed ({r.returncode}):\n{r.stdout}{r.stderr}")
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build(verbose: bool = False) -> str:
     srcs = []
     for s in SOURCES:
@@ -43,6 +60,7 @@ def build(verbose: bool = False) -> str:
     if verbose and out.strip():
         print(out)
     os.replace(tmp, LIB)
+    build_driver(verbose=verbose)
     return LIB
 
 

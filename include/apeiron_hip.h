@@ -1,6 +1,6 @@
 /*
  * apeiron_hip.h -- C ABI of the MI355X (gfx950) backend for apeiron's quantized
- * linear-layer path: GGUF block-quantized weights (Q8_0, Q4_K, Q6_K) times the
+ * linear-layer path: GGUF block-quantized weights (Q8_0, Q5_0, Q4_K, Q6_K) times the
  * power-of-two int8 activation quantizer, as a GEMV at decode (N = 1) and a GEMM at
  * prefill (N > 1).
  *

@@ -66,7 +66,7 @@ def small_payload(t, rng, n_out, n_in, scale):
     raw = synth.payload(t, rng, n_out, n_in).copy()
     qk, bb = synth.GEOM[t]
     blk = raw.reshape(-1, bb)
-    for off in ((0,) if t == Q8_0 else (0, 2) if t == Q4_K else (208,)):
+    for off in ((0,) if t in (Q8_0, Q5_0) else (0, 2) if t == Q4_K else (208,)):
         d = blk[:, off:off + 2].copy().view(np.float16).astype(np.float32) * scale
         blk[:, off:off + 2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
     return raw

@@ -3,7 +3,9 @@
  *
  * TEST/BENCH INFRASTRUCTURE ONLY (the CPU baseline leg of bench.py and its tests).
  *
- * Restates the chart row kernels of the reference: each 32-lane group yields an exact i32
+ * Restates the chart row kernels of the reference, one row at a time (the reference's two-row
+ * tiling, x86.rs:782-1192, and AVX-VNNI cores, x86.rs:74-85, are not restated: this is a lower
+ * bound on its rate): each 32-lane group yields an exact i32
  * dot (AVX2 maddubs/madd, chart/x86.rs:175-449) and one i128 fold
  * acc += S_b * (w_scale*dot - w_min*xsum) (RowAcc::emit, chart/mod.rs:501-514); the row ends
  * with round_shift_32 and the i64 range check (chart/mod.rs:1739-1753).  Rows are split into

@@ -90,6 +90,7 @@ int aho_matvec_q8act(uint32_t ggml_type, const uint8_t *raw, size_t raw_len, siz
 
 /* Exact per-group integer dots of one row against quantized activation codes.
  *   Q8_0: dots[b] = sum_{l<32} q*xq over 32-block b                (ceil(K/32) entries)
+ *   Q5_0: dots[b] = sum_{l<32} (q-16)*xq over 32-block b           (ceil(K/32) entries)
  *   Q4_K: dots[j] = sum nibble*xq over 32-sub-block j              (ceil(K/32) entries)
  *   Q6_K: dots[g] = sum (u-32)*xq over 16-group g                  (ceil(K/16) entries)
  * xsums[b] = sum xq over 32-block b (ceil(K/32) entries).  Lanes >= K contribute nothing.
@@ -103,9 +104,11 @@ int aho_row_absdot(uint32_t ggml_type, const uint8_t *raw, size_t raw_len, size_
                    size_t n_in, const int8_t *codes, const int64_t *scales, double *out);
 
 /* The reference's fast CPU path restated for host timing: chart row kernels (block dot +
- * i128 fold, chart/mod.rs:501-514, x86.rs cores) with two-row tiling (x86.rs:782-1192) over
- * contiguous row chunks on a thread pool (chart/ffn.rs:667-727).  Bit-equal to
- * aho_matvec_q8act; falls back to it when the fast bound (chart/mod.rs:336-383) fails. */
+ * i128 fold, chart/mod.rs:501-514, x86.rs cores) one row at a time over contiguous row chunks on
+ * a thread pool (chart/ffn.rs:667-727), with AVX2 maddubs dots.  Not restated: the reference's
+ * two-row tiling (x86.rs:782-1192) and its AVX-VNNI dispatch (x86.rs:74-85), so this baseline is
+ * a lower bound on the reference's own CPU rate.  Bit-equal to aho_matvec_q8act; falls back to
+ * it when the fast bound (chart/mod.rs:336-383) fails. */
 int aho_matvec_q8act_fast(uint32_t ggml_type, const uint8_t *raw, size_t raw_len, size_t n_out,
                           size_t n_in, const int8_t *codes, const int64_t *scales, int64_t *y,
                           int n_threads);

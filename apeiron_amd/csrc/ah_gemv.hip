@@ -170,8 +170,10 @@ AH_DEV QuadIn quad_load_row(const ActRsrc &r, uint32_t src, uint32_t n_in, uint3
     return in;
 }
 
+// fast: the f32 source may take the f32-arithmetic code path (below); false keeps the integer form
+// (a kernel whose register budget the float path's extra temporaries would overflow).
 AH_DEV QuadOut quad_quant(const QuadIn &in, uint32_t src, uint32_t b, unsigned long long *status,
-                          unsigned long long key_base) {
+                          unsigned long long key_base, bool fast = true) {
     const uint32_t q = threadIdx.x & 3;
     const uint32_t k0 = b * 32 + 8 * q;
     const uint32_t take = in.take;
@@ -255,7 +257,39 @@ AH_DEV QuadOut quad_quant(const QuadIn &in, uint32_t src, uint32_t b, unsigned l
     if (!refused) {
         e = ah_act_scale_exp(maxm);
         bad = e == 63;
-        if (e >= 0 && e < 63) {
+        if (fast && src == AH_SRC_F32 && e >= 0 && e < 56) {
+            // The f32 path in f32 arithmetic, ~5 VALU an element instead of ~25 for the 32-bit
+            // integer form (ah_act_code_f32), with the same codes.  v = |x| * 2^(32 - e) is exact
+            // (a power-of-two scaling, v <= 127.5, no underflow for e <= 55), and for an exact
+            // v >= 0, floor(fl(v + 1/2)) = floor(v + 1/2): a rounding of v + 1/2 never crosses an
+            // integer.  For |x| >= 2^-9 to_q32 is exact, so that is the code's one rounding.  Below
+            // 2^-9 to_q32 rounds first: q = floor(fl(|x| * 2^32 + 1/2)) (exact, q < 2^23), then the
+            // code rounds q * 2^-e the same way; waves with such an element take a second pass.
+            // e <= 55 also means no code * 2^e can leave int64 (127 * 2^55 < 2^62).  Element by
+            // element, so the path holds no more registers than the integer form.
+            const float sc = __builtin_ldexpf(1.0f, 32 - e), se = __builtin_ldexpf(1.0f, -e);
+            bool tiny = false;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t a = bits[i] & 0x7fffffffu;
+                tiny |= a != 0u && a < (118u << 23);
+            }
+            const bool twice = __builtin_amdgcn_ballot_w64(tiny) != 0ull;  // uniform
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t a = bits[i] & 0x7fffffffu;
+                const float f = __builtin_bit_cast(float, a);
+                uint32_t cm = (uint32_t)__builtin_fmaf(f, sc, 0.5f);
+                if (twice && a < (118u << 23))
+                    cm = (uint32_t)__builtin_fmaf(__builtin_floorf(__builtin_fmaf(f, 0x1p32f, 0.5f)), se, 0.5f);
+                const int c = (bits[i] >> 31) ? -(int)cm : (int)cm;
+                if (i < 4)
+                    o.c0 |= (uint32_t)(c & 0xff) << (8 * i);
+                else
+                    o.c1 |= (uint32_t)(c & 0xff) << (8 * (i - 4));
+                s8 += c;
+            }
+        } else if (e >= 0 && e < 63) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 int c;
@@ -947,6 +981,9 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
         r_begin = (uint32_t)((uint64_t)P.n_out * wl / n_waves);
         r_end = (uint32_t)((uint64_t)P.n_out * (wl + 1) / n_waves);
     }
+    // GEMV parts take f32 or code inputs (the Q32.32 form is the quantizer's alone): telling the
+    // compiler drops that form's 16-word inputs from the prologue's registers
+    __builtin_assume(P.src != AH_SRC_Q32);
     const uint32_t kpad = (P.n_in + 255) / 256 * 256;
     const ActLds A = carve(smem + aoff, kpad);
     uint8_t *tl = smem + act_bytes + wave * kSlotBytes;
@@ -983,13 +1020,16 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
         const uint32_t n_act = D->n_act;
         for (uint32_t a = 0; a < n_act; ++a) {
             const GemvPart Pa = part_at(parts, D->act_part[a]);
+            __builtin_assume(Pa.src != AH_SRC_Q32);
             const uint32_t nbpa = (Pa.n_in + 255) / 256 * 8;
             const ActLds Aa = carve(smem + D->act_off[a], nbpa * 32);
             const ActRsrc xra = act_rsrc(Pa.x, Pa.scales, Pa.src, Pa.n_in);
             for (uint32_t base = 0; base < nbpa; base += QB) {
                 if (base + wave * 16 >= nbpa) break;  // this wave's 16 blocks lie past the activation
                 const uint32_t b = base + threadIdx.x / 4;
-                const QuadOut o = quad_quant(quad_load_row(xra, Pa.src, Pa.n_in, b), Pa.src, b, status, 0);
+                // (the Q6_K plan kernel sits at its register budget: the integer code form there)
+                const QuadOut o = quad_quant(quad_load_row(xra, Pa.src, Pa.n_in, b), Pa.src, b, status, 0,
+                                             TYPE != AH_GGML_Q6_K);
                 if (b < nbpa) store_quad(Aa, b, o);
             }
         }
@@ -1001,17 +1041,25 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
         const QuadIn x1 = quad_load_row(xr, P.src, P.n_in, QB + threadIdx.x / 4);  // past the row: zeros
         ah_lds_barrier();
         load_tile(0);
-        // a wave whose 16 blocks all lie past the activation has nothing to quantize
-#pragma unroll
-        for (uint32_t p = 0; p < 2; ++p) {
-            const uint32_t b = p * QB + threadIdx.x / 4;
-            if (p < passes && p * QB + wave * 16 < nbp) {
-                const QuadOut o = quad_quant(p ? x1 : x0, P.src, b, status, 0);
-                if (b < nbp) store_quad(A, b, o);
-            }
+        // Pass p quantizes blocks p*QB + tid/4.  A wave whose 16 blocks of a pass all lie past the
+        // activation has nothing to quantize in it (nor in any later pass).  The third pass's
+        // input (K > 8192) is requested once pass 0 has consumed x0, so its load overlaps pass 1.
+        const uint32_t b0 = threadIdx.x / 4;
+        const bool w0 = wave * 16 < nbp;
+        QuadOut o0 = {};
+        if (w0) o0 = quad_quant(x0, P.src, b0, status, 0);
+        const QuadIn x2 = quad_load_row(xr, P.src, P.n_in, 2 * QB + b0);  // past the row: zeros
+        if (w0 && b0 < nbp) store_quad(A, b0, o0);
+        if (passes > 1 && QB + wave * 16 < nbp) {
+            const QuadOut o = quad_quant(x1, P.src, QB + b0, status, 0);
+            if (QB + b0 < nbp) store_quad(A, QB + b0, o);
         }
-        for (uint32_t p = 2; p < passes; ++p) {  // activations past 2 * 128 blocks (K > 8192)
-            const uint32_t b = p * QB + threadIdx.x / 4;
+        if (passes > 2 && 2 * QB + wave * 16 < nbp) {
+            const QuadOut o = quad_quant(x2, P.src, 2 * QB + b0, status, 0);
+            if (2 * QB + b0 < nbp) store_quad(A, 2 * QB + b0, o);
+        }
+        for (uint32_t p = 3; p < passes; ++p) {  // activations past 3 * 128 blocks (K > 12288)
+            const uint32_t b = p * QB + b0;
             if (p * QB + wave * 16 >= nbp) break;
             const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, 0);
             if (b < nbp) store_quad(A, b, o);

@@ -103,3 +103,57 @@ def test_act_code_f32_32bit_matches_quant_act():
         assert act_code_f32_32bit(int(bits[i]), e) == int(codes[i]), (i, float(x[i]), e)
         n_checked += 1
     assert n_checked > 15000
+
+
+def act_code_f32_float(bits: int, e: int) -> int:
+    """The kernels' f32-arithmetic code (quad_quant's fast path, e <= 55), on numpy float32:
+    v = |x| * 2^(32-e) exact, code = trunc(fl(v + 0.5)); below 2^-9 to_q32's rounding first."""
+    a = bits & 0x7FFFFFFF
+    f = np.array([a], np.uint32).view(np.float32)[0]
+    if a != 0 and a < (118 << 23):
+        q = np.floor(np.float32(f * np.float32(2.0 ** 32)) + np.float32(0.5))
+        v = np.float32(q * np.float32(np.ldexp(1.0, -e)))
+    else:
+        v = np.float32(f * np.float32(np.ldexp(1.0, 32 - e)))
+    c = int(np.float32(v + np.float32(0.5)))
+    return -c if bits >> 31 else c
+
+
+def test_act_code_f32_float_path_matches_quant_act():
+    """The same sweep for the float form: every element of every block whose exponent admits it
+    (e <= 55) gets quant_act_f32's code."""
+    rng = np.random.default_rng(18)
+    blocks = []
+    for top in list(range(-60, 24)) + [-126, -149]:
+        amax = np.float32(np.ldexp(1.0 + rng.random(), top)) if top > -149 else np.float32(np.ldexp(1.0, -149))
+        for _ in range(6):
+            rel = rng.integers(-40, 1, size=31)
+            body = np.ldexp(rng.random(31) + 0.5, top + rel).astype(np.float32)
+            body *= np.where(rng.random(31) < 0.5, -1, 1).astype(np.float32)
+            body[0] = np.float32(np.ldexp(1.5, top - 6))
+            body[1] = np.float32(np.ldexp(0.5, -32))
+            body[2] = np.float32(-np.ldexp(1.5, -33))
+            body[3] = np.float32(0.0)
+            body[4] = np.float32(-0.0)
+            body[5] = np.float32(np.ldexp(1.0, -149))
+            # half-way points of the code rounding just below 2^-9 (two roundings) and above it
+            body[6] = np.float32(np.ldexp(1.0, -9) * (1 - 2 ** -24))
+            body[7] = np.float32(np.ldexp(1.0, -9))
+            blocks.append(np.concatenate([[amax], body]).astype(np.float32))
+    # N(0,1) activations, the common case
+    blocks.append(rng.standard_normal(32 * 400).astype(np.float32))
+    x = np.concatenate(blocks)
+    st, codes, scales = oracle.quant_act_f32(x)
+    assert st == 0
+    bits = x.view(np.uint32)
+    n_checked = 0
+    for i in range(x.shape[0]):
+        s = int(scales[i // 32])
+        if s == 0:
+            continue
+        e = s.bit_length() - 1
+        if e > 55:
+            continue
+        assert act_code_f32_float(int(bits[i]), e) == int(codes[i]), (i, float(x[i]), e)
+        n_checked += 1
+    assert n_checked > 25000

@@ -170,14 +170,76 @@ AH_DEV QuadIn quad_load_row(const ActRsrc &r, uint32_t src, uint32_t n_in, uint3
     return in;
 }
 
-// fast: the f32 source may take the f32-arithmetic code path (below); false keeps the integer form
-// (a kernel whose register budget the float path's extra temporaries would overflow).
+// The common case of an f32 block, straight-line in f32 arithmetic: every block of the wave has
+// its largest magnitude in [2^-9, 2^29) or is all zero (ballot-uniform; otherwise the whole wave
+// takes the general form below).  Then no element is non-finite or past to_q32's range, and with
+// the block's largest magnitude m * 2^(ee - 150) (m the 24-bit significand, ee in [118, 155]) its
+// Q32.32 magnitude is m * 2^k, k = ee - 118, of bit length 24 + k: ah_act_scale_exp gives
+// e = 17 + k + [m > 127 * 2^17], in [17, 55], so no code * 2^e leaves int64.
+// Codes: v = |x| * 2^(32 - e) is exact (a power-of-two scaling, v <= 127, no underflow), and for
+// |x| >= 2^-9 to_q32 is exact too, so the code is the one rounding floor(v + 1/2).  For v >= 1/2,
+// floor(fl(v + 1/2)) is that value: v + 1/2 is exact while it stays in v's binade, and past it
+// (in [2^j, 2^j + 1/2) for the next power 2^j) its rounding cannot reach the next integer.  Below
+// 1/2 the code is 0, but fl(v + 1/2) rounds v = 1/2 - 2^-25 up to 1 (a tie, to even), so elements
+// with |x| < 2^(e-33) (v < 1/2) are given 0 by a compare.  The sign rides on the addend:
+// trunc(fl(x * 2^(32-e) + copysign(1/2, x))) = sign(x) * floor(fl(v + 1/2)), round-to-nearest
+// being symmetric.  Below 2^-9, to_q32 rounds first: q = floor(fl(|x| * 2^32 + 1/2)), then the code
+// rounds q * 2^-e the same way (q * 2^-e is a multiple of 2^-e >= 2^-24, so that sum is exact
+// below 1; q itself is exact but at |x| * 2^32 = 1/2 - 2^-25, where it is 1 for 0, which no code
+// at e >= 2 sees).  Both roundings give 0 when e >= 25 (q <= 2^23 < 2^(e-1)), so the second form
+// runs only in waves with a block at e <= 24 (a largest magnitude below 1/2).
+AH_DEV bool quad_quant_f32(const QuadIn &in, QuadOut &o) {
+    uint32_t maxb = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) maxb = __builtin_elementwise_max(maxb, in.w[i] & 0x7fffffffu);
+    maxb = __builtin_elementwise_max(maxb, quad_xor1(maxb));
+    maxb = __builtin_elementwise_max(maxb, quad_xor2(maxb));
+    const bool common = maxb == 0u || maxb - 0x3B000000u < 0x4E000000u - 0x3B000000u;
+    if (__builtin_amdgcn_ballot_w64(!common) != 0ull) return false;
+    const int e = maxb == 0u ? -1 : (int)(maxb >> 23) - 101 + ((maxb & 0x7fffffu) > 0x7E0000u ? 1 : 0);
+    const float sc = __builtin_ldexpf(1.0f, 32 - e), half_unit = __builtin_ldexpf(1.0f, e - 33);
+    int c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t w = in.w[i];
+        const float x = __builtin_bit_cast(float, w);
+        const int r = (int)__builtin_fmaf(x, sc, __builtin_bit_cast(float, (w & 0x80000000u) | 0x3F000000u));
+        c[i] = __builtin_fabsf(x) >= half_unit ? r : 0;
+    }
+    if (__builtin_amdgcn_ballot_w64(e >= 0 && e <= 24) != 0ull) {
+        const float se = __builtin_ldexpf(1.0f, -e);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t a = in.w[i] & 0x7fffffffu;
+            const float qv = __builtin_floorf(__builtin_fmaf(__builtin_bit_cast(float, a), 0x1p32f, 0.5f));
+            const int cm = (int)__builtin_fmaf(qv, se, 0.5f);
+            if (a < 0x3B000000u) c[i] = (in.w[i] >> 31) ? -cm : cm;
+        }
+    }
+    // low bytes of the codes, four to a dword (v_perm: bytes 0-3 of the second operand, 4-7 of the first)
+    const uint32_t p01 = __builtin_amdgcn_perm((uint32_t)c[1], (uint32_t)c[0], 0x0c0c0400u);
+    const uint32_t p23 = __builtin_amdgcn_perm((uint32_t)c[3], (uint32_t)c[2], 0x0c0c0400u);
+    const uint32_t p45 = __builtin_amdgcn_perm((uint32_t)c[5], (uint32_t)c[4], 0x0c0c0400u);
+    const uint32_t p67 = __builtin_amdgcn_perm((uint32_t)c[7], (uint32_t)c[6], 0x0c0c0400u);
+    o.c0 = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+    o.c1 = __builtin_amdgcn_perm(p67, p45, 0x05040100u);
+    const int s8 = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+    o.s16 = s8 + (int)quad_xor1((uint32_t)s8);
+    o.s32 = o.s16 + (int)quad_xor2((uint32_t)o.s16);
+    o.e = e;
+    o.fsc = e < 0 ? 0.0f : __builtin_ldexpf(1.0f, e - 32);
+    return true;
+}
+
+// fast: an f32 source tries quad_quant_f32 first; false keeps the general form only (a kernel
+// whose register budget the fast form's temporaries would overflow).
 AH_DEV QuadOut quad_quant(const QuadIn &in, uint32_t src, uint32_t b, unsigned long long *status,
                           unsigned long long key_base, bool fast = true) {
     const uint32_t q = threadIdx.x & 3;
     const uint32_t k0 = b * 32 + 8 * q;
     const uint32_t take = in.take;
     QuadOut o;
+    if (fast && src == AH_SRC_F32 && quad_quant_f32(in, o)) return o;
     if (src == AH_SRC_CODES) {
         // precomputed codes (bytes past n_in cleared): only the code sums are derived here
         o.c0 = in.w[0] & (take >= 4 ? 0xffffffffu : (1u << (8 * take)) - 1u);
@@ -257,39 +319,7 @@ AH_DEV QuadOut quad_quant(const QuadIn &in, uint32_t src, uint32_t b, unsigned l
     if (!refused) {
         e = ah_act_scale_exp(maxm);
         bad = e == 63;
-        if (fast && src == AH_SRC_F32 && e >= 0 && e < 56) {
-            // The f32 path in f32 arithmetic, ~5 VALU an element instead of ~25 for the 32-bit
-            // integer form (ah_act_code_f32), with the same codes.  v = |x| * 2^(32 - e) is exact
-            // (a power-of-two scaling, v <= 127.5, no underflow for e <= 55), and for an exact
-            // v >= 0, floor(fl(v + 1/2)) = floor(v + 1/2): a rounding of v + 1/2 never crosses an
-            // integer.  For |x| >= 2^-9 to_q32 is exact, so that is the code's one rounding.  Below
-            // 2^-9 to_q32 rounds first: q = floor(fl(|x| * 2^32 + 1/2)) (exact, q < 2^23), then the
-            // code rounds q * 2^-e the same way; waves with such an element take a second pass.
-            // e <= 55 also means no code * 2^e can leave int64 (127 * 2^55 < 2^62).  Element by
-            // element, so the path holds no more registers than the integer form.
-            const float sc = __builtin_ldexpf(1.0f, 32 - e), se = __builtin_ldexpf(1.0f, -e);
-            bool tiny = false;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t a = bits[i] & 0x7fffffffu;
-                tiny |= a != 0u && a < (118u << 23);
-            }
-            const bool twice = __builtin_amdgcn_ballot_w64(tiny) != 0ull;  // uniform
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t a = bits[i] & 0x7fffffffu;
-                const float f = __builtin_bit_cast(float, a);
-                uint32_t cm = (uint32_t)__builtin_fmaf(f, sc, 0.5f);
-                if (twice && a < (118u << 23))
-                    cm = (uint32_t)__builtin_fmaf(__builtin_floorf(__builtin_fmaf(f, 0x1p32f, 0.5f)), se, 0.5f);
-                const int c = (bits[i] >> 31) ? -(int)cm : (int)cm;
-                if (i < 4)
-                    o.c0 |= (uint32_t)(c & 0xff) << (8 * i);
-                else
-                    o.c1 |= (uint32_t)(c & 0xff) << (8 * (i - 4));
-                s8 += c;
-            }
-        } else if (e >= 0 && e < 63) {
+        if (e >= 0 && e < 63) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 int c;
@@ -331,17 +361,21 @@ AH_DEV QuadOut quant_quad(const void *x, uint32_t src, uint32_t n_in, size_t row
 }
 
 // Store one quad's block to the LDS activation.
-AH_DEV void store_quad(const ActLds &A, uint32_t b, const QuadOut &o) {
+// One per-block word per lane: lane 0 the scale, lane 2 the block sum, lanes 1 / 3 their own
+// 16-group sums (elements 0..15 / 16..31).  The words arrive as values (not through the QuadOut)
+// so that the per-lane choice is a register select rather than a load from a chosen field.
+AH_DEV void store_quad_words(const ActLds &A, uint32_t b, uint32_t c0, uint32_t c1, uint32_t fsc, uint32_t s32,
+                             uint32_t s16) {
     const uint32_t q = threadIdx.x & 3;
     u32x2 *dst = reinterpret_cast<u32x2 *>(A.codes + pad_k(32 * b + 8 * q));
-    *dst = (u32x2){o.c0, o.c1};
-    if (q == 0) {
-        A.fsc[b] = o.fsc;
-        A.xs32[b] = o.s32;
-        A.xs16[2 * b] = o.s16;
-    } else if (q == 2) {
-        A.xs16[2 * b + 1] = o.s16;
-    }
+    *dst = (u32x2){c0, c1};
+    uint32_t *const p = q == 0 ? reinterpret_cast<uint32_t *>(A.fsc) + b
+                      : q == 2 ? reinterpret_cast<uint32_t *>(A.xs32) + b
+                               : reinterpret_cast<uint32_t *>(A.xs16) + 2 * b + (q >> 1);
+    *p = q == 0 ? fsc : q == 2 ? s32 : s16;
+}
+AH_DEV void store_quad(const ActLds &A, uint32_t b, const QuadOut &o) {
+    store_quad_words(A, b, o.c0, o.c1, __builtin_bit_cast(uint32_t, o.fsc), (uint32_t)o.s32, (uint32_t)o.s16);
 }
 
 // Fill the LDS activation of part P: blocks past n_in (up to kpad) are zero, so ragged rows need
@@ -1058,10 +1092,13 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
             const QuadOut o = quad_quant(x2, P.src, 2 * QB + b0, status, 0);
             if (2 * QB + b0 < nbp) store_quad(A, 2 * QB + b0, o);
         }
-        for (uint32_t p = 3; p < passes; ++p) {  // activations past 3 * 128 blocks (K > 12288)
+        // activations past 3 * 128 blocks (K > 12288); Q6_K keeps the general form here, as the
+        // fast one's temporaries in this loop push its tile loop's allocation into spills
+        for (uint32_t p = 3; p < passes; ++p) {
             const uint32_t b = p * QB + b0;
             if (p * QB + wave * 16 >= nbp) break;
-            const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, 0);
+            const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, 0,
+                                         TYPE != AH_GGML_Q6_K);
             if (b < nbp) store_quad(A, b, o);
         }
     }

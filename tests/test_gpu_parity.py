@@ -14,6 +14,7 @@ import pytest
 
 import oracle
 from apeiron_amd import chart, synth
+from quant_edges import edge_blocks_f32
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -101,6 +102,49 @@ def test_quant_act_f32_bit_exact(dev):
             ost, oc, os_ = oracle.quant_act_f32(x[r])
             assert ost == 0
             assert (c[r] == oc).all() and (s[r] == os_).all(), (n_tok, n_in, r)
+
+
+@pytest.mark.parametrize("t", [6, 8, 12, 14])
+def test_f32_quantizer_rounding_edges(dev, t):
+    """Activations built on the quantizer's rounding edges (tests/quant_edges.py: the element just
+    below half a code unit, second roundings below 2^-9, the exponent's mantissa boundary, blocks
+    outside the f32 fast form in the same waves as blocks inside it), over more than three passes
+    of the streaming kernels' 128-block prologue: the device quantizer equals quant_act_f32, and
+    the fused-quantizer GEMV equals the codes-input GEMV on the oracle's codes."""
+    x = edge_blocks_f32(np.random.default_rng(31), normal_blocks=120)
+    n_in = x.shape[0]
+    assert n_in > 3 * 128 * 32
+    ost, oc, os_ = oracle.quant_act_f32(x)
+    assert ost == 0
+    st, c, s = quant_f32_gpu(dev, x[None, :])
+    assert st == 0
+    assert (c[0] == oc).all() and (s[0] == os_).all()
+    # The raw activation's largest blocks (up to 2^31) can overflow a row's output, which both
+    # paths must refuse alike; a copy with every block above 2^8 scaled down by a power of two
+    # (each block's rounding edges are relative to its own exponent, so they stay) must project.
+    xb = x.reshape(-1, 32)
+    amax = np.abs(xb).max(axis=1)
+    shift = np.where(amax > 256.0, np.ceil(np.log2(np.maximum(amax, 1.0))) - 8, 0.0)
+    tame = (xb * np.ldexp(1.0, -shift.astype(np.int64))[:, None]).astype(np.float32).reshape(-1)
+    rng = synth.rng_for(7, t)
+    for n_out in (64, 1536):
+        w = dev.upload(t, synth.payload(t, rng, n_out, n_in), n_out, n_in)
+        for name, xa in (("raw", x), ("tame", tame)):
+            qst, qc, qs = oracle.quant_act_f32(xa)
+            assert qst == 0
+            # (device inputs held in names: a temporary's memory could be reused before the launch)
+            dc, ds, dx = to_dev(qc), to_dev(qs), to_dev(xa)
+            y = torch.empty(n_out, dtype=torch.float32, device="cuda")
+            w.gemv_q8_dev(ptr(dc), ptr(ds), ptr(y), stream())
+            st_codes = dev.sync_status(stream())
+            yf = torch.empty(n_out, dtype=torch.float32, device="cuda")
+            w.gemv_f32_dev(ptr(dx), ptr(yf), stream())
+            st_f32 = dev.sync_status(stream())
+            assert st_f32 == st_codes, (t, n_out, name)
+            assert st_codes in ((0, 9) if name == "raw" else (0,)), (t, n_out, name, st_codes)
+            if st_codes == 0:
+                assert (yf.cpu().numpy() == y.cpu().numpy()).all(), (t, n_out, name)
+        w.free()
 
 
 def test_quant_act_f32_refusals(dev):

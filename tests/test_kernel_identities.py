@@ -4,11 +4,16 @@
   (kern/pow2.rs:11-39) -- the kernels avoid a 64-bit division by 127;
 * the GEMM's exact f16 operands: every int8 code, Q4_K sc*q (<= 945) and Q6_K u-32 is an
   integer f16 represents exactly, and the split X = 64*floor(X/64) + (X mod 64) of a 32-code sum
-  is exact in two f16 pieces.
+  is exact in two f16 pieces;
+* the f32 quantizer's two forms, the 32-bit integer one (ah_act_code_f32) and the f32-arithmetic
+  one (quad_quant_f32: exponent from the largest magnitude's bits, codes by one fma rounding,
+  cleared below half a code unit, a second rounding below 2^-9 at exponents <= 24), against
+  quant_act_f32, with a brute force over every f32 of the fma's sum.
 """
 import numpy as np
 
 import oracle
+from quant_edges import edge_blocks_f32
 
 
 def act_scale_exp_by_bitlength(a: int) -> int:
@@ -105,55 +110,73 @@ def test_act_code_f32_32bit_matches_quant_act():
     assert n_checked > 15000
 
 
-def act_code_f32_float(bits: int, e: int) -> int:
-    """The kernels' f32-arithmetic code (quad_quant's fast path, e <= 55), on numpy float32:
-    v = |x| * 2^(32-e) exact, code = trunc(fl(v + 0.5)); below 2^-9 to_q32's rounding first."""
-    a = bits & 0x7FFFFFFF
-    f = np.array([a], np.uint32).view(np.float32)[0]
-    if a != 0 and a < (118 << 23):
-        q = np.floor(np.float32(f * np.float32(2.0 ** 32)) + np.float32(0.5))
-        v = np.float32(q * np.float32(np.ldexp(1.0, -e)))
-    else:
-        v = np.float32(f * np.float32(np.ldexp(1.0, 32 - e)))
-    c = int(np.float32(v + np.float32(0.5)))
-    return -c if bits >> 31 else c
+def test_code_rounding_by_float_sum_brute_force():
+    """Every f32 v in [2^-26, 128): trunc(fl(v + 1/2)) = floor(v + 1/2) (exact in f64) for
+    v >= 1/2, and below 1/2 the one exception is v = 1/2 - 2^-25 (rounded up to 1, a tie to
+    even), which quad_quant_f32 clears with its |x| >= 2^(e-33) compare."""
+    bad = []
+    for binade in range(-26, 7):
+        m = np.arange(1 << 23, dtype=np.uint32)
+        v = ((np.uint32(binade + 127) << np.uint32(23)) | m).view(np.float32)
+        got = np.trunc(v + np.float32(0.5))
+        want = np.floor(v.astype(np.float64) + 0.5)
+        bad.extend(float(t) for t in v[got != want])
+    assert bad == [0.5 - 2.0 ** -25]
 
 
-def test_act_code_f32_float_path_matches_quant_act():
-    """The same sweep for the float form: every element of every block whose exponent admits it
-    (e <= 55) gets quant_act_f32's code."""
-    rng = np.random.default_rng(18)
-    blocks = []
-    for top in list(range(-60, 24)) + [-126, -149]:
-        amax = np.float32(np.ldexp(1.0 + rng.random(), top)) if top > -149 else np.float32(np.ldexp(1.0, -149))
-        for _ in range(6):
-            rel = rng.integers(-40, 1, size=31)
-            body = np.ldexp(rng.random(31) + 0.5, top + rel).astype(np.float32)
-            body *= np.where(rng.random(31) < 0.5, -1, 1).astype(np.float32)
-            body[0] = np.float32(np.ldexp(1.5, top - 6))
-            body[1] = np.float32(np.ldexp(0.5, -32))
-            body[2] = np.float32(-np.ldexp(1.5, -33))
-            body[3] = np.float32(0.0)
-            body[4] = np.float32(-0.0)
-            body[5] = np.float32(np.ldexp(1.0, -149))
-            # half-way points of the code rounding just below 2^-9 (two roundings) and above it
-            body[6] = np.float32(np.ldexp(1.0, -9) * (1 - 2 ** -24))
-            body[7] = np.float32(np.ldexp(1.0, -9))
-            blocks.append(np.concatenate([[amax], body]).astype(np.float32))
-    # N(0,1) activations, the common case
-    blocks.append(rng.standard_normal(32 * 400).astype(np.float32))
-    x = np.concatenate(blocks)
+def quad_quant_f32_block(bits: np.ndarray, second: bool = True, clear: bool = True):
+    """quad_quant_f32 on one 32-block of f32 bit patterns, restated on numpy float32: None outside
+    its common case (a largest magnitude outside [2^-9, 2^29) and nonzero), else (e, codes).
+    The exponent comes from the largest magnitude's bits, e = ee - 101 + [m > 0xFE0000]; each code
+    is trunc(fl(x * 2^(32-e) + copysign(1/2, x))) (x * 2^(32-e) is exact, so the numpy product and
+    sum are the kernel's one fma rounding), 0 where |x| < 2^(e-33) (with `clear`); with `second`,
+    elements below 2^-9 take to_q32's rounding first, q = floor(fl(|x| * 2^32 + 1/2)), then code = trunc(fl(q * 2^-e + 1/2))."""
+    bits = np.asarray(bits, np.uint32)
+    a = bits & np.uint32(0x7FFFFFFF)
+    maxb = int(a.max())
+    if not (maxb == 0 or 0x3B000000 <= maxb < 0x4E000000):
+        return None
+    e = -1 if maxb == 0 else (maxb >> 23) - 101 + (1 if (maxb & 0x7FFFFF) > 0x7E0000 else 0)
+    x = bits.view(np.float32)
+    half = ((bits & np.uint32(0x80000000)) | np.uint32(0x3F000000)).view(np.float32)
+    codes = np.trunc(x * np.float32(np.ldexp(1.0, 32 - e)) + half).astype(np.int64)
+    if clear:
+        codes = np.where(np.abs(x) >= np.float32(np.ldexp(1.0, e - 33)), codes, 0)
+    if second:
+        fa = a.view(np.float32)
+        q = np.floor(fa * np.float32(2.0 ** 32) + np.float32(0.5))
+        cm = np.trunc(q * np.float32(np.ldexp(1.0, -e)) + np.float32(0.5)).astype(np.int64)
+        tiny = a < np.uint32(0x3B000000)
+        codes = np.where(tiny, np.where(bits >> 31 != 0, -cm, cm), codes)
+    return e, codes
+
+
+def test_act_code_f32_fast_block_matches_quant_act():
+    """Every block of a sweep that quad_quant_f32 accepts gets quant_act_f32's exponent and codes;
+    at e >= 25 the second rounding is not needed (the kernel runs it only in waves holding a block
+    at e <= 24) and is harmless where it runs; at e = 24 it is needed."""
+    x = edge_blocks_f32(np.random.default_rng(18))
     st, codes, scales = oracle.quant_act_f32(x)
     assert st == 0
     bits = x.view(np.uint32)
-    n_checked = 0
-    for i in range(x.shape[0]):
-        s = int(scales[i // 32])
-        if s == 0:
+    n_blocks = n_second = n_clear = 0
+    for bi in range(x.shape[0] // 32):
+        got = quad_quant_f32_block(bits[32 * bi:32 * bi + 32])
+        if got is None:
             continue
-        e = s.bit_length() - 1
-        if e > 55:
-            continue
-        assert act_code_f32_float(int(bits[i]), e) == int(codes[i]), (i, float(x[i]), e)
-        n_checked += 1
-    assert n_checked > 25000
+        s = int(scales[bi])
+        want_e = -1 if s == 0 else s.bit_length() - 1
+        want = codes[32 * bi:32 * bi + 32].astype(np.int64)
+        assert got[0] == want_e, (bi, got[0], want_e)
+        assert (got[1] == want).all(), (bi, want_e)
+        if (quad_quant_f32_block(bits[32 * bi:32 * bi + 32], clear=False)[1] != want).any():
+            n_clear += 1
+        one = quad_quant_f32_block(bits[32 * bi:32 * bi + 32], second=False)[1]
+        if want_e >= 25:
+            assert (one == want).all(), (bi, want_e)
+        elif (one != want).any():
+            n_second += 1
+        n_blocks += 1
+    assert n_blocks > 500
+    assert n_second > 0  # the second rounding decides some code at e <= 24
+    assert n_clear >= 4  # and the clear below half a unit some code at each sampled e

@@ -936,18 +936,21 @@ __global__ void scan_scales_kernel(const uint8_t *w, uint64_t n_blocks, uint32_t
 // A row is owned by G = P.lanes consecutive lanes, lane g taking units g, g+G, ...; the G partial
 // sums meet through DPP row operations (and, for G > 16, lane shuffles) in a fixed order.
 
-template <int CTRL>
+template <int CTRL, int ROWS = 0xF>
 AH_DEV float dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
 }
-// Sum over aligned groups of G lanes (G a power of two <= 64); every lane gets its group's sum.
+// Sum over aligned groups of G lanes (G a power of two <= 64), in the group's last lane
+// (g = G - 1).  Up to 16 lanes the butterflies stay within a DPP row and every lane gets the sum;
+// for 32 and 64 the rows' sums are folded upward by row broadcasts (VALU, no LDS permute): lane 15
+// of rows 0 / 2 into rows 1 / 3, then lane 31 into rows 2 and 3 (rows outside the mask keep theirs).
 AH_DEV float group_sum(float s, uint32_t G) {
-    if (G >= 2) s += dpp<0xB1>(s);   // quad_perm [1,0,3,2]: lane ^ 1
-    if (G >= 4) s += dpp<0x4E>(s);   // quad_perm [2,3,0,1]: lane ^ 2
-    if (G >= 8) s += dpp<0x141>(s);  // row_half_mirror: the other quad of the half-row
-    if (G >= 16) s += dpp<0x140>(s); // row_mirror: the other half of the row
-    if (G >= 32) s += __shfl_xor(s, 16, 64);
-    if (G >= 64) s += __shfl_xor(s, 32, 64);
+    if (G >= 2) s += dpp<0xB1>(s);        // quad_perm [1,0,3,2]: lane ^ 1
+    if (G >= 4) s += dpp<0x4E>(s);        // quad_perm [2,3,0,1]: lane ^ 2
+    if (G >= 8) s += dpp<0x141>(s);       // row_half_mirror: the other quad of the half-row
+    if (G >= 16) s += dpp<0x140>(s);      // row_mirror: the other half of the row
+    if (G >= 32) s += dpp<0x142, 0xA>(s); // row_bcast:15 into rows 1 and 3
+    if (G >= 64) s += dpp<0x143, 0xC>(s); // row_bcast:31 into rows 2 and 3
     return s;
 }
 
@@ -1153,15 +1156,15 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
         }
         acc = group_sum(acc, G);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), ry,
-                                              (g == 0 && owns) ? row * 4u : kOob, 0, 0);
+                                              (g == G - 1 && owns) ? row * 4u : kOob, 0, 0);
         const uint32_t oc = ah_out_code(acc);
-        const uint64_t ob = __builtin_amdgcn_ballot_w64(g == 0 && owns && oc != 0u);
+        const uint64_t ob = __builtin_amdgcn_ballot_w64(g == G - 1 && owns && oc != 0u);
         if (ob) {  // uniform: lanes own rows in lane order, so the lowest lane is the earliest row
             const uint32_t k = __builtin_amdgcn_readlane((row << 1) | (oc == 9u ? 1u : 0u), (int)__builtin_ctzll(ob));
             obad = k < obad ? k : obad;
         }
         __builtin_amdgcn_wave_barrier();  // all lanes are done reading the slot before it is refilled
-        stage(t + 1);
+        if (t + 1 < n_t) stage(t + 1);    // (past the last tile nothing is staged: no wait for its loads)
     }
     if (obad != 0xFFFFFFFFu && lane == 0) ah_record(status, ah_out_key(obad >> 1, (obad & 1u) ? 9u : 8u));
 }
@@ -1467,15 +1470,15 @@ AH_DEV void seq_gemv_stage(const SeqArgs &a, uint32_t s, uint32_t r, bool &broke
         }
         acc = group_sum(acc, G);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), ry,
-                                              (g == 0 && owns) ? row * 4u : kOob, 0, kCoherent);
+                                              (g == G - 1 && owns) ? row * 4u : kOob, 0, kCoherent);
         const uint32_t oc = ah_out_code(acc);
-        const uint64_t ob = __builtin_amdgcn_ballot_w64(g == 0 && owns && oc != 0u);
+        const uint64_t ob = __builtin_amdgcn_ballot_w64(g == G - 1 && owns && oc != 0u);
         if (ob) {
             const uint32_t k = __builtin_amdgcn_readlane((row << 1) | (oc == 9u ? 1u : 0u), (int)__builtin_ctzll(ob));
             obad = k < obad ? k : obad;
         }
         __builtin_amdgcn_wave_barrier();
-        stage(t + 1);
+        if (t + 1 < n_t) stage(t + 1);
     }
     if (obad != 0xFFFFFFFFu && lane == 0) ah_record(st, ah_out_key(obad >> 1, (obad & 1u) ? 9u : 8u));
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's outputs are complete

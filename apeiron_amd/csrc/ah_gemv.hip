@@ -1008,11 +1008,26 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
         r_end = idle ? r_begin : D->r_end[wv];
         aoff = D->act_off[D->wave_act[wv]];
     } else {
-        // the workgroup's part: uniform compares and selects (no run-time index into the arguments)
-        P = sp.p[0];
+        // The workgroup's part.  One round of argument loads brings the part count, the later
+        // parts' first workgroups and every word of part 0 (held in scalar registers by the empty
+        // asm statements, so the loads go out together); a workgroup of a later part then reads
+        // that part's words in a second round, at a uniform offset into the arguments.
+        auto pin = [](const GemvPart &q) {
+            uint32_t pw[sizeof(GemvPart) / 4];
+            __builtin_memcpy(pw, &q, sizeof(GemvPart));
 #pragma unroll
-        for (uint32_t i = 1; i < kStreamArgParts; ++i)
-            if (i < sp.n && blockIdx.x >= sp.p[i].wg_begin) P = sp.p[i];
+            for (uint32_t i = 0; i < sizeof(GemvPart) / 4; ++i) __asm__ volatile("" ::"s"(pw[i]));
+        };
+        P = sp.p[0];
+        const uint32_t np = sp.n, b1 = sp.p[1].wg_begin, b2 = sp.p[2].wg_begin, b3 = sp.p[3].wg_begin;
+        __asm__ volatile("" ::"s"(np), "s"(b1), "s"(b2), "s"(b3));
+        pin(P);
+        const uint32_t pi = (1u < np && blockIdx.x >= b1 ? 1u : 0u) + (2u < np && blockIdx.x >= b2 ? 1u : 0u) +
+                            (3u < np && blockIdx.x >= b3 ? 1u : 0u);
+        if (pi != 0) {
+            P = sp.p[__builtin_amdgcn_readfirstlane(pi)];
+            pin(P);
+        }
         const uint32_t n_waves = P.wg_count * kSWaves;
         const uint32_t wl = (blockIdx.x - P.wg_begin) * kSWaves + wave;
         r_begin = (uint32_t)((uint64_t)P.n_out * wl / n_waves);

@@ -20,7 +20,8 @@ hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart 
 uint32_t ah_gemv_nc(uint32_t row_bytes);
 uint32_t ah_gemv_rows_per_tile(uint32_t row_bytes, uint32_t units);
 hipError_t ah_gemv_init_attrs();
-bool ah_gemv_stream_geometry(uint32_t row_bytes, uint32_t units, uint32_t &rows, uint32_t &lanes);
+bool ah_gemv_stream_geometry(uint32_t type, uint32_t row_bytes, uint32_t units, uint32_t n_out, uint32_t &rows,
+                             uint32_t &lanes);
 size_t ah_gemv_stream_lds_bytes(uint32_t kpad_max);
 size_t ah_gemv_act_bytes(uint32_t kpad);
 size_t ah_gemv_stream_slot_bytes();
@@ -174,10 +175,19 @@ int32_t ensure_scratch(ah_ctx *ctx, size_t bytes) {
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Work units of a row: Q8_0 / Q5_0 blocks, Q4_K super-blocks, Q6_K half super-blocks (128 elements).
-uint32_t units_per_row(uint32_t t, uint32_t n_in) {
-    return ah_blk32((int)t) ? (n_in + 31) / 32 : t == AH_GGML_Q4_K ? (n_in + 255) / 256 : (n_in + 127) / 128;
+// Work units of a row: Q8_0 / Q5_0 blocks, Q4_K super-blocks (or, with `pairs`, sub-block pairs
+// of 64 elements), Q6_K half super-blocks (128 elements).
+uint32_t units_per_row(uint32_t t, uint32_t n_in, bool pairs = false) {
+    return ah_blk32((int)t)        ? (n_in + 31) / 32
+           : t == AH_GGML_Q4_K     ? (pairs ? (n_in + 63) / 64 : (n_in + 255) / 256)
+                                   : (n_in + 127) / 128;
 }
+// A streaming Q4_K part of a latency launch (a single projection, a plan of argument parts, a
+// decode sequence) whose super-block geometry leaves fewer tiles than this takes pair units: it
+// then has idle lanes and CUs to spread its super-blocks over.  A large part's waves are already
+// busy, and a table plan (many projections at once) is bound by throughput, where pairs would
+// only add their per-pair scale work: those keep super-block units.
+constexpr uint32_t kQ4kPairTiles = 512;
 
 uint32_t kpad_of(size_t n_in) { return (uint32_t)((n_in + 255) / 256 * 256); }
 
@@ -186,7 +196,7 @@ uint32_t kpad_of(size_t n_in) { return (uint32_t)((n_in + 255) / 256 * 256); }
 // a part's geometry; deal_wgs then sizes every part's workgroup count.
 
 GemvPart make_part(const ah_tensor *w, uint32_t src, const void *x, const int64_t *scales, float *y,
-                   int32_t *dots, bool &stream) {
+                   int32_t *dots, bool &stream, bool latency = true) {
     GemvPart P;
     std::memset(&P, 0, sizeof(P));
     P.w = w->d;
@@ -200,7 +210,11 @@ GemvPart make_part(const ah_tensor *w, uint32_t src, const void *x, const int64_
     P.row_bytes = (uint32_t)w->row_bytes;
     P.units = units_per_row(w->type, P.n_in);
     uint32_t rows = 0, lanes = 0;
-    stream = ah_gemv_stream_geometry(P.row_bytes, P.units, rows, lanes);
+    stream = ah_gemv_stream_geometry(w->type, P.row_bytes, P.units, P.n_out, rows, lanes);
+    if (latency && stream && w->type == AH_GGML_Q4_K && P.n_in > 64 && (P.n_out + rows - 1) / rows < kQ4kPairTiles) {
+        P.units = units_per_row(w->type, P.n_in, true);
+        stream = ah_gemv_stream_geometry(w->type, P.row_bytes, P.units, P.n_out, rows, lanes);
+    }
     if (stream) {
         P.rows_per_tile = rows;
         P.lanes = lanes;
@@ -929,6 +943,11 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
         p->act_bytes = (uint32_t)ah_gemv_act_bytes(kpad_max);
         *out = p;
         return AH_OK;
+    }
+    // A table plan serves many projections at once (throughput): its parts keep whole units.
+    for (size_t i = 0; i < n_parts; ++i) {
+        bool st = false;
+        parts[i] = make_part(w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr, st, false);
     }
     // Streaming plan: waves dealt over the parts, activations sharing a workgroup's LDS region of
     // at most `budget` bytes (15 KB keeps two workgroups per CU; a larger activation raises it).

@@ -544,6 +544,46 @@ AH_DEV float unit_q4(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
     return acc;
 }
 
+// Q4_K in units of one pair of sub-blocks (64 elements; u = 4 s + P for super-block s and pair
+// P), used where a projection is small enough that spreading a super-block over up to four lanes
+// shortens its waves.  Pair P takes bytes 2(P & 1) and 2(P & 1) + 1 of the low (P < 2) or high
+// (P >= 2) (sc, m) words above.
+template <bool DOTS>
+AH_DEV float unit_q4p(const uint8_t *tl, uint32_t off, uint32_t u, uint32_t n_in, const ActLds &A,
+                      int32_t *dots) {
+    const uint32_t P = u & 3u, g0 = 2 * u;  // pair P of super-block u / 4; its first 32-block
+    const u32x4 *sb = reinterpret_cast<const u32x4 *>(tl + off);  // the super-block, 16-byte aligned
+    const u32x4 h = sb[0];
+    const u32x4 qa = sb[1 + 2 * P], qb = sb[2 + 2 * P];
+    const float fd = ah_f16_bits_to_f32(h.x & 0xffffu), fdm = ah_f16_bits_to_f32(h.x >> 16);
+    const bool hi47 = P >= 2;
+    const uint32_t scw = hi47 ? ((h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u)) : (h.y & 0x3F3F3F3Fu);
+    const uint32_t mw = hi47 ? (((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u)) : (h.z & 0x3F3F3F3Fu);
+    const uint32_t bsh = 16 * (P & 1u);
+    const float sc0 = (float)((scw >> bsh) & 0xffu), sc1 = (float)((scw >> (bsh + 8)) & 0xffu);
+    const float m0 = (float)((mw >> bsh) & 0xffu), m1 = (float)((mw >> (bsh + 8)) & 0xffu);
+    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g0));
+    const u32x4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+    const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+    int32_t Dlo = 0, Dhi = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        Dlo = ah_sdot4(q[i] & 0x0F0F0F0Fu, xl[i], Dlo);
+        Dhi = ah_sdot4((q[i] >> 4) & 0x0F0F0F0Fu, xh[i], Dhi);
+    }
+    if (DOTS && dots) {
+        const uint32_t nb32 = (n_in + 31) / 32;
+        dots[g0] = Dlo;
+        if (g0 + 1 < nb32) dots[g0 + 1] = Dhi;  // a ragged row ends on an odd 32-block
+    }
+    // (past a ragged row's end the codes are zero: the pair's second half adds nothing)
+    const float tlo = (fd * sc0) * (float)Dlo - (fdm * m0) * (float)A.xs32[g0];
+    const float thi = (fd * sc1) * (float)Dhi - (fdm * m1) * (float)A.xs32[g0 + 1];
+    return A.fsc[g0] * tlo + A.fsc[g0 + 1] * thi;
+}
+
 // Q6_K super-block s (format/quant.rs:556-599): ql[128] @0, qh[64] @128, int8 sc[16] @192,
 // f16 d @208.  Element 128n + 32t + l = (nibble t/2 of ql[64n + 32(t&1) + l]
 // | ((qh[32n + l] >> 2t) & 3) << 4) - 32.  The unit is one half n (128 elements: ql[64n..],
@@ -599,30 +639,33 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, ui
     return acc;
 }
 
-template <int TYPE, bool DOTS>
-AH_DEV float comp_unit(const GemvPart &P, const uint8_t *tl, uint32_t off, uint32_t row, uint32_t u,
+// Q4_K parts use pair units where the host chose them for a small projection (units = ceil(K/64)
+// then exceeds the super-block count ceil(K/256); for K <= 64 the two forms are one).
+AH_DEV bool q4k_pair_units(const GemvPart &P) { return P.units > (P.n_in + 255) / 256; }
+
+// Unit u of the row that starts at byte `row_off` of the tile.  PAIRS: the kernel may meet Q4_K
+// pair units (the latency launches' kernels); table plans and the workgroup-tile kernel never do.
+template <int TYPE, bool DOTS, bool PAIRS = false>
+AH_DEV float comp_unit(const GemvPart &P, const uint8_t *tl, uint32_t row_off, uint32_t row, uint32_t u,
                        const ActLds &A) {
     if constexpr (TYPE == AH_GGML_Q8_0) {
         const uint32_t nb32 = (P.n_in + 31) / 32;
-        return unit_q8<DOTS>(tl, off, u, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
+        return unit_q8<DOTS>(tl, row_off + 34u * u, u, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
     } else if constexpr (TYPE == AH_GGML_Q5_0) {
         const uint32_t nb32 = (P.n_in + 31) / 32;
-        return unit_q5<DOTS>(tl, off, u, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
+        return unit_q5<DOTS>(tl, row_off + 22u * u, u, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
     } else if constexpr (TYPE == AH_GGML_Q4_K) {
         const uint32_t nb32 = (P.n_in + 31) / 32;
-        return unit_q4<DOTS>(tl, off, u, P.n_in, A, DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr);
+        int32_t *dots = DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr;
+        if (PAIRS && q4k_pair_units(P)) return unit_q4p<DOTS>(tl, row_off + 144u * (u >> 2), u, P.n_in, A, dots);
+        return unit_q4<DOTS>(tl, row_off + 144u * u, u, P.n_in, A, dots);
     } else {
         const uint32_t nb16 = (P.n_in + 15) / 16;
-        return unit_q6<DOTS>(tl, off, u >> 1, u & 1u, P.n_in, A, DOTS && P.dots ? P.dots + (size_t)row * nb16 : nullptr);
+        return unit_q6<DOTS>(tl, row_off + 210u * (u >> 1), u >> 1, u & 1u, P.n_in, A,
+                             DOTS && P.dots ? P.dots + (size_t)row * nb16 : nullptr);
     }
 }
 
-// Byte offset of unit u within a row: Q8_0 / Q5_0 blocks, Q4_K super-blocks, Q6_K half
-// super-blocks (both halves of a super-block start at its first byte).
-constexpr uint32_t unit_off(int type, uint32_t u) {
-    return type == AH_GGML_Q8_0 ? 34u * u : type == AH_GGML_Q5_0 ? 22u * u
-         : type == AH_GGML_Q4_K ? 144u * u : 210u * (u >> 1);
-}
 constexpr uint32_t kRedSlots = 1024;  // unit partials of one tile
 constexpr uint32_t kTileSlack = 128;  // bytes past a tile that realigned or compact-row unit reads may touch
 
@@ -674,7 +717,7 @@ __global__ void __launch_bounds__(kThreads)
         for (uint32_t f = threadIdx.x; f < TU; f += kThreads) {
             const uint32_t r = f / U, u = f - r * U, row = tile * R + r;
             float v = 0.0f;
-            if (row < P.n_out) v = comp_unit<TYPE, true>(P, tl, toff + r * RB + unit_off(TYPE, u), row, u, A);
+            if (row < P.n_out) v = comp_unit<TYPE, true>(P, tl, toff + r * RB, row, u, A);
             A.red[f] = v;
         }
         ah_lds_barrier();
@@ -1149,24 +1192,24 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
                 if (P.type == AH_GGML_Q4_K) {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q4_K, DOTS>(P, tl, toff + r * RB + unit_off(AH_GGML_Q4_K, u), row, u, A);
+                        acc += comp_unit<AH_GGML_Q4_K, DOTS, !PLAN>(P, tl, toff + r * RB, row, u, A);
                 } else if (P.type == AH_GGML_Q6_K) {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q6_K, DOTS>(P, tl, toff + r * RB + unit_off(AH_GGML_Q6_K, u), row, u, A);
+                        acc += comp_unit<AH_GGML_Q6_K, DOTS, !PLAN>(P, tl, toff + r * RB, row, u, A);
                 } else if (P.type == AH_GGML_Q5_0) {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q5_0, DOTS>(P, tl, toff + r * RB + unit_off(AH_GGML_Q5_0, u), row, u, A);
+                        acc += comp_unit<AH_GGML_Q5_0, DOTS, !PLAN>(P, tl, toff + r * RB, row, u, A);
                 } else {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q8_0, DOTS>(P, tl, toff + r * RB + unit_off(AH_GGML_Q8_0, u), row, u, A);
+                        acc += comp_unit<AH_GGML_Q8_0, DOTS, !PLAN>(P, tl, toff + r * RB, row, u, A);
                 }
             } else {
 #pragma unroll 1
                 for (uint32_t u = g; u < U; u += G)
-                    acc += comp_unit<TYPE, DOTS>(P, tl, toff + r * RB + unit_off(TYPE, u), row, u, A);
+                    acc += comp_unit<TYPE, DOTS, !PLAN>(P, tl, toff + r * RB, row, u, A);
             }
         }
         acc = group_sum(acc, G);
@@ -1463,24 +1506,24 @@ AH_DEV void seq_gemv_stage(const SeqArgs &a, uint32_t s, uint32_t r, bool &broke
                 if (P.type == AH_GGML_Q4_K) {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q4_K, false>(P, tl, toff + rr * RB + unit_off(AH_GGML_Q4_K, u), row, u, A);
+                        acc += comp_unit<AH_GGML_Q4_K, false, true>(P, tl, toff + rr * RB, row, u, A);
                 } else if (P.type == AH_GGML_Q6_K) {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q6_K, false>(P, tl, toff + rr * RB + unit_off(AH_GGML_Q6_K, u), row, u, A);
+                        acc += comp_unit<AH_GGML_Q6_K, false, true>(P, tl, toff + rr * RB, row, u, A);
                 } else if (P.type == AH_GGML_Q5_0) {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q5_0, false>(P, tl, toff + rr * RB + unit_off(AH_GGML_Q5_0, u), row, u, A);
+                        acc += comp_unit<AH_GGML_Q5_0, false, true>(P, tl, toff + rr * RB, row, u, A);
                 } else {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
-                        acc += comp_unit<AH_GGML_Q8_0, false>(P, tl, toff + rr * RB + unit_off(AH_GGML_Q8_0, u), row, u, A);
+                        acc += comp_unit<AH_GGML_Q8_0, false, true>(P, tl, toff + rr * RB, row, u, A);
                 }
             } else {
 #pragma unroll 1
                 for (uint32_t u = g; u < U; u += G)
-                    acc += comp_unit<TYPE, false>(P, tl, toff + rr * RB + unit_off(TYPE, u), row, u, A);
+                    acc += comp_unit<TYPE, false, true>(P, tl, toff + rr * RB, row, u, A);
             }
         }
         acc = group_sum(acc, G);
@@ -1534,18 +1577,44 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>()) gemv
 // A lane computes ceil(units / G) units of its row per tile, so (rows, G) is chosen for the most
 // row bytes per round of unit work (ties to more rows): e.g. Q4_K at K = 1536 takes 8 rows of 8
 // lanes (one super-block each) rather than 9 rows of 4 (two each).
-bool ah_gemv_stream_geometry(uint32_t row_bytes, uint32_t units, uint32_t &rows, uint32_t &lanes) {
+// Rows per wave tile and lanes per row of a streaming part.  Whole-unit parts (32-blocks, Q4_K
+// super-blocks, Q6_K halves) maximize the bytes a wave streams per round of units (measured best
+// for them at every decode and batch shape).  Q4_K pair units (chosen for small projections, see
+// units_per_row's callers) minimize a wave's time instead: tiles per wave times the rounds of pairs
+// per tile plus the tile's fixed steps (staging, the row sums, the store: about two pairs), over a
+// device of kLatencyWaves waves, so a small projection spreads over many waves with one round each.
+// Ties go to more rows per tile (fewer workgroups).  The choice depends on the part alone.
+bool ah_gemv_stream_geometry(uint32_t type, uint32_t row_bytes, uint32_t units, uint32_t n_out, uint32_t &rows,
+                             uint32_t &lanes) {
     if (row_bytes == 0 || row_bytes + 16 > kStreamTile) return false;
     const uint32_t fit = (kStreamTile - 16) / row_bytes;
-    uint64_t best = 0;
+    const bool pairs = type == AH_GGML_Q4_K && row_bytes / (units ? units : 1u) < 64;
     rows = 1;
     lanes = 64;
+    if (!pairs) {
+        uint64_t best = 0;
+        for (uint32_t G = 1; G <= 64; G <<= 1) {
+            const uint32_t r = fit < 64 / G ? fit : 64 / G;
+            const uint32_t rounds = units > G ? (units + G - 1) / G : 1u;
+            const uint64_t score = (uint64_t)r * row_bytes * 64 / rounds;
+            if (score > best) {
+                best = score;
+                rows = r;
+                lanes = G;
+            }
+        }
+        return true;
+    }
+    constexpr uint64_t kLatencyWaves = 2048;  // 8 waves on each of 256 CUs
+    uint64_t best = ~0ull;
     for (uint32_t G = 1; G <= 64; G <<= 1) {
         const uint32_t r = fit < 64 / G ? fit : 64 / G;
-        const uint32_t rounds = units > G ? (units + G - 1) / G : 1u;
-        const uint64_t score = (uint64_t)r * row_bytes * 64 / rounds;
-        if (score > best) {
-            best = score;
+        const uint64_t rounds = units > G ? (units + G - 1) / G : 1u;
+        const uint64_t tiles = (n_out + r - 1) / r;
+        const uint64_t per_wave = (tiles + kLatencyWaves - 1) / kLatencyWaves;
+        const uint64_t cost = per_wave * (rounds + 2);
+        if (cost < best || (cost == best && r > rows)) {
+            best = cost;
             rows = r;
             lanes = G;
         }

@@ -266,49 +266,81 @@ def test_gemv_linearity_full_size(dev):
     w.free()
 
 
+def rows_vs_oracle(t, raw, n_in, x, y, what, max_rows=2048):
+    """y (one projection's outputs for f32 input x) within the contract of the oracle, on every row
+    up to max_rows and a sample past them."""
+    n_out = y.shape[0]
+    rows = np.arange(n_out) if n_out <= max_rows else np.unique(
+        np.concatenate([np.arange(64), np.random.default_rng(n_out).integers(0, n_out, max_rows)]))
+    rb = synth.row_bytes(t, n_in)
+    sub = np.concatenate([raw[r * rb:(r + 1) * rb] for r in rows])
+    st, codes, scales = oracle.quant_act_f32(x)
+    assert st == 0
+    st, yref = oracle.matvec_q8act(t, sub, len(rows), n_in, codes, scales)
+    st2, absdot = oracle.row_absdot(t, sub, len(rows), n_in, codes, scales)
+    assert st == 0 and st2 == 0
+    assert_close(np.asarray(y)[rows], yref, absdot, what)
+
+
 def test_grouped_plan_matches_single_launches(dev):
+    """A table plan (more than four parts) of configs[1]-shaped Q4_K projections, and the same
+    projections launched one by one, each within the contract of the oracle.  A table plan keeps
+    whole super-blocks where a single launch of a small projection cuts sub-block pairs, so the two
+    forms meet through the oracle rather than bit for bit."""
     rng = synth.rng_for(1, 99)
     shapes = [(896, 896), (128, 896), (128, 896), (896, 896), (4864, 896), (4864, 896), (896, 4864)]
-    ws, xs, ys, singles = [], [], [], []
+    ws, xs, ys, singles, raws, xnp = [], [], [], [], [], []
     for n_out, n_in in shapes:
         raw = synth.payload(12, rng, n_out, n_in)
         w = dev.upload(12, raw, n_out, n_in)
-        x = to_dev(synth.activations(rng, n_in))
+        xa = synth.activations(rng, n_in)
+        x = to_dev(xa)
         y = torch.zeros(n_out, dtype=torch.float32, device="cuda")
         ys1 = torch.zeros(n_out, dtype=torch.float32, device="cuda")
         w.gemv_f32_dev(ptr(x), ptr(ys1), stream())
-        ws.append(w), xs.append(x), ys.append(y), singles.append(ys1)
+        ws.append(w), xs.append(x), ys.append(y), singles.append(ys1), raws.append(raw), xnp.append(xa)
     plan = chart.GemvPlan(dev, ws, [ptr(x) for x in xs], [ptr(y) for y in ys])
     for _ in range(3):
         plan.run(stream())
     assert dev.sync_status(stream()) == 0
-    for y, s in zip(ys, singles):
-        assert torch.equal(y, s)
+    for i, ((n_out, n_in), y, s) in enumerate(zip(shapes, ys, singles)):
+        rows_vs_oracle(12, raws[i], n_in, xnp[i], y.cpu().numpy(), f"plan part {i}")
+        rows_vs_oracle(12, raws[i], n_in, xnp[i], s.cpu().numpy(), f"single {i}")
     plan.free()
     for w in ws:
         w.free()
 
 
 def _plan_vs_singles(dev, t, shapes, seed):
-    """A plan's outputs equal single launches bit for bit.  t is one ggml type for every part, or a
-    list with one type per shape (a mixed-type plan)."""
+    """A plan's outputs equal single launches bit for bit, but for the Q4_K parts of a table plan
+    (more than four parts): single launches of small projections cut sub-block pairs where a table
+    plan keeps whole super-blocks, so those parts meet through the oracle (both forms within its
+    contract).  t is one ggml type for every part, or a list with one type per shape (a mixed-type
+    plan)."""
     rng = synth.rng_for(5, seed)
     types = t if isinstance(t, list) else [t] * len(shapes)
-    ws, xs, ys, singles = [], [], [], []
+    ws, xs, ys, singles, raws, xnp = [], [], [], [], [], []
     for (n_out, n_in), t in zip(shapes, types):
         raw = synth.payload(t, rng, n_out, n_in)
         w = dev.upload(t, raw, n_out, n_in)
-        x = to_dev(synth.activations(rng, n_in))
+        xa = synth.activations(rng, n_in)
+        x = to_dev(xa)
         y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
         ys1 = torch.zeros(n_out, dtype=torch.float32, device="cuda")
         w.gemv_f32_dev(ptr(x), ptr(ys1), stream())
-        ws.append(w), xs.append(x), ys.append(y), singles.append(ys1)
+        ws.append(w), xs.append(x), ys.append(y), singles.append(ys1), raws.append(raw), xnp.append(xa)
     plan = chart.GemvPlan(dev, ws, [ptr(x) for x in xs], [ptr(y) for y in ys])
     for _ in range(2):
         plan.run(stream())
     assert dev.sync_status(stream()) == 0
+    table = len(shapes) > 4
     for i, (y, s1) in enumerate(zip(ys, singles)):
-        assert torch.equal(y, s1), (t, i, shapes[i])
+        if table and types[i] == 12:
+            n_in = shapes[i][1]
+            rows_vs_oracle(12, raws[i], n_in, xnp[i], y.cpu().numpy(), f"plan part {i} {shapes[i]}")
+            rows_vs_oracle(12, raws[i], n_in, xnp[i], s1.cpu().numpy(), f"single {i} {shapes[i]}")
+        else:
+            assert torch.equal(y, s1), (t, i, shapes[i])
     plan.free()
     for w in ws:
         w.free()

@@ -132,12 +132,16 @@ AH_DEV QuadIn quad_load(const void *x, const int64_t *scales, uint32_t src, uint
     return in;
 }
 
-// The same inputs for one activation row read through buffer resources: elements past n_in lie
-// past the resource's range and read as zero.  Every source kind issues the same five buffer loads
-// (offsets picked by `src`, unused ones out of range) and nothing here touches the loaded words,
-// so there is no branch and no wait: the loads return in issue order ahead of the weight stream,
-// and quad_quant, which waits for them, never waits for the weights.  Codes are read a whole dword
-// at a time (the base must be 4-byte aligned); quad_quant clears bytes past n_in.
+// The same inputs for one activation row of a GEMV read through buffer resources: elements past
+// n_in lie past the resource's range and read as zero.  A GEMV's activation is f32 or codes (the
+// Q32.32 form is the standalone quantizer's alone, which reads through quad_load), and either
+// source issues the same three buffer loads (offsets picked by `src`; the Q32 words stay zero) and
+// nothing here touches the loaded words, so there is no branch and no wait: the loads return in
+// issue order, and quad_quant, which waits for them, never waits for a load issued after them.
+// An unused load's offset lies out of range by a lane-dependent amount: with one constant offset
+// for the whole wave the compiler would take its (zero) result for a wave-uniform value and move
+// it to a scalar register, which waits for the load.  Codes are read a whole dword at a time (the
+// base must be 4-byte aligned); quad_quant clears bytes past n_in.
 struct ActRsrc {
     __amdgpu_buffer_rsrc_t x, s;
 };
@@ -154,17 +158,16 @@ AH_DEV QuadIn quad_load_row(const ActRsrc &r, uint32_t src, uint32_t n_in, uint3
     QuadIn in;
     const uint32_t k0 = b * 32 + 8 * (threadIdx.x & 3);
     in.take = n_in > k0 ? (n_in - k0 < 8 ? n_in - k0 : 8) : 0;
-    const bool f = src == AH_SRC_F32, q = src == AH_SRC_Q32;
-    const uint32_t base = f ? 4 * k0 : q ? 8 * k0 : k0;
+    const bool f = src == AH_SRC_F32;
+    const uint32_t base = f ? 4 * k0 : k0;
+    const uint32_t oob = kActOob - 16 * (threadIdx.x & 3);  // past any activation resource
     const u32x4 l0 = ah_ld128p<CP>(r.x, base);
-    const u32x4 l1 = ah_ld128p<CP>(r.x, f || q ? base + 16 : kActOob);
-    const u32x4 l2 = ah_ld128p<CP>(r.x, q ? base + 32 : kActOob);
-    const u32x4 l3 = ah_ld128p<CP>(r.x, q ? base + 48 : kActOob);
-    const u32x2 sc = ah_ld64<CP>(r.s, f || q ? kActOob : 8 * b);
+    const u32x4 l1 = ah_ld128p<CP>(r.x, f ? base + 16 : oob);
+    const u32x2 sc = ah_ld64<CP>(r.s, f ? oob : 8 * b);
     in.w[0] = l0.x; in.w[1] = l0.y; in.w[2] = l0.z; in.w[3] = l0.w;
     in.w[4] = l1.x; in.w[5] = l1.y; in.w[6] = l1.z; in.w[7] = l1.w;
-    in.w[8] = l2.x; in.w[9] = l2.y; in.w[10] = l2.z; in.w[11] = l2.w;
-    in.w[12] = l3.x; in.w[13] = l3.y; in.w[14] = l3.z; in.w[15] = l3.w;
+#pragma unroll
+    for (int i = 8; i < 16; ++i) in.w[i] = 0u;
     in.s0 = sc.x;
     in.s1 = sc.y;
     return in;

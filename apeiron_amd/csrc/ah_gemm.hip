@@ -137,9 +137,15 @@ template <int TYPE> constexpr uint32_t max_parts() { return ah_blk32(TYPE) ? 1u 
 uint32_t max_parts_of(uint32_t type) { return ah_blk32((int)type) ? 1u : kGemmMaxParts; }
 template <int TYPE> constexpr int tok() { return 32 * nm<TYPE>(); }              // tokens per workgroup
 template <int TYPE> constexpr int act_bytes() { return tok<TYPE>() * kKS * 2; }   // f16 slice of a stage
-template <int TYPE> constexpr int buf_bytes() {                                    // + Q4_K split sums
-    return act_bytes<TYPE>() + (TYPE == AH_GGML_Q4_K ? tok<TYPE>() * 32 : 0);
-}
+template <int TYPE> constexpr int buf_bytes() { return act_bytes<TYPE>(); }         // one ring slot
+// Q4_K split code sums of a super-block (32 bytes per token), loaded once per super-block by one
+// 16-byte direct-to-LDS instruction per wave into a region of their own after the ring: wave w's
+// lanes l < xlanes<W>() take tokens [w * xtok<W>(), +xtok<W>()), two lanes per token; its other
+// lanes read out of range into the rest of the wave's 1 KB.
+template <int W> constexpr int xtok() { return tok<AH_GGML_Q4_K>() / W; }
+template <int W> constexpr int xlanes() { return 2 * xtok<W>(); }
+template <int TYPE, int W> constexpr int xregion() { return TYPE == AH_GGML_Q4_K ? W * 1024 : 0; }
+template <int TYPE, int W, int R> constexpr int lds_bytes() { return R * buf_bytes<TYPE>() + xregion<TYPE, W>(); }
 // Split granularity in stages (Q8_0 pairs, K-quant super-blocks); the loop body is 4 stages.
 template <int TYPE> constexpr int unroll() { return ah_blk32(TYPE) ? 2 : 4; }
 // Weight register sets and how many stages ahead they are fetched (Q6_K's 27-register set
@@ -147,18 +153,24 @@ template <int TYPE> constexpr int unroll() { return ah_blk32(TYPE) ? 2 : 4; }
 // The prologue replays ring - 1 notional stages, so a fetch is at most ring - 1 stages ahead.
 template <int TYPE, int R> constexpr int dw() { return TYPE == AH_GGML_Q6_K || R < 3 ? 1 : 2; }
 template <int TYPE, int R> constexpr int nw() { return dw<TYPE, R>() == 1 ? 2 : 4; }
-// Per-wave direct-to-LDS instructions of one stage's slice: activation (16-byte loads, 1 KB per
-// instruction) and Q4_K split sums (4-byte loads, 256 B each).
+// Per-wave direct-to-LDS instructions of one stage's slice (16-byte loads, 1 KB per
+// instruction), and of a super-block's Q4_K split sums (issued at its first stage).
 template <int TYPE, int W> constexpr int an() { return tok<TYPE>() * kKS * 2 / 1024 / W; }
-template <int TYPE, int W> constexpr int xn() { return TYPE == AH_GGML_Q4_K ? tok<TYPE>() * 32 / 256 / W : 0; }
-// The vmcnt the top of a stage waits for.  The stage's slice was issued R - 1 stages earlier (R
-// ring slots); after it came the slices of the R - 2 stages that follow and the weight fetches.
-// Only the slices are counted: the compiler merges or drops weight loads that coincide across
-// the unrolled stages (the Q6_K d dword is one address for a whole super-block), so their number
-// per stage is not fixed, while every slice instruction is issued.  Vector memory loads complete
-// in issue order, so vmcnt <= the slice instructions issued since makes the stage's slice (and
-// any weight fetch older than those) complete, whatever the weight loads' count.
-template <int TYPE, int W, int R> constexpr int wait_count() { return (R - 2) * (xn<TYPE, W>() + an<TYPE, W>()); }
+template <int TYPE> constexpr int xn() { return TYPE == AH_GGML_Q4_K ? 1 : 0; }
+// The vmcnt the top of stage u (of a super-block) waits for.  The stage's slice was issued R - 1
+// stages earlier (R ring slots); after it came the slices of the R - 2 stages that follow, the
+// split sums issued at a super-block's first stage (before that stage's slice, R = 4) and the
+// weight fetches.  Only the slices and split sums are counted: the compiler merges or drops
+// weight loads that coincide across the unrolled stages (the Q6_K d dword is one address for a
+// whole super-block), so their number per stage is not fixed, while every slice instruction is
+// issued.  Vector memory loads complete in issue order, so vmcnt <= the slice instructions issued
+// since makes the stage's slice (and any load older than it, such as the split sums issued just
+// before the slice of a super-block's last stage) complete, whatever the weight loads' count.
+template <int TYPE, int W, int R> constexpr int wait_count(int u) {
+    int n = 0;
+    for (int v = u - (R - 2); v < u; ++v) n += an<TYPE, W>() + (((v % 4) + 4) % 4 == 0 ? xn<TYPE>() : 0);
+    return n;
+}
 inline uint32_t tok_of(uint32_t type) {
     return type == AH_GGML_Q4_K ? tok<AH_GGML_Q4_K>() : type == AH_GGML_Q6_K ? tok<AH_GGML_Q6_K>() : tok<AH_GGML_Q8_0>();
 }
@@ -429,11 +441,13 @@ template <int TYPE, int WV, int RG>
 // (by value: with a reference to the kernel argument the Q8_0 kernel grows from 207 to 256 VGPRs)
 AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds_base) {
     constexpr int NN = rb::kNN, NM = rb::nm<TYPE>(), NW = rb::nw<TYPE, RG>(), DW = rb::dw<TYPE, RG>();
-    constexpr int kTok = rb::tok<TYPE>(), kActBytes = rb::act_bytes<TYPE>();
-    constexpr int kAN = rb::an<TYPE, WV>(), kXN = rb::xn<TYPE, WV>();
+    constexpr int kTok = rb::tok<TYPE>();
+    constexpr int kAN = rb::an<TYPE, WV>();
     constexpr int kR = RG;
+    static_assert(TYPE != AH_GGML_Q4_K || kR == 4, "the split sums ride with a super-block's last slice");
     constexpr uint32_t kBuf = rb::buf_bytes<TYPE>();
     auto lds = [&](int k) -> uint8_t * { return lds_base + k * kBuf; };
+    uint8_t *const xmin_lds = lds_base + kR * kBuf;  // Q4_K split sums of the current super-block
     // XCD-aware order: dispatch i goes to XCD i % 8, so XCD x takes logical ids
     // [x * per, (x + 1) * per).  Consecutive logical ids share a weight row tile and split, so the
     // workgroups reading the same weights share one XCD's L2.  The grid is a multiple of 8.
@@ -495,15 +509,18 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
                 rx, (__attribute__((address_space(3))) void *)(buf + (wv * kAN + i) * 1024u), 16,
                 live && t < ntile ? (t * a.kpad + st * kKS + 8 * c) * 2u : kOob, 0, 0, 0);
         }
+    };
+    // Q4_K: the 32-byte split code sums of super-block sb for the tile's tokens, issued at the
+    // super-block's first stage just before the slice of its last stage, the one that reads them.
+    // Wave w, lane l < xlanes: token w * xtok + l / 2, bytes 16 (l & 1) .. +16.
+    auto xmin_dma = [&](uint32_t st) {
         if constexpr (TYPE == AH_GGML_Q4_K) {
-            // the 32-byte split code sums of the stage's super-block, [token][32 B] after the slice
-#pragma unroll
-            for (int i = 0; i < kXN; ++i) {
-                const uint32_t o = (wv * kXN + i) * 256u + lane * 4u, t = o >> 5;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rm, (__attribute__((address_space(3))) void *)(buf + kActBytes + (wv * kXN + i) * 256u), 4,
-                    live && t < ntile ? (t * nsb + st / 4) * 32u + (o & 31u) : kOob, 0, 0, 0);
-            }
+            constexpr uint32_t kXT = rb::xtok<WV>(), kXL = rb::xlanes<WV>();
+            const uint32_t t = wv * kXT + ((uint32_t)lane >> 1);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rm, (__attribute__((address_space(3))) void *)(xmin_lds + wv * 1024u), 16,
+                st < st_end && (uint32_t)lane < kXL && t < ntile ? (t * nsb + st / 4) * 32u + 16u * (lane & 1) : kOob,
+                0, 0, 0);
         }
     };
     const uint32_t sw = (uint32_t)(j >> 1) & 7u;
@@ -543,7 +560,8 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
         constexpr int u = decltype(uc)::value;
         // the slice of this stage is complete in every wave, and every wave is done with the slot
         // the next slice goes to (read by the previous stage)
-        ah_vm_lds_barrier<rb::wait_count<TYPE, WV, RG>()>();
+        ah_vm_lds_barrier<rb::wait_count<TYPE, WV, RG>(u)>();
+        if constexpr (u == 0) xmin_dma(st);
         act_dma(lds((u + kR - 1) % kR), st + kR - 1);
         W[(u + DW) % NW] = fetch_rb<TYPE, (u + DW) % 4, NN>(rs, rbase, rl, st + DW, a.n_in, h, st + DW < st_end);
         __builtin_amdgcn_sched_barrier(0);  // the requests above stay ahead of this stage's work
@@ -727,7 +745,9 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
                     const f16x8 bm = pack8(as_u(m01), as_u(m23), as_u(m45), as_u(m67));
 #pragma unroll
                     for (int m = 0; m < NM; ++m) {
-                        const f16x8 am = *reinterpret_cast<const f16x8 *>(cur + kActBytes + (32 * m + j) * 32 + 16 * h);
+                        constexpr uint32_t kXT = rb::xtok<WV>();
+                        const uint32_t T = 32 * m + j;
+                        const f16x8 am = *reinterpret_cast<const f16x8 *>(xmin_lds + (T / kXT) * 1024u + (T % kXT) * 32u + 16u * h);
                         const f32x16 pm = mfma(am, bm, (f32x16){});
 #pragma unroll
                         for (int r = 0; r < 16; ++r)
@@ -756,7 +776,7 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
 
 template <int TYPE, int WV, int RG>
 __global__ void __launch_bounds__(64 * WV, TYPE == AH_GGML_Q4_K ? 4 : 2) gemm_rb_kernel(GemmArgs a) {
-    __shared__ __align__(16) uint8_t lds[RG * rb::buf_bytes<TYPE>()];
+    __shared__ __align__(16) uint8_t lds[rb::lds_bytes<TYPE, WV, RG>()];
     gemm_rb_body<TYPE, WV, RG>(a, lds);
 }
 
@@ -938,9 +958,9 @@ __global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
 // each workgroup runs its part's body, a branch uniform over the workgroup.  A group's runs of
 // the two types (q/k beside v) then share the CUs one run alone leaves idle.
 __global__ void __launch_bounds__(256, 2) gemm_rb_kquant_kernel(GemmArgs a) {
-    constexpr uint32_t kB = rb::buf_bytes<AH_GGML_Q4_K>() > rb::buf_bytes<AH_GGML_Q6_K>()
-                                ? rb::buf_bytes<AH_GGML_Q4_K>() : rb::buf_bytes<AH_GGML_Q6_K>();
-    __shared__ __align__(16) uint8_t lds[4 * kB];
+    // the larger of the two bodies' LDS (the Q4_K ring and its split-sum region fit in Q6_K's ring)
+    constexpr int kL4 = rb::lds_bytes<AH_GGML_Q4_K, 4, 4>(), kL6 = rb::lds_bytes<AH_GGML_Q6_K, 4, 4>();
+    __shared__ __align__(16) uint8_t lds[kL4 > kL6 ? kL4 : kL6];
     const uint32_t per = gridDim.x >> 3;
     const uint32_t L = (blockIdx.x & 7u) * per + (blockIdx.x >> 3);
     if (L >= a.n_wg) return;

@@ -1,10 +1,10 @@
 """Properties of the compiled GEMM kernel that its LDS ring depends on (CPU: hipcc cross-compiles).
 
-The ring's barrier waits for `vmcnt <= (slots - 2) * slice instructions`: vector memory loads
-complete in issue order, so every slice instruction issued before the last (slots - 2) stages'
-slices has landed.  That holds only if each slice instruction is issued on every path, so no
-direct-to-LDS load may sit where an `s_cbranch_execz` can jump over it, and every barrier must use
-the count of its instantiation.
+The ring's barrier at stage u waits for `vmcnt <=` the slice instructions issued in the
+(slots - 2) stages before u (plus, for Q4_K, the one split-sum load issued at a super-block's first
+stage): vector memory loads complete in issue order, so every load issued before those has landed.
+That holds only if each slice instruction is issued on every path, so no direct-to-LDS load may sit
+where an `s_cbranch_execz` can jump over it, and every barrier must use the count of its stage.
 """
 from __future__ import annotations
 
@@ -22,11 +22,12 @@ KS = 64  # K depth of one stage
 TYPES = {8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}
 
 
-def expected_vmcnt(t: int, waves: int, slots: int) -> int:
+def expected_vmcnt(t: int, waves: int, slots: int) -> list[int]:
+    """The count of each of the loop's four stages (u = 0..3 of a super-block)."""
     tok = 64 if t == 12 else 128
     an = tok * KS * 2 // 1024 // waves
-    xn = tok * 32 // 256 // waves if t == 12 else 0
-    return (slots - 2) * (an + xn)
+    xn = 1 if t == 12 else 0  # Q4_K split sums: one load per wave at a super-block's stage 0
+    return [sum(an + (xn if v % 4 == 0 else 0) for v in range(u - (slots - 2), u)) for u in range(4)]
 
 
 @pytest.fixture(scope="module")
@@ -69,33 +70,32 @@ def test_ring_barriers_wait_for_the_slice_count(gemm_asm):
     for (t, waves, slots), body in kernels(gemm_asm):
         want = expected_vmcnt(t, waves, slots)
         bars = [i for i, l in enumerate(body) if l.startswith("s_barrier")]
-        assert bars, (t, waves, slots)
-        for i in bars:
+        assert len(bars) == 4, (t, waves, slots, len(bars))  # the loop body's four stages, in order
+        for i, w in zip(bars, want):
             m = re.match(r"s_waitcnt vmcnt\((\d+)\) lgkmcnt\(0\)", body[i - 1])
-            assert m and int(m.group(1)) == want, (TYPES[t], waves, slots, body[i - 1], want)
+            assert m and int(m.group(1)) == w, (TYPES[t], waves, slots, body[i - 1], want)
 
 
 def test_mixed_kquant_kernel_barriers(gemm_asm):
-    """The grid of Q4_K and Q6_K parts holds both bodies on a 4-slot ring of 4 waves; both wait
-    for 8 slice instructions and no slice load sits behind an execz branch."""
+    """The grid of Q4_K and Q6_K parts holds both bodies on a 4-slot ring of 4 waves; each
+    body's barriers wait for its own stage counts and no slice load sits behind an execz branch."""
     starts = [i for i, l in enumerate(gemm_asm) if re.match(r"^_ZN12_GLOBAL__N_121gemm_rb_kquant_kernel\S*:", l)]
     assert starts
     end = next(j for j in range(starts[0], len(gemm_asm)) if "s_endpgm" in gemm_asm[j])
     body = [x.strip() for x in gemm_asm[starts[0]:end]]
-    want = expected_vmcnt(12, 4, 4)
-    assert want == expected_vmcnt(14, 4, 4)
-    ring = 0
+    q4, q6 = expected_vmcnt(12, 4, 4), expected_vmcnt(14, 4, 4)
+    seen = []
     for i, l in enumerate(body):
         if l.startswith("s_barrier"):
             m = re.match(r"s_waitcnt vmcnt\((\d+)\) lgkmcnt\(0\)$", body[i - 1])
             if m:
-                ring += 1
-                assert int(m.group(1)) == want, body[i - 1]
+                seen.append(int(m.group(1)))
         m = re.match(r"s_cbranch_execz\s+(\S+)", l)
         if m:
             for x in skipped_by_execz(body, i, m.group(1)):
                 assert not (x.startswith("buffer_load") and x.endswith(" lds")), x
-    assert ring >= 8, ring  # four stages in each body
+    # four stages in each body, in loop order, one body after the other
+    assert seen in (q4 + q6, q6 + q4), (seen, q4, q6)
 
 
 def test_no_slice_load_can_be_skipped(gemm_asm):

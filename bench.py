@@ -31,8 +31,9 @@ Also reported, beside the value:
                 designs, int8 and f16), the MFMA-only probe, and the configs[4] N = 512 prefill
                 (--only gemm3: the configs[3] GEMMs alone, for profiling);
   heads         configs[0] (Q8_0 4864x896) and configs[2] (151936x896 head, Q6_K and Q8_0);
-  cpu_baseline  the restated reference fast path (oracle/ah_cpu_fast.c) on the same token's
-                projections, on this host's cores; cpu_baseline_gemm the same for N = 512.
+  cpu_baseline  the restated reference fast path (oracle/ah_cpu_fast.c: AVX-VNNI or AVX2 dots,
+                two-row tiles) on the same token's projections, on this host's cores;
+                cpu_baseline_gemm the same for N = 512.
 """
 from __future__ import annotations
 
@@ -523,7 +524,8 @@ def main() -> int:
             "sample": f"{best['layers']} configs[4] layers ({best['layers'] / CFG4_LAYERS:.1f} tokens, the head "
                       f"once per 28 layers), f32 input quantized once per input width, {best['seconds']} s, "
                       f"{n_copies} rotating host copies of the layer payloads",
-            "cpu": _cpu_name(), "host_cpus": os.cpu_count(), "cpu_flags": cpu_flags(), "runs": runs}
+            "cpu": _cpu_name(), "host_cpus": os.cpu_count(), "cpu_flags": cpu_flags(),
+            "cores_form": ("portable", "avx2", "avx_vnni")[oracle.cpu_path()], "runs": runs}
         del copies
     if args.only in (None, "gemm") and not args.no_cpu and not args.no_gemm and not args.no_extras:
         import oracle
@@ -542,7 +544,8 @@ def main() -> int:
                 el = time.perf_counter() - t0
                 gops = 2.0 * k * n_out * n_in / el / 1e9
                 cg.append({"type": synth.NAMES[gt], "shape": [n_out, n_in], "columns": k, "threads": threads,
-                           "seconds": round(el, 3), "gops": round(gops, 1)})
+                           "seconds": round(el, 3), "gops": round(gops, 1),
+                           "cores_form": ("portable", "avx2", "avx_vnni")[oracle.cpu_path()]})
         result["cpu_baseline_gemm"] = cg
         log(f"[bench] cpu gemm baseline: {[c['gops'] for c in cg]} GOPS")
 

@@ -44,6 +44,7 @@ def lib():
         L.aho_row_absdot.argtypes = [ctypes.c_uint32, c_ptr, c_size, c_size, c_size, c_ptr, c_ptr, c_ptr]
         L.aho_matvec_q8act_fast.argtypes = [ctypes.c_uint32, c_ptr, c_size, c_size, c_size, c_ptr, c_ptr, c_ptr, ctypes.c_int]
         L.aho_matmat_q8act_fast.argtypes = [ctypes.c_uint32, c_ptr, c_size, c_size, c_size, c_size, c_ptr, c_ptr, c_ptr, ctypes.c_int]
+        L.aho_set_cpu_path.argtypes = [ctypes.c_int]
         L.aho_row_bytes.argtypes = [ctypes.c_uint32, c_size, ctypes.POINTER(c_size)]
         L.aho_fixed_exp.argtypes = [ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]
         L.aho_silu_fixed.argtypes = [ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]
@@ -212,3 +213,16 @@ def swiglu_quant_f32(gate, up):
 def q32_to_real(y: np.ndarray) -> np.ndarray:
     """Q32.32 integers as real values (float64; exact for |y| < 2^53)."""
     return np.asarray(y, dtype=np.float64) / 4294967296.0
+
+
+CPU_PORTABLE, CPU_AVX2, CPU_VNNI = 0, 1, 2
+
+
+def set_cpu_path(path: int) -> int:
+    """Forces the fast path's cores (clamped to what the host has; -1: the host's best) and
+    returns the path now in use."""
+    return lib().aho_set_cpu_path(path)
+
+
+def cpu_path() -> int:
+    return lib().aho_cpu_path()

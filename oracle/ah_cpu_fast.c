@@ -3,20 +3,22 @@
  *
  * TEST/BENCH INFRASTRUCTURE ONLY (the CPU baseline leg of bench.py and its tests).
  *
- * Restates the chart row kernels of the reference, one row at a time (the reference's two-row
- * tiling, x86.rs:782-1192, and AVX-VNNI cores, x86.rs:74-85, are not restated: this is a lower
- * bound on its rate): each 32-lane group yields an exact i32
- * dot (AVX2 maddubs/madd, chart/x86.rs:175-449) and one i128 fold
- * acc += S_b * (w_scale*dot - w_min*xsum) (RowAcc::emit, chart/mod.rs:501-514); the row ends
- * with round_shift_32 and the i64 range check (chart/mod.rs:1739-1753).  Rows are split into
- * contiguous chunks over a thread pool (chart/ffn.rs:667-727); the GEMM form decodes each
- * row's groups once and dots them against every token column (chart/kcols.rs k-column form).
+ * Restates the chart row kernels of the reference: each 32-lane group yields an exact i32 dot
+ * (chart/x86.rs:175-449; AVX-VNNI vpdpbusd where the host has it, else AVX2 vpmaddubsw/vpmaddwd,
+ * chosen at run time as dot32_lanes does, x86.rs:175-205) and one i128 fold
+ * acc += S_b * (w_scale*dot - w_min*xsum) (RowAcc::emit, chart/mod.rs:501-514); Q8_0, Q5_0 and Q4_K
+ * rows go two at a time, sharing each block's activation loads (tiled2, x86.rs:782-1192); the row
+ * ends with round_shift_32 and the i64 range check (chart/mod.rs:1739-1753).  Rows are split into
+ * contiguous chunks over a thread pool (chart/ffn.rs:667-727); the GEMM form decodes each pair of
+ * rows once and dots them against every token column (chart/kcols.rs k-column form).  The cores
+ * live in ah_cpu_rows.inc, compiled once per dot form.
  * When the call-level fast bound (chart/mod.rs:336-383) fails, or a weight scale is
  * non-finite, the call falls back to the exact contract, as the reference does
  * (chart/mod.rs:1847-1854), so the values are always aho_matvec_q8act's.
  */
 #include "ah_oracle.h"
 
+#include <cpuid.h>
 #include <immintrin.h>
 #include <omp.h>
 #include <stdlib.h>
@@ -37,19 +39,7 @@ static inline int64_t f16_fixed_or_marker(uint16_t h) {
     return aho_f16_to_fixed(h, &v) ? 1 : v;
 }
 
-/* ---- exact 32-lane dots -------------------------------------------------------------- */
-
-__attribute__((target("avx2"))) static inline __m256i dot_i8_avx2(__m256i w, __m256i x) {
-    /* |w| as u8 times x*sign(w): maddubs pairs stay below 2*128*127 = 32512 (no saturation). */
-    const __m256i ones = _mm256_set1_epi16(1);
-    __m256i p = _mm256_maddubs_epi16(_mm256_sign_epi8(w, w), _mm256_sign_epi8(x, w));
-    return _mm256_madd_epi16(p, ones);
-}
-
-__attribute__((target("avx2"))) static inline __m256i dot_u8_avx2(__m256i u, __m256i x) {
-    const __m256i ones = _mm256_set1_epi16(1);
-    return _mm256_madd_epi16(_mm256_maddubs_epi16(u, x), ones);
-}
+/* ---- lane sums ---------------------------------------------------------------------- */
 
 __attribute__((target("avx2"))) static inline int32_t hsum8(__m256i v) {
     __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
@@ -184,23 +174,6 @@ static inline int finish(i128 acc, int64_t *y) {
     return AHO_OK;
 }
 
-/* Exact row accumulator over decoded groups against one token's padded codes. */
-__attribute__((target("avx2"))) static i128 row_acc_avx2(const int8_t *wc, const grp_coef *cf,
-                                                         size_t nb32, const int8_t *xc,
-                                                         const int64_t *sc, const int32_t *xs) {
-    i128 acc = 0;
-    for (size_t b = 0; b < nb32; b++) {
-        __m256i w = _mm256_loadu_si256((const __m256i *)(wc + 32 * b));
-        __m256i x = _mm256_loadu_si256((const __m256i *)(xc + 32 * b));
-        __m256i p = dot_i8_avx2(w, x);
-        int32_t lo, hi;
-        hsum_halves(p, &lo, &hi);
-        i128 inner = (i128)cf[b].clo * lo + (i128)cf[b].chi * hi - (i128)cf[b].cmin * xs[b];
-        acc += (i128)sc[b] * inner;
-    }
-    return acc;
-}
-
 static i128 row_acc_portable(const int8_t *wc, const grp_coef *cf, size_t nb32,
                              const int8_t *xc, const int64_t *sc, const int32_t *xs) {
     i128 acc = 0;
@@ -212,106 +185,6 @@ static i128 row_acc_portable(const int8_t *wc, const grp_coef *cf, size_t nb32,
         acc += (i128)sc[b] * inner;
     }
     return acc;
-}
-
-/* Direct Q8_0 fast row from the GGUF bytes (no decode pass): the memory-bound decode path. */
-__attribute__((target("avx2"))) static int q8_0_row_direct(const uint8_t *row, size_t nb32,
-                                                           const int8_t *xc, const int64_t *sc,
-                                                           i128 *out) {
-    i128 acc = 0;
-    int64_t bad = 0;
-    for (size_t b = 0; b < nb32; b++) {
-        const uint8_t *blk = row + 34 * b;
-        int64_t d = f16_fixed_or_marker(rd16(blk));
-        bad |= d;
-        __m256i w = _mm256_loadu_si256((const __m256i *)(blk + 2));
-        __m256i x = _mm256_loadu_si256((const __m256i *)(xc + 32 * b));
-        int32_t D = hsum8(dot_i8_avx2(w, x));
-        acc += (i128)sc[b] * ((i128)d * D);
-    }
-    *out = acc;
-    return (bad & 1) != 0;
-}
-
-/* Direct Q4_K fast row: nibble unpack in registers, chart/x86.rs:386-435 shape. */
-__attribute__((target("avx2"))) static int q4_k_row_direct(const uint8_t *row, size_t nb32,
-                                                           const int8_t *xc, const int64_t *sc,
-                                                           const int32_t *xs, i128 *out) {
-    i128 acc = 0;
-    int64_t bad = 0;
-    const __m256i m4 = _mm256_set1_epi8(0x0F);
-    size_t nsb = (nb32 + 7) / 8;
-    for (size_t s = 0; s < nsb; s++) {
-        const uint8_t *blk = row + 144 * s;
-        int64_t d = f16_fixed_or_marker(rd16(blk)), dm = f16_fixed_or_marker(rd16(blk + 2));
-        bad |= d | dm;
-        const uint8_t *scb = blk + 4;
-        for (int p = 0; p < 4; p++) {
-            size_t g = s * 8 + 2 * p;
-            if (g >= nb32) break;
-            __m256i q = _mm256_loadu_si256((const __m256i *)(blk + 16 + 32 * p));
-            __m256i lo = _mm256_and_si256(q, m4), hi = _mm256_and_si256(_mm256_srli_epi16(q, 4), m4);
-            int32_t Dl = hsum8(dot_u8_avx2(lo, _mm256_loadu_si256((const __m256i *)(xc + 32 * g))));
-            int32_t Dh = hsum8(dot_u8_avx2(hi, _mm256_loadu_si256((const __m256i *)(xc + 32 * g + 32))));
-            for (int h = 0; h < 2; h++) {
-                int j = 2 * p + h, scv, mv;
-                if (j < 4) {
-                    scv = scb[j] & 63;
-                    mv = scb[j + 4] & 63;
-                } else {
-                    scv = (scb[j + 4] & 0xF) | ((scb[j - 4] >> 6) << 4);
-                    mv = (scb[j + 4] >> 4) | ((scb[j] >> 6) << 4);
-                }
-                if (g + h >= nb32) break;
-                i128 inner = (i128)(d * scv) * (h ? Dh : Dl) - (i128)(dm * mv) * xs[g + h];
-                acc += (i128)sc[g + h] * inner;
-            }
-        }
-    }
-    *out = acc;
-    return (bad & 1) != 0;
-}
-
-/* Direct Q6_K fast row: 4+2-bit plane assembly in registers, chart/x86.rs:700-762 shape. */
-__attribute__((target("avx2"))) static int q6_k_row_direct(const uint8_t *row, size_t nb32,
-                                                           const int8_t *xc, const int64_t *sc,
-                                                           const int32_t *xs16, i128 *out) {
-    i128 acc = 0;
-    int64_t bad = 0;
-    const __m256i m4 = _mm256_set1_epi8(0x0F), m2 = _mm256_set1_epi8(0x03);
-    size_t nsb = (nb32 + 7) / 8;
-    for (size_t s = 0; s < nsb; s++) {
-        const uint8_t *blk = row + 210 * s;
-        int64_t d = f16_fixed_or_marker(rd16(blk + 208));
-        bad |= d;
-        for (int n = 0; n < 2; n++) {
-            __m256i l0 = _mm256_loadu_si256((const __m256i *)(blk + 64 * n));
-            __m256i l1 = _mm256_loadu_si256((const __m256i *)(blk + 64 * n + 32));
-            __m256i h = _mm256_loadu_si256((const __m256i *)(blk + 128 + 32 * n));
-            __m256i u[4];
-            u[0] = _mm256_or_si256(_mm256_and_si256(l0, m4), _mm256_slli_epi16(_mm256_and_si256(h, m2), 4));
-            u[1] = _mm256_or_si256(_mm256_and_si256(l1, m4),
-                                   _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(h, 2), m2), 4));
-            u[2] = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(l0, 4), m4),
-                                   _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(h, 4), m2), 4));
-            u[3] = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(l1, 4), m4),
-                                   _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(h, 6), m2), 4));
-            for (int tq = 0; tq < 4; tq++) {
-                size_t g = s * 8 + 4 * n + tq;
-                if (g >= nb32) break;
-                __m256i x = _mm256_loadu_si256((const __m256i *)(xc + 32 * g));
-                int32_t lo, hi;
-                hsum_halves(dot_u8_avx2(u[tq], x), &lo, &hi);
-                lo -= 32 * xs16[2 * g];
-                hi -= 32 * xs16[2 * g + 1];
-                const uint8_t *scb = blk + 192 + 8 * n + 2 * tq;
-                i128 inner = (i128)(d * (int64_t)(int8_t)scb[0]) * lo + (i128)(d * (int64_t)(int8_t)scb[1]) * hi;
-                acc += (i128)sc[g] * inner;
-            }
-        }
-    }
-    *out = acc;
-    return (bad & 1) != 0;
 }
 
 /* Shared per-token activation data: codes padded to whole super-blocks, per-32 and per-16 sums. */
@@ -342,6 +215,53 @@ static void free_act(padded_act *pa) {
     free(pa->xs16);
 }
 
+/* Q4_K sub-block scale and min of sub-block j from the 12 packed bytes (format/quant.rs:200-213). */
+static inline void q4k_sc_m(const uint8_t *scb, int j, int *scv, int *mv) {
+    if (j < 4) {
+        *scv = scb[j] & 63;
+        *mv = scb[j + 4] & 63;
+    } else {
+        *scv = (scb[j + 4] & 0xF) | ((scb[j - 4] >> 6) << 4);
+        *mv = (scb[j + 4] >> 4) | ((scb[j] >> 6) << 4);
+    }
+}
+
+/* ---- the x86 cores, once per dot form -------------------------------------------------- */
+
+#define RK_VNNI 0
+#define RK_ATTR __attribute__((target("avx2")))
+#define RK(name) name##_avx2
+#include "ah_cpu_rows.inc"
+#undef RK_VNNI
+#undef RK_ATTR
+#undef RK
+
+#define RK_VNNI 1
+#define RK_ATTR __attribute__((target("avx2,avxvnni")))
+#define RK(name) name##_vnni
+#include "ah_cpu_rows.inc"
+#undef RK_VNNI
+#undef RK_ATTR
+#undef RK
+
+/* The host's cores: AVX-VNNI is CPUID leaf 7, sub-leaf 1, EAX bit 4 (on top of AVX2). */
+static int host_path(void) {
+    if (!aho_has_avx2()) return AHO_CPU_PORTABLE;
+    unsigned a, b, c, d;
+    if (__get_cpuid_count(7, 1, &a, &b, &c, &d) && (a & (1u << 4))) return AHO_CPU_VNNI;
+    return AHO_CPU_AVX2;
+}
+
+static int forced_path = -1;
+
+int aho_set_cpu_path(int path) {
+    int host = host_path();
+    forced_path = path < 0 ? -1 : path > host ? host : path;
+    return aho_cpu_path();
+}
+
+int aho_cpu_path(void) { return forced_path >= 0 ? forced_path : host_path(); }
+
 int aho_matvec_q8act_fast(uint32_t t, const uint8_t *raw, size_t raw_len, size_t n_out,
                           size_t n_in, const int8_t *codes, const int64_t *scales, int64_t *y,
                           int n_threads) {
@@ -362,7 +282,7 @@ int aho_matvec_q8act_fast(uint32_t t, const uint8_t *raw, size_t raw_len, size_t
         free_act(&pa);
         return AHO_ERR_LENGTH_OVERFLOW;
     }
-    int avx2 = aho_has_avx2();
+    const int path = aho_cpu_path();
     if (n_threads < 1) n_threads = 1;
     /* tasks = max(chunks, 2*width) contiguous row chunks (chart/ffn.rs:705-706). */
     size_t tasks = (size_t)(2 * n_threads);
@@ -372,32 +292,21 @@ int aho_matvec_q8act_fast(uint32_t t, const uint8_t *raw, size_t raw_len, size_t
 #pragma omp parallel for schedule(static) num_threads(n_threads) reduction(| : nonfinite, overflow)
     for (size_t task = 0; task < tasks; task++) {
         size_t lo = task * per, hi = lo + per < n_out ? lo + per : n_out;
-        int8_t *wc = NULL;
-        grp_coef *cf = NULL;
-        if (!avx2 || t == AHO_Q5_0) {
-            wc = (int8_t *)malloc(nb32 * 32 + 32);
-            cf = (grp_coef *)malloc((nb32 + 8) * sizeof(grp_coef));
-        }
-        for (size_t r = lo; r < hi; r++) {
-            const uint8_t *row = raw + r * row_bytes;
-            i128 acc = 0;
-            int bad;
-            if (avx2 && t == AHO_Q5_0) {  /* decoded row, then the shared AVX2 accumulator */
-                bad = decode_row(t, row, nb32, wc, cf);
-                if (!bad) acc = row_acc_avx2(wc, cf, nb32, pa.codes, scales, pa.xs32);
-            } else if (avx2) {
-                if (t == AHO_Q8_0) bad = q8_0_row_direct(row, nb32, pa.codes, scales, &acc);
-                else if (t == AHO_Q4_K) bad = q4_k_row_direct(row, nb32, pa.codes, scales, pa.xs32, &acc);
-                else bad = q6_k_row_direct(row, nb32, pa.codes, scales, pa.xs16, &acc);
-            } else {
-                bad = decode_row(t, row, nb32, wc, cf);
-                if (!bad) acc = row_acc_portable(wc, cf, nb32, pa.codes, scales, pa.xs32);
+        /* two decode buffers (rows r and r + 1) for the decoded forms */
+        int8_t *wc = (int8_t *)malloc(2 * (nb32 * 32 + 32));
+        grp_coef *cf = (grp_coef *)malloc(2 * (nb32 + 8) * sizeof(grp_coef));
+        if (path == AHO_CPU_VNNI) {
+            rows_task_vnni(t, raw, row_bytes, lo, hi, nb32, &pa, scales, wc, cf, y, &nonfinite, &overflow);
+        } else if (path == AHO_CPU_AVX2) {
+            rows_task_avx2(t, raw, row_bytes, lo, hi, nb32, &pa, scales, wc, cf, y, &nonfinite, &overflow);
+        } else {
+            for (size_t r = lo; r < hi; r++) {
+                if (decode_row(t, raw + r * row_bytes, nb32, wc, cf)) {
+                    nonfinite = 1;
+                    break;
+                }
+                if (finish(row_acc_portable(wc, cf, nb32, pa.codes, scales, pa.xs32), &y[r])) overflow = 1;
             }
-            if (bad) {
-                nonfinite = 1;
-                break;
-            }
-            if (finish(acc, &y[r])) overflow = 1;
         }
         free(wc);
         free(cf);
@@ -437,25 +346,36 @@ int aho_matmat_q8act_fast(uint32_t t, const uint8_t *raw, size_t raw_len, size_t
         if (!fast_bound_ok(t, n_in, ss, nb32)) slow[c] = 1;
         if (pad_act(cc, n_in, nb32, &pas[c])) ret = AHO_ERR_LENGTH_OVERFLOW;
     }
-    int avx2 = aho_has_avx2();
+    const int path = aho_cpu_path();
     int nonfinite = 0, overflow = 0;
     if (ret == AHO_OK) {
         if (n_threads < 1) n_threads = 1;
+        const size_t pairs = (n_out + 1) / 2;
 #pragma omp parallel num_threads(n_threads) reduction(| : nonfinite, overflow)
         {
-            int8_t *wc = (int8_t *)malloc(nb32 * 32 + 32);
-            grp_coef *cf = (grp_coef *)malloc((nb32 + 8) * sizeof(grp_coef));
+            int8_t *wc = (int8_t *)malloc(2 * (nb32 * 32 + 32));
+            grp_coef *cf = (grp_coef *)malloc(2 * (nb32 + 8) * sizeof(grp_coef));
 #pragma omp for schedule(static)
-            for (size_t r = 0; r < n_out; r++) {
-                if (decode_row(t, raw + r * row_bytes, nb32, wc, cf)) {
-                    nonfinite = 1;
-                    continue;
-                }
-                for (size_t c = 0; c < n_tok; c++) {
-                    if (slow[c]) continue;
-                    i128 acc = avx2 ? row_acc_avx2(wc, cf, nb32, pas[c].codes, scales + c * nb32, pas[c].xs32)
-                                    : row_acc_portable(wc, cf, nb32, pas[c].codes, scales + c * nb32, pas[c].xs32);
-                    if (finish(acc, &y[c * n_out + r])) overflow = 1;
+            for (size_t p = 0; p < pairs; p++) {
+                const size_t r0 = 2 * p, r1 = r0 + 2 < n_out ? r0 + 2 : n_out;
+                if (path == AHO_CPU_VNNI) {
+                    gemm_rows_vnni(t, raw, row_bytes, r0, r1, nb32, n_out, n_tok, pas, slow, scales, wc, cf, y,
+                                   &nonfinite, &overflow);
+                } else if (path == AHO_CPU_AVX2) {
+                    gemm_rows_avx2(t, raw, row_bytes, r0, r1, nb32, n_out, n_tok, pas, slow, scales, wc, cf, y,
+                                   &nonfinite, &overflow);
+                } else {
+                    for (size_t r = r0; r < r1; r++) {
+                        if (decode_row(t, raw + r * row_bytes, nb32, wc, cf)) {
+                            nonfinite = 1;
+                            continue;
+                        }
+                        for (size_t c = 0; c < n_tok; c++) {
+                            if (slow[c]) continue;
+                            i128 acc = row_acc_portable(wc, cf, nb32, pas[c].codes, scales + c * nb32, pas[c].xs32);
+                            if (finish(acc, &y[c * n_out + r])) overflow = 1;
+                        }
+                    }
                 }
             }
             free(wc);

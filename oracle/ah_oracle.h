@@ -104,11 +104,11 @@ int aho_row_absdot(uint32_t ggml_type, const uint8_t *raw, size_t raw_len, size_
                    size_t n_in, const int8_t *codes, const int64_t *scales, double *out);
 
 /* The reference's fast CPU path restated for host timing: chart row kernels (block dot +
- * i128 fold, chart/mod.rs:501-514, x86.rs cores) one row at a time over contiguous row chunks on
- * a thread pool (chart/ffn.rs:667-727), with AVX2 maddubs dots.  Not restated: the reference's
- * two-row tiling (x86.rs:782-1192) and its AVX-VNNI dispatch (x86.rs:74-85), so this baseline is
- * a lower bound on the reference's own CPU rate.  Bit-equal to aho_matvec_q8act; falls back to
- * it when the fast bound (chart/mod.rs:336-383) fails. */
+ * i128 fold, chart/mod.rs:501-514, x86.rs cores) over contiguous row chunks on a thread pool
+ * (chart/ffn.rs:667-727); Q8_0, Q5_0 and Q4_K rows two at a time (tiled2, x86.rs:782-1192), the
+ * 32-lane dots on AVX-VNNI vpdpbusd where the host has it, else AVX2 vpmaddubsw/vpmaddwd
+ * (x86.rs:74-85, 175-205).  Bit-equal to aho_matvec_q8act; falls back to it when the fast bound
+ * (chart/mod.rs:336-383) fails. */
 int aho_matvec_q8act_fast(uint32_t ggml_type, const uint8_t *raw, size_t raw_len, size_t n_out,
                           size_t n_in, const int8_t *codes, const int64_t *scales, int64_t *y,
                           int n_threads);
@@ -133,6 +133,16 @@ int aho_swiglu_quant_f32(const float *gate, const float *up, size_t n, int8_t *c
 
 /* 1 when the host has AVX2 (the fast cores), else 0 (portable loops are used). */
 int aho_has_avx2(void);
+
+/* The cores the fast path runs: portable loops, AVX2 dots, or AVX-VNNI dots. */
+#define AHO_CPU_PORTABLE 0
+#define AHO_CPU_AVX2 1
+#define AHO_CPU_VNNI 2
+/* The path in use: the host's best unless forced. */
+int aho_cpu_path(void);
+/* Forces a path (clamped to what the host has; negative: the host's best) and returns the path
+ * now in use (tests run every form the host offers). */
+int aho_set_cpu_path(int path);
 
 #ifdef __cplusplus
 }

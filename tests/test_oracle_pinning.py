@@ -244,7 +244,7 @@ def test_extreme_scales_and_codes(t):
     assert oracle.matvec_q8act_fast(t, raw, 2, 256, codes, scales, 1)[1].tolist() == want
 
 
-def test_q8_0_scale_sets_and_spread():
+def test_q8_0_scale_sets_and_spread(cpu_path):
     # kern/gemm.rs:2613-2617 scale-word sets (subnormal, negative, zero, largest) and wide
     # activation spreads (kern/gemm.rs:2490-2506).
     sets = [[0x2000, 0x2400, 0x1C00, 0xA000], [0x0001, 0x03FF, 0x0400, 0x8200],
@@ -274,8 +274,9 @@ def test_q8_0_scale_sets_and_spread():
             assert stf == 0 and yf.tolist() == want
 
 
-def test_nonfinite_scale_refuses():
-    # kern/gemm.rs:2756-2763: an f16 +inf scale refuses (NonFiniteScale), also on the fast path.
+def test_nonfinite_scale_refuses(cpu_path):
+    # kern/gemm.rs:2756-2763: an f16 +inf scale refuses (NonFiniteScale), also on the fast path
+    # (every core form: the bad scale sits in the second row, i.e. in a two-row tile).
     rng = np.random.default_rng(1)
     for t in (8, 12, 14):
         raw = synth.random_bytes_payload(rng, t, 3, 256, 0x3800, 0x3800)
@@ -301,7 +302,7 @@ def test_zero_activation_blocks():
         assert oracle.matvec_q8act(t, raw, 1, 96, codes, scales)[1].tolist() == want
 
 
-def test_matmat_fast_equals_per_column_contract():
+def test_matmat_fast_equals_per_column_contract(cpu_path):
     # kern/matmat.rs:973-1149 shape: every column equals the per-column contract.
     rng = np.random.default_rng(21)
     for t, n_out, n_in in [(8, 17, 64), (12, 9, 512), (14, 7, 256), (12, 5, 896), (8, 3, 96), (6, 11, 96),
@@ -351,3 +352,47 @@ def test_synth_generators_roundtrip():
         blk[208:210] = [0x00, 0x3C]
         w = oracle.dequant_row(14, blk, 256)[1]
         assert (w // ONE + 32).tolist() == u[i].tolist()
+
+
+@pytest.fixture(params=[oracle.CPU_PORTABLE, oracle.CPU_AVX2, oracle.CPU_VNNI], ids=["portable", "avx2", "vnni"])
+def cpu_path(request):
+    """Each core form of the fast CPU path the host offers (skipped where the host lacks it)."""
+    got = oracle.set_cpu_path(request.param)
+    try:
+        if got != request.param:
+            pytest.skip("the host lacks this core form")
+        yield got
+    finally:
+        oracle.set_cpu_path(-1)
+
+
+@pytest.mark.parametrize("t", [6, 8, 12, 14])
+def test_fast_cores_equal_contract(t, cpu_path):
+    """Every core form (portable, AVX2 maddubs, AVX-VNNI vpdpbusd; rows one at a time or in the
+    two-row tiles of x86.rs:782-1192) equals the exact contract, on odd and even row counts (a
+    trailing single row after the pairs), ragged K, zero blocks and the reference's extreme scales,
+    for the GEMV and for every column of the GEMM."""
+    rng = np.random.default_rng(0xC0DE + t)
+    for n_out, n_in in [(1, 256), (2, 96), (7, 512), (8, 896), (5, 300), (9, 1536)]:
+        raw = synth.random_bytes_payload(rng, t, n_out, n_in, 0x3800, 0x2400)
+        if t in (6, 8):  # the reference's scale words, including the largest and subnormal ones
+            bb = 34 if t == 8 else 22
+            words = rng.choice([0x0001, 0x03FF, 0x7BFF, 0x3C00, 0x0000, 0x8200], size=len(raw) // bb)
+            blocks = raw.reshape(-1, bb)
+            blocks[:, 0], blocks[:, 1] = words & 0xFF, words >> 8
+        x = synth.activations(rng, n_in, 5)
+        x[1, : min(64, n_in)] = 0.0  # zero blocks
+        st, codes, scales = oracle.quant_act_f32_batch(x)
+        assert st == 0
+        want = []
+        for c in range(5):
+            stc, yc = oracle.matvec_q8act(t, raw, n_out, n_in, codes[c], scales[c])
+            want.append((stc, yc.tolist()))
+            stf, yf = oracle.matvec_q8act_fast(t, raw, n_out, n_in, codes[c], scales[c], 3)
+            assert stf == stc, (t, n_out, n_in, c)
+            if stc == 0:
+                assert yf.tolist() == yc.tolist(), (t, n_out, n_in, c)
+        if all(w[0] == 0 for w in want):
+            st, y = oracle.matmat_q8act_fast(t, raw, n_out, n_in, codes, scales, 3)
+            assert st == 0
+            assert [y[c].tolist() for c in range(5)] == [w[1] for w in want], (t, n_out, n_in)

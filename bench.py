@@ -538,13 +538,18 @@ def main() -> int:
                 x = synth.activations(synth.rng_for(3, 5), n_in, k).reshape(k, n_in)
                 st, codes, scales = oracle.quant_act_f32_batch(x)
                 threads = max(1, min(args.cpu_threads, os.cpu_count() or 1))
-                oracle.matmat_q8act_fast(gt, raw, n_out, n_in, codes[:2], scales[:2], threads)
-                t0 = time.perf_counter()
-                oracle.matmat_q8act_fast(gt, raw, n_out, n_in, codes, scales, threads)
-                el = time.perf_counter() - t0
+                oracle.matmat_q8act_fast(gt, raw, n_out, n_in, codes[:2], scales[:2], threads)  # warm-up
+                reps = []
+                for _ in range(5):  # median of 5 timed calls
+                    t0 = time.perf_counter()
+                    oracle.matmat_q8act_fast(gt, raw, n_out, n_in, codes, scales, threads)
+                    reps.append(time.perf_counter() - t0)
+                el = sorted(reps)[2]
                 gops = 2.0 * k * n_out * n_in / el / 1e9
                 cg.append({"type": synth.NAMES[gt], "shape": [n_out, n_in], "columns": k, "threads": threads,
                            "seconds": round(el, 3), "gops": round(gops, 1),
+                           "route": "per-column matvec (K % 256 != 0)" if gt == synth.Q4_K and n_in % 256
+                                    else "k-column",
                            "cores_form": ("portable", "avx2", "avx_vnni")[oracle.cpu_path()]})
         result["cpu_baseline_gemm"] = cg
         log(f"[bench] cpu gemm baseline: {[c['gops'] for c in cg]} GOPS")

@@ -326,6 +326,17 @@ int aho_matmat_q8act_fast(uint32_t t, const uint8_t *raw, size_t raw_len, size_t
     if (raw_len < n_out * row_bytes) return AHO_ERR_SHORT_PAYLOAD;
     size_t nb32 = (n_in + 31) / 32;
     if (n_tok == 0 || n_out == 0) return AHO_OK;
+    /* matmat_q8act routing (kern/matmat.rs:140-180): the K-quant k-column kernels admit only
+     * whole super-blocks (K % 256 == 0, chart/kcols.rs:1399-1518); other K-quant widths take the
+     * per-column matvec_q8act path (matmat.rs:392-413), one projection per token column, in order. */
+    if ((t == AHO_Q4_K || t == AHO_Q6_K) && n_in % 256 != 0) {
+        for (size_t c = 0; c < n_tok; c++) {
+            int st = aho_matvec_q8act_fast(t, raw, raw_len, n_out, n_in, codes + c * n_in, scales + c * nb32,
+                                           y + c * n_out, n_threads);
+            if (st) return st;
+        }
+        return AHO_OK;
+    }
     /* Per-token admission: a token whose bound fails (or that does not dequantize) takes the
      * per-column contract, as kern/matmat.rs falls back per call. */
     padded_act *pas = (padded_act *)calloc(n_tok, sizeof(padded_act));

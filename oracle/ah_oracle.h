@@ -113,8 +113,10 @@ int aho_matvec_q8act_fast(uint32_t ggml_type, const uint8_t *raw, size_t raw_len
                           size_t n_in, const int8_t *codes, const int64_t *scales, int64_t *y,
                           int n_threads);
 /* kern/matmat.rs:134 semantics: column c of y (n_tok x n_out, token-major) equals
- * aho_matvec_q8act on token c.  Rows are tiled over threads; each row's blocks are decoded
- * once and dotted against every column (the k-column form of chart/kcols.rs). */
+ * aho_matvec_q8act on token c.  Routing as matmat_q8act's (matmat.rs:140-180): Q4_K / Q6_K widths
+ * that are not whole super-blocks run one aho_matvec_q8act_fast per column (the per-column path,
+ * matmat.rs:392-413); otherwise row pairs are tiled over threads, each pair's blocks decoded once
+ * and dotted against every column (the k-column form of chart/kcols.rs). */
 int aho_matmat_q8act_fast(uint32_t ggml_type, const uint8_t *raw, size_t raw_len, size_t n_out,
                           size_t n_in, size_t n_tok, const int8_t *codes, const int64_t *scales,
                           int64_t *y, int n_threads);

@@ -193,6 +193,24 @@ def gemm_group_q8_dev(dev: "Device", tensors: list["Tensor"], codes_ptr: int, sc
            "gemm_group_q8")
 
 
+def ffn_gate_up_dev(dev: "Device", gate: "Tensor", up: "Tensor", x_ptr: int, h_codes_ptr: int,
+                    h_scales_ptr: int, gate_y_ptr: int | None = None, up_y_ptr: int | None = None,
+                    stream: int | None = None) -> None:
+    """The fused FFN's gate/up launch with the SwiGLU + hidden requantize epilogue
+    (ah_ffn_gate_up_dev): the hidden QuantAct ffn_q8act_prepared_into (chart/ffn.rs:1609) feeds
+    its down projection."""
+    _check(dev.lib.ah_ffn_gate_up_dev(dev.h, gate.h, up.h, x_ptr, gate_y_ptr, up_y_ptr, h_codes_ptr,
+                                      h_scales_ptr, stream), "ffn_gate_up")
+
+
+def ffn_dev(dev: "Device", gate: "Tensor", up: "Tensor", down: "Tensor", x_ptr: int, y_ptr: int,
+            h_codes_ptr: int, h_scales_ptr: int, stream: int | None = None) -> None:
+    """The fused FFN, ffn_q8act_prepared_into (chart/ffn.rs:1609): y = down . quant_act(SwiGLU(gate . x,
+    up . x)) in two launches (ah_ffn_dev)."""
+    _check(dev.lib.ah_ffn_dev(dev.h, gate.h, up.h, down.h, x_ptr, y_ptr, h_codes_ptr, h_scales_ptr, stream),
+           "ffn")
+
+
 class GemvPlan:
     """A grouped GEMV launch over fixed device pointers (ah_gemv_plan_*)."""
 

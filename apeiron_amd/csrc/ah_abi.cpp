@@ -31,6 +31,8 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const StreamParts &sp, const Gem
                                  const StreamWG *d_wgd, uint32_t grid, uint32_t act_bytes,
                                  unsigned long long *status, hipStream_t stream);
 hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream);
+hipError_t ah_launch_ffn_gate_up(uint32_t type, const StreamParts &sp, const FfnArgs &fa, uint32_t grid,
+                                 uint32_t act_bytes, unsigned long long *status, hipStream_t stream);
 int ah_gemv_seq_occupancy(uint32_t type, size_t act_bytes);
 hipError_t ah_launch_gemv_seq(uint32_t type, const SeqArgs &a, uint32_t grid, hipStream_t stream);
 hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes, uint32_t off0,
@@ -63,6 +65,9 @@ struct ah_ctx {
     int device = -1;
     uint8_t *noalloc = nullptr;  // this device's copy of `scratch`
     hipStream_t stream = nullptr;
+    // Two status words: [0] every call's refusals; [1] the refusals of a fused FFN's down
+    // projection, reported only when [0] holds none (the reference refuses the FFN at its first
+    // failing step, so a refused hidden activation is never projected).
     unsigned long long *d_status = nullptr;
     int last_hip = 0;
     uint32_t last_bad_bits = 0;  // f16 bits behind the last AH_ERR_NONFINITE_SCALE
@@ -421,7 +426,9 @@ uint32_t deal_waves(const GemvPart *parts, size_t n, uint32_t n_wg, size_t act_b
 }
 
 int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
-                    const int64_t *scales, float *y, int32_t *dots, void *stream) {
+                    const int64_t *scales, float *y, int32_t *dots, void *stream,
+                    unsigned long long *status = nullptr) {
+    if (ctx && !status) status = ctx->d_status;
     if (!ctx || !w || (!x && w->n_in) || (!y && w->n_out)) return AH_ERR_INVALID_ARG;
     if (src == AH_SRC_CODES && !scales && w->n_in) return AH_ERR_INVALID_ARG;
     // the kernels read codes a dword at a time, f32 / Q32.32 values at their natural alignment
@@ -440,16 +447,16 @@ int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     if (grid == 0) return AH_ERR_OUT_OF_MEMORY;
     if (st)
         AH_HIP(ctx, ah_launch_gemv_stream(w->type, sp, nullptr, nullptr, grid, (uint32_t)ah_gemv_act_bytes(kp),
-                                          ctx->d_status, pick(ctx, stream)));
+                                          status, pick(ctx, stream)));
     else
         AH_HIP(ctx, ah_launch_gemv(w->type, P, nullptr, nullptr, grid, kp, ah_gemv_nc(P.row_bytes),
-                                   ctx->d_status, pick(ctx, stream)));
+                                   status, pick(ctx, stream)));
     return AH_OK;
 }
 
 int32_t reset_status(ah_ctx *ctx) {
-    const unsigned long long none = AH_ST_NONE;
-    AH_HIP(ctx, hipMemcpy(ctx->d_status, &none, sizeof(none), hipMemcpyHostToDevice));
+    const unsigned long long none[2] = {AH_ST_NONE, AH_ST_NONE};
+    AH_HIP(ctx, hipMemcpy(ctx->d_status, none, sizeof(none), hipMemcpyHostToDevice));
     return AH_OK;
 }
 
@@ -672,7 +679,7 @@ int32_t ah_init(int32_t device, ah_ctx **out) {
     ctx->device = device;
     ctx->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess ||
-        hipMalloc(&ctx->d_status, sizeof(unsigned long long)) != hipSuccess ||
+        hipMalloc(&ctx->d_status, 2 * sizeof(unsigned long long)) != hipSuccess ||
         ah_gemv_init_attrs() != hipSuccess) {
         delete ctx;
         return AH_ERR_HIP;
@@ -876,6 +883,46 @@ int32_t ah_gemv_q8_dots_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_cod
                             const int64_t *d_scales, float *d_y, int32_t *d_dots, void *stream) {
     if (!d_dots) return AH_ERR_INVALID_ARG;
     return gemv_launch(ctx, w, AH_SRC_CODES, d_codes, d_scales, d_y, d_dots, stream);
+}
+
+int32_t ah_ffn_gate_up_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const float *d_x,
+                           float *d_gate_y, float *d_up_y, int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
+    if (!ctx || !gate || !up || !d_x || !d_h_codes || !d_h_scales) return AH_ERR_INVALID_ARG;
+    if (gate->type != up->type || gate->n_out != up->n_out || gate->n_in != up->n_in || gate->n_in == 0)
+        return AH_ERR_INVALID_ARG;
+    if (reinterpret_cast<uintptr_t>(d_x) % 4 || reinterpret_cast<uintptr_t>(d_h_scales) % 8) return AH_ERR_INVALID_ARG;
+    if (gate->n_out == 0) return AH_OK;
+    if (gate->n_out > 0x7FFFFFE0u) return AH_ERR_INVALID_ARG;
+    StreamParts sp = {};
+    sp.n = 2;
+    bool s0 = false, s1 = false;
+    // whole units (not the latency launches' Q4_K pairs): each wave streams a few whole rows
+    sp.p[0] = make_part(gate, AH_SRC_F32, d_x, nullptr, d_gate_y, nullptr, s0, false);
+    sp.p[1] = make_part(up, AH_SRC_F32, d_x, nullptr, d_up_y, nullptr, s1, false);
+    if (!s0 || !s1) return AH_ERR_INVALID_ARG;  // rows past one streaming tile
+    const uint32_t kp = kpad_of(gate->n_in);
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    // hidden blocks per workgroup: as few as fill the resident grid, at most kFfnMaxBlocks
+    const uint32_t nb = (uint32_t)((gate->n_out + 31) / 32);
+    const uint64_t res = resident_wgs(ctx, gate->type, true, kp);
+    uint32_t per = (uint32_t)((nb + res - 1) / res);
+    per = per < 1 ? 1 : per > kFfnMaxBlocks ? kFfnMaxBlocks : per;
+    FfnArgs fa = {d_h_codes, d_h_scales, (uint32_t)gate->n_out, per};
+    AH_HIP(ctx, ah_launch_ffn_gate_up(gate->type, sp, fa, (nb + per - 1) / per, (uint32_t)ah_gemv_act_bytes(kp),
+                                      ctx->d_status, pick(ctx, stream)));
+    return AH_OK;
+}
+
+int32_t ah_ffn_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                   const float *d_x, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
+    if (!ctx || !down || !d_y) return AH_ERR_INVALID_ARG;
+    if (!gate || down->n_in != gate->n_out || down->n_out != gate->n_in) return AH_ERR_INVALID_ARG;
+    if (reinterpret_cast<uintptr_t>(d_h_codes) % 4) return AH_ERR_INVALID_ARG;
+    int32_t st = ah_ffn_gate_up_dev(ctx, gate, up, d_x, nullptr, nullptr, d_h_codes, d_h_scales, stream);
+    if (st) return st;
+    // the down projection's refusals go to the second status word (reported only when the
+    // gate/up launch refused nothing)
+    return gemv_launch(ctx, down, AH_SRC_CODES, d_h_codes, d_h_scales, d_y, nullptr, stream, ctx->d_status + 1);
 }
 
 int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w,
@@ -1306,12 +1353,12 @@ int32_t ah_sync_status(ah_ctx *ctx, void *stream) {
     if (!ctx) return AH_ERR_INVALID_ARG;
     AH_HIP(ctx, hipSetDevice(ctx->device));
     AH_HIP(ctx, hipStreamSynchronize(pick(ctx, stream)));
-    unsigned long long key = AH_ST_NONE;
-    AH_HIP(ctx, hipMemcpy(&key, ctx->d_status, sizeof(key), hipMemcpyDeviceToHost));
-    if (key == AH_ST_NONE) return AH_OK;
+    unsigned long long keys[2] = {AH_ST_NONE, AH_ST_NONE};
+    AH_HIP(ctx, hipMemcpy(keys, ctx->d_status, sizeof(keys), hipMemcpyDeviceToHost));
+    if (keys[0] == AH_ST_NONE && keys[1] == AH_ST_NONE) return AH_OK;
     int32_t r = reset_status(ctx);
     if (r) return r;
-    return (int32_t)(key & 0xffu);
+    return (int32_t)((keys[0] != AH_ST_NONE ? keys[0] : keys[1]) & 0xffu);
 }
 
 // ---- diagnostics ----

@@ -1000,6 +1000,92 @@ AH_DEV float group_sum(float s, uint32_t G) {
     return s;
 }
 
+// ---- exact SwiGLU (the fused FFN's hidden activation) ------------------------------------------
+
+typedef __int128 i128;
+constexpr int64_t kOneQ32 = (int64_t)1 << 32;
+
+// round(v / 2^32), ties away from zero (numeric/fixed_exp.rs round_div_2p32)
+AH_DEV i128 round_div_2p32(i128 v) {
+    const i128 half = (i128)1 << 31;
+    return v >= 0 ? (v + half) >> 32 : -((-v + half) >> 32);
+}
+// exp(x) in Q32.32 for x in [-16, 21] (numeric/fixed_exp.rs:40-131): k = round(x / ln 2),
+// r = x - k ln 2, the degree-7 Taylor sum of exp(r) by Horner with round_div_2p32, then 2^k.
+AH_DEV int fx_exp(int64_t x, int64_t &out) {
+    if (x < -16 * kOneQ32 || x > 21 * kOneQ32) return AH_ERR_EXP_RANGE;
+    const int64_t k = (int64_t)(((i128)x * 6196328019LL + ((i128)1 << 63)) >> 64);
+    const int64_t r = x - k * 2977044472LL;
+    i128 acc = 852176;
+    acc = round_div_2p32(acc * r) + 5965232;
+    acc = round_div_2p32(acc * r) + 35791394;
+    acc = round_div_2p32(acc * r) + 178956971;
+    acc = round_div_2p32(acc * r) + 715827883;
+    acc = round_div_2p32(acc * r) + 2147483648LL;
+    acc = round_div_2p32(acc * r) + 4294967296LL;
+    acc = round_div_2p32(acc * r) + 4294967296LL;
+    i128 v;
+    if (k >= 0) {
+        if (k >= 64) return AH_ERR_EXP_RANGE;
+        v = acc << k;
+    } else {
+        const int64_t n = -k;
+        if (n >= 64) {
+            out = 0;
+            return 0;
+        }
+        v = (acc + ((i128)1 << (n - 1))) >> n;
+    }
+    if (v > (i128)INT64_MAX || v < (i128)INT64_MIN) return AH_ERR_EXP_RANGE;
+    out = (int64_t)v;
+    return 0;
+}
+// silu(v) = round(|v| * 2^32 / (2^32 + exp(-v))) with v's sign on -21 < v < 16, v above, 0 below
+// (engine/ops/silu.rs:18-60).  The quotient is below 2^37: a double estimate of the i128 division,
+// then exact correction against the remainder (the hardware has no i128 divide).
+AH_DEV int silu_fx(int64_t v, int64_t &out) {
+    if (v >= 16 * kOneQ32) {
+        out = v;
+        return 0;
+    }
+    if (v <= -21 * kOneQ32) {
+        out = 0;
+        return 0;
+    }
+    int64_t e;
+    if (fx_exp(-v, e)) return AH_ERR_EXP_RANGE;
+    if (e > INT64_MAX - kOneQ32) return AH_ERR_FFN_OVERFLOW;
+    const int64_t den = kOneQ32 + e;
+    if (den <= 0) return AH_ERR_ZERO_DENOMINATOR;
+    const uint64_t mag = v < 0 ? 0ull - (uint64_t)v : (uint64_t)v;
+    const i128 n2 = (i128)mag * kOneQ32 + (den >> 1);  // div_round_nearest's num + den / 2
+    const double nd = (double)(uint64_t)(n2 >> 32) * 4294967296.0 + (double)(uint64_t)(n2 & 0xFFFFFFFFu);
+    int64_t q = (int64_t)(nd / (double)den);
+    i128 rem = n2 - (i128)q * den;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (rem < 0) {
+            --q;
+            rem += den;
+        } else if (rem >= den) {
+            ++q;
+            rem -= den;
+        }
+    }
+    out = v < 0 ? -q : q;
+    return 0;
+}
+// h = round_shift_32(silu(gate) * up) (engine/chart/ffn.rs:246-252)
+AH_DEV int swiglu_fx(int64_t g, int64_t u, int64_t &h) {
+    int64_t s;
+    const int st = silu_fx(g, s);
+    if (st) return st;
+    const i128 r = ((i128)s * u + ((i128)1 << 31)) >> 32;
+    if (r > (i128)INT64_MAX || r < (i128)INT64_MIN) return AH_ERR_FFN_OVERFLOW;
+    h = (int64_t)r;
+    return 0;
+}
+
 constexpr uint32_t kSThreads = 512;                // threads of a streaming workgroup
 constexpr uint32_t kSWaves = kSThreads / 64;
 constexpr uint32_t kChunks = 8;                    // 16-byte loads per lane per tile
@@ -1035,17 +1121,106 @@ AH_DEV GemvPart part_at(const GemvPart *__restrict__ parts, uint32_t i) {
 template <int TYPE>
 constexpr int stream_waves_per_simd() { return TYPE == kMixedType ? 2 : 4; }
 
-template <int TYPE, bool PLAN, bool DOTS>
-__global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
+// LDS of the fused FFN's gate/up launch past the tile slots: the gate and up row sums of the
+// workgroup's hidden blocks (f32), then the hidden h of one element per thread (i64).
+constexpr uint32_t kFfnRows = 32 * kFfnMaxBlocks;
+constexpr uint32_t kFfnLdsBytes = 2 * kFfnRows * 4 + kSThreads * 8;
+
+// The fused FFN's epilogue over the workgroup's hidden blocks [b0, b1): each thread takes one
+// element, converts its gate and up row sums to Q32.32 (to_q32) and forms
+// h = round_shift_32(silu_fixed(gate) * up) (engine/ops/ffn.rs:80, chart/ffn.rs:246-252); then a
+// quad of lanes per block quantizes h (quant_act) into the hidden QuantAct.  Refusals keep the
+// reference FFN's order (chart/ffn.rs:1712-1720): the projections' outputs (recorded by the tile
+// loop, gate rows then up rows), then the elements' conversion or SwiGLU refusals, then the
+// quantizer's, each class keyed past the one before.
+AH_DEV void ffn_epilogue(const FfnArgs &fa, uint32_t b0, uint32_t b1, const float *hsum, int64_t *hl,
+                         unsigned long long *status) {
+    ah_lds_barrier();  // every wave's row sums are in LDS
+    const uint32_t n = fa.n_ff, nb = (n + 31) / 32;
+    const uint32_t tid = threadIdx.x, q = tid & 3;
+    const uint32_t j = tid / 32, k = 32 * (b0 + j) + (tid & 31);  // b1 - b0 <= kSThreads / 32
+    int64_t h = 0;
+    if (b0 + j < b1 && k < n) {
+        const uint32_t gb = __builtin_bit_cast(uint32_t, hsum[k - 32 * b0]);
+        const uint32_t ub = __builtin_bit_cast(uint32_t, hsum[kFfnRows + k - 32 * b0]);
+        uint64_t mg, mu;
+        bool ng, nu;
+        int e = ah_to_q32_mag(gb, mg, ng);
+        if (!e) e = ah_to_q32_mag(ub, mu, nu);
+        if (!e) e = swiglu_fx(ng ? (int64_t)(0ull - mg) : (int64_t)mg, nu ? (int64_t)(0ull - mu) : (int64_t)mu, h);
+        if (e) {
+            ah_record(status, ah_out_key(2ull * n + k, (uint32_t)e));
+            h = 0;
+        }
+    }
+    hl[tid] = h;
+    ah_lds_barrier();
+    if (tid < 4 * kFfnMaxBlocks) {
+        const uint32_t jb = tid / 4, b = b0 + jb, k0 = 32 * b + 8 * q;
+        QuadIn in;
+        in.take = b < b1 && n > k0 ? (n - k0 < 8 ? n - k0 : 8) : 0;
+        in.s0 = in.s1 = 0;
+        uint32_t nz = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint64_t v = (uint32_t)i < in.take ? (uint64_t)hl[32 * jb + 8 * q + i] : 0ull;
+            in.w[2 * i] = (uint32_t)v;
+            in.w[2 * i + 1] = (uint32_t)(v >> 32);
+            nz |= in.w[2 * i] | in.w[2 * i + 1];
+        }
+        nz |= quad_xor1(nz);
+        nz |= quad_xor2(nz);
+        // the quantizer's own refusal key would sort before the projections' outputs: a block
+        // it refuses (nonzero, yet no scale) is recorded here, after the SwiGLU class
+        const QuadOut o = quad_quant(in, AH_SRC_Q32, b, nullptr, 0);
+        if (b < b1) {
+            if (q == 0 && nz != 0 && o.e < 0) ah_record(status, ah_out_key(3ull * n + b, 7u));
+            const __amdgpu_buffer_rsrc_t rc = ah_rsrc(fa.h_codes, n), rs = ah_rsrc(fa.h_scales, nb * 8u);
+            if (in.take == 8) {
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, (u32x2){o.c0, o.c1}), rc, k0, 0, 0);
+            } else {
+#pragma unroll
+                for (uint32_t i = 0; i < 8; ++i)
+                    if (i < in.take)
+                        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(((i < 4 ? o.c0 : o.c1) >> (8 * (i & 3))) & 0xffu),
+                                                             rc, k0 + i, 0, 0);
+            }
+            if (q == 0) {
+                const uint64_t S64 = o.e < 0 ? 0ull : (1ull << o.e);
+                __builtin_amdgcn_raw_buffer_store_b64(
+                    __builtin_bit_cast(u32x2, (u32x2){(uint32_t)S64, (uint32_t)(S64 >> 32)}), rs, 8 * b, 0, 0);
+            }
+        }
+    }
+}
+
+// FFN: the fused FFN's gate/up launch (argument parts 0 = gate, 1 = up; FfnArgs): workgroup w
+// serves hidden blocks [w * blocks_per_wg, +blocks_per_wg), waves 0-3 its gate rows and waves 4-7
+// its up rows; the row sums also go to LDS, and the SwiGLU epilogue writes the hidden QuantAct.
+// (The FFN launch has about one workgroup per CU: it is built for 2 waves per SIMD, so its
+// epilogue's i128 arithmetic never spills.)
+template <int TYPE, bool PLAN, bool DOTS, bool FFN = false>
+__global__ void __launch_bounds__(kSThreads, FFN ? 2 : stream_waves_per_simd<TYPE>())
     gemv_stream_kernel(StreamParts sp, const GemvPart *__restrict__ parts,
                        const StreamWG *__restrict__ wgd, uint32_t act_bytes,
-                       unsigned long long *status) {
+                       unsigned long long *status, FfnArgs fa) {
+    static_assert(!FFN || (!PLAN && !DOTS), "the FFN launch takes argument parts");
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
     GemvPart P;
     uint32_t r_begin, r_end, aoff = 0;
-    if constexpr (PLAN) {
+    uint32_t f_b0 = 0, f_b1 = 0;  // FFN: the workgroup's hidden blocks
+    if constexpr (FFN) {
+        P = wv < kSWaves / 2 ? sp.p[0] : sp.p[1];
+        const uint32_t nb = (fa.n_ff + 31) / 32;
+        f_b0 = blockIdx.x * fa.blocks_per_wg;
+        f_b1 = f_b0 + fa.blocks_per_wg < nb ? f_b0 + fa.blocks_per_wg : nb;
+        const uint32_t row0 = 32 * f_b0, rows = (32 * f_b1 < fa.n_ff ? 32 * f_b1 : fa.n_ff) - row0;
+        const uint32_t qw = wv % (kSWaves / 2);
+        r_begin = row0 + rows * qw / (kSWaves / 2);
+        r_end = row0 + rows * (qw + 1) / (kSWaves / 2);
+    } else if constexpr (PLAN) {
         const StreamWG *D = wgd + blockIdx.x;
         const uint32_t pi = D->wave_part[wv];
         const bool idle = pi == kIdleWave;
@@ -1177,7 +1352,8 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
     // Row sums leave through a buffer store that every lane issues (lanes that own no row store
     // out of range, which writes nothing): a store behind a branch would make the compiler wait for
     // its completion before the next tile is staged.
-    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(P.y, P.n_out * 4u);
+    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(P.y, P.y ? P.n_out * 4u : 0u);  // FFN: y optional
+    float *const hsum = reinterpret_cast<float *>(smem + act_bytes + kSWaves * kSlotBytes);
     const uint32_t r = lane / G, g = lane & (G - 1);
     // earliest refused output row of the wave, (row << 1) | (code == 9), kept in a scalar register
     // (a ballot, no memory operation in the loop); recorded once after the last tile
@@ -1218,6 +1394,8 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
         acc = group_sum(acc, G);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), ry,
                                               (g == G - 1 && owns) ? row * 4u : kOob, 0, 0);
+        if constexpr (FFN)
+            if (g == G - 1 && owns) hsum[(wv < kSWaves / 2 ? 0u : kFfnRows) + row - 32 * f_b0] = acc;
         const uint32_t oc = ah_out_code(acc);
         const uint64_t ob = __builtin_amdgcn_ballot_w64(g == G - 1 && owns && oc != 0u);
         if (ob) {  // uniform: lanes own rows in lane order, so the lowest lane is the earliest row
@@ -1227,7 +1405,14 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
         __builtin_amdgcn_wave_barrier();  // all lanes are done reading the slot before it is refilled
         if (t + 1 < n_t) stage(t + 1);    // (past the last tile nothing is staged: no wait for its loads)
     }
-    if (obad != 0xFFFFFFFFu && lane == 0) ah_record(status, ah_out_key(obad >> 1, (obad & 1u) ? 9u : 8u));
+    if constexpr (FFN) {
+        // gate rows keep their index, up rows follow them (the reference projects gate, then up)
+        if (obad != 0xFFFFFFFFu && lane == 0)
+            ah_record(status, ah_out_key((obad >> 1) + (wv < kSWaves / 2 ? 0u : fa.n_ff), (obad & 1u) ? 9u : 8u));
+        ffn_epilogue(fa, f_b0, f_b1, hsum, reinterpret_cast<int64_t *>(hsum + 2 * kFfnRows), status);
+    } else {
+        if (obad != 0xFFFFFFFFu && lane == 0) ah_record(status, ah_out_key(obad >> 1, (obad & 1u) ? 9u : 8u));
+    }
 }
 
 // ---- persistent decode sequence ---------------------------------------------------------------
@@ -1251,90 +1436,6 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
 // bounded (past spin_limit the stage records AH_ERR_SEQ_TIMEOUT and waits no more in this launch).
 // A workgroup's run number is its own device counter, read at start and bumped at the end.  The
 // grid is launched cooperatively, which guarantees that every workgroup is resident.
-
-typedef __int128 i128;
-constexpr int64_t kOneQ32 = (int64_t)1 << 32;
-
-// round(v / 2^32), ties away from zero (numeric/fixed_exp.rs round_div_2p32)
-AH_DEV i128 round_div_2p32(i128 v) {
-    const i128 half = (i128)1 << 31;
-    return v >= 0 ? (v + half) >> 32 : -((-v + half) >> 32);
-}
-// exp(x) in Q32.32 for x in [-16, 21] (numeric/fixed_exp.rs:40-131): k = round(x / ln 2),
-// r = x - k ln 2, the degree-7 Taylor sum of exp(r) by Horner with round_div_2p32, then 2^k.
-AH_DEV int fx_exp(int64_t x, int64_t &out) {
-    if (x < -16 * kOneQ32 || x > 21 * kOneQ32) return AH_ERR_EXP_RANGE;
-    const int64_t k = (int64_t)(((i128)x * 6196328019LL + ((i128)1 << 63)) >> 64);
-    const int64_t r = x - k * 2977044472LL;
-    i128 acc = 852176;
-    acc = round_div_2p32(acc * r) + 5965232;
-    acc = round_div_2p32(acc * r) + 35791394;
-    acc = round_div_2p32(acc * r) + 178956971;
-    acc = round_div_2p32(acc * r) + 715827883;
-    acc = round_div_2p32(acc * r) + 2147483648LL;
-    acc = round_div_2p32(acc * r) + 4294967296LL;
-    acc = round_div_2p32(acc * r) + 4294967296LL;
-    i128 v;
-    if (k >= 0) {
-        if (k >= 64) return AH_ERR_EXP_RANGE;
-        v = acc << k;
-    } else {
-        const int64_t n = -k;
-        if (n >= 64) {
-            out = 0;
-            return 0;
-        }
-        v = (acc + ((i128)1 << (n - 1))) >> n;
-    }
-    if (v > (i128)INT64_MAX || v < (i128)INT64_MIN) return AH_ERR_EXP_RANGE;
-    out = (int64_t)v;
-    return 0;
-}
-// silu(v) = round(|v| * 2^32 / (2^32 + exp(-v))) with v's sign on -21 < v < 16, v above, 0 below
-// (engine/ops/silu.rs:18-60).  The quotient is below 2^37: a double estimate of the i128 division,
-// then exact correction against the remainder (the hardware has no i128 divide).
-AH_DEV int silu_fx(int64_t v, int64_t &out) {
-    if (v >= 16 * kOneQ32) {
-        out = v;
-        return 0;
-    }
-    if (v <= -21 * kOneQ32) {
-        out = 0;
-        return 0;
-    }
-    int64_t e;
-    if (fx_exp(-v, e)) return AH_ERR_EXP_RANGE;
-    if (e > INT64_MAX - kOneQ32) return AH_ERR_FFN_OVERFLOW;
-    const int64_t den = kOneQ32 + e;
-    if (den <= 0) return AH_ERR_ZERO_DENOMINATOR;
-    const uint64_t mag = v < 0 ? 0ull - (uint64_t)v : (uint64_t)v;
-    const i128 n2 = (i128)mag * kOneQ32 + (den >> 1);  // div_round_nearest's num + den / 2
-    const double nd = (double)(uint64_t)(n2 >> 32) * 4294967296.0 + (double)(uint64_t)(n2 & 0xFFFFFFFFu);
-    int64_t q = (int64_t)(nd / (double)den);
-    i128 rem = n2 - (i128)q * den;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (rem < 0) {
-            --q;
-            rem += den;
-        } else if (rem >= den) {
-            ++q;
-            rem -= den;
-        }
-    }
-    out = v < 0 ? -q : q;
-    return 0;
-}
-// h = round_shift_32(silu(gate) * up) (engine/chart/ffn.rs:246-252)
-AH_DEV int swiglu_fx(int64_t g, int64_t u, int64_t &h) {
-    int64_t s;
-    const int st = silu_fx(g, s);
-    if (st) return st;
-    const i128 r = ((i128)s * u + ((i128)1 << 31)) >> 32;
-    if (r > (i128)INT64_MAX || r < (i128)INT64_MIN) return AH_ERR_FFN_OVERFLOW;
-    h = (int64_t)r;
-    return 0;
-}
 
 // The SwiGLU stage: the hidden activation's 32-blocks are dealt to the workgroups, 16 blocks per
 // round (one element per thread): gate and up from f32 to Q32.32 (to_q32), h = swiglu into LDS,
@@ -1703,13 +1804,13 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const StreamParts &sp, const Gem
 #define AH_SLAUNCH(T)                                                                              \
     if (d_parts)                                                                                   \
         hipLaunchKernelGGL((gemv_stream_kernel<T, true, false>), dim3(grid), dim3(kSThreads), lds,  \
-                           stream, sp, d_parts, d_wgd, act_bytes, status);                        \
+                           stream, sp, d_parts, d_wgd, act_bytes, status, FfnArgs{});             \
     else if (sp.p[0].dots)                                                                         \
         hipLaunchKernelGGL((gemv_stream_kernel<T, false, true>), dim3(grid), dim3(kSThreads), lds,  \
-                           stream, sp, d_parts, d_wgd, act_bytes, status);                        \
+                           stream, sp, d_parts, d_wgd, act_bytes, status, FfnArgs{});             \
     else                                                                                           \
         hipLaunchKernelGGL((gemv_stream_kernel<T, false, false>), dim3(grid), dim3(kSThreads), lds, \
-                           stream, sp, d_parts, d_wgd, act_bytes, status);
+                           stream, sp, d_parts, d_wgd, act_bytes, status, FfnArgs{});
     switch (type) {
     case AH_GGML_Q8_0: AH_SLAUNCH(AH_GGML_Q8_0) break;
     case AH_GGML_Q5_0: AH_SLAUNCH(AH_GGML_Q5_0) break;
@@ -1718,14 +1819,53 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const StreamParts &sp, const Gem
     case kMixedType:
         if (d_parts)
             hipLaunchKernelGGL((gemv_stream_kernel<kMixedType, true, false>), dim3(grid), dim3(kSThreads), lds,
-                               stream, sp, d_parts, d_wgd, act_bytes, status);
+                               stream, sp, d_parts, d_wgd, act_bytes, status, FfnArgs{});
         else
             hipLaunchKernelGGL((gemv_stream_kernel<kMixedType, false, false>), dim3(grid), dim3(kSThreads), lds,
-                               stream, sp, d_parts, d_wgd, act_bytes, status);
+                               stream, sp, d_parts, d_wgd, act_bytes, status, FfnArgs{});
         break;
     default: return hipErrorInvalidValue;
     }
 #undef AH_SLAUNCH
+    return hipGetLastError();
+}
+
+// The fused FFN's gate/up launch: one workgroup per `fa.blocks_per_wg` hidden blocks (no
+// residency requirement: workgroups do not wait for one another).
+static const void *ffn_fn(uint32_t type) {
+    switch (type) {
+    case AH_GGML_Q8_0: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q8_0, false, false, true>);
+    case AH_GGML_Q5_0: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q5_0, false, false, true>);
+    case AH_GGML_Q4_K: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q4_K, false, false, true>);
+    case AH_GGML_Q6_K: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q6_K, false, false, true>);
+    default: return nullptr;
+    }
+}
+
+size_t ah_ffn_lds_bytes(uint32_t kpad) { return ah_gemv_stream_lds_bytes(kpad) + kFfnLdsBytes; }
+
+hipError_t ah_launch_ffn_gate_up(uint32_t type, const StreamParts &sp, const FfnArgs &fa, uint32_t grid,
+                                 uint32_t act_bytes, unsigned long long *status, hipStream_t stream) {
+    if (!ffn_fn(type) || fa.blocks_per_wg == 0 || fa.blocks_per_wg > kFfnMaxBlocks) return hipErrorInvalidValue;
+    const size_t lds = act_bytes + ah_gemv_stream_slot_bytes() + kFfnLdsBytes;
+    switch (type) {
+    case AH_GGML_Q8_0:
+        hipLaunchKernelGGL((gemv_stream_kernel<AH_GGML_Q8_0, false, false, true>), dim3(grid), dim3(kSThreads), lds,
+                           stream, sp, nullptr, nullptr, act_bytes, status, fa);
+        break;
+    case AH_GGML_Q5_0:
+        hipLaunchKernelGGL((gemv_stream_kernel<AH_GGML_Q5_0, false, false, true>), dim3(grid), dim3(kSThreads), lds,
+                           stream, sp, nullptr, nullptr, act_bytes, status, fa);
+        break;
+    case AH_GGML_Q4_K:
+        hipLaunchKernelGGL((gemv_stream_kernel<AH_GGML_Q4_K, false, false, true>), dim3(grid), dim3(kSThreads), lds,
+                           stream, sp, nullptr, nullptr, act_bytes, status, fa);
+        break;
+    default:
+        hipLaunchKernelGGL((gemv_stream_kernel<AH_GGML_Q6_K, false, false, true>), dim3(grid), dim3(kSThreads), lds,
+                           stream, sp, nullptr, nullptr, act_bytes, status, fa);
+        break;
+    }
     return hipGetLastError();
 }
 
@@ -1788,6 +1928,8 @@ hipError_t ah_gemv_init_attrs() {
             e = hipFuncSetAttribute(stream_fn(kMixedType, v == 1), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     for (uint32_t t : {(uint32_t)kMixedType, (uint32_t)AH_GGML_Q8_0, (uint32_t)AH_GGML_Q4_K, (uint32_t)AH_GGML_Q6_K})
         if (e == hipSuccess) e = hipFuncSetAttribute(seq_fn(t), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+    for (uint32_t t : {AH_GGML_Q8_0, AH_GGML_Q5_0, AH_GGML_Q4_K, AH_GGML_Q6_K})
+        if (e == hipSuccess) e = hipFuncSetAttribute(ffn_fn(t), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     return e;
 }
 

@@ -204,6 +204,17 @@ struct StreamParts {
     uint32_t n;
 };
 
+// The fused FFN's gate/up launch (ah_ffn_gate_up_dev): gate is argument part 0, up part 1 (same
+// type and shape, same input); workgroup w serves hidden 32-blocks [w * blocks_per_wg, +blocks_per_wg)
+// and writes their SwiGLU, requantized, as the hidden QuantAct.
+constexpr uint32_t kFfnMaxBlocks = 16;  // hidden blocks per workgroup (one element per thread)
+struct FfnArgs {
+    int8_t *h_codes;          // [n_ff]
+    int64_t *h_scales;        // [ceil(n_ff / 32)]
+    uint32_t n_ff;            // gate / up rows
+    uint32_t blocks_per_wg;   // <= kFfnMaxBlocks
+};
+
 // GEMM workgroup forms (waves x LDS ring slots), chosen per launch by ah_gemm_pick_waves.
 // kFormI8x4 / kFormI8x2: the int8-MFMA design (Q8_0), 4 or 2 waves.
 enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2, kFormI8x4 = 3, kFormI8x2 = 4 };

@@ -143,6 +143,28 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
 int32_t ah_gemv_plan_run(ah_ctx *ctx, const ah_gemv_plan *plan, void *stream);
 int32_t ah_gemv_plan_free(ah_ctx *ctx, ah_gemv_plan *plan);
 
+/* Fused FFN (ffn_q8act_prepared_into, chart/ffn.rs:1609; fused_ffn_task, chart/ffn.rs:1532-1594):
+ * h = quant_act(round_shift_32(silu_fixed(to_q32(gate . x)) * to_q32(up . x))) exactly
+ * (ops/ffn.rs:80, ops/silu.rs:18-60, chart/ffn.rs:246-252), then y = down . h.
+ * ah_ffn_gate_up_dev is ONE launch: gate and up rows stream in the same workgroups (waves 0-3
+ * gate, 4-7 up, over 32-row hidden blocks), their row sums meet in LDS and the workgroup's
+ * epilogue writes the hidden QuantAct: d_h_codes[n_ff] (int8) and d_h_scales[ceil(n_ff/32)]
+ * (int64; 8-byte aligned).  gate and up share type and shape (n_ff x n_embd) and take the same
+ * f32 input d_x[n_embd] (4-byte aligned); d_gate_y / d_up_y (optional, NULL to skip) receive
+ * the f32 gate and up values the SwiGLU consumed.  Their rows must fit the streaming kernel's
+ * 8 KB tiles (Q8_0 K <= 7680, Q4_K K <= 14336, Q6_K K <= 9728), else AH_ERR_INVALID_ARG.
+ * ah_ffn_dev adds the down projection (n_embd x n_ff, any type) from that QuantAct (d_h_codes
+ * 4-byte aligned): two launches.  Refusals (ah_sync_status) in the reference FFN's order
+ * (chart/ffn.rs:1712-1720): the input's conversion and quantization, gate then up outputs, the
+ * hidden elements' conversion or SwiGLU (AH_ERR_FFN_OVERFLOW, AH_ERR_EXP_RANGE,
+ * AH_ERR_ZERO_DENOMINATOR), the hidden quantizer's, and only when none of those occurred, the
+ * down projection's. */
+int32_t ah_ffn_gate_up_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const float *d_x,
+                           float *d_gate_y, float *d_up_y, int8_t *d_h_codes, int64_t *d_h_scales,
+                           void *stream);
+int32_t ah_ffn_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                   const float *d_x, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales, void *stream);
+
 /* Persistent decode sequence: a token's chain of projection stages in ONE launch.  Stage s may
  * read outputs of stages before it (q/k/v -> o -> gate/up -> SwiGLU -> down per layer, then the
  * head): every workgroup of a resident grid finishes its share of stage s, then all meet at a

@@ -33,6 +33,7 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const StreamParts &sp, const Gem
 hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream);
 hipError_t ah_launch_ffn_gate_up(uint32_t type, const StreamParts &sp, const FfnArgs &fa, uint32_t grid,
                                  uint32_t act_bytes, unsigned long long *status, hipStream_t stream);
+int ah_ffn_occupancy(uint32_t type, uint32_t kpad);
 int ah_gemv_seq_occupancy(uint32_t type, size_t act_bytes);
 hipError_t ah_launch_gemv_seq(uint32_t type, const SeqArgs &a, uint32_t grid, hipStream_t stream);
 hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes, uint32_t off0,
@@ -902,9 +903,10 @@ int32_t ah_ffn_gate_up_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *
     if (!s0 || !s1) return AH_ERR_INVALID_ARG;  // rows past one streaming tile
     const uint32_t kp = kpad_of(gate->n_in);
     AH_HIP(ctx, hipSetDevice(ctx->device));
-    // hidden blocks per workgroup: as few as fill the resident grid, at most kFfnMaxBlocks
+    // hidden blocks per workgroup: as few as keep the grid resident (one round), at most kFfnMaxBlocks
     const uint32_t nb = (uint32_t)((gate->n_out + 31) / 32);
-    const uint64_t res = resident_wgs(ctx, gate->type, true, kp);
+    const int occ = ah_ffn_occupancy(gate->type, kp);
+    const uint64_t res = (uint64_t)(occ > 0 ? occ : 1) * (uint64_t)ctx->cu_count;
     uint32_t per = (uint32_t)((nb + res - 1) / res);
     per = per < 1 ? 1 : per > kFfnMaxBlocks ? kFfnMaxBlocks : per;
     FfnArgs fa = {d_h_codes, d_h_scales, (uint32_t)gate->n_out, per};

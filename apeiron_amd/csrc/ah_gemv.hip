@@ -256,12 +256,18 @@ AH_DEV QuadOut quad_quant(const QuadIn &in, uint32_t src, uint32_t b, unsigned l
         const int64_t S = (int64_t)(((uint64_t)in.s1 << 32) | in.s0);
         o.fsc = (float)S * 0x1p-32f;
         // QuantAct::dequantizes (chart/mod.rs:128-134): every S * code must be an i64, else the
-        // call refuses with Dequant(FixedOverflow) before it projects
+        // call refuses with Dequant(FixedOverflow) before it projects.  A code is in [-128, 127],
+        // so |S| <= 2^56 can never overflow (127 * 2^56 < 2^63, -128 * 2^56 = -2^63): the per-code
+        // products are checked only in a wave with a larger scale (quantized activations have
+        // S <= 2^57, past 2^56 only for magnitudes near 2^63).
         bool bad = false;
+        const uint64_t mag = S < 0 ? 0ull - (uint64_t)S : (uint64_t)S;
+        if (__builtin_amdgcn_ballot_w64(mag > (1ull << 56)) != 0ull) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            int64_t prod;
-            bad |= __builtin_mul_overflow(S, (int64_t)(int8_t)((((i < 4) ? o.c0 : o.c1) >> (8 * (i & 3))) & 0xffu), &prod);
+            for (int i = 0; i < 8; ++i) {
+                int64_t prod;
+                bad |= __builtin_mul_overflow(S, (int64_t)(int8_t)((((i < 4) ? o.c0 : o.c1) >> (8 * (i & 3))) & 0xffu), &prod);
+            }
         }
         const uint32_t badq = (uint32_t)bad | quad_xor1((uint32_t)bad);
         if ((badq | quad_xor2(badq)) != 0 && q == 0)
@@ -1005,39 +1011,42 @@ AH_DEV float group_sum(float s, uint32_t G) {
 typedef __int128 i128;
 constexpr int64_t kOneQ32 = (int64_t)1 << 32;
 
-// round(v / 2^32), ties away from zero (numeric/fixed_exp.rs round_div_2p32)
-AH_DEV i128 round_div_2p32(i128 v) {
-    const i128 half = (i128)1 << 31;
-    return v >= 0 ? (v + half) >> 32 : -((-v + half) >> 32);
+// round(v / 2^32), ties away from zero, for |v| <= 2^63 - 2^31, branch-free in i64
+AH_DEV int64_t round_div_2p32_i64(int64_t v) {
+    const int64_t s = v >> 63;
+    const uint64_t a = (uint64_t)((v ^ s) - s);
+    const int64_t q = (int64_t)((a + (1ull << 31)) >> 32);
+    return (q ^ s) - s;
 }
 // exp(x) in Q32.32 for x in [-16, 21] (numeric/fixed_exp.rs:40-131): k = round(x / ln 2),
 // r = x - k ln 2, the degree-7 Taylor sum of exp(r) by Horner with round_div_2p32, then 2^k.
+// The reference sums in i128; here in i64, exactly: |r| <= ln 2 / 2 * 2^32 < 2^30.5 and every
+// partial sum lies in (0, e^(ln 2 / 2) * 2^32) < 2^32.6, so each product acc * r stays below
+// 2^63 (the bounds are checked step by step against the oracle in the CPU tests).
 AH_DEV int fx_exp(int64_t x, int64_t &out) {
     if (x < -16 * kOneQ32 || x > 21 * kOneQ32) return AH_ERR_EXP_RANGE;
     const int64_t k = (int64_t)(((i128)x * 6196328019LL + ((i128)1 << 63)) >> 64);
     const int64_t r = x - k * 2977044472LL;
-    i128 acc = 852176;
-    acc = round_div_2p32(acc * r) + 5965232;
-    acc = round_div_2p32(acc * r) + 35791394;
-    acc = round_div_2p32(acc * r) + 178956971;
-    acc = round_div_2p32(acc * r) + 715827883;
-    acc = round_div_2p32(acc * r) + 2147483648LL;
-    acc = round_div_2p32(acc * r) + 4294967296LL;
-    acc = round_div_2p32(acc * r) + 4294967296LL;
-    i128 v;
+    int64_t acc = 852176;
+    acc = round_div_2p32_i64(acc * r) + 5965232;
+    acc = round_div_2p32_i64(acc * r) + 35791394;
+    acc = round_div_2p32_i64(acc * r) + 178956971;
+    acc = round_div_2p32_i64(acc * r) + 715827883;
+    acc = round_div_2p32_i64(acc * r) + 2147483648LL;
+    acc = round_div_2p32_i64(acc * r) + 4294967296LL;
+    acc = round_div_2p32_i64(acc * r) + 4294967296LL;
     if (k >= 0) {
-        if (k >= 64) return AH_ERR_EXP_RANGE;
-        v = acc << k;
-    } else {
-        const int64_t n = -k;
-        if (n >= 64) {
-            out = 0;
-            return 0;
-        }
-        v = (acc + ((i128)1 << (n - 1))) >> n;
+        // acc * 2^k must be an i64 (the reference's range check on the i128 value)
+        if (k >= 63 || acc > (INT64_MAX >> k) || acc < (INT64_MIN >> k)) return AH_ERR_EXP_RANGE;
+        out = acc << k;
+        return 0;
     }
-    if (v > (i128)INT64_MAX || v < (i128)INT64_MIN) return AH_ERR_EXP_RANGE;
-    out = (int64_t)v;
+    const int64_t n = -k;
+    if (n >= 63) {
+        out = 0;
+        return 0;
+    }
+    out = (acc + ((int64_t)1 << (n - 1))) >> n;
     return 0;
 }
 // silu(v) = round(|v| * 2^32 / (2^32 + exp(-v))) with v's sign on -21 < v < 16, v above, 0 below
@@ -1197,10 +1206,8 @@ AH_DEV void ffn_epilogue(const FfnArgs &fa, uint32_t b0, uint32_t b1, const floa
 // FFN: the fused FFN's gate/up launch (argument parts 0 = gate, 1 = up; FfnArgs): workgroup w
 // serves hidden blocks [w * blocks_per_wg, +blocks_per_wg), waves 0-3 its gate rows and waves 4-7
 // its up rows; the row sums also go to LDS, and the SwiGLU epilogue writes the hidden QuantAct.
-// (The FFN launch has about one workgroup per CU: it is built for 2 waves per SIMD, so its
-// epilogue's i128 arithmetic never spills.)
 template <int TYPE, bool PLAN, bool DOTS, bool FFN = false>
-__global__ void __launch_bounds__(kSThreads, FFN ? 2 : stream_waves_per_simd<TYPE>())
+__global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
     gemv_stream_kernel(StreamParts sp, const GemvPart *__restrict__ parts,
                        const StreamWG *__restrict__ wgd, uint32_t act_bytes,
                        unsigned long long *status, FfnArgs fa) {
@@ -1212,7 +1219,9 @@ __global__ void __launch_bounds__(kSThreads, FFN ? 2 : stream_waves_per_simd<TYP
     uint32_t r_begin, r_end, aoff = 0;
     uint32_t f_b0 = 0, f_b1 = 0;  // FFN: the workgroup's hidden blocks
     if constexpr (FFN) {
-        P = wv < kSWaves / 2 ? sp.p[0] : sp.p[1];
+        // one part's words per wave, read at a uniform index (selecting between both parts'
+        // words would hold them all in scalar registers)
+        P = sp.p[__builtin_amdgcn_readfirstlane(wv < kSWaves / 2 ? 0u : 1u)];
         const uint32_t nb = (fa.n_ff + 31) / 32;
         f_b0 = blockIdx.x * fa.blocks_per_wg;
         f_b1 = f_b0 + fa.blocks_per_wg < nb ? f_b0 + fa.blocks_per_wg : nb;
@@ -1843,6 +1852,15 @@ static const void *ffn_fn(uint32_t type) {
 }
 
 size_t ah_ffn_lds_bytes(uint32_t kpad) { return ah_gemv_stream_lds_bytes(kpad) + kFfnLdsBytes; }
+
+// Workgroups of the FFN gate/up kernel that fit one CU at once (its grid is sized to them).
+int ah_ffn_occupancy(uint32_t type, uint32_t kpad) {
+    int n = 0;
+    const void *f = ffn_fn(type);
+    if (!f || hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, kSThreads, ah_ffn_lds_bytes(kpad)) != hipSuccess)
+        return 0;
+    return n;
+}
 
 hipError_t ah_launch_ffn_gate_up(uint32_t type, const StreamParts &sp, const FfnArgs &fa, uint32_t grid,
                                  uint32_t act_bytes, unsigned long long *status, hipStream_t stream) {

@@ -23,8 +23,10 @@ Also reported, beside the value:
   roofline      the token's dominant kernel (the Q4_K stage launches, o / gate-up / Q4_K down:
                 most of a token's time) against the 8 TB/s HBM peak, HIP events on the launch
                 stream over those launches back to back;
-  decode        the same token as one persistent launch (ah_seq_*, with and without the fused
-                FFN's SwiGLU stage), as eager launches, and with its 197 projections batched as
+  decode        the same token as eager launches; with the fused FFN in launch form (gate/up with
+                the exact SwiGLU + hidden requantize in one launch, down from the hidden codes:
+                the FFN's real data dependency); as one persistent launch (ah_seq_*, with and
+                without the fused FFN's SwiGLU stage); and with its 197 projections batched as
                 independent parts (two launches: not a dependency-respecting token);
   config1       BASELINE configs[1] (Qwen2.5-0.5B, 24 layers, Q4_K) as one batched launch;
   gemm          configs[3] N = 512 GEMMs against the 5.0 POPS int8 MFMA peak (Q8_0 on both MFMA
@@ -286,6 +288,28 @@ def main() -> int:
         if not args.no_extras:
             reps = 20
             decode["us_per_token_eager"] = round(event_us(token_eager, reps), 1)
+            # the token with the fused FFN in launch form (ffn_q8act_prepared_into): per layer q/k/v
+            # -> o -> gate/up with the exact SwiGLU and hidden requantize in one launch
+            # (ah_ffn_gate_up_dev) -> down from the hidden codes, then the head: 85 launches, one graph
+            hc_g = torch.zeros(8960, dtype=torch.int8, device="cuda")
+            hs_g = torch.zeros(280, dtype=torch.int64, device="cuda")
+
+            def token_fused(s):
+                for li, L in enumerate(W):
+                    plans[4 * li].run(s)
+                    plans[4 * li + 1].run(s)
+                    chart.ffn_dev(dev, L["gate"][3], L["up"][3], L["down"][3], ptr(X["ffn"]), ptr(Y["down"]),
+                                  ptr(hc_g), ptr(hs_g), s)
+                plans[-1].run(s)
+
+            graph_f = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph_f, stream=cap):
+                token_fused(torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            clock_up(graph_f.replay, 0.05)
+            decode["us_per_token_graph_fused_ffn"] = round(event_us(graph_f.replay, reps), 1)
+            assert dev.sync_status(sh) == 0
+            del graph_f
             # one persistent launch per token (ah_seq_*): the same stages; and with the fused FFN's
             # SwiGLU stage between gate/up and down (down then reads the hidden QuantAct)
             hc = torch.zeros(8960, dtype=torch.int8, device="cuda")
@@ -326,7 +350,8 @@ def main() -> int:
             for p in by_type:
                 p.free()
             assert dev.sync_status(sh) == 0
-            log(f"[bench] decode token: eager {decode['us_per_token_eager']} us, persistent "
+            log(f"[bench] decode token: eager {decode['us_per_token_eager']} us, graph with the fused FFN "
+                f"{decode['us_per_token_graph_fused_ffn']} us, persistent "
                 f"{decode['us_per_token_persistent']} us, persistent with fused FFN "
                 f"{decode['us_per_token_persistent_fused_ffn']} us, independent parts {us_b:.1f} us")
         result["decode"] = decode

@@ -180,3 +180,59 @@ def test_act_code_f32_fast_block_matches_quant_act():
     assert n_blocks > 500
     assert n_second > 0  # the second rounding decides some code at e <= 24
     assert n_clear >= 4  # and the clear below half a unit some code at each sampled e
+
+
+# ---- the fused FFN's exp in i64 (fx_exp in ah_gemv.hip) -----------------------------------------
+
+_EXP_C = [852176, 5965232, 35791394, 178956971, 715827883, 2147483648, 4294967296, 4294967296]
+I64_MAX, I64_MIN = (1 << 63) - 1, -(1 << 63)
+
+
+def _rdiv32(v: int) -> int:
+    """round(v / 2^32), ties away from zero: the device's branch-free i64 form (valid for
+    |v| <= 2^63 - 2^31)."""
+    assert -(1 << 63) + (1 << 31) <= v <= (1 << 63) - (1 << 31), v
+    a = -v if v < 0 else v
+    q = (a + (1 << 31)) >> 32
+    return -q if v < 0 else q
+
+
+def fx_exp_i64(x: int):
+    """The device's exp(x) in Q32.32, step for step, asserting that every product of its Horner
+    sum is an i64 (the reason the reference's i128 sum may run in i64 there)."""
+    if x < -16 * (1 << 32) or x > 21 * (1 << 32):
+        return 13, 0
+    k = (x * 6196328019 + (1 << 63)) >> 64
+    r = x - k * 2977044472
+    assert abs(r) < 1 << 31
+    acc = _EXP_C[0]
+    for c in _EXP_C[1:]:
+        p = acc * r
+        assert I64_MIN <= p <= I64_MAX, (x, acc, r)
+        acc = _rdiv32(p) + c
+        assert 0 < acc < (1 << 33), (x, acc)
+    if k >= 0:
+        if k >= 63 or acc > (I64_MAX >> k) or acc < (I64_MIN >> k):
+            return 13, 0
+        return 0, acc << k
+    n = -k
+    return 0, (0 if n >= 63 else (acc + (1 << (n - 1))) >> n)
+
+
+def test_fx_exp_i64_equals_fixed_exp():
+    """fx_exp's i64 Horner equals the reference's i128 one (oracle aho_fixed_exp, pinned by the
+    reference's KATs in test_oracle_ffn.py) across the whole domain: every half-way point of
+    k = round(x / ln 2) (where |r| is largest) with its neighbours, the range ends, powers of two
+    and a random sweep; no product leaves i64 on the way."""
+    one = 1 << 32
+    xs = [-16 * one, 21 * one, -16 * one - 1, 21 * one + 1, 0, 1, -1, one, -one]
+    ln2 = 2977044472
+    for k in range(-24, 32):
+        mid = (2 * k + 1) * ln2 // 2
+        xs += [mid + d for d in range(-3, 4)] + [k * ln2 + d for d in (-1, 0, 1)]
+    for e in range(0, 37):
+        xs += [1 << e, -(1 << e), (1 << e) - 1]
+    rng = np.random.default_rng(0xE4B)
+    xs += [int(v) for v in rng.integers(-16 * one, 21 * one, size=20000, dtype=np.int64)]
+    for x in xs:
+        assert fx_exp_i64(x) == tuple(oracle.fixed_exp(x)), x

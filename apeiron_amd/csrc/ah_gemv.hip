@@ -1130,26 +1130,42 @@ AH_DEV GemvPart part_at(const GemvPart *__restrict__ parts, uint32_t i) {
 template <int TYPE>
 constexpr int stream_waves_per_simd() { return TYPE == kMixedType ? 2 : 4; }
 
-// LDS of the fused FFN's gate/up launch past the tile slots: the gate and up row sums of the
-// workgroup's hidden blocks (f32), then the hidden h of one element per thread (i64).
+// LDS of the fused FFN's gate/up launch past the tile slots: the gate and up row sums (f32) of
+// the workgroup's hidden blocks.
 constexpr uint32_t kFfnRows = 32 * kFfnMaxBlocks;
-constexpr uint32_t kFfnLdsBytes = 2 * kFfnRows * 4 + kSThreads * 8;
+constexpr uint32_t kFfnLdsBytes = 2 * kFfnRows * 4;
 
-// The fused FFN's epilogue over the workgroup's hidden blocks [b0, b1): each thread takes one
-// element, converts its gate and up row sums to Q32.32 (to_q32) and forms
-// h = round_shift_32(silu_fixed(gate) * up) (engine/ops/ffn.rs:80, chart/ffn.rs:246-252); then a
-// quad of lanes per block quantizes h (quant_act) into the hidden QuantAct.  Refusals keep the
-// reference FFN's order (chart/ffn.rs:1712-1720): the projections' outputs (recorded by the tile
-// loop, gate rows then up rows), then the elements' conversion or SwiGLU refusals, then the
-// quantizer's, each class keyed past the one before.
-AH_DEV void ffn_epilogue(const FfnArgs &fa, uint32_t b0, uint32_t b1, const float *hsum, int64_t *hl,
+// Largest value over each aligned group of 32 lanes (every lane of the group gets it): DPP within
+// a row of 16 (quad exchanges, then the half-row and row mirrors), then one exchange of rows.
+template <int CTRL>
+AH_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+AH_DEV int max32(int v) {
+    v = __builtin_elementwise_max(v, dpp_i<0xB1>(v));   // lane ^ 1
+    v = __builtin_elementwise_max(v, dpp_i<0x4E>(v));   // lane ^ 2
+    v = __builtin_elementwise_max(v, dpp_i<0x141>(v));  // row_half_mirror
+    v = __builtin_elementwise_max(v, dpp_i<0x140>(v));  // row_mirror
+    return __builtin_elementwise_max(v, __shfl_xor(v, 16, 64));
+}
+
+// The fused FFN's epilogue over the workgroup's hidden blocks [b0, b1): one thread per element,
+// 32 lanes per block.  Each converts its gate and up row sums to Q32.32 (to_q32) and forms
+// h = round_shift_32(silu_fixed(gate) * up) (engine/ops/ffn.rs:80, chart/ffn.rs:246-252), then
+// quantizes it (quant_act) with its block's lanes: act_scale is monotone in the block's largest
+// magnitude, so the block exponent is the largest of the lanes' own exponents (a 32-lane max of
+// small integers), and each lane forms its own code.  Refusals keep the reference FFN's order
+// (chart/ffn.rs:1712-1720): the projections' outputs (recorded by the tile loop, gate rows then
+// up rows), then the elements' conversion or SwiGLU refusals, then the quantizer's, each class
+// keyed past the one before.
+AH_DEV void ffn_epilogue(const FfnArgs &fa, uint32_t b0, uint32_t b1, const float *hsum,
                          unsigned long long *status) {
     ah_lds_barrier();  // every wave's row sums are in LDS
     const uint32_t n = fa.n_ff, nb = (n + 31) / 32;
-    const uint32_t tid = threadIdx.x, q = tid & 3;
-    const uint32_t j = tid / 32, k = 32 * (b0 + j) + (tid & 31);  // b1 - b0 <= kSThreads / 32
+    const uint32_t tid = threadIdx.x, j = tid / 32, l = tid & 31;
+    const uint32_t b = b0 + j, k = 32 * b + l;  // b1 - b0 <= kSThreads / 32
+    if (b0 + j >= b1) return;                    // whole half-waves: uniform per 32-lane group
+    const bool live = k < n;
     int64_t h = 0;
-    if (b0 + j < b1 && k < n) {
+    if (live) {
         const uint32_t gb = __builtin_bit_cast(uint32_t, hsum[k - 32 * b0]);
         const uint32_t ub = __builtin_bit_cast(uint32_t, hsum[kFfnRows + k - 32 * b0]);
         uint64_t mg, mu;
@@ -1162,44 +1178,21 @@ AH_DEV void ffn_epilogue(const FfnArgs &fa, uint32_t b0, uint32_t b1, const floa
             h = 0;
         }
     }
-    hl[tid] = h;
-    ah_lds_barrier();
-    if (tid < 4 * kFfnMaxBlocks) {
-        const uint32_t jb = tid / 4, b = b0 + jb, k0 = 32 * b + 8 * q;
-        QuadIn in;
-        in.take = b < b1 && n > k0 ? (n - k0 < 8 ? n - k0 : 8) : 0;
-        in.s0 = in.s1 = 0;
-        uint32_t nz = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint64_t v = (uint32_t)i < in.take ? (uint64_t)hl[32 * jb + 8 * q + i] : 0ull;
-            in.w[2 * i] = (uint32_t)v;
-            in.w[2 * i + 1] = (uint32_t)(v >> 32);
-            nz |= in.w[2 * i] | in.w[2 * i + 1];
-        }
-        nz |= quad_xor1(nz);
-        nz |= quad_xor2(nz);
-        // the quantizer's own refusal key would sort before the projections' outputs: a block
-        // it refuses (nonzero, yet no scale) is recorded here, after the SwiGLU class
-        const QuadOut o = quad_quant(in, AH_SRC_Q32, b, nullptr, 0);
-        if (b < b1) {
-            if (q == 0 && nz != 0 && o.e < 0) ah_record(status, ah_out_key(3ull * n + b, 7u));
-            const __amdgpu_buffer_rsrc_t rc = ah_rsrc(fa.h_codes, n), rs = ah_rsrc(fa.h_scales, nb * 8u);
-            if (in.take == 8) {
-                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, (u32x2){o.c0, o.c1}), rc, k0, 0, 0);
-            } else {
-#pragma unroll
-                for (uint32_t i = 0; i < 8; ++i)
-                    if (i < in.take)
-                        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(((i < 4 ? o.c0 : o.c1) >> (8 * (i & 3))) & 0xffu),
-                                                             rc, k0 + i, 0, 0);
-            }
-            if (q == 0) {
-                const uint64_t S64 = o.e < 0 ? 0ull : (1ull << o.e);
-                __builtin_amdgcn_raw_buffer_store_b64(
-                    __builtin_bit_cast(u32x2, (u32x2){(uint32_t)S64, (uint32_t)(S64 >> 32)}), rs, 8 * b, 0, 0);
-            }
-        }
+    // quant_act of the block (chart/mod.rs:258-334): S = act_scale(max |h|), codes q + [2r >= S]
+    const bool neg = h < 0;
+    const uint64_t mag = neg ? 0ull - (uint64_t)h : (uint64_t)h;
+    const int e = max32(mag ? ah_act_scale_exp(mag) : -1);
+    bool bad = e == 63;  // act_scale's None
+    const int c = e >= 0 && e < 63 ? ah_act_code(mag, neg, e, bad) : 0;
+    const uint64_t group = 0xFFFFFFFFull << (tid & 32);
+    const bool bad_block = (__builtin_amdgcn_ballot_w64(bad) & group) != 0ull;
+    const __amdgpu_buffer_rsrc_t rc = ah_rsrc(fa.h_codes, n), rs = ah_rsrc(fa.h_scales, nb * 8u);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(bad_block ? 0 : c), rc, live ? k : kActOob, 0, 0);
+    if (l == 0) {
+        if (bad_block) ah_record(status, ah_out_key(3ull * n + b, 7u));
+        const uint64_t S64 = bad_block || e < 0 ? 0ull : (1ull << e);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, (u32x2){(uint32_t)S64, (uint32_t)(S64 >> 32)}),
+                                              rs, 8 * b, 0, 0);
     }
 }
 
@@ -1418,7 +1411,7 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
         // gate rows keep their index, up rows follow them (the reference projects gate, then up)
         if (obad != 0xFFFFFFFFu && lane == 0)
             ah_record(status, ah_out_key((obad >> 1) + (wv < kSWaves / 2 ? 0u : fa.n_ff), (obad & 1u) ? 9u : 8u));
-        ffn_epilogue(fa, f_b0, f_b1, hsum, reinterpret_cast<int64_t *>(hsum + 2 * kFfnRows), status);
+        ffn_epilogue(fa, f_b0, f_b1, hsum, status);
     } else {
         if (obad != 0xFFFFFFFFu && lane == 0) ah_record(status, ah_out_key(obad >> 1, (obad & 1u) ? 9u : 8u));
     }

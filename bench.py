@@ -131,6 +131,8 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true", help="headline only (decode token + roofline)")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--cpu-threads", type=int, default=8)
+    ap.add_argument("--no-seq", action="store_true",
+                    help="skip the persistent (cooperative-launch) token forms of the decode extras")
     ap.add_argument("--only", choices=["decode", "gemm", "gemm3", "config1", "heads", "copy"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -264,10 +266,21 @@ def main() -> int:
             per_kind[kind] = {"launches_per_token": len(idx), "us_per_launch": round(us, 2),
                               "bytes_per_launch": int(nbytes), "gbs": round(nbytes / us / 1e3, 1),
                               "us_per_token": round(us * len(idx), 1)}
+        # The roofline kernel's launches, timed as the token runs them: the Q4_K stage launches in
+        # token order captured into one graph, replayed on the launch stream between HIP events.
         q4 = [i for i, k in enumerate(kinds) if k[2] == (synth.Q4_K,)]
-        us_q4 = event_us(lambda: [plans[i].run(sh) for i in q4], 4) / len(q4)
+        graph_q4 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph_q4, stream=cap):
+            s_q4 = torch.cuda.current_stream().cuda_stream
+            for i in q4:
+                plans[i].run(s_q4)
+        torch.cuda.synchronize()
+        clock_up(graph_q4.replay, 0.05)
+        us_q4 = min(event_us(graph_q4.replay, 10) for _ in range(3)) / len(q4)
+        us_q4_eager = event_us(lambda: [plans[i].run(sh) for i in q4], 4) / len(q4)
         b_q4 = sum(kinds[i][1] for i in q4) / len(q4)
         assert dev.sync_status(sh) == 0
+        del graph_q4
         traffic = profile_value("traffic_bytes_per_launch", int)
         result["roofline"] = {
             "bound": "hbm",
@@ -276,9 +289,11 @@ def main() -> int:
             "achieved": round(b_q4 / us_q4 / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(b_q4 / us_q4 / 1e3 / HBM_PEAK_GBS, 4), "traffic": traffic,
             "bytes_per_launch": int(b_q4), "us_per_launch": round(us_q4, 3),
-            "note": "us_per_launch: HIP events over the launches back to back, dispatch gaps between "
-                    "dependent launches included; traffic and kernel_us_profile: the committed rocprofv3 "
-                    "summary (profiles/decode_config4_token.md)",
+            "us_per_launch_eager": round(us_q4_eager, 3),
+            "note": "us_per_launch: HIP events around replays of one graph of these launches in token "
+                    "order (the dependent chain as the token runs it); us_per_launch_eager: the same "
+                    "launches back to back from the host; traffic and kernel_us_profile: the committed "
+                    "rocprofv3 summary (profiles/decode_config4_token.md)",
             "kernel_us_profile": profile_value("kernel_us_per_launch")}
         result["_value"], result["_ms"] = value, ms_per_step
         decode = {"stages": len(plans), "bytes_per_token": tok_bytes, "us_per_token_graph": round(ms_per_step * 1e3, 1),
@@ -314,7 +329,7 @@ def main() -> int:
             # SwiGLU stage between gate/up and down (down then reads the hidden QuantAct)
             hc = torch.zeros(8960, dtype=torch.int8, device="cuda")
             hs = torch.zeros(280, dtype=torch.int64, device="cuda")
-            for fused in (False, True):
+            for fused in (() if args.no_seq else (False, True)):
                 stages = []
                 for L in W:
                     part = lambda n, x=None: (L[n][3], x if x is not None else ptr(X[src[n]]), ptr(Y[n]))
@@ -352,8 +367,8 @@ def main() -> int:
             assert dev.sync_status(sh) == 0
             log(f"[bench] decode token: eager {decode['us_per_token_eager']} us, graph with the fused FFN "
                 f"{decode['us_per_token_graph_fused_ffn']} us, persistent "
-                f"{decode['us_per_token_persistent']} us, persistent with fused FFN "
-                f"{decode['us_per_token_persistent_fused_ffn']} us, independent parts {us_b:.1f} us")
+                f"{decode.get('us_per_token_persistent')} us, persistent with fused FFN "
+                f"{decode.get('us_per_token_persistent_fused_ffn')} us, independent parts {us_b:.1f} us")
         result["decode"] = decode
         for p in plans:
             p.free()

@@ -10,6 +10,8 @@ benchmark configurations:
   super-blocks; their unused tail is random and must be ignored by every kernel.
 * Q6_K: 6-bit quants uniform 0..63; int8 16-group scales uniform in [-128, 127];
   d = f16(|N(0, 0.01)|).
+* Q2_K / Q3_K (format/quant.rs:308-476): every code, scale and mask byte uniform 0..255;
+  d (and Q2_K's dmin) = f16(|N(0, 0.01)|).
 * Activations: f32 N(0, 1).
 
 f16 rounding is numpy's float16 conversion (round to nearest even).  The RNG is numpy's
@@ -19,9 +21,11 @@ from __future__ import annotations
 
 import numpy as np
 
-Q5_0, Q8_0, Q4_K, Q6_K = 6, 8, 12, 14
-GEOM = {Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
-NAMES = {Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q6_K = 6, 8, 10, 11, 12, 14
+GEOM = {Q5_0: (32, 22), Q8_0: (32, 34), Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144), Q6_K: (256, 210)}
+NAMES = {Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+# f16 scale words of a block: (byte offset of d, byte offset of dmin or None)
+SCALE_AT = {Q5_0: (0, None), Q8_0: (0, None), Q2_K: (80, 82), Q3_K: (108, None), Q4_K: (0, 2), Q6_K: (208, None)}
 
 
 def row_bytes(ggml_type: int, n_in: int) -> int:
@@ -38,6 +42,11 @@ def needed_row_bytes(ggml_type: int, n_in: int) -> int:
         # header 16 B + the qs bytes of the used sub-block pairs
         tail = 0 if rem == 0 else 16 + 32 * (-(-rem // 64))
         return 144 * full + tail
+    if ggml_type in (Q2_K, Q3_K):
+        # a used half (128 elements) reads its 32 qs bytes; the rest of the block is read whole
+        # (Q2_K: scales 16 + d/dmin 4; Q3_K: hmask 32 + scales 12 + d 2)
+        other = 20 if ggml_type == Q2_K else 46
+        return GEOM[ggml_type][1] * full + (0 if rem == 0 else other + 32 * (-(-rem // 128)))
     # Q6_K: ql + qh + sc of the used halves + d
     if rem == 0:
         return 210 * full
@@ -133,7 +142,23 @@ def q6_k_payload(rng: np.random.Generator, rows: int, n_in: int, sigma: float = 
     return blk.reshape(-1)
 
 
+def q23_k_payload(ggml_type: int, rng: np.random.Generator, rows: int, n_in: int,
+                  sigma: float = 0.01) -> np.ndarray:
+    """Q2_K / Q3_K super-blocks: random code, scale and mask bytes, f16 d (and dmin) = |N(0, sigma)|."""
+    bb = GEOM[ggml_type][1]
+    n = rows * (-(-n_in // 256))
+    blk = rng.integers(0, 256, size=(n, bb), dtype=np.uint8)
+    od, om = SCALE_AT[ggml_type]
+    for o in (od, om):
+        if o is not None:
+            w = _f16_abs_normal(rng, n, sigma)
+            blk[:, o], blk[:, o + 1] = w & 0xFF, w >> 8
+    return blk.reshape(-1)
+
+
 def payload(ggml_type: int, rng: np.random.Generator, rows: int, n_in: int) -> np.ndarray:
+    if ggml_type in (Q2_K, Q3_K):
+        return q23_k_payload(ggml_type, rng, rows, n_in)
     if ggml_type == Q8_0:
         return q8_0_payload(rng, rows, n_in)
     if ggml_type == Q5_0:
@@ -151,13 +176,10 @@ def random_bytes_payload(rng: np.random.Generator, ggml_type: int, rows: int, n_
     qk, bb = GEOM[ggml_type]
     nblk = rows * (-(-n_in // qk))
     raw = rng.integers(0, 256, size=(nblk, bb), dtype=np.uint8)
-    if ggml_type in (Q8_0, Q5_0):
-        raw[:, 0], raw[:, 1] = d & 0xFF, d >> 8
-    elif ggml_type == Q4_K:
-        raw[:, 0], raw[:, 1] = d & 0xFF, d >> 8
-        raw[:, 2], raw[:, 3] = dmin & 0xFF, dmin >> 8
-    else:
-        raw[:, 208], raw[:, 209] = d & 0xFF, d >> 8
+    od, om = SCALE_AT[ggml_type]
+    raw[:, od], raw[:, od + 1] = d & 0xFF, d >> 8
+    if om is not None:
+        raw[:, om], raw[:, om + 1] = dmin & 0xFF, dmin >> 8
     return raw.reshape(-1)
 
 

@@ -164,7 +164,7 @@ def matmat_q8act_fast(t: int, raw, n_out: int, n_in: int, codes2d, scales2d, thr
 def block_dots(t: int, row, n_in: int, codes) -> tuple[int, np.ndarray, np.ndarray]:
     row = np.ascontiguousarray(row, dtype=np.uint8)
     codes = np.ascontiguousarray(codes, dtype=np.int8)
-    nd = -(-n_in // 16) if t == 14 else -(-n_in // 32)
+    nd = -(-n_in // 16) if t in (10, 11, 14) else -(-n_in // 32)  # per-16 groups: Q2_K, Q3_K, Q6_K
     dots = np.zeros(max(nd, 1), dtype=np.int32)
     xs = np.zeros(max(-(-n_in // 32), 1), dtype=np.int32)
     st = lib().aho_block_dots(t, _p(row), row.shape[0], n_in, _p(codes), _p(dots), _p(xs))

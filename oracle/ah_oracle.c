@@ -16,6 +16,8 @@ typedef unsigned __int128 u128;
 #define QK_K 256
 #define Q8_0_BYTES 34
 #define Q5_0_BYTES 22
+#define Q2_K_BYTES 84
+#define Q3_K_BYTES 110
 #define Q4_K_BYTES 144
 #define Q6_K_BYTES 210
 
@@ -24,6 +26,8 @@ int aho_block_geom(uint32_t t, size_t *qk, size_t *bb) {
     switch (t) {
     case AHO_Q8_0: *qk = 32; *bb = Q8_0_BYTES; return 1;
     case AHO_Q5_0: *qk = 32; *bb = Q5_0_BYTES; return 1;
+    case AHO_Q2_K: *qk = QK_K; *bb = Q2_K_BYTES; return 1;
+    case AHO_Q3_K: *qk = QK_K; *bb = Q3_K_BYTES; return 1;
     case AHO_Q4_K: *qk = QK_K; *bb = Q4_K_BYTES; return 1;
     case AHO_Q6_K: *qk = QK_K; *bb = Q6_K_BYTES; return 1;
     default: return 0;
@@ -209,6 +213,34 @@ static void q50_codes(const uint8_t *blk, int8_t *out) {
     }
 }
 
+/* format/quant.rs:336-364 and :426-458: Q2_K / Q3_K codes in output order.  Each half of 128
+ * outputs reads its 32 qs bytes four times, one bit pair per pass (shift 0, 2, 4, 6); a pass emits
+ * the 16 bytes of plane 0, then the 16 of plane 1.  Q3_K subtracts 4 from each value whose hmask
+ * bit is clear: mask byte 16*plane + l, bit (4*half + pass). */
+static void k23_codes(const uint8_t *qs, const uint8_t *hm, int8_t *out) {
+    int y = 0;
+    for (int half = 0; half < 2; half++)
+        for (int pass = 0; pass < 4; pass++)
+            for (int plane = 0; plane < 2; plane++)
+                for (int l = 0; l < 16; l++, y++) {
+                    int v = (qs[32 * half + 16 * plane + l] >> (2 * pass)) & 3;
+                    if (hm && !((hm[16 * plane + l] >> (4 * half + pass)) & 1)) v -= 4;
+                    out[y] = (int8_t)v;
+                }
+}
+
+/* format/quant.rs:391-417: the sixteen 6-bit Q3_K scales from the 12 packed bytes, as the four
+ * little-endian words of kmask shuffles (kmask1 = 0x03030303, kmask2 = 0x0f0f0f0f). */
+static void q3k_scales(const uint8_t *p, int *sc) {
+    uint32_t a0 = (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24;
+    uint32_t a1 = (uint32_t)p[4] | (uint32_t)p[5] << 8 | (uint32_t)p[6] << 16 | (uint32_t)p[7] << 24;
+    uint32_t t = (uint32_t)p[8] | (uint32_t)p[9] << 8 | (uint32_t)p[10] << 16 | (uint32_t)p[11] << 24;
+    const uint32_t m1 = 0x03030303u, m2 = 0x0f0f0f0fu;
+    uint32_t w[4] = {(a0 & m2) | ((t & m1) << 4), (a1 & m2) | (((t >> 2) & m1) << 4),
+                     ((a0 >> 4) & m2) | (((t >> 4) & m1) << 4), ((a1 >> 4) & m2) | (((t >> 6) & m1) << 4)};
+    for (int j = 0; j < 16; j++) sc[j] = (int)((w[j / 4] >> (8 * (j % 4))) & 0xff);
+}
+
 /* The integer codes of one super-block / block in output order (Q4_K: nibbles 0..15). */
 static void q4k_codes(const uint8_t *blk, uint8_t *out) {
     const uint8_t *qs = blk + 16;
@@ -242,6 +274,31 @@ int aho_dequant_row(uint32_t t, const uint8_t *row, size_t row_len, size_t n, in
             int8_t c[32];
             q50_codes(blk, c);
             for (size_t l = 0; l < take; l++) out[b * qk + l] = d * (int64_t)c[l];
+        } else if (t == AHO_Q2_K) {
+            /* num/dequant.rs:395-462: w = d*sc*q - dmin*m per 16-group (sc low nibble, m high) */
+            int64_t d, dmin;
+            if ((st = aho_f16_to_fixed(rd16(blk + 80), &d))) return st;
+            if ((st = aho_f16_to_fixed(rd16(blk + 82), &dmin))) return st;
+            int8_t c[QK_K];
+            k23_codes(blk + 16, NULL, c);
+            for (int g = 0; g < 16; g++) {
+                int64_t slope = d * (blk[g] & 0xF), icpt = dmin * (blk[g] >> 4);
+                for (int l = 0; l < 16; l++) vals[16 * g + l] = slope * c[16 * g + l] - icpt;
+            }
+            memcpy(out + b * qk, vals, take * sizeof(int64_t));
+        } else if (t == AHO_Q3_K) {
+            /* num/dequant.rs:464-512: w = d*(sc-32)*c per 16-group */
+            int64_t d;
+            if ((st = aho_f16_to_fixed(rd16(blk + 108), &d))) return st;
+            int8_t c[QK_K];
+            int sc[16];
+            k23_codes(blk + 32, blk, c);
+            q3k_scales(blk + 96, sc);
+            for (int g = 0; g < 16; g++) {
+                int64_t slope = d * (sc[g] - 32);
+                for (int l = 0; l < 16; l++) vals[16 * g + l] = slope * c[16 * g + l];
+            }
+            memcpy(out + b * qk, vals, take * sizeof(int64_t));
         } else if (t == AHO_Q4_K) {
             int64_t d, dmin;
             if ((st = aho_f16_to_fixed(rd16(blk), &d))) return st;
@@ -368,7 +425,10 @@ int aho_block_dots(uint32_t t, const uint8_t *row, size_t row_len, size_t n_in,
         size_t nb16 = (n_in + 15) / 16;
         for (size_t sb = 0; sb < blocks; sb++) {
             int8_t c[QK_K];
-            q6k_codes(row + sb * bb, c);
+            const uint8_t *blk = row + sb * bb;
+            if (t == AHO_Q2_K) k23_codes(blk + 16, NULL, c);
+            else if (t == AHO_Q3_K) k23_codes(blk + 32, blk, c);
+            else q6k_codes(blk, c);
             for (int j = 0; j < 16; j++) {
                 size_t g = sb * 16 + j;
                 if (g >= nb16) break;

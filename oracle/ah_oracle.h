@@ -53,7 +53,7 @@ enum {
     AHO_ERR_ZERO_DENOMINATOR = 14         /* FfnError::ZeroDenominator                  */
 };
 
-enum { AHO_Q5_0 = 6, AHO_Q8_0 = 8, AHO_Q4_K = 12, AHO_Q6_K = 14 };
+enum { AHO_Q5_0 = 6, AHO_Q8_0 = 8, AHO_Q2_K = 10, AHO_Q3_K = 11, AHO_Q4_K = 12, AHO_Q6_K = 14 };
 
 /* (weights per block, bytes per block) -- format/quant.rs:129-147.  0 on unknown type. */
 int aho_block_geom(uint32_t ggml_type, size_t *qk, size_t *block_bytes);
@@ -73,7 +73,8 @@ int aho_quant_act_f32(const float *x, size_t n, int8_t *codes, int64_t *scales);
 /* QuantAct::dequant (chart/mod.rs:186-209): x_hat = S_b * xq, or FIXED_OVERFLOW. */
 int aho_dequant_act(const int8_t *codes, const int64_t *scales, size_t n, int64_t *xhat);
 
-/* num/dequant.rs:99-122 for Q8_0 (:315-351), Q4_K (:514-617), Q6_K (:619-671).
+/* num/dequant.rs:99-122 for Q8_0 (:315-351), Q2_K (:395-462), Q3_K (:464-512), Q4_K (:514-617),
+ * Q6_K (:619-671).
  * row must hold ceil(n/qk) whole blocks. */
 int aho_dequant_row(uint32_t ggml_type, const uint8_t *row, size_t row_len, size_t n,
                     int64_t *out);
@@ -93,6 +94,8 @@ int aho_matvec_q8act(uint32_t ggml_type, const uint8_t *raw, size_t raw_len, siz
  *   Q5_0: dots[b] = sum_{l<32} (q-16)*xq over 32-block b           (ceil(K/32) entries)
  *   Q4_K: dots[j] = sum nibble*xq over 32-sub-block j              (ceil(K/32) entries)
  *   Q6_K: dots[g] = sum (u-32)*xq over 16-group g                  (ceil(K/16) entries)
+ *   Q2_K: dots[g] = sum q*xq over 16-group g, q in 0..3            (ceil(K/16) entries)
+ *   Q3_K: dots[g] = sum c*xq over 16-group g, c in -4..3           (ceil(K/16) entries)
  * xsums[b] = sum xq over 32-block b (ceil(K/32) entries).  Lanes >= K contribute nothing.
  * The factorisation is chart/mod.rs:11-16 (RowAcc::emit :501-514). */
 int aho_block_dots(uint32_t ggml_type, const uint8_t *row, size_t row_len, size_t n_in,

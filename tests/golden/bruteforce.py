@@ -108,6 +108,49 @@ def q5_0_codes(blk: bytes) -> list[int]:
     return lo + hi
 
 
+def k23_position(e: int) -> tuple[int, int, int]:
+    """Where Q2_K / Q3_K element e (0..255) sits: the qs byte index, the bit shift of its two bits,
+    and the bit of the hmask byte (16 * plane + l) that carries Q3_K's third bit.  Elements run in
+    two halves of 128; a half is four rounds of 32 (each round one bit pair of every qs byte of the
+    half), a round two planes of 16 consecutive qs bytes."""
+    half, r = divmod(e, 128)
+    rnd, r = divmod(r, 32)
+    plane, l = divmod(r, 16)
+    return 32 * half + 16 * plane + l, 2 * rnd, 4 * half + rnd
+
+
+def q2k_codes(blk: bytes) -> list[int]:
+    """The 256 two-bit Q2_K values 0..3 (qs at byte 16)."""
+    out = []
+    for e in range(256):
+        i, sh, _ = k23_position(e)
+        out.append((blk[16 + i] >> sh) & 3)
+    return out
+
+
+def q3k_codes(blk: bytes) -> list[int]:
+    """The 256 signed Q3_K codes: the two qs bits (qs at byte 32) minus 4 unless the hmask bit is set."""
+    out = []
+    for e in range(256):
+        i, sh, hb = k23_position(e)
+        q = (blk[32 + i] >> sh) & 3
+        h = (blk[e % 32] >> hb) & 1
+        out.append(q - (0 if h else 4))
+    return out
+
+
+def q3k_scales(sc12: bytes) -> list[int]:
+    """The sixteen 6-bit Q3_K group scales: low four bits from the nibbles of bytes 0..7 (group j < 8
+    the low nibble of byte j, group j >= 8 the high nibble of byte j - 8), high two bits from bit pair
+    j // 4 of byte 8 + j % 4."""
+    out = []
+    for j in range(16):
+        lo = (sc12[j] & 0xF) if j < 8 else (sc12[j - 8] >> 4)
+        hi = (sc12[8 + j % 4] >> (2 * (j // 4))) & 3
+        out.append(lo | (hi << 4))
+    return out
+
+
 def weights_row(ggml_type: int, row: bytes, n: int) -> list[int] | None:
     """Exact Q32.32 weights of one row, or None for a non-finite scale."""
     w: list[int] = []
@@ -140,6 +183,22 @@ def weights_row(ggml_type: int, row: bytes, n: int) -> list[int] | None:
                     q = (byte >> 4) if j % 2 else (byte & 0xF)
                     vals[32 * j + l] = d * sc * q - dm * m
             w += vals
+    elif ggml_type == 10:
+        for s in range(-(-n // 256)):
+            blk = row[84 * s:84 * s + 84]
+            d, dm = f16_q32(blk[80] | (blk[81] << 8)), f16_q32(blk[82] | (blk[83] << 8))
+            if d is None or dm is None:
+                return None
+            q = q2k_codes(blk)
+            w += [d * (blk[e // 16] & 0xF) * q[e] - dm * (blk[e // 16] >> 4) for e in range(256)]
+    elif ggml_type == 11:
+        for s in range(-(-n // 256)):
+            blk = row[110 * s:110 * s + 110]
+            d = f16_q32(blk[108] | (blk[109] << 8))
+            if d is None:
+                return None
+            c, sc = q3k_codes(blk), q3k_scales(blk[96:108])
+            w += [d * (sc[e // 16] - 32) * c[e] for e in range(256)]
     elif ggml_type == 14:
         for s in range(-(-n // 256)):
             blk = row[210 * s:210 * s + 210]
@@ -164,8 +223,8 @@ def weights_row(ggml_type: int, row: bytes, n: int) -> list[int] | None:
 
 def matvec(ggml_type: int, raw: bytes, n_out: int, n_in: int, xhat: list[int]):
     """floor((sum w*xhat + 2^31) / 2^32) per row, or None on a refusal."""
-    rb = {6: 22 * -(-n_in // 32), 8: 34 * -(-n_in // 32), 12: 144 * -(-n_in // 256),
-          14: 210 * -(-n_in // 256)}[ggml_type]
+    rb = {6: 22 * -(-n_in // 32), 8: 34 * -(-n_in // 32), 10: 84 * -(-n_in // 256), 11: 110 * -(-n_in // 256),
+          12: 144 * -(-n_in // 256), 14: 210 * -(-n_in // 256)}[ggml_type]
     ys = []
     for o in range(n_out):
         w = weights_row(ggml_type, raw[o * rb:(o + 1) * rb], n_in)
@@ -177,7 +236,8 @@ def matvec(ggml_type: int, raw: bytes, n_out: int, n_in: int, xhat: list[int]):
 
 
 def block_dots(ggml_type: int, row: bytes, n_in: int, codes: list[int]):
-    """Exact integer group dots: per-32 (Q8_0 codes, Q5_0 q-16, Q4_K nibbles), per-16 (Q6_K u-32)."""
+    """Exact integer group dots: per-32 (Q8_0 codes, Q5_0 q-16, Q4_K nibbles), per-16 (Q6_K u-32,
+    Q2_K's two-bit values, Q3_K's signed codes)."""
     w_codes: list[int] = []
     if ggml_type == 8:
         for b in range(-(-n_in // 32)):
@@ -195,6 +255,12 @@ def block_dots(ggml_type: int, row: bytes, n_in: int, codes: list[int]):
                     byte = blk[16 + 32 * (j // 2) + l]
                     w_codes.append((byte >> 4) if j % 2 else (byte & 0xF))
         g = 32
+    elif ggml_type in (10, 11):
+        bb = 84 if ggml_type == 10 else 110
+        for s in range(-(-n_in // 256)):
+            blk = row[bb * s:bb * s + bb]
+            w_codes += q2k_codes(blk) if ggml_type == 10 else q3k_codes(blk)
+        g = 16
     else:
         for s in range(-(-n_in // 256)):
             blk = row[210 * s:210 * s + 210]

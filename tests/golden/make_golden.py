@@ -88,6 +88,22 @@ def main() -> None:
     cases.append(("extreme", case_from_q32(6, raw, 2, 256, [127 if j % 2 == 0 else -127 for j in range(256)])))
     raw = synth.random_bytes_payload(rng5, 6, 1, 96, 0x3800, 0x3800)
     cases.append(("zeroblk", case_from_q32(6, raw, 1, 96, [0] * 64 + [1000 - 100 * j for j in range(64, 96)])))
+    # Q2_K and Q3_K (format/quant.rs:308-476), each with a stream of its own: the same families
+    for t, seed in ((10, 0x60DE10), (11, 0x60DE11)):
+        rk = np.random.default_rng(seed)
+        for rows, n_in in shapes + [(2, w) for w in (47, 65, 257, 271)]:
+            raw = synth.random_bytes_payload(rk, t, rows, n_in, 0x3800, 0x3400)
+            x = rk.integers(-2048, 2048, size=n_in)
+            cases.append(("random", case_from_q32(t, raw, rows, n_in, x)))
+        raw = synth.payload(t, rk, 3, 896)
+        xf = rk.standard_normal(896).astype(np.float32)
+        c = case_from_q32(t, raw, 3, 896, [bf.f32_q32(int(w)) for w in xf.view(np.uint32)])
+        c["xf"] = xf
+        cases.append(("f32", c))
+        raw = synth.random_bytes_payload(rk, t, 2, 256, 0x7BFF, 0x7BFF)
+        cases.append(("extreme", case_from_q32(t, raw, 2, 256, [127 if j % 2 == 0 else -127 for j in range(256)])))
+        raw = synth.random_bytes_payload(rk, t, 1, 96, 0x3800, 0x3800)
+        cases.append(("zeroblk", case_from_q32(t, raw, 1, 96, [0] * 64 + [1000 - 100 * j for j in range(64, 96)])))
     out = {}
     for i, (kind, c) in enumerate(cases):
         p = f"c{i:03d}_"

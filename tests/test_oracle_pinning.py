@@ -198,10 +198,14 @@ def test_matvec_fixed_reference_kats():
     assert oracle.matvec_fixed(999, np.zeros(4, np.uint8), 1, 1, [ONE])[0] == 5
 
 
+# families the CPU baseline's fast cores cover (the benchmarked ones); Q2_K and Q3_K have the
+# contract only
+FAST_TYPES = (6, 8, 12, 14)
+
 SHAPES = [(4, 32), (3, 48), (2, 33), (2, 300), (1, 64), (5, 0), (1, 256), (2, 512), (2, 256)]
 
 
-@pytest.mark.parametrize("t", [6, 8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 10, 11, 12, 14])
 def test_matvec_random_payloads_vs_bruteforce(t):
     # chart/tests.rs:222-267 shapes, random block bytes with d = dmin = 0x3800.
     rng = np.random.default_rng(0x12345678 + t)
@@ -214,8 +218,9 @@ def test_matvec_random_payloads_vs_bruteforce(t):
         xhat = oracle.dequant_act(codes, scales)[1]
         want = bf.matvec(t, raw.tobytes(), rows, n_in, xhat.tolist())
         assert st == 0 and y.tolist() == want, (t, rows, n_in)
-        stf, yf = oracle.matvec_q8act_fast(t, raw, rows, n_in, codes, scales, 2)
-        assert stf == 0 and yf.tolist() == want, (t, rows, n_in)
+        if t in FAST_TYPES:
+            stf, yf = oracle.matvec_q8act_fast(t, raw, rows, n_in, codes, scales, 2)
+            assert stf == 0 and yf.tolist() == want, (t, rows, n_in)
         # the tolerance basis sum_i |w_i * xhat_i| (real units) against exact integers
         sta, absdot = oracle.row_absdot(t, raw, rows, n_in, codes, scales)
         assert sta == 0
@@ -231,7 +236,7 @@ def test_matvec_random_payloads_vs_bruteforce(t):
             assert xs.tolist() == [int(codes[b:b + 32].astype(np.int64).sum()) for b in range(0, n_in, 32)]
 
 
-@pytest.mark.parametrize("t", [6, 8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 10, 11, 12, 14])
 def test_extreme_scales_and_codes(t):
     # chart/tests.rs:269-307: largest finite scale 0x7BFF, codes +-127 at unit scale.
     rng = np.random.default_rng(0x51FF0000 + t)
@@ -241,7 +246,73 @@ def test_extreme_scales_and_codes(t):
     st, y = oracle.matvec_q8act(t, raw, 2, 256, codes, scales)
     want = bf.matvec(t, raw.tobytes(), 2, 256, [int(c) for c in codes])
     assert st == 0 and y.tolist() == want
-    assert oracle.matvec_q8act_fast(t, raw, 2, 256, codes, scales, 1)[1].tolist() == want
+    if t in FAST_TYPES:
+        assert oracle.matvec_q8act_fast(t, raw, 2, 256, codes, scales, 1)[1].tolist() == want
+
+
+def test_q2_k_q3_k_unpack_kats():
+    # format/quant.rs:811-822: qs byte 16 = 0b11_10_01_00 carries outputs 0, 32, 64, 96 (one bit
+    # pair each, consecutive pairs 32 outputs apart); output 16 (the next plane) is 0.  Read
+    # through the dequantizer with d = 1.0, dmin = 0 and every group scale 1, so w = q.
+    b2 = np.zeros(84, np.uint8)
+    b2[0:16] = 0x01
+    b2[16] = 0b11_10_01_00
+    b2[80:82] = [0x00, 0x3C]
+    st, w = oracle.dequant_row(10, b2, 256)
+    assert st == 0
+    assert [int(w[i]) // ONE for i in (0, 32, 64, 96, 16)] == [0, 1, 2, 3, 0]
+    # format/quant.rs:859-869: scale byte 0x51 is (scale 1, min 5); d = 1.0 at byte 80, dmin = 0.5
+    # at byte 82 -- so group 0 holds w = q - 2.5 and every other (zero) group w = 0
+    b2 = np.zeros(84, np.uint8)
+    b2[0] = 0x51
+    b2[16] = 0b11_10_01_11
+    b2[80:84] = [0x00, 0x3C, 0x00, 0x38]
+    st, w = oracle.dequant_row(10, b2, 256)
+    assert st == 0
+    assert int(w[0]) == 3 * ONE - 5 * ONE // 2 and int(w[1]) == -5 * ONE // 2 and int(w[16]) == 0
+    # format/quant.rs:870-872: Q3_K's d sits at byte 108.  All other bytes zero: every 6-bit scale
+    # 0 (factor 0 - 32) and every hmask bit clear (code 0 - 4), so w = 1.0 * -32 * -4 = 128
+    b3 = np.zeros(110, np.uint8)
+    b3[108:110] = [0x00, 0x3C]
+    st, w = oracle.dequant_row(11, b3, 256)
+    assert st == 0 and set((w // ONE).tolist()) == {128}
+    # Q3_K's scale shuffle (format/quant.rs:391-417): groups whose 6-bit scale is 32 + j for j in
+    # 0..15, packed positionally (low nibbles in bytes 0..7, high bit pairs in bytes 8..11); all
+    # hmask bits set and qs bits 1, so every code is 1 and w = j in group j
+    want = [32 + j for j in range(16)]
+    b3 = np.zeros(110, np.uint8)
+    b3[0:32] = 0xFF
+    b3[32:96] = 0b01010101
+    for j, v in enumerate(want):
+        if j < 8:
+            b3[96 + j] |= v & 0xF
+        else:
+            b3[96 + j - 8] |= (v & 0xF) << 4
+        b3[104 + j % 4] |= ((v >> 4) & 3) << (2 * (j // 4))
+    b3[108:110] = [0x00, 0x3C]
+    assert bf.q3k_scales(bytes(b3[96:108])) == want
+    st, w = oracle.dequant_row(11, b3, 256)
+    assert st == 0 and (w // ONE).tolist() == [e // 16 for e in range(256)]
+    # every (qs bit pair, hmask bit) position: one set bit at a time against the brute force
+    for byte in range(96):
+        for bit in range(8):
+            b3 = np.zeros(110, np.uint8)
+            b3[96:108] = rng_bytes(byte * 8 + bit)
+            b3[108:110] = [0x00, 0x3C]
+            b3[byte] = 1 << bit
+            st, w = oracle.dequant_row(11, b3, 256)
+            assert st == 0 and w.tolist() == bf.weights_row(11, bytes(b3), 256)
+            b2 = np.zeros(84, np.uint8)
+            b2[0:16] = rng_bytes(byte * 8 + bit)[:12].tolist() + [0x21, 0x43, 0x65, 0x87]
+            b2[80:84] = [0x00, 0x3C, 0x00, 0x34]
+            if 16 <= byte < 80:
+                b2[byte] = 1 << bit
+            st, w = oracle.dequant_row(10, b2, 256)
+            assert st == 0 and w.tolist() == bf.weights_row(10, bytes(b2), 256)
+
+
+def rng_bytes(seed):
+    return np.random.default_rng(seed).integers(0, 256, size=12, dtype=np.uint8)
 
 
 def test_q8_0_scale_sets_and_spread(cpu_path):
@@ -278,14 +349,16 @@ def test_nonfinite_scale_refuses(cpu_path):
     # kern/gemm.rs:2756-2763: an f16 +inf scale refuses (NonFiniteScale), also on the fast path
     # (every core form: the bad scale sits in the second row, i.e. in a two-row tile).
     rng = np.random.default_rng(1)
-    for t in (8, 12, 14):
+    for t in (8, 10, 11, 12, 14):
         raw = synth.random_bytes_payload(rng, t, 3, 256, 0x3800, 0x3800)
         rb = synth.row_bytes(t, 256)
-        off = rb + (208 if t == 14 else 0)
+        od, om = synth.SCALE_AT[t]
+        off = rb + (om if om is not None else od)  # Q2_K / Q4_K: the dmin word
         raw[off:off + 2] = [0x00, 0x7C]
         st, codes, scales = oracle.quant_act(np.arange(256, dtype=np.int64) - 100)
         assert oracle.matvec_q8act(t, raw, 3, 256, codes, scales)[0] == 6
-        assert oracle.matvec_q8act_fast(t, raw, 3, 256, codes, scales, 2)[0] == 6
+        if t in FAST_TYPES:
+            assert oracle.matvec_q8act_fast(t, raw, 3, 256, codes, scales, 2)[0] == 6
 
 
 def test_zero_activation_blocks():

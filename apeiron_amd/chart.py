@@ -25,7 +25,7 @@ import numpy as np
 
 from . import _lib
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
+Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q6_K = 6, 8, 10, 11, 12, 14
 
 
 class MatvecError(Exception):

@@ -128,6 +128,8 @@ bool geom(uint32_t t, size_t &qk, size_t &bb) {
     switch (t) {
     case AH_GGML_Q8_0: qk = 32; bb = 34; return true;
     case AH_GGML_Q5_0: qk = 32; bb = 22; return true;
+    case AH_GGML_Q2_K: qk = 256; bb = 84; return true;
+    case AH_GGML_Q3_K: qk = 256; bb = 110; return true;
     case AH_GGML_Q4_K: qk = 256; bb = 144; return true;
     case AH_GGML_Q6_K: qk = 256; bb = 210; return true;
     default: return false;
@@ -151,6 +153,8 @@ int32_t validate(uint32_t t, size_t raw_len, size_t n_out, size_t n_in, size_t &
 void scale_offsets(uint32_t t, uint32_t &o0, uint32_t &o1, uint32_t &bb) {
     if (t == AH_GGML_Q8_0) { o0 = o1 = 0; bb = 34; }
     else if (t == AH_GGML_Q5_0) { o0 = o1 = 0; bb = 22; }
+    else if (t == AH_GGML_Q2_K) { o0 = 80; o1 = 82; bb = 84; }
+    else if (t == AH_GGML_Q3_K) { o0 = o1 = 108; bb = 110; }
     else if (t == AH_GGML_Q4_K) { o0 = 0; o1 = 2; bb = 144; }
     else { o0 = o1 = 208; bb = 210; }
 }
@@ -182,7 +186,7 @@ int32_t ensure_scratch(ah_ctx *ctx, size_t bytes) {
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Work units of a row: Q8_0 / Q5_0 blocks, Q4_K super-blocks (or, with `pairs`, sub-block pairs
-// of 64 elements), Q6_K half super-blocks (128 elements).
+// of 64 elements), Q2_K / Q3_K / Q6_K half super-blocks (128 elements).
 uint32_t units_per_row(uint32_t t, uint32_t n_in, bool pairs = false) {
     return ah_blk32((int)t)        ? (n_in + 31) / 32
            : t == AH_GGML_Q4_K     ? (pairs ? (n_in + 63) / 64 : (n_in + 255) / 256)
@@ -487,6 +491,58 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     if (!x && n_tok && n_in_sz) return AH_ERR_INVALID_ARG;
     if (n_tok == 0) return AH_OK;
     if (n_tok >= (1ull << 24)) return AH_ERR_INVALID_ARG;
+    // Q2_K / Q3_K parts take one GEMV launch per token, as matmat_q8act serves these families one
+    // column at a time (kern/matmat.rs:392-413); the other parts then go through the GEMM below.
+    // Nothing is allocated on this route (parts past kStackParts aside).
+    size_t n23 = 0;
+    for (size_t i = 0; i < n_parts; ++i) n23 += ah_k23((int)w[i]->type) ? 1 : 0;
+    if (n23) {
+        const size_t nb = (n_in_sz + 31) / 32;
+        // the GEMV reads codes a dword at a time: token rows of codes whose length is not a multiple
+        // of 4 are first copied to 4-byte aligned rows of the context scratch (same stream, so the
+        // GEMM below may reuse the scratch after these launches)
+        size_t pitch = src == AH_SRC_F32 ? n_in_sz * 4 : n_in_sz;
+        const int8_t *codes = static_cast<const int8_t *>(x);
+        if (src == AH_SRC_CODES && n_in_sz % 4) {
+            if (fixed) return AH_ERR_INVALID_ARG;
+            pitch = (n_in_sz + 3) & ~(size_t)3;
+            int32_t st = ensure_scratch(ctx, n_tok * pitch);
+            if (st) return st;
+            AH_HIP(ctx, hipSetDevice(ctx->device));
+            AH_HIP(ctx, hipMemcpy2DAsync(ctx->scratch, pitch, x, n_in_sz, n_in_sz, n_tok, hipMemcpyDeviceToDevice,
+                                         pick(ctx, stream)));
+            codes = static_cast<const int8_t *>(ctx->scratch);
+        }
+        for (size_t i = 0; i < n_parts; ++i) {
+            if (!ah_k23((int)w[i]->type)) continue;
+            for (size_t c = 0; c < n_tok; ++c) {
+                const void *xc = src == AH_SRC_F32 ? static_cast<const void *>(static_cast<const float *>(x) + c * n_in_sz)
+                                                   : static_cast<const void *>(codes + c * pitch);
+                const int32_t st = gemv_launch(ctx, w[i], src, xc, src == AH_SRC_CODES ? scales_in + c * nb : nullptr,
+                                               y[i] + c * w[i]->n_out, nullptr, stream);
+                if (st) return st;
+            }
+        }
+        if (n23 == n_parts) return AH_OK;
+        const ah_tensor *rw_stack[kStackParts];
+        float *ry_stack[kStackParts];
+        std::vector<const ah_tensor *> rw_heap;
+        std::vector<float *> ry_heap;
+        if (n_parts > kStackParts) {
+            if (fixed) return AH_ERR_INVALID_ARG;
+            rw_heap.resize(n_parts);
+            ry_heap.resize(n_parts);
+        }
+        const ah_tensor **rw = n_parts > kStackParts ? rw_heap.data() : rw_stack;
+        float **ry = n_parts > kStackParts ? ry_heap.data() : ry_stack;
+        size_t k = 0;
+        for (size_t i = 0; i < n_parts; ++i)
+            if (!ah_k23((int)w[i]->type)) {
+                rw[k] = w[i];
+                ry[k++] = y[i];
+            }
+        return gemm_group_launch(ctx, k, rw, src, x, scales_in, n_tok, ry, stream, fixed, fixed_cap);
+    }
     const uint32_t n_in = (uint32_t)n_in_sz, N = (uint32_t)n_tok;
     const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
     const uint32_t cus = (uint32_t)ctx->cu_count;

@@ -648,6 +648,77 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, ui
     return acc;
 }
 
+// Q2_K and Q3_K (format/quant.rs:308-476) in units of one half n of super-block s (128 elements,
+// like Q6_K).  Element 128n + 32r + 16p + l takes bit pair r of qs[32n + 16p + l]; group j = 2r + p
+// of the half is those 16 elements, consecutive in the activation.
+//   Q2_K (84 bytes: scales[16] @0, qs @16, f16 d @80, f16 dmin @82; 4-byte aligned): group g's
+//   byte scales[g] holds sc (low nibble) and m (high); term S * (d*sc*D - dmin*m*X) with D the
+//   group's sum q*xq (q in 0..3) and X its code sum.
+//   Q3_K (110 bytes: hmask[32] @0, qs @32, scales[12] @96, f16 d @108; 2-byte aligned, realigned
+//   as Q6_K): the third bit of element (r, p, l) of half n is bit 4n + r of hmask[16p + l], and the
+//   code is (q | hbit << 2) - 4; the 16 6-bit scales come from the 12 bytes by the kmask shuffle
+//   (four little-endian words a0, a1, t: half n's groups 0-3 are ((a0 >> 4n) & 0x0F0F0F0F) |
+//   ((t >> 4n) & 0x03030303) << 4, groups 4-7 the same from a1 and t >> (4n + 2)); term
+//   S * d * (sc - 32) * D with D = sum (q | hbit << 2) * xq - 4 X.
+// D is formed by four dot4 instructions per group on the masked bit pairs.
+template <int TYPE, bool DOTS>
+AH_DEV float unit_k23(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, uint32_t n_in, const ActLds &A,
+                      int32_t *dots16) {
+    constexpr bool Q3 = TYPE == AH_GGML_Q3_K;
+    const uint32_t sh = off & 3u;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(tl + (off & ~3u));
+    auto V = [&](int i) -> uint32_t { return Q3 ? ah_alignbyte(p[i + 1], p[i], sh) : p[i]; };
+    float fd, fdm = 0.0f;
+    uint32_t sw[2];
+    if constexpr (Q3) {
+        fd = ah_f16_bits_to_f32(V(27) & 0xffffu);
+        const uint32_t a0 = V(24), a1 = V(25), t = V(26);
+        sw[0] = ((a0 >> (4 * n)) & 0x0F0F0F0Fu) | (((t >> (4 * n)) & 0x03030303u) << 4);
+        sw[1] = ((a1 >> (4 * n)) & 0x0F0F0F0Fu) | (((t >> (4 * n + 2)) & 0x03030303u) << 4);
+    } else {
+        const uint32_t dd = V(20);
+        fd = ah_f16_bits_to_f32(dd & 0xffffu);
+        fdm = ah_f16_bits_to_f32(dd >> 16);
+        sw[0] = V(2 * n);
+        sw[1] = V(2 * n + 1);
+    }
+    constexpr int kQs = Q3 ? 8 : 4;  // dword of qs[0]
+    uint32_t q[8], hm[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        q[i] = V(kQs + 8 * (int)n + i);
+        hm[i] = Q3 ? V(i) : 0u;
+    }
+    const uint32_t nb16 = (n_in + 15) / 16;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int r = j >> 1, pl = j & 1;
+        const uint32_t g = 16 * s + 8 * n + (uint32_t)j;  // 16-group of the row
+        if (DOTS && g >= nb16) break;
+        const u32x4 xv = *reinterpret_cast<const u32x4 *>(A.codes + pad_k(16 * g));
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+        int32_t D = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t v = (q[4 * pl + i] >> (2 * r)) & 0x03030303u;
+            if constexpr (Q3) v |= ((hm[4 * pl + i] >> (4 * n + r)) & 0x01010101u) << 2;
+            D = ah_sdot4(v, xw[i], D);
+        }
+        const int32_t X = A.xs16[g];
+        const uint32_t sb = (sw[j >> 2] >> (8 * (j & 3))) & 0xffu;
+        if constexpr (Q3) {
+            D -= 4 * X;
+            if (DOTS && dots16) dots16[g] = D;
+            acc += A.fsc[g >> 1] * (fd * ((float)((int)sb - 32) * (float)D));
+        } else {
+            if (DOTS && dots16) dots16[g] = D;
+            acc += A.fsc[g >> 1] * ((fd * (float)(sb & 15u)) * (float)D - (fdm * (float)(sb >> 4)) * (float)X);
+        }
+    }
+    return acc;
+}
+
 // Q4_K parts use pair units where the host chose them for a small projection (units = ceil(K/64)
 // then exceeds the super-block count ceil(K/256); for K <= 64 the two forms are one).
 AH_DEV bool q4k_pair_units(const GemvPart &P) { return P.units > (P.n_in + 255) / 256; }
@@ -668,6 +739,10 @@ AH_DEV float comp_unit(const GemvPart &P, const uint8_t *tl, uint32_t row_off, u
         int32_t *dots = DOTS && P.dots ? P.dots + (size_t)row * nb32 : nullptr;
         if (PAIRS && q4k_pair_units(P)) return unit_q4p<DOTS>(tl, row_off + 144u * (u >> 2), u, P.n_in, A, dots);
         return unit_q4<DOTS>(tl, row_off + 144u * u, u, P.n_in, A, dots);
+    } else if constexpr (TYPE == AH_GGML_Q2_K || TYPE == AH_GGML_Q3_K) {
+        const uint32_t nb16 = (P.n_in + 15) / 16;
+        return unit_k23<TYPE, DOTS>(tl, row_off + (TYPE == AH_GGML_Q2_K ? 84u : 110u) * (u >> 1), u >> 1, u & 1u,
+                                    P.n_in, A, DOTS && P.dots ? P.dots + (size_t)row * nb16 : nullptr);
     } else {
         const uint32_t nb16 = (P.n_in + 15) / 16;
         return unit_q6<DOTS>(tl, row_off + 210u * (u >> 1), u >> 1, u & 1u, P.n_in, A,
@@ -1382,6 +1457,14 @@ __global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
                         acc += comp_unit<AH_GGML_Q5_0, DOTS, !PLAN>(P, tl, toff + r * RB, row, u, A);
+                } else if (P.type == AH_GGML_Q2_K) {
+#pragma unroll 1
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q2_K, DOTS, !PLAN>(P, tl, toff + r * RB, row, u, A);
+                } else if (P.type == AH_GGML_Q3_K) {
+#pragma unroll 1
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q3_K, DOTS, !PLAN>(P, tl, toff + r * RB, row, u, A);
                 } else {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
@@ -1621,6 +1704,14 @@ AH_DEV void seq_gemv_stage(const SeqArgs &a, uint32_t s, uint32_t r, bool &broke
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
                         acc += comp_unit<AH_GGML_Q5_0, false, true>(P, tl, toff + rr * RB, row, u, A);
+                } else if (P.type == AH_GGML_Q2_K) {
+#pragma unroll 1
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q2_K, false, true>(P, tl, toff + rr * RB, row, u, A);
+                } else if (P.type == AH_GGML_Q3_K) {
+#pragma unroll 1
+                    for (uint32_t u = g; u < U; u += G)
+                        acc += comp_unit<AH_GGML_Q3_K, false, true>(P, tl, toff + rr * RB, row, u, A);
                 } else {
 #pragma unroll 1
                     for (uint32_t u = g; u < U; u += G)
@@ -1748,6 +1839,8 @@ static const void *stream_fn(uint32_t type, bool plan, bool dots = false) {
     switch (type) {
     case AH_GGML_Q8_0: AH_SFN(AH_GGML_Q8_0)
     case AH_GGML_Q5_0: AH_SFN(AH_GGML_Q5_0)
+    case AH_GGML_Q2_K: AH_SFN(AH_GGML_Q2_K)
+    case AH_GGML_Q3_K: AH_SFN(AH_GGML_Q3_K)
     case AH_GGML_Q4_K: AH_SFN(AH_GGML_Q4_K)
     case AH_GGML_Q6_K: AH_SFN(AH_GGML_Q6_K)
     default: return nullptr;
@@ -1759,7 +1852,9 @@ static const void *seq_fn(uint32_t type) {
     switch (type) {
     case kMixedType: return reinterpret_cast<const void *>(&gemv_seq_kernel<kMixedType>);
     case AH_GGML_Q8_0: return reinterpret_cast<const void *>(&gemv_seq_kernel<AH_GGML_Q8_0>);
-    case AH_GGML_Q5_0: return reinterpret_cast<const void *>(&gemv_seq_kernel<kMixedType>);  // rare: no own form
+    case AH_GGML_Q5_0:  // rare families: no own form
+    case AH_GGML_Q2_K:
+    case AH_GGML_Q3_K: return reinterpret_cast<const void *>(&gemv_seq_kernel<kMixedType>);
     case AH_GGML_Q4_K: return reinterpret_cast<const void *>(&gemv_seq_kernel<AH_GGML_Q4_K>);
     case AH_GGML_Q6_K: return reinterpret_cast<const void *>(&gemv_seq_kernel<AH_GGML_Q6_K>);
     default: return nullptr;
@@ -1816,6 +1911,8 @@ hipError_t ah_launch_gemv_stream(uint32_t type, const StreamParts &sp, const Gem
     switch (type) {
     case AH_GGML_Q8_0: AH_SLAUNCH(AH_GGML_Q8_0) break;
     case AH_GGML_Q5_0: AH_SLAUNCH(AH_GGML_Q5_0) break;
+    case AH_GGML_Q2_K: AH_SLAUNCH(AH_GGML_Q2_K) break;
+    case AH_GGML_Q3_K: AH_SLAUNCH(AH_GGML_Q3_K) break;
     case AH_GGML_Q4_K: AH_SLAUNCH(AH_GGML_Q4_K) break;
     case AH_GGML_Q6_K: AH_SLAUNCH(AH_GGML_Q6_K) break;
     case kMixedType:
@@ -1838,6 +1935,8 @@ static const void *ffn_fn(uint32_t type) {
     switch (type) {
     case AH_GGML_Q8_0: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q8_0, false, false, true>);
     case AH_GGML_Q5_0: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q5_0, false, false, true>);
+    case AH_GGML_Q2_K: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q2_K, false, false, true>);
+    case AH_GGML_Q3_K: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q3_K, false, false, true>);
     case AH_GGML_Q4_K: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q4_K, false, false, true>);
     case AH_GGML_Q6_K: return reinterpret_cast<const void *>(&gemv_stream_kernel<AH_GGML_Q6_K, false, false, true>);
     default: return nullptr;
@@ -1866,6 +1965,14 @@ hipError_t ah_launch_ffn_gate_up(uint32_t type, const StreamParts &sp, const Ffn
         break;
     case AH_GGML_Q5_0:
         hipLaunchKernelGGL((gemv_stream_kernel<AH_GGML_Q5_0, false, false, true>), dim3(grid), dim3(kSThreads), lds,
+                           stream, sp, nullptr, nullptr, act_bytes, status, fa);
+        break;
+    case AH_GGML_Q2_K:
+        hipLaunchKernelGGL((gemv_stream_kernel<AH_GGML_Q2_K, false, false, true>), dim3(grid), dim3(kSThreads), lds,
+                           stream, sp, nullptr, nullptr, act_bytes, status, fa);
+        break;
+    case AH_GGML_Q3_K:
+        hipLaunchKernelGGL((gemv_stream_kernel<AH_GGML_Q3_K, false, false, true>), dim3(grid), dim3(kSThreads), lds,
                            stream, sp, nullptr, nullptr, act_bytes, status, fa);
         break;
     case AH_GGML_Q4_K:
@@ -1927,10 +2034,12 @@ hipError_t ah_gemv_init_attrs() {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     AH_ATTR(AH_GGML_Q8_0, 4) AH_ATTR(AH_GGML_Q8_0, 8) AH_ATTR(AH_GGML_Q8_0, 12)
     AH_ATTR(AH_GGML_Q5_0, 4) AH_ATTR(AH_GGML_Q5_0, 8) AH_ATTR(AH_GGML_Q5_0, 12)
+    AH_ATTR(AH_GGML_Q2_K, 4) AH_ATTR(AH_GGML_Q2_K, 8) AH_ATTR(AH_GGML_Q2_K, 12)
+    AH_ATTR(AH_GGML_Q3_K, 4) AH_ATTR(AH_GGML_Q3_K, 8) AH_ATTR(AH_GGML_Q3_K, 12)
     AH_ATTR(AH_GGML_Q4_K, 4) AH_ATTR(AH_GGML_Q4_K, 8) AH_ATTR(AH_GGML_Q4_K, 12)
     AH_ATTR(AH_GGML_Q6_K, 4) AH_ATTR(AH_GGML_Q6_K, 8) AH_ATTR(AH_GGML_Q6_K, 12)
 #undef AH_ATTR
-    for (uint32_t t : {AH_GGML_Q8_0, AH_GGML_Q5_0, AH_GGML_Q4_K, AH_GGML_Q6_K})
+    for (uint32_t t : {AH_GGML_Q8_0, AH_GGML_Q5_0, AH_GGML_Q2_K, AH_GGML_Q3_K, AH_GGML_Q4_K, AH_GGML_Q6_K})
         for (int v = 0; v < 3; ++v)
             if (e == hipSuccess)
                 e = hipFuncSetAttribute(stream_fn(t, v == 1, v == 2), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
@@ -1939,7 +2048,7 @@ hipError_t ah_gemv_init_attrs() {
             e = hipFuncSetAttribute(stream_fn(kMixedType, v == 1), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     for (uint32_t t : {(uint32_t)kMixedType, (uint32_t)AH_GGML_Q8_0, (uint32_t)AH_GGML_Q4_K, (uint32_t)AH_GGML_Q6_K})
         if (e == hipSuccess) e = hipFuncSetAttribute(seq_fn(t), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
-    for (uint32_t t : {AH_GGML_Q8_0, AH_GGML_Q5_0, AH_GGML_Q4_K, AH_GGML_Q6_K})
+    for (uint32_t t : {AH_GGML_Q8_0, AH_GGML_Q5_0, AH_GGML_Q2_K, AH_GGML_Q3_K, AH_GGML_Q4_K, AH_GGML_Q6_K})
         if (e == hipSuccess) e = hipFuncSetAttribute(ffn_fn(t), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     return e;
 }
@@ -1954,6 +2063,12 @@ hipError_t ah_launch_gemv(uint32_t type, const GemvPart &single, const GemvPart 
         break;
     case AH_GGML_Q5_0:
         launch_type<AH_GGML_Q5_0>(nc, dim3(grid), lds, stream, single, d_parts, d_wg_part, kpad_max, status);
+        break;
+    case AH_GGML_Q2_K:
+        launch_type<AH_GGML_Q2_K>(nc, dim3(grid), lds, stream, single, d_parts, d_wg_part, kpad_max, status);
+        break;
+    case AH_GGML_Q3_K:
+        launch_type<AH_GGML_Q3_K>(nc, dim3(grid), lds, stream, single, d_parts, d_wg_part, kpad_max, status);
         break;
     case AH_GGML_Q4_K:
         launch_type<AH_GGML_Q4_K>(nc, dim3(grid), lds, stream, single, d_parts, d_wg_part, kpad_max, status);

@@ -17,6 +17,8 @@
 // Types of 32-element blocks with one f16 scale each (Q8_0, Q5_0): one group per block, the same
 // unit, stage and split geometry in every kernel.
 constexpr bool ah_blk32(int t) { return t == AH_GGML_Q8_0 || t == AH_GGML_Q5_0; }
+// K-quant families with no GEMM form of their own (their prefill is one GEMV launch per token).
+constexpr bool ah_k23(int t) { return t == AH_GGML_Q2_K || t == AH_GGML_Q3_K; }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));

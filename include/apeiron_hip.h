@@ -1,6 +1,6 @@
 /*
  * apeiron_hip.h -- C ABI of the MI355X (gfx950) backend for apeiron's quantized
- * linear-layer path: GGUF block-quantized weights (Q8_0, Q5_0, Q4_K, Q6_K) times the
+ * linear-layer path: GGUF block-quantized weights (Q8_0, Q5_0, Q2_K, Q3_K, Q4_K, Q6_K) times the
  * power-of-two int8 activation quantizer, as a GEMV at decode (N = 1) and a GEMM at
  * prefill (N > 1).
  *
@@ -64,6 +64,8 @@ extern "C" {
 /* ggml type ids (format/quant.rs:20-49) */
 #define AH_GGML_Q5_0 6   /* format/quant.rs:28-29, :261-297 */
 #define AH_GGML_Q8_0 8
+#define AH_GGML_Q2_K 10  /* format/quant.rs:30-31, :308-386; GEMM: one GEMV launch per token */
+#define AH_GGML_Q3_K 11  /* format/quant.rs:32-33, :388-476; GEMM: one GEMV launch per token */
 #define AH_GGML_Q4_K 12
 #define AH_GGML_Q6_K 14
 

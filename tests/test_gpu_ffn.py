@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
 Q32 = 2.0 ** -32
-Q5_0, Q8_0, Q4_K, Q6_K = 6, 8, 12, 14
+Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q6_K = 6, 8, 10, 11, 12, 14
 
 
 @pytest.fixture(scope="module")
@@ -64,7 +64,7 @@ def scaled_payload(t, rng, n_out, n_in, scale):
     raw = synth.payload(t, rng, n_out, n_in).copy()
     qk, bb = synth.GEOM[t]
     blk = raw.reshape(-1, bb)
-    for off in ((0,) if t in (Q8_0, Q5_0) else (0, 2) if t == Q4_K else (208,)):
+    for off in (o for o in synth.SCALE_AT[t] if o is not None):
         d = blk[:, off:off + 2].copy().view(np.float16).astype(np.float32) * scale
         blk[:, off:off + 2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
     return raw
@@ -77,6 +77,8 @@ def scaled_payload(t, rng, n_out, n_in, scale):
     (Q8_0, Q8_0, 256, 300),     # ragged hidden width (a partial last block)
     (Q6_K, Q5_0, 512, 1000),
     (Q5_0, Q8_0, 96, 4000),     # several hidden blocks per workgroup
+    (Q3_K, Q2_K, 512, 1000),    # the K-quant families with no GEMM form of their own
+    (Q2_K, Q3_K, 256, 300),
 ])
 def test_ffn_vs_oracle(dev, gu_type, down_type, n_embd, n_ff):
     rng = synth.rng_for(11, n_ff + gu_type)

@@ -49,7 +49,7 @@ def gemv_q8(dev, w, codes, scales, dots=False):
     dc, ds = to_dev(codes), to_dev(scales)
     y = torch.empty(max(n_out, 1), dtype=torch.float32, device="cuda")
     if dots:
-        ng = -(-w.n_in // 16) if w.ggml_type == 14 else -(-w.n_in // 32)
+        ng = -(-w.n_in // 16) if w.ggml_type in (10, 11, 14) else -(-w.n_in // 32)
         dd = torch.full((max(n_out, 1), max(ng, 1)), -7, dtype=torch.int32, device="cuda")
         w.gemv_q8_dots_dev(ptr(dc), ptr(ds), ptr(y), ptr(dd), stream())
         assert dev.sync_status(stream()) == 0
@@ -199,7 +199,7 @@ def test_gemv_golden_fixtures(dev):
     assert n >= 40
 
 
-@pytest.mark.parametrize("t", [6, 8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 10, 11, 12, 14])
 @pytest.mark.parametrize("n_out,n_in", [(4864, 896), (896, 4864), (128, 896), (333, 1536), (37, 8960), (5, 100),
                                          (301, 300), (2001, 576), (7, 32768), (9, 20000)])
 def test_gemv_config_shapes(dev, t, n_out, n_in):
@@ -434,7 +434,7 @@ def gemm_check(dev, t, n_out, n_in, n_tok, sample_cols=None, seed=0):
     return Y
 
 
-@pytest.mark.parametrize("t", [6, 8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 10, 11, 12, 14])
 @pytest.mark.parametrize("n_out,n_in,n_tok", [(64, 256, 8), (96, 300, 33), (200, 896, 130), (33, 64, 2)])
 def test_gemm_small_shapes(dev, t, n_out, n_in, n_tok):
     gemm_check(dev, t, n_out, n_in, n_tok)
@@ -518,7 +518,7 @@ def test_mfma_probe_within_published_peaks(dev):
         dev.probe_mfma_peak(2)
 
 
-@pytest.mark.parametrize("t", [6, 8, 12, 14])
+@pytest.mark.parametrize("t", [6, 8, 10, 11, 12, 14])
 @pytest.mark.parametrize("n_out,n_in,n_tok", [(96, 301, 5), (130, 8960, 70), (64, 20000, 3), (256, 1536, 129)])
 def test_gemm_codes_input_equals_f32_input(dev, t, n_out, n_in, n_tok):
     """The codes-input GEMM (quantizer output handed over) equals the f32-input GEMM bit for bit:
@@ -557,6 +557,21 @@ def test_mixed_type_plan_matches_single_launches(dev):
              (14, 1536, 8960), (12, 1536, 8960), (8, 300, 896), (14, 5000, 1536), (8, 77, 7680),
              (12, 129, 300), (14, 33, 256)]
     _plan_vs_singles(dev, [t for t, _, _ in parts], [(n, k) for _, n, k in parts], 91)
+
+
+def test_mixed_type_plan_with_q2_k_q3_k(dev):
+    """Q2_K and Q3_K parts beside Q4_K / Q6_K / Q8_0 ones in one mixed-type launch (ragged widths
+    included): each part's output equals its own single-type launch bit for bit."""
+    parts = [(10, 1536, 1536), (11, 256, 1536), (12, 256, 1536), (14, 300, 896), (11, 77, 300),
+             (10, 33, 4864), (8, 129, 896)]
+    _plan_vs_singles(dev, [t for t, _, _ in parts], [(n, k) for _, n, k in parts], 92)
+
+
+@pytest.mark.parametrize("t", [10, 11])
+def test_plan_q2_k_q3_k_single_type(dev, t):
+    """Single-type argument plans (up to four parts) and table plans of Q2_K / Q3_K projections."""
+    _plan_vs_singles(dev, t, [(896, 896), (128, 896), (4864, 896)], 93 + t)
+    _plan_vs_singles(dev, t, [(896, 896), (128, 896), (128, 896), (896, 896), (4864, 896), (896, 4864)], 95 + t)
 
 
 def test_mixed_type_plan_refuses_rows_past_the_stream_tile(dev):

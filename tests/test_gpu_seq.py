@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
 Q32 = 2.0 ** -32
-Q5_0, Q8_0, Q4_K, Q6_K = 6, 8, 12, 14
+Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q6_K = 6, 8, 10, 11, 12, 14
 ONE = 1 << 32
 
 
@@ -66,7 +66,7 @@ def small_payload(t, rng, n_out, n_in, scale):
     raw = synth.payload(t, rng, n_out, n_in).copy()
     qk, bb = synth.GEOM[t]
     blk = raw.reshape(-1, bb)
-    for off in ((0,) if t in (Q8_0, Q5_0) else (0, 2) if t == Q4_K else (208,)):
+    for off in (o for o in synth.SCALE_AT[t] if o is not None):
         d = blk[:, off:off + 2].copy().view(np.float16).astype(np.float32) * scale
         blk[:, off:off + 2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
     return raw
@@ -118,7 +118,7 @@ def ffn_case(dev, rng, n_embd, n_ff, down_type, sigma=1.0 / 32):
 
 
 @pytest.mark.parametrize("n_embd,n_ff,down_type", [(1536, 8960, Q6_K), (896, 4864, Q4_K), (256, 300, Q8_0),
-                                                    (896, 4864, Q5_0)])
+                                                    (896, 4864, Q5_0), (512, 1000, Q3_K)])
 def test_seq_fused_ffn_vs_oracle(dev, n_embd, n_ff, down_type):
     rng = synth.rng_for(9, n_ff)
     raws, W = ffn_case(dev, rng, n_embd, n_ff, down_type)

@@ -1274,8 +1274,9 @@ AH_DEV void ffn_epilogue(const FfnArgs &fa, uint32_t b0, uint32_t b1, const floa
 // FFN: the fused FFN's gate/up launch (argument parts 0 = gate, 1 = up; FfnArgs): workgroup w
 // serves hidden blocks [w * blocks_per_wg, +blocks_per_wg), waves 0-3 its gate rows and waves 4-7
 // its up rows; the row sums also go to LDS, and the SwiGLU epilogue writes the hidden QuantAct.
+// (The fused FFN's Q6_K form is built for 2 waves per SIMD: at 4 it spilled 16 bytes a lane.)
 template <int TYPE, bool PLAN, bool DOTS, bool FFN = false>
-__global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>())
+__global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : stream_waves_per_simd<TYPE>())
     gemv_stream_kernel(StreamParts sp, const GemvPart *__restrict__ parts,
                        const StreamWG *__restrict__ wgd, uint32_t act_bytes,
                        unsigned long long *status, FfnArgs fa) {
@@ -1756,8 +1757,11 @@ AH_DEV void seq_swiglu_stage(const SeqArgs &a, uint32_t s, uint32_t r, bool &bro
     seq_signal(a, s);
 }
 
+// Built for 2 waves per SIMD (one resident workgroup per CU, <= 256 VGPRs): at 4 the Q4_K and
+// Q6_K forms spilled ~100 bytes a lane, and the configs[4] token measured the same either way
+// (827-829 us).
 template <int TYPE>
-__global__ void __launch_bounds__(kSThreads, stream_waves_per_simd<TYPE>()) gemv_seq_kernel(SeqArgs a) {
+__global__ void __launch_bounds__(kSThreads, 2) gemv_seq_kernel(SeqArgs a) {
     // this launch's run number (nothing writes the counter until the workgroup ends)
     const uint32_t r = __builtin_amdgcn_readfirstlane(
         __hip_atomic_load(a.runs + blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1);

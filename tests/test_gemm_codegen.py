@@ -164,3 +164,12 @@ def test_no_packed_fp32_instructions(gemm_asm, gemv_asm):
     for asm in (gemm_asm, gemv_asm):
         bad = [l.strip() for l in asm if re.match(r"\s*v_pk_(add|mul|fma)_f32\b", l)]
         assert not bad, bad[:5]
+
+
+def test_no_kernel_spills(gemm_asm, gemv_asm):
+    """No kernel of either translation unit keeps registers in scratch memory: each kernel's
+    `.private_segment_fixed_size` is 0 (a spill would add scratch traffic to every launch)."""
+    for asm in (gemm_asm, gemv_asm):
+        sizes = [int(m.group(1)) for l in asm if (m := re.match(r"\s*\.private_segment_fixed_size:\s*(\d+)", l))]
+        assert len(sizes) >= 10
+        assert max(sizes) == 0, [s for s in sizes if s]

@@ -63,7 +63,8 @@ def drive(tmp_path, t, raw, n_out, n_in, codes, scales, x):
     return read_out(fo, n_out, n_in, codes.shape[0])
 
 
-@pytest.mark.parametrize("t,n_out,n_in", [(6, 100, 896), (8, 77, 300), (12, 64, 896), (14, 50, 1536)])
+@pytest.mark.parametrize("t,n_out,n_in", [(6, 100, 896), (8, 77, 300), (10, 40, 300), (11, 64, 1536), (12, 64, 896),
+                                         (14, 50, 1536)])
 def test_driver_host_forms_vs_oracle(tmp_path, t, n_out, n_in):
     rng = synth.rng_for(7, 1000 * t + n_in)
     raw = synth.payload(t, rng, n_out, n_in)

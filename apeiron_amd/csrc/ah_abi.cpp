@@ -276,7 +276,10 @@ uint32_t deal_wgs(GemvPart *parts, size_t n, uint64_t target, bool stream) {
         double load;
         uint32_t i;
     };
-    Item *heap = static_cast<Item *>(std::malloc(n * sizeof(Item)));
+    // argument-part launches (up to 4 parts) keep the heap on the stack: the no-alloc GEMM's
+    // Q2_K / Q3_K route comes through here
+    Item local[4];
+    Item *heap = n <= 4 ? local : static_cast<Item *>(std::malloc(n * sizeof(Item)));
     if (!heap) return 0;
     size_t hn = 0;
     auto tiles_of = [](const GemvPart &P) -> double {
@@ -322,7 +325,7 @@ uint32_t deal_wgs(GemvPart *parts, size_t n, uint64_t target, bool stream) {
         ++used;
         if (P.wg_count < cap_of(P)) push({tiles_of(P) / P.wg_count, it.i});
     }
-    std::free(heap);
+    if (heap != local) std::free(heap);
     uint32_t wg = 0;
     for (size_t i = 0; i < n; ++i) {
         parts[i].wg_begin = wg;
@@ -513,14 +516,39 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                                          pick(ctx, stream)));
             codes = static_cast<const int8_t *>(ctx->scratch);
         }
+        auto x_of = [&](size_t c) -> const void * {
+            return src == AH_SRC_F32 ? static_cast<const void *>(static_cast<const float *>(x) + c * n_in_sz)
+                                     : static_cast<const void *>(codes + c * pitch);
+        };
+        const uint32_t kp = kpad_of(n_in_sz);
+        AH_HIP(ctx, hipSetDevice(ctx->device));
         for (size_t i = 0; i < n_parts; ++i) {
-            if (!ah_k23((int)w[i]->type)) continue;
-            for (size_t c = 0; c < n_tok; ++c) {
-                const void *xc = src == AH_SRC_F32 ? static_cast<const void *>(static_cast<const float *>(x) + c * n_in_sz)
-                                                   : static_cast<const void *>(codes + c * pitch);
-                const int32_t st = gemv_launch(ctx, w[i], src, xc, src == AH_SRC_CODES ? scales_in + c * nb : nullptr,
-                                               y[i] + c * w[i]->n_out, nullptr, stream);
-                if (st) return st;
+            if (!ah_k23((int)w[i]->type) || w[i]->n_out == 0) continue;
+            // rows that fit the streaming kernel's tile: four tokens per launch, as the argument
+            // parts of one launch (each workgroup quantizes its own token's activation), so each
+            // launch fills more of the device and the weight rows are re-read from L2
+            bool stream_ok = false;
+            (void)make_part(w[i], src, x_of(0), nullptr, y[i], nullptr, stream_ok);
+            for (size_t c = 0; c < n_tok;) {
+                if (!stream_ok) {
+                    const int32_t st = gemv_launch(ctx, w[i], src, x_of(c), src == AH_SRC_CODES ? scales_in + c * nb : nullptr,
+                                                   y[i] + c * w[i]->n_out, nullptr, stream);
+                    if (st) return st;
+                    ++c;
+                    continue;
+                }
+                StreamParts sp = {};
+                sp.n = (uint32_t)(n_tok - c < 4 ? n_tok - c : 4);
+                for (uint32_t j = 0; j < sp.n; ++j) {
+                    bool st_j = false;
+                    sp.p[j] = make_part(w[i], src, x_of(c + j), src == AH_SRC_CODES ? scales_in + (c + j) * nb : nullptr,
+                                        y[i] + (c + j) * w[i]->n_out, nullptr, st_j);
+                }
+                const uint32_t grid = deal_wgs(sp.p, sp.n, resident_wgs(ctx, w[i]->type, true, kp), true);
+                if (grid == 0) return AH_ERR_OUT_OF_MEMORY;
+                AH_HIP(ctx, ah_launch_gemv_stream(w[i]->type, sp, nullptr, nullptr, grid,
+                                                  (uint32_t)ah_gemv_act_bytes(kp), ctx->d_status, pick(ctx, stream)));
+                c += sp.n;
             }
         }
         if (n23 == n_parts) return AH_OK;

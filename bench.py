@@ -22,7 +22,7 @@ warm-up steps, then the K timed steps between two synchronizations.
 Also reported, beside the value:
   roofline      the token's dominant kernel (the Q4_K stage launches, o / gate-up / Q4_K down:
                 most of a token's time) against the 8 TB/s HBM peak, HIP events on the launch
-                stream over those launches back to back;
+                stream around replays of one graph of those launches in token order;
   decode        the same token as eager launches; with the fused FFN in launch form (gate/up with
                 the exact SwiGLU + hidden requantize in one launch, down from the hidden codes:
                 the FFN's real data dependency); as one persistent launch (ah_seq_*, with and
@@ -33,6 +33,8 @@ Also reported, beside the value:
                 designs, int8 and f16), the MFMA-only probe, and the configs[4] N = 512 prefill
                 (--only gemm3: the configs[3] GEMMs alone, for profiling);
   heads         configs[0] (Q8_0 4864x896) and configs[2] (151936x896 head, Q6_K and Q8_0);
+  families      Q5_0, Q2_K and Q3_K: a 151936x896 launch (bandwidth), a 4864x896 launch
+                (latency) and the N = 512 GEMM at 4864x896;
   cpu_baseline  the restated reference fast path (oracle/ah_cpu_fast.c: AVX-VNNI or AVX2 dots,
                 two-row tiles) on the same token's projections, on this host's cores;
                 cpu_baseline_gemm the same for N = 512.
@@ -133,7 +135,8 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=8)
     ap.add_argument("--no-seq", action="store_true",
                     help="skip the persistent (cooperative-launch) token forms of the decode extras")
-    ap.add_argument("--only", choices=["decode", "gemm", "gemm3", "config1", "heads", "copy"], default=None)
+    ap.add_argument("--only", choices=["decode", "gemm", "gemm3", "config1", "heads", "families", "copy"],
+                    default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
@@ -521,6 +524,53 @@ def main() -> int:
             del wc
         result["heads"] = singles
 
+    # ---- the other weight families (Q5_0, Q2_K, Q3_K): a vocab-head-shaped launch (bandwidth) and a
+    # configs[0]-shaped one (latency) over rotating copies, and the N = 512 GEMM at 4864x896 (Q5_0 on
+    # its f16-MFMA form; Q2_K / Q3_K one GEMV launch per token, as the reference serves them)
+    if args.only in (None, "families") and not args.no_heads and not args.no_extras:
+        fam = []
+        for gt in (synth.Q5_0, synth.Q2_K, synth.Q3_K):
+            row = {"type": synth.NAMES[gt]}
+            for key, n_out, n_in in (("head", 151936, 896), ("single", 4864, 896)):
+                raw = synth.payload(gt, synth.rng_for(6, gt + n_out), n_out, n_in)
+                copies = max(2, -(-int(1.1 * 2 ** 30) // raw.nbytes))
+                wc = [dev.upload(gt, raw, n_out, n_in) for _ in range(copies)]
+                del raw
+                x = torch.from_numpy(synth.activations(synth.rng_for(6, 99), n_in)).cuda()
+                y = torch.empty(n_out, dtype=torch.float32, device="cuda")
+                ctr = [0]
+
+                def one():
+                    wc[ctr[0] % copies].gemv_f32_dev(ptr(x), ptr(y), sh)
+                    ctr[0] += 1
+                clock_up(one, 0.05)
+                assert dev.sync_status(sh) == 0
+                us = event_us(one, 400 if n_out < 100000 else 60)
+                nbytes = proj_bytes(synth, gt, n_out, n_in)
+                row[key] = {"shape": [n_out, n_in], "us": round(us, 2), "bytes": nbytes,
+                            "gbs": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+                log(f"[bench] {synth.NAMES[gt]} {n_out}x{n_in}: {us:.2f} us/launch, {nbytes / us / 1e3:.0f} GB/s")
+                for w in wc:
+                    w.free()
+                del wc
+            n_tok, n_out, n_in = 512, 4864, 896
+            raw = synth.payload(gt, synth.rng_for(6, gt), n_out, n_in)
+            w = dev.upload(gt, raw, n_out, n_in)
+            x = torch.from_numpy(synth.activations(synth.rng_for(6, 5), n_in, n_tok).reshape(n_tok, n_in)).cuda()
+            y = torch.empty((n_tok, n_out), dtype=torch.float32, device="cuda")
+            run = lambda: w.gemm_f32_dev(ptr(x), n_tok, ptr(y), sh)
+            clock_up(run, 0.03)
+            assert dev.sync_status(sh) == 0
+            us = event_us(run, 10)
+            tops = 2.0 * n_tok * n_out * n_in / us / 1e6
+            row["gemm"] = {"shape": [n_out, n_in], "n_tok": n_tok, "us": round(us, 2), "tops": round(tops, 1),
+                           "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                           "form": "f16 MFMA" if gt == synth.Q5_0 else "one GEMV launch per token"}
+            log(f"[bench] gemm {synth.NAMES[gt]} {n_out}x{n_in} N{n_tok}: {us:.1f} us {tops:.0f} TOPS")
+            w.free()
+            fam.append(row)
+        result["families"] = fam
+
     # ---- CPU baselines: the same token (and N = 512 sample) on the host ---------------------------
     if run_decode and not args.no_cpu:
         import oracle
@@ -624,6 +674,7 @@ def main() -> int:
         "mfma_probe": result.get("mfma_probe"),
         "config1": result.get("config1"),
         "config0_config2": result.get("heads"),
+        "families": result.get("families"),
         "cpu_baseline_gemm": result.get("cpu_baseline_gemm"),
     }
     print(json.dumps(line))

@@ -64,3 +64,19 @@ def test_noalloc_gemm_refuses_past_its_scratch(dev):
     st = dev.lib.ah_gemm_f32_noalloc_dev(dev.h, w.h, x.data_ptr(), n_tok, y.data_ptr(), None)
     assert st == 24  # AH_ERR_SCRATCH_LIMIT, before anything is enqueued
     w.free()
+
+
+@pytest.mark.parametrize("t", [10, 11])
+def test_noalloc_gemm_q2_k_q3_k_route(dev, t):
+    """The Q2_K / Q3_K prefill route (GEMV launches of four tokens' argument parts) through the
+    no-alloc entry point equals the ordinary one bit for bit, on two calls in a row, the second
+    with a smaller input."""
+    L = dev.lib
+    for n_out, n_in, n_tok in ((300, 896, 9), (64, 512, 3)):
+        rng = synth.rng_for(12, t * 10 + n_tok)
+        w = dev.upload(t, synth.payload(t, rng, n_out, n_in), n_out, n_in)
+        x = torch.from_numpy(synth.activations(rng, n_in, n_tok).reshape(n_tok, n_in)).cuda()
+        y1 = run(dev, L.ah_gemm_f32_dev, w, x)
+        y2 = run(dev, L.ah_gemm_f32_noalloc_dev, w, x)
+        assert torch.isfinite(y1).all() and torch.equal(y1, y2)
+        w.free()

@@ -683,11 +683,11 @@ AH_DEV float unit_k23(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, u
         sw[1] = V(2 * n + 1);
     }
     constexpr int kQs = Q3 ? 8 : 4;  // dword of qs[0]
-    uint32_t q[8], hm[8];
+    uint32_t q[8], hn[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         q[i] = V(kQs + 8 * (int)n + i);
-        hm[i] = Q3 ? V(i) : 0u;
+        hn[i] = Q3 ? V(i) >> (4 * n) : 0u;  // this half's four hmask bits of each byte, at bits 0-3
     }
     const uint32_t nb16 = (n_in + 15) / 16;
     float acc = 0.0f;
@@ -698,13 +698,22 @@ AH_DEV float unit_k23(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, u
         if (DOTS && g >= nb16) break;
         const u32x4 xv = *reinterpret_cast<const u32x4 *>(A.codes + pad_k(16 * g));
         const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+        // Bit pairs r = 1, 2 are masked in place: each byte then holds its value times 4^r (at most
+        // 7 * 16 = 112, still a positive int8), so the dot is 4^r D exactly and one shift recovers
+        // D; pair 3 is shifted down first (in place it would read as negative bytes).  Q3_K's
+        // hmask bit goes to the bit above the pair (hn: the half's bits moved to bits 0-3).
         int32_t D = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            uint32_t v = (q[4 * pl + i] >> (2 * r)) & 0x03030303u;
-            if constexpr (Q3) v |= ((hm[4 * pl + i] >> (4 * n + r)) & 0x01010101u) << 2;
+            const uint32_t qw = q[4 * pl + i];
+            uint32_t v = r == 3 ? (qw >> 6) & 0x03030303u : qw & (0x03030303u << (2 * r));
+            if constexpr (Q3) {
+                const uint32_t hb = hn[4 * pl + i] & (0x01010101u << r);
+                v |= r == 3 ? hb >> 1 : hb << (r + 2);
+            }
             D = ah_sdot4(v, xw[i], D);
         }
+        if (r == 1 || r == 2) D >>= 2 * r;
         const int32_t X = A.xs16[g];
         const uint32_t sb = (sw[j >> 2] >> (8 * (j & 3))) & 0xffu;
         if constexpr (Q3) {

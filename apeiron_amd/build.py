@@ -59,6 +59,12 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{out}")
     if verbose and out.strip():
         print(out)
+    # A kernel whose host stub clang did not emit leaves an undefined __device_stub__ symbol: the
+    # library would link and then fail to load.  Refuse it here.
+    nm = subprocess.run(["nm", "-u", tmp], capture_output=True, text=True)
+    missing = [l.split()[-1] for l in nm.stdout.splitlines() if "__device_stub__" in l]
+    if missing:
+        raise RuntimeError(f"kernel host stubs missing from the build: {missing}")
     os.replace(tmp, LIB)
     build_driver(verbose=verbose)
     return LIB

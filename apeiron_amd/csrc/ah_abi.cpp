@@ -39,16 +39,17 @@ hipError_t ah_launch_gemv_seq(uint32_t type, const SeqArgs &a, uint32_t grid, hi
 hipError_t ah_launch_scan(const uint8_t *w, uint64_t n_blocks, uint32_t block_bytes, uint32_t off0,
                           uint32_t off1, unsigned long long *d_bad, hipStream_t stream);
 hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_in,
-                          uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xmin,
+                          uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xf, const _Float16 *xmin,
+                          const _Float16 *xmin16,
                           const float *tok_scale, const int8_t *fcodes, const int64_t *fscales,
                           const int8_t *xc, const uint32_t *xsp,
                           unsigned long long *status, uint32_t form, hipStream_t stream);
 hipError_t ah_launch_splitk_reduce(uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_tok,
                                    const float *tok_scale, unsigned long long *status, hipStream_t stream);
 uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
-                             uint32_t cus, bool int8);
+                             uint32_t cus, uint32_t kind);
 uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits,
-                          bool int8);
+                          uint32_t kind);
 uint32_t ah_gemm_max_parts(uint32_t type);
 uint32_t ah_gemm_pick_waves(uint32_t type, uint64_t n_wg4, uint32_t cus, bool int8);
 hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream);
@@ -73,7 +74,7 @@ struct ah_ctx {
     int last_hip = 0;
     uint32_t last_bad_bits = 0;  // f16 bits behind the last AH_ERR_NONFINITE_SCALE
     int cu_count = 256;
-    uint32_t q8_design = AH_GEMM_DESIGN_AUTO;  // Q8_0 GEMM design (ah_set_gemm_design)
+    uint32_t design[32] = {};  // GEMM design per GGUF type (ah_set_gemm_design; 0 = AUTO)
     void *scratch = nullptr;  // device scratch for GEMM operands / host-form staging
     size_t scratch_bytes = 0;
     // streaming-GEMV occupancy by (type, LDS bytes): a runtime query per launch costs more host
@@ -494,11 +495,25 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     if (!x && n_tok && n_in_sz) return AH_ERR_INVALID_ARG;
     if (n_tok == 0) return AH_OK;
     if (n_tok >= (1ull << 24)) return AH_ERR_INVALID_ARG;
-    // Q2_K / Q3_K parts take one GEMV launch per token, as matmat_q8act serves these families one
-    // column at a time (kern/matmat.rs:392-413); the other parts then go through the GEMM below.
-    // Nothing is allocated on this route (parts past kStackParts aside).
+    // The design of each part's type (ah_set_gemm_design): Q8_0 parts take the int8-MFMA design
+    // when it is selected, the operand pass then writing int8 codes and block factors (and the f16
+    // operand only if another part needs it); Q4_K parts may take the dequantize-once tiles.
+    auto kind_of = [&](uint32_t type) -> uint32_t {
+        const uint32_t d = type < 32 ? ctx->design[type] : 0u;
+        if (type == AH_GGML_Q8_0 && d == AH_GEMM_DESIGN_INT8) return kGemmKindI8;
+        if (type == AH_GGML_Q4_K && d == AH_GEMM_DESIGN_F16_TILE) return kGemmKindTile;
+        // Q2_K / Q3_K: the tiles are their only MFMA design (AH_GEMM_DESIGN_F16 keeps the
+        // per-token GEMV route)
+        if (ah_k23((int)type) && d != AH_GEMM_DESIGN_F16) return kGemmKindTile;
+        return kGemmKindRb;
+    };
+    // Q2_K / Q3_K parts whose design is AH_GEMM_DESIGN_F16 take GEMV launches of a few tokens
+    // each, as matmat_q8act serves these families one column at a time (kern/matmat.rs:392-413);
+    // the other parts then go through the GEMM below.  Nothing is allocated on this route (parts
+    // past kStackParts aside).  By default these families take the dequantize-once MFMA tiles.
+    auto gemv23 = [&](const ah_tensor *t) { return ah_k23((int)t->type) && kind_of(t->type) != kGemmKindTile; };
     size_t n23 = 0;
-    for (size_t i = 0; i < n_parts; ++i) n23 += ah_k23((int)w[i]->type) ? 1 : 0;
+    for (size_t i = 0; i < n_parts; ++i) n23 += gemv23(w[i]) ? 1 : 0;
     if (n23) {
         const size_t nb = (n_in_sz + 31) / 32;
         // the GEMV reads codes a dword at a time: token rows of codes whose length is not a multiple
@@ -523,7 +538,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         const uint32_t kp = kpad_of(n_in_sz);
         AH_HIP(ctx, hipSetDevice(ctx->device));
         for (size_t i = 0; i < n_parts; ++i) {
-            if (!ah_k23((int)w[i]->type) || w[i]->n_out == 0) continue;
+            if (!gemv23(w[i]) || w[i]->n_out == 0) continue;
             // rows that fit the streaming kernel's tile: four tokens per launch, as the argument
             // parts of one launch (each workgroup quantizes its own token's activation), so each
             // launch fills more of the device and the weight rows are re-read from L2
@@ -565,7 +580,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         float **ry = n_parts > kStackParts ? ry_heap.data() : ry_stack;
         size_t k = 0;
         for (size_t i = 0; i < n_parts; ++i)
-            if (!ah_k23((int)w[i]->type)) {
+            if (!gemv23(w[i])) {
                 rw[k] = w[i];
                 ry[k++] = y[i];
             }
@@ -574,15 +589,12 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     const uint32_t n_in = (uint32_t)n_in_sz, N = (uint32_t)n_tok;
     const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
     const uint32_t cus = (uint32_t)ctx->cu_count;
-    // Q8_0 parts take the int8-MFMA design when it is selected (the f16 design, the faster one
-    // measured, is the default); the operand pass then writes int8 codes and block factors, and
-    // the f16 operand only if another part needs it
-    const bool q8_int8 = ctx->q8_design == AH_GEMM_DESIGN_INT8;
-    bool any_int8 = false, any_f16 = false;
+    bool any_int8 = false, any_f16 = false, any_tile = false;
     for (size_t i = 0; i < n_parts; ++i) {
-        const bool i8p = q8_int8 && w[i]->type == AH_GGML_Q8_0;
-        any_int8 = any_int8 || i8p;
-        any_f16 = any_f16 || !i8p;
+        const uint32_t k = kind_of(w[i]->type);
+        any_int8 = any_int8 || k == kGemmKindI8;
+        any_f16 = any_f16 || k == kGemmKindRb;
+        any_tile = any_tile || k == kGemmKindTile;
     }
     // every split part has its own partials region: the parts of a launch run together and the
     // reduction reads them all at the end
@@ -605,9 +617,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         d.w_bytes = (uint32_t)w[i]->bytes;
         d.row_bytes = (uint32_t)w[i]->row_bytes;
         d.n_out = (uint32_t)w[i]->n_out;
-        d.splits = d.n_out ? ah_gemm_pick_splits(w[i]->type, d.n_out, n_in, N, cus,
-                                                 q8_int8 && w[i]->type == AH_GGML_Q8_0)
-                           : 1;
+        d.splits = d.n_out ? ah_gemm_pick_splits(w[i]->type, d.n_out, n_in, N, cus, kind_of(w[i]->type)) : 1;
         d.y = y[i];
         d.partials = nullptr;
         if (d.splits > 1) {
@@ -618,10 +628,15 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
 
     size_t off = 0;
     const size_t o_xh = off; off = align256(off + (any_f16 ? (size_t)N * kpad * 2 : 0));
+    // fragment order: whole 32-token blocks (the rows past n_tok are never stored from)
+    const size_t o_xf = off; off = align256(off + (any_tile ? (size_t)((N + 31) / 32 * 32) * kpad * 2 : 0));
     const size_t o_xc = off; off = align256(off + (any_int8 ? (size_t)N * kpad : 0));
     const size_t o_xsp = off; off = align256(off + (any_int8 ? (size_t)N * (kpad / 32) * 4 : 0));
     const size_t o_ts = off; off = align256(off + (size_t)N * 4);
     const size_t o_xmin = off; off = align256(off + (any_q4k ? (size_t)N * nsb * 32 : 0));
+    bool any_k23 = false;
+    for (size_t i = 0; i < n_parts; ++i) any_k23 = any_k23 || ah_k23((int)w[i]->type);
+    const size_t o_xmin16 = off; off = align256(off + (any_k23 ? (size_t)N * nsb * 32 : 0));
     // flagged tokens' QuantAct (f32 input; codes input is read in place)
     const bool keep = src == AH_SRC_F32;
     const size_t o_fc = off; off = align256(off + (keep ? (size_t)N * n_in : 0));
@@ -636,10 +651,12 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         S = static_cast<uint8_t *>(ctx->scratch);
     }
     _Float16 *xh = any_f16 ? reinterpret_cast<_Float16 *>(S + o_xh) : nullptr;
+    _Float16 *xf = any_tile ? reinterpret_cast<_Float16 *>(S + o_xf) : nullptr;
     int8_t *xc = any_int8 ? reinterpret_cast<int8_t *>(S + o_xc) : nullptr;
     uint32_t *xsp = any_int8 ? reinterpret_cast<uint32_t *>(S + o_xsp) : nullptr;
     float *ts = reinterpret_cast<float *>(S + o_ts);
     _Float16 *xmin = reinterpret_cast<_Float16 *>(S + o_xmin);
+    _Float16 *xmin16 = any_k23 ? reinterpret_cast<_Float16 *>(S + o_xmin16) : nullptr;
     int8_t *fcodes = keep ? reinterpret_cast<int8_t *>(S + o_fc) : static_cast<int8_t *>(const_cast<void *>(x));
     int64_t *fscales = keep ? reinterpret_cast<int64_t *>(S + o_fs) : const_cast<int64_t *>(scales_in);
     for (size_t i = 0; i < n_parts; ++i)
@@ -652,8 +669,10 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     o.x = x;
     o.scales = scales_in;
     o.xh = xh;
+    o.xf = xf;
     o.tok_scale = ts;
     o.xmin = any_q4k ? xmin : nullptr;
+    o.xmin16 = xmin16;
     o.fcodes = keep ? fcodes : nullptr;
     o.fscales = keep ? fscales : nullptr;
     o.xc = xc;
@@ -676,6 +695,18 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         GemmPartDesc run[kGemmMaxParts];
         uint32_t nr = 0;
         uint64_t wg4 = 0;
+        if (kind_of(type) == kGemmKindTile) {
+            // dequantize-once tiles: runs of up to four parts of this type
+            for (; i < n_parts && nr < kGemmMaxParts; ++i) {
+                if (pd[i].n_out == 0) continue;
+                if (w[i]->type != type) break;
+                run[nr++] = pd[i];
+                any_split = any_split || pd[i].splits > 1;
+            }
+            AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp,
+                                       ctx->d_status, kFormTile, s));
+            continue;
+        }
         // K-quant parts of both types (q/k beside v) share one grid when together they leave CUs
         // idle: one run of consecutive Q4_K/Q6_K parts, if it holds both types and its 4-wave
         // grid is at most two workgroups per CU; otherwise runs of one type
@@ -685,8 +716,9 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
             for (size_t j = i; j < n_parts && k < kGemmMaxParts; ++j) {
                 if (pd[j].n_out == 0) continue;
                 if (w[j]->type != AH_GGML_Q4_K && w[j]->type != AH_GGML_Q6_K) break;
+                if (kind_of(w[j]->type) != kGemmKindRb) break;
                 types |= w[j]->type == AH_GGML_Q4_K ? 1u : 2u;
-                g4 += ah_gemm_part_wg4(w[j]->type, pd[j].n_out, n_in, N, pd[j].splits, false);
+                g4 += ah_gemm_part_wg4(w[j]->type, pd[j].n_out, n_in, N, pd[j].splits, kGemmKindRb);
                 ++k;
             }
             if (types == 3u && g4 <= 2ull * cus) type = kGemmMixedKQuant;
@@ -695,18 +727,18 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         for (; i < n_parts && nr < max_run; ++i) {
             if (pd[i].n_out == 0) continue;
             const bool fits = type == kGemmMixedKQuant
-                                  ? (w[i]->type == AH_GGML_Q4_K || w[i]->type == AH_GGML_Q6_K)
+                                  ? ((w[i]->type == AH_GGML_Q4_K || w[i]->type == AH_GGML_Q6_K) &&
+                                     kind_of(w[i]->type) == kGemmKindRb)
                                   : w[i]->type == type;
             if (!fits) break;
             run[nr++] = pd[i];
-            wg4 += ah_gemm_part_wg4(w[i]->type, pd[i].n_out, n_in, N, pd[i].splits,
-                                    q8_int8 && w[i]->type == AH_GGML_Q8_0);
+            wg4 += ah_gemm_part_wg4(w[i]->type, pd[i].n_out, n_in, N, pd[i].splits, kind_of(w[i]->type));
             any_split = any_split || pd[i].splits > 1;
         }
         const uint32_t form = type == kGemmMixedKQuant
                                   ? kForm4x4
-                                  : ah_gemm_pick_waves(type, wg4, cus, q8_int8 && type == AH_GGML_Q8_0);
-        AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xmin, ts, fcodes, fscales, xc, xsp,
+                                  : ah_gemm_pick_waves(type, wg4, cus, kind_of(type) == kGemmKindI8);
+        AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp,
                                    ctx->d_status, form, s));
     }
     if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd, N, ts, ctx->d_status, s));
@@ -1404,11 +1436,13 @@ int32_t ah_gemm_f32_noalloc_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_
 }
 
 int32_t ah_set_gemm_design(ah_ctx *ctx, uint32_t ggml_type, uint32_t design) {
-    if (!ctx || design > AH_GEMM_DESIGN_INT8) return AH_ERR_INVALID_ARG;
+    if (!ctx || design > AH_GEMM_DESIGN_F16_TILE) return AH_ERR_INVALID_ARG;
     size_t qk = 0, bb = 0;
-    if (!geom(ggml_type, qk, bb)) return AH_ERR_UNSUPPORTED_QUANT;
-    if (ggml_type != AH_GGML_Q8_0) return design == AH_GEMM_DESIGN_INT8 ? AH_ERR_UNSUPPORTED_QUANT : AH_OK;
-    ctx->q8_design = design;
+    if (!geom(ggml_type, qk, bb) || ggml_type >= 32) return AH_ERR_UNSUPPORTED_QUANT;
+    if (design == AH_GEMM_DESIGN_INT8 && ggml_type != AH_GGML_Q8_0) return AH_ERR_UNSUPPORTED_QUANT;
+    if (design == AH_GEMM_DESIGN_F16_TILE && ggml_type != AH_GGML_Q4_K && !ah_k23((int)ggml_type))
+        return AH_ERR_UNSUPPORTED_QUANT;
+    ctx->design[ggml_type] = design;
     return AH_OK;
 }
 

@@ -99,7 +99,9 @@ struct GemmArgs {
     GemmPartArgs p[kGemmMaxParts];
     uint32_t n_parts, n_in, n_tok, kpad;
     const _Float16 *xh;        // [n_tok][kpad]
+    const _Float16 *xf;        // the same in fragment order (OperandArgs::xf), for the tile design
     const _Float16 *xmin;      // Q4_K: [n_tok][kpad/256][16] split code sums (see quant pass)
+    const _Float16 *xmin16;    // Q2_K / Q3_K tiles: [n_tok][kpad/256][16] 16-group code sums
     const float *tok_scale;    // [n_tok]; bit 0 set: the token is served by the exact path
     unsigned long long *status;
     const int8_t *fcodes;      // [n_tok][n_in] codes of flagged tokens
@@ -325,6 +327,35 @@ AH_DEV float exact_row(const uint8_t *row, const int8_t *xq, const int64_t *sc, 
                     X += (int)xq[k];
                 }
                 acc += s_of(sc, 8 * u + j) * ((d * (float)scj) * (float)D - (dmin * (float)mj) * (float)X);
+            }
+        } else if constexpr (TYPE == AH_GGML_Q2_K || TYPE == AH_GGML_Q3_K) {
+            // element 16g + l of the super-block is bit pair r of the qs byte 32n + 16p + l, with
+            // g = 8n + 2r + p (format/quant.rs:308-476); Q3_K adds bit 4n + r of hmask[16p + l]
+            // as the code's third bit and subtracts 4
+            constexpr bool Q3 = TYPE == AH_GGML_Q3_K;
+            const uint8_t *sb = row + (Q3 ? 110u : 84u) * u;
+            const float d = Q3 ? f16_at(sb + 108) : f16_at(sb + 80), dmin = Q3 ? 0.0f : f16_at(sb + 82);
+            for (uint32_t g = 0; g < 16 && 256 * u + 16 * g < n_in; ++g) {
+                const uint32_t n = g / 8, r = (g % 8) / 2, pp = g % 2;
+                int D = 0, X = 0;
+                for (uint32_t l = 0; l < 16; ++l) {
+                    const uint32_t k = 256 * u + 16 * g + l;
+                    if (k >= n_in) break;
+                    int q = (int)((byte_at(sb + (Q3 ? 32 : 16), 32 * n + 16 * pp + l) >> (2 * r)) & 3u);
+                    if (Q3) q = (q | (int)(((byte_at(sb, 16 * pp + l) >> (4 * n + r)) & 1u) << 2)) - 4;
+                    D += q * (int)xq[k];
+                    X += (int)xq[k];
+                }
+                const float S = s_of(sc, (256 * u + 16 * g) / 32);
+                if constexpr (Q3) {
+                    const uint32_t j = g % 8, hi = j / 4, i = j % 4;
+                    const uint32_t av = byte_at(sb + 96, 4 * hi + i), tv = byte_at(sb + 104, i);
+                    const int scg = (int)(((av >> (4 * n)) & 15u) | (((tv >> (4 * n + 2 * hi)) & 3u) << 4)) - 32;
+                    acc += S * ((d * (float)scg) * (float)D);
+                } else {
+                    const uint32_t sv = byte_at(sb, g);
+                    acc += S * ((d * (float)(sv & 15u)) * (float)D - (dmin * (float)(sv >> 4)) * (float)X);
+                }
             }
         } else {  // Q6_K: element 128n + 32t + l (format/quant.rs:556-599), 16-groups g
             const uint8_t *sb = row + 210 * u;
@@ -1044,6 +1075,478 @@ __global__ void splitk_reduce(ReduceArgs r) {
     }
 }
 
+
+// ---- dequantize-once design (gemm_dq_kernel) --------------------------------------------------
+//
+// The register-blocked kernel above converts every weight fragment once per wave that uses it, so
+// its dequantization is paid once per 32- or 64-token tile.  Here a workgroup covers 128 weight
+// rows x 128 tokens with 4 waves in a 2 x 2 grid (each wave 64 rows x 64 tokens: 2 x 2 MFMA
+// tiles).  Every stage of 64 K the workgroup's 256 threads read the stage's raw GGUF bytes of the
+// 128 rows with coalesced loads, convert each weight once to its exact f16 operand and write it
+// to an LDS plane [128 rows][64 K]; the activation slice [128 tokens][64 K] comes global -> LDS
+// by direct loads.  Waves then read both operands as MFMA fragments (1 KB of LDS per MFMA).  The
+// conversion is paid once per 128 tokens and is independent of the MFMA layout, so every GGUF
+// family only needs its own stage decoder.  Both planes are double-buffered: while the waves
+// multiply stage s, the threads convert stage s + 1 into the other buffer and the loads of the
+// stages after it are in flight, so one barrier per stage orders everything.
+//
+// Operands and exactness are the register-blocked kernel's: the activation is xq * 2^(e_b - E_tok)
+// (the operand pass), the Q4_K weight operand sc_j * q, folded with d once per super-block, the
+// dmin * m * X term on one extra MFMA per super-block.
+namespace dq {
+constexpr uint32_t kBM = 128, kBN = 128;
+constexpr uint32_t kPlane = 128u * kKS * 2u;  // one [128][64] f16 plane: 16 KB
+// Chunk c (8 K values, 16 B) of row r of a [128][64] plane: rows of 128 B, chunks XOR-swizzled
+// by (r >> 1) & 7 so that the 32 rows of one fragment read (two chunks each) cover all 64 banks.
+AH_DEV uint32_t swz(uint32_t r, uint32_t c) { return r * 128u + 16u * (c ^ ((r >> 1) & 7u)); }
+
+// Super-block bytes and the families this design serves.  Every family's stage (64 K of a row)
+// splits the same way over a row's two lane halves h: elements at stage K 16h .. 16h + 15 (the
+// "low run") and 32 + 16h .. 32 + 16h + 15 (the "high run"), each from 16 bytes the thread loads.
+template <int TYPE> constexpr uint32_t sb_bytes() { return TYPE == AH_GGML_Q4_K ? 144u : TYPE == AH_GGML_Q2_K ? 84u : 110u; }
+template <int TYPE> constexpr bool served() { return TYPE == AH_GGML_Q4_K || TYPE == AH_GGML_Q2_K || TYPE == AH_GGML_Q3_K; }
+
+// 16 bytes from a 2-aligned offset (Q3_K blocks are 110 bytes): five dwords realigned.
+AH_DEV u32x4 ld16_u2(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    const uint32_t a = off & ~3u, sh = off & 3u;
+    const u32x4 v = ah_ld128(rs, a);
+    const uint32_t e = ah_ld32(rs, a + 16u);
+    return (u32x4){ah_alignbyte(v.y, v.x, sh), ah_alignbyte(v.z, v.y, sh), ah_alignbyte(v.w, v.z, sh), ah_alignbyte(e, v.w, sh)};
+}
+
+// This thread's raw bytes of one stage at super-block position P (half n = P >> 1):
+//   Q4_K (format/quant.rs:481-510): q = qs[32P + 16h .. +16] (low nibble: sub-block 2P, high:
+//        2P + 1); at P = 0 hd = the header (d, dmin, scales[12]).
+//   Q2_K (format/quant.rs:308-360): q = qs[32n + 16h .. +16]: element 128n + 32r + 16h + l is bit
+//        pair r of byte l, so the stage takes pairs r0 = 2 (P & 1) and r0 + 1; at P = 0 hd = the
+//        16 scale bytes (sc low nibble, m high, group g at byte g), x.x = d | dmin << 16.
+//   Q3_K (format/quant.rs:362-476): q = qs[32n + 16h .. +16] as Q2_K, x = hmask[16h .. +16] (bit
+//        4n + r of byte l is the third bit of element 128n + 32r + 16h + l); at P = 0 hd = the 12
+//        scale bytes and d.
+struct Raw {
+    u32x4 q, x, hd;
+};
+template <int TYPE, int P>
+AH_DEV Raw fetch(__amdgpu_buffer_rsrc_t rs, uint32_t base, uint32_t h, bool live) {
+    Raw w;
+    w.x = w.hd = (u32x4){0u, 0u, 0u, 0u};
+    if constexpr (TYPE == AH_GGML_Q4_K) {
+        w.q = ah_ld128(rs, live ? base + 16u + 32u * P + 16u * h : kOob);
+        if constexpr (P == 0) w.hd = ah_ld128(rs, live ? base : kOob);
+    } else if constexpr (TYPE == AH_GGML_Q2_K) {
+        w.q = ah_ld128(rs, live ? base + 16u + 32u * (P >> 1) + 16u * h : kOob);
+        if constexpr (P == 0) {
+            w.hd = ah_ld128(rs, live ? base : kOob);
+            w.x.x = ah_ld32(rs, live ? base + 80u : kOob);
+        }
+    } else {
+        w.q = ld16_u2(rs, live ? base + 32u + 32u * (P >> 1) + 16u * h : kOob);
+        w.x = ld16_u2(rs, live ? base + 16u * h : kOob);
+        if constexpr (P == 0) w.hd = ld16_u2(rs, live ? base + 96u : kOob);
+    }
+    return w;
+}
+
+// Per-thread scale state of the super-block being converted (from its header).
+struct Scales {
+    uint32_t w[4];
+};
+AH_DEV Scales scales_of(const Raw &w) { return Scales{{w.hd.x, w.hd.y, w.hd.z, w.hd.w}}; }
+// Q3_K's 6-bit scales of half n (format/quant.rs:420-447, the kmask shuffle of the 12 bytes
+// a0 | a1 | t): groups 0-3 and 4-7 of the half as bytes of two words
+AH_DEV uint32_t q3_scw(const Scales &S, uint32_t n, uint32_t hi) {
+    const uint32_t a = hi ? S.w[1] : S.w[0], t = S.w[2];
+    return ((a >> (4 * n)) & 0x0F0F0F0Fu) | (((t >> (4 * n + 2 * hi)) & 0x03030303u) << 4);
+}
+
+// Side data of a super-block for the fold: d, dmin' and 16 f16 "min weights" per row, where the
+// fold is acc += d P - dmin' (sum_k mw_k X_k) and X are the min-term operand's code sums:
+//   Q4_K: dmin' = dmin, mw = m_j of the 8 sub-blocks (the operand's split sums, hi then lo);
+//   Q2_K: dmin' = dmin, mw = m_g of the 16 groups (16-group sums);
+//   Q3_K: dmin' = 4 d, mw = sc_g - 32 (the weight operand carries q + 4 = (q2 | h << 2), so the
+//         -4 of each code returns as -4 d (sc_g - 32) X_g).
+template <int TYPE>
+AH_DEV void side(const Raw &w, const Scales &S, float &d, float &dm, uint32_t (&mw)[8]) {
+    if constexpr (TYPE == AH_GGML_Q4_K) {
+        d = ah_f16_bits_to_f32(w.hd.x & 0xffffu);
+        dm = ah_f16_bits_to_f32(w.hd.x >> 16);
+        const uint32_t s0 = S.w[1], s1 = S.w[2], s2 = S.w[3];
+        const f16x2 m01 = {(_Float16)(float)q4k_scale<0, true>(s0, s1, s2), (_Float16)(float)q4k_scale<1, true>(s0, s1, s2)};
+        const f16x2 m23 = {(_Float16)(float)q4k_scale<2, true>(s0, s1, s2), (_Float16)(float)q4k_scale<3, true>(s0, s1, s2)};
+        const f16x2 m45 = {(_Float16)(float)q4k_scale<4, true>(s0, s1, s2), (_Float16)(float)q4k_scale<5, true>(s0, s1, s2)};
+        const f16x2 m67 = {(_Float16)(float)q4k_scale<6, true>(s0, s1, s2), (_Float16)(float)q4k_scale<7, true>(s0, s1, s2)};
+        mw[0] = mw[4] = as_u(m01);
+        mw[1] = mw[5] = as_u(m23);
+        mw[2] = mw[6] = as_u(m45);
+        mw[3] = mw[7] = as_u(m67);
+    } else if constexpr (TYPE == AH_GGML_Q2_K) {
+        d = ah_f16_bits_to_f32(w.x.x & 0xffffu);
+        dm = ah_f16_bits_to_f32(w.x.x >> 16);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t b = S.w[i >> 1] >> (16 * (i & 1));
+            const f16x2 v = {(_Float16)(float)((b >> 4) & 15u), (_Float16)(float)((b >> 12) & 15u)};
+            mw[i] = as_u(v);
+        }
+    } else {
+        d = ah_f16_bits_to_f32(S.w[3] & 0xffffu);
+        dm = 4.0f * d;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t sw = q3_scw(S, (uint32_t)(i >> 2), (uint32_t)((i >> 1) & 1));
+            const uint32_t b = sw >> (16 * (i & 1));
+            const f16x2 v = {(_Float16)(float)((int)(b & 0xffu) - 32), (_Float16)(float)((int)((b >> 8) & 0xffu) - 32)};
+            mw[i] = as_u(v);
+        }
+    }
+}
+
+// The weight operand of the stage at position P, per K-step k (qs word k): the low run's four
+// values (lo0, lo1) and the high run's (hi0, hi1), each exact in f16.  The scale operands
+// (per run: multiplier and offset of nib4_times) are formed once per stage by `run_scales`.
+struct RunScales {
+    f16x2 ml, ol, mh, oh;
+};
+template <int TYPE, int P>
+AH_DEV RunScales run_scales(const Scales &S, uint32_t h) {
+    RunScales r;
+    _Float16 sl, sh;  // the runs' group scales as multipliers of the byte values below
+    _Float16 kl, kh;  // the byte values' place factors (the byte holds value * kl)
+    if constexpr (TYPE == AH_GGML_Q4_K) {
+        sl = (_Float16)(uint16_t)q4k_scale<2 * P, false>(S.w[1], S.w[2], S.w[3]);
+        sh = (_Float16)(uint16_t)q4k_scale<2 * P + 1, false>(S.w[1], S.w[2], S.w[3]);
+        kl = (_Float16)1.0f;
+        kh = (_Float16)16.0f;
+    } else if constexpr (TYPE == AH_GGML_Q2_K) {
+        // groups 8n + 2 r0 + h and + 2: bytes h and h + 2 of scale word P (low nibbles)
+        const uint32_t wd = S.w[P];
+        sl = (_Float16)(float)((wd >> (8 * h)) & 15u);
+        sh = (_Float16)(float)((wd >> (8 * h + 16)) & 15u);
+        kl = (_Float16)(float)(1u << (4 * (P & 1)));      // pair r0 = 2 (P & 1) in place: 4^r0
+        kh = (_Float16)(float)(1u << (4 * (P & 1) + 2));  // pair r0 + 1
+    } else {
+        const uint32_t sw = q3_scw(S, P >> 1, P & 1);  // groups 4 (P & 1) .. +3 of half P >> 1
+        sl = (_Float16)(float)((int)((sw >> (8 * h)) & 0xffu) - 32);
+        sh = (_Float16)(float)((int)((sw >> (8 * h + 16)) & 0xffu) - 32);
+        kl = (_Float16)1.0f;
+        kh = (_Float16)1.0f;
+    }
+    // (1024 + k v) * (s / k) - 1024 s / k = v s: s / k and 1024 s / k are exact in f16 (k a power
+    // of two) and v s is representable, so the fused rounding is exact
+    const _Float16 ml = sl / kl, mh = sh / kh;
+    r.ml = (f16x2){ml, ml};
+    r.mh = (f16x2){mh, mh};
+    r.ol = (f16x2){ml * (_Float16)(-1024.0f), ml * (_Float16)(-1024.0f)};
+    r.oh = (f16x2){mh * (_Float16)(-1024.0f), mh * (_Float16)(-1024.0f)};
+    return r;
+}
+template <int TYPE, int P>
+AH_DEV void convert_word(const Raw &w, const RunScales &rs, uint32_t k, uint32_t &lo0, uint32_t &lo1, uint32_t &hi0,
+                         uint32_t &hi1) {
+    const uint32_t qw = k == 0 ? w.q.x : k == 1 ? w.q.y : k == 2 ? w.q.z : w.q.w;
+    uint32_t bl, bh;  // byte values (times their place factor) of the low and high run
+    if constexpr (TYPE == AH_GGML_Q4_K) {
+        bl = qw & 0x0F0F0F0Fu;
+        bh = qw & 0xF0F0F0F0u;
+    } else if constexpr (TYPE == AH_GGML_Q2_K) {
+        constexpr uint32_t r0 = 2 * (P & 1);
+        bl = qw & (0x03030303u << (2 * r0));
+        bh = qw & (0x03030303u << (2 * r0 + 2));
+    } else {
+        constexpr uint32_t r0 = 2 * (P & 1), n = P >> 1;
+        const uint32_t hw = k == 0 ? w.x.x : k == 1 ? w.x.y : k == 2 ? w.x.z : w.x.w;
+        // v = q2 | hbit << 2 in 0..7 (the code plus 4), hbit = bit 4n + r of the hmask byte
+        constexpr int sl = (int)(4 * n + r0) - 2, sh = sl + 1;
+        const uint32_t hl = sl >= 0 ? hw >> sl : hw << -sl, hh = sh >= 0 ? hw >> sh : hw << -sh;
+        bl = ((qw >> (2 * r0)) & 0x03030303u) | (hl & 0x04040404u);
+        bh = ((qw >> (2 * r0 + 2)) & 0x03030303u) | (hh & 0x04040404u);
+    }
+    nib4_times(bl, rs.ml, rs.ol, lo0, lo1);
+    nib4_times(bh, rs.mh, rs.oh, hi0, hi1);
+}
+
+}  // namespace dq
+
+// Epilogue of the dequantize-once design: the wave's 2 x 2 tiles of 32 tokens x 32 rows.  As
+// gemm_store: token scales applied (partials stay unscaled), lanes past n_out, tokens past n_tok
+// and flagged tokens store out of range, output refusals recorded from a rare second pass over
+// this lane's own stores, flagged tokens recomputed per row by the exact path.  `ts` is the
+// wave's 64 token scales in LDS (staged at the start of the workgroup: two dependent global
+// round trips here had cost ~4 us per tile).
+template <int TYPE>
+AH_DEV __attribute__((always_inline)) void dq_store(const GemmArgs &a, const GemmPartArgs &pa, const f32x16 (&acc)[2][2],
+                                                    const float *ts, uint32_t row_w, uint32_t tok_w, uint32_t split,
+                                                    uint32_t u_lo, uint32_t u_hi) {
+    const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+    const uint32_t ntile = a.n_tok > tok_w ? (a.n_tok - tok_w < 64u ? a.n_tok - tok_w : 64u) : 0u;
+    float *ybase = pa.splits == 1 ? pa.y + (size_t)tok_w * pa.n_out
+                                  : pa.y + ((size_t)split * a.n_tok + tok_w) * pa.n_out;
+    const __amdgpu_buffer_rsrc_t ry = ah_rsrc(ybase, ntile * pa.n_out * 4u);
+    const bool scaled = pa.splits == 1;
+    bool rl[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) rl[n] = row_w + 32u * n + j < pa.n_out;
+    // flagged tokens of the wave: lane l holds token l's scale
+    const uint64_t fm = __builtin_amdgcn_ballot_w64(
+        (uint32_t)lane < ntile && ah_ts_flagged(__builtin_bit_cast(uint32_t, ts[lane])));
+    bool bad = false;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        // lanes of half h hold tokens 32m + 8q + 4h + i (q = r / 4, i = r % 4): four consecutive
+        uint32_t sc[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(ts + 32 * m + 8 * q + 4 * h);
+            sc[4 * q] = v.x;
+            sc[4 * q + 1] = v.y;
+            sc[4 * q + 2] = v.z;
+            sc[4 * q + 3] = v.w;
+        }
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            const uint32_t row = row_w + 32 * n + j;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t tl = 32 * m + 8 * (r / 4) + 4 * h + (r % 4);
+                const bool ok = rl[n] && tl < ntile && !ah_ts_flagged(sc[r]);
+                const float v = acc[m][n][r] * (scaled ? ah_ts_value(sc[r]) : 1.0f);
+                bad = bad || (ok && !(__builtin_fabsf(v) < 0x1p31f));
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
+                                                      ok ? (tl * pa.n_out + row) * 4u : kOob, 0, 0);
+            }
+        }
+    }
+    if (scaled && __builtin_amdgcn_ballot_w64(bad) != 0ull) {
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (uint32_t e = 0; e < 64u; ++e) {
+            const uint32_t m = e / 32, n = (e / 16) % 2, r = e % 16;
+            const uint32_t tl = 32 * m + 8 * (r / 4) + 4 * h + (r % 4), row = row_w + 32 * n + j;
+            if (!rl[n] || tl >= ntile || ah_ts_flagged(__builtin_bit_cast(uint32_t, ts[tl]))) continue;
+            const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, (tl * pa.n_out + row) * 4u, 0, 1));
+            if (const uint32_t oc = ah_out_code(v)) ah_record(a.status, ah_out_key((uint64_t)(tok_w + tl) * pa.n_out + row, oc));
+        }
+    }
+    if (fm != 0ull) {
+        // flagged tokens: the split's K range, per row tile, the lane halves taking alternate units
+        const uint32_t nb32 = (a.n_in + 31) / 32;
+        if (ah_blk32(TYPE) && u_hi > nb32) u_hi = nb32;
+        uint64_t mk = fm;
+        while (mk) {
+            const uint32_t tl = (uint32_t)__builtin_ctzll(mk);
+            mk &= mk - 1;
+            const size_t t = (size_t)tok_w + tl;
+            const float tsv = ah_ts_value(__builtin_bit_cast(uint32_t, ts[tl]));
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const uint32_t row = row_w + 32 * n + j;
+                float v = rl[n] ? exact_row<TYPE>(pa.w + (size_t)row * pa.row_bytes, a.fcodes + t * a.n_in,
+                                                  a.fscales + t * nb32, a.n_in, u_lo, u_hi, (uint32_t)h)
+                                : 0.0f;
+                v += __shfl_xor(v, 32, 64);
+                if (h == 0 && rl[n]) {
+                    ybase[(size_t)tl * pa.n_out + row] = scaled ? v : v / tsv;
+                    if (const uint32_t oc = scaled ? ah_out_code(v) : 0u) ah_record(a.status, ah_out_key((uint64_t)t * pa.n_out + row, oc));
+                }
+            }
+        }
+    }
+}
+
+// A workgroup is 4 waves (2 x 2, each 64 rows x 64 tokens) over a 128 x 128 tile, two
+// workgroups per CU.  The activation fragments come straight from global memory into registers
+// (the operand in fragment order: one coalesced 1 KB load per fragment, a stage ahead, each
+// fragment's registers reloaded for the next stage right after its MFMAs), so LDS only carries
+// the converted weights: per stage 16 KB written and 32 KB of fragment reads, where staging the
+// activations as well doubled that.  The raw weight bytes are requested two stages ahead; each
+// stage converts the next stage's weights into the other plane while it multiplies (one word of
+// each run per K-step, interleaved with the MFMAs), and one barrier per stage hands the plane over.
+// At the end of a super-block the MFMA sums fold with the row's d, and the min term (Q4_K, Q2_K
+// mins; Q3_K the codes' -4) rides on one more MFMA per tile.
+template <int TYPE>
+__global__ void __launch_bounds__(256, 2) gemm_dq_kernel(GemmArgs a) {
+    static_assert(dq::served<TYPE>(), "dequantize-once design: Q4_K, Q2_K, Q3_K");
+    constexpr uint32_t kSB = dq::sb_bytes<TYPE>();
+    constexpr uint32_t kOD = 2 * dq::kPlane, kOM = kOD + 2048, kOT = kOM + 8192;
+    __shared__ __align__(16) uint8_t lds[kOT + 512];
+    const uint32_t per = gridDim.x >> 3;
+    const uint32_t L = (blockIdx.x & 7u) * per + (blockIdx.x >> 3);
+    if (L >= a.n_wg) return;
+    uint32_t pi = 0;
+#pragma unroll
+    for (uint32_t i = 1; i < kGemmMaxParts; ++i)
+        if (i < a.n_parts && L >= a.p[i].wg_begin) pi = i;
+    const GemmPartArgs &pa = a.p[pi];
+    const uint32_t Lp = L - pa.wg_begin;
+    const uint32_t tt = Lp % pa.tok_tiles, rest = Lp / pa.tok_tiles;
+    const uint32_t split = rest % pa.splits, rtile = rest / pa.splits;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, j = lane & 31u, h = lane >> 5;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wr = wv & 1u, wt = wv >> 1;  // the wave's row half and token half
+    const uint32_t row0 = rtile * dq::kBM, tok0 = tt * dq::kBN;
+    const uint32_t ntile = a.n_tok - tok0 < dq::kBN ? a.n_tok - tok0 : dq::kBN;
+    // this thread's conversion row (32 per wave) and its byte offset
+    const uint32_t crow = 32u * wv + j;
+    const bool clive = row0 + crow < pa.n_out;
+    const uint32_t croff = clive ? (row0 + crow) * pa.row_bytes : 0u;
+    const __amdgpu_buffer_rsrc_t rs = ah_rsrc(pa.w, pa.w_bytes);
+    const uint32_t nkb = a.kpad / 16, nsb = a.kpad / 256;
+    const uint32_t ntb = (a.n_tok + 31) / 32;
+    // the wave's two 32-token blocks of the fragment-order operand
+    const uint32_t tb0 = tok0 / 32 + 2 * wt;
+    const __amdgpu_buffer_rsrc_t rf = ah_rsrc(a.xf, ntb * nkb * 1024u);
+    const __amdgpu_buffer_rsrc_t rm = ah_rsrc(TYPE == AH_GGML_Q4_K ? a.xmin : a.xmin16, a.n_tok * nsb * 32u);
+
+    const uint32_t nstages = a.kpad / kKS;
+    const uint32_t st_begin = split * pa.stages_per_split;
+    const uint32_t st_end = st_begin + pa.stages_per_split < nstages ? st_begin + pa.stages_per_split : nstages;
+
+    uint8_t *const B[2] = {lds, lds + dq::kPlane};
+    float *const Dd = reinterpret_cast<float *>(lds + kOD);  // [par][0..127] d, [par][128..255] dmin'
+    uint8_t *const M = lds + kOM;                            // [par][128 rows][16] f16 min weights
+    float *const TS = reinterpret_cast<float *>(lds + kOT);  // the tile's 128 token scales
+
+    // activation fragment (token block tb0 + m, K-step k16 of stage st); past the split or the
+    // operand: zeros (the rows of a partial token block past n_tok are never stored from)
+    auto loadA = [&](uint32_t st, uint32_t m, uint32_t k16) -> f16x8 {
+        const uint32_t off = (((tb0 + m) * nkb + st * 4 + k16) * 64 + lane) * 16u;
+        return __builtin_bit_cast(f16x8, ah_ld128(rf, st < st_end ? off : kOob));
+    };
+    // the min-term operand of super-block sb for token tile m: lane (token j, half h) holds its
+    // code sums 8h .. 8h + 7
+    auto loadX = [&](uint32_t sb, uint32_t m) -> f16x8 {
+        const uint32_t t = tok0 + 64u * wt + 32u * m + j;
+        return __builtin_bit_cast(f16x8, ah_ld128(rm, t < a.n_tok ? (t * nsb + sb) * 32u + 16u * h : kOob));
+    };
+
+    f32x16 acc[2][2], P[2][2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int n = 0; n < 2; ++n) acc[m][n] = P[m][n] = (f32x16){};
+    dq::Scales S = {{0u, 0u, 0u, 0u}};  // scale words of the super-block being converted
+
+    // a super-block's header at its first conversion: the scale words, and d, dmin' and the min
+    // weights into parity `par` (both lane halves of a row write the same values)
+    auto header = [&](const dq::Raw &w, uint32_t par) {
+        S = dq::scales_of(w);
+        float d, dm;
+        uint32_t mw[8];
+        dq::side<TYPE>(w, S, d, dm, mw);
+        Dd[256 * par + crow] = d;
+        Dd[256 * par + 128 + crow] = dm;
+        *reinterpret_cast<u32x4 *>(M + par * 4096u + crow * 32u) = (u32x4){mw[0], mw[1], mw[2], mw[3]};
+        *reinterpret_cast<u32x4 *>(M + par * 4096u + crow * 32u + 16u) = (u32x4){mw[4], mw[5], mw[6], mw[7]};
+    };
+    auto fetch = [&](auto pc, uint32_t st) -> dq::Raw {
+        return dq::fetch<TYPE, decltype(pc)::value>(rs, croff + kSB * (st / 4), h, clive && st < st_end);
+    };
+    // the whole conversion of a stage (the prologue's; the loop interleaves it with the MFMAs)
+    auto convert_all = [&](auto pc, const dq::Raw &w, uint8_t *plane) {
+        constexpr int PC = decltype(pc)::value;
+        const dq::RunScales r = dq::run_scales<TYPE, PC>(S, h);
+#pragma unroll
+        for (uint32_t k16 = 0; k16 < 4; ++k16) {
+            uint32_t f0, f1, g0, g1;
+            dq::convert_word<TYPE, PC>(w, r, k16, f0, f1, g0, g1);
+            *reinterpret_cast<u32x2 *>(plane + dq::swz(crow, 2 * h + (k16 >> 1)) + 8 * (k16 & 1)) = (u32x2){f0, f1};
+            *reinterpret_cast<u32x2 *>(plane + dq::swz(crow, 4 + 2 * h + (k16 >> 1)) + 8 * (k16 & 1)) = (u32x2){g0, g1};
+        }
+    };
+
+    const uint32_t sw = (j >> 1) & 7u;
+    auto fragB = [&](const uint8_t *buf, uint32_t n, uint32_t k16) -> f16x8 {
+        const uint32_t r = 64u * wr + 32u * n + j;
+        return *reinterpret_cast<const f16x8 *>(buf + r * 128u + 16u * ((2u * k16 + h) ^ sw));
+    };
+
+    // prologue: the token scales, stage 0's activation fragments, raw bytes of stages 0 and 1,
+    // stage 0 converted
+    f16x8 fa[4][2];
+    if (wv == 0 && lane < 32u) {
+        const u32x4 v = ah_ld128(ah_rsrc(a.tok_scale + tok0, ntile * 4u), 16u * lane);
+        *reinterpret_cast<u32x4 *>(TS + 4 * lane) = v;
+    }
+#pragma unroll
+    for (uint32_t k16 = 0; k16 < 4; ++k16)
+#pragma unroll
+        for (uint32_t m = 0; m < 2; ++m) fa[k16][m] = loadA(st_begin, m, k16);
+    dq::Raw W[2];
+    W[0] = fetch(std::integral_constant<int, 0>{}, st_begin);
+    W[1] = fetch(std::integral_constant<int, 1>{}, st_begin + 1);
+    header(W[0], 0u);
+    convert_all(std::integral_constant<int, 0>{}, W[0], B[0]);
+    ah_lds_barrier();
+
+    f16x8 am[2];  // the min-term operand of the current super-block
+    // Stage st at super-block position U (compile-time; slot U & 1), the super-block's side data
+    // in parity `par`.
+    auto stage = [&](auto uc, uint32_t st, uint32_t par) {
+        constexpr int U = decltype(uc)::value, UN = (U + 1) & 3, PF = (U + 2) & 3;
+        const uint8_t *Bc = B[U & 1];
+        uint8_t *Bn = B[(U + 1) & 1];
+        f16x8 fb[2][2];
+        fb[0][0] = fragB(Bc, 0, 0);
+        fb[0][1] = fragB(Bc, 1, 0);
+        if constexpr (U == 0) {
+            am[0] = loadX(st / 4, 0);
+            am[1] = loadX(st / 4, 1);
+        }
+        W[U & 1] = fetch(std::integral_constant<int, PF>{}, st + 2);
+        // the next stage's conversion (stage st + 1): scale operands, and its super-block header
+        const dq::Raw &wn = W[(U + 1) & 1];
+        if constexpr (UN == 0) header(wn, par ^ 1u);
+        const dq::RunScales rsc = dq::run_scales<TYPE, UN>(S, h);
+#pragma unroll
+        for (uint32_t k16 = 0; k16 < 4; ++k16) {
+            const uint32_t cb = k16 & 1u, nb = cb ^ 1u;
+            if (k16 < 3) {
+                fb[nb][0] = fragB(Bc, 0, k16 + 1);
+                fb[nb][1] = fragB(Bc, 1, k16 + 1);
+            }
+            P[0][0] = mfma(fa[k16][0], fb[cb][0], P[0][0]);
+            P[0][1] = mfma(fa[k16][0], fb[cb][1], P[0][1]);
+            P[1][0] = mfma(fa[k16][1], fb[cb][0], P[1][0]);
+            P[1][1] = mfma(fa[k16][1], fb[cb][1], P[1][1]);
+            // this K-step's activation registers are free: the next stage's fragments
+            fa[k16][0] = loadA(st + 1, 0, k16);
+            fa[k16][1] = loadA(st + 1, 1, k16);
+            uint32_t f0, f1, g0, g1;
+            dq::convert_word<TYPE, UN>(wn, rsc, k16, f0, f1, g0, g1);
+            *reinterpret_cast<u32x2 *>(Bn + dq::swz(crow, 2 * h + (k16 >> 1)) + 8 * (k16 & 1)) = (u32x2){f0, f1};
+            *reinterpret_cast<u32x2 *>(Bn + dq::swz(crow, 4 + 2 * h + (k16 >> 1)) + 8 * (k16 & 1)) = (u32x2){g0, g1};
+        }
+        if constexpr (U == 3) {
+            // fold the super-block: d * P - dmin' * (sum_k mw_k X_k), the latter one MFMA per tile
+#pragma unroll
+            for (uint32_t n = 0; n < 2; ++n) {
+                const uint32_t r = 64u * wr + 32u * n + j;
+                const float fd = Dd[256 * par + r], fdm = Dd[256 * par + 128 + r];
+                const f16x8 bm = *reinterpret_cast<const f16x8 *>(M + par * 4096u + r * 32u + 16u * h);
+#pragma unroll
+                for (uint32_t m = 0; m < 2; ++m) {
+                    const f32x16 pm = mfma(am[m], bm, (f32x16){});
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        acc[m][n][e] = __builtin_fmaf(-fdm, pm[e], __builtin_fmaf(fd, P[m][n][e], acc[m][n][e]));
+                    P[m][n] = (f32x16){};
+                }
+            }
+        }
+        // the next stage's weights are in LDS and every wave is done with this stage's plane
+        ah_lds_barrier();
+    };
+    uint32_t par = 0;
+    for (uint32_t st = st_begin; st < st_end; st += 4) {
+        stage(std::integral_constant<int, 0>{}, st, par);
+        stage(std::integral_constant<int, 1>{}, st + 1, par);
+        stage(std::integral_constant<int, 2>{}, st + 2, par);
+        stage(std::integral_constant<int, 3>{}, st + 3, par);
+        par ^= 1u;
+    }
+    dq_store<TYPE>(a, pa, acc, TS + 64u * wt, row0 + 64u * wr, tok0 + 64u * wt, split, st_begin / 4, st_end / 4);
+}
+
 }  // namespace
 
 namespace {
@@ -1052,9 +1555,10 @@ namespace {
 struct GemmGeom {
     uint32_t nstages, unroll, rows, toks;
 };
-GemmGeom geom_of(uint32_t type, uint32_t n_in, uint32_t kpad, uint32_t waves = 4, bool int8 = false) {
+GemmGeom geom_of(uint32_t type, uint32_t n_in, uint32_t kpad, uint32_t waves = 4, uint32_t kind = kGemmKindRb) {
     const uint32_t rows = 32u * rb::kNN * waves;
-    if (int8) return {i8::stages(n_in), 1, rows, i8::kTok};  // stages of 4 blocks
+    if (kind == kGemmKindI8) return {i8::stages(n_in), 1, rows, i8::kTok};  // stages of 4 blocks
+    if (kind == kGemmKindTile) return {kpad / kKS, 4, dq::kBM, dq::kBN};
     if (ah_blk32((int)type)) return {(n_in + 2 * kKS - 1) / (2 * kKS) * 2, 2, rows, rb::tok_of(type)};
     return {kpad / kKS, 4, rows, rb::tok_of(type)};  // K-quants: whole super-blocks
 }
@@ -1075,10 +1579,11 @@ uint32_t per_split(const GemmGeom &g, uint32_t splits) {
 //   a split GEMM adds the reduction: 4.8 us fixed plus the partials' write and read-back,
 //   (splits + 1) * n_tok * n_out * 4 bytes at 0.253 us per MB.
 uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
-                             uint32_t cus, bool int8) {
-    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4, int8);
+                             uint32_t cus, uint32_t kind) {
+    const bool int8 = kind == kGemmKindI8;
+    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4, kind);
     const uint64_t tiles = (uint64_t)((n_out + g.rows - 1) / g.rows) * ((n_tok + g.toks - 1) / g.toks);
-    const double c = int8 ? 1.0 : ah_blk32((int)type) ? 0.806 : type == AH_GGML_Q4_K ? 0.400 : 1.081;
+    const double c = kind == kGemmKindTile ? 0.55 : int8 ? 1.0 : ah_blk32((int)type) ? 0.806 : type == AH_GGML_Q4_K ? 0.400 : 1.081;
     uint32_t best = 1;
     double best_cost = 1e30;
     for (uint32_t want = 1; want <= 64 && want <= g.nstages; ++want) {
@@ -1101,8 +1606,8 @@ uint32_t ah_gemm_max_parts(uint32_t type) { return rb::max_parts_of(type); }
 
 // 4-wave workgroups (tiles x splits) of one part.
 uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok, uint32_t splits,
-                          bool int8) {
-    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4, int8);
+                          uint32_t kind) {
+    const GemmGeom g = geom_of(type, n_in, (n_in + 255) / 256 * 256, 4, kind);
     return ((n_out + g.rows - 1) / g.rows) * ((n_tok + g.toks - 1) / g.toks) * splits;
 }
 
@@ -1218,23 +1723,31 @@ hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, ui
 }
 
 hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_in,
-                          uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xmin,
+                          uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xf, const _Float16 *xmin,
+                          const _Float16 *xmin16,
                           const float *tok_scale, const int8_t *fcodes, const int64_t *fscales,
                           const int8_t *xc, const uint32_t *xsp,
                           unsigned long long *status, uint32_t form, hipStream_t stream) {
     const bool mixed = type == kGemmMixedKQuant;  // Q4_K and Q6_K parts, 4-wave form
     const bool int8 = form == kFormI8x4 || form == kFormI8x2;
-    if (n_parts == 0 || n_parts > (mixed ? kGemmMaxParts : rb::max_parts_of(type))) return hipErrorInvalidValue;
+    const bool tile = form == kFormTile;
+    if (n_parts == 0 || n_parts > (mixed || tile ? kGemmMaxParts : rb::max_parts_of(type))) return hipErrorInvalidValue;
     if (int8 && (type != AH_GGML_Q8_0 || !xc || !xsp)) return hipErrorInvalidValue;
-    if (!int8 && (mixed || type == AH_GGML_Q4_K || form > kForm2x4)) form = kForm4x4;
-    const uint32_t waves = form == kForm4x4 || form == kFormI8x4 ? 4u : 2u;
+    if (tile && (!xf || (type != AH_GGML_Q4_K && type != AH_GGML_Q2_K && type != AH_GGML_Q3_K) ||
+                 (type != AH_GGML_Q4_K && !xmin16)))
+        return hipErrorInvalidValue;
+    if (!int8 && !tile && (mixed || type == AH_GGML_Q4_K || form > kForm2x4)) form = kForm4x4;
+    const uint32_t kind = int8 ? kGemmKindI8 : tile ? kGemmKindTile : kGemmKindRb;
+    const uint32_t waves = form == kForm4x4 || form == kFormI8x4 || tile ? 4u : 2u;
     GemmArgs a;
     a.n_parts = n_parts;
     a.n_in = n_in;
     a.n_tok = n_tok;
     a.kpad = kpad;
     a.xh = xh;
+    a.xf = xf;
     a.xmin = xmin;
+    a.xmin16 = xmin16;
     a.tok_scale = tok_scale;
     a.fcodes = fcodes;
     a.status = status;
@@ -1252,7 +1765,7 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
         const GemmPartDesc &d = parts[i];
         const uint32_t pt = mixed ? d.type : type;
         if (mixed && pt != AH_GGML_Q4_K && pt != AH_GGML_Q6_K) return hipErrorInvalidValue;
-        const GemmGeom g = geom_of(pt, n_in, kpad, waves, int8);
+        const GemmGeom g = geom_of(pt, n_in, kpad, waves, kind);
         const uint32_t per = per_split(g, d.splits ? d.splits : 1);
         P.w = d.w;
         P.w_bytes = d.w_bytes;
@@ -1275,6 +1788,12 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     if (form == kForm2x2) hipLaunchKernelGGL((gemm_rb_kernel<T, 2, 2>), rb_grid, blk, 0, stream, a);    \
     else if (form == kForm2x4) hipLaunchKernelGGL((gemm_rb_kernel<T, 2, 4>), rb_grid, blk, 0, stream, a); \
     else hipLaunchKernelGGL((gemm_rb_kernel<T, 4, 4>), rb_grid, blk, 0, stream, a);
+    if (tile) {
+        if (type == AH_GGML_Q4_K) hipLaunchKernelGGL(gemm_dq_kernel<AH_GGML_Q4_K>, rb_grid, dim3(256), 0, stream, a);
+        else if (type == AH_GGML_Q2_K) hipLaunchKernelGGL(gemm_dq_kernel<AH_GGML_Q2_K>, rb_grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL(gemm_dq_kernel<AH_GGML_Q3_K>, rb_grid, dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
     if (form == kFormI8x4) {
         hipLaunchKernelGGL(gemm_i8_kernel<4>, rb_grid, blk, 0, stream, a);
         return hipGetLastError();

@@ -934,7 +934,7 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
         in[u] = bytewise ? quad_load(o.x, srow, SRC, o.n_in, row, b, b < o.nb32) : operand_load<SRC>(r, o.n_in, b);
     }
     uint32_t c0[R], c1[R];
-    int ex[R], sum[R];
+    int ex[R], sum[R], sum16[R];
     int emax = -1, emin = 64;  // largest block exponent, smallest of a nonzero block
     bool odd = false;          // a codes scale that is not a power of two
 #pragma unroll
@@ -955,6 +955,7 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
         c1[u] = qo.c1;
         ex[u] = e;
         sum[u] = qo.s32;
+        sum16[u] = qo.s16;
         emax = e > emax ? e : emax;
         emin = e >= 0 && e < emin ? e : emin;
     }
@@ -975,7 +976,7 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
     // a nonzero block below the f16 band (when the f16 operand is written; the int8 design's
     // bf16 block factors carry any gap), or a scale that is not a power of two: the GEMM serves
     // this token exactly from its codes
-    const bool flagged = o.xh ? Emin < E - kF16Band : Emin < -500;
+    const bool flagged = (o.xh || o.xf) ? Emin < E - kF16Band : Emin < -500;
     if (tid == 0) {
         const float ts = E < 0 ? 0.0f : __builtin_ldexpf(1.0f, E - 32);
         o.tok_scale[tok] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, ts) | (flagged ? 1u : 0u));
@@ -1013,8 +1014,11 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
             }
         }
     }
-    if (!o.xh) return;
-    _Float16 *xh = o.xh + (size_t)tok * o.kpad;
+    if (!o.xh && !o.xf) return;
+    _Float16 *xh = o.xh ? o.xh + (size_t)tok * o.kpad : nullptr;
+    // fragment order: token tok's 16 bytes of K chunk k0 = 32 b + 8 q sit in block (tok / 32, k0 / 16)
+    // at lane 32 ((k0 / 8) & 1) + tok % 32
+    _Float16 *xf = o.xf ? o.xf + ((size_t)(tok / 32) * (o.kpad / 16)) * 512 + (tok % 32) * 8 : nullptr;
 #pragma unroll
     for (uint32_t u = 0; u < R; ++u) {
         if (u * kOpBlocks + wb0 >= nbp) break;
@@ -1027,7 +1031,16 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
             const int c = (int)(int8_t)(((i < 4 ? c0[u] : c1[u]) >> (8 * (i & 3))) & 0xffu);
             hv[i] = e < 0 ? (_Float16)0.0f : (_Float16)__builtin_ldexpf((float)c, sh);
         }
-        *reinterpret_cast<u32x4 *>(xh + 32 * b + 8 * q) = __builtin_bit_cast(u32x4, hv);
+        if (xh) *reinterpret_cast<u32x4 *>(xh + 32 * b + 8 * q) = __builtin_bit_cast(u32x4, hv);
+        if (xf) {
+            const uint32_t k0 = 32 * b + 8 * q;
+            *reinterpret_cast<u32x4 *>(xf + (size_t)(k0 / 16) * 512 + 256 * ((k0 / 8) & 1)) = __builtin_bit_cast(u32x4, hv);
+        }
+        if (o.xmin16 && (q & 1u) == 0) {
+            // lanes 0 and 2 hold the sums of the block's 16-groups 2 (b % 8) and 2 (b % 8) + 1
+            _Float16 *m = o.xmin16 + ((size_t)tok * (o.kpad / 256) + b / 8) * 16;
+            m[2 * (b % 8) + (q >> 1)] = e < 0 ? (_Float16)0.0f : (_Float16)__builtin_ldexpf((float)sum16[u], sh);
+        }
         if (o.xmin && q == 0) {
             const int X = sum[u];
             const int hq = (X >= 0 ? X : X - 63) / 64;  // floor(X / 64)

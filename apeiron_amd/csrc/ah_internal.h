@@ -219,7 +219,11 @@ struct FfnArgs {
 
 // GEMM workgroup forms (waves x LDS ring slots), chosen per launch by ah_gemm_pick_waves.
 // kFormI8x4 / kFormI8x2: the int8-MFMA design (Q8_0), 4 or 2 waves.
-enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2, kFormI8x4 = 3, kFormI8x2 = 4 };
+// kFormTile: the dequantize-once design (gemm_dq_kernel: 128 rows x 128 tokens, 4 waves).
+enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2, kFormI8x4 = 3, kFormI8x2 = 4, kFormTile = 5 };
+// The GEMM design of a part: register-blocked f16 (gemm_rb_kernel), int8 (gemm_i8_kernel),
+// dequantize-once f16 tiles (gemm_dq_kernel).  Picks its geometry and split model.
+enum : uint32_t { kGemmKindRb = 0, kGemmKindI8 = 1, kGemmKindTile = 2 };
 
 // One projection of a GEMM launch: the parts of a launch share the GGUF type, the input and its
 // operand (n_in, n_tok), and run in one grid.  `splits` is the part's own split-K count (its
@@ -305,9 +309,15 @@ AH_DEV bool ah_ts_flagged(uint32_t bits) { return (bits & 1u) != 0; }
 struct OperandArgs {
     const void *x;         // f32 / Q32.32 int64 [n_tok][n_in], or int8 codes with `scales`
     const int64_t *scales; // [n_tok][nb32] with AH_SRC_CODES
-    _Float16 *xh;          // [n_tok][kpad]
+    _Float16 *xh;          // [n_tok][kpad], or nullptr
+    // the same operand in MFMA fragment order, or nullptr: 1 KB per (32-token block tb, 16-K
+    // block kb), at ((tb * kpad / 16 + kb) * 64 + lane) * 16 bytes the 8 values K = 16 kb + 8 (lane
+    // >> 5) .. +7 of token 32 tb + (lane & 31) -- one coalesced 16-byte load per lane per fragment
+    _Float16 *xf;
     float *tok_scale;      // [n_tok] (bit 0: flagged)
     _Float16 *xmin;        // [n_tok][kpad/256][16] for Q4_K, else nullptr
+    _Float16 *xmin16;      // [n_tok][kpad/256][16] 16-group code sums X16 * 2^(e_b - E) (|X16| <= 2032:
+                           // exact in f16 unsplit) for Q2_K, else nullptr
     int8_t *fcodes;        // [n_tok][n_in] (f32 input only; flagged rows written)
     int64_t *fscales;      // [n_tok][nb32] (f32 input only; flagged rows written)
     int8_t *xc;            // int8 design: codes [n_tok][kpad] (zero past n_in), or nullptr

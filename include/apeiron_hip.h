@@ -250,6 +250,7 @@ int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
 #define AH_GEMM_DESIGN_AUTO 0u
 #define AH_GEMM_DESIGN_F16 1u
 #define AH_GEMM_DESIGN_INT8 2u
+#define AH_GEMM_DESIGN_F16_TILE 3u
 int32_t ah_set_gemm_design(ah_ctx *ctx, uint32_t ggml_type, uint32_t design);
 
 /* Grouped prefill: n_parts projections of ONE input (q/k/v, gate/up).  gemm_q8_0_group

@@ -94,11 +94,13 @@ class Device:
         _check(self.lib.ah_last_refusal_bits(self.h, ctypes.byref(b)), "last_refusal_bits")
         return b.value
 
-    GEMM_AUTO, GEMM_F16, GEMM_INT8 = 0, 1, 2
+    GEMM_AUTO, GEMM_F16, GEMM_INT8, GEMM_F16_TILE = 0, 1, 2, 3
 
     def set_gemm_design(self, ggml_type: int, design: int) -> None:
-        """The prefill GEMM design of `ggml_type` on this context (ah_set_gemm_design; F16 is the
-        default and the K-quants' only design, INT8 exists for Q8_0)."""
+        """The prefill GEMM design of `ggml_type` on this context (ah_set_gemm_design).  AUTO is
+        F16 for every type but Q2_K and Q3_K, where it is F16_TILE (the dequantize-once tiles);
+        INT8 exists for Q8_0 only, F16_TILE for Q4_K, Q2_K and Q3_K; F16 on Q2_K / Q3_K serves the
+        prefill as one streaming GEMV per token."""
         _check(self.lib.ah_set_gemm_design(self.h, ggml_type, design), "set_gemm_design")
 
     def probe_mfma_peak(self, kind: int) -> float:

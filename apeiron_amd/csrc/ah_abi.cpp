@@ -436,7 +436,7 @@ uint32_t deal_waves(const GemvPart *parts, size_t n, uint32_t n_wg, size_t act_b
 
 int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
                     const int64_t *scales, float *y, int32_t *dots, void *stream,
-                    unsigned long long *status = nullptr) {
+                    unsigned long long *status = nullptr, uint32_t key_tok = 0) {
     if (ctx && !status) status = ctx->d_status;
     if (!ctx || !w || (!x && w->n_in) || (!y && w->n_out)) return AH_ERR_INVALID_ARG;
     if (src == AH_SRC_CODES && !scales && w->n_in) return AH_ERR_INVALID_ARG;
@@ -450,6 +450,7 @@ int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     sp.n = 1;
     GemvPart &P = sp.p[0];
     P = make_part(w, src, x, scales, y, dots, st);
+    P.key_tok = key_tok;
     const uint32_t kp = kpad_of(w->n_in);
     AH_HIP(ctx, hipSetDevice(ctx->device));
     const uint32_t grid = deal_wgs(&P, 1, resident_wgs(ctx, w->type, st, kp), st);
@@ -547,7 +548,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
             for (size_t c = 0; c < n_tok;) {
                 if (!stream_ok) {
                     const int32_t st = gemv_launch(ctx, w[i], src, x_of(c), src == AH_SRC_CODES ? scales_in + c * nb : nullptr,
-                                                   y[i] + c * w[i]->n_out, nullptr, stream);
+                                                   y[i] + c * w[i]->n_out, nullptr, stream, nullptr, (uint32_t)c);
                     if (st) return st;
                     ++c;
                     continue;
@@ -558,6 +559,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                     bool st_j = false;
                     sp.p[j] = make_part(w[i], src, x_of(c + j), src == AH_SRC_CODES ? scales_in + (c + j) * nb : nullptr,
                                         y[i] + (c + j) * w[i]->n_out, nullptr, st_j);
+                    sp.p[j].key_tok = (uint32_t)(c + j);
                 }
                 const uint32_t grid = deal_wgs(sp.p, sp.n, resident_wgs(ctx, w[i]->type, true, kp), true);
                 if (grid == 0) return AH_ERR_OUT_OF_MEMORY;

@@ -395,7 +395,8 @@ AH_DEV void load_activation(const GemvPart &P, uint32_t kpad, const ActLds &A,
     const ActRsrc xr = act_rsrc(P.x, P.scales, P.src, P.n_in);
     for (uint32_t base = 0; base < nbp; base += kThreads / 4) {
         const uint32_t b = base + threadIdx.x / 4;
-        const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, 0);
+        const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status,
+                                     (unsigned long long)P.key_tok * P.n_in);
         if (b < nbp) store_quad(A, b, o);
     }
 }
@@ -826,7 +827,7 @@ __global__ void __launch_bounds__(kThreads)
         if (r < R && gl == 0 && row < P.n_out) {
             P.y[row] = sum;
             const uint32_t oc = ah_out_code(sum);
-            if (oc) ah_record(status, ah_out_key(row, oc));
+            if (oc) ah_record(status, ah_out_key((uint64_t)P.key_tok * P.n_out + row, oc));
         }
     }
 }
@@ -1419,16 +1420,17 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
         // input (K > 8192) is requested once pass 0 has consumed x0, so its load overlaps pass 1.
         const uint32_t b0 = threadIdx.x / 4;
         const bool w0 = wave * 16 < nbp;
+        const unsigned long long kb = (unsigned long long)P.key_tok * P.n_in;
         QuadOut o0 = {};
-        if (w0) o0 = quad_quant(x0, P.src, b0, status, 0);
+        if (w0) o0 = quad_quant(x0, P.src, b0, status, kb);
         const QuadIn x2 = quad_load_row(xr, P.src, P.n_in, 2 * QB + b0);  // past the row: zeros
         if (w0 && b0 < nbp) store_quad(A, b0, o0);
         if (passes > 1 && QB + wave * 16 < nbp) {
-            const QuadOut o = quad_quant(x1, P.src, QB + b0, status, 0);
+            const QuadOut o = quad_quant(x1, P.src, QB + b0, status, kb);
             if (QB + b0 < nbp) store_quad(A, QB + b0, o);
         }
         if (passes > 2 && 2 * QB + wave * 16 < nbp) {
-            const QuadOut o = quad_quant(x2, P.src, 2 * QB + b0, status, 0);
+            const QuadOut o = quad_quant(x2, P.src, 2 * QB + b0, status, kb);
             if (2 * QB + b0 < nbp) store_quad(A, 2 * QB + b0, o);
         }
         // activations past 3 * 128 blocks (K > 12288); Q6_K keeps the general form here, as the
@@ -1436,7 +1438,7 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
         for (uint32_t p = 3; p < passes; ++p) {
             const uint32_t b = p * QB + b0;
             if (p * QB + wave * 16 >= nbp) break;
-            const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, 0,
+            const QuadOut o = quad_quant(quad_load_row(xr, P.src, P.n_in, b), P.src, b, status, kb,
                                          TYPE != AH_GGML_Q6_K);
             if (b < nbp) store_quad(A, b, o);
         }
@@ -1519,7 +1521,8 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
             ah_record(status, ah_out_key((obad >> 1) + (wv < kSWaves / 2 ? 0u : fa.n_ff), (obad & 1u) ? 9u : 8u));
         ffn_epilogue(fa, f_b0, f_b1, hsum, status);
     } else {
-        if (obad != 0xFFFFFFFFu && lane == 0) ah_record(status, ah_out_key(obad >> 1, (obad & 1u) ? 9u : 8u));
+        if (obad != 0xFFFFFFFFu && lane == 0)
+            ah_record(status, ah_out_key((uint64_t)P.key_tok * P.n_out + (obad >> 1), (obad & 1u) ? 9u : 8u));
     }
 }
 

@@ -238,15 +238,23 @@ int32_t ah_gemm_noalloc_scratch_bytes(size_t *bytes);
 int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
                        const int64_t *d_scales, size_t n_tok, float *d_y, void *stream);
 
-/* Design of the Q8_0 prefill GEMM.  The reference has one CPU kernel per type (gemm_q8_0,
- * kern/gemm.rs:488-580); here two MFMA designs meet the same contract, selectable per context for
- * comparison (results agree within the tolerance, not bit for bit):
+/* Design of a type's prefill GEMM.  The reference has one CPU kernel per type (gemm_q8_0,
+ * kern/gemm.rs:488-580); here several MFMA designs meet the same contract, selectable per context
+ * and type for comparison (results agree within the tolerance, not bit for bit):
  *   AH_GEMM_DESIGN_INT8: v_mfma_i32_32x32x32_i8 exact block dots of the int8 codes, folded with
  *     d * 2^(e_b - E) formed exactly by a bf16 outer-product MFMA (no exponent band);
  *   AH_GEMM_DESIGN_F16: v_mfma_f32_32x32x16_f16 on exact f16 operands (the K-quants' design);
  *   AH_GEMM_DESIGN_AUTO (the default): the F16 design, measured 17-25% faster on MI355X at the
  *     configs[3] shapes (N = 512).
- * Only Q8_0 has an INT8 design (other types: AH_ERR_UNSUPPORTED_QUANT). */
+ *   AH_GEMM_DESIGN_F16_TILE: the dequantize-once design for Q4_K, Q2_K and Q3_K: each 256-thread
+ *     workgroup owns a 128-row x 128-token tile, converts each weight super-block to exact f16
+ *     (sc * q, folded with d and the min term per super-block) once into LDS, and every wave
+ *     feeds v_mfma_f32_32x32x16_f16 from that LDS copy and from activation fragments in
+ *     registers.
+ * Per type: Q8_0 takes AUTO, F16 or INT8; Q4_K takes AUTO (= F16), F16 or F16_TILE; Q2_K and
+ * Q3_K take AUTO (= F16_TILE) or F16, which for these two types serves the prefill as one
+ * streaming GEMV per token (the reference's matmat_q8act loop, chart/mod.rs:1955-1975); Q5_0,
+ * Q6_K and Q8_K take AUTO or F16.  Any other pairing returns AH_ERR_UNSUPPORTED_QUANT. */
 #define AH_GEMM_DESIGN_AUTO 0u
 #define AH_GEMM_DESIGN_F16 1u
 #define AH_GEMM_DESIGN_INT8 2u

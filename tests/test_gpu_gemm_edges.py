@@ -386,3 +386,52 @@ def test_gemm_odd_scale_quantacts(dev):
         st, Y = gemm_codes(dev, w, codes, scales)
         check_call(t, raw, n_out, n_in, codes, scales, st, Y, f"odd scales t{t}")
         w.free()
+
+
+def big_k23_payload(t, n_out, n_in):
+    """Every weight of every row the same sign and near the type's largest magnitude: Q2_K scale
+    bytes 0xFF (sc = m = 15), codes 3, d = 65504, dmin = -65504 (w = 65504 * 60); Q3_K all-zero
+    code, mask and scale bytes (sc - 32 = -32, q - 4 = -4) with d = 65504 (w = 65504 * 128)."""
+    rb = synth.row_bytes(t, n_in)
+    blk = np.zeros((n_out * (n_in // 256), rb // (n_in // 256)), np.uint8)
+    if t == 10:
+        blk[:, 0:80] = 0xFF
+        blk[:, 80], blk[:, 81], blk[:, 82], blk[:, 83] = 0xFF, 0x7B, 0xFF, 0xFB
+    else:
+        blk[:, 108], blk[:, 109] = 0xFF, 0x7B
+    return blk.reshape(-1)
+
+
+@pytest.mark.parametrize("t", [10, 11])
+@pytest.mark.parametrize("design", [0, 1])
+def test_k23_refusal_order_across_tokens(dev, t, design):
+    """The first refusal of a prefill is the first refusing column's (chart/mod.rs:1955-1975 runs
+    matvec_q8act column by column), also when a later column refuses at an earlier row with a
+    smaller code: OutputOverflow (9) of column 0 wins over AccumulatorOverflow (8) of column 1
+    and the reverse.  Q2_K / Q3_K through the tiles (AUTO) and the per-token GEMV route (F16)."""
+    n_out, n_in = 3, 4096
+    raw = big_k23_payload(t, n_out, n_in)
+    w = dev.upload(t, raw, n_out, n_in)
+    dev.set_gemm_design(t, design)
+    try:
+        mid = (np.full(n_in, 127, np.int8), np.full(n_in // 32, 1 << 40, np.int64))  # |y| ~ 2^50
+        top = (np.full(n_in, 127, np.int8), np.full(n_in // 32, 1 << 56, np.int64))   # |y| >= 2^63
+        low = (np.full(n_in, 1, np.int8), np.full(n_in // 32, 1 << 20, np.int64))     # no refusal
+        for c, want in (((mid, top), 9), ((top, mid), 8), ((low, mid), 9), ((low, top), 8),
+                        ((low, low, top, mid, low), 8), ((low, low, low, low, mid, top), 9)):
+            codes = np.stack([q[0] for q in c])
+            scales = np.stack([q[1] for q in c])
+            firsts = [oracle.matvec_q8act(t, raw, n_out, n_in, q[0], q[1])[0] for q in c]
+            assert next(s for s in firsts if s) == want  # the contract, column by column
+            st, _ = gemm_codes(dev, w, codes, scales)
+            assert st == want, (t, design, firsts, st)
+        # the same from f32 activations: 127 * 2^8 quantizes to codes 127 at scale 2^40, 2^30 to
+        # codes 64 at scale 2^56 (|y| >= 2^63 still)
+        xm = np.full(n_in, 127.0 * 256.0, np.float32)
+        xt = np.full(n_in, 2.0 ** 30, np.float32)
+        for rows, want in (((xm, xt), 9), ((xt, xm), 8)):
+            st, _ = gemm_f32(dev, w, np.stack(rows))
+            assert st == want, (t, design, st)
+    finally:
+        dev.set_gemm_design(t, 0)
+        w.free()

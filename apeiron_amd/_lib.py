@@ -28,7 +28,8 @@ EXPORTS = [
     "ah_gemv_q8_dots_dev", "ah_sync_status", "ah_matvec_q8act", "ah_matmat_q8act",
     "ah_quant_act", "ah_probe_mfma_peak", "ah_gemm_group_f32_dev", "ah_gemm_group_q8_dev",
     "ah_last_refusal_bits", "ah_gemm_f32_noalloc_dev", "ah_gemm_noalloc_scratch_bytes",
-    "ah_set_gemm_design", "ah_ffn_gate_up_dev", "ah_ffn_dev",
+    "ah_set_gemm_design", "ah_ffn_gate_up_dev", "ah_ffn_dev", "ah_ffn_gate_up_prefill_dev",
+    "ah_ffn_prefill_dev", "ah_set_ffn_prefill_fusion", "ah_swiglu_quant_dev",
     "ah_seq_create", "ah_seq_run", "ah_seq_sync_status", "ah_seq_free", "ah_seq_info",
 ]
 
@@ -80,6 +81,10 @@ def load() -> ctypes.CDLL:
         "ah_gemm_f32_dev": (I32, [P, P, P, S, P, P]),
         "ah_ffn_gate_up_dev": (I32, [P, P, P, P, P, P, P, P, P]),
         "ah_ffn_dev": (I32, [P, P, P, P, P, P, P, P, P]),
+        "ah_ffn_gate_up_prefill_dev": (I32, [P, P, P, P, S, P, P, P, P, P]),
+        "ah_ffn_prefill_dev": (I32, [P, P, P, P, P, S, P, P, P, P]),
+        "ah_set_ffn_prefill_fusion": (I32, [P, U32]),
+        "ah_swiglu_quant_dev": (I32, [P, P, P, S, S, P, P, P]),
         "ah_gemm_f32_noalloc_dev": (I32, [P, P, P, S, P, P]),
         "ah_gemm_noalloc_scratch_bytes": (I32, [ctypes.POINTER(S)]),
         "ah_set_gemm_design": (I32, [P, U32, U32]),

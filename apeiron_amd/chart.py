@@ -103,6 +103,11 @@ class Device:
         prefill as one streaming GEMV per token."""
         _check(self.lib.ah_set_gemm_design(self.h, ggml_type, design), "set_gemm_design")
 
+    def set_ffn_prefill_fusion(self, fused: bool) -> None:
+        """Fused (the default: one launch for Q4_K / Q2_K / Q3_K) or two-pass prefill FFN
+        (ah_set_ffn_prefill_fusion)."""
+        _check(self.lib.ah_set_ffn_prefill_fusion(self.h, 1 if fused else 0), "set_ffn_prefill_fusion")
+
     def probe_mfma_peak(self, kind: int) -> float:
         """Measured MFMA-only rate in tera-ops/s (kind 0: int8 32x32x32, 1: f16 32x32x16)."""
         out = ctypes.c_double(0.0)
@@ -211,6 +216,32 @@ def ffn_dev(dev: "Device", gate: "Tensor", up: "Tensor", down: "Tensor", x_ptr: 
     up . x)) in two launches (ah_ffn_dev)."""
     _check(dev.lib.ah_ffn_dev(dev.h, gate.h, up.h, down.h, x_ptr, y_ptr, h_codes_ptr, h_scales_ptr, stream),
            "ffn")
+
+
+def ffn_gate_up_prefill_dev(dev: "Device", gate: "Tensor", up: "Tensor", x_ptr: int, n_tok: int,
+                            h_codes_ptr: int, h_scales_ptr: int, gate_y_ptr: int | None = None,
+                            up_y_ptr: int | None = None, stream: int | None = None) -> None:
+    """The prefill FFN's gate/up with the exact SwiGLU and the hidden quant_act
+    (ah_ffn_gate_up_prefill_dev; the column path of step/cols.rs:1026-1067): f32 x[n_tok][n_embd]
+    into the hidden QuantAct codes[n_tok][n_ff] / scales[n_tok][ceil(n_ff/32)], optionally the f32
+    gate and up values it consumed."""
+    _check(dev.lib.ah_ffn_gate_up_prefill_dev(dev.h, gate.h, up.h, x_ptr, n_tok, gate_y_ptr, up_y_ptr,
+                                              h_codes_ptr, h_scales_ptr, stream), "ffn_gate_up_prefill")
+
+
+def ffn_prefill_dev(dev: "Device", gate: "Tensor", up: "Tensor", down: "Tensor", x_ptr: int, n_tok: int,
+                    y_ptr: int, h_codes_ptr: int, h_scales_ptr: int, stream: int | None = None) -> None:
+    """The prefill FFN, y[n_tok][n_embd] = down . quant_act(SwiGLU(gate . x, up . x)) per token
+    (ah_ffn_prefill_dev)."""
+    _check(dev.lib.ah_ffn_prefill_dev(dev.h, gate.h, up.h, down.h, x_ptr, n_tok, y_ptr, h_codes_ptr,
+                                      h_scales_ptr, stream), "ffn_prefill")
+
+
+def swiglu_quant_dev(dev: "Device", gate_ptr: int, up_ptr: int, n_tok: int, n_ff: int, h_codes_ptr: int,
+                     h_scales_ptr: int, stream: int | None = None) -> None:
+    """swiglu_cols + quant_cols over f32 gate / up [n_tok][n_ff] (ah_swiglu_quant_dev)."""
+    _check(dev.lib.ah_swiglu_quant_dev(dev.h, gate_ptr, up_ptr, n_tok, n_ff, h_codes_ptr, h_scales_ptr, stream),
+           "swiglu_quant")
 
 
 class GemvPlan:

@@ -43,7 +43,8 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
                           const _Float16 *xmin16,
                           const float *tok_scale, const int8_t *fcodes, const int64_t *fscales,
                           const int8_t *xc, const uint32_t *xsp,
-                          unsigned long long *status, uint32_t form, hipStream_t stream);
+                          unsigned long long *status, uint32_t form, hipStream_t stream,
+                          const GemmFfn *ffn = nullptr);
 hipError_t ah_launch_splitk_reduce(uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_tok,
                                    const float *tok_scale, unsigned long long *status, hipStream_t stream);
 uint32_t ah_gemm_pick_splits(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t n_tok,
@@ -53,6 +54,7 @@ uint32_t ah_gemm_part_wg4(uint32_t type, uint32_t n_out, uint32_t n_in, uint32_t
 uint32_t ah_gemm_max_parts(uint32_t type);
 uint32_t ah_gemm_pick_waves(uint32_t type, uint64_t n_wg4, uint32_t cus, bool int8);
 hipError_t ah_launch_gemm_operand(const OperandArgs &o, hipStream_t stream);
+hipError_t ah_launch_swiglu_quant(const SwigluArgs &a, hipStream_t stream);
 hipError_t ah_probe_mfma(uint32_t kind, uint32_t cus, const uint32_t *d_seed, uint32_t *d_sink,
                          hipStream_t stream, double *tops);
 
@@ -76,6 +78,10 @@ struct ah_ctx {
     int cu_count = 256;
     uint32_t design[32] = {};  // GEMM design per GGUF type (ah_set_gemm_design; 0 = AUTO)
     void *scratch = nullptr;  // device scratch for GEMM operands / host-form staging
+    // the unfused prefill FFN's gate / up outputs when the caller keeps none (grown on demand)
+    void *ffn_buf = nullptr;
+    size_t ffn_buf_bytes = 0;
+    bool ffn_unfused = false;  // ah_set_ffn_prefill_fusion(ctx, 0): the two-pass prefill FFN
     size_t scratch_bytes = 0;
     // streaming-GEMV occupancy by (type, LDS bytes): a runtime query per launch costs more host
     // time than a small GEMV takes on the device
@@ -480,15 +486,31 @@ int32_t reset_status(ah_ctx *ctx) {
 // `fixed` (with `fixed_cap` bytes) replaces the context's growable scratch: the call then neither
 // allocates nor frees anything (device or host, for up to kStackParts parts), and refuses with
 // AH_ERR_SCRATCH_LIMIT when its operands and partials need more than `fixed_cap`.
+// `opt` (optional): per-part token offsets of the refusal keys (part i's refusals are keyed as if
+// its tokens were numbered from tok0[i]: the prefill FFN's up projection after its gate), the
+// status word the call records into, and the fused FFN form (parts {gate, up} of one
+// dequantize-once type: one launch whose epilogue writes the hidden QuantAct; `y` then names the
+// optional f32 gate / up outputs).
 constexpr size_t kStackParts = 16;
+struct GroupOpts {
+    const uint32_t *tok0 = nullptr;
+    unsigned long long *status = nullptr;
+    const GemmFfn *ffn = nullptr;
+};
 int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w, uint32_t src,
                           const void *x, const int64_t *scales_in, size_t n_tok, float *const *y,
-                          void *stream, uint8_t *fixed = nullptr, size_t fixed_cap = 0) {
+                          void *stream, uint8_t *fixed = nullptr, size_t fixed_cap = 0,
+                          const GroupOpts *opt = nullptr) {
     if (!ctx || !w || !y || n_parts == 0 || n_parts > 65536 || !w[0]) return AH_ERR_INVALID_ARG;
+    const GemmFfn *ffn = opt ? opt->ffn : nullptr;
+    unsigned long long *const status = opt && opt->status ? opt->status : ctx->d_status;
+    auto tok0_of = [&](size_t i) -> uint32_t { return opt && opt->tok0 ? opt->tok0[i] : 0u; };
     const size_t n_in_sz = w[0]->n_in;
     bool any_q4k = false;
+    if (ffn && (n_parts != 2 || !w[1] || w[0]->type != w[1]->type || w[0]->n_out != w[1]->n_out))
+        return AH_ERR_INVALID_ARG;
     for (size_t i = 0; i < n_parts; ++i) {
-        if (!w[i] || (!y[i] && w[i]->n_out) || w[i]->n_in != n_in_sz) return AH_ERR_INVALID_ARG;
+        if (!w[i] || (!ffn && !y[i] && w[i]->n_out) || w[i]->n_in != n_in_sz) return AH_ERR_INVALID_ARG;
         // a workgroup's output rows (128 tokens x n_out f32) are addressed with 32-bit offsets
         if (w[i]->n_out > (0xFFFFFF00ull / (128 * 4))) return AH_ERR_INVALID_ARG;
         any_q4k = any_q4k || w[i]->type == AH_GGML_Q4_K;
@@ -500,6 +522,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     // when it is selected, the operand pass then writing int8 codes and block factors (and the f16
     // operand only if another part needs it); Q4_K parts may take the dequantize-once tiles.
     auto kind_of = [&](uint32_t type) -> uint32_t {
+        if (ffn) return kGemmKindTile;  // the fused FFN form runs on the dequantize-once tiles
         const uint32_t d = type < 32 ? ctx->design[type] : 0u;
         if (type == AH_GGML_Q8_0 && d == AH_GEMM_DESIGN_INT8) return kGemmKindI8;
         if (type == AH_GGML_Q4_K && d == AH_GEMM_DESIGN_F16_TILE) return kGemmKindTile;
@@ -548,7 +571,8 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
             for (size_t c = 0; c < n_tok;) {
                 if (!stream_ok) {
                     const int32_t st = gemv_launch(ctx, w[i], src, x_of(c), src == AH_SRC_CODES ? scales_in + c * nb : nullptr,
-                                                   y[i] + c * w[i]->n_out, nullptr, stream, nullptr, (uint32_t)c);
+                                                   y[i] + c * w[i]->n_out, nullptr, stream, status,
+                                                   tok0_of(i) + (uint32_t)c);
                     if (st) return st;
                     ++c;
                     continue;
@@ -559,12 +583,12 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                     bool st_j = false;
                     sp.p[j] = make_part(w[i], src, x_of(c + j), src == AH_SRC_CODES ? scales_in + (c + j) * nb : nullptr,
                                         y[i] + (c + j) * w[i]->n_out, nullptr, st_j);
-                    sp.p[j].key_tok = (uint32_t)(c + j);
+                    sp.p[j].key_tok = tok0_of(i) + (uint32_t)(c + j);
                 }
                 const uint32_t grid = deal_wgs(sp.p, sp.n, resident_wgs(ctx, w[i]->type, true, kp), true);
                 if (grid == 0) return AH_ERR_OUT_OF_MEMORY;
                 AH_HIP(ctx, ah_launch_gemv_stream(w[i]->type, sp, nullptr, nullptr, grid,
-                                                  (uint32_t)ah_gemv_act_bytes(kp), ctx->d_status, pick(ctx, stream)));
+                                                  (uint32_t)ah_gemv_act_bytes(kp), status, pick(ctx, stream)));
                 c += sp.n;
             }
         }
@@ -586,7 +610,19 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                 rw[k] = w[i];
                 ry[k++] = y[i];
             }
-        return gemm_group_launch(ctx, k, rw, src, x, scales_in, n_tok, ry, stream, fixed, fixed_cap);
+        if (opt && opt->tok0) {  // the remaining parts keep their token offsets
+            GroupOpts o2 = *opt;
+            uint32_t t_stack[kStackParts];
+            std::vector<uint32_t> t_heap;
+            if (n_parts > kStackParts) t_heap.resize(n_parts);
+            uint32_t *t0 = n_parts > kStackParts ? t_heap.data() : t_stack;
+            size_t q = 0;
+            for (size_t i = 0; i < n_parts; ++i)
+                if (!gemv23(w[i])) t0[q++] = tok0_of(i);
+            o2.tok0 = t0;
+            return gemm_group_launch(ctx, k, rw, src, x, scales_in, n_tok, ry, stream, fixed, fixed_cap, &o2);
+        }
+        return gemm_group_launch(ctx, k, rw, src, x, scales_in, n_tok, ry, stream, fixed, fixed_cap, opt);
     }
     const uint32_t n_in = (uint32_t)n_in_sz, N = (uint32_t)n_tok;
     const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
@@ -619,9 +655,10 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         d.w_bytes = (uint32_t)w[i]->bytes;
         d.row_bytes = (uint32_t)w[i]->row_bytes;
         d.n_out = (uint32_t)w[i]->n_out;
-        d.splits = d.n_out ? ah_gemm_pick_splits(w[i]->type, d.n_out, n_in, N, cus, kind_of(w[i]->type)) : 1;
+        d.splits = d.n_out && !ffn ? ah_gemm_pick_splits(w[i]->type, d.n_out, n_in, N, cus, kind_of(w[i]->type)) : 1;
         d.y = y[i];
         d.partials = nullptr;
+        d.key0 = (uint64_t)tok0_of(i) * d.n_out;
         if (d.splits > 1) {
             part_off[i] = part_bytes;
             part_bytes = align256(part_bytes + (size_t)d.splits * N * d.n_out * 4);
@@ -679,13 +716,19 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     o.fscales = keep ? fscales : nullptr;
     o.xc = xc;
     o.xsp = xsp;
-    o.status = ctx->d_status;
+    o.status = status;
     o.n_tok = N;
     o.n_in = n_in;
     o.nb32 = nb32;
     o.kpad = kpad;
     o.src = src;
     AH_HIP(ctx, ah_launch_gemm_operand(o, s));
+    if (ffn) {
+        if (pd[0].n_out == 0) return AH_OK;
+        AH_HIP(ctx, ah_launch_gemm(w[0]->type, 1, pd, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp,
+                                   status, kFormTileFfn, s, ffn));
+        return AH_OK;
+    }
     // runs of consecutive parts of one type (parts with no rows skipped)
     bool any_split = false;
     for (size_t i = 0; i < n_parts;) {
@@ -706,7 +749,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                 any_split = any_split || pd[i].splits > 1;
             }
             AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp,
-                                       ctx->d_status, kFormTile, s));
+                                       status, kFormTile, s));
             continue;
         }
         // K-quant parts of both types (q/k beside v) share one grid when together they leave CUs
@@ -741,9 +784,9 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                                   ? kForm4x4
                                   : ah_gemm_pick_waves(type, wg4, cus, kind_of(type) == kGemmKindI8);
         AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp,
-                                   ctx->d_status, form, s));
+                                   status, form, s));
     }
-    if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd, N, ts, ctx->d_status, s));
+    if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd, N, ts, status, s));
     return AH_OK;
 }
 
@@ -822,6 +865,7 @@ int32_t ah_destroy(ah_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->ffn_buf) (void)hipFree(ctx->ffn_buf);
     (void)hipFree(ctx->d_status);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -1043,6 +1087,105 @@ int32_t ah_ffn_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, cons
     // the down projection's refusals go to the second status word (reported only when the
     // gate/up launch refused nothing)
     return gemv_launch(ctx, down, AH_SRC_CODES, d_h_codes, d_h_scales, d_y, nullptr, stream, ctx->d_status + 1);
+}
+
+int32_t ah_swiglu_quant_dev(ah_ctx *ctx, const float *d_gate, const float *d_up, size_t n_tok, size_t n_ff,
+                            int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
+    if (!ctx) return AH_ERR_INVALID_ARG;
+    if (n_tok == 0 || n_ff == 0) return AH_OK;
+    if (!d_gate || !d_up || !d_h_codes || !d_h_scales) return AH_ERR_INVALID_ARG;
+    if (reinterpret_cast<uintptr_t>(d_gate) % 4 || reinterpret_cast<uintptr_t>(d_up) % 4 ||
+        reinterpret_cast<uintptr_t>(d_h_scales) % 8)
+        return AH_ERR_INVALID_ARG;
+    if (n_tok >= (1ull << 24) || n_ff >= (1ull << 31) || (uint64_t)n_tok * n_ff >= (1ull << 45)) return AH_ERR_INVALID_ARG;
+    SwigluArgs a = {d_gate, d_up, d_h_codes, d_h_scales, (uint32_t)n_tok, (uint32_t)n_ff, 0ull,
+                    (uint64_t)n_tok * n_ff, ctx->d_status};
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, ah_launch_swiglu_quant(a, pick(ctx, stream)));
+    return AH_OK;
+}
+
+int32_t ah_set_ffn_prefill_fusion(ah_ctx *ctx, uint32_t fused) {
+    if (!ctx || fused > 1) return AH_ERR_INVALID_ARG;
+    ctx->ffn_unfused = fused == 0;
+    return AH_OK;
+}
+
+int32_t ah_ffn_gate_up_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const float *d_x,
+                                   size_t n_tok, float *d_gate_y, float *d_up_y, int8_t *d_h_codes,
+                                   int64_t *d_h_scales, void *stream) {
+    if (!ctx || !gate || !up) return AH_ERR_INVALID_ARG;
+    if (gate->type != up->type || gate->n_out != up->n_out || gate->n_in != up->n_in) return AH_ERR_INVALID_ARG;
+    const size_t n_ff = gate->n_out;
+    if (n_tok == 0 || n_ff == 0) return AH_OK;
+    if (!d_x || !d_h_codes || !d_h_scales || gate->n_in == 0) return AH_ERR_INVALID_ARG;
+    if (reinterpret_cast<uintptr_t>(d_x) % 4 || reinterpret_cast<uintptr_t>(d_h_scales) % 8 ||
+        reinterpret_cast<uintptr_t>(d_gate_y) % 4 || reinterpret_cast<uintptr_t>(d_up_y) % 4)
+        return AH_ERR_INVALID_ARG;
+    // refusal keys up to 4 * n_tok * n_ff (gate, up, SwiGLU, hidden blocks)
+    if (n_tok >= (1ull << 24) || (uint64_t)n_tok * n_ff >= (1ull << 45)) return AH_ERR_INVALID_ARG;
+    const ah_tensor *w2[2] = {gate, up};
+    const uint32_t t = gate->type;
+    if (!ctx->ffn_unfused && (t == AH_GGML_Q4_K || t == AH_GGML_Q2_K || t == AH_GGML_Q3_K)) {
+        // one launch: gate and up rows of the same hidden indices in each tile, the SwiGLU and the
+        // hidden quantizer in its epilogue
+        GemmFfn f = {up->d, d_gate_y, d_up_y, d_h_codes, d_h_scales};
+        float *y2[2] = {d_gate_y, d_up_y};
+        GroupOpts o;
+        o.ffn = &f;
+        return gemm_group_launch(ctx, 2, w2, AH_SRC_F32, d_x, nullptr, n_tok, y2, stream, nullptr, 0, &o);
+    }
+    // two passes: gate and up as one grouped GEMM (up's refusals keyed after all of gate's), then
+    // the SwiGLU + hidden quantizer over their f32 outputs
+    float *g = d_gate_y, *u = d_up_y;
+    if (!g || !u) {
+        const size_t want = 2 * align256(n_tok * n_ff * 4);
+        if (want > ctx->ffn_buf_bytes) {
+            if (ctx->ffn_buf) {
+                AH_HIP(ctx, hipDeviceSynchronize());  // queued kernels may still use the old buffer
+                AH_HIP(ctx, hipFree(ctx->ffn_buf));
+                ctx->ffn_buf = nullptr;
+                ctx->ffn_buf_bytes = 0;
+            }
+            if (hipMalloc(&ctx->ffn_buf, want) != hipSuccess) {
+                ctx->ffn_buf = nullptr;
+                return AH_ERR_OUT_OF_MEMORY;
+            }
+            ctx->ffn_buf_bytes = want;
+        }
+        float *b = static_cast<float *>(ctx->ffn_buf);
+        if (!g) g = b;
+        if (!u) u = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(b) + align256(n_tok * n_ff * 4));
+    }
+    float *y2[2] = {g, u};
+    const uint32_t tok0[2] = {0u, (uint32_t)n_tok};
+    GroupOpts o;
+    o.tok0 = tok0;
+    int32_t st = gemm_group_launch(ctx, 2, w2, AH_SRC_F32, d_x, nullptr, n_tok, y2, stream, nullptr, 0, &o);
+    if (st) return st;
+    const uint64_t NF = (uint64_t)n_tok * n_ff;
+    SwigluArgs a = {g, u, d_h_codes, d_h_scales, (uint32_t)n_tok, (uint32_t)n_ff, 2 * NF, 3 * NF, ctx->d_status};
+    AH_HIP(ctx, ah_launch_swiglu_quant(a, pick(ctx, stream)));
+    return AH_OK;
+}
+
+int32_t ah_ffn_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                           const float *d_x, size_t n_tok, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales,
+                           void *stream) {
+    if (!ctx || !gate || !down) return AH_ERR_INVALID_ARG;
+    if (down->n_in != gate->n_out || down->n_out != gate->n_in) return AH_ERR_INVALID_ARG;
+    if (n_tok && down->n_out && !d_y) return AH_ERR_INVALID_ARG;
+    if (reinterpret_cast<uintptr_t>(d_h_codes) % 4) return AH_ERR_INVALID_ARG;
+    int32_t st = ah_ffn_gate_up_prefill_dev(ctx, gate, up, d_x, n_tok, nullptr, nullptr, d_h_codes, d_h_scales,
+                                            stream);
+    if (st) return st;
+    if (n_tok == 0 || down->n_out == 0) return AH_OK;
+    // the down projection from the hidden QuantAct; its refusals go to the second status word
+    // (reported only when nothing before it refused)
+    GroupOpts o;
+    o.status = ctx->d_status + 1;
+    return gemm_group_launch(ctx, 1, &down, AH_SRC_CODES, d_h_codes, d_h_scales, n_tok, &d_y, stream, nullptr, 0,
+                             &o);
 }
 
 int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w,

@@ -30,6 +30,7 @@
 // launch may cover several projections of one input (parts).  Split-K writes partials that one
 // pass per grouped call reduces in fixed order.
 #include "ah_internal.h"
+#include "ah_swiglu.h"
 
 namespace {
 
@@ -94,6 +95,7 @@ struct GemmPartArgs {
     uint32_t splits, wg_begin;
     uint32_t tok_tiles;        // token tiles of the part's type
     uint32_t type;             // GGUF type (read by the mixed K-quant kernel)
+    uint64_t key0;             // added to the part's output refusal keys (GemmPartDesc::key0)
 };
 struct GemmArgs {
     GemmPartArgs p[kGemmMaxParts];
@@ -109,6 +111,7 @@ struct GemmArgs {
     const int8_t *xc;          // int8 design: codes [n_tok][kpad] (zero past n_in)
     const uint32_t *xsp;       // int8 design: [n_tok][kpad/32] block factors 2^(e_b - E_tok), bf16 x2
     uint32_t n_wg;             // real workgroup count over all parts
+    GemmFfn ffn;               // kFormTileFfn: the up projection and the hidden QuantAct outputs
 };
 
 constexpr uint32_t kOob = 0xFFFFFFF0u;  // a buffer offset past any operand: reads zeros
@@ -437,7 +440,7 @@ AH_DEV __attribute__((always_inline)) void gemm_store(const GemmArgs &a, const G
             const uint32_t tl = 32 * m + 8 * (r / 4) + 4 * h + (r % 4), row = row_w + 32 * n + j;
             if (!rl[n] || tl >= ntile || ah_ts_flagged(ah_ld32(rt, 4 * tl))) continue;
             const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, (tl * pa.n_out + row) * 4u, 0, 1));
-            if (const uint32_t oc = ah_out_code(v)) ah_record(a.status, ah_out_key((uint64_t)(tok0 + tl) * pa.n_out + row, oc));
+            if (const uint32_t oc = ah_out_code(v)) ah_record(a.status, ah_out_key(pa.key0 + (uint64_t)(tok0 + tl) * pa.n_out + row, oc));
         }
     }
     if ((fm[0] | fm[1]) != 0ull) {
@@ -460,7 +463,7 @@ AH_DEV __attribute__((always_inline)) void gemm_store(const GemmArgs &a, const G
                 const float ts = ah_ts_value(__builtin_bit_cast(uint32_t, a.tok_scale[t]));
                 if (h == 0 && rl[0]) {
                     ybase[(size_t)tl * pa.n_out + row] = scaled ? v : v / ts;
-                    if (const uint32_t oc = scaled ? ah_out_code(v) : 0u) ah_record(a.status, ah_out_key((uint64_t)t * pa.n_out + row, oc));
+                    if (const uint32_t oc = scaled ? ah_out_code(v) : 0u) ah_record(a.status, ah_out_key(pa.key0 + (uint64_t)t * pa.n_out + row, oc));
                 }
             }
         }
@@ -1013,6 +1016,7 @@ struct ReducePart {
     const float *part;
     float *y;
     uint64_t begin;  // first work item of the part
+    uint64_t key0;   // added to the part's output refusal keys
     uint32_t n_out, splits;
 };
 struct ReduceArgs {
@@ -1057,7 +1061,7 @@ __global__ void splitk_reduce(ReduceArgs r) {
             const float ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                if (const uint32_t oc = ah_out_code(ov[c])) { ah_record(r.status, ah_out_key(e + c, oc)); break; }
+                if (const uint32_t oc = ah_out_code(ov[c])) { ah_record(r.status, ah_out_key(P.key0 + e + c, oc)); break; }
         } else {
             float s = 0.0f;
             for (uint32_t z = 0; z < P.splits; z += kReduceBatch) {
@@ -1070,7 +1074,7 @@ __global__ void splitk_reduce(ReduceArgs r) {
                     if (z + j < P.splits) s += v[j];
             }
             P.y[li] = s * ts_at(r.tok_scale, li / P.n_out);
-            if (const uint32_t oc = ah_out_code(P.y[li])) ah_record(r.status, ah_out_key(li, oc));
+            if (const uint32_t oc = ah_out_code(P.y[li])) ah_record(r.status, ah_out_key(P.key0 + li, oc));
         }
     }
 }
@@ -1323,7 +1327,7 @@ AH_DEV __attribute__((always_inline)) void dq_store(const GemmArgs &a, const Gem
             const uint32_t tl = 32 * m + 8 * (r / 4) + 4 * h + (r % 4), row = row_w + 32 * n + j;
             if (!rl[n] || tl >= ntile || ah_ts_flagged(__builtin_bit_cast(uint32_t, ts[tl]))) continue;
             const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, (tl * pa.n_out + row) * 4u, 0, 1));
-            if (const uint32_t oc = ah_out_code(v)) ah_record(a.status, ah_out_key((uint64_t)(tok_w + tl) * pa.n_out + row, oc));
+            if (const uint32_t oc = ah_out_code(v)) ah_record(a.status, ah_out_key(pa.key0 + (uint64_t)(tok_w + tl) * pa.n_out + row, oc));
         }
     }
     if (fm != 0ull) {
@@ -1345,9 +1349,86 @@ AH_DEV __attribute__((always_inline)) void dq_store(const GemmArgs &a, const Gem
                 v += __shfl_xor(v, 32, 64);
                 if (h == 0 && rl[n]) {
                     ybase[(size_t)tl * pa.n_out + row] = scaled ? v : v / tsv;
-                    if (const uint32_t oc = scaled ? ah_out_code(v) : 0u) ah_record(a.status, ah_out_key((uint64_t)t * pa.n_out + row, oc));
+                    if (const uint32_t oc = scaled ? ah_out_code(v) : 0u) ah_record(a.status, ah_out_key(pa.key0 + (uint64_t)t * pa.n_out + row, oc));
                 }
             }
+        }
+    }
+}
+
+// Epilogue of the prefill FFN's fused gate/up tiles (kFormTileFfn).  The wave's accumulators
+// hold gate (n = 0) and up (n = 1) of the same 32 hidden indices for its 64 tokens.  They go
+// through the wave's own 16 KB of LDS ([2][64 tokens][32 hidden] f32, token scales applied,
+// flagged tokens replaced by the exact path's values), then each of 32 rounds takes two tokens,
+// one per half-wave, 32 hidden values each: the optional f32 gate / up outputs, their output
+// refusals, h = round_shift_32(silu_fixed(to_q32(gate)) * to_q32(up)) and quant_act of the
+// 32-block, all in the reference FFN's refusal order (chart/ffn.rs:1712-1720, step/cols.rs:
+// 1026-1067): the gate projection's outputs (key t * n_ff + k), the up projection's (past all
+// gate keys), the elements' conversion or SwiGLU, then the hidden quantizer's blocks.
+template <int TYPE>
+AH_DEV __attribute__((always_inline)) void dq_ffn_store(const GemmArgs &a, const GemmPartArgs &pa,
+                                                        const f32x16 (&acc)[2][2], const float *ts, float *E,
+                                                        uint32_t hid_w, uint32_t tok_w) {
+    const uint32_t lane = threadIdx.x & 63u, j = lane & 31u, h = lane >> 5;
+    const uint32_t n_ff = pa.n_out, N = a.n_tok;
+    const uint32_t ntile = N > tok_w ? (N - tok_w < 64u ? N - tok_w : 64u) : 0u;
+    const uint32_t k = hid_w + j;
+    const bool kl = k < n_ff;
+    const uint64_t NF = (uint64_t)N * n_ff;
+    const uint32_t nbh = (n_ff + 31) / 32, blk = hid_w / 32;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(ts + 32 * m + 8 * q + 4 * h);
+            const uint32_t sc[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t tl = 32 * m + 8 * q + 4 * h + i;
+                const float f = ah_ts_value(sc[i]);
+                E[tl * 32 + j] = acc[m][0][4 * q + i] * f;
+                E[2048 + tl * 32 + j] = acc[m][1][4 * q + i] * f;
+            }
+        }
+    }
+    // flagged tokens: both projections' rows by the exact path, the lane halves taking
+    // alternate super-blocks
+    uint64_t fm = __builtin_amdgcn_ballot_w64(lane < ntile && ah_ts_flagged(__builtin_bit_cast(uint32_t, ts[lane])));
+    const uint32_t nb32 = (a.n_in + 31) / 32, nsb = a.kpad / 256;
+    while (fm) {
+        const uint32_t tl = (uint32_t)__builtin_ctzll(fm);
+        fm &= fm - 1;
+        const size_t t = (size_t)tok_w + tl;
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            const uint8_t *w = n ? a.ffn.w_up : pa.w;
+            float v = kl ? exact_row<TYPE>(w + (size_t)k * pa.row_bytes, a.fcodes + t * a.n_in, a.fscales + t * nb32,
+                                           a.n_in, 0u, nsb, h)
+                         : 0.0f;
+            v += __shfl_xor(v, 32, 64);
+            if (h == 0) E[2048 * n + tl * 32 + j] = v;
+        }
+    }
+    const size_t pitch = n_ff;
+    for (uint32_t i = 0; i < 32u; ++i) {
+        const uint32_t tl = 2 * i + h;
+        const bool tv = tl < ntile, live = tv && kl;
+        const uint64_t t = (uint64_t)tok_w + tl;
+        const float g = E[tl * 32 + j], u = E[2048 + tl * 32 + j];
+        const size_t e = (size_t)t * pitch + k;
+        if (live) {
+            if (a.ffn.gy) a.ffn.gy[e] = g;
+            if (a.ffn.uy) a.ffn.uy[e] = u;
+            if (const uint32_t oc = ah_out_code(g)) ah_record(a.status, ah_out_key(e, oc));
+            if (const uint32_t oc = ah_out_code(u)) ah_record(a.status, ah_out_key(NF + e, oc));
+        }
+        const HiddenQ hq = swiglu_quant32(__builtin_bit_cast(uint32_t, g), __builtin_bit_cast(uint32_t, u), live);
+        if (hq.err) ah_record(a.status, ah_out_key(2 * NF + e, (uint32_t)hq.err));
+        if (live) a.ffn.h_codes[e] = (int8_t)hq.code;
+        if (tv && j == 0) {
+            const uint64_t bi = t * nbh + blk;
+            if (hq.bad_block) ah_record(a.status, ah_out_key(3 * NF + bi, 7u));
+            a.ffn.h_scales[bi] = (int64_t)hq.scale;
         }
     }
 }
@@ -1362,11 +1443,19 @@ AH_DEV __attribute__((always_inline)) void dq_store(const GemmArgs &a, const Gem
 // each run per K-step, interleaved with the MFMAs), and one barrier per stage hands the plane over.
 // At the end of a super-block the MFMA sums fold with the row's d, and the min term (Q4_K, Q2_K
 // mins; Q3_K the codes' -4) rides on one more MFMA per tile.
-template <int TYPE>
+//
+// FFN (kFormTileFfn): the tile's 128 rows are 64 hidden indices of a gate/up pair: row
+// 64 s + 32 n + i is hidden index 64 rtile + 32 s + i of the gate (n = 0) or up (n = 1)
+// projection, so each wave's two row blocks are the gate and up of the same 32 hidden indices,
+// and the epilogue (dq_ffn_store) writes the hidden QuantAct.  No split-K: the SwiGLU needs whole
+// sums.  Its LDS grows to 64 KB (the epilogue's exchange reuses the planes), still two
+// workgroups per CU.
+template <int TYPE, bool FFN = false>
 __global__ void __launch_bounds__(256, 2) gemm_dq_kernel(GemmArgs a) {
     static_assert(dq::served<TYPE>(), "dequantize-once design: Q4_K, Q2_K, Q3_K");
     constexpr uint32_t kSB = dq::sb_bytes<TYPE>();
-    constexpr uint32_t kOD = 2 * dq::kPlane, kOM = kOD + 2048, kOT = kOM + 8192;
+    constexpr uint32_t kOD = 2 * dq::kPlane, kOM = kOD + 2048;
+    constexpr uint32_t kOT = FFN ? 65536u : kOM + 8192;
     __shared__ __align__(16) uint8_t lds[kOT + 512];
     const uint32_t per = gridDim.x >> 3;
     const uint32_t L = (blockIdx.x & 7u) * per + (blockIdx.x >> 3);
@@ -1385,11 +1474,13 @@ __global__ void __launch_bounds__(256, 2) gemm_dq_kernel(GemmArgs a) {
     const uint32_t wr = wv & 1u, wt = wv >> 1;  // the wave's row half and token half
     const uint32_t row0 = rtile * dq::kBM, tok0 = tt * dq::kBN;
     const uint32_t ntile = a.n_tok - tok0 < dq::kBN ? a.n_tok - tok0 : dq::kBN;
-    // this thread's conversion row (32 per wave) and its byte offset
+    // this thread's conversion row (32 per wave) and its byte offset; FFN: hidden index
+    // 64 rtile + 32 (wv / 2) + j of the gate (even waves) or up (odd waves) projection
     const uint32_t crow = 32u * wv + j;
-    const bool clive = row0 + crow < pa.n_out;
-    const uint32_t croff = clive ? (row0 + crow) * pa.row_bytes : 0u;
-    const __amdgpu_buffer_rsrc_t rs = ah_rsrc(pa.w, pa.w_bytes);
+    const uint32_t csrc = FFN ? rtile * 64u + 32u * (wv >> 1) + j : row0 + crow;
+    const bool clive = csrc < pa.n_out;
+    const uint32_t croff = clive ? csrc * pa.row_bytes : 0u;
+    const __amdgpu_buffer_rsrc_t rs = ah_rsrc(FFN && (wv & 1u) ? a.ffn.w_up : pa.w, pa.w_bytes);
     const uint32_t nkb = a.kpad / 16, nsb = a.kpad / 256;
     const uint32_t ntb = (a.n_tok + 31) / 32;
     // the wave's two 32-token blocks of the fragment-order operand
@@ -1544,7 +1635,11 @@ __global__ void __launch_bounds__(256, 2) gemm_dq_kernel(GemmArgs a) {
         stage(std::integral_constant<int, 3>{}, st + 3, par);
         par ^= 1u;
     }
-    dq_store<TYPE>(a, pa, acc, TS + 64u * wt, row0 + 64u * wr, tok0 + 64u * wt, split, st_begin / 4, st_end / 4);
+    if constexpr (FFN)
+        dq_ffn_store<TYPE>(a, pa, acc, TS + 64u * wt, reinterpret_cast<float *>(lds) + 4096u * wv,
+                           rtile * 64u + 32u * wr, tok0 + 64u * wt);
+    else
+        dq_store<TYPE>(a, pa, acc, TS + 64u * wt, row0 + 64u * wr, tok0 + 64u * wt, split, st_begin / 4, st_end / 4);
 }
 
 }  // namespace
@@ -1727,11 +1822,14 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
                           const _Float16 *xmin16,
                           const float *tok_scale, const int8_t *fcodes, const int64_t *fscales,
                           const int8_t *xc, const uint32_t *xsp,
-                          unsigned long long *status, uint32_t form, hipStream_t stream) {
+                          unsigned long long *status, uint32_t form, hipStream_t stream, const GemmFfn *ffn) {
     const bool mixed = type == kGemmMixedKQuant;  // Q4_K and Q6_K parts, 4-wave form
     const bool int8 = form == kFormI8x4 || form == kFormI8x2;
-    const bool tile = form == kFormTile;
+    const bool ffn_form = form == kFormTileFfn;
+    const bool tile = form == kFormTile || ffn_form;
     if (n_parts == 0 || n_parts > (mixed || tile ? kGemmMaxParts : rb::max_parts_of(type))) return hipErrorInvalidValue;
+    if (ffn_form && (!ffn || !ffn->w_up || !ffn->h_codes || !ffn->h_scales || n_parts != 1 || parts[0].splits > 1))
+        return hipErrorInvalidValue;
     if (int8 && (type != AH_GGML_Q8_0 || !xc || !xsp)) return hipErrorInvalidValue;
     if (tile && (!xf || (type != AH_GGML_Q4_K && type != AH_GGML_Q2_K && type != AH_GGML_Q3_K) ||
                  (type != AH_GGML_Q4_K && !xmin16)))
@@ -1754,6 +1852,7 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     a.fscales = fscales;
     a.xc = xc;
     a.xsp = xsp;
+    a.ffn = ffn_form ? *ffn : GemmFfn{};
     uint32_t wg = 0;
     for (uint32_t i = 0; i < kGemmMaxParts; ++i) {
         GemmPartArgs &P = a.p[i];
@@ -1778,7 +1877,9 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
         P.wg_begin = wg;
         P.tok_tiles = (n_tok + g.toks - 1) / g.toks;
         P.type = pt;
-        wg += ((d.n_out + g.rows - 1) / g.rows) * P.tok_tiles * P.splits;
+        P.key0 = d.key0;
+        const uint32_t rows = ffn_form ? g.rows / 2 : g.rows;  // FFN: a tile's rows are hidden pairs
+        wg += ((d.n_out + rows - 1) / rows) * P.tok_tiles * P.splits;
     }
     a.n_wg = wg;
     if (wg == 0) return hipSuccess;
@@ -1788,6 +1889,12 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     if (form == kForm2x2) hipLaunchKernelGGL((gemm_rb_kernel<T, 2, 2>), rb_grid, blk, 0, stream, a);    \
     else if (form == kForm2x4) hipLaunchKernelGGL((gemm_rb_kernel<T, 2, 4>), rb_grid, blk, 0, stream, a); \
     else hipLaunchKernelGGL((gemm_rb_kernel<T, 4, 4>), rb_grid, blk, 0, stream, a);
+    if (ffn_form) {
+        if (type == AH_GGML_Q4_K) hipLaunchKernelGGL((gemm_dq_kernel<AH_GGML_Q4_K, true>), rb_grid, dim3(256), 0, stream, a);
+        else if (type == AH_GGML_Q2_K) hipLaunchKernelGGL((gemm_dq_kernel<AH_GGML_Q2_K, true>), rb_grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((gemm_dq_kernel<AH_GGML_Q3_K, true>), rb_grid, dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
     if (tile) {
         if (type == AH_GGML_Q4_K) hipLaunchKernelGGL(gemm_dq_kernel<AH_GGML_Q4_K>, rb_grid, dim3(256), 0, stream, a);
         else if (type == AH_GGML_Q2_K) hipLaunchKernelGGL(gemm_dq_kernel<AH_GGML_Q2_K>, rb_grid, dim3(256), 0, stream, a);
@@ -1836,6 +1943,7 @@ hipError_t ah_launch_splitk_reduce(uint32_t n_parts, const GemmPartDesc *parts, 
             P.y = d.y;
             P.n_out = d.n_out;
             P.splits = d.splits;
+            P.key0 = d.key0;
         }
         if (r.n_parts == 0) continue;
         uint64_t total = 0;

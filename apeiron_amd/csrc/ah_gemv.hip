@@ -19,6 +19,7 @@
 // The activation is quantized once per workgroup into LDS by one lane per 32-block (no
 // cross-lane traffic): codes, per-32 f32 scale, per-32 and per-16 code sums.
 #include "ah_internal.h"
+#include "ah_swiglu.h"
 
 namespace {
 
@@ -1104,94 +1105,6 @@ AH_DEV float group_sum(float s, uint32_t G) {
     return s;
 }
 
-// ---- exact SwiGLU (the fused FFN's hidden activation) ------------------------------------------
-
-typedef __int128 i128;
-constexpr int64_t kOneQ32 = (int64_t)1 << 32;
-
-// round(v / 2^32), ties away from zero, for |v| <= 2^63 - 2^31, branch-free in i64
-AH_DEV int64_t round_div_2p32_i64(int64_t v) {
-    const int64_t s = v >> 63;
-    const uint64_t a = (uint64_t)((v ^ s) - s);
-    const int64_t q = (int64_t)((a + (1ull << 31)) >> 32);
-    return (q ^ s) - s;
-}
-// exp(x) in Q32.32 for x in [-16, 21] (numeric/fixed_exp.rs:40-131): k = round(x / ln 2),
-// r = x - k ln 2, the degree-7 Taylor sum of exp(r) by Horner with round_div_2p32, then 2^k.
-// The reference sums in i128; here in i64, exactly: |r| <= ln 2 / 2 * 2^32 < 2^30.5 and every
-// partial sum lies in (0, e^(ln 2 / 2) * 2^32) < 2^32.6, so each product acc * r stays below
-// 2^63 (the bounds are checked step by step against the oracle in the CPU tests).
-AH_DEV int fx_exp(int64_t x, int64_t &out) {
-    if (x < -16 * kOneQ32 || x > 21 * kOneQ32) return AH_ERR_EXP_RANGE;
-    const int64_t k = (int64_t)(((i128)x * 6196328019LL + ((i128)1 << 63)) >> 64);
-    const int64_t r = x - k * 2977044472LL;
-    int64_t acc = 852176;
-    acc = round_div_2p32_i64(acc * r) + 5965232;
-    acc = round_div_2p32_i64(acc * r) + 35791394;
-    acc = round_div_2p32_i64(acc * r) + 178956971;
-    acc = round_div_2p32_i64(acc * r) + 715827883;
-    acc = round_div_2p32_i64(acc * r) + 2147483648LL;
-    acc = round_div_2p32_i64(acc * r) + 4294967296LL;
-    acc = round_div_2p32_i64(acc * r) + 4294967296LL;
-    if (k >= 0) {
-        // acc * 2^k must be an i64 (the reference's range check on the i128 value)
-        if (k >= 63 || acc > (INT64_MAX >> k) || acc < (INT64_MIN >> k)) return AH_ERR_EXP_RANGE;
-        out = acc << k;
-        return 0;
-    }
-    const int64_t n = -k;
-    if (n >= 63) {
-        out = 0;
-        return 0;
-    }
-    out = (acc + ((int64_t)1 << (n - 1))) >> n;
-    return 0;
-}
-// silu(v) = round(|v| * 2^32 / (2^32 + exp(-v))) with v's sign on -21 < v < 16, v above, 0 below
-// (engine/ops/silu.rs:18-60).  The quotient is below 2^37: a double estimate of the i128 division,
-// then exact correction against the remainder (the hardware has no i128 divide).
-AH_DEV int silu_fx(int64_t v, int64_t &out) {
-    if (v >= 16 * kOneQ32) {
-        out = v;
-        return 0;
-    }
-    if (v <= -21 * kOneQ32) {
-        out = 0;
-        return 0;
-    }
-    int64_t e;
-    if (fx_exp(-v, e)) return AH_ERR_EXP_RANGE;
-    if (e > INT64_MAX - kOneQ32) return AH_ERR_FFN_OVERFLOW;
-    const int64_t den = kOneQ32 + e;
-    if (den <= 0) return AH_ERR_ZERO_DENOMINATOR;
-    const uint64_t mag = v < 0 ? 0ull - (uint64_t)v : (uint64_t)v;
-    const i128 n2 = (i128)mag * kOneQ32 + (den >> 1);  // div_round_nearest's num + den / 2
-    const double nd = (double)(uint64_t)(n2 >> 32) * 4294967296.0 + (double)(uint64_t)(n2 & 0xFFFFFFFFu);
-    int64_t q = (int64_t)(nd / (double)den);
-    i128 rem = n2 - (i128)q * den;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (rem < 0) {
-            --q;
-            rem += den;
-        } else if (rem >= den) {
-            ++q;
-            rem -= den;
-        }
-    }
-    out = v < 0 ? -q : q;
-    return 0;
-}
-// h = round_shift_32(silu(gate) * up) (engine/chart/ffn.rs:246-252)
-AH_DEV int swiglu_fx(int64_t g, int64_t u, int64_t &h) {
-    int64_t s;
-    const int st = silu_fx(g, s);
-    if (st) return st;
-    const i128 r = ((i128)s * u + ((i128)1 << 31)) >> 32;
-    if (r > (i128)INT64_MAX || r < (i128)INT64_MIN) return AH_ERR_FFN_OVERFLOW;
-    h = (int64_t)r;
-    return 0;
-}
 
 constexpr uint32_t kSThreads = 512;                // threads of a streaming workgroup
 constexpr uint32_t kSWaves = kSThreads / 64;
@@ -1233,17 +1146,6 @@ constexpr int stream_waves_per_simd() { return TYPE == kMixedType ? 2 : 4; }
 constexpr uint32_t kFfnRows = 32 * kFfnMaxBlocks;
 constexpr uint32_t kFfnLdsBytes = 2 * kFfnRows * 4;
 
-// Largest value over each aligned group of 32 lanes (every lane of the group gets it): DPP within
-// a row of 16 (quad exchanges, then the half-row and row mirrors), then one exchange of rows.
-template <int CTRL>
-AH_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
-AH_DEV int max32(int v) {
-    v = __builtin_elementwise_max(v, dpp_i<0xB1>(v));   // lane ^ 1
-    v = __builtin_elementwise_max(v, dpp_i<0x4E>(v));   // lane ^ 2
-    v = __builtin_elementwise_max(v, dpp_i<0x141>(v));  // row_half_mirror
-    v = __builtin_elementwise_max(v, dpp_i<0x140>(v));  // row_mirror
-    return __builtin_elementwise_max(v, __shfl_xor(v, 16, 64));
-}
 
 // The fused FFN's epilogue over the workgroup's hidden blocks [b0, b1): one thread per element,
 // 32 lanes per block.  Each converts its gate and up row sums to Q32.32 (to_q32) and forms
@@ -1262,35 +1164,48 @@ AH_DEV void ffn_epilogue(const FfnArgs &fa, uint32_t b0, uint32_t b1, const floa
     const uint32_t b = b0 + j, k = 32 * b + l;  // b1 - b0 <= kSThreads / 32
     if (b0 + j >= b1) return;                    // whole half-waves: uniform per 32-lane group
     const bool live = k < n;
-    int64_t h = 0;
-    if (live) {
-        const uint32_t gb = __builtin_bit_cast(uint32_t, hsum[k - 32 * b0]);
-        const uint32_t ub = __builtin_bit_cast(uint32_t, hsum[kFfnRows + k - 32 * b0]);
-        uint64_t mg, mu;
-        bool ng, nu;
-        int e = ah_to_q32_mag(gb, mg, ng);
-        if (!e) e = ah_to_q32_mag(ub, mu, nu);
-        if (!e) e = swiglu_fx(ng ? (int64_t)(0ull - mg) : (int64_t)mg, nu ? (int64_t)(0ull - mu) : (int64_t)mu, h);
-        if (e) {
-            ah_record(status, ah_out_key(2ull * n + k, (uint32_t)e));
-            h = 0;
-        }
-    }
+    const uint32_t gb = live ? __builtin_bit_cast(uint32_t, hsum[k - 32 * b0]) : 0u;
+    const uint32_t ub = live ? __builtin_bit_cast(uint32_t, hsum[kFfnRows + k - 32 * b0]) : 0u;
     // quant_act of the block (chart/mod.rs:258-334): S = act_scale(max |h|), codes q + [2r >= S]
-    const bool neg = h < 0;
-    const uint64_t mag = neg ? 0ull - (uint64_t)h : (uint64_t)h;
-    const int e = max32(mag ? ah_act_scale_exp(mag) : -1);
-    bool bad = e == 63;  // act_scale's None
-    const int c = e >= 0 && e < 63 ? ah_act_code(mag, neg, e, bad) : 0;
-    const uint64_t group = 0xFFFFFFFFull << (tid & 32);
-    const bool bad_block = (__builtin_amdgcn_ballot_w64(bad) & group) != 0ull;
+    const HiddenQ q = swiglu_quant32(gb, ub, live);
+    if (q.err) ah_record(status, ah_out_key(2ull * n + k, (uint32_t)q.err));
     const __amdgpu_buffer_rsrc_t rc = ah_rsrc(fa.h_codes, n), rs = ah_rsrc(fa.h_scales, nb * 8u);
-    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(bad_block ? 0 : c), rc, live ? k : kActOob, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)q.code, rc, live ? k : kActOob, 0, 0);
     if (l == 0) {
-        if (bad_block) ah_record(status, ah_out_key(3ull * n + b, 7u));
-        const uint64_t S64 = bad_block || e < 0 ? 0ull : (1ull << e);
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, (u32x2){(uint32_t)S64, (uint32_t)(S64 >> 32)}),
+        if (q.bad_block) ah_record(status, ah_out_key(3ull * n + b, 7u));
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, (u32x2){(uint32_t)q.scale, (uint32_t)(q.scale >> 32)}),
                                               rs, 8 * b, 0, 0);
+    }
+}
+
+// The unfused prefill FFN's SwiGLU pass: the gate and up projections' f32 outputs [n_tok][n_ff]
+// into the hidden QuantAct, codes [n_tok][n_ff] and scales [n_tok][ceil(n_ff / 32)], as
+// swiglu_cols then quant_cols do per column (chart/ffn.rs:493-560, chart/mod.rs:258-334).  One
+// 32-lane half-wave per (token, hidden block), the wave's two blocks consecutive; refusals keyed
+// past the projections': an element's conversion or SwiGLU at key_sw + t * n_ff + k, a block's
+// quantizer at key_q + t * ceil(n_ff / 32) + b.
+__global__ void __launch_bounds__(kThreads) swiglu_quant_kernel(SwigluArgs a) {
+    const uint32_t nbh = (a.n_ff + 31) / 32;
+    const uint64_t total = (uint64_t)a.n_tok * nbh;
+    const uint32_t lane = threadIdx.x & 63u, l = lane & 31u, half = lane >> 5;
+    const uint64_t wave = ((uint64_t)blockIdx.x * kThreads + threadIdx.x) / 64;
+    const uint64_t waves = (uint64_t)gridDim.x * (kThreads / 64);
+    for (uint64_t p = wave; 2 * p < total; p += waves) {  // the same trip count for the whole wave
+        const uint64_t blk = 2 * p + half;
+        const bool vb = blk < total;
+        const uint32_t t = vb ? (uint32_t)(blk / nbh) : 0u, b = vb ? (uint32_t)(blk % nbh) : 0u;
+        const uint32_t k = 32u * b + l;
+        const bool live = vb && k < a.n_ff;
+        const size_t e = (size_t)t * a.n_ff + k;
+        const uint32_t gb = live ? __builtin_bit_cast(uint32_t, a.gate[e]) : 0u;
+        const uint32_t ub = live ? __builtin_bit_cast(uint32_t, a.up[e]) : 0u;
+        const HiddenQ q = swiglu_quant32(gb, ub, live);
+        if (q.err) ah_record(a.status, ah_out_key(a.key_sw + e, (uint32_t)q.err));
+        if (live) a.h_codes[e] = (int8_t)q.code;
+        if (vb && l == 0) {
+            if (q.bad_block) ah_record(a.status, ah_out_key(a.key_q + blk, 7u));
+            a.h_scales[blk] = (int64_t)q.scale;
+        }
     }
 }
 
@@ -2138,6 +2053,15 @@ hipError_t ah_launch_quant(const QuantArgs &q, hipStream_t stream) {
     size_t grid = (total + kThreads / 4 - 1) / (kThreads / 4);
     if (grid > 8192) grid = 8192;
     hipLaunchKernelGGL(quant_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, stream, q);
+    return hipGetLastError();
+}
+
+hipError_t ah_launch_swiglu_quant(const SwigluArgs &a, hipStream_t stream) {
+    const uint64_t total = (uint64_t)a.n_tok * ((a.n_ff + 31) / 32);
+    if (total == 0) return hipSuccess;
+    uint64_t grid = (total + 7) / 8;  // 8 blocks per 256-thread workgroup
+    if (grid > 8192) grid = 8192;
+    hipLaunchKernelGGL(swiglu_quant_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -223,7 +223,9 @@ struct FfnArgs {
 // GEMM workgroup forms (waves x LDS ring slots), chosen per launch by ah_gemm_pick_waves.
 // kFormI8x4 / kFormI8x2: the int8-MFMA design (Q8_0), 4 or 2 waves.
 // kFormTile: the dequantize-once design (gemm_dq_kernel: 128 rows x 128 tokens, 4 waves).
-enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2, kFormI8x4 = 3, kFormI8x2 = 4, kFormTile = 5 };
+// kFormTileFfn: the same tiles over a gate/up pair with the SwiGLU + hidden quantizer epilogue.
+enum : uint32_t { kForm4x4 = 0, kForm2x2 = 1, kForm2x4 = 2, kFormI8x4 = 3, kFormI8x2 = 4, kFormTile = 5,
+                  kFormTileFfn = 6 };
 // The GEMM design of a part: register-blocked f16 (gemm_rb_kernel), int8 (gemm_i8_kernel),
 // dequantize-once f16 tiles (gemm_dq_kernel).  Picks its geometry and split model.
 enum : uint32_t { kGemmKindRb = 0, kGemmKindI8 = 1, kGemmKindTile = 2 };
@@ -240,6 +242,28 @@ struct GemmPartDesc {
     uint32_t w_bytes, row_bytes, n_out, splits;
     float *y;         // [n_tok][n_out]
     float *partials;  // with splits > 1
+    uint64_t key0;    // added to the part's output refusal keys (t * n_out + row): orders the
+                      // refusals of parts that one launch serves (the prefill FFN's gate before up)
+};
+
+// The prefill FFN's fused gate/up launch (kFormTileFfn): part 0 is the gate projection, `w_up`
+// the up projection of the same type and shape; hidden block rows pair up in the tiles, and the
+// epilogue writes the hidden QuantAct instead of the projections' outputs (those optionally).
+struct GemmFfn {
+    const uint8_t *w_up;
+    float *gy, *uy;     // [n_tok][n_ff] f32 gate / up values the SwiGLU consumed, or nullptr
+    int8_t *h_codes;    // [n_tok][n_ff]
+    int64_t *h_scales;  // [n_tok][ceil(n_ff / 32)]
+};
+
+// The unfused prefill FFN's SwiGLU pass over the gate and up projections' f32 outputs.
+struct SwigluArgs {
+    const float *gate, *up;  // [n_tok][n_ff]
+    int8_t *h_codes;         // [n_tok][n_ff]
+    int64_t *h_scales;       // [n_tok][ceil(n_ff / 32)]
+    uint32_t n_tok, n_ff;
+    uint64_t key_sw, key_q;  // refusal key bases: element conversion / SwiGLU, block quantizer
+    unsigned long long *status;
 };
 
 // The streaming kernel instantiation whose plan mixes GGUF types (each wave dispatches on its

@@ -167,6 +167,43 @@ int32_t ah_ffn_gate_up_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *
 int32_t ah_ffn_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
                    const float *d_x, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales, void *stream);
 
+/* Prefill FFN, N = n_tok > 1 (the step's column path, step/cols.rs:1026-1067: quant_cols, the
+ * [W_gate; W_up] GEMM with the SwiGLU epilogue, gemm_q8_0_swiglu_carrier, kern/gemm.rs:955-1168,
+ * or gate/up proj_cols + swiglu_cols, chart/ffn.rs:493-560; then the down proj_cols).  For every
+ * token t and hidden index i: h[t][i] = round_shift_32(silu_fixed(to_q32(gate[t][i])) *
+ * to_q32(up[t][i])) exactly, from the f32 gate / up values of the GEMM (within the GEMM's
+ * tolerance of the exact projections), and the hidden QuantAct: d_h_codes[n_tok][n_ff] (int8)
+ * and d_h_scales[n_tok][ceil(n_ff/32)] (int64, 8-byte aligned), quant_act of each token's row.
+ * ah_ffn_gate_up_prefill_dev takes f32 input d_x[n_tok][n_embd]; d_gate_y / d_up_y (optional,
+ * [n_tok][n_ff], NULL to skip) receive the f32 gate and up values the SwiGLU consumed.  Q4_K,
+ * Q2_K and Q3_K run as ONE launch (after the input's operand pass): the dequantize-once tiles
+ * hold gate and up rows of the same 64 hidden indices, and the epilogue writes the hidden
+ * QuantAct (no gate / up matrix in memory); other types, or after ah_set_ffn_prefill_fusion(ctx,
+ * 0), run the grouped gate/up GEMM, then a SwiGLU pass (ah_swiglu_quant_dev's kernel).
+ * ah_ffn_prefill_dev adds the down projection (n_embd x n_ff, any type) from the hidden QuantAct
+ * (d_h_codes 4-byte aligned) into d_y[n_tok][n_embd].  Refusals (ah_sync_status) in the
+ * reference FFN's order: the input's quantization, the gate projection's outputs (token-major),
+ * then the up projection's, the elements' conversion or SwiGLU (AH_ERR_FFN_OVERFLOW,
+ * AH_ERR_EXP_RANGE, AH_ERR_ZERO_DENOMINATOR; token-major), the hidden quantizer's, and only when
+ * none of those occurred, the down projection's.  Uses the context's GEMM scratch (as
+ * ah_gemm_f32_dev) and, for the two-pass form without d_gate_y / d_up_y, a context buffer of
+ * 8 * n_tok * n_ff bytes (grown on demand). */
+int32_t ah_ffn_gate_up_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const float *d_x,
+                                   size_t n_tok, float *d_gate_y, float *d_up_y, int8_t *d_h_codes,
+                                   int64_t *d_h_scales, void *stream);
+int32_t ah_ffn_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                           const float *d_x, size_t n_tok, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales,
+                           void *stream);
+/* 1 (the default): Q4_K / Q2_K / Q3_K prefill FFNs take the one-launch fused form; 0: the
+ * two-pass form for every type (for comparison; results are bit-identical given the same gate /
+ * up values, which agree within the GEMM tolerance). */
+int32_t ah_set_ffn_prefill_fusion(ah_ctx *ctx, uint32_t fused);
+/* swiglu_cols + quant_cols (chart/ffn.rs:493-560, chart/mod.rs:258-334) over f32 gate / up
+ * values [n_tok][n_ff] (4-byte aligned): the hidden QuantAct as above.  Refusals token-major: an
+ * element's conversion or SwiGLU, then the quantizer's blocks. */
+int32_t ah_swiglu_quant_dev(ah_ctx *ctx, const float *d_gate, const float *d_up, size_t n_tok, size_t n_ff,
+                            int8_t *d_h_codes, int64_t *d_h_scales, void *stream);
+
 /* Persistent decode sequence: a token's chain of projection stages in ONE launch.  Stage s may
  * read outputs of stages before it (q/k/v -> o -> gate/up -> SwiGLU -> down per layer, then the
  * head): every workgroup of a resident grid finishes its share of stage s, then all meet at a

@@ -29,7 +29,7 @@ EXPORTS = [
     "ah_quant_act", "ah_probe_mfma_peak", "ah_gemm_group_f32_dev", "ah_gemm_group_q8_dev",
     "ah_last_refusal_bits", "ah_gemm_f32_noalloc_dev", "ah_gemm_noalloc_scratch_bytes",
     "ah_set_gemm_design", "ah_ffn_gate_up_dev", "ah_ffn_dev", "ah_ffn_gate_up_prefill_dev",
-    "ah_ffn_prefill_dev", "ah_set_ffn_prefill_fusion", "ah_swiglu_quant_dev",
+    "ah_ffn_prefill_dev", "ah_set_ffn_prefill_form", "ah_swiglu_quant_dev",
     "ah_seq_create", "ah_seq_run", "ah_seq_sync_status", "ah_seq_free", "ah_seq_info",
 ]
 
@@ -83,7 +83,7 @@ def load() -> ctypes.CDLL:
         "ah_ffn_dev": (I32, [P, P, P, P, P, P, P, P, P]),
         "ah_ffn_gate_up_prefill_dev": (I32, [P, P, P, P, S, P, P, P, P, P]),
         "ah_ffn_prefill_dev": (I32, [P, P, P, P, P, S, P, P, P, P]),
-        "ah_set_ffn_prefill_fusion": (I32, [P, U32]),
+        "ah_set_ffn_prefill_form": (I32, [P, U32]),
         "ah_swiglu_quant_dev": (I32, [P, P, P, S, S, P, P, P]),
         "ah_gemm_f32_noalloc_dev": (I32, [P, P, P, S, P, P]),
         "ah_gemm_noalloc_scratch_bytes": (I32, [ctypes.POINTER(S)]),

@@ -103,10 +103,12 @@ class Device:
         prefill as one streaming GEMV per token."""
         _check(self.lib.ah_set_gemm_design(self.h, ggml_type, design), "set_gemm_design")
 
-    def set_ffn_prefill_fusion(self, fused: bool) -> None:
-        """Fused (the default: one launch for Q4_K / Q2_K / Q3_K) or two-pass prefill FFN
-        (ah_set_ffn_prefill_fusion)."""
-        _check(self.lib.ah_set_ffn_prefill_fusion(self.h, 1 if fused else 0), "set_ffn_prefill_fusion")
+    FFN_AUTO, FFN_FUSED, FFN_TWO_PASS = 0, 1, 2
+
+    def set_ffn_prefill_form(self, form: int) -> None:
+        """The prefill FFN's form (ah_set_ffn_prefill_form): AUTO (two passes), FUSED (one launch
+        for Q4_K / Q2_K / Q3_K gate/up) or TWO_PASS."""
+        _check(self.lib.ah_set_ffn_prefill_form(self.h, form), "set_ffn_prefill_form")
 
     def probe_mfma_peak(self, kind: int) -> float:
         """Measured MFMA-only rate in tera-ops/s (kind 0: int8 32x32x32, 1: f16 32x32x16)."""

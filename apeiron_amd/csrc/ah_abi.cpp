@@ -81,7 +81,7 @@ struct ah_ctx {
     // the unfused prefill FFN's gate / up outputs when the caller keeps none (grown on demand)
     void *ffn_buf = nullptr;
     size_t ffn_buf_bytes = 0;
-    bool ffn_unfused = false;  // ah_set_ffn_prefill_fusion(ctx, 0): the two-pass prefill FFN
+    uint32_t ffn_form = AH_FFN_PREFILL_AUTO;  // ah_set_ffn_prefill_form
     size_t scratch_bytes = 0;
     // streaming-GEMV occupancy by (type, LDS bytes): a runtime query per launch costs more host
     // time than a small GEMV takes on the device
@@ -1105,9 +1105,9 @@ int32_t ah_swiglu_quant_dev(ah_ctx *ctx, const float *d_gate, const float *d_up,
     return AH_OK;
 }
 
-int32_t ah_set_ffn_prefill_fusion(ah_ctx *ctx, uint32_t fused) {
-    if (!ctx || fused > 1) return AH_ERR_INVALID_ARG;
-    ctx->ffn_unfused = fused == 0;
+int32_t ah_set_ffn_prefill_form(ah_ctx *ctx, uint32_t form) {
+    if (!ctx || form > AH_FFN_PREFILL_TWO_PASS) return AH_ERR_INVALID_ARG;
+    ctx->ffn_form = form;
     return AH_OK;
 }
 
@@ -1126,7 +1126,9 @@ int32_t ah_ffn_gate_up_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_
     if (n_tok >= (1ull << 24) || (uint64_t)n_tok * n_ff >= (1ull << 45)) return AH_ERR_INVALID_ARG;
     const ah_tensor *w2[2] = {gate, up};
     const uint32_t t = gate->type;
-    if (!ctx->ffn_unfused && (t == AH_GGML_Q4_K || t == AH_GGML_Q2_K || t == AH_GGML_Q3_K)) {
+    // AUTO takes the two passes: on MI355X at the configs[4] FFN (N = 512) they measured 110-139 us
+    // against 175-197 us for the fused launch, whose SwiGLU epilogue runs at two waves per SIMD
+    if (ctx->ffn_form == AH_FFN_PREFILL_FUSED && (t == AH_GGML_Q4_K || t == AH_GGML_Q2_K || t == AH_GGML_Q3_K)) {
         // one launch: gate and up rows of the same hidden indices in each tile, the SwiGLU and the
         // hidden quantizer in its epilogue
         GemmFfn f = {up->d, d_gate_y, d_up_y, d_h_codes, d_h_scales};

@@ -116,6 +116,20 @@ def q4_k_payload(rng: np.random.Generator, rows: int, n_in: int, sigma: float = 
     return blk.reshape(-1)
 
 
+def q4_k_centered_payload(rng: np.random.Generator, rows: int, n_in: int, sigma: float = 0.01) -> np.ndarray:
+    """Q4_K super-blocks whose weights average about zero (dmin = d, m = round(7.5 sc), sc in
+    1..8): rows without the common positive bias of q4_k_payload, whose projections of a token
+    then share its sign and make SwiGLU hidden vectors with far smaller blocks than their
+    largest (tokens the GEMM's f16 band cannot carry)."""
+    raw = q4_k_payload(rng, rows, n_in, sigma)
+    blk = raw.reshape(-1, 144)
+    n = blk.shape[0]
+    sc = rng.integers(1, 9, size=(n, 8))
+    blk[:, 2:4] = blk[:, 0:2]
+    blk[:, 4:16] = pack_q4_k_scales(sc, np.minimum(63, np.round(sc * 7.5)).astype(np.int64))
+    return raw
+
+
 def pack_q6_k_codes(u: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """Inverse of q6_k_codes (format/quant.rs:574-599): (n, 256) values 0..63 -> ql (n,128), qh (n,64)."""
     u = u.astype(np.uint8).reshape(-1, 2, 4, 32)  # [n][half][t][l]

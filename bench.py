@@ -25,19 +25,25 @@ Also reported, beside the value:
                 stream around replays of one graph of those launches in token order;
   decode        the same token as eager launches; with the fused FFN in launch form (gate/up with
                 the exact SwiGLU + hidden requantize in one launch, down from the hidden codes:
-                the FFN's real data dependency); as one persistent launch (ah_seq_*, with and
-                without the fused FFN's SwiGLU stage); and with its 197 projections batched as
-                independent parts (two launches: not a dependency-respecting token);
+                the FFN's real data dependency) and, its baseline, with the plain gate/up launch
+                then the SwiGLU as a launch of its own; as one persistent launch (ah_seq_*, with and
+                without the fused FFN's SwiGLU stage); with its 197 projections batched as
+                independent parts (two launches: not a dependency-respecting token); and the
+                launch floor: a graph of 113 minimal launches on one stream;
   config1       BASELINE configs[1] (Qwen2.5-0.5B, 24 layers, Q4_K) as one batched launch;
   gemm          configs[3] N = 512 GEMMs against the 5.0 POPS int8 MFMA peak (Q8_0 on both MFMA
-                designs, int8 and f16), the MFMA-only probe, and the configs[4] N = 512 prefill
-                (--only gemm3: the configs[3] GEMMs alone, for profiling);
+                designs, int8 and f16; Q4_K on the f16 and the dequantize-once tile designs), each
+                from pre-quantized codes and from the f32 input, the MFMA-only probe, the configs[4]
+                N = 512 prefill, and its FFN fused (gate/up + exact SwiGLU + hidden quant_act in one
+                launch) and two-pass (--only gemm3: the configs[3] GEMMs alone, for profiling);
   heads         configs[0] (Q8_0 4864x896) and configs[2] (151936x896 head, Q6_K and Q8_0);
   families      Q5_0, Q2_K and Q3_K: a 151936x896 launch (bandwidth), a 4864x896 launch
-                (latency) and the N = 512 GEMM at 4864x896;
+                (latency) and the N = 512 GEMM at 4864x896 (Q2_K / Q3_K on the dequantize-once
+                tiles, and on the per-token GEMV route for comparison);
   cpu_baseline  the restated reference fast path (oracle/ah_cpu_fast.c: AVX-VNNI or AVX2 dots,
                 two-row tiles) on the same token's projections, on this host's cores;
-                cpu_baseline_gemm the same for N = 512.
+                cpu_baseline_gemm the same for all 512 columns of the four configs[3] shapes per
+                type, at --cpu-threads and at all host cores.
 """
 from __future__ import annotations
 
@@ -328,6 +334,37 @@ def main() -> int:
             decode["us_per_token_graph_fused_ffn"] = round(event_us(graph_f.replay, reps), 1)
             assert dev.sync_status(sh) == 0
             del graph_f
+            # its like-for-like baseline: the plain gate/up launch, then the SwiGLU + hidden quantizer
+            # as a launch of its own (ah_swiglu_quant_dev), then down from the hidden codes
+            def token_swiglu(s):
+                for li, L in enumerate(W):
+                    plans[4 * li].run(s)
+                    plans[4 * li + 1].run(s)
+                    plans[4 * li + 2].run(s)
+                    chart.swiglu_quant_dev(dev, ptr(Y["gate"]), ptr(Y["up"]), 1, 8960, ptr(hc_g), ptr(hs_g), s)
+                    L["down"][3].gemv_q8_dev(ptr(hc_g), ptr(hs_g), ptr(Y["down"]), s)
+                plans[-1].run(s)
+
+            graph_s = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph_s, stream=cap):
+                token_swiglu(torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            clock_up(graph_s.replay, 0.05)
+            decode["us_per_token_graph_plain_then_swiglu"] = round(event_us(graph_s.replay, reps), 1)
+            assert dev.sync_status(sh) == 0
+            del graph_s
+            # the launch floor of a dependent token: a graph of as many minimal launches (a one-element
+            # fill each) on one stream as the token has stages
+            tiny = torch.zeros(1, dtype=torch.float32, device="cuda")
+            graph_e = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph_e, stream=cap):
+                for _ in range(len(plans)):
+                    tiny.fill_(1.0)
+            torch.cuda.synchronize()
+            clock_up(graph_e.replay, 0.05)
+            decode["floor_us_per_token"] = round(event_us(graph_e.replay, reps), 1)
+            decode["floor_launches"] = len(plans)
+            del graph_e
             # one persistent launch per token (ah_seq_*): the same stages; and with the fused FFN's
             # SwiGLU stage between gate/up and down (down then reads the hidden QuantAct)
             hc = torch.zeros(8960, dtype=torch.int8, device="cuda")
@@ -423,8 +460,9 @@ def main() -> int:
         n_tok = 512
         # Q8_0 on both MFMA designs (int8, the default, and f16); the K-quants have the f16 design
         for gt, design in ((synth.Q8_0, chart.Device.GEMM_INT8), (synth.Q8_0, chart.Device.GEMM_F16),
-                           (synth.Q4_K, chart.Device.GEMM_F16)):
-            dname = "int8" if design == chart.Device.GEMM_INT8 else "f16"
+                           (synth.Q4_K, chart.Device.GEMM_F16), (synth.Q4_K, chart.Device.GEMM_F16_TILE)):
+            dname = {chart.Device.GEMM_INT8: "int8", chart.Device.GEMM_F16: "f16",
+                     chart.Device.GEMM_F16_TILE: "f16 tiles"}[design]
             dev.set_gemm_design(gt, design)
             for n_out, n_in in GEMM_SHAPES:
                 rng3 = synth.rng_for(3, gt * 10 + n_in)
@@ -438,20 +476,76 @@ def main() -> int:
                 clock_up(run, 0.03)
                 assert dev.sync_status(sh) == 0
                 us = event_us(run, 50)
+                # the same GEMM from the f32 input (the quantizer pass inside the timing, as configs[3]
+                # specifies it)
+                run_f = lambda: w.gemm_f32_dev(ptr(x), n_tok, ptr(y), sh)
+                clock_up(run_f, 0.02)
+                assert dev.sync_status(sh) == 0
+                us_f = event_us(run_f, 50)
                 ops = 2.0 * n_tok * n_out * n_in
                 tops = ops / us / 1e6
                 traffic = n_out * synth.needed_row_bytes(gt, n_in) + 4.0 * n_tok * n_out + n_tok * n_in
                 attain = min(INT8_PEAK_TOPS, ops / traffic * HBM_PEAK_GBS / 1e3)
                 gemm.append({"type": synth.NAMES[gt], "design": dname, "shape": [n_out, n_in], "n_tok": n_tok,
                              "us": round(us, 2), "tops": round(tops, 1),
+                             "us_f32_input": round(us_f, 2), "tops_f32_input": round(ops / us_f / 1e6, 1),
                              "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                              "frac_f16_probe": round(tops / probe["f16_tflops"], 4),
                              "attainable_tops": round(attain, 1), "frac_attainable": round(tops / attain, 4)})
                 log(f"[bench] gemm {synth.NAMES[gt]} ({dname} MFMA) {n_out}x{n_in} N{n_tok}: {us:.1f} us "
-                    f"{tops:.0f} TOPS ({100 * tops / INT8_PEAK_TOPS:.1f}% int8 peak)")
+                    f"{tops:.0f} TOPS ({100 * tops / INT8_PEAK_TOPS:.1f}% int8 peak); from f32 {us_f:.1f} us")
                 w.free()
             dev.set_gemm_design(gt, chart.Device.GEMM_AUTO)
         result["gemm"] = gemm
+
+        # configs[4] prefill FFN at N = 512 (gate/up Q4_K 8960x1536, down Q6_K 1536x8960): the fused
+        # gate/up launch (SwiGLU + hidden quant_act in the tiles' epilogue) against the two-pass
+        # form (grouped gate/up GEMM, then the SwiGLU pass), alone and with the down projection
+        # (gate/up rows centred on zero, as trained FFN weights are: q4_k_payload's common positive
+        # row bias makes ~1 token in 16 a hidden vector the f16 band cannot carry, which the down
+        # GEMM then serves on its exact path -- measured below as down_exact_path)
+        rngf = synth.rng_for(4, 77)
+        Gf = dev.upload(synth.Q4_K, synth.q4_k_centered_payload(rngf, 8960, 1536), 8960, 1536)
+        Uf = dev.upload(synth.Q4_K, synth.q4_k_centered_payload(rngf, 8960, 1536), 8960, 1536)
+        Df = dev.upload(synth.Q6_K, synth.payload(synth.Q6_K, rngf, 1536, 8960), 1536, 8960)
+        xf = torch.from_numpy(synth.activations(rngf, 1536, n_tok).reshape(n_tok, 1536).astype(np.float32)).cuda()
+        hcf = torch.empty((n_tok, 8960), dtype=torch.int8, device="cuda")
+        hsf = torch.empty((n_tok, 280), dtype=torch.int64, device="cuda")
+        yf = torch.empty((n_tok, 1536), dtype=torch.float32, device="cuda")
+        ffn = {"n_tok": n_tok, "shapes": {"gate_up": [8960, 1536], "down": [1536, 8960]},
+               "types": {"gate_up": "Q4_K", "down": "Q6_K"}}
+        gu_ops = 2 * 2.0 * n_tok * 8960 * 1536
+        for fused in (True, False):
+            dev.set_ffn_prefill_form(chart.Device.FFN_FUSED if fused else chart.Device.FFN_TWO_PASS)
+            gu = lambda: chart.ffn_gate_up_prefill_dev(dev, Gf, Uf, ptr(xf), n_tok, ptr(hcf), ptr(hsf), None, None, sh)
+            whole = lambda: chart.ffn_prefill_dev(dev, Gf, Uf, Df, ptr(xf), n_tok, ptr(yf), ptr(hcf), ptr(hsf), sh)
+            clock_up(gu, 0.03)
+            assert dev.sync_status(sh) == 0, "ffn prefill refused (synthetic scale)"
+            key = "fused" if fused else "two_pass"
+            us_gu = event_us(gu, 20)
+            clock_up(whole, 0.02)
+            assert dev.sync_status(sh) == 0
+            us_all = event_us(whole, 20)
+            ffn[key] = {"gate_up_us": round(us_gu, 2), "gate_up_tops": round(gu_ops / us_gu / 1e6, 1),
+                        "ffn_us": round(us_all, 2),
+                        "ffn_tops": round((gu_ops + 2.0 * n_tok * 8960 * 1536) / us_all / 1e6, 1)}
+            log(f"[bench] configs[4] prefill FFN N{n_tok} ({key}): gate/up+SwiGLU {us_gu:.1f} us, "
+                f"whole FFN {us_all:.1f} us")
+        dev.set_ffn_prefill_form(chart.Device.FFN_AUTO)
+        # the down GEMM alone from that hidden QuantAct, and from one of biased rows' (some tokens
+        # flagged: the exact path)
+        down = lambda: Df.gemm_q8_dev(ptr(hcf), ptr(hsf), n_tok, ptr(yf), sh)
+        ffn["down_us"] = round(event_us(down, 20), 2)
+        Gb = dev.upload(synth.Q4_K, synth.payload(synth.Q4_K, rngf, 8960, 1536), 8960, 1536)
+        Ub = dev.upload(synth.Q4_K, synth.payload(synth.Q4_K, rngf, 8960, 1536), 8960, 1536)
+        chart.ffn_gate_up_prefill_dev(dev, Gb, Ub, ptr(xf), n_tok, ptr(hcf), ptr(hsf), None, None, sh)
+        assert dev.sync_status(sh) == 0
+        ffn["down_exact_path_us"] = round(event_us(down, 3), 1)
+        log(f"[bench] configs[4] prefill FFN down alone {ffn['down_us']} us; with flagged hidden tokens "
+            f"{ffn['down_exact_path_us']} us")
+        result["ffn_prefill"] = ffn
+        for w_ in (Gf, Uf, Df, Gb, Ub):
+            w_.free()
 
     # ---- the 168 projections of a Qwen2.5-0.5B token batched in one launch ------------
     if args.only in (None, "config1") and not args.no_extras:
@@ -561,12 +655,22 @@ def main() -> int:
             run = lambda: w.gemm_f32_dev(ptr(x), n_tok, ptr(y), sh)
             clock_up(run, 0.03)
             assert dev.sync_status(sh) == 0
-            us = event_us(run, 10)
+            us = event_us(run, 20)
             tops = 2.0 * n_tok * n_out * n_in / us / 1e6
             row["gemm"] = {"shape": [n_out, n_in], "n_tok": n_tok, "us": round(us, 2), "tops": round(tops, 1),
                            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                           "form": "f16 MFMA" if gt == synth.Q5_0 else "one GEMV launch per token"}
+                           "form": "f16 MFMA" if gt == synth.Q5_0 else "f16 MFMA, dequantize-once tiles"}
             log(f"[bench] gemm {synth.NAMES[gt]} {n_out}x{n_in} N{n_tok}: {us:.1f} us {tops:.0f} TOPS")
+            if gt != synth.Q5_0:
+                # the per-token GEMV route (AH_GEMM_DESIGN_F16 for these families): one streaming GEMV
+                # per few tokens, as the reference serves them column by column
+                dev.set_gemm_design(gt, chart.Device.GEMM_F16)
+                run(); torch.cuda.synchronize()
+                us_g = event_us(run, 3)
+                assert dev.sync_status(sh) == 0
+                dev.set_gemm_design(gt, chart.Device.GEMM_AUTO)
+                row["gemm"]["gemv_route_us"] = round(us_g, 1)
+                log(f"[bench] gemm {synth.NAMES[gt]} per-token GEMV route: {us_g:.1f} us")
             w.free()
             fam.append(row)
         result["families"] = fam
@@ -621,26 +725,27 @@ def main() -> int:
         import oracle
 
         cg = []
+        k = 512  # every token column of the configs[3] GEMMs
+        thread_set = sorted({max(1, min(args.cpu_threads, os.cpu_count() or 1)), os.cpu_count() or 1})
         for gt in (synth.Q8_0, synth.Q4_K):
-            for n_out, n_in in ((4864, 896), (8960, 1536)):
+            for n_out, n_in in GEMM_SHAPES:
                 raw = synth.payload(gt, synth.rng_for(3, gt * 10 + n_in), n_out, n_in)
-                k = 32  # a bounded sample of the N = 512 token columns
                 x = synth.activations(synth.rng_for(3, 5), n_in, k).reshape(k, n_in)
                 st, codes, scales = oracle.quant_act_f32_batch(x)
-                threads = max(1, min(args.cpu_threads, os.cpu_count() or 1))
-                oracle.matmat_q8act_fast(gt, raw, n_out, n_in, codes[:2], scales[:2], threads)  # warm-up
-                reps = []
-                for _ in range(5):  # median of 5 timed calls
-                    t0 = time.perf_counter()
-                    oracle.matmat_q8act_fast(gt, raw, n_out, n_in, codes, scales, threads)
-                    reps.append(time.perf_counter() - t0)
-                el = sorted(reps)[2]
-                gops = 2.0 * k * n_out * n_in / el / 1e9
-                cg.append({"type": synth.NAMES[gt], "shape": [n_out, n_in], "columns": k, "threads": threads,
-                           "seconds": round(el, 3), "gops": round(gops, 1),
-                           "route": "per-column matvec (K % 256 != 0)" if gt == synth.Q4_K and n_in % 256
-                                    else "k-column",
-                           "cores_form": ("portable", "avx2", "avx_vnni")[oracle.cpu_path()]})
+                for threads in thread_set:
+                    oracle.matmat_q8act_fast(gt, raw, n_out, n_in, codes[:2], scales[:2], threads)  # warm-up
+                    reps = []
+                    for _ in range(3):  # median of 3 timed calls
+                        t0 = time.perf_counter()
+                        oracle.matmat_q8act_fast(gt, raw, n_out, n_in, codes, scales, threads)
+                        reps.append(time.perf_counter() - t0)
+                    el = sorted(reps)[1]
+                    gops = 2.0 * k * n_out * n_in / el / 1e9
+                    cg.append({"type": synth.NAMES[gt], "shape": [n_out, n_in], "columns": k, "threads": threads,
+                               "seconds": round(el, 4), "gops": round(gops, 1),
+                               "route": "per-column matvec (K % 256 != 0)" if gt == synth.Q4_K and n_in % 256
+                                        else "k-column",
+                               "cores_form": ("portable", "avx2", "avx_vnni")[oracle.cpu_path()]})
         result["cpu_baseline_gemm"] = cg
         log(f"[bench] cpu gemm baseline: {[c['gops'] for c in cg]} GOPS")
 
@@ -675,6 +780,7 @@ def main() -> int:
         "config1": result.get("config1"),
         "config0_config2": result.get("heads"),
         "families": result.get("families"),
+        "ffn_prefill": result.get("ffn_prefill"),
         "cpu_baseline_gemm": result.get("cpu_baseline_gemm"),
     }
     print(json.dumps(line))

@@ -178,8 +178,9 @@ int32_t ah_ffn_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, cons
  * [n_tok][n_ff], NULL to skip) receive the f32 gate and up values the SwiGLU consumed.  Q4_K,
  * Q2_K and Q3_K run as ONE launch (after the input's operand pass): the dequantize-once tiles
  * hold gate and up rows of the same 64 hidden indices, and the epilogue writes the hidden
- * QuantAct (no gate / up matrix in memory); other types, or after ah_set_ffn_prefill_fusion(ctx,
- * 0), run the grouped gate/up GEMM, then a SwiGLU pass (ah_swiglu_quant_dev's kernel).
+ * QuantAct (no gate / up matrix in memory) -- the form ah_set_ffn_prefill_form selects with
+ * AH_FFN_PREFILL_FUSED; the default (AUTO, and every other type) runs the grouped gate/up GEMM,
+ * then a SwiGLU pass (ah_swiglu_quant_dev's kernel), which measured faster on MI355X.
  * ah_ffn_prefill_dev adds the down projection (n_embd x n_ff, any type) from the hidden QuantAct
  * (d_h_codes 4-byte aligned) into d_y[n_tok][n_embd].  Refusals (ah_sync_status) in the
  * reference FFN's order: the input's quantization, the gate projection's outputs (token-major),
@@ -194,10 +195,13 @@ int32_t ah_ffn_gate_up_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_
 int32_t ah_ffn_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
                            const float *d_x, size_t n_tok, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales,
                            void *stream);
-/* 1 (the default): Q4_K / Q2_K / Q3_K prefill FFNs take the one-launch fused form; 0: the
- * two-pass form for every type (for comparison; results are bit-identical given the same gate /
- * up values, which agree within the GEMM tolerance). */
-int32_t ah_set_ffn_prefill_fusion(ah_ctx *ctx, uint32_t fused);
+/* The prefill FFN's form per context: AUTO (the default: two passes), FUSED (one launch for
+ * Q4_K / Q2_K / Q3_K gate/up; other types keep two passes) or TWO_PASS.  The hidden QuantAct is
+ * bit-identical given the same gate / up values; those agree within the GEMM tolerance. */
+#define AH_FFN_PREFILL_AUTO 0u
+#define AH_FFN_PREFILL_FUSED 1u
+#define AH_FFN_PREFILL_TWO_PASS 2u
+int32_t ah_set_ffn_prefill_form(ah_ctx *ctx, uint32_t form);
 /* swiglu_cols + quant_cols (chart/ffn.rs:493-560, chart/mod.rs:258-334) over f32 gate / up
  * values [n_tok][n_ff] (4-byte aligned): the hidden QuantAct as above.  Refusals token-major: an
  * element's conversion or SwiGLU, then the quantizer's blocks. */

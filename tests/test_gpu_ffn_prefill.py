@@ -84,7 +84,7 @@ def run_case(dev, gu_type, down_type, n_embd, n_ff, n_tok, fused, spread=False, 
     gy, uy = nan2d(n_tok, n_ff), nan2d(n_tok, n_ff)
     hc = torch.zeros((n_tok, n_ff), dtype=torch.int8, device="cuda")
     hs = torch.zeros((n_tok, nbh), dtype=torch.int64, device="cuda")
-    dev.set_ffn_prefill_fusion(fused)
+    dev.set_ffn_prefill_form(chart.Device.FFN_FUSED if fused else chart.Device.FFN_TWO_PASS)
     try:
         chart.ffn_gate_up_prefill_dev(dev, G, U, x.data_ptr(), n_tok, hc.data_ptr(), hs.data_ptr(),
                                       gy.data_ptr(), uy.data_ptr(), stream())
@@ -119,7 +119,7 @@ def run_case(dev, gu_type, down_type, n_embd, n_ff, n_tok, fused, spread=False, 
         assert dev.sync_status(stream()) == 0
         assert torch.equal(y, y2)
     finally:
-        dev.set_ffn_prefill_fusion(True)
+        dev.set_ffn_prefill_form(chart.Device.FFN_AUTO)
         for w in (G, U, D):
             w.free()
 
@@ -129,6 +129,7 @@ def run_case(dev, gu_type, down_type, n_embd, n_ff, n_tok, fused, spread=False, 
     (Q4_K, Q4_K, 1536, 8960, 512, False),   # the same shape, two passes
     (Q4_K, Q4_K, 896, 4864, 77, True),      # configs[1] FFN, a partial token tile
     (Q2_K, Q3_K, 512, 1000, 33, True),      # hidden width past whole tiles and a partial block
+    (Q2_K, Q3_K, 512, 1000, 33, False),
     (Q3_K, Q2_K, 256, 300, 130, True),
     (Q8_0, Q8_0, 256, 300, 40, True),       # types without the tile form: two passes
     (Q6_K, Q5_0, 512, 1000, 20, True),
@@ -180,7 +181,7 @@ def test_ffn_prefill_refusal_order(dev, t, fused):
         chart.ffn_gate_up_prefill_dev(dev, G, U, x.data_ptr(), 2, hc.data_ptr(), hs.data_ptr(), None, None, stream())
         return dev.sync_status(stream())
 
-    dev.set_ffn_prefill_fusion(fused)
+    dev.set_ffn_prefill_form(chart.Device.FFN_FUSED if fused else chart.Device.FFN_TWO_PASS)
     try:
         # token 0: gate = up = 2^16, h = 2^32 leaves i64 (SwiGLU refusal, 12); token 1: gate = up =
         # 2^32 (OutputOverflow, 9).  The gate projection of token 1 comes first.
@@ -205,7 +206,7 @@ def test_ffn_prefill_refusal_order(dev, t, fused):
         # and clear afterwards
         assert gate_up(G1, U1, 1.0, 0.5) == 0
     finally:
-        dev.set_ffn_prefill_fusion(True)
+        dev.set_ffn_prefill_form(chart.Device.FFN_AUTO)
         for w in (G1, U1, Gs, Dbig):
             w.free()
 

@@ -239,6 +239,21 @@ def ffn_prefill_dev(dev: "Device", gate: "Tensor", up: "Tensor", down: "Tensor",
                                       h_scales_ptr, stream), "ffn_prefill")
 
 
+def ffn_q8_dev(dev: "Device", gate: "Tensor", up: "Tensor", down: "Tensor", codes_ptr: int, scales_ptr: int,
+               y_ptr: int, h_codes_ptr: int, h_scales_ptr: int, stream: int | None = None) -> None:
+    """ffn_dev from a QuantAct (ah_ffn_q8_dev)."""
+    _check(dev.lib.ah_ffn_q8_dev(dev.h, gate.h, up.h, down.h, codes_ptr, scales_ptr, y_ptr, h_codes_ptr,
+                                 h_scales_ptr, stream), "ffn_q8")
+
+
+def ffn_prefill_q8_dev(dev: "Device", gate: "Tensor", up: "Tensor", down: "Tensor", codes_ptr: int,
+                       scales_ptr: int, n_tok: int, y_ptr: int, h_codes_ptr: int, h_scales_ptr: int,
+                       stream: int | None = None) -> None:
+    """ffn_prefill_dev from the tokens' QuantActs (ah_ffn_prefill_q8_dev)."""
+    _check(dev.lib.ah_ffn_prefill_q8_dev(dev.h, gate.h, up.h, down.h, codes_ptr, scales_ptr, n_tok, y_ptr,
+                                         h_codes_ptr, h_scales_ptr, stream), "ffn_prefill_q8")
+
+
 def swiglu_quant_dev(dev: "Device", gate_ptr: int, up_ptr: int, n_tok: int, n_ff: int, h_codes_ptr: int,
                      h_scales_ptr: int, stream: int | None = None) -> None:
     """swiglu_cols + quant_cols over f32 gate / up [n_tok][n_ff] (ah_swiglu_quant_dev)."""

@@ -442,7 +442,7 @@ uint32_t deal_waves(const GemvPart *parts, size_t n, uint32_t n_wg, size_t act_b
 
 int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x,
                     const int64_t *scales, float *y, int32_t *dots, void *stream,
-                    unsigned long long *status = nullptr, uint32_t key_tok = 0) {
+                    unsigned long long *status = nullptr, uint32_t key_tok = 0, uint64_t out_key0 = 0) {
     if (ctx && !status) status = ctx->d_status;
     if (!ctx || !w || (!x && w->n_in) || (!y && w->n_out)) return AH_ERR_INVALID_ARG;
     if (src == AH_SRC_CODES && !scales && w->n_in) return AH_ERR_INVALID_ARG;
@@ -457,6 +457,7 @@ int32_t gemv_launch(ah_ctx *ctx, const ah_tensor *w, uint32_t src, const void *x
     GemvPart &P = sp.p[0];
     P = make_part(w, src, x, scales, y, dots, st);
     P.key_tok = key_tok;
+    P.out_key0 = out_key0;
     const uint32_t kp = kpad_of(w->n_in);
     AH_HIP(ctx, hipSetDevice(ctx->device));
     const uint32_t grid = deal_wgs(&P, 1, resident_wgs(ctx, w->type, st, kp), st);
@@ -486,14 +487,15 @@ int32_t reset_status(ah_ctx *ctx) {
 // `fixed` (with `fixed_cap` bytes) replaces the context's growable scratch: the call then neither
 // allocates nor frees anything (device or host, for up to kStackParts parts), and refuses with
 // AH_ERR_SCRATCH_LIMIT when its operands and partials need more than `fixed_cap`.
-// `opt` (optional): per-part token offsets of the refusal keys (part i's refusals are keyed as if
-// its tokens were numbered from tok0[i]: the prefill FFN's up projection after its gate), the
-// status word the call records into, and the fused FFN form (parts {gate, up} of one
-// dequantize-once type: one launch whose epilogue writes the hidden QuantAct; `y` then names the
-// optional f32 gate / up outputs).
+// Output refusals are keyed part by part (part i's key t * n_out_i + row offset by the n_tok *
+// n_out of every part before it: the first refusal in projection-then-column-then-row order, as
+// separate calls joined left to right would return it; the prefill FFN's gate before its up).
+// `opt` (optional): explicit per-part key offsets in place of those, the status word the call
+// records into, and the fused FFN form (parts {gate, up} of one dequantize-once type: one launch
+// whose epilogue writes the hidden QuantAct; `y` then names the optional f32 gate / up outputs).
 constexpr size_t kStackParts = 16;
 struct GroupOpts {
-    const uint32_t *tok0 = nullptr;
+    const uint64_t *key0 = nullptr;
     unsigned long long *status = nullptr;
     const GemmFfn *ffn = nullptr;
 };
@@ -504,7 +506,21 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     if (!ctx || !w || !y || n_parts == 0 || n_parts > 65536 || !w[0]) return AH_ERR_INVALID_ARG;
     const GemmFfn *ffn = opt ? opt->ffn : nullptr;
     unsigned long long *const status = opt && opt->status ? opt->status : ctx->d_status;
-    auto tok0_of = [&](size_t i) -> uint32_t { return opt && opt->tok0 ? opt->tok0[i] : 0u; };
+    uint64_t k0_stack[kStackParts];
+    std::vector<uint64_t> k0_heap;
+    if (n_parts > kStackParts && !(opt && opt->key0)) {
+        if (fixed) return AH_ERR_INVALID_ARG;
+        k0_heap.resize(n_parts);
+    }
+    uint64_t *const k0_own = n_parts > kStackParts ? k0_heap.data() : k0_stack;
+    const uint64_t *const key0 = opt && opt->key0 ? opt->key0 : k0_own;
+    if (!(opt && opt->key0)) {
+        uint64_t acc = 0;
+        for (size_t i = 0; i < n_parts; ++i) {
+            k0_own[i] = acc;
+            acc += w[i] ? (uint64_t)n_tok * w[i]->n_out : 0u;
+        }
+    }
     const size_t n_in_sz = w[0]->n_in;
     bool any_q4k = false;
     if (ffn && (n_parts != 2 || !w[1] || w[0]->type != w[1]->type || w[0]->n_out != w[1]->n_out))
@@ -571,8 +587,8 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
             for (size_t c = 0; c < n_tok;) {
                 if (!stream_ok) {
                     const int32_t st = gemv_launch(ctx, w[i], src, x_of(c), src == AH_SRC_CODES ? scales_in + c * nb : nullptr,
-                                                   y[i] + c * w[i]->n_out, nullptr, stream, status,
-                                                   tok0_of(i) + (uint32_t)c);
+                                                   y[i] + c * w[i]->n_out, nullptr, stream, status, (uint32_t)c,
+                                                   key0[i] + (uint64_t)c * w[i]->n_out);
                     if (st) return st;
                     ++c;
                     continue;
@@ -583,7 +599,8 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                     bool st_j = false;
                     sp.p[j] = make_part(w[i], src, x_of(c + j), src == AH_SRC_CODES ? scales_in + (c + j) * nb : nullptr,
                                         y[i] + (c + j) * w[i]->n_out, nullptr, st_j);
-                    sp.p[j].key_tok = tok0_of(i) + (uint32_t)(c + j);
+                    sp.p[j].key_tok = (uint32_t)(c + j);
+                    sp.p[j].out_key0 = key0[i] + (uint64_t)(c + j) * w[i]->n_out;
                 }
                 const uint32_t grid = deal_wgs(sp.p, sp.n, resident_wgs(ctx, w[i]->type, true, kp), true);
                 if (grid == 0) return AH_ERR_OUT_OF_MEMORY;
@@ -610,19 +627,17 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                 rw[k] = w[i];
                 ry[k++] = y[i];
             }
-        if (opt && opt->tok0) {  // the remaining parts keep their token offsets
-            GroupOpts o2 = *opt;
-            uint32_t t_stack[kStackParts];
-            std::vector<uint32_t> t_heap;
-            if (n_parts > kStackParts) t_heap.resize(n_parts);
-            uint32_t *t0 = n_parts > kStackParts ? t_heap.data() : t_stack;
-            size_t q = 0;
-            for (size_t i = 0; i < n_parts; ++i)
-                if (!gemv23(w[i])) t0[q++] = tok0_of(i);
-            o2.tok0 = t0;
-            return gemm_group_launch(ctx, k, rw, src, x, scales_in, n_tok, ry, stream, fixed, fixed_cap, &o2);
-        }
-        return gemm_group_launch(ctx, k, rw, src, x, scales_in, n_tok, ry, stream, fixed, fixed_cap, opt);
+        // the remaining parts keep their key offsets
+        GroupOpts o2 = opt ? *opt : GroupOpts{};
+        uint64_t t_stack[kStackParts];
+        std::vector<uint64_t> t_heap;
+        if (n_parts > kStackParts) t_heap.resize(n_parts);
+        uint64_t *t0 = n_parts > kStackParts ? t_heap.data() : t_stack;
+        size_t q = 0;
+        for (size_t i = 0; i < n_parts; ++i)
+            if (!gemv23(w[i])) t0[q++] = key0[i];
+        o2.key0 = t0;
+        return gemm_group_launch(ctx, k, rw, src, x, scales_in, n_tok, ry, stream, fixed, fixed_cap, &o2);
     }
     const uint32_t n_in = (uint32_t)n_in_sz, N = (uint32_t)n_tok;
     const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
@@ -658,7 +673,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         d.splits = d.n_out && !ffn ? ah_gemm_pick_splits(w[i]->type, d.n_out, n_in, N, cus, kind_of(w[i]->type)) : 1;
         d.y = y[i];
         d.partials = nullptr;
-        d.key0 = (uint64_t)tok0_of(i) * d.n_out;
+        d.key0 = key0[i];
         if (d.splits > 1) {
             part_off[i] = part_bytes;
             part_bytes = align256(part_bytes + (size_t)d.splits * N * d.n_out * 4);
@@ -1048,9 +1063,13 @@ int32_t ah_gemv_q8_dots_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_cod
     return gemv_launch(ctx, w, AH_SRC_CODES, d_codes, d_scales, d_y, d_dots, stream);
 }
 
-int32_t ah_ffn_gate_up_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const float *d_x,
-                           float *d_gate_y, float *d_up_y, int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
+// The decode FFN's gate/up launch from an f32 input (src AH_SRC_F32) or a QuantAct (AH_SRC_CODES:
+// x = codes, 4-byte aligned, with `scales`).
+static int32_t ffn_gate_up_launch(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, uint32_t src,
+                                  const void *d_x, const int64_t *d_scales, float *d_gate_y, float *d_up_y,
+                                  int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
     if (!ctx || !gate || !up || !d_x || !d_h_codes || !d_h_scales) return AH_ERR_INVALID_ARG;
+    if (src == AH_SRC_CODES && (!d_scales || reinterpret_cast<uintptr_t>(d_scales) % 8)) return AH_ERR_INVALID_ARG;
     if (gate->type != up->type || gate->n_out != up->n_out || gate->n_in != up->n_in || gate->n_in == 0)
         return AH_ERR_INVALID_ARG;
     if (reinterpret_cast<uintptr_t>(d_x) % 4 || reinterpret_cast<uintptr_t>(d_h_scales) % 8) return AH_ERR_INVALID_ARG;
@@ -1060,8 +1079,8 @@ int32_t ah_ffn_gate_up_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *
     sp.n = 2;
     bool s0 = false, s1 = false;
     // whole units (not the latency launches' Q4_K pairs): each wave streams a few whole rows
-    sp.p[0] = make_part(gate, AH_SRC_F32, d_x, nullptr, d_gate_y, nullptr, s0, false);
-    sp.p[1] = make_part(up, AH_SRC_F32, d_x, nullptr, d_up_y, nullptr, s1, false);
+    sp.p[0] = make_part(gate, src, d_x, d_scales, d_gate_y, nullptr, s0, false);
+    sp.p[1] = make_part(up, src, d_x, d_scales, d_up_y, nullptr, s1, false);
     if (!s0 || !s1) return AH_ERR_INVALID_ARG;  // rows past one streaming tile
     const uint32_t kp = kpad_of(gate->n_in);
     AH_HIP(ctx, hipSetDevice(ctx->device));
@@ -1077,16 +1096,33 @@ int32_t ah_ffn_gate_up_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *
     return AH_OK;
 }
 
-int32_t ah_ffn_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
-                   const float *d_x, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
+static int32_t ffn_launch(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                          uint32_t src, const void *d_x, const int64_t *d_scales, float *d_y, int8_t *d_h_codes,
+                          int64_t *d_h_scales, void *stream) {
     if (!ctx || !down || !d_y) return AH_ERR_INVALID_ARG;
     if (!gate || down->n_in != gate->n_out || down->n_out != gate->n_in) return AH_ERR_INVALID_ARG;
     if (reinterpret_cast<uintptr_t>(d_h_codes) % 4) return AH_ERR_INVALID_ARG;
-    int32_t st = ah_ffn_gate_up_dev(ctx, gate, up, d_x, nullptr, nullptr, d_h_codes, d_h_scales, stream);
+    int32_t st = ffn_gate_up_launch(ctx, gate, up, src, d_x, d_scales, nullptr, nullptr, d_h_codes, d_h_scales, stream);
     if (st) return st;
     // the down projection's refusals go to the second status word (reported only when the
     // gate/up launch refused nothing)
     return gemv_launch(ctx, down, AH_SRC_CODES, d_h_codes, d_h_scales, d_y, nullptr, stream, ctx->d_status + 1);
+}
+
+int32_t ah_ffn_gate_up_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const float *d_x,
+                           float *d_gate_y, float *d_up_y, int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
+    return ffn_gate_up_launch(ctx, gate, up, AH_SRC_F32, d_x, nullptr, d_gate_y, d_up_y, d_h_codes, d_h_scales, stream);
+}
+
+int32_t ah_ffn_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                   const float *d_x, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
+    return ffn_launch(ctx, gate, up, down, AH_SRC_F32, d_x, nullptr, d_y, d_h_codes, d_h_scales, stream);
+}
+
+int32_t ah_ffn_q8_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                      const int8_t *d_codes, const int64_t *d_scales, float *d_y, int8_t *d_h_codes,
+                      int64_t *d_h_scales, void *stream) {
+    return ffn_launch(ctx, gate, up, down, AH_SRC_CODES, d_codes, d_scales, d_y, d_h_codes, d_h_scales, stream);
 }
 
 int32_t ah_swiglu_quant_dev(ah_ctx *ctx, const float *d_gate, const float *d_up, size_t n_tok, size_t n_ff,
@@ -1111,15 +1147,18 @@ int32_t ah_set_ffn_prefill_form(ah_ctx *ctx, uint32_t form) {
     return AH_OK;
 }
 
-int32_t ah_ffn_gate_up_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const float *d_x,
-                                   size_t n_tok, float *d_gate_y, float *d_up_y, int8_t *d_h_codes,
-                                   int64_t *d_h_scales, void *stream) {
+// The prefill FFN's gate/up (+ SwiGLU + hidden quantizer) from f32 x[n_tok][n_in] or, with
+// src AH_SRC_CODES, a QuantAct per token (codes [n_tok][n_in], scales [n_tok][ceil(n_in/32)]).
+static int32_t ffn_prefill_gate_up(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, uint32_t src,
+                                   const void *d_x, const int64_t *d_scales, size_t n_tok, float *d_gate_y,
+                                   float *d_up_y, int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
     if (!ctx || !gate || !up) return AH_ERR_INVALID_ARG;
     if (gate->type != up->type || gate->n_out != up->n_out || gate->n_in != up->n_in) return AH_ERR_INVALID_ARG;
     const size_t n_ff = gate->n_out;
     if (n_tok == 0 || n_ff == 0) return AH_OK;
     if (!d_x || !d_h_codes || !d_h_scales || gate->n_in == 0) return AH_ERR_INVALID_ARG;
-    if (reinterpret_cast<uintptr_t>(d_x) % 4 || reinterpret_cast<uintptr_t>(d_h_scales) % 8 ||
+    if (src == AH_SRC_CODES && !d_scales) return AH_ERR_INVALID_ARG;
+    if ((src == AH_SRC_F32 && reinterpret_cast<uintptr_t>(d_x) % 4) || reinterpret_cast<uintptr_t>(d_h_scales) % 8 ||
         reinterpret_cast<uintptr_t>(d_gate_y) % 4 || reinterpret_cast<uintptr_t>(d_up_y) % 4)
         return AH_ERR_INVALID_ARG;
     // refusal keys up to 4 * n_tok * n_ff (gate, up, SwiGLU, hidden blocks)
@@ -1135,9 +1174,10 @@ int32_t ah_ffn_gate_up_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_
         float *y2[2] = {d_gate_y, d_up_y};
         GroupOpts o;
         o.ffn = &f;
-        return gemm_group_launch(ctx, 2, w2, AH_SRC_F32, d_x, nullptr, n_tok, y2, stream, nullptr, 0, &o);
+        return gemm_group_launch(ctx, 2, w2, src, d_x, d_scales, n_tok, y2, stream, nullptr, 0, &o);
     }
-    // two passes: gate and up as one grouped GEMM (up's refusals keyed after all of gate's), then
+    // two passes: gate and up as one grouped GEMM (part order: up's refusals keyed after all of
+    // gate's), then
     // the SwiGLU + hidden quantizer over their f32 outputs
     float *g = d_gate_y, *u = d_up_y;
     if (!g || !u) {
@@ -1160,10 +1200,7 @@ int32_t ah_ffn_gate_up_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_
         if (!u) u = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(b) + align256(n_tok * n_ff * 4));
     }
     float *y2[2] = {g, u};
-    const uint32_t tok0[2] = {0u, (uint32_t)n_tok};
-    GroupOpts o;
-    o.tok0 = tok0;
-    int32_t st = gemm_group_launch(ctx, 2, w2, AH_SRC_F32, d_x, nullptr, n_tok, y2, stream, nullptr, 0, &o);
+    int32_t st = gemm_group_launch(ctx, 2, w2, src, d_x, d_scales, n_tok, y2, stream);
     if (st) return st;
     const uint64_t NF = (uint64_t)n_tok * n_ff;
     SwigluArgs a = {g, u, d_h_codes, d_h_scales, (uint32_t)n_tok, (uint32_t)n_ff, 2 * NF, 3 * NF, ctx->d_status};
@@ -1171,15 +1208,22 @@ int32_t ah_ffn_gate_up_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_
     return AH_OK;
 }
 
-int32_t ah_ffn_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
-                           const float *d_x, size_t n_tok, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales,
-                           void *stream) {
+int32_t ah_ffn_gate_up_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const float *d_x,
+                                   size_t n_tok, float *d_gate_y, float *d_up_y, int8_t *d_h_codes,
+                                   int64_t *d_h_scales, void *stream) {
+    return ffn_prefill_gate_up(ctx, gate, up, AH_SRC_F32, d_x, nullptr, n_tok, d_gate_y, d_up_y, d_h_codes,
+                               d_h_scales, stream);
+}
+
+static int32_t ffn_prefill(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                           uint32_t src, const void *d_x, const int64_t *d_scales, size_t n_tok, float *d_y,
+                           int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
     if (!ctx || !gate || !down) return AH_ERR_INVALID_ARG;
     if (down->n_in != gate->n_out || down->n_out != gate->n_in) return AH_ERR_INVALID_ARG;
     if (n_tok && down->n_out && !d_y) return AH_ERR_INVALID_ARG;
     if (reinterpret_cast<uintptr_t>(d_h_codes) % 4) return AH_ERR_INVALID_ARG;
-    int32_t st = ah_ffn_gate_up_prefill_dev(ctx, gate, up, d_x, n_tok, nullptr, nullptr, d_h_codes, d_h_scales,
-                                            stream);
+    int32_t st = ffn_prefill_gate_up(ctx, gate, up, src, d_x, d_scales, n_tok, nullptr, nullptr, d_h_codes,
+                                     d_h_scales, stream);
     if (st) return st;
     if (n_tok == 0 || down->n_out == 0) return AH_OK;
     // the down projection from the hidden QuantAct; its refusals go to the second status word
@@ -1188,6 +1232,61 @@ int32_t ah_ffn_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *
     o.status = ctx->d_status + 1;
     return gemm_group_launch(ctx, 1, &down, AH_SRC_CODES, d_h_codes, d_h_scales, n_tok, &d_y, stream, nullptr, 0,
                              &o);
+}
+
+int32_t ah_ffn_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                           const float *d_x, size_t n_tok, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales,
+                           void *stream) {
+    return ffn_prefill(ctx, gate, up, down, AH_SRC_F32, d_x, nullptr, n_tok, d_y, d_h_codes, d_h_scales, stream);
+}
+
+int32_t ah_ffn_prefill_q8_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                              const int8_t *d_codes, const int64_t *d_scales, size_t n_tok, float *d_y,
+                              int8_t *d_h_codes, int64_t *d_h_scales, void *stream) {
+    return ffn_prefill(ctx, gate, up, down, AH_SRC_CODES, d_codes, d_scales, n_tok, d_y, d_h_codes, d_h_scales,
+                       stream);
+}
+
+// ---- device buffers for callers without a HIP runtime of their own -----------------------------
+
+int32_t ah_dev_alloc(ah_ctx *ctx, size_t bytes, void **d) {
+    if (!ctx || !d) return AH_ERR_INVALID_ARG;
+    *d = nullptr;
+    if (bytes == 0) return AH_OK;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    if (hipMalloc(d, bytes) != hipSuccess) {
+        *d = nullptr;
+        return AH_ERR_OUT_OF_MEMORY;
+    }
+    return AH_OK;
+}
+
+int32_t ah_dev_free(ah_ctx *ctx, void *d) {
+    if (!ctx) return AH_ERR_INVALID_ARG;
+    if (!d) return AH_OK;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, hipStreamSynchronize(ctx->stream));  // the context's queued work may still read it
+    AH_HIP(ctx, hipFree(d));
+    return AH_OK;
+}
+
+int32_t ah_copy_to_dev(ah_ctx *ctx, void *d_dst, const void *src, size_t bytes, void *stream) {
+    if (!ctx || ((!d_dst || !src) && bytes)) return AH_ERR_INVALID_ARG;
+    if (bytes == 0) return AH_OK;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, hipMemcpyAsync(d_dst, src, bytes, hipMemcpyHostToDevice, pick(ctx, stream)));
+    // the host buffer may be reused as soon as the call returns
+    AH_HIP(ctx, hipStreamSynchronize(pick(ctx, stream)));
+    return AH_OK;
+}
+
+int32_t ah_copy_to_host(ah_ctx *ctx, void *dst, const void *d_src, size_t bytes, void *stream) {
+    if (!ctx || ((!dst || !d_src) && bytes)) return AH_ERR_INVALID_ARG;
+    if (bytes == 0) return AH_OK;
+    AH_HIP(ctx, hipSetDevice(ctx->device));
+    AH_HIP(ctx, hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, pick(ctx, stream)));
+    AH_HIP(ctx, hipStreamSynchronize(pick(ctx, stream)));
+    return AH_OK;
 }
 
 int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w,
@@ -1207,6 +1306,7 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
         mixed = mixed || w[i]->type != w[0]->type;
         bool st = false;
         parts[i] = make_part(w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr, st);
+        parts[i].out_key0 = i ? parts[i - 1].out_key0 + w[i - 1]->n_out : 0;  // projection-then-row order
         all_stream = all_stream && st;
         const uint32_t kp = kpad_of(w[i]->n_in);
         kpad_max = kp > kpad_max ? kp : kpad_max;
@@ -1259,7 +1359,9 @@ int32_t ah_gemv_plan_create(ah_ctx *ctx, size_t n_parts, const ah_tensor *const 
     // A table plan serves many projections at once (throughput): its parts keep whole units.
     for (size_t i = 0; i < n_parts; ++i) {
         bool st = false;
+        const uint64_t k0 = parts[i].out_key0;
         parts[i] = make_part(w[i], AH_SRC_F32, d_x[i], nullptr, d_y[i], nullptr, st, false);
+        parts[i].out_key0 = k0;
     }
     // Streaming plan: waves dealt over the parts, activations sharing a workgroup's LDS region of
     // at most `budget` bytes (15 KB keeps two workgroups per CU; a larger activation raises it).

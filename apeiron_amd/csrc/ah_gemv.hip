@@ -828,7 +828,7 @@ __global__ void __launch_bounds__(kThreads)
         if (r < R && gl == 0 && row < P.n_out) {
             P.y[row] = sum;
             const uint32_t oc = ah_out_code(sum);
-            if (oc) ah_record(status, ah_out_key((uint64_t)P.key_tok * P.n_out + row, oc));
+            if (oc) ah_record(status, ah_out_key(P.out_key0 + row, oc));
         }
     }
 }
@@ -1437,7 +1437,7 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
         ffn_epilogue(fa, f_b0, f_b1, hsum, status);
     } else {
         if (obad != 0xFFFFFFFFu && lane == 0)
-            ah_record(status, ah_out_key((uint64_t)P.key_tok * P.n_out + (obad >> 1), (obad & 1u) ? 9u : 8u));
+            ah_record(status, ah_out_key(P.out_key0 + (obad >> 1), (obad & 1u) ? 9u : 8u));
     }
 }
 

@@ -194,9 +194,10 @@ struct GemvPart {
     uint32_t wg_count;     // workgroups of this part
     uint32_t src;          // AH_SRC_*
     uint32_t type;         // GGUF type (AH_GGML_*): read by the mixed-type streaming plan
-    uint32_t key_tok;      // token (column) index of a prefill served by GEMV launches: refusals are
-                           // keyed key_tok * n_in + element (input) and key_tok * n_out + row
-                           // (output), token-major as matmat_q8act reports them; 0 otherwise
+    uint32_t key_tok;      // token (column) index of a prefill served by GEMV launches: input
+                           // refusals are keyed key_tok * n_in + element; 0 otherwise
+    uint64_t out_key0;     // added to the output refusal key (row): the part's and the token's place
+                           // in a grouped prefill, token-major per part as matmat_q8act reports
 };
 
 // The parts of a streaming launch without a workgroup table: a single projection, or a plan of at

@@ -166,6 +166,12 @@ int32_t ah_ffn_gate_up_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *
                            void *stream);
 int32_t ah_ffn_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
                    const float *d_x, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales, void *stream);
+/* ah_ffn_dev from a QuantAct (the engine's own quantized activation, ffn_q8act_prepared_into's
+ * `q = quantize(x)`): d_codes[n_embd] (4-byte aligned) and d_scales[ceil(n_embd/32)] (8-byte
+ * aligned) in place of the f32 input; the same launches and refusal order after the input's. */
+int32_t ah_ffn_q8_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                      const int8_t *d_codes, const int64_t *d_scales, float *d_y, int8_t *d_h_codes,
+                      int64_t *d_h_scales, void *stream);
 
 /* Prefill FFN, N = n_tok > 1 (the step's column path, step/cols.rs:1026-1067: quant_cols, the
  * [W_gate; W_up] GEMM with the SwiGLU epilogue, gemm_q8_0_swiglu_carrier, kern/gemm.rs:955-1168,
@@ -195,6 +201,11 @@ int32_t ah_ffn_gate_up_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_
 int32_t ah_ffn_prefill_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
                            const float *d_x, size_t n_tok, float *d_y, int8_t *d_h_codes, int64_t *d_h_scales,
                            void *stream);
+/* ah_ffn_prefill_dev from the columns' QuantActs (step/cols.rs:1026's `qs = quant_cols(xs)`):
+ * d_codes[n_tok][n_embd] and d_scales[n_tok][ceil(n_embd/32)] (8-byte aligned). */
+int32_t ah_ffn_prefill_q8_dev(ah_ctx *ctx, const ah_tensor *gate, const ah_tensor *up, const ah_tensor *down,
+                              const int8_t *d_codes, const int64_t *d_scales, size_t n_tok, float *d_y,
+                              int8_t *d_h_codes, int64_t *d_h_scales, void *stream);
 /* The prefill FFN's form per context: AUTO (the default: two passes), FUSED (one launch for
  * Q4_K / Q2_K / Q3_K gate/up; other types keep two passes) or TWO_PASS.  The hidden QuantAct is
  * bit-identical given the same gate / up values; those agree within the GEMM tolerance. */
@@ -207,6 +218,17 @@ int32_t ah_set_ffn_prefill_form(ah_ctx *ctx, uint32_t form);
  * element's conversion or SwiGLU, then the quantizer's blocks. */
 int32_t ah_swiglu_quant_dev(ah_ctx *ctx, const float *d_gate, const float *d_up, size_t n_tok, size_t n_ff,
                             int8_t *d_h_codes, int64_t *d_h_scales, void *stream);
+
+/* Device buffers and copies for callers that bind only this library (no HIP runtime of their
+ * own, as the engine's dlopen binding): the device-pointer forms above take these.  No
+ * counterpart in the reference (its CPU path owns host memory only; its Vulkan backend allocates
+ * through its own device object).  ah_dev_free first waits for the context's stream.  The copies
+ * run on `stream` (NULL: the context's) and return once complete, so the host buffer may be
+ * reused at once. */
+int32_t ah_dev_alloc(ah_ctx *ctx, size_t bytes, void **d);
+int32_t ah_dev_free(ah_ctx *ctx, void *d);
+int32_t ah_copy_to_dev(ah_ctx *ctx, void *d_dst, const void *src, size_t bytes, void *stream);
+int32_t ah_copy_to_host(ah_ctx *ctx, void *dst, const void *d_src, size_t bytes, void *stream);
 
 /* Persistent decode sequence: a token's chain of projection stages in ONE launch.  Stage s may
  * read outputs of stages before it (q/k/v -> o -> gate/up -> SwiGLU -> down per layer, then the

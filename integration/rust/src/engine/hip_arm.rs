@@ -1,5 +1,5 @@
 // The engine side of the `hip` backend: what a maintainer adds to the reference's engine so that
-// every projection can run on the MI355X.  Three insertions, each an item of its own below, with
+// every projection can run on the MI355X.  Four insertions, each an item of its own below, with
 // the place it goes; nothing else in the engine changes (the GGUF layouts, the projection entry
 // points and the CPU kernels stay as they are, and a machine without the library runs exactly as
 // before).
@@ -43,7 +43,12 @@ pub(crate) fn load_hip(engine: &crate::engine::Engine, device: i32) -> Option<cr
     for (idx, t) in engine.table().entries().iter().enumerate() {
         let served = matches!(
             t.ggml_type,
-            quant::GGML_TYPE_Q8_0 | quant::GGML_TYPE_Q5_0 | quant::GGML_TYPE_Q4_K | quant::GGML_TYPE_Q6_K
+            quant::GGML_TYPE_Q8_0
+                | quant::GGML_TYPE_Q5_0
+                | quant::GGML_TYPE_Q2_K
+                | quant::GGML_TYPE_Q3_K
+                | quant::GGML_TYPE_Q4_K
+                | quant::GGML_TYPE_Q6_K
         );
         if !served || t.dims.len() != 2 {
             continue;
@@ -99,6 +104,162 @@ pub(crate) fn hip_projection(
     }
 }
 
-// The prefill form is the same shape: `matmat_q8act` (src/engine/kern/matmat.rs:134) routes to
-// `Hip::matmat_q8act(idx, &cols)` with `cols[c] = (qs[c].codes(), qs[c].scales())`, one Q32.32
-// vector per column, under the same Some / None / refusal rule.
+// ---- 4. Device-resident forms: the grouped projections, the FFN and the column (prefill) path ---
+//
+// Each helper below returns Some(outputs) when the device served the call, None when the caller
+// keeps its CPU path (a tensor not resident, no backend, a backend failure), and the contract's own
+// refusal as the value the CPU path would return.  The activation goes up once per call, every
+// projection of the call (and the FFN's hidden activation) stays on the device, and only the
+// outputs come back.
+
+/// The backend's answer mapped onto the engine's: Ok(None) = take the CPU path.
+#[cfg(feature = "hip")]
+fn served<T, E>(r: Result<T, crate::gpu::hip::HipError>, refusal: impl Fn(crate::gpu::hip::HipError) -> Option<E>) -> Result<Option<T>, E> {
+    match r {
+        Ok(v) => Ok(Some(v)),
+        Err(e) => match refusal(e) {
+            Some(err) => Err(err),
+            None => Ok(None),
+        },
+    }
+}
+
+/// src/engine/step.rs:911-1000 `group_q8act_at` (q/k/v, and gate/up outside the fused FFN) — at
+/// the top of its final step, before `projections_q8act(self.resident(), ...)`:
+///
+///     #[cfg(feature = "hip")]
+///     if self.kernel_mode == KernelMode::Hip {
+///         if let Some(out) = hip_group(&self.hip, &idxs, x)? {
+///             return Ok(out);
+///         }
+///     }
+///
+/// `projections_q8act`'s quantization (`quantize(x)`, chart/ffn.rs:236-238) happens here on the
+/// host, so its refusal and the QuantAct are the CPU path's; the projections run on the device in
+/// projection-then-row refusal order.
+#[cfg(feature = "hip")]
+pub(crate) fn hip_group(
+    hip: &std::sync::Mutex<Option<crate::gpu::hip::Hip>>,
+    idxs: &[usize],
+    x: &[i64],
+) -> Result<Option<Vec<Vec<i64>>>, crate::engine::step::StepError> {
+    use crate::engine::step::StepError;
+    use crate::engine::{EngineError, MatvecError};
+    use crate::gpu::hip::HipError;
+    let Ok(mut guard) = hip.lock() else { return Ok(None) };
+    let Some(h) = guard.as_mut() else { return Ok(None) };
+    if !idxs.iter().all(|&i| h.has(i)) {
+        return Ok(None);
+    }
+    let q = crate::engine::chart::ffn::quant_act_pooled(x)
+        .ok_or(StepError::Matvec(MatvecError::Dequant(EngineError::FixedOverflow)))?;
+    served(h.projections_q8act(idxs, q.codes(), q.scales()), |e| match e {
+        HipError::Matvec(m) => Some(StepError::Matvec(m)),
+        HipError::Input(_) | HipError::Ffn(_) | HipError::Backend { .. } => None,
+    })
+}
+
+/// src/engine/step.rs:1004-1037 `ffn_q8act_at` — before the `ffn_q8act_prepared_into(...)` call
+/// (chart/ffn.rs:1609), with `idxs = [li.at(4, layer)?, li.at(5, layer)?, li.at(6, layer)?]`:
+///
+///     #[cfg(feature = "hip")]
+///     if self.kernel_mode == KernelMode::Hip {
+///         if let Some(y) = hip_ffn(&self.hip, idxs, x)? {
+///             return Ok(y);
+///         }
+///     }
+///
+/// gate / up with the exact SwiGLU and the hidden quant_act run in one device launch, down from
+/// that QuantAct in a second: the hidden activation never comes back to the host.  Refusals in
+/// the reference FFN's order: `quantize(x)`'s, a projection's (`FfnError::Matvec`), the SwiGLU's.
+#[cfg(feature = "hip")]
+pub(crate) fn hip_ffn(
+    hip: &std::sync::Mutex<Option<crate::gpu::hip::Hip>>,
+    idxs: [usize; 3],
+    x: &[i64],
+) -> Result<Option<Vec<i64>>, crate::engine::step::StepError> {
+    use crate::engine::step::StepError;
+    use crate::engine::{EngineError, FfnError, MatvecError};
+    use crate::gpu::hip::HipError;
+    let Ok(mut guard) = hip.lock() else { return Ok(None) };
+    let Some(h) = guard.as_mut() else { return Ok(None) };
+    if !idxs.iter().all(|&i| h.has(i)) {
+        return Ok(None);
+    }
+    let q = crate::engine::chart::ffn::quant_act_pooled(x)
+        .ok_or(StepError::Ffn(FfnError::Matvec(MatvecError::Dequant(EngineError::FixedOverflow))))?;
+    served(h.ffn_q8act(idxs[0], idxs[1], idxs[2], q.codes(), q.scales()), |e| match e {
+        HipError::Matvec(m) => Some(StepError::Ffn(FfnError::Matvec(m))),
+        HipError::Ffn(f) => Some(StepError::Ffn(f)),
+        HipError::Input(_) | HipError::Backend { .. } => None,
+    })
+}
+
+/// src/engine/step/cols.rs:485-575 `proj_cols` — in its `xs.len() > 1` branch, once `qs` holds
+/// the columns' QuantActs and before the `matmat_q8act(...)` call:
+///
+///     #[cfg(feature = "hip")]
+///     if mode == KernelMode::Hip {
+///         if let Some(mut cols) = hip_proj_cols(&self.hip, &[idx], qs)? {
+///             return Ok(cols.swap_remove(0));
+///         }
+///     }
+///
+/// (the q/k/v group of the column path passes its three indices at once: one operand pass, one
+/// MFMA launch, refusals projection-then-column-then-row).
+#[cfg(feature = "hip")]
+pub(crate) fn hip_proj_cols(
+    hip: &std::sync::Mutex<Option<crate::gpu::hip::Hip>>,
+    idxs: &[usize],
+    qs: &[crate::engine::chart::QuantAct],
+) -> Result<Option<Vec<Vec<Vec<i64>>>>, crate::engine::step::StepError> {
+    use crate::engine::step::StepError;
+    use crate::gpu::hip::HipError;
+    let Ok(mut guard) = hip.lock() else { return Ok(None) };
+    let Some(h) = guard.as_mut() else { return Ok(None) };
+    if !idxs.iter().all(|&i| h.has(i)) {
+        return Ok(None);
+    }
+    let cols: Vec<(&[i8], &[i64])> = qs.iter().map(|q| (q.codes(), q.scales())).collect();
+    served(h.matmat_group_q8act(idxs, &cols), |e| match e {
+        HipError::Matvec(m) => Some(StepError::Matvec(m)),
+        HipError::Input(_) | HipError::Ffn(_) | HipError::Backend { .. } => None,
+    })
+}
+
+/// src/engine/step/cols.rs:1026-1067 — the column FFN: after `let qs = quant_cols(xs)?;` and
+/// before the fused / separate gate-up branch (a recording tap keeps the CPU path, which holds the
+/// gate and up words the tap stores):
+///
+///     #[cfg(feature = "hip")]
+///     if mode == KernelMode::Hip && tap.is_none() {
+///         let idxs = [li.at(4, layer)?, li.at(5, layer)?, li.at(6, layer)?];
+///         if let Some(out) = hip_ffn_cols(&self.hip, idxs, &qs)? {
+///             return Ok(out);
+///         }
+///     }
+///
+/// gate/up, the exact SwiGLU, the hidden columns' quant_act and down on the device; refusals in
+/// the column path's order (gate for every column, then up, then the SwiGLU, then down).
+#[cfg(feature = "hip")]
+pub(crate) fn hip_ffn_cols(
+    hip: &std::sync::Mutex<Option<crate::gpu::hip::Hip>>,
+    idxs: [usize; 3],
+    qs: &[crate::engine::chart::QuantAct],
+) -> Result<Option<Vec<Vec<i64>>>, crate::engine::step::StepError> {
+    use crate::engine::step::StepError;
+    use crate::gpu::hip::HipError;
+    let Ok(mut guard) = hip.lock() else { return Ok(None) };
+    let Some(h) = guard.as_mut() else { return Ok(None) };
+    if !idxs.iter().all(|&i| h.has(i)) {
+        return Ok(None);
+    }
+    let cols: Vec<(&[i8], &[i64])> = qs.iter().map(|q| (q.codes(), q.scales())).collect();
+    served(h.ffn_cols_q8act(idxs[0], idxs[1], idxs[2], &cols), |e| match e {
+        // the column path reports a gate / up / down projection's refusal as StepError::Matvec
+        // (proj_cols) and the SwiGLU's as StepError::Ffn (swiglu_cols)
+        HipError::Matvec(m) => Some(StepError::Matvec(m)),
+        HipError::Ffn(f) => Some(StepError::Ffn(f)),
+        HipError::Input(_) | HipError::Backend { .. } => None,
+    })
+}

@@ -8,6 +8,12 @@
 //! symbol, or no gfx950 device — exactly as `Vk::load` treats a missing Vulkan loader
 //! (`src/gpu/vulkan.rs:1097-1106`); the engine then keeps its CPU kernels.
 //!
+//! Two kinds of call: the host forms (`matvec_q8act`, `matmat_q8act`, `quant_act`: host buffers in
+//! and out, each call its own copies), and the device-resident forms (`projections_q8act`,
+//! `ffn_q8act`, `matmat_group_q8act`, `ffn_cols_q8act`): one upload of the QuantAct per call into
+//! a staging region the module keeps on the device, every projection of the call (and the FFN's
+//! hidden activation) on the device, one synchronization, one download of the outputs.
+//!
 //! Every ABI status maps to exactly one error value (`HipError::from_status`): statuses 1-9 to the
 //! nine `MatvecError` variants (`src/engine/ops/matvec.rs:11-48`) with their struct fields filled
 //! from the call, 10-11 to `F32Error`, 12-14 to `FfnError`, 20-25 to `HipError::Backend`.
@@ -49,6 +55,24 @@ type MatmatQ8 = unsafe extern "C" fn(*mut AhCtx, *const AhTensor, *const i8, *co
 type QuantAct = unsafe extern "C" fn(*mut AhCtx, *const i64, usize, *mut i8, *mut i64) -> i32;
 type RefusalBits = unsafe extern "C" fn(*mut AhCtx, *mut u32) -> i32;
 type ProbeMfma = unsafe extern "C" fn(*mut AhCtx, u32, *mut f64) -> i32;
+// device-pointer forms (`stream` NULL: the context's stream)
+type SyncStatus = unsafe extern "C" fn(*mut AhCtx, *mut c_void) -> i32;
+type GemvQ8Dev = unsafe extern "C" fn(*mut AhCtx, *const AhTensor, *const i8, *const i64, *mut f32, *mut c_void) -> i32;
+type GemmGroupQ8Dev = unsafe extern "C" fn(
+    *mut AhCtx, usize, *const *const AhTensor, *const i8, *const i64, usize, *const *mut f32, *mut c_void,
+) -> i32;
+type FfnQ8Dev = unsafe extern "C" fn(
+    *mut AhCtx, *const AhTensor, *const AhTensor, *const AhTensor, *const i8, *const i64, *mut f32, *mut i8,
+    *mut i64, *mut c_void,
+) -> i32;
+type FfnPrefillQ8Dev = unsafe extern "C" fn(
+    *mut AhCtx, *const AhTensor, *const AhTensor, *const AhTensor, *const i8, *const i64, usize, *mut f32,
+    *mut i8, *mut i64, *mut c_void,
+) -> i32;
+type DevAlloc = unsafe extern "C" fn(*mut AhCtx, usize, *mut *mut c_void) -> i32;
+type DevFree = unsafe extern "C" fn(*mut AhCtx, *mut c_void) -> i32;
+type CopyToDev = unsafe extern "C" fn(*mut AhCtx, *mut c_void, *const c_void, usize, *mut c_void) -> i32;
+type CopyToHost = unsafe extern "C" fn(*mut AhCtx, *mut c_void, *const c_void, usize, *mut c_void) -> i32;
 
 /// The resolved entry points.
 #[derive(Clone, Copy)]
@@ -62,6 +86,15 @@ struct Fns {
     quant: QuantAct,
     refusal_bits: RefusalBits,
     probe: ProbeMfma,
+    sync: SyncStatus,
+    gemv_q8: GemvQ8Dev,
+    gemm_group_q8: GemmGroupQ8Dev,
+    ffn_q8: FfnQ8Dev,
+    ffn_prefill_q8: FfnPrefillQ8Dev,
+    dev_alloc: DevAlloc,
+    dev_free: DevFree,
+    to_dev: CopyToDev,
+    to_host: CopyToHost,
 }
 
 /// A refusal or failure of a backend call: one value per ABI status.
@@ -123,6 +156,32 @@ struct Resident {
     n_in: usize,
 }
 
+/// The device staging region of the device-resident forms: one allocation, grown on demand and
+/// carved per call into 256-byte aligned pieces (activation codes and scales in, outputs and the
+/// FFN's hidden QuantAct out), so a call allocates nothing once the region has its size.
+struct Stage {
+    d: *mut c_void,
+    bytes: usize,
+}
+
+/// Offsets of a call's pieces in the staging region.
+struct Carve {
+    at: Vec<usize>,
+    total: usize,
+}
+
+impl Carve {
+    fn new(sizes: &[usize]) -> Carve {
+        let mut at = Vec::with_capacity(sizes.len());
+        let mut total = 0usize;
+        for &s in sizes {
+            at.push(total);
+            total += s.div_ceil(256) * 256;
+        }
+        Carve { at, total }
+    }
+}
+
 /// The loaded backend: one context on one GPU and the engine's resident projection tensors,
 /// keyed by directory index.  Not thread-safe (one context, as the reference's pool lock).
 pub struct Hip {
@@ -130,6 +189,7 @@ pub struct Hip {
     ctx: *mut AhCtx,
     f: Fns,
     tensors: HashMap<usize, Resident>,
+    stage: Stage,
 }
 
 // SAFETY: the context and tensor handles are plain device-side objects of the library, usable from
@@ -175,6 +235,15 @@ impl Hip {
                 quant: sym(lib, b"ah_quant_act\0")?,
                 refusal_bits: sym(lib, b"ah_last_refusal_bits\0")?,
                 probe: sym(lib, b"ah_probe_mfma_peak\0")?,
+                sync: sym(lib, b"ah_sync_status\0")?,
+                gemv_q8: sym(lib, b"ah_gemv_q8_dev\0")?,
+                gemm_group_q8: sym(lib, b"ah_gemm_group_q8_dev\0")?,
+                ffn_q8: sym(lib, b"ah_ffn_q8_dev\0")?,
+                ffn_prefill_q8: sym(lib, b"ah_ffn_prefill_q8_dev\0")?,
+                dev_alloc: sym(lib, b"ah_dev_alloc\0")?,
+                dev_free: sym(lib, b"ah_dev_free\0")?,
+                to_dev: sym(lib, b"ah_copy_to_dev\0")?,
+                to_host: sym(lib, b"ah_copy_to_host\0")?,
             })
         })();
         let f = match resolved {
@@ -191,7 +260,7 @@ impl Hip {
             libc::dlclose(lib);
             return Err(format!("ah_init: {msg} (status {st})"));
         }
-        Ok(Hip { lib, ctx, f, tensors: HashMap::new() })
+        Ok(Hip { lib, ctx, f, tensors: HashMap::new(), stage: Stage { d: std::ptr::null_mut(), bytes: 0 } })
     }
 
     fn check(&self, st: i32, shape: CallShape, what: &str) -> Result<(), HipError> {
@@ -286,6 +355,247 @@ impl Hip {
         }
     }
 
+    // ---- device-resident forms ------------------------------------------------------------
+    //
+    // One upload of the activation per call, every projection of the call on the device, one
+    // synchronization and one download of the outputs: the grouped decode projections, the FFN
+    // with its hidden activation kept on the device, and the prefill forms.
+
+    fn resident(&self, idx: usize) -> Result<&Resident, HipError> {
+        self.tensors.get(&idx).ok_or(HipError::Backend { status: 21, what: "tensor not resident".into() })
+    }
+
+    /// The staging region with at least `bytes`, as a base address.
+    fn stage(&mut self, bytes: usize) -> Result<*mut u8, HipError> {
+        if bytes > self.stage.bytes {
+            // SAFETY: the old region came from ah_dev_alloc on this context (ah_dev_free waits for
+            // the context's stream first).
+            unsafe {
+                if !self.stage.d.is_null() {
+                    (self.f.dev_free)(self.ctx, self.stage.d);
+                }
+            }
+            self.stage = Stage { d: std::ptr::null_mut(), bytes: 0 };
+            let want = bytes + bytes / 4;
+            let mut d: *mut c_void = std::ptr::null_mut();
+            // SAFETY: d receives a device address or stays null.
+            let st = unsafe { (self.f.dev_alloc)(self.ctx, want, &mut d) };
+            self.check(st, CallShape::default(), "ah_dev_alloc")?;
+            self.stage = Stage { d, bytes: want };
+        }
+        Ok(self.stage.d.cast::<u8>())
+    }
+
+    fn upload_bytes<T>(&self, d: *mut u8, host: &[T]) -> Result<(), HipError> {
+        let n = std::mem::size_of_val(host);
+        // SAFETY: d has room for n bytes (carved from the staging region); host is live.
+        let st = unsafe { (self.f.to_dev)(self.ctx, d.cast::<c_void>(), host.as_ptr().cast::<c_void>(), n, std::ptr::null_mut()) };
+        self.check(st, CallShape::default(), "ah_copy_to_dev")
+    }
+
+    fn download_bytes<T>(&self, host: &mut [T], d: *const u8) -> Result<(), HipError> {
+        let n = std::mem::size_of_val(host);
+        // SAFETY: d holds n bytes the call wrote; host is live and exclusively borrowed.
+        let st = unsafe { (self.f.to_host)(self.ctx, host.as_mut_ptr().cast::<c_void>(), d.cast::<c_void>(), n, std::ptr::null_mut()) };
+        self.check(st, CallShape::default(), "ah_copy_to_host")
+    }
+
+    /// The f32 outputs as Q32.32 words (`F32::to_q32`, within the tolerance of the exact value).
+    fn to_q32(y: &[f32]) -> Result<Vec<i64>, HipError> {
+        y.iter().map(|v| F32(v.to_bits()).to_q32().ok_or(HipError::Matvec(MatvecError::OutputOverflow))).collect()
+    }
+
+    /// `projections_q8act_prepared` (`src/engine/chart/ffn.rs:940-954`): the resident projections
+    /// `idxs` (one n_in) over ONE QuantAct, uploaded once, one launch each on the device, one
+    /// synchronization.  The first refusal in projection-then-row order: when the batch refuses,
+    /// the projections run again one at a time to name the first (a rare path: the contract's
+    /// refusals are overflows).
+    pub fn projections_q8act(&mut self, idxs: &[usize], codes: &[i8], scales: &[i64]) -> Result<Vec<Vec<i64>>, HipError> {
+        let mut rs: Vec<(*mut AhTensor, u32, usize, usize)> = Vec::with_capacity(idxs.len());
+        for &i in idxs {
+            let r = self.resident(i)?;
+            if r.n_in != codes.len() {
+                return Err(HipError::Matvec(MatvecError::ShapeMismatch { x: codes.len(), n_in: r.n_in }));
+            }
+            rs.push((r.t, r.ggml_type, r.n_out, r.n_in));
+        }
+        if scales.len() != codes.len().div_ceil(32) {
+            return Err(HipError::Backend { status: 21, what: "scales length".into() });
+        }
+        let mut sizes = vec![codes.len(), 8 * scales.len()];
+        sizes.extend(rs.iter().map(|r| 4 * r.2));
+        let c = Carve::new(&sizes);
+        let base = self.stage(c.total)?;
+        // SAFETY (all pointer arithmetic below): every offset lies inside the carve's total.
+        let (dc, ds) = unsafe { (base.add(c.at[0]), base.add(c.at[1])) };
+        self.upload_bytes(dc, codes)?;
+        self.upload_bytes(ds, scales)?;
+        let launch_all = |hip: &Hip, upto: Option<usize>| -> i32 {
+            for (k, r) in rs.iter().enumerate() {
+                if upto.is_some_and(|u| k != u) {
+                    continue;
+                }
+                // SAFETY: device pointers carved above; the tensor is resident on this context.
+                let st = unsafe {
+                    (hip.f.gemv_q8)(hip.ctx, r.0, dc.cast::<i8>(), ds.cast::<i64>(), base.add(c.at[2 + k]).cast::<f32>(), std::ptr::null_mut())
+                };
+                if st != AH_OK {
+                    return st;
+                }
+            }
+            // SAFETY: the context is live; NULL is its own stream.
+            unsafe { (hip.f.sync)(hip.ctx, std::ptr::null_mut()) }
+        };
+        let st = launch_all(self, None);
+        if st != AH_OK {
+            for (k, r) in rs.iter().enumerate() {
+                let sk = launch_all(self, Some(k));
+                if sk != AH_OK {
+                    let shape = CallShape { ggml_type: r.1, n_in: r.3, x_len: codes.len(), need: 0, have: 0 };
+                    self.check(sk, shape, "ah_gemv_q8_dev")?;
+                }
+            }
+            self.check(st, CallShape::default(), "ah_gemv_q8_dev")?;
+        }
+        let mut out = Vec::with_capacity(rs.len());
+        for (k, r) in rs.iter().enumerate() {
+            let mut y = vec![0f32; r.2];
+            // SAFETY: offset inside the carve.
+            self.download_bytes(&mut y, unsafe { base.add(c.at[2 + k]) })?;
+            out.push(Self::to_q32(&y)?);
+        }
+        Ok(out)
+    }
+
+    /// `ffn_q8act_prepared_into` (`src/engine/chart/ffn.rs:1609`) on the device: gate / up with the
+    /// exact SwiGLU and the hidden quant_act in one launch, down from that QuantAct in a second;
+    /// the hidden activation never leaves the device.  `codes` / `scales` are `quantize(x)`.
+    /// Refusals in the reference FFN's order: a projection's as `HipError::Matvec` (the caller's
+    /// `FfnError::Matvec`), the SwiGLU's as `HipError::Ffn`.
+    pub fn ffn_q8act(&mut self, gate: usize, up: usize, down: usize, codes: &[i8], scales: &[i64]) -> Result<Vec<i64>, HipError> {
+        let (g, u, d) = (self.resident(gate)?.t, self.resident(up)?.t, self.resident(down)?);
+        let (dt, n_embd, n_ff, d_type) = (d.t, d.n_out, d.n_in, d.ggml_type);
+        if codes.len() != n_embd || scales.len() != n_embd.div_ceil(32) {
+            return Err(HipError::Matvec(MatvecError::ShapeMismatch { x: codes.len(), n_in: n_embd }));
+        }
+        let c = Carve::new(&[codes.len(), 8 * scales.len(), 4 * n_embd, n_ff, 8 * n_ff.div_ceil(32)]);
+        let base = self.stage(c.total)?;
+        // SAFETY (pointer arithmetic): offsets inside the carve.
+        let p = |k: usize| unsafe { base.add(c.at[k]) };
+        self.upload_bytes(p(0), codes)?;
+        self.upload_bytes(p(1), scales)?;
+        // SAFETY: device pointers carved above; the tensors are resident on this context.
+        let mut st = unsafe {
+            (self.f.ffn_q8)(self.ctx, g, u, dt, p(0).cast::<i8>(), p(1).cast::<i64>(), p(2).cast::<f32>(), p(3).cast::<i8>(),
+                            p(4).cast::<i64>(), std::ptr::null_mut())
+        };
+        if st == AH_OK {
+            // SAFETY: the context is live.
+            st = unsafe { (self.f.sync)(self.ctx, std::ptr::null_mut()) };
+        }
+        self.check(st, CallShape { ggml_type: d_type, n_in: n_embd, x_len: codes.len(), need: 0, have: 0 }, "ah_ffn_q8_dev")?;
+        let mut y = vec![0f32; n_embd];
+        self.download_bytes(&mut y, p(2))?;
+        Self::to_q32(&y)
+    }
+
+    /// The column path's projection (`proj_cols`, `src/engine/step/cols.rs:485-575`; the grouped
+    /// form `gemm_q8_0_group`, `src/engine/kern/gemm.rs:818`): the resident projections `idxs` of
+    /// every column `qs[c] = (codes, scales)`, one operand pass and one MFMA launch per run of
+    /// projections, one Q32.32 vector per projection and column.  First refusal in
+    /// projection-then-column-then-row order.
+    pub fn matmat_group_q8act(&mut self, idxs: &[usize], qs: &[(&[i8], &[i64])]) -> Result<Vec<Vec<Vec<i64>>>, HipError> {
+        let mut ts: Vec<*const AhTensor> = Vec::with_capacity(idxs.len());
+        let mut outs: Vec<usize> = Vec::with_capacity(idxs.len());
+        let mut n_in = 0usize;
+        for &i in idxs {
+            let r = self.resident(i)?;
+            if n_in != 0 && r.n_in != n_in {
+                return Err(HipError::Backend { status: 21, what: "group n_in".into() });
+            }
+            n_in = r.n_in;
+            ts.push(r.t.cast_const());
+            outs.push(r.n_out);
+        }
+        let nb = n_in.div_ceil(32);
+        let k = qs.len();
+        let mut codes = Vec::with_capacity(k * n_in);
+        let mut scales = Vec::with_capacity(k * nb);
+        for (cc, ss) in qs {
+            if cc.len() != n_in {
+                return Err(HipError::Matvec(MatvecError::ShapeMismatch { x: cc.len(), n_in }));
+            }
+            if ss.len() != nb {
+                return Err(HipError::Backend { status: 21, what: "scales length".into() });
+            }
+            codes.extend_from_slice(cc);
+            scales.extend_from_slice(ss);
+        }
+        let mut sizes = vec![codes.len(), 8 * scales.len()];
+        sizes.extend(outs.iter().map(|&n| 4 * n * k));
+        let c = Carve::new(&sizes);
+        let base = self.stage(c.total)?;
+        // SAFETY (pointer arithmetic): offsets inside the carve.
+        let p = |j: usize| unsafe { base.add(c.at[j]) };
+        self.upload_bytes(p(0), &codes)?;
+        self.upload_bytes(p(1), &scales)?;
+        let ys: Vec<*mut f32> = (0..outs.len()).map(|j| p(2 + j).cast::<f32>()).collect();
+        // SAFETY: device pointers carved above; tensors resident; ts / ys live for the call.
+        let mut st = unsafe {
+            (self.f.gemm_group_q8)(self.ctx, ts.len(), ts.as_ptr(), p(0).cast::<i8>(), p(1).cast::<i64>(), k, ys.as_ptr(), std::ptr::null_mut())
+        };
+        if st == AH_OK {
+            // SAFETY: the context is live.
+            st = unsafe { (self.f.sync)(self.ctx, std::ptr::null_mut()) };
+        }
+        self.check(st, CallShape { ggml_type: 0, n_in, x_len: n_in, need: 0, have: 0 }, "ah_gemm_group_q8_dev")?;
+        let mut res = Vec::with_capacity(outs.len());
+        for (j, &n_out) in outs.iter().enumerate() {
+            let mut y = vec![0f32; n_out * k];
+            self.download_bytes(&mut y, p(2 + j))?;
+            res.push(y.chunks(n_out.max(1)).take(k).map(Self::to_q32).collect::<Result<Vec<_>, _>>()?);
+        }
+        Ok(res)
+    }
+
+    /// The column path's FFN (`src/engine/step/cols.rs:1026-1067`: the `[W_gate; W_up]` GEMM with
+    /// the SwiGLU, then the down `proj_cols`) over every column's QuantAct, the hidden columns kept
+    /// on the device; one Q32.32 vector of n_embd per column.
+    pub fn ffn_cols_q8act(&mut self, gate: usize, up: usize, down: usize, qs: &[(&[i8], &[i64])]) -> Result<Vec<Vec<i64>>, HipError> {
+        let (g, u, d) = (self.resident(gate)?.t, self.resident(up)?.t, self.resident(down)?);
+        let (dt, n_embd, n_ff) = (d.t, d.n_out, d.n_in);
+        let nb = n_embd.div_ceil(32);
+        let k = qs.len();
+        let mut codes = Vec::with_capacity(k * n_embd);
+        let mut scales = Vec::with_capacity(k * nb);
+        for (cc, ss) in qs {
+            if cc.len() != n_embd || ss.len() != nb {
+                return Err(HipError::Matvec(MatvecError::ShapeMismatch { x: cc.len(), n_in: n_embd }));
+            }
+            codes.extend_from_slice(cc);
+            scales.extend_from_slice(ss);
+        }
+        let c = Carve::new(&[codes.len(), 8 * scales.len(), 4 * n_embd * k, n_ff * k, 8 * n_ff.div_ceil(32) * k]);
+        let base = self.stage(c.total)?;
+        // SAFETY (pointer arithmetic): offsets inside the carve.
+        let p = |j: usize| unsafe { base.add(c.at[j]) };
+        self.upload_bytes(p(0), &codes)?;
+        self.upload_bytes(p(1), &scales)?;
+        // SAFETY: device pointers carved above; tensors resident on this context.
+        let mut st = unsafe {
+            (self.f.ffn_prefill_q8)(self.ctx, g, u, dt, p(0).cast::<i8>(), p(1).cast::<i64>(), k, p(2).cast::<f32>(),
+                                    p(3).cast::<i8>(), p(4).cast::<i64>(), std::ptr::null_mut())
+        };
+        if st == AH_OK {
+            // SAFETY: the context is live.
+            st = unsafe { (self.f.sync)(self.ctx, std::ptr::null_mut()) };
+        }
+        self.check(st, CallShape { ggml_type: 0, n_in: n_embd, x_len: n_embd, need: 0, have: 0 }, "ah_ffn_prefill_q8_dev")?;
+        let mut y = vec![0f32; n_embd * k];
+        self.download_bytes(&mut y, p(2))?;
+        y.chunks(n_embd.max(1)).take(k).map(Self::to_q32).collect()
+    }
+
     /// The device's measured MFMA-only rate (kind 0: int8 32x32x32, 1: f16 32x32x16), tera-ops/s:
     /// a diagnostic beside the engine's DP4A roofline probe, never on the projection path.
     pub fn probe_mfma_peak(&self, kind: u32) -> Result<f64, HipError> {
@@ -303,6 +613,9 @@ impl Drop for Hip {
         unsafe {
             for (_, r) in self.tensors.drain() {
                 (self.f.free_tensor)(self.ctx, r.t);
+            }
+            if !self.stage.d.is_null() {
+                (self.f.dev_free)(self.ctx, self.stage.d);
             }
             (self.f.destroy)(self.ctx);
             libc::dlclose(self.lib);

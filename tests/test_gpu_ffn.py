@@ -111,6 +111,19 @@ def test_ffn_vs_oracle(dev, gu_type, down_type, n_embd, n_ff):
     D.gemv_q8_dev(hc.data_ptr(), hs.data_ptr(), y2.data_ptr(), stream())
     assert dev.sync_status(stream()) == 0
     assert torch.equal(y, y2)
+    # from the input's QuantAct (ffn_q8act_prepared_into's `quantize(x)`): the same activation in
+    # the workgroups' LDS, so the same hidden QuantAct and output bit for bit
+    st, qc, qs = oracle.quant_act_f32(xs)
+    assert st == 0
+    dqc = torch.zeros(n_embd + 4, dtype=torch.int8, device="cuda")
+    dqc[:n_embd] = torch.from_numpy(qc).cuda()
+    dqs = torch.from_numpy(qs).cuda()
+    y3 = dbuf(n_embd)
+    hc3, hs3 = torch.zeros_like(hc), torch.zeros_like(hs)
+    chart.ffn_q8_dev(dev, G, U, D, dqc.data_ptr(), dqs.data_ptr(), y3.data_ptr(), hc3.data_ptr(), hs3.data_ptr(),
+                     stream())
+    assert dev.sync_status(stream()) == 0
+    assert torch.equal(hc3[:n_ff], hc[:n_ff]) and torch.equal(hs3, hs) and torch.equal(y3, y)
     for w in (G, U, D):
         w.free()
 

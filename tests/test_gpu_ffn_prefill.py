@@ -118,6 +118,17 @@ def run_case(dev, gu_type, down_type, n_embd, n_ff, n_tok, fused, spread=False, 
         D.gemm_q8_dev(hc.data_ptr(), hs.data_ptr(), n_tok, y2.data_ptr(), stream())
         assert dev.sync_status(stream()) == 0
         assert torch.equal(y, y2)
+        # from the tokens' QuantActs (the engine's own quantized columns): the same operand, so the
+        # same hidden QuantAct and outputs bit for bit
+        st, qc, qs = oracle.quant_act_f32_batch(xn)
+        assert st == 0
+        dqc, dqs = torch.from_numpy(qc).cuda(), torch.from_numpy(qs).cuda()
+        y3 = nan2d(n_tok, n_embd)
+        hc3, hs3 = torch.zeros_like(hc), torch.zeros_like(hs)
+        chart.ffn_prefill_q8_dev(dev, G, U, D, dqc.data_ptr(), dqs.data_ptr(), n_tok, y3.data_ptr(), hc3.data_ptr(),
+                                 hs3.data_ptr(), stream())
+        assert dev.sync_status(stream()) == 0
+        assert torch.equal(hc3, hc) and torch.equal(hs3, hs) and torch.equal(y3, y)
     finally:
         dev.set_ffn_prefill_form(chart.Device.FFN_AUTO)
         for w in (G, U, D):

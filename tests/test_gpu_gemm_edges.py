@@ -432,6 +432,16 @@ def test_k23_refusal_order_across_tokens(dev, t, design):
         for rows, want in (((xm, xt), 9), ((xt, xm), 8)):
             st, _ = gemm_f32(dev, w, np.stack(rows))
             assert st == want, (t, design, st)
+        # input refusals across tokens: token 0 out of range (InputRange, 11) at element 100, token 1
+        # non-finite (NonFinite, 10) at element 0 -- the first token's refusal
+        xr = np.full(n_in, 1.0, np.float32)
+        xr[100] = 2.0 ** 32
+        xn = np.full(n_in, 1.0, np.float32)
+        xn[0] = np.nan
+        for rows, want in (((xr, xn), 11), ((xn, xr), 10)):
+            assert [oracle.quant_act_f32(r)[0] for r in rows][0] == want
+            st, _ = gemm_f32(dev, w, np.stack(rows))
+            assert st == want, (t, design, st)
     finally:
         dev.set_gemm_design(t, 0)
         w.free()

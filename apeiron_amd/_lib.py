@@ -30,7 +30,7 @@ EXPORTS = [
     "ah_last_refusal_bits", "ah_gemm_f32_noalloc_dev", "ah_gemm_noalloc_scratch_bytes",
     "ah_set_gemm_design", "ah_ffn_gate_up_dev", "ah_ffn_dev", "ah_ffn_gate_up_prefill_dev",
     "ah_ffn_prefill_dev", "ah_set_ffn_prefill_form", "ah_swiglu_quant_dev", "ah_ffn_q8_dev",
-    "ah_ffn_prefill_q8_dev", "ah_dev_alloc", "ah_dev_free", "ah_copy_to_dev", "ah_copy_to_host",
+    "ah_ffn_prefill_q8_dev", "ah_dev_alloc", "ah_dev_free", "ah_copy_to_dev", "ah_copy_to_host", "ah_seq_set_spin_limit", "ah_ctx_scratch_bytes",
     "ah_seq_create", "ah_seq_run", "ah_seq_sync_status", "ah_seq_free", "ah_seq_info",
 ]
 
@@ -92,6 +92,8 @@ def load() -> ctypes.CDLL:
         "ah_dev_free": (I32, [P, P]),
         "ah_copy_to_dev": (I32, [P, P, P, S, P]),
         "ah_copy_to_host": (I32, [P, P, P, S, P]),
+        "ah_seq_set_spin_limit": (I32, [P, U32]),
+        "ah_ctx_scratch_bytes": (I32, [P, ctypes.POINTER(S)]),
         "ah_gemm_f32_noalloc_dev": (I32, [P, P, P, S, P, P]),
         "ah_gemm_noalloc_scratch_bytes": (I32, [ctypes.POINTER(S)]),
         "ah_set_gemm_design": (I32, [P, U32, U32]),

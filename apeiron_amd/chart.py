@@ -316,6 +316,10 @@ class Seq:
     def run(self, stream: int | None = None) -> None:
         _check(self.dev.lib.ah_seq_run(self.dev.h, self.h, stream), "seq_run")
 
+    def set_spin_limit(self, polls: int) -> None:
+        """Polls a grid-barrier wait makes before it gives up (0: the default)."""
+        _check(self.dev.lib.ah_seq_set_spin_limit(self.h, polls), "seq_set_spin_limit")
+
     def sync_status(self, stream: int | None = None) -> tuple[int, int]:
         """(status, stage) of the first refusal since the last call, in stage order."""
         stage = ctypes.c_uint32(0)

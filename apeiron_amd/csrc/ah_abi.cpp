@@ -118,6 +118,7 @@ struct ah_seq {
     unsigned *d_done = nullptr;   // per stage and group, a completion counter (128-byte lines)
     unsigned *d_runs = nullptr;   // per workgroup, completed launches
     unsigned long long *d_status = nullptr;
+    uint32_t spin_limit = kSeqSpinLimit;  // polls before a grid-barrier wait gives up
 };
 
 #define AH_HIP(ctx, call)                                                                       \
@@ -1633,9 +1634,15 @@ int32_t ah_seq_run(ah_ctx *ctx, const ah_seq *seq, void *stream) {
     a.status = seq->d_status;
     a.n_stages = seq->n_stages;
     a.act_bytes = seq->act_bytes;
-    a.spin_limit = 1u << 21;
+    a.spin_limit = seq->spin_limit;
     AH_HIP(ctx, hipSetDevice(ctx->device));
     AH_HIP(ctx, ah_launch_gemv_seq(seq->type, a, seq->grid, pick(ctx, stream)));
+    return AH_OK;
+}
+
+int32_t ah_seq_set_spin_limit(ah_seq *seq, uint32_t polls) {
+    if (!seq) return AH_ERR_INVALID_ARG;
+    seq->spin_limit = polls ? polls : kSeqSpinLimit;
     return AH_OK;
 }
 
@@ -1650,7 +1657,7 @@ int32_t ah_seq_sync_status(ah_ctx *ctx, const ah_seq *seq, void *stream, uint32_
         std::vector<unsigned long long> none(seq->n_stages, AH_ST_NONE);
         AH_HIP(ctx, hipMemcpy(seq->d_status, none.data(), none.size() * sizeof(unsigned long long), hipMemcpyHostToDevice));
         if (stage) *stage = s;
-        return (int32_t)(st[s] & 0xffu);
+        return st[s] == kSeqTimeoutKey ? AH_ERR_SEQ_TIMEOUT : (int32_t)(st[s] & 0xffu);
     }
     return AH_OK;
 }
@@ -1692,6 +1699,12 @@ int32_t ah_set_gemm_design(ah_ctx *ctx, uint32_t ggml_type, uint32_t design) {
     if (design == AH_GEMM_DESIGN_F16_TILE && ggml_type != AH_GGML_Q4_K && !ah_k23((int)ggml_type))
         return AH_ERR_UNSUPPORTED_QUANT;
     ctx->design[ggml_type] = design;
+    return AH_OK;
+}
+
+int32_t ah_ctx_scratch_bytes(const ah_ctx *ctx, size_t *bytes) {
+    if (!ctx || !bytes) return AH_ERR_INVALID_ARG;
+    *bytes = ctx->scratch_bytes;
     return AH_OK;
 }
 

@@ -1540,7 +1540,7 @@ AH_DEV void seq_wait(const SeqArgs &a, uint32_t sp, uint32_t r, unsigned long lo
         const unsigned v = lane < ngrp ? __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
         if (__builtin_amdgcn_ballot_w64(v < need) == 0) break;
         if (++polls >= a.spin_limit) {  // every later wait of this launch is skipped
-            if (lane == 0) ah_record(st, AH_ERR_SEQ_TIMEOUT);
+            if (lane == 0) ah_record(st, kSeqTimeoutKey);
             broken = true;
             break;
         }

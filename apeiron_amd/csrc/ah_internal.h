@@ -312,6 +312,13 @@ struct SeqArgs {
     uint32_t spin_limit;           // polls before a wait gives up (AH_ERR_SEQ_TIMEOUT)
 };
 
+// Polls of a persistent sequence's grid-barrier wait before it gives up (about 0.1 s of s_sleep).
+constexpr uint32_t kSeqSpinLimit = 1u << 21;
+// A wait that gave up records this key, below every refusal key (those hold a status code >= 1 in
+// their low byte after an index), so the stage reports AH_ERR_SEQ_TIMEOUT ahead of what its
+// workgroups then computed from inputs that were not ready.
+constexpr unsigned long long kSeqTimeoutKey = 0ull;
+
 struct QuantArgs {
     const void *x;         // f32 or int64 [n_tok][n_in]
     int8_t *codes;         // [n_tok][n_in]

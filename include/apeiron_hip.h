@@ -273,6 +273,12 @@ int32_t ah_seq_run(ah_ctx *ctx, const ah_seq *seq, void *stream);
  * AH_ERR_SEQ_TIMEOUT: a grid barrier waited past its limit (the run's outputs are not valid). */
 int32_t ah_seq_sync_status(ah_ctx *ctx, const ah_seq *seq, void *stream, uint32_t *stage);
 int32_t ah_seq_free(ah_ctx *ctx, ah_seq *seq);
+/* Polls a grid-barrier wait of this sequence makes before it gives up (0: the default, 2^21, about
+ * 0.1 s).  A wait that gives up records AH_ERR_SEQ_TIMEOUT at its stage and every later wait of
+ * that launch is skipped, so every workgroup still runs to the end and signals each of its
+ * stages: the barrier counters stay consistent and the next run is a whole run again.  No
+ * counterpart in the reference; for tests of that path. */
+int32_t ah_seq_set_spin_limit(ah_seq *seq, uint32_t polls);
 /* The sequence's resident grid (workgroups of 512 threads) and its per-workgroup activation LDS. */
 int32_t ah_seq_info(const ah_seq *seq, uint32_t *grid, uint32_t *act_bytes);
 
@@ -297,6 +303,9 @@ int32_t ah_gemm_f32_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, size_
 int32_t ah_gemm_f32_noalloc_dev(ah_ctx *ctx, const ah_tensor *w, const float *d_x, size_t n_tok,
                                 float *d_y, void *stream);
 int32_t ah_gemm_noalloc_scratch_bytes(size_t *bytes);
+/* Bytes of device scratch the context holds (grown on demand by the allocating GEMM forms; 0 until
+ * one of them runs): lets a caller check that a sequence of calls allocated nothing. */
+int32_t ah_ctx_scratch_bytes(const ah_ctx *ctx, size_t *bytes);
 /* Same from pre-quantized codes[n_tok][n_in] + scales[n_tok][ceil(n_in/32)]. */
 int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
                        const int64_t *d_scales, size_t n_tok, float *d_y, void *stream);

@@ -254,3 +254,37 @@ def test_seq_config4_token_vs_oracle(dev):
     for L, *_ in checks:
         for v in L.values():
             v[4].free()
+
+
+def test_seq_timeout_then_whole_run(dev):
+    """A grid-barrier wait that gives up (a one-poll limit set from the host) reports
+    AH_ERR_SEQ_TIMEOUT at a waiting stage and every workgroup still finishes the launch; the next
+    runs with the default limit are whole runs again, equal to separate launches bit for bit."""
+    rng = synth.rng_for(9, 7)
+    shapes = [(Q4_K, 8960, 1536), (Q6_K, 1536, 8960), (Q8_0, 640, 1536), (Q4_K, 256, 640)]
+    W = [dev.upload(t, small_payload(t, rng, n_out, n_in, 1.0 / 16), n_out, n_in) for t, n_out, n_in in shapes]
+    x0 = torch.from_numpy(synth.activations(rng, 1536)).cuda()
+    ys = [dbuf(n_out) for _, n_out, _ in shapes]
+    inputs = [x0] + ys[:-1]
+    seq = chart.Seq(dev, [("gemv", [(w, x.data_ptr(), y.data_ptr())]) for w, x, y in zip(W, inputs, ys)])
+    ref = [dbuf(n_out) for _, n_out, _ in shapes]
+    inp = x0
+    for w, y in zip(W, ref):
+        w.gemv_f32_dev(inp.data_ptr(), y.data_ptr(), stream())
+        inp = y
+    assert dev.sync_status(stream()) == 0
+    seq.set_spin_limit(1)
+    seq.run(stream())
+    st, stage = seq.sync_status(stream())
+    assert st == 25 and 1 <= stage < len(shapes), (st, stage)
+    seq.set_spin_limit(0)
+    for run in range(2):
+        for y in ys:
+            y.fill_(float("nan"))
+        seq.run(stream())
+        assert seq.sync_status(stream()) == (0, 0)
+        for i, (y, r) in enumerate(zip(ys, ref)):
+            assert torch.equal(y, r), (run, i)
+    seq.free()
+    for w in W:
+        w.free()

@@ -80,3 +80,51 @@ def test_noalloc_gemm_q2_k_q3_k_route(dev, t):
         y2 = run(dev, L.ah_gemm_f32_noalloc_dev, w, x)
         assert torch.isfinite(y1).all() and torch.equal(y1, y2)
         w.free()
+
+
+def test_noalloc_allocates_nothing(dev):
+    """On a context that has never run an allocating GEMM: the no-alloc entry point leaves the
+    device's free memory and the context's scratch exactly as they were, on the MFMA route (Q4_K),
+    the dequantize-once tiles (Q3_K) and the per-token GEMV route (Q3_K, AH_GEMM_DESIGN_F16)."""
+    L = dev.lib
+    cases = [(12, 1536, 8960, 512, 0), (11, 896, 1536, 128, 0), (11, 300, 896, 9, 1)]
+    # the kernels' code is loaded on first use: warm every route on the module's context first
+    ws = {}
+    for t, n_out, n_in, n_tok, design in cases:
+        rng = synth.rng_for(13, t * 10 + design)
+        raw = synth.payload(t, rng, n_out, n_in)
+        x = torch.from_numpy(synth.activations(rng, n_in, n_tok).reshape(n_tok, n_in)).cuda()
+        dev.set_gemm_design(t, design)
+        w = dev.upload(t, raw, n_out, n_in)
+        y_ref = run(dev, L.ah_gemm_f32_noalloc_dev, w, x)
+        dev.set_gemm_design(t, 0)
+        w.free()
+        ws[(t, design)] = (raw, x, y_ref)
+    fresh = chart.Device(0)
+    try:
+        W = {k: fresh.upload(k[0], ws[k][0], n_out, n_in) for (t, n_out, n_in, _, design) in cases
+             for k in [(t, design)]}
+        ys = {k: torch.empty((ws[k][1].shape[0], W[k].n_out), dtype=torch.float32, device="cuda") for k in W}
+        probe = torch.zeros(W[(11, 1)].n_out, dtype=torch.float32, device="cuda")
+        W[(11, 1)].gemv_f32_dev(ws[(11, 1)][1].data_ptr(), probe.data_ptr(), None)  # the stream's first launch
+        assert fresh.sync_status(None) == 0
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        sts = []
+        for (t, design), w in W.items():
+            fresh.set_gemm_design(t, design)
+            x = ws[(t, design)][1]
+            st = L.ah_gemm_f32_noalloc_dev(fresh.h, w.h, x.data_ptr(), x.shape[0], ys[(t, design)].data_ptr(), None)
+            sts.append((st, fresh.sync_status(None)))
+        torch.cuda.synchronize()
+        free1 = torch.cuda.mem_get_info()[0]  # before any torch work that could grow its cache
+        assert free1 == free0, (free0, free1)
+        assert all(s == (0, 0) for s in sts), sts
+        for k in W:
+            assert torch.equal(ys[k], ws[k][2]), k
+        held = ctypes.c_size_t(1)
+        assert L.ah_ctx_scratch_bytes(fresh.h, ctypes.byref(held)) == 0 and held.value == 0
+        for w in W.values():
+            w.free()
+    finally:
+        fresh.close()

@@ -1461,7 +1461,7 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
 // Lane g of wave 0 polls group g's counter, so one load instruction checks every group; polls are
 // bounded (past spin_limit the stage records AH_ERR_SEQ_TIMEOUT and waits no more in this launch).
 // A workgroup's run number is its own device counter, read at start and bumped at the end.  The
-// grid is launched cooperatively, which guarantees that every workgroup is resident.
+// grid is at most what the device holds at once (see ah_launch_gemv_seq).
 
 // The SwiGLU stage: the hidden activation's 32-blocks are dealt to the workgroups, 16 blocks per
 // round (one element per thread): gate and up from f32 to Q32.32 (to_q32), h = swiglu into LDS,
@@ -1814,15 +1814,21 @@ int ah_gemv_seq_occupancy(uint32_t type, size_t act_bytes) {
     return n;
 }
 
-// One cooperative launch runs the whole sequence: every workgroup is resident, which the grid
-// barriers between stages require (the launch fails rather than run a grid that does not fit).
+// One launch runs the whole sequence, its grid at most the workgroups the device holds at once
+// (ah_gemv_seq_occupancy per CU), so on a device the launch has to itself every workgroup is
+// resident, as the grid barriers between stages need.  An ordinary launch, not a cooperative one:
+// it measured 2% faster on the configs[4] token (817 against 835 us), and rocprofv3's kernel trace
+// of a process that made cooperative launches ended in a segmentation fault at exit, before it
+// wrote its results, while the same trace with ordinary launches completes.  Should other work
+// hold CUs so that some workgroups start late, the waits are bounded: the run then reports
+// AH_ERR_SEQ_TIMEOUT instead of hanging.
 hipError_t ah_launch_gemv_seq(uint32_t type, const SeqArgs &a, uint32_t grid, hipStream_t stream) {
     const void *f = seq_fn(type);
     if (!f) return hipErrorInvalidValue;
     SeqArgs arg = a;
     void *args[] = {&arg};
-    return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kSThreads), args,
-                                      (unsigned)(a.act_bytes + ah_gemv_stream_slot_bytes()), stream);
+    return hipLaunchKernel(f, dim3(grid), dim3(kSThreads), args,
+                           (unsigned)(a.act_bytes + ah_gemv_stream_slot_bytes()), stream);
 }
 
 // Workgroups of the streaming kernel that fit one CU at once with `lds` bytes of LDS each

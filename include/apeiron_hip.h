@@ -266,7 +266,10 @@ typedef struct ah_seq_stage {
 } ah_seq_stage;
 /* Plans the sequence (every device pointer is fixed here) and uploads its tables. */
 int32_t ah_seq_create(ah_ctx *ctx, size_t n_stages, const ah_seq_stage *stages, ah_seq **out);
-/* Enqueues the whole sequence as one cooperative launch on `stream`. */
+/* Enqueues the whole sequence as one launch on `stream`; its grid is what the device holds at
+ * once, so the stages' grid barriers need the device to itself for the run (other work holding
+ * CUs delays some workgroups: the bounded waits then give up and the run reports
+ * AH_ERR_SEQ_TIMEOUT). */
 int32_t ah_seq_run(ah_ctx *ctx, const ah_seq *seq, void *stream);
 /* Synchronizes `stream`, then returns (and clears) the first refusal of the sequence's last runs
  * in stage order, as ah_sync_status does per call; *stage (optional) receives its stage index.

@@ -140,7 +140,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--cpu-threads", type=int, default=8)
     ap.add_argument("--no-seq", action="store_true",
-                    help="skip the persistent (cooperative-launch) token forms of the decode extras")
+                    help="skip the persistent (one-launch) token forms of the decode extras")
     ap.add_argument("--only", choices=["decode", "gemm", "gemm3", "config1", "heads", "families", "copy"],
                     default=None)
     args = ap.parse_args()

@@ -644,10 +644,12 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, ui
             if (2 * g + 1 < nb16) dots16[2 * g + 1] = Dhi;  // ragged row ends on a 16-group
         }
         const uint32_t sw = scw[t >> 1] >> (16 * (t & 1));
-        const float sclo = (float)(int)(int8_t)(sw & 0xffu), schi = (float)(int)(int8_t)((sw >> 8) & 0xffu);
-        acc += A.fsc[g] * fd * (sclo * (float)Dlo + schi * (float)Dhi);
+        // the block's two scale-weighted group dots as one integer (|sc * D| < 2^23, 24-bit
+        // multiplies); d multiplies once per unit
+        const int32_t I = __mul24((int)(int8_t)(sw & 0xffu), Dlo) + __mul24((int)(int8_t)((sw >> 8) & 0xffu), Dhi);
+        acc = __builtin_fmaf(A.fsc[g], (float)I, acc);
     }
-    return acc;
+    return fd * acc;
 }
 
 // Q2_K and Q3_K (format/quant.rs:308-476) in units of one half n of super-block s (128 elements,
@@ -692,7 +694,11 @@ AH_DEV float unit_k23(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, u
         hn[i] = Q3 ? V(i) >> (4 * n) : 0u;  // this half's four hmask bits of each byte, at bits 0-3
     }
     const uint32_t nb16 = (n_in + 15) / 16;
-    float acc = 0.0f;
+    // The two 16-groups of a 32-block share its activation scale: their scale-weighted dots (and
+    // Q2_K's min terms) are summed as integers, exactly (|sc * D| < 2^18 with 24-bit multiplies),
+    // and each 32-block adds one f32 term per sum; d and dmin multiply once per unit.
+    float aI = 0.0f, aM = 0.0f;
+    int32_t Ip = 0, Mp = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int r = j >> 1, pl = j & 1;
@@ -721,13 +727,22 @@ AH_DEV float unit_k23(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, u
         if constexpr (Q3) {
             D -= 4 * X;
             if (DOTS && dots16) dots16[g] = D;
-            acc += A.fsc[g >> 1] * (fd * ((float)((int)sb - 32) * (float)D));
+            Ip += __mul24((int)sb - 32, D);
         } else {
             if (DOTS && dots16) dots16[g] = D;
-            acc += A.fsc[g >> 1] * ((fd * (float)(sb & 15u)) * (float)D - (fdm * (float)(sb >> 4)) * (float)X);
+            Ip += __mul24((int)(sb & 15u), D);
+            Mp += __mul24((int)(sb >> 4), X);
+        }
+        // the 32-block's end (or, in the debug form, the ragged row's last group)
+        if ((j & 1) || (DOTS && g + 1 >= nb16)) {
+            const float f = A.fsc[g >> 1];
+            aI = __builtin_fmaf(f, (float)Ip, aI);
+            if constexpr (!Q3) aM = __builtin_fmaf(f, (float)Mp, aM);
+            Ip = 0;
+            Mp = 0;
         }
     }
-    return acc;
+    return Q3 ? fd * aI : fd * aI - fdm * aM;
 }
 
 // Q4_K parts use pair units where the host chose them for a small projection (units = ceil(K/64)

@@ -182,7 +182,7 @@ def test_act_code_f32_fast_block_matches_quant_act():
     assert n_clear >= 4  # and the clear below half a unit some code at each sampled e
 
 
-# ---- the fused FFN's exp in i64 (fx_exp in ah_gemv.hip) -----------------------------------------
+# ---- the fused FFN's exp in i64 (fx_exp in ah_swiglu.h) -------------------------------------------
 
 _EXP_C = [852176, 5965232, 35791394, 178956971, 715827883, 2147483648, 4294967296, 4294967296]
 I64_MAX, I64_MIN = (1 << 63) - 1, -(1 << 63)
@@ -236,3 +236,46 @@ def test_fx_exp_i64_equals_fixed_exp():
     xs += [int(v) for v in rng.integers(-16 * one, 21 * one, size=20000, dtype=np.int64)]
     for x in xs:
         assert fx_exp_i64(x) == tuple(oracle.fixed_exp(x)), x
+
+
+def silu_one_step(v: int):
+    """The device's silu (silu_fx in ah_swiglu.h) step for step: the f64 estimate of the rounded
+    quotient, truncated, then ONE correction against the exact remainder; also returns how far the
+    truncated estimate was from the exact quotient."""
+    one = 1 << 32
+    if v >= 16 * one:
+        return v, 0
+    if v <= -21 * one:
+        return 0, 0
+    st, e = fx_exp_i64(-v)
+    assert st == 0
+    den = one + e
+    mag = -v if v < 0 else v
+    n2 = mag * one + (den >> 1)
+    nd = float(n2 >> 32) * 4294967296.0 + float(n2 & 0xFFFFFFFF)  # each term exact; one rounding
+    q0 = int(nd / float(den))                                       # truncation toward zero
+    rem = n2 - q0 * den
+    q = q0 + (-1 if rem < 0 else 1 if rem >= den else 0)
+    return (-q if v < 0 else q), q0 - n2 // den
+
+
+def test_silu_single_correction_is_exact():
+    """One correction step after the f64 estimate gives the exact rounded quotient (the oracle's
+    i128 division, pinned by the reference's values in test_oracle_ffn.py): over the saturation
+    bounds, the exp range reduction's half-way points, small and large magnitudes and a random
+    sweep, the corrected quotient equals the oracle's and the estimate was never off by more
+    than one."""
+    one = 1 << 32
+    vs = [16 * one - 1, 16 * one, -21 * one + 1, -21 * one, 0, 1, -1, one, -one, 15 * one, -20 * one]
+    ln2 = 2977044472
+    for k in range(-24, 32):
+        mid = (2 * k + 1) * ln2 // 2
+        vs += [-(mid + d) for d in range(-2, 3)]
+    for e in range(0, 36):
+        vs += [1 << e, -(1 << e)]
+    rng = np.random.default_rng(0x5117)
+    vs += [int(v) for v in rng.integers(-21 * one, 16 * one, size=50000, dtype=np.int64)]
+    for v in vs:
+        got, off = silu_one_step(v)
+        st, ref = oracle.silu_fixed(v)
+        assert st == 0 and got == ref and abs(off) <= 1, (v, off)

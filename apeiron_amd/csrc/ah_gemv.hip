@@ -161,10 +161,13 @@ AH_DEV QuadIn quad_load_row(const ActRsrc &r, uint32_t src, uint32_t n_in, uint3
     in.take = n_in > k0 ? (n_in - k0 < 8 ? n_in - k0 : 8) : 0;
     const bool f = src == AH_SRC_F32;
     const uint32_t base = f ? 4 * k0 : k0;
-    const uint32_t oob = kActOob - 16 * (threadIdx.x & 3);  // past any activation resource
+    // only the source's own words are requested: an out-of-range load still takes the vector
+    // memory path (a decode token took 2% longer with one per row and the empty passes' below)
     const u32x4 l0 = ah_ld128p<CP>(r.x, base);
-    const u32x4 l1 = ah_ld128p<CP>(r.x, f ? base + 16 : oob);
-    const u32x2 sc = ah_ld64<CP>(r.s, f ? oob : 8 * b);
+    u32x4 l1 = {0u, 0u, 0u, 0u};
+    u32x2 sc = {0u, 0u};
+    if (f) l1 = ah_ld128p<CP>(r.x, base + 16);
+    else sc = ah_ld64<CP>(r.s, 8 * b);
     in.w[0] = l0.x; in.w[1] = l0.y; in.w[2] = l0.z; in.w[3] = l0.w;
     in.w[4] = l1.x; in.w[5] = l1.y; in.w[6] = l1.z; in.w[7] = l1.w;
 #pragma unroll
@@ -1343,8 +1346,10 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
         const uint32_t nbp = kpad / 32;
         const uint32_t passes = (nbp + QB - 1) / QB;
         const ActRsrc xr = act_rsrc(P.x, P.scales, P.src, P.n_in);
-        const QuadIn x0 = quad_load_row(xr, P.src, P.n_in, threadIdx.x / 4);
-        const QuadIn x1 = quad_load_row(xr, P.src, P.n_in, QB + threadIdx.x / 4);  // past the row: zeros
+        // (a wave whose blocks of a pass all lie past the activation requests nothing for it)
+        QuadIn x0 = {}, x1 = {};
+        if (wave * 16 < nbp) x0 = quad_load_row(xr, P.src, P.n_in, threadIdx.x / 4);
+        if (QB + wave * 16 < nbp) x1 = quad_load_row(xr, P.src, P.n_in, QB + threadIdx.x / 4);
         ah_lds_barrier();
         load_tile(0);
         // Pass p quantizes blocks p*QB + tid/4.  A wave whose 16 blocks of a pass all lie past the
@@ -1355,7 +1360,8 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
         const unsigned long long kb = (unsigned long long)P.key_tok * P.n_in;
         QuadOut o0 = {};
         if (w0) o0 = quad_quant(x0, P.src, b0, status, kb);
-        const QuadIn x2 = quad_load_row(xr, P.src, P.n_in, 2 * QB + b0);  // past the row: zeros
+        QuadIn x2 = {};
+        if (2 * QB + wave * 16 < nbp) x2 = quad_load_row(xr, P.src, P.n_in, 2 * QB + b0);
         if (w0 && b0 < nbp) store_quad(A, b0, o0);
         if (passes > 1 && QB + wave * 16 < nbp) {
             const QuadOut o = quad_quant(x1, P.src, QB + b0, status, kb);

@@ -84,7 +84,8 @@ struct QuadOut {
 
 // The raw inputs of one quad lane for one 32-block, loaded apart from the arithmetic so that a
 // kernel can issue these loads ahead of its weight stream: 8 f32 bit patterns (w[0..7]), 8 Q32.32
-// values (lo/hi in w[2i], w[2i+1]), or 8 int8 codes (w[0..1]) with the block scale (w[2..3]).
+// values (lo/hi in w[2i], w[2i+1]), or 8 int8 codes (w[0..1]) with the block scale (s0, s1).
+// Words a source does not use may hold other bytes; its consumer never reads them.
 struct QuadIn {
     uint32_t w[16];
     uint32_t s0, s1;  // codes: the block scale
@@ -135,14 +136,14 @@ AH_DEV QuadIn quad_load(const void *x, const int64_t *scales, uint32_t src, uint
 
 // The same inputs for one activation row of a GEMV read through buffer resources: elements past
 // n_in lie past the resource's range and read as zero.  A GEMV's activation is f32 or codes (the
-// Q32.32 form is the standalone quantizer's alone, which reads through quad_load), and either
-// source issues the same three buffer loads (offsets picked by `src`; the Q32 words stay zero) and
-// nothing here touches the loaded words, so there is no branch and no wait: the loads return in
-// issue order, and quad_quant, which waits for them, never waits for a load issued after them.
-// An unused load's offset lies out of range by a lane-dependent amount: with one constant offset
-// for the whole wave the compiler would take its (zero) result for a wave-uniform value and move
-// it to a scalar register, which waits for the load.  Codes are read a whole dword at a time (the
-// base must be 4-byte aligned); quad_quant clears bytes past n_in.
+// Q32.32 form is the standalone quantizer's alone, which reads through quad_load).  Either source
+// issues the same two 16-byte loads: the first 16 bytes of the lane's elements, then (resource
+// and offset picked by `src` with scalar selects) f32 elements 4-7 or the codes' block scale with
+// the next block's.  Their words land in w[4..7] and s0/s1 alike and each consumer reads only its
+// own, so nothing here touches the loaded words: no branch, no copy and no wait (a branch between
+// the sources' loads had made the compiler wait for the codes' scale before the weight loads went
+// out), and no load out of range (those still take the vector memory path).  Codes are read a
+// whole dword at a time (the base must be 4-byte aligned); quad_quant clears bytes past n_in.
 struct ActRsrc {
     __amdgpu_buffer_rsrc_t x, s;
 };
@@ -161,19 +162,14 @@ AH_DEV QuadIn quad_load_row(const ActRsrc &r, uint32_t src, uint32_t n_in, uint3
     in.take = n_in > k0 ? (n_in - k0 < 8 ? n_in - k0 : 8) : 0;
     const bool f = src == AH_SRC_F32;
     const uint32_t base = f ? 4 * k0 : k0;
-    // only the source's own words are requested: an out-of-range load still takes the vector
-    // memory path (a decode token took 2% longer with one per row and the empty passes' below)
     const u32x4 l0 = ah_ld128p<CP>(r.x, base);
-    u32x4 l1 = {0u, 0u, 0u, 0u};
-    u32x2 sc = {0u, 0u};
-    if (f) l1 = ah_ld128p<CP>(r.x, base + 16);
-    else sc = ah_ld64<CP>(r.s, 8 * b);
+    const u32x4 l1 = ah_ld128p<CP>(f ? r.x : r.s, f ? base + 16 : 8 * b);
     in.w[0] = l0.x; in.w[1] = l0.y; in.w[2] = l0.z; in.w[3] = l0.w;
     in.w[4] = l1.x; in.w[5] = l1.y; in.w[6] = l1.z; in.w[7] = l1.w;
 #pragma unroll
     for (int i = 8; i < 16; ++i) in.w[i] = 0u;
-    in.s0 = sc.x;
-    in.s1 = sc.y;
+    in.s0 = l1.x;
+    in.s1 = l1.y;
     return in;
 }
 
@@ -1346,7 +1342,8 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
         const uint32_t nbp = kpad / 32;
         const uint32_t passes = (nbp + QB - 1) / QB;
         const ActRsrc xr = act_rsrc(P.x, P.scales, P.src, P.n_in);
-        // (a wave whose blocks of a pass all lie past the activation requests nothing for it)
+        // (a wave whose blocks of a pass all lie past the activation requests nothing for it: the
+        // empty passes' out-of-range loads had cost a decode token 2%)
         QuadIn x0 = {}, x1 = {};
         if (wave * 16 < nbp) x0 = quad_load_row(xr, P.src, P.n_in, threadIdx.x / 4);
         if (QB + wave * 16 < nbp) x1 = quad_load_row(xr, P.src, P.n_in, QB + threadIdx.x / 4);

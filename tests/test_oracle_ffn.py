@@ -2,7 +2,9 @@
 
 * fixed_exp: the reference's own KATs and bounds (numeric/fixed_exp.rs zero_and_boundaries), its
   accuracy contract against exp on a grid (ACHIEVED_REL 1e-8 + 4 ulp on [-16, 21], the same
-  bound the reference's accuracy test asserts) and monotonicity;
+  bound the reference's accuracy test asserts), monotonicity, and the Horner loop's per-step
+  rounding: to nearest by its error against the exact rational polynomial, ties away from zero
+  on inputs where a step lands on a half (a floor, truncating or ties-to-even step fails them);
 * silu_fixed: the reference's KATs (engine/tests.rs:949-963), the closed form v / (1 + e^-v) to
   within the exp tolerance, the saturation bounds and odd-symmetry-breaking sign handling;
 * swiglu: the exact product rounding round_shift_32(silu * up) checked with Python big ints
@@ -102,3 +104,67 @@ def test_swiglu_quant_f32_composition():
     bad = gate.copy()
     bad[10] = np.inf
     assert oracle.swiglu_quant_f32(bad, up)[0] == 10
+
+
+def _horner_exact(r):
+    """exp's degree-7 Taylor polynomial at r / 2^32 in Q32.32, evaluated without rounding: the
+    coefficients are round(2^32 / j!) (the reference's table, numeric/fixed_exp.rs:68-84), each
+    Horner step acc * r / 2^32 + c exact in rationals."""
+    from fractions import Fraction
+    c = [round(Fraction(ONE, math.factorial(7 - i))) for i in range(8)]
+    h = Fraction(c[0])
+    for i in range(1, 8):
+        h = h * r / ONE + c[i]
+    return h, c
+
+
+def _horner_rounded(r, tie_away):
+    """The same evaluation with each step rounded to the nearest integer, ties away from zero or
+    to even: the two readings of 'round' whose difference the oracle must resolve."""
+    from fractions import Fraction
+    _, c = _horner_exact(0)
+    acc = c[0]
+    for i in range(1, 8):
+        p = Fraction(acc * r, ONE)
+        fl = p.numerator // p.denominator
+        frac = p - fl
+        if frac > Fraction(1, 2) or (frac == Fraction(1, 2) and (p > 0 if tie_away else fl % 2 == 1)):
+            fl += 1
+        acc = fl + c[i]
+    return acc
+
+
+def test_fixed_exp_horner_rounds_each_step_to_nearest():
+    """The per-step rounding of fixed_exp's Horner loop, pinned by its error against the exact
+    polynomial.  At k = 0 (|x| < ln2 / 2) the output is the Horner result itself.  Rounding each
+    of the 7 steps to nearest leaves |out - exact| <= 1/2 * sum_j |r|^j (|r| < 0.35 in units of
+    one, each earlier error shrunk by the later multiplications) with an error mean near 0; a
+    floor or truncating step errs by up to a whole unit per step, one-sided, and fails both."""
+    rng = np.random.default_rng(11)
+    half_ln2 = LN2_Q32 // 2
+    xs = [int(v) for v in rng.integers(-half_ln2 + 1, half_ln2, size=4000)]
+    xs += [1, -1, 2, -2, half_ln2 - 1, -half_ln2 + 1, 1 << 27, -(1 << 27)]
+    errs = []
+    for x in xs:
+        st, v = oracle.fixed_exp(x)
+        assert st == 0
+        exact, _ = _horner_exact(x)
+        t = abs(x) / ONE
+        bound = 0.5 * sum(t ** j for j in range(7)) + 1e-9
+        err = float(v - exact)
+        assert abs(err) <= bound, (x, err, bound)
+        errs.append(err)
+    assert abs(sum(errs) / len(errs)) < 0.05, sum(errs) / len(errs)
+
+
+def test_fixed_exp_horner_ties_away_from_zero():
+    """Inputs where some Horner step lands exactly on a half and the two tie rules then give
+    different outputs: the oracle takes ties away from zero, as the reference's round_div_2p32
+    does (numeric/fixed_exp.rs:68-84).  The inputs were found by searching multiples of 2^18
+    (positive) and 2^14 (negative; such ties that survive to the output are rare there) for a
+    difference between the two rules; the test re-derives that they differ."""
+    for x in (799539200, 805306368, 1375731712, -751026176):
+        away, even = _horner_rounded(x, True), _horner_rounded(x, False)
+        assert away != even, x
+        st, v = oracle.fixed_exp(x)
+        assert st == 0 and v == away, (x, v, away, even)

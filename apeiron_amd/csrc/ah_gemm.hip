@@ -31,6 +31,7 @@
 // pass per grouped call reduces in fixed order.
 #include "ah_internal.h"
 #include "ah_swiglu.h"
+#include "ah_units.h"
 
 namespace {
 
@@ -382,6 +383,162 @@ AH_DEV float exact_row(const uint8_t *row, const int8_t *xq, const int64_t *sc, 
     return acc;
 }
 
+// The exact path at speed: the flagged tokens of a workgroup tile through the streaming GEMV's
+// dot units (exact v_dot4 group dots folded in f32 with the token's own block scales, so no band
+// applies; the same arithmetic as a decode GEMV of that token).  The loop is uniform over the
+// workgroup: `fm` holds the tile's flagged tokens (bit tl) alike in every wave, and every wave
+// calls this.  Per token and per window of kWin 32-blocks of the split's K range, the
+// workgroup's threads stage the token's codes, block scales and code sums in LDS (`win`: the
+// MFMA operand ring or planes, free once every wave is past its loop) in the GEMV's layout,
+// shifted so the units index it by absolute block; then lane (j, h) of each wave takes row
+// row_w + 32 n + j, the two lane halves alternating units, reading the weights from the GGUF
+// rows in memory.  A unit whose reads could pass the tensor's end (the units read up to a dword
+// past their bytes; the tail of a caller-wrapped payload), or any unit of a payload whose start
+// is not 16-byte aligned, takes exact_row.  Partials (scaled == false) are stored in the reduction's units, divided by
+// the token scale.
+namespace xp {
+constexpr uint32_t kWin = 64;   // 32-blocks per staged window (2048 K; 3.2 KB of LDS per token)
+constexpr uint32_t kBatch = 8;  // flagged tokens staged at once, LDS permitting
+constexpr uint32_t kWinBytes = kWin * 32 + kWin * 32 / 16 + kWin * 4 + kWin * 4 + kWin * 2 * 4;
+// unit count per 32-block group of a family's GEMV unit, and the unit's bytes
+template <int TYPE> constexpr uint32_t unit_blocks() {
+    return ah_blk32(TYPE) ? 1u : TYPE == AH_GGML_Q4_K ? 8u : 4u;
+}
+template <int TYPE> constexpr uint32_t unit_bytes() {
+    return TYPE == AH_GGML_Q8_0 ? 34u : TYPE == AH_GGML_Q5_0 ? 22u : TYPE == AH_GGML_Q4_K ? 144u
+         : TYPE == AH_GGML_Q6_K ? 210u : TYPE == AH_GGML_Q2_K ? 84u : 110u;  // (super-block bytes)
+}
+// GEMV unit v of the row at byte `roff` of the tensor `w` (Q8_0 / Q5_0 blocks, Q4_K super-blocks,
+// Q6_K / Q2_K / Q3_K half super-blocks), read from global memory.  The units realign their words
+// from the byte offset itself, so `w` is passed with the row's offset: only `w` must be aligned
+// (16 bytes; Q4_K rows are multiples of 16).
+template <int TYPE>
+AH_DEV float unit(const uint8_t *w, uint32_t roff, uint32_t v, uint32_t n_in, const ActLds &A) {
+    if constexpr (TYPE == AH_GGML_Q8_0) return unit_q8<false>(w, roff + 34u * v, v, A, nullptr);
+    else if constexpr (TYPE == AH_GGML_Q5_0) return unit_q5<false>(w, roff + 22u * v, v, A, nullptr);
+    else if constexpr (TYPE == AH_GGML_Q4_K) return unit_q4<false>(w, roff + 144u * v, v, n_in, A, nullptr);
+    else if constexpr (TYPE == AH_GGML_Q6_K)
+        return unit_q6<false>(w, roff + 210u * (v >> 1), v >> 1, v & 1u, n_in, A, nullptr);
+    else return unit_k23<TYPE, false>(w, roff + unit_bytes<TYPE>() * (v >> 1), v >> 1, v & 1u, n_in, A, nullptr);
+}
+}  // namespace xp
+
+template <int TYPE, int NN>
+AH_DEV void exact_tokens(const GemmArgs &a, const GemmPartArgs &pa, uint8_t *win, uint32_t win_bytes, uint64_t fm0,
+                         uint64_t fm1, uint32_t tok_base, uint32_t row_w, uint32_t tok_lo, uint32_t tok_hi,
+                         float *ybase, bool scaled, uint32_t u_lo, uint32_t u_hi) {
+    const uint32_t lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+    const uint32_t nb32 = (a.n_in + 31) / 32;
+    // the split's K range in 32-blocks, and in GEMV units (halves for Q6_K / Q2_K / Q3_K)
+    constexpr bool kHalves = !ah_blk32(TYPE) && TYPE != AH_GGML_Q4_K;
+    const uint32_t b_lo = ah_blk32(TYPE) ? u_lo : 8u * u_lo;
+    const uint32_t b_hi = ah_blk32(TYPE) ? (u_hi < nb32 ? u_hi : nb32) : 8u * u_hi;
+    const uint32_t v_lo = kHalves ? 2u * u_lo : u_lo, v_hi = kHalves ? 2u * u_hi : (ah_blk32(TYPE) ? b_hi : u_hi);
+    constexpr uint32_t kVB = kHalves ? 4u : xp::unit_blocks<TYPE>();  // 32-blocks per GEMV unit
+    const bool aligned = (reinterpret_cast<uintptr_t>(pa.w) & 15u) == 0;
+    // tokens per batch: each staged in a window of its own, so that one weight unit read from
+    // memory serves every token of the batch (the later reads hit the cache); the lanes' sums per
+    // token and row block sit after the windows, one slot per lane (no lane reads another's)
+    const uint32_t waves = blockDim.x / 64, wave = threadIdx.x / 64;
+    const uint32_t acc_bytes = waves * xp::kBatch * NN * 256u;
+    uint32_t nmax = (win_bytes - acc_bytes) / xp::kWinBytes;
+    nmax = nmax < xp::kBatch ? nmax : xp::kBatch;
+    float *const vacc = reinterpret_cast<float *>(win + win_bytes - acc_bytes) + wave * xp::kBatch * NN * 64u + lane;
+    auto vslot = [&](uint32_t i, int n) -> float & { return vacc[(i * NN + (uint32_t)n) * 64u]; };
+    uint64_t rest0 = fm0, rest1 = fm1;
+    while ((rest0 | rest1) != 0ull) {
+        // the batch: up to nmax of the remaining tokens, lowest first (masks over the tile)
+        uint64_t bm0 = 0ull, bm1 = 0ull;
+        uint32_t nt = 0;
+        while (nt < nmax && (rest0 | rest1) != 0ull) {
+            if (rest0) {
+                bm0 |= rest0 & (0ull - rest0);
+                rest0 &= rest0 - 1;
+            } else {
+                bm1 |= rest1 & (0ull - rest1);
+                rest1 &= rest1 - 1;
+            }
+            ++nt;
+        }
+        // the batch's tokens in order: (tl, i) for i = 0, 1, ... (i picks the token's window)
+        auto for_tokens = [&](auto &&fn) {
+            uint32_t i = 0;
+            for (uint64_t m = bm0; m; m &= m - 1) fn((uint32_t)__builtin_ctzll(m), i++);
+            for (uint64_t m = bm1; m; m &= m - 1) fn(64u + (uint32_t)__builtin_ctzll(m), i++);
+        };
+        for_tokens([&](uint32_t, uint32_t i) {
+#pragma unroll
+            for (int n = 0; n < NN; ++n) vslot(i, n) = 0.0f;
+        });
+        auto act = [&](uint32_t i, uint32_t g0) {  // token i's window, indexed by absolute block
+            uint8_t *wb = win + i * xp::kWinBytes;
+            ActLds A;
+            A.codes = reinterpret_cast<int8_t *>(wb) - pad_k(32u * g0);
+            A.fsc = reinterpret_cast<float *>(wb + codes_bytes(32u * xp::kWin)) - g0;
+            A.xs32 = reinterpret_cast<int32_t *>(A.fsc + g0 + xp::kWin) - g0;
+            A.xs16 = reinterpret_cast<int32_t *>(A.xs32 + g0 + xp::kWin) - 2u * g0;
+            return A;
+        };
+        for (uint32_t g0 = b_lo & ~7u; g0 < b_hi; g0 += xp::kWin) {
+            ah_lds_barrier();  // every wave is past its loop (first window) or the last window
+            for_tokens([&](uint32_t tl, uint32_t i) {
+                const size_t t = (size_t)tok_base + tl;
+                const ActLds A = act(i, g0);
+                // (whole quads: blockDim is a multiple of 64, and so is 4 kWin)
+                for (uint32_t q = threadIdx.x; q < 4u * xp::kWin; q += blockDim.x) {
+                    const uint32_t b = g0 + q / 4;
+                    const QuadOut o = quad_quant(quad_load(a.fcodes + t * a.n_in, a.fscales + t * nb32, AH_SRC_CODES,
+                                                           a.n_in, 0, b, b < nb32),
+                                                 AH_SRC_CODES, b, nullptr, 0);
+                    store_quad(A, b, o);
+                }
+            });
+            ah_lds_barrier();
+            const uint32_t w_lo = v_lo > g0 / kVB ? v_lo : g0 / kVB;
+            const uint32_t w_end = (g0 + xp::kWin) / kVB, w_hi = v_hi < w_end ? v_hi : w_end;
+#pragma unroll
+            for (int n = 0; n < NN; ++n) {
+                const uint32_t row = row_w + 32u * n + j;
+                if (row >= pa.n_out) continue;
+                const uint32_t roff = row * pa.row_bytes;
+                for (uint32_t u = w_lo + h; u < w_hi; u += 2) {
+                    const uint32_t sb = kHalves ? u >> 1 : u;  // the unit's block / super-block
+                    const size_t end = (size_t)roff + (size_t)xp::unit_bytes<TYPE>() * (sb + 1) + 16u;
+                    const bool fast = aligned && end <= pa.w_bytes;
+                    for_tokens([&](uint32_t tl, uint32_t i) {
+                        if (tl < tok_lo || tl >= tok_hi) return;  // another wave's tokens
+                        float add = 0.0f;
+                        if (fast) add = xp::unit<TYPE>(pa.w, roff, u, a.n_in, act(i, g0));
+                        else if (!kHalves || (u & 1u) == 0) {  // a half's super-block once, whole
+                            const size_t t = (size_t)tok_base + tl;
+                            add = exact_row<TYPE>(pa.w + roff, a.fcodes + t * a.n_in, a.fscales + t * nb32, a.n_in,
+                                                  sb, sb + 1, 0);
+                        }
+                        vslot(i, n) += add;
+                    });
+                }
+            }
+        }
+        for_tokens([&](uint32_t tl, uint32_t i) {
+            if (tl < tok_lo || tl >= tok_hi) return;
+            const size_t t = (size_t)tok_base + tl;
+            const float ts = ah_ts_value(__builtin_bit_cast(uint32_t, a.tok_scale[t]));
+#pragma unroll
+            for (int n = 0; n < NN; ++n) {
+                const float vi = vslot(i, n);
+                const uint32_t row = row_w + 32u * n + j;
+                const float sum = vi + __shfl_xor(vi, 32, 64);
+                if (h == 0 && row < pa.n_out) {
+                    ybase[(size_t)(tl - tok_lo) * pa.n_out + row] = scaled ? sum : sum / ts;
+                    if (const uint32_t oc = scaled ? ah_out_code(sum) : 0u)
+                        ah_record(a.status, ah_out_key(pa.key0 + (uint64_t)t * pa.n_out + row, oc));
+                }
+            }
+        });
+    }
+}
+
+
 // The epilogue of both GEMM designs.  acc[m][n] holds the wave's sums in the 32x32 MFMA D layout
 // (token tiles m, 32-row tiles n from row_w); units [u_lo, u_hi) (Q8_0 blocks, K-quant
 // super-blocks) are the split's K range, which the exact path of flagged tokens recomputes.
@@ -390,7 +547,7 @@ AH_DEV __attribute__((always_inline)) void gemm_store(const GemmArgs &a, const G
                                                       const f32x16 (&acc)[NM][NN], uint32_t row_w,
                                                       const bool (&rl)[NN], const uint32_t (&rbase)[NN],
                                                       uint32_t tok0, uint32_t ntile, uint32_t split,
-                                                      uint32_t u_lo, uint32_t u_hi) {
+                                                      uint32_t u_lo, uint32_t u_hi, uint8_t *win, uint32_t win_bytes) {
     const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
     // D layout of a 32x32 MFMA: lane (j, h), register r -> row i = 8*(r/4) + 4*h + (r%4), col j.
     // Token scales (1.0 for partials) are loaded up front; lanes past n_out, tokens past n_tok and
@@ -443,31 +600,9 @@ AH_DEV __attribute__((always_inline)) void gemm_store(const GemmArgs &a, const G
             if (const uint32_t oc = ah_out_code(v)) ah_record(a.status, ah_out_key(pa.key0 + (uint64_t)(tok0 + tl) * pa.n_out + row, oc));
         }
     }
-    if ((fm[0] | fm[1]) != 0ull) {
-        // Flagged tokens: this wave's 32 rows, the split's K range, the lane halves taking
-        // alternate units; split partials are stored in the reduction's units (divided by the
-        // token scale, an exact power of two).
-        const uint32_t nb32 = (a.n_in + 31) / 32;
-        if (ah_blk32(TYPE) && u_hi > nb32) u_hi = nb32;
-        const uint32_t row = row_w + j;
-        for (int half = 0; half < 2; ++half) {
-            uint64_t mk = fm[half];
-            while (mk) {
-                const uint32_t tl = 64 * half + (uint32_t)__builtin_ctzll(mk);
-                mk &= mk - 1;
-                const size_t t = (size_t)tok0 + tl;
-                float v = rl[0] ? exact_row<TYPE>(pa.w + rbase[0], a.fcodes + t * a.n_in, a.fscales + t * nb32,
-                                                  a.n_in, u_lo, u_hi, (uint32_t)h)
-                                : 0.0f;
-                v += __shfl_xor(v, 32, 64);
-                const float ts = ah_ts_value(__builtin_bit_cast(uint32_t, a.tok_scale[t]));
-                if (h == 0 && rl[0]) {
-                    ybase[(size_t)tl * pa.n_out + row] = scaled ? v : v / ts;
-                    if (const uint32_t oc = scaled ? ah_out_code(v) : 0u) ah_record(a.status, ah_out_key(pa.key0 + (uint64_t)t * pa.n_out + row, oc));
-                }
-            }
-        }
-    }
+    // flagged tokens (the same in every wave: the workgroup's waves share its tokens)
+    if ((fm[0] | fm[1]) != 0ull)
+        exact_tokens<TYPE, NN>(a, pa, win, win_bytes, fm[0], fm[1], tok0, row_w, 0u, ntile, ybase, scaled, u_lo, u_hi);
 }
 
 // The kernel body, on an LDS ring of RG slots of buf_bytes<TYPE> at `lds`.
@@ -805,7 +940,10 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
 
     const uint32_t u_lo = ah_blk32(TYPE) ? 2 * st_begin : st_begin / 4;
     const uint32_t u_hi = ah_blk32(TYPE) ? 2 * st_end : st_end / 4;
-    gemm_store<TYPE, NM, NN>(a, pa, acc, row_w, rl, rbase, tok0, ntile, split, u_lo, u_hi);
+    static_assert(rb::lds_bytes<TYPE, WV, RG>() >= xp::kWinBytes + WV * xp::kBatch * NN * 256u,
+                  "the exact path stages a token window and its sums in the ring");
+    gemm_store<TYPE, NM, NN>(a, pa, acc, row_w, rl, rbase, tok0, ntile, split, u_lo, u_hi, lds_base,
+                             rb::lds_bytes<TYPE, WV, RG>());
 }
 
 template <int TYPE, int WV, int RG>
@@ -985,7 +1123,10 @@ __global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
     }
     // the slices requested past the split must land before this workgroup's LDS is released
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    gemm_store<AH_GGML_Q8_0, NM, 1>(a, pa, acc, row_w, rl, rbase, tok0, ntile, split, 4 * st_begin, 4 * st_end);
+    static_assert(i8::kR * i8::kSlot >= xp::kWinBytes + 4 * xp::kBatch * 256u,
+                  "the exact path stages a token window and its sums in the slots");
+    gemm_store<AH_GGML_Q8_0, NM, 1>(a, pa, acc, row_w, rl, rbase, tok0, ntile, split, 4 * st_begin, 4 * st_end, lds,
+                                    i8::kR * i8::kSlot);
 }
 
 // Q4_K and Q6_K parts of one input in one grid (4 waves, 4 slots sized for the larger type):
@@ -1280,7 +1421,8 @@ AH_DEV void convert_word(const Raw &w, const RunScales &rs, uint32_t k, uint32_t
 template <int TYPE>
 AH_DEV __attribute__((always_inline)) void dq_store(const GemmArgs &a, const GemmPartArgs &pa, const f32x16 (&acc)[2][2],
                                                     const float *ts, uint32_t row_w, uint32_t tok_w, uint32_t split,
-                                                    uint32_t u_lo, uint32_t u_hi) {
+                                                    uint32_t u_lo, uint32_t u_hi, const float *TS, uint32_t tok0,
+                                                    uint8_t *win, uint32_t win_bytes) {
     const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
     const uint32_t ntile = a.n_tok > tok_w ? (a.n_tok - tok_w < 64u ? a.n_tok - tok_w : 64u) : 0u;
     float *ybase = pa.splits == 1 ? pa.y + (size_t)tok_w * pa.n_out
@@ -1330,30 +1472,16 @@ AH_DEV __attribute__((always_inline)) void dq_store(const GemmArgs &a, const Gem
             if (const uint32_t oc = ah_out_code(v)) ah_record(a.status, ah_out_key(pa.key0 + (uint64_t)(tok_w + tl) * pa.n_out + row, oc));
         }
     }
-    if (fm != 0ull) {
-        // flagged tokens: the split's K range, per row tile, the lane halves taking alternate units
-        const uint32_t nb32 = (a.n_in + 31) / 32;
-        if (ah_blk32(TYPE) && u_hi > nb32) u_hi = nb32;
-        uint64_t mk = fm;
-        while (mk) {
-            const uint32_t tl = (uint32_t)__builtin_ctzll(mk);
-            mk &= mk - 1;
-            const size_t t = (size_t)tok_w + tl;
-            const float tsv = ah_ts_value(__builtin_bit_cast(uint32_t, ts[tl]));
-#pragma unroll
-            for (int n = 0; n < 2; ++n) {
-                const uint32_t row = row_w + 32 * n + j;
-                float v = rl[n] ? exact_row<TYPE>(pa.w + (size_t)row * pa.row_bytes, a.fcodes + t * a.n_in,
-                                                  a.fscales + t * nb32, a.n_in, u_lo, u_hi, (uint32_t)h)
-                                : 0.0f;
-                v += __shfl_xor(v, 32, 64);
-                if (h == 0 && rl[n]) {
-                    ybase[(size_t)tl * pa.n_out + row] = scaled ? v : v / tsv;
-                    if (const uint32_t oc = scaled ? ah_out_code(v) : 0u) ah_record(a.status, ah_out_key(pa.key0 + (uint64_t)t * pa.n_out + row, oc));
-                }
-            }
-        }
-    }
+    // flagged tokens: the workgroup's, both token halves (`TS`: its 128 token scales), so that
+    // the exact path's loop is the same in every wave
+    (void)fm;
+    const uint32_t nt = a.n_tok > tok0 ? (a.n_tok - tok0 < 128u ? a.n_tok - tok0 : 128u) : 0u;
+    const uint64_t f0 = __builtin_amdgcn_ballot_w64((uint32_t)lane < nt && ah_ts_flagged(__builtin_bit_cast(uint32_t, TS[lane])));
+    const uint64_t f1 =
+        __builtin_amdgcn_ballot_w64(64u + (uint32_t)lane < nt && ah_ts_flagged(__builtin_bit_cast(uint32_t, TS[64 + lane])));
+    if ((f0 | f1) != 0ull)
+        exact_tokens<TYPE, 2>(a, pa, win, win_bytes, f0, f1, tok0, row_w, tok_w - tok0, tok_w - tok0 + ntile, ybase, scaled,
+                              u_lo, u_hi);
 }
 
 // Epilogue of the prefill FFN's fused gate/up tiles (kFormTileFfn).  The wave's accumulators
@@ -1635,11 +1763,15 @@ __global__ void __launch_bounds__(256, 2) gemm_dq_kernel(GemmArgs a) {
         stage(std::integral_constant<int, 3>{}, st + 3, par);
         par ^= 1u;
     }
-    if constexpr (FFN)
+    if constexpr (FFN) {
         dq_ffn_store<TYPE>(a, pa, acc, TS + 64u * wt, reinterpret_cast<float *>(lds) + 4096u * wv,
                            rtile * 64u + 32u * wr, tok0 + 64u * wt);
-    else
-        dq_store<TYPE>(a, pa, acc, TS + 64u * wt, row0 + 64u * wr, tok0 + 64u * wt, split, st_begin / 4, st_end / 4);
+    } else {
+        static_assert(kOT >= xp::kWinBytes + 4 * xp::kBatch * 2 * 256u,
+                      "the exact path stages a token window and its sums in the planes");
+        dq_store<TYPE>(a, pa, acc, TS + 64u * wt, row0 + 64u * wr, tok0 + 64u * wt, split, st_begin / 4, st_end / 4, TS,
+                       tok0, lds, kOT);
+    }
 }
 
 }  // namespace

@@ -541,8 +541,13 @@ def main() -> int:
         chart.ffn_gate_up_prefill_dev(dev, Gb, Ub, ptr(xf), n_tok, ptr(hcf), ptr(hsf), None, None, sh)
         assert dev.sync_status(sh) == 0
         ffn["down_exact_path_us"] = round(event_us(down, 3), 1)
+        # tokens the operand pass flags: a nonzero block more than 24 binades below the largest
+        hs_np = hsf.cpu().numpy()
+        e = np.log2(np.maximum(hs_np, 1).astype(np.float64))
+        span = np.where(hs_np > 0, e, -np.inf).max(axis=1) - np.where(hs_np > 0, e, np.inf).min(axis=1)
+        ffn["down_flagged_tokens"] = int(np.sum(span > 24))
         log(f"[bench] configs[4] prefill FFN down alone {ffn['down_us']} us; with flagged hidden tokens "
-            f"{ffn['down_exact_path_us']} us")
+            f"{ffn['down_exact_path_us']} us ({ffn['down_flagged_tokens']} of {n_tok} tokens flagged)")
         result["ffn_prefill"] = ffn
         for w_ in (Gf, Uf, Df, Gb, Ub):
             w_.free()

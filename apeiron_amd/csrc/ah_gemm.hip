@@ -387,15 +387,15 @@ AH_DEV float exact_row(const uint8_t *row, const int8_t *xq, const int64_t *sc, 
 // dot units (exact v_dot4 group dots folded in f32 with the token's own block scales, so no band
 // applies; the same arithmetic as a decode GEMV of that token).  The loop is uniform over the
 // workgroup: `fm` holds the tile's flagged tokens (bit tl) alike in every wave, and every wave
-// calls this.  Per token and per window of kWin 32-blocks of the split's K range, the
-// workgroup's threads stage the token's codes, block scales and code sums in LDS (`win`: the
-// MFMA operand ring or planes, free once every wave is past its loop) in the GEMV's layout,
-// shifted so the units index it by absolute block; then lane (j, h) of each wave takes row
-// row_w + 32 n + j, the two lane halves alternating units, reading the weights from the GGUF
-// rows in memory.  A unit whose reads could pass the tensor's end (the units read up to a dword
-// past their bytes; the tail of a caller-wrapped payload), or any unit of a payload whose start
-// is not 16-byte aligned, takes exact_row.  Partials (scaled == false) are stored in the reduction's units, divided by
-// the token scale.
+// calls this.  Per batch of up to kBatch tokens and per window of kWin 32-blocks of the split's
+// K range, the workgroup's threads stage each token's codes, block scales and code sums in LDS
+// (`win`: the MFMA operand ring or planes, free once every wave is past its loop) in the GEMV's
+// layout, shifted so the units index it by absolute block; then lane (j, h) of each wave takes
+// row row_w + 32 n + j, the two lane halves alternating units, reading the weights from the GGUF
+// rows in memory once for the whole batch.  A unit whose reads could pass the tensor's end (the
+// units read up to a dword past their bytes; the tail of a caller-wrapped payload), or any unit
+// of a payload whose start is not 16-byte aligned, takes exact_row.  Partials (scaled == false)
+// are stored in the reduction's units, divided by the token scale.
 namespace xp {
 constexpr uint32_t kWin = 64;   // 32-blocks per staged window (2048 K; 3.2 KB of LDS per token)
 constexpr uint32_t kBatch = 8;  // flagged tokens staged at once, LDS permitting

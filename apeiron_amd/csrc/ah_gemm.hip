@@ -475,8 +475,8 @@ AH_DEV void exact_tokens(const GemmArgs &a, const GemmPartArgs &pa, uint8_t *win
             ActLds A;
             A.codes = reinterpret_cast<int8_t *>(wb) - pad_k(32u * g0);
             A.fsc = reinterpret_cast<float *>(wb + codes_bytes(32u * xp::kWin)) - g0;
-            A.xs32 = reinterpret_cast<int32_t *>(A.fsc + g0 + xp::kWin) - g0;
-            A.xs16 = reinterpret_cast<int32_t *>(A.xs32 + g0 + xp::kWin) - 2u * g0;
+            A.fx32 = A.fsc + xp::kWin;  // (each array shifted by its window's first block)
+            A.xs16 = reinterpret_cast<int32_t *>(A.fx32 + g0 + xp::kWin) - 2u * g0;
             return A;
         };
         for (uint32_t g0 = b_lo & ~7u; g0 < b_hi; g0 += xp::kWin) {

@@ -1064,7 +1064,7 @@ bool ah_gemv_stream_geometry(uint32_t type, uint32_t row_bytes, uint32_t units, 
     return true;
 }
 
-// LDS bytes of one part's quantized activation (codes with padding, fsc, xs32, xs16): a multiple
+// LDS bytes of one part's quantized activation (codes with padding, fsc, fx32, xs16): a multiple
 // of 16 for any kpad that is a multiple of 256.
 size_t ah_gemv_act_bytes(uint32_t kpad) {
     return kpad + kpad / 16 + (size_t)kpad / 32 * 8 + (size_t)kpad / 16 * 4;

@@ -26,7 +26,8 @@ AH_DEV u32x4 ah_ld128p(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 struct ActLds {
     int8_t *codes;   // [kpad]
     float *fsc;      // [kpad/32]   S_b * 2^-32
-    int32_t *xs32;   // [kpad/32]   sum of codes per 32-block
+    float *fx32;     // [kpad/32]   fsc * X: the 32-block's code sum X times its scale (exact for a
+                     //             power-of-two scale)
     int32_t *xs16;   // [kpad/16]   sum of codes per 16-group
     float *red;      // [1024]      unit partials of one tile (the tile copy follows)
 };
@@ -40,8 +41,8 @@ AH_DEV ActLds carve(uint8_t *smem, uint32_t kpad) {
     ActLds a;
     a.codes = reinterpret_cast<int8_t *>(smem);
     a.fsc = reinterpret_cast<float *>(smem + codes_bytes(kpad));
-    a.xs32 = reinterpret_cast<int32_t *>(a.fsc + kpad / 32);
-    a.xs16 = a.xs32 + kpad / 32;
+    a.fx32 = a.fsc + kpad / 32;
+    a.xs16 = reinterpret_cast<int32_t *>(a.fx32 + kpad / 32);
     a.red = reinterpret_cast<float *>(a.xs16 + kpad / 16);
     return a;
 }
@@ -354,21 +355,23 @@ AH_DEV QuadOut quant_quad(const void *x, uint32_t src, uint32_t n_in, size_t row
 }
 
 // Store one quad's block to the LDS activation.
-// One per-block word per lane: lane 0 the scale, lane 2 the block sum, lanes 1 / 3 their own
-// 16-group sums (elements 0..15 / 16..31).  The words arrive as values (not through the QuadOut)
+// One per-block word per lane: lane 0 the scale, lane 2 the scaled block sum fsc * X, lanes 1 / 3
+// their own 16-group sums (elements 0..15 / 16..31).  The words arrive as values (not through the QuadOut)
 // so that the per-lane choice is a register select rather than a load from a chosen field.
-AH_DEV void store_quad_words(const ActLds &A, uint32_t b, uint32_t c0, uint32_t c1, uint32_t fsc, uint32_t s32,
+AH_DEV void store_quad_words(const ActLds &A, uint32_t b, uint32_t c0, uint32_t c1, uint32_t fsc, uint32_t fx,
                              uint32_t s16) {
     const uint32_t q = threadIdx.x & 3;
     u32x2 *dst = reinterpret_cast<u32x2 *>(A.codes + pad_k(32 * b + 8 * q));
     *dst = (u32x2){c0, c1};
     uint32_t *const p = q == 0 ? reinterpret_cast<uint32_t *>(A.fsc) + b
-                      : q == 2 ? reinterpret_cast<uint32_t *>(A.xs32) + b
+                      : q == 2 ? reinterpret_cast<uint32_t *>(A.fx32) + b
                                : reinterpret_cast<uint32_t *>(A.xs16) + 2 * b + (q >> 1);
-    *p = q == 0 ? fsc : q == 2 ? s32 : s16;
+    *p = q == 0 ? fsc : q == 2 ? fx : s16;
 }
 AH_DEV void store_quad(const ActLds &A, uint32_t b, const QuadOut &o) {
-    store_quad_words(A, b, o.c0, o.c1, __builtin_bit_cast(uint32_t, o.fsc), (uint32_t)o.s32, (uint32_t)o.s16);
+    // |X| <= 32 * 128: (float)X is exact, and so is fsc * X when fsc is a power of two
+    store_quad_words(A, b, o.c0, o.c1, __builtin_bit_cast(uint32_t, o.fsc),
+                     __builtin_bit_cast(uint32_t, o.fsc * (float)o.s32), (uint32_t)o.s16);
 }
 
 // ---- per-family units, read from the LDS copy of the tile -------------------------------------
@@ -402,7 +405,9 @@ AH_DEV float unit_q8(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &
 // qh (a little-endian u32) at 2..5, 16 bytes of nibbles at 6..21.  Output j < 16 is qs[j] & 15 with
 // qh bit j as its fifth bit, output 16 + j is qs[j] >> 4 with qh bit 16 + j, each minus 16.  The
 // five-bit values u (0..31) go to v_dot4 as bytes (four qh bits spread to bit 4 of four bytes by
-// one multiply), and the -16 offset is folded through the block's code sum: D = sum u*xq - 16*X.
+// one multiply), and the -16 offset is folded through the block's code sum: D = sum u*xq - 16*X,
+// applied as fsc * D = fsc * sum u*xq - 16 * fx32 (exact for a power-of-two fsc: both terms and
+// their difference are representable).
 template <bool DOTS>
 AH_DEV float unit_q5(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &A, int32_t *dots) {
     const bool odd = (off & 3u) != 0;  // 2-byte aligned blocks: 6 dwords from the 4-aligned start
@@ -424,9 +429,13 @@ AH_DEV float unit_q5(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &
         D = ah_sdot4((qs & 0x0F0F0F0Fu) | blo, xw[i], D);
         D = ah_sdot4(((qs >> 4) & 0x0F0F0F0Fu) | bhi, xw[4 + i], D);
     }
-    D -= 16 * A.xs32[b];
-    if (DOTS && dots) dots[b] = D;
-    return ah_f16_bits_to_f32(d16) * A.fsc[b] * (float)D;
+    if (DOTS && dots) {
+        int32_t X = 0;  // the block's code sum, from the codes (the LDS holds it scaled)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) X = ah_sdot4(0x01010101u, xw[i], X);
+        dots[b] = D - 16 * X;
+    }
+    return ah_f16_bits_to_f32(d16) * __builtin_fmaf(-16.0f, A.fx32[b], A.fsc[b] * (float)D);
 }
 
 // Q4_K super-block s (format/quant.rs:481-510): d, dmin, 12 packed 6-bit (scale, min) pairs,
@@ -435,34 +444,28 @@ AH_DEV float unit_q5(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &
 //
 // The eight (sc, m) pairs of get_scale_min_k4 (format/quant.rs:482-491) unpack as four words of
 // four bytes each: sc 0-3 = b[0..3] & 63, m 0-3 = b[4..7] & 63, sc 4-7 = (b[8..11] & 15) |
-// (b[0..3] >> 6) << 4, m 4-7 = (b[8..11] >> 4) | (b[4..7] >> 6) << 4.  d*sc_j and dmin*m_j are
-// formed once per super-block; the per-sub-block arithmetic is f32 (no integer multiplies).
+// (b[0..3] >> 6) << 4, m 4-7 = (b[8..11] >> 4) | (b[4..7] >> 6) << 4.  sc_j * D_j is an exact
+// integer (sc_j <= 63, |D_j| <= 32 * 15 * 128: below 2^22, one 24-bit multiply), so the unit sums
+// S_j * (sc_j * D_j) and m_j * (S_j * X_j) (the activation's fx32) in f32, and d and dmin multiply
+// once per unit.
 struct Q4kScales {
-    float dsc[8], dm[8];
+    uint32_t sc[2], m[2];  // the bytes of sc 0-3, sc 4-7, m 0-3, m 4-7
 };
-AH_DEV Q4kScales q4k_scales(uint32_t s0, uint32_t s1, uint32_t s2, float fd, float fdm) {
-    const uint32_t sc03 = s0 & 0x3F3F3F3Fu, m03 = s1 & 0x3F3F3F3Fu;
-    const uint32_t sc47 = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-    const uint32_t m47 = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+AH_DEV Q4kScales q4k_scales(uint32_t s0, uint32_t s1, uint32_t s2) {
     Q4kScales q;
-    const uint32_t w[4] = {sc03, sc47, m03, m47};
-    float b[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) b[4 * i + k] = (float)((w[i] >> (8 * k)) & 0xffu);  // v_cvt_f32_ubyteN
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        q.dsc[j] = fd * b[j];
-        q.dm[j] = fdm * b[8 + j];
-    }
+    q.sc[0] = s0 & 0x3F3F3F3Fu;
+    q.m[0] = s1 & 0x3F3F3F3Fu;
+    q.sc[1] = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    q.m[1] = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
     return q;
 }
+AH_DEV int32_t q4k_byte(uint32_t w, uint32_t k) { return (int32_t)((w >> (8 * k)) & 0xffu); }
 
+// Pair P of a super-block (sub-blocks 2P, 2P + 1 from the low / high nibbles of qs[32P..32P+31]):
+// adds its two terms to ad (S * sc * D) and am (m * S * X).
 template <int P, bool DOTS>
-AH_DEV float q4k_pair(const u32x4 *sb, const Q4kScales &q4, uint32_t g0, uint32_t nb32, const ActLds &A,
-                      int32_t *dots, float flo, float fhi, float xlo, float xhi) {
+AH_DEV void q4k_pair(const u32x4 *sb, const Q4kScales &q4, uint32_t g0, uint32_t nb32, const ActLds &A,
+                     int32_t *dots, float flo, float fhi, float xlo, float xhi, float &ad, float &am) {
     const u32x4 qa = sb[1 + 2 * P], qb = sb[2 + 2 * P];
     const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
     const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g0));
@@ -479,33 +482,36 @@ AH_DEV float q4k_pair(const u32x4 *sb, const Q4kScales &q4, uint32_t g0, uint32_
         dots[g0] = Dlo;
         if (g0 + 1 < nb32) dots[g0 + 1] = Dhi;  // a ragged row ends on an odd sub-block
     }
-    const float tlo = q4.dsc[2 * P] * (float)Dlo - q4.dm[2 * P] * xlo;
-    const float thi = q4.dsc[2 * P + 1] * (float)Dhi - q4.dm[2 * P + 1] * xhi;
-    return flo * tlo + fhi * thi;
+    const uint32_t scw = q4.sc[P >> 1], mw = q4.m[P >> 1], k = 2 * (P & 1);
+    ad = __builtin_fmaf(flo, (float)__mul24(q4k_byte(scw, k), Dlo), ad);
+    ad = __builtin_fmaf(fhi, (float)__mul24(q4k_byte(scw, k + 1), Dhi), ad);
+    am = __builtin_fmaf((float)q4k_byte(mw, k), xlo, am);
+    am = __builtin_fmaf((float)q4k_byte(mw, k + 1), xhi, am);
 }
 template <bool DOTS>
 AH_DEV float unit_q4(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in, const ActLds &A,
                      int32_t *dots) {
     const u32x4 *sb = reinterpret_cast<const u32x4 *>(tl + off);  // 16-byte aligned
     const u32x4 h = sb[0];
-    // the super-block's eight activation scales and code sums, read ahead of the pairs
-    float fs[8], xs[8];
+    // the super-block's eight activation scales and scaled code sums, read ahead of the pairs
+    float fs[8], fx[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         fs[i] = A.fsc[8 * s + i];
-        xs[i] = (float)A.xs32[8 * s + i];  // |X| <= 32 * 128: exact
+        fx[i] = A.fx32[8 * s + i];
     }
     const float fd = ah_f16_bits_to_f32(h.x & 0xffffu), fdm = ah_f16_bits_to_f32(h.x >> 16);
-    const Q4kScales q4 = q4k_scales(h.y, h.z, h.w, fd, fdm);
+    const Q4kScales q4 = q4k_scales(h.y, h.z, h.w);
     const uint32_t nb32 = (n_in + 31) / 32, rem = n_in - 256 * s;
     // a ragged row's last super-block uses fewer pairs; without DOTS the rest meet zero activations
     const uint32_t npairs = !DOTS || rem >= 256 ? 4u : (rem + 63) / 64;
     const uint32_t g = 8 * s;
-    float acc = q4k_pair<0, DOTS>(sb, q4, g, nb32, A, dots, fs[0], fs[1], xs[0], xs[1]);
-    if (npairs > 1) acc += q4k_pair<1, DOTS>(sb, q4, g + 2, nb32, A, dots, fs[2], fs[3], xs[2], xs[3]);
-    if (npairs > 2) acc += q4k_pair<2, DOTS>(sb, q4, g + 4, nb32, A, dots, fs[4], fs[5], xs[4], xs[5]);
-    if (npairs > 3) acc += q4k_pair<3, DOTS>(sb, q4, g + 6, nb32, A, dots, fs[6], fs[7], xs[6], xs[7]);
-    return acc;
+    float ad = 0.0f, am = 0.0f;
+    q4k_pair<0, DOTS>(sb, q4, g, nb32, A, dots, fs[0], fs[1], fx[0], fx[1], ad, am);
+    if (npairs > 1) q4k_pair<1, DOTS>(sb, q4, g + 2, nb32, A, dots, fs[2], fs[3], fx[2], fx[3], ad, am);
+    if (npairs > 2) q4k_pair<2, DOTS>(sb, q4, g + 4, nb32, A, dots, fs[4], fs[5], fx[4], fx[5], ad, am);
+    if (npairs > 3) q4k_pair<3, DOTS>(sb, q4, g + 6, nb32, A, dots, fs[6], fs[7], fx[6], fx[7], ad, am);
+    return __builtin_fmaf(fd, ad, -(fdm * am));
 }
 
 // Q4_K in units of one pair of sub-blocks (64 elements; u = 4 s + P for super-block s and pair
@@ -523,9 +529,7 @@ AH_DEV float unit_q4p(const uint8_t *tl, uint32_t off, uint32_t u, uint32_t n_in
     const bool hi47 = P >= 2;
     const uint32_t scw = hi47 ? ((h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u)) : (h.y & 0x3F3F3F3Fu);
     const uint32_t mw = hi47 ? (((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u)) : (h.z & 0x3F3F3F3Fu);
-    const uint32_t bsh = 16 * (P & 1u);
-    const float sc0 = (float)((scw >> bsh) & 0xffu), sc1 = (float)((scw >> (bsh + 8)) & 0xffu);
-    const float m0 = (float)((mw >> bsh) & 0xffu), m1 = (float)((mw >> (bsh + 8)) & 0xffu);
+    const uint32_t k = 2 * (P & 1u);
     const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
     const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g0));
     const u32x4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
@@ -543,9 +547,10 @@ AH_DEV float unit_q4p(const uint8_t *tl, uint32_t off, uint32_t u, uint32_t n_in
         if (g0 + 1 < nb32) dots[g0 + 1] = Dhi;  // a ragged row ends on an odd 32-block
     }
     // (past a ragged row's end the codes are zero: the pair's second half adds nothing)
-    const float tlo = (fd * sc0) * (float)Dlo - (fdm * m0) * (float)A.xs32[g0];
-    const float thi = (fd * sc1) * (float)Dhi - (fdm * m1) * (float)A.xs32[g0 + 1];
-    return A.fsc[g0] * tlo + A.fsc[g0 + 1] * thi;
+    const float ad = __builtin_fmaf(A.fsc[g0 + 1], (float)__mul24(q4k_byte(scw, k + 1), Dhi),
+                                    A.fsc[g0] * (float)__mul24(q4k_byte(scw, k), Dlo));
+    const float am = __builtin_fmaf((float)q4k_byte(mw, k + 1), A.fx32[g0 + 1], (float)q4k_byte(mw, k) * A.fx32[g0]);
+    return __builtin_fmaf(fd, ad, -(fdm * am));
 }
 
 // Q6_K super-block s (format/quant.rs:556-599): ql[128] @0, qh[64] @128, int8 sc[16] @192,

@@ -91,6 +91,14 @@ template <int N> AH_DEV void ah_vm_lds_barrier() {
 AH_DEV int32_t ah_sdot4(uint32_t a, uint32_t b, int32_t c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
+// A dot chain's first step: the three-operand form with an inline 0 accumulator.  From the
+// builtin the compiler picks the accumulating two-operand v_dot4c, which first moves 0 into its
+// destination: one VALU instruction per chain.
+AH_DEV int32_t ah_sdot4_first(uint32_t a, uint32_t b) {
+    int32_t d;
+    __asm__("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
 AH_DEV uint32_t ah_alignbyte(uint32_t hi, uint32_t lo, uint32_t sh) {
     return __builtin_amdgcn_alignbyte(hi, lo, sh);
 }

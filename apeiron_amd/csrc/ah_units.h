@@ -395,7 +395,7 @@ AH_DEV float unit_q8(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const uint32_t c = sh ? w[i + 1] : ah_alignbyte(w[i + 1], w[i], 2);
-        D = ah_sdot4(c, xw[i], D);
+        D = i == 0 ? ah_sdot4_first(c, xw[i]) : ah_sdot4(c, xw[i], D);
     }
     if (DOTS && dots) dots[b] = D;
     return ah_f16_bits_to_f32(d16) * A.fsc[b] * (float)D;
@@ -426,7 +426,7 @@ AH_DEV float unit_q5(const uint8_t *tl, uint32_t off, uint32_t b, const ActLds &
         const uint32_t qs = odd ? w[i + 2] : ah_alignbyte(w[i + 2], w[i + 1], 2);
         const uint32_t blo = ((((qh >> (4 * i)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
         const uint32_t bhi = ((((qh >> (16 + 4 * i)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
-        D = ah_sdot4((qs & 0x0F0F0F0Fu) | blo, xw[i], D);
+        D = i == 0 ? ah_sdot4_first((qs & 0x0F0F0F0Fu) | blo, xw[i]) : ah_sdot4((qs & 0x0F0F0F0Fu) | blo, xw[i], D);
         D = ah_sdot4(((qs >> 4) & 0x0F0F0F0Fu) | bhi, xw[4 + i], D);
     }
     if (DOTS && dots) {
@@ -475,8 +475,9 @@ AH_DEV void q4k_pair(const u32x4 *sb, const Q4kScales &q4, uint32_t g0, uint32_t
     int32_t Dlo = 0, Dhi = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        Dlo = ah_sdot4(q[i] & 0x0F0F0F0Fu, xl[i], Dlo);
-        Dhi = ah_sdot4((q[i] >> 4) & 0x0F0F0F0Fu, xh[i], Dhi);
+        Dlo = i == 0 ? ah_sdot4_first(q[i] & 0x0F0F0F0Fu, xl[i]) : ah_sdot4(q[i] & 0x0F0F0F0Fu, xl[i], Dlo);
+        Dhi = i == 0 ? ah_sdot4_first((q[i] >> 4) & 0x0F0F0F0Fu, xh[i])
+                     : ah_sdot4((q[i] >> 4) & 0x0F0F0F0Fu, xh[i], Dhi);
     }
     if (DOTS && dots) {
         dots[g0] = Dlo;
@@ -538,8 +539,9 @@ AH_DEV float unit_q4p(const uint8_t *tl, uint32_t off, uint32_t u, uint32_t n_in
     int32_t Dlo = 0, Dhi = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        Dlo = ah_sdot4(q[i] & 0x0F0F0F0Fu, xl[i], Dlo);
-        Dhi = ah_sdot4((q[i] >> 4) & 0x0F0F0F0Fu, xh[i], Dhi);
+        Dlo = i == 0 ? ah_sdot4_first(q[i] & 0x0F0F0F0Fu, xl[i]) : ah_sdot4(q[i] & 0x0F0F0F0Fu, xl[i], Dlo);
+        Dhi = i == 0 ? ah_sdot4_first((q[i] >> 4) & 0x0F0F0F0Fu, xh[i])
+                     : ah_sdot4((q[i] >> 4) & 0x0F0F0F0Fu, xh[i], Dhi);
     }
     if (DOTS && dots) {
         const uint32_t nb32 = (n_in + 31) / 32;
@@ -591,9 +593,9 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, ui
             const uint32_t hi = (2 * t <= 4 ? (qh[i] << (4 - 2 * t)) : (qh[i] >> (2 * t - 4))) & 0x30303030u;
             const uint32_t uu = ((t < 2 ? qlw : (qlw >> 4)) & 0x0F0F0F0Fu) | hi;
             if (i < 4)
-                Dlo = ah_sdot4(uu, xw[i], Dlo);
+                Dlo = i == 0 ? ah_sdot4_first(uu, xw[i]) : ah_sdot4(uu, xw[i], Dlo);
             else
-                Dhi = ah_sdot4(uu, xw[i], Dhi);
+                Dhi = i == 4 ? ah_sdot4_first(uu, xw[i]) : ah_sdot4(uu, xw[i], Dhi);
         }
         Dlo -= 32 * A.xs16[2 * g];
         Dhi -= 32 * A.xs16[2 * g + 1];
@@ -677,7 +679,7 @@ AH_DEV float unit_k23(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, u
                 const uint32_t hb = hn[4 * pl + i] & (0x01010101u << r);
                 v |= r == 3 ? hb >> 1 : hb << (r + 2);
             }
-            D = ah_sdot4(v, xw[i], D);
+            D = i == 0 ? ah_sdot4_first(v, xw[i]) : ah_sdot4(v, xw[i], D);
         }
         if (r == 1 || r == 2) D >>= 2 * r;
         const int32_t X = A.xs16[g];

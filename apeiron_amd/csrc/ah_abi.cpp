@@ -427,6 +427,8 @@ uint32_t deal_waves(const GemvPart *parts, size_t n, uint32_t n_wg, size_t act_b
                 D.wave_act[wi] = D.n_act - 1;
                 D.r_begin[wi] = tb * RW < parts[p].n_out ? tb * RW : parts[p].n_out;
                 D.r_end[wi] = te * RW < parts[p].n_out ? te * RW : parts[p].n_out;
+                D.t_first[wi] = k;
+                D.t_stride[wi] = nw[p];
                 ++c;
             }
         }

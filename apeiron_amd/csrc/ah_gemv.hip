@@ -518,7 +518,11 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
     GemvPart P;
-    uint32_t r_begin, r_end, aoff = 0;
+    // The wave's rows: tiles t_k, t_k + t_s, t_k + 2 t_s, ... of RW rows each, counted from row
+    // r_begin and cut at r_end.  A part's waves take its tiles strided (t_k the wave's index among
+    // them, t_s their number), so that at any time they read adjacent tiles of the weights: a bare
+    // read at this grid measured 6.2 TB/s against 5.8 with each wave on a contiguous range.
+    uint32_t r_begin, r_end, aoff = 0, t_k = 0, t_s = 1;
     uint32_t f_b0 = 0, f_b1 = 0;  // FFN: the workgroup's hidden blocks
     if constexpr (FFN) {
         // one part's words per wave, read at a uniform index (selecting between both parts'
@@ -536,8 +540,10 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
         const uint32_t pi = D->wave_part[wv];
         const bool idle = pi == kIdleWave;
         P = part_at(parts, idle ? D->act_part[0] : pi);  // an idle wave streams no rows
-        r_begin = D->r_begin[wv];
-        r_end = idle ? r_begin : D->r_end[wv];
+        r_begin = 0;
+        r_end = idle ? 0u : P.n_out;
+        t_k = D->t_first[wv];
+        t_s = D->t_stride[wv];
         aoff = D->act_off[D->wave_act[wv]];
     } else {
         // The workgroup's part.  One round of argument loads brings the part count, the later
@@ -560,10 +566,10 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
             P = sp.p[__builtin_amdgcn_readfirstlane(pi)];
             pin(P);
         }
-        const uint32_t n_waves = P.wg_count * kSWaves;
-        const uint32_t wl = (blockIdx.x - P.wg_begin) * kSWaves + wave;
-        r_begin = (uint32_t)((uint64_t)P.n_out * wl / n_waves);
-        r_end = (uint32_t)((uint64_t)P.n_out * (wl + 1) / n_waves);
+        r_begin = 0;
+        r_end = P.n_out;
+        t_k = (blockIdx.x - P.wg_begin) * kSWaves + wv;
+        t_s = P.wg_count * kSWaves;
     }
     // GEMV parts take f32 or code inputs (the Q32.32 form is the quantizer's alone): telling the
     // compiler drops that form's 16-word inputs from the prologue's registers
@@ -573,7 +579,8 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
     uint8_t *tl = smem + act_bytes + wave * kSlotBytes;
     const __amdgpu_buffer_rsrc_t rs = ah_rsrc(P.w, (uint32_t)P.w_bytes);
     const uint32_t U = P.units, RW = P.rows_per_tile, RB = P.row_bytes, G = P.lanes;
-    const uint32_t n_t = (r_end - r_begin + RW - 1) / RW;
+    const uint32_t n_tiles = (r_end - r_begin + RW - 1) / RW;
+    const uint32_t n_t = t_k < n_tiles ? (n_tiles - t_k + t_s - 1) / t_s : 0u;
 
     // Tile t's loads.  All kChunks loads are issued, chunks past the tile out of range (they read
     // nothing), so that the compiler's load counting sees the same loads on every path and never
@@ -582,7 +589,7 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
     // path (a decode token took 3% longer with them).
     u32x4 chunk[kChunks];
     auto load_tile = [&](uint32_t t) {
-        const uint32_t r0 = r_begin + t * RW;
+        const uint32_t r0 = r_begin + (t_k + t * t_s) * RW;
         const uint32_t rows = t >= n_t ? 0u : (r_end - r0 < RW ? r_end - r0 : RW);
         const uint32_t start = rows ? r0 * RB : 0u, a0 = start & ~15u;
         const uint32_t nch = rows ? (rows * RB + (start - a0) + 15) / 16 : 0u;
@@ -679,7 +686,7 @@ __global__ void __launch_bounds__(kSThreads, FFN && TYPE == AH_GGML_Q6_K ? 2 : s
     for (uint32_t t = 0; t < n_t; ++t) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS stores have landed
         __builtin_amdgcn_wave_barrier();
-        const uint32_t r0 = r_begin + t * RW;
+        const uint32_t r0 = r_begin + (t_k + t * t_s) * RW;
         const uint32_t toff = (r0 * RB) & 15u;
         const uint32_t row = r0 + r;
         const bool owns = r < RW && row < r_end;

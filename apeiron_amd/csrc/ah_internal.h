@@ -289,7 +289,11 @@ struct StreamWG {
     uint32_t act_off[8];   // LDS byte offsets of their activations
     uint32_t wave_part[8]; // per wave: part index, or kIdleWave
     uint32_t wave_act[8];  // per wave: index into act_*
-    uint32_t r_begin[8], r_end[8];
+    uint32_t r_begin[8], r_end[8];  // per wave: its rows as one contiguous range of whole tiles
+    // per wave, the same count of tiles taken strided (the streaming kernel's form): tiles
+    // t_first, t_first + t_stride, ... of its part, so that the part's waves read adjacent tiles
+    // at the same time
+    uint32_t t_first[8], t_stride[8];
 };
 
 // Persistent decode sequence (gemv_seq_kernel): stages run in order on one resident grid, each

@@ -560,9 +560,8 @@ AH_DEV float unit_q4p(const uint8_t *tl, uint32_t off, uint32_t u, uint32_t n_in
 // | ((qh[32n + l] >> 2t) & 3) << 4) - 32.  The unit is one half n (128 elements: ql[64n..],
 // qh[32n..], sc[8n..], d), so a row of K elements has ceil(K/128) units and a lane's work per
 // unit is half a super-block.  Super-blocks are 2-byte aligned: the half's dwords are read from the
-// 4-aligned address below and realigned.  The 6-bit value is built with one and-or per word (the
-// high bits are moved into place by one shift and mask), and the group terms are f32 (no integer
-// multiplies).
+// 4-aligned address below and realigned.  The 6-bit value is built per word by one bit-field
+// select (see below), and the block terms are exact integers folded in f32.
 template <bool DOTS>
 AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, uint32_t n_in,
                      const ActLds &A, int32_t *dots16) {
@@ -574,14 +573,22 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, ui
     auto V = [&](const uint32_t *b, int i) -> uint32_t { return ah_alignbyte(b[i + 1], b[i], sh); };
     const float fd = ah_f16_bits_to_f32(V(p, 52) & 0xffffu);
     float acc = 0.0f;
-    uint32_t qh[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qh[i] = V(ph, i);
     const uint32_t scw[2] = {V(ps, 0), V(ps, 1)};
+    // The qh pairs of a byte are bits (2t, 2t+1) for block t.  One mask per qh word keeps the
+    // pairs of blocks 0 and 2 in place (bits 0-1, 4-5), one shift and mask brings those of blocks
+    // 1 and 3 there; the 6-bit value is then (ql nibble) | (the pair moved to bits 4-5), one
+    // bit-field insert after at most one shift per operand.  Blocks go in the order 0, 2, 1, 3,
+    // so that only one of the two masked sets is live at a time.
+    uint32_t qm[8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int tt = 0; tt < 4; ++tt) {
+        const int t = tt == 1 ? 2 : tt == 2 ? 1 : tt;
         const uint32_t g = 8 * s + 4 * n + t;
-        if (DOTS && g >= nb32) break;
+        if (tt == 0 || tt == 2) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qm[i] = ((t & 1) ? V(ph, i) >> 2 : V(ph, i)) & 0x33333333u;
+        }
+        if (DOTS && g >= nb32) continue;
         const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g));
         const u32x4 x0 = xv[0], x1 = xv[1];
         const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -589,9 +596,11 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, ui
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t qlw = V(pl, 8 * (t & 1) + i);
-            // bits 4-5 of each byte: qh bits 2t, 2t+1
-            const uint32_t hi = (2 * t <= 4 ? (qh[i] << (4 - 2 * t)) : (qh[i] >> (2 * t - 4))) & 0x30303030u;
-            const uint32_t uu = ((t < 2 ? qlw : (qlw >> 4)) & 0x0F0F0F0Fu) | hi;
+            const uint32_t lo = t < 2 ? qlw : qlw >> 4;    // the nibble at bits 0-3
+            const uint32_t hi = t < 2 ? qm[i] << 4 : qm[i];  // the pair at bits 4-5 (6-7 clear)
+            // (lo & 0x0F0F0F0F) | (hi & ~0x0F0F0F0F) as one v_bitop3 (table 0xE4: C ? A : B); the
+            // builtin keeps the compiler from re-deriving the masks per block
+            const uint32_t uu = __builtin_amdgcn_bitop3_b32(lo, hi, 0x0F0F0F0Fu, 0xE4);
             if (i < 4)
                 Dlo = i == 0 ? ah_sdot4_first(uu, xw[i]) : ah_sdot4(uu, xw[i], Dlo);
             else

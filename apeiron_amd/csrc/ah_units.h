@@ -464,11 +464,11 @@ AH_DEV int32_t q4k_byte(uint32_t w, uint32_t k) { return (int32_t)((w >> (8 * k)
 // Pair P of a super-block (sub-blocks 2P, 2P + 1 from the low / high nibbles of qs[32P..32P+31]):
 // adds its two terms to ad (S * sc * D) and am (m * S * X).
 template <int P, bool DOTS>
-AH_DEV void q4k_pair(const u32x4 *sb, const Q4kScales &q4, uint32_t g0, uint32_t nb32, const ActLds &A,
+AH_DEV void q4k_pair(const u32x4 *sb, const Q4kScales &q4, uint32_t g0, uint32_t nb32, const int8_t *cb,
                      int32_t *dots, float flo, float fhi, float xlo, float xhi, float &ad, float &am) {
     const u32x4 qa = sb[1 + 2 * P], qb = sb[2 + 2 * P];
     const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-    const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g0));
+    const u32x4 *xv = reinterpret_cast<const u32x4 *>(cb + 64 * P);  // pad_k(32 g0), g0 = 8s + 2P
     const u32x4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
     const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
     const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
@@ -508,10 +508,11 @@ AH_DEV float unit_q4(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n_in,
     const uint32_t npairs = !DOTS || rem >= 256 ? 4u : (rem + 63) / 64;
     const uint32_t g = 8 * s;
     float ad = 0.0f, am = 0.0f;
-    q4k_pair<0, DOTS>(sb, q4, g, nb32, A, dots, fs[0], fs[1], fx[0], fx[1], ad, am);
-    if (npairs > 1) q4k_pair<1, DOTS>(sb, q4, g + 2, nb32, A, dots, fs[2], fs[3], fx[2], fx[3], ad, am);
-    if (npairs > 2) q4k_pair<2, DOTS>(sb, q4, g + 4, nb32, A, dots, fs[4], fs[5], fx[4], fx[5], ad, am);
-    if (npairs > 3) q4k_pair<3, DOTS>(sb, q4, g + 6, nb32, A, dots, fs[6], fs[7], fx[6], fx[7], ad, am);
+    const int8_t *const cb = A.codes + 272u * s;  // pad_k(32 * 8s): the super-block's codes
+    q4k_pair<0, DOTS>(sb, q4, g, nb32, cb, dots, fs[0], fs[1], fx[0], fx[1], ad, am);
+    if (npairs > 1) q4k_pair<1, DOTS>(sb, q4, g + 2, nb32, cb, dots, fs[2], fs[3], fx[2], fx[3], ad, am);
+    if (npairs > 2) q4k_pair<2, DOTS>(sb, q4, g + 4, nb32, cb, dots, fs[4], fs[5], fx[4], fx[5], ad, am);
+    if (npairs > 3) q4k_pair<3, DOTS>(sb, q4, g + 6, nb32, cb, dots, fs[6], fs[7], fx[6], fx[7], ad, am);
     return __builtin_fmaf(fd, ad, -(fdm * am));
 }
 
@@ -579,6 +580,11 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, ui
     // 1 and 3 there; the 6-bit value is then (ql nibble) | (the pair moved to bits 4-5), one
     // bit-field insert after at most one shift per operand.  Blocks go in the order 0, 2, 1, 3,
     // so that only one of the two masked sets is live at a time.
+    // the half's activation blocks g = 8s + 4n + t: pad_k(32 g) = 272 s + 128 n + 32 t (4n + t < 8),
+    // so one base per unit and constant offsets per block
+    const int8_t *const cb = A.codes + 272u * s + 128u * n;
+    const int32_t *const x16 = A.xs16 + 16u * s + 8u * n;
+    const float *const fb = A.fsc + 8u * s + 4u * n;
     uint32_t qm[8];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
@@ -589,7 +595,7 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, ui
             for (int i = 0; i < 8; ++i) qm[i] = ((t & 1) ? V(ph, i) >> 2 : V(ph, i)) & 0x33333333u;
         }
         if (DOTS && g >= nb32) continue;
-        const u32x4 *xv = reinterpret_cast<const u32x4 *>(A.codes + pad_k(32 * g));
+        const u32x4 *xv = reinterpret_cast<const u32x4 *>(cb + 32 * t);
         const u32x4 x0 = xv[0], x1 = xv[1];
         const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         int32_t Dlo = 0, Dhi = 0;
@@ -606,8 +612,8 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, ui
             else
                 Dhi = i == 4 ? ah_sdot4_first(uu, xw[i]) : ah_sdot4(uu, xw[i], Dhi);
         }
-        Dlo -= 32 * A.xs16[2 * g];
-        Dhi -= 32 * A.xs16[2 * g + 1];
+        Dlo -= 32 * x16[2 * t];
+        Dhi -= 32 * x16[2 * t + 1];
         if (DOTS && dots16) {
             dots16[2 * g] = Dlo;
             if (2 * g + 1 < nb16) dots16[2 * g + 1] = Dhi;  // ragged row ends on a 16-group
@@ -616,7 +622,7 @@ AH_DEV float unit_q6(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, ui
         // the block's two scale-weighted group dots as one integer (|sc * D| < 2^23, 24-bit
         // multiplies); d multiplies once per unit
         const int32_t I = __mul24((int)(int8_t)(sw & 0xffu), Dlo) + __mul24((int)(int8_t)((sw >> 8) & 0xffu), Dhi);
-        acc = __builtin_fmaf(A.fsc[g], (float)I, acc);
+        acc = __builtin_fmaf(fb[t], (float)I, acc);
     }
     return fd * acc;
 }
@@ -668,12 +674,16 @@ AH_DEV float unit_k23(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, u
     // and each 32-block adds one f32 term per sum; d and dmin multiply once per unit.
     float aI = 0.0f, aM = 0.0f;
     int32_t Ip = 0, Mp = 0;
+    // the half's 16-groups g = 16s + 8n + j: pad_k(16 g) = 272 s + 128 n + 16 j (8n + j < 16)
+    const int8_t *const cb = A.codes + 272u * s + 128u * n;
+    const int32_t *const x16 = A.xs16 + 16u * s + 8u * n;
+    const float *const fb = A.fsc + 8u * s + 4u * n;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int r = j >> 1, pl = j & 1;
         const uint32_t g = 16 * s + 8 * n + (uint32_t)j;  // 16-group of the row
         if (DOTS && g >= nb16) break;
-        const u32x4 xv = *reinterpret_cast<const u32x4 *>(A.codes + pad_k(16 * g));
+        const u32x4 xv = *reinterpret_cast<const u32x4 *>(cb + 16 * j);
         const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
         // Bit pairs r = 1, 2 are masked in place: each byte then holds its value times 4^r (at most
         // 7 * 16 = 112, still a positive int8), so the dot is 4^r D exactly and one shift recovers
@@ -691,7 +701,7 @@ AH_DEV float unit_k23(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, u
             D = i == 0 ? ah_sdot4_first(v, xw[i]) : ah_sdot4(v, xw[i], D);
         }
         if (r == 1 || r == 2) D >>= 2 * r;
-        const int32_t X = A.xs16[g];
+        const int32_t X = x16[j];
         const uint32_t sb = (sw[j >> 2] >> (8 * (j & 3))) & 0xffu;
         if constexpr (Q3) {
             D -= 4 * X;
@@ -704,7 +714,7 @@ AH_DEV float unit_k23(const uint8_t *tl, uint32_t off, uint32_t s, uint32_t n, u
         }
         // the 32-block's end (or, in the debug form, the ragged row's last group)
         if ((j & 1) || (DOTS && g + 1 >= nb16)) {
-            const float f = A.fsc[g >> 1];
+            const float f = fb[j >> 1];
             aI = __builtin_fmaf(f, (float)Ip, aI);
             if constexpr (!Q3) aM = __builtin_fmaf(f, (float)Mp, aM);
             Ip = 0;

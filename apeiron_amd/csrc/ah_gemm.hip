@@ -918,9 +918,12 @@ AH_DEV __attribute__((always_inline)) void gemm_rb_body(GemmArgs a, uint8_t *lds
                         const uint32_t T = 32 * m + j;
                         const f16x8 am = *reinterpret_cast<const f16x8 *>(xmin_lds + (T / kXT) * 1024u + (T % kXT) * 32u + 16u * h);
                         const f32x16 pm = mfma(am, bm, (f32x16){});
+                        // the d P pass first (it needs no pm), then the dmin pass: the same two
+                        // FMAs per element as one fused chain, while the min MFMA completes
 #pragma unroll
-                        for (int r = 0; r < 16; ++r)
-                            acc[m][n][r] = __builtin_fmaf(-fdm[n], pm[r], __builtin_fmaf(fd[n], P[m][n][r], acc[m][n][r]));
+                        for (int r = 0; r < 16; ++r) acc[m][n][r] = __builtin_fmaf(fd[n], P[m][n][r], acc[m][n][r]);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[m][n][r] = __builtin_fmaf(-fdm[n], pm[r], acc[m][n][r]);
                         P[m][n] = (f32x16){};
                     }
                 }
@@ -1745,9 +1748,11 @@ __global__ void __launch_bounds__(256, 2) gemm_dq_kernel(GemmArgs a) {
 #pragma unroll
                 for (uint32_t m = 0; m < 2; ++m) {
                     const f32x16 pm = mfma(am[m], bm, (f32x16){});
+                    // d P first, then dmin' pm (the same FMAs per element), while the MFMA completes
 #pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        acc[m][n][e] = __builtin_fmaf(-fdm, pm[e], __builtin_fmaf(fd, P[m][n][e], acc[m][n][e]));
+                    for (int e = 0; e < 16; ++e) acc[m][n][e] = __builtin_fmaf(fd, P[m][n][e], acc[m][n][e]);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[m][n][e] = __builtin_fmaf(-fdm, pm[e], acc[m][n][e]);
                     P[m][n] = (f32x16){};
                 }
             }

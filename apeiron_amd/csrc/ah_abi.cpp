@@ -209,8 +209,8 @@ constexpr uint32_t kQ4kPairTiles = 512;
 
 uint32_t kpad_of(size_t n_in) { return (uint32_t)((n_in + 255) / 256 * 256); }
 
-// Two kernels serve the GEMV.  The streaming kernel (rows up to one 8 KB tile) gives every wave a
-// contiguous range of whole rows; the workgroup-tile kernel serves longer rows.  make_part fills
+// Two kernels serve the GEMV.  The streaming kernel (rows up to one 8 KB tile) deals a part's
+// tiles of whole rows to its waves; the workgroup-tile kernel serves longer rows.  make_part fills
 // a part's geometry; deal_wgs then sizes every part's workgroup count.
 
 GemvPart make_part(const ah_tensor *w, uint32_t src, const void *x, const int64_t *scales, float *y,
@@ -348,7 +348,9 @@ uint32_t deal_wgs(GemvPart *parts, size_t n, uint64_t target, bool stream) {
 // A workgroup quantizes the activation of every part its waves use into its own LDS region, so
 // a workgroup takes at most 8 parts and `act_budget` bytes of activations: a part that would
 // overflow it starts the next workgroup (the waves skipped are idle).  Wave k of a part with n
-// waves streams tiles [T*k/n, T*(k+1)/n).  Returns the workgroup count (0: does not fit).
+// waves gets the contiguous tiles [T*k/n, T*(k+1)/n) (r_begin / r_end, the persistent
+// sequence's form) and, for the streaming kernel, the same count of tiles strided: k, k + n, ...
+// (t_first / t_stride).  Returns the workgroup count (0: does not fit).
 uint32_t deal_waves(const GemvPart *parts, size_t n, uint32_t n_wg, size_t act_budget, StreamWG *out) {
     const uint64_t W = (uint64_t)n_wg * 8;
     if (n > W) return 0;

@@ -368,12 +368,12 @@ __global__ void scan_scales_kernel(const uint8_t *w, uint64_t n_blocks, uint32_t
 
 // ---- streaming GEMV ---------------------------------------------------------------------------
 //
-// Each wave owns a contiguous range of whole rows of its part (the part's rows split evenly over
-// its waves) and streams them in tiles of whole rows, at most kStreamTile bytes each.  A tile is
-// read with 16-byte buffer loads in which lane l takes chunks l, l+64, ... (each load instruction
-// reads 1 KB contiguous; a chunk past the tile takes an out-of-range offset and reads nothing),
-// held in registers while the wave computes the previous tile from its LDS slot, then written to
-// the slot.  Eight waves share a workgroup and its quantized activation; the tile loop has no
+// A part's rows are cut into tiles of whole rows, at most kStreamTile bytes each, and its waves
+// take the tiles strided (wave k of n: tiles k, k + n, ...), so the tiles in flight at any time
+// are adjacent in memory.  A tile is read with 16-byte buffer loads in which lane l takes chunks
+// l, l+64, ... (each load instruction reads 1 KB contiguous; a chunk past the tile takes an
+// out-of-range offset and reads nothing), held in registers while the wave computes the previous
+// tile from its LDS slot, then written to the slot.  Eight waves share a workgroup and its quantized activation; the tile loop has no
 // workgroup barrier.
 //
 // The activation loads go out before the first tile's, so waiting for them does not wait for the

@@ -309,6 +309,43 @@ def test_gemm_f32_input_wide_spread_tokens(dev, t):
         w.free()
 
 
+@pytest.mark.parametrize("t", [6, 8, 10, 11, 12, 14])
+def test_gemm_exact_path_every_row_to_the_payload_end(dev, t):
+    """Flagged tokens (blocks spanning 40 binades, past the f16 band) checked at every row, the
+    last included: the exact path reads each weight unit from memory, and a unit within 16 bytes
+    of the payload's end takes the byte-exact row form instead.  Twenty flagged tokens, more than
+    one batch (8) per token tile, on an uploaded payload (its device size is the payload's) and on
+    a wrapped one of exactly the payload's bytes."""
+    rng = np.random.default_rng(1234 + t)
+    n_out, n_in, n_tok = 72, 1024, 40
+    raw = synth.payload(t, rng, n_out, n_in)
+    x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
+    nb = n_in // 32
+    spread = np.repeat(np.exp2(np.arange(nb) * 40.0 / nb - 20.0), 32).astype(np.float32)
+    for tok in range(0, n_tok, 2):
+        x[tok] *= spread
+    ref = []
+    for c in range(n_tok):
+        sto, codes, scales = oracle.quant_act_f32(x[c])
+        assert sto == 0
+        st1, yref = oracle.matvec_q8act(t, raw, n_out, n_in, codes, scales)
+        st2, absdot = oracle.row_absdot(t, raw, n_out, n_in, codes, scales)
+        assert st1 == 0 and st2 == 0
+        ref.append((yref.astype(np.float64) * Q32, absdot))
+    draw = to_dev(raw)
+    for form in ("upload", "wrap"):
+        if form == "upload":
+            w = dev.upload(t, raw, n_out, n_in)
+        else:
+            w = dev.wrap(t, draw.data_ptr(), raw.nbytes, n_out, n_in)
+        st, Y = gemm_f32(dev, w, x)
+        assert st == 0, (t, form)
+        for c, (yr, absdot) in enumerate(ref):
+            err = np.abs(Y[c].astype(np.float64) - yr)
+            assert (err <= TOL * absdot + Q32).all(), (t, form, c, int(np.argmax(err)), err.max())
+        w.free()
+
+
 def test_refusal_classes_match_reference(dev):
     """chart/tests.rs:525-560 through the GPU forms: each refusal class gives the contract's."""
     rng = np.random.default_rng(7)

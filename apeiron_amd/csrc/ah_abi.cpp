@@ -417,7 +417,10 @@ uint32_t deal_waves(const GemvPart *parts, size_t n, uint32_t n_wg, size_t act_b
                 if (wi == 0 || k == 0) {
                     if (wi == 0) {
                         std::memset(&D, 0, sizeof(D));
-                        for (int i = 0; i < 8; ++i) D.wave_part[i] = kIdleWave;
+                        for (int i = 0; i < 8; ++i) {
+                            D.wave_part[i] = kIdleWave;
+                            D.t_stride[i] = 1;  // an idle wave streams no tiles (its row range is empty)
+                        }
                     }
                     D.act_part[D.n_act] = (uint32_t)p;
                     D.act_off[D.n_act] = D.n_act ? D.act_off[D.n_act - 1] + (uint32_t)actb(D.act_part[D.n_act - 1]) : 0u;

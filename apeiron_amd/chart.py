@@ -99,7 +99,7 @@ class Device:
     def set_gemm_design(self, ggml_type: int, design: int) -> None:
         """The prefill GEMM design of `ggml_type` on this context (ah_set_gemm_design).  AUTO is
         F16 for every type but Q2_K and Q3_K, where it is F16_TILE (the dequantize-once tiles);
-        INT8 exists for Q8_0 only, F16_TILE for Q4_K, Q2_K and Q3_K; F16 on Q2_K / Q3_K serves the
+        INT8 exists for Q8_0 and Q4_K, F16_TILE for Q4_K, Q2_K and Q3_K; F16 on Q2_K / Q3_K serves the
         prefill as one streaming GEMV per token."""
         _check(self.lib.ah_set_gemm_design(self.h, ggml_type, design), "set_gemm_design")
 

@@ -42,7 +42,7 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
                           uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xf, const _Float16 *xmin,
                           const _Float16 *xmin16,
                           const float *tok_scale, const int8_t *fcodes, const int64_t *fscales,
-                          const int8_t *xc, const uint32_t *xsp,
+                          const int8_t *xc, const uint32_t *xsp, const uint32_t *xsx,
                           unsigned long long *status, uint32_t form, hipStream_t stream,
                           const GemmFfn *ffn = nullptr);
 hipError_t ah_launch_splitk_reduce(uint32_t n_parts, const GemmPartDesc *parts, uint32_t n_tok,
@@ -542,13 +542,14 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     if (!x && n_tok && n_in_sz) return AH_ERR_INVALID_ARG;
     if (n_tok == 0) return AH_OK;
     if (n_tok >= (1ull << 24)) return AH_ERR_INVALID_ARG;
-    // The design of each part's type (ah_set_gemm_design): Q8_0 parts take the int8-MFMA design
-    // when it is selected, the operand pass then writing int8 codes and block factors (and the f16
-    // operand only if another part needs it); Q4_K parts may take the dequantize-once tiles.
+    // The design of each part's type (ah_set_gemm_design): Q8_0 and Q4_K parts take the int8-MFMA
+    // design when it is selected, the operand pass then writing int8 codes and block factors (for
+    // Q4_K also the scaled code sums; the f16 operand only if another part needs it); Q4_K parts
+    // may take the dequantize-once tiles.
     auto kind_of = [&](uint32_t type) -> uint32_t {
         if (ffn) return kGemmKindTile;  // the fused FFN form runs on the dequantize-once tiles
         const uint32_t d = type < 32 ? ctx->design[type] : 0u;
-        if (type == AH_GGML_Q8_0 && d == AH_GEMM_DESIGN_INT8) return kGemmKindI8;
+        if ((type == AH_GGML_Q8_0 || type == AH_GGML_Q4_K) && d == AH_GEMM_DESIGN_INT8) return kGemmKindI8;
         if (type == AH_GGML_Q4_K && d == AH_GEMM_DESIGN_F16_TILE) return kGemmKindTile;
         // Q2_K / Q3_K: the tiles are their only MFMA design (AH_GEMM_DESIGN_F16 keeps the
         // per-token GEMV route)
@@ -650,10 +651,11 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     const uint32_t n_in = (uint32_t)n_in_sz, N = (uint32_t)n_tok;
     const uint32_t kpad = kpad_of(n_in), nb32 = (n_in + 31) / 32, nsb = kpad / 256;
     const uint32_t cus = (uint32_t)ctx->cu_count;
-    bool any_int8 = false, any_f16 = false, any_tile = false;
+    bool any_int8 = false, any_f16 = false, any_tile = false, any_i8q4 = false;
     for (size_t i = 0; i < n_parts; ++i) {
         const uint32_t k = kind_of(w[i]->type);
         any_int8 = any_int8 || k == kGemmKindI8;
+        any_i8q4 = any_i8q4 || (k == kGemmKindI8 && w[i]->type == AH_GGML_Q4_K);
         any_f16 = any_f16 || k == kGemmKindRb;
         any_tile = any_tile || k == kGemmKindTile;
     }
@@ -694,6 +696,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     const size_t o_xf = off; off = align256(off + (any_tile ? (size_t)((N + 31) / 32 * 32) * kpad * 2 : 0));
     const size_t o_xc = off; off = align256(off + (any_int8 ? (size_t)N * kpad : 0));
     const size_t o_xsp = off; off = align256(off + (any_int8 ? (size_t)N * (kpad / 32) * 4 : 0));
+    const size_t o_xsx = off; off = align256(off + (any_i8q4 ? (size_t)N * (kpad / 32) * 4 : 0));
     const size_t o_ts = off; off = align256(off + (size_t)N * 4);
     const size_t o_xmin = off; off = align256(off + (any_q4k ? (size_t)N * nsb * 32 : 0));
     bool any_k23 = false;
@@ -716,6 +719,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     _Float16 *xf = any_tile ? reinterpret_cast<_Float16 *>(S + o_xf) : nullptr;
     int8_t *xc = any_int8 ? reinterpret_cast<int8_t *>(S + o_xc) : nullptr;
     uint32_t *xsp = any_int8 ? reinterpret_cast<uint32_t *>(S + o_xsp) : nullptr;
+    uint32_t *xsx = any_i8q4 ? reinterpret_cast<uint32_t *>(S + o_xsx) : nullptr;
     float *ts = reinterpret_cast<float *>(S + o_ts);
     _Float16 *xmin = reinterpret_cast<_Float16 *>(S + o_xmin);
     _Float16 *xmin16 = any_k23 ? reinterpret_cast<_Float16 *>(S + o_xmin16) : nullptr;
@@ -739,6 +743,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     o.fscales = keep ? fscales : nullptr;
     o.xc = xc;
     o.xsp = xsp;
+    o.xsx = xsx;
     o.status = status;
     o.n_tok = N;
     o.n_in = n_in;
@@ -748,7 +753,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
     AH_HIP(ctx, ah_launch_gemm_operand(o, s));
     if (ffn) {
         if (pd[0].n_out == 0) return AH_OK;
-        AH_HIP(ctx, ah_launch_gemm(w[0]->type, 1, pd, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp,
+        AH_HIP(ctx, ah_launch_gemm(w[0]->type, 1, pd, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp, xsx,
                                    status, kFormTileFfn, s, ffn));
         return AH_OK;
     }
@@ -771,7 +776,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
                 run[nr++] = pd[i];
                 any_split = any_split || pd[i].splits > 1;
             }
-            AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp,
+            AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp, xsx,
                                        status, kFormTile, s));
             continue;
         }
@@ -791,7 +796,9 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
             }
             if (types == 3u && g4 <= 2ull * cus) type = kGemmMixedKQuant;
         }
-        const uint32_t max_run = type == kGemmMixedKQuant ? kGemmMaxParts : ah_gemm_max_parts(type);
+        // (an int8 launch takes one part)
+        const uint32_t max_run = type == kGemmMixedKQuant ? kGemmMaxParts
+                                 : kind_of(type) == kGemmKindI8 ? 1u : ah_gemm_max_parts(type);
         for (; i < n_parts && nr < max_run; ++i) {
             if (pd[i].n_out == 0) continue;
             const bool fits = type == kGemmMixedKQuant
@@ -806,7 +813,7 @@ int32_t gemm_group_launch(ah_ctx *ctx, size_t n_parts, const ah_tensor *const *w
         const uint32_t form = type == kGemmMixedKQuant
                                   ? kForm4x4
                                   : ah_gemm_pick_waves(type, wg4, cus, kind_of(type) == kGemmKindI8);
-        AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp,
+        AH_HIP(ctx, ah_launch_gemm(type, nr, run, n_in, N, kpad, xh, xf, xmin, xmin16, ts, fcodes, fscales, xc, xsp, xsx,
                                    status, form, s));
     }
     if (any_split) AH_HIP(ctx, ah_launch_splitk_reduce((uint32_t)n_parts, pd, N, ts, status, s));
@@ -1702,7 +1709,8 @@ int32_t ah_set_gemm_design(ah_ctx *ctx, uint32_t ggml_type, uint32_t design) {
     if (!ctx || design > AH_GEMM_DESIGN_F16_TILE) return AH_ERR_INVALID_ARG;
     size_t qk = 0, bb = 0;
     if (!geom(ggml_type, qk, bb) || ggml_type >= 32) return AH_ERR_UNSUPPORTED_QUANT;
-    if (design == AH_GEMM_DESIGN_INT8 && ggml_type != AH_GGML_Q8_0) return AH_ERR_UNSUPPORTED_QUANT;
+    if (design == AH_GEMM_DESIGN_INT8 && ggml_type != AH_GGML_Q8_0 && ggml_type != AH_GGML_Q4_K)
+        return AH_ERR_UNSUPPORTED_QUANT;
     if (design == AH_GEMM_DESIGN_F16_TILE && ggml_type != AH_GGML_Q4_K && !ah_k23((int)ggml_type))
         return AH_ERR_UNSUPPORTED_QUANT;
     ctx->design[ggml_type] = design;

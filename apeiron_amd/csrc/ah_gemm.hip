@@ -111,6 +111,7 @@ struct GemmArgs {
     const int64_t *fscales;    // [n_tok][nb32] their scales
     const int8_t *xc;          // int8 design: codes [n_tok][kpad] (zero past n_in)
     const uint32_t *xsp;       // int8 design: [n_tok][kpad/32] block factors 2^(e_b - E_tok), bf16 x2
+    const uint32_t *xsx;       // int8 Q4_K: [n_tok][kpad/32] 2^(e_b - E_tok) X_b as bf16 (hi, lo)
     uint32_t n_wg;             // real workgroup count over all parts
     GemmFfn ffn;               // kFormTileFfn: the up projection and the hidden QuantAct outputs
 };
@@ -984,8 +985,11 @@ namespace i8 {
 constexpr uint32_t kTok = 128, kKS = 128, kR = 3;
 constexpr uint32_t kAct = kTok * kKS;       // activation codes of a slot
 constexpr uint32_t kSlot = kAct + 4096;     // + block factors (one 1 KB load per wave)
+// Q4_K also stages the tokens' scaled block code sums (one more 1 KB load per wave)
+template <int TYPE> constexpr uint32_t slot_bytes() { return kSlot + (TYPE == AH_GGML_Q4_K ? 4096u : 0u); }
+template <int TYPE> constexpr int side_loads() { return TYPE == AH_GGML_Q4_K ? 2 : 1; }
 template <int W> constexpr int an() { return (int)(kAct / 1024) / W; }
-template <int W> constexpr int wait_count() { return (int)(kR - 2) * (an<W>() + 1); }
+template <int TYPE, int W> constexpr int wait_count() { return (int)(kR - 2) * (an<W>() + side_loads<TYPE>()); }
 constexpr uint32_t stages(uint32_t n_in) { return ((n_in + 31) / 32 + 3) / 4; }
 }  // namespace i8
 
@@ -993,11 +997,25 @@ typedef int v4i8x4 __attribute__((ext_vector_type(4)));     // 16 int8 codes
 typedef int v16i32 __attribute__((ext_vector_type(16)));
 typedef short v4bf16 __attribute__((ext_vector_type(4)));   // 4 bf16 bit patterns
 
-template <int W>
+// v = a + b + c exactly as three bf16 (the top 8 significant bits, the next 8, the rest), for an
+// f32 of at most 24 significant bits whose remainder after 16 fits a bf16 (here d sc and dmin m:
+// an f16 times a 6-bit integer, at most 17 bits); the slots [a, b, c, 0] of a bf16 MFMA operand.
+AH_DEV v4bf16 bf16x3(float v) {
+    const uint32_t a = __builtin_bit_cast(uint32_t, v) & 0xffff0000u;
+    const float r = v - __builtin_bit_cast(float, a);  // exact: the bits below a's
+    const uint32_t b = __builtin_bit_cast(uint32_t, r) & 0xffff0000u;
+    const uint32_t c = __builtin_bit_cast(uint32_t, r - __builtin_bit_cast(float, b)) & 0xffff0000u;
+    return __builtin_bit_cast(v4bf16, (u32x2){(a >> 16) | b, c >> 16});
+}
+
+template <int TYPE, int W>
 __global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
+    static_assert(TYPE == AH_GGML_Q8_0 || TYPE == AH_GGML_Q4_K, "the int8 design serves Q8_0 and Q4_K");
+    constexpr bool Q4 = TYPE == AH_GGML_Q4_K;
     constexpr int NM = 4, AN = i8::an<W>();
     constexpr uint32_t TPW = i8::kTok / W;  // tokens whose block factors one wave loads
-    __shared__ __align__(16) uint8_t lds[i8::kR * i8::kSlot];
+    constexpr uint32_t kSlotB = i8::slot_bytes<TYPE>();
+    __shared__ __align__(16) uint8_t lds[i8::kR * kSlotB];
     const uint32_t per = gridDim.x >> 3;  // XCD-aware order, as gemm_rb_body
     const uint32_t L = (blockIdx.x & 7u) * per + (blockIdx.x >> 3);
     if (L >= a.n_wg) return;
@@ -1017,11 +1035,12 @@ __global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t rs = ah_rsrc(pa.w, pa.w_bytes);
     const __amdgpu_buffer_rsrc_t rx = ah_rsrc(a.xc + (size_t)tok0 * a.kpad, ntile * a.kpad);
     const __amdgpu_buffer_rsrc_t rp = ah_rsrc(a.xsp + (size_t)tok0 * nbp, ntile * nbp * 4u);
+    const __amdgpu_buffer_rsrc_t rq = ah_rsrc(Q4 ? a.xsx + (size_t)tok0 * nbp : a.xsp, Q4 ? ntile * nbp * 4u : 0u);
     const uint32_t nstages = i8::stages(a.n_in);
     const uint32_t st_begin = split * pa.stages_per_split;
     const uint32_t st_end = st_begin + pa.stages_per_split < nstages ? st_begin + pa.stages_per_split : nstages;
 
-    auto slot = [&](uint32_t k) -> uint8_t * { return lds + k * i8::kSlot; };
+    auto slot = [&](uint32_t k) -> uint8_t * { return lds + k * kSlotB; };
     // slice of stage st: wave w's instruction i fills slot bytes [(w*AN + i) KB, +1 KB), lane l at
     // +16 l: token t = o / 128 at LDS chunk (o / 16) % 8, which holds the token's K chunk
     // ((o / 16) % 8) ^ ((t >> 1) & 7); then its block factors, lanes < TPW taking tokens w*TPW + l
@@ -1039,6 +1058,10 @@ __global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rp, (__attribute__((address_space(3))) void *)(buf + i8::kAct + wv * 1024u), 16,
             live && lane < TPW && t < ntile ? (t * nbp + 4 * st) * 4u : kOob, 0, 0, 0);
+        if constexpr (Q4)  // the tokens' scaled code sums of the stage's four blocks, the same way
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rq, (__attribute__((address_space(3))) void *)(buf + i8::kSlot + wv * 1024u), 16,
+                live && lane < TPW && t < ntile ? (t * nbp + 4 * st) * 4u : kOob, 0, 0, 0);
     };
     // weight bytes of stage st for row j: per block the lane half's 16 codes (4-aligned window
     // plus the dword after it) and, for half 0, the dword holding d
@@ -1046,9 +1069,19 @@ __global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
         u32x4 v[4];
         uint32_t s[4], d[4];
     };
+    // Q4_K: a stage is half a super-block (sub-blocks 4 (st & 1) .. + 3, pairs 2 (st & 1) and
+    // 2 (st & 1) + 1): v[0] = the super-block's header (d, dmin, the 12 scale bytes), v[1] / v[2]
+    // = the lane half's 16 qs bytes of the two pairs (low nibbles: the pair's first sub-block)
     auto fetch = [&](uint32_t st) -> Wt {
         Wt f;
         const bool live = st < st_end && rl[0];
+        if constexpr (Q4) {
+            const uint32_t sb = rbase[0] + 144u * (st >> 1), p0 = 2u * (st & 1u);
+            f.v[0] = ah_ld128(rs, live ? sb : kOob);
+            f.v[1] = ah_ld128(rs, live ? sb + 16u + 32u * p0 + 16u * h : kOob);
+            f.v[2] = ah_ld128(rs, live ? sb + 48u + 32u * p0 + 16u * h : kOob);
+            return f;
+        }
 #pragma unroll
         for (int bb = 0; bb < 4; ++bb) {
             const uint32_t b = 4 * st + bb;
@@ -1068,6 +1101,52 @@ __global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
     auto compute = [&](const uint8_t *buf, const Wt &f, uint32_t st) {
         v4i8x4 A[4];
         v4bf16 Dp[4];
+        if constexpr (Q4) {
+            // Per sub-block j: the int8 MFMA gives the exact dots D of the codes q (0..15) and the
+            // token's codes; the fold is acc += D (2^(e - E) d sc_j) - (2^(e - E) X) (dmin m_j),
+            // both products formed exactly-split by a bf16 MFMA as outer products: the token
+            // side 2^(e - E) (one bf16) and 2^(e - E) X (two, hi and lo, the operand pass's xsx),
+            // the row side d sc_j and dmin m_j (at most 17 bits: three bf16 each, bf16x3).
+            const u32x4 hd = f.v[0];
+            const uint32_t par = st & 1u;
+            const float d = ah_f16_bits_to_f32(hd.x & 0xffffu), dmin = ah_f16_bits_to_f32(hd.x >> 16);
+            const uint32_t scw = par ? (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u) : hd.y & 0x3F3F3F3Fu;
+            const uint32_t mw = par ? ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u) : hd.z & 0x3F3F3F3Fu;
+            v4bf16 Mp[4];
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                const u32x4 q = f.v[1 + (bb >> 1)];
+                const uint32_t sh = (bb & 1) ? 4u : 0u;
+                A[bb] = (v4i8x4){(int)((q.x >> sh) & 0x0F0F0F0Fu), (int)((q.y >> sh) & 0x0F0F0F0Fu),
+                                 (int)((q.z >> sh) & 0x0F0F0F0Fu), (int)((q.w >> sh) & 0x0F0F0F0Fu)};
+                const float ds = d * (float)((scw >> (8 * bb)) & 0xffu);
+                const float dm = dmin * (float)((mw >> (8 * bb)) & 0xffu);
+                Dp[bb] = h ? (v4bf16){0, 0, 0, 0} : bf16x3(ds);  // the scale's slots: K 0..3 only
+                Mp[bb] = bf16x3(dm);                             // the min's: K 0..3 and 4..7
+            }
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const uint32_t t = 32 * m + j;
+                const u32x4 sv = *reinterpret_cast<const u32x4 *>(buf + i8::kAct + (t / TPW) * 1024u + (t % TPW) * 16u);
+                const u32x4 xv = *reinterpret_cast<const u32x4 *>(buf + i8::kSlot + (t / TPW) * 1024u + (t % TPW) * 16u);
+                const uint32_t s4[4] = {sv.x, sv.y, sv.z, sv.w}, x4[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) {
+                    const v4i8x4 B = *reinterpret_cast<const v4i8x4 *>(buf + t * i8::kKS + 16 * ((uint32_t)(2 * bb + h) ^ sw));
+                    const v16i32 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(B, A[bb], (v16i32){}, 0, 0, 0);
+                    // token factor f in K slots 0..2 (half 0); the scaled code sum's hi piece in
+                    // slots 0..2 and its lo piece in slots 4..6
+                    const uint32_t fb = s4[bb] & 0xffffu, xb = h ? x4[bb] >> 16 : x4[bb] & 0xffffu;
+                    const u32x2 sp = {h ? 0u : fb | (fb << 16), h ? 0u : fb};
+                    const u32x2 xp2 = {xb | (xb << 16), xb};
+                    const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(v4bf16, sp), Dp[bb], (f32x16){}, 0, 0, 0);
+                    const f32x16 Pm = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(v4bf16, xp2), Mp[bb], (f32x16){}, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[m][0][r] = __builtin_fmaf((float)D[r], P[r], acc[m][0][r]) - Pm[r];
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int bb = 0; bb < 4; ++bb) {
             const uint32_t blk = rbase[0] + 34 * (4 * st + bb);
@@ -1108,7 +1187,7 @@ __global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     uint32_t k = 0;  // slot of the current stage
     for (uint32_t st = st_begin; st < st_end; st += 2) {
-        ah_vm_lds_barrier<i8::wait_count<W>()>();  // slice st (and weights st) landed; slot k+2 free
+        ah_vm_lds_barrier<i8::wait_count<TYPE, W>()>();  // slice st (and weights st) landed; slot k+2 free
         F1 = fetch(st + 1);
         __builtin_amdgcn_sched_barrier(0);
         dma(slot(k == 0 ? 2u : k - 1), st + 2);
@@ -1116,7 +1195,7 @@ __global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
         compute(slot(k), F0, st);
         k = k == 2 ? 0u : k + 1;
         if (st + 1 >= st_end) break;
-        ah_vm_lds_barrier<i8::wait_count<W>()>();
+        ah_vm_lds_barrier<i8::wait_count<TYPE, W>()>();
         F0 = fetch(st + 2);
         __builtin_amdgcn_sched_barrier(0);
         dma(slot(k == 0 ? 2u : k - 1), st + 3);
@@ -1126,10 +1205,12 @@ __global__ void __launch_bounds__(64 * W, 2) gemm_i8_kernel(GemmArgs a) {
     }
     // the slices requested past the split must land before this workgroup's LDS is released
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    static_assert(i8::kR * i8::kSlot >= xp::kWinBytes + 4 * xp::kBatch * 256u,
+    static_assert(i8::kR * kSlotB >= xp::kWinBytes + 4 * xp::kBatch * 256u,
                   "the exact path stages a token window and its sums in the slots");
-    gemm_store<AH_GGML_Q8_0, NM, 1>(a, pa, acc, row_w, rl, rbase, tok0, ntile, split, 4 * st_begin, 4 * st_end, lds,
-                                    i8::kR * i8::kSlot);
+    // the split's K range in the exact path's units: Q8_0 blocks, Q4_K super-blocks (splits are
+    // whole super-blocks: two stages)
+    gemm_store<TYPE, NM, 1>(a, pa, acc, row_w, rl, rbase, tok0, ntile, split, Q4 ? st_begin / 2 : 4 * st_begin,
+                            Q4 ? (st_end + 1) / 2 : 4 * st_end, lds, i8::kR * kSlotB);
 }
 
 // Q4_K and Q6_K parts of one input in one grid (4 waves, 4 slots sized for the larger type):
@@ -1789,7 +1870,8 @@ struct GemmGeom {
 };
 GemmGeom geom_of(uint32_t type, uint32_t n_in, uint32_t kpad, uint32_t waves = 4, uint32_t kind = kGemmKindRb) {
     const uint32_t rows = 32u * rb::kNN * waves;
-    if (kind == kGemmKindI8) return {i8::stages(n_in), 1, rows, i8::kTok};  // stages of 4 blocks
+    // int8: stages of 4 blocks (Q4_K: half super-blocks, split in whole super-blocks)
+    if (kind == kGemmKindI8) return {i8::stages(n_in), type == AH_GGML_Q4_K ? 2u : 1u, rows, i8::kTok};
     if (kind == kGemmKindTile) return {kpad / kKS, 4, dq::kBM, dq::kBN};
     if (ah_blk32((int)type)) return {(n_in + 2 * kKS - 1) / (2 * kKS) * 2, 2, rows, rb::tok_of(type)};
     return {kpad / kKS, 4, rows, rb::tok_of(type)};  // K-quants: whole super-blocks
@@ -1958,7 +2040,7 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
                           uint32_t n_tok, uint32_t kpad, const _Float16 *xh, const _Float16 *xf, const _Float16 *xmin,
                           const _Float16 *xmin16,
                           const float *tok_scale, const int8_t *fcodes, const int64_t *fscales,
-                          const int8_t *xc, const uint32_t *xsp,
+                          const int8_t *xc, const uint32_t *xsp, const uint32_t *xsx,
                           unsigned long long *status, uint32_t form, hipStream_t stream, const GemmFfn *ffn) {
     const bool mixed = type == kGemmMixedKQuant;  // Q4_K and Q6_K parts, 4-wave form
     const bool int8 = form == kFormI8x4 || form == kFormI8x2;
@@ -1967,7 +2049,9 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     if (n_parts == 0 || n_parts > (mixed || tile ? kGemmMaxParts : rb::max_parts_of(type))) return hipErrorInvalidValue;
     if (ffn_form && (!ffn || !ffn->w_up || !ffn->h_codes || !ffn->h_scales || n_parts != 1 || parts[0].splits > 1))
         return hipErrorInvalidValue;
-    if (int8 && (type != AH_GGML_Q8_0 || !xc || !xsp)) return hipErrorInvalidValue;
+    if (int8 && ((type != AH_GGML_Q8_0 && type != AH_GGML_Q4_K) || !xc || !xsp || (type == AH_GGML_Q4_K && !xsx) ||
+                 n_parts != 1))
+        return hipErrorInvalidValue;
     if (tile && (!xf || (type != AH_GGML_Q4_K && type != AH_GGML_Q2_K && type != AH_GGML_Q3_K) ||
                  (type != AH_GGML_Q4_K && !xmin16)))
         return hipErrorInvalidValue;
@@ -1989,6 +2073,7 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
     a.fscales = fscales;
     a.xc = xc;
     a.xsp = xsp;
+    a.xsx = xsx;
     a.ffn = ffn_form ? *ffn : GemmFfn{};
     uint32_t wg = 0;
     for (uint32_t i = 0; i < kGemmMaxParts; ++i) {
@@ -2039,11 +2124,13 @@ hipError_t ah_launch_gemm(uint32_t type, uint32_t n_parts, const GemmPartDesc *p
         return hipGetLastError();
     }
     if (form == kFormI8x4) {
-        hipLaunchKernelGGL(gemm_i8_kernel<4>, rb_grid, blk, 0, stream, a);
+        if (type == AH_GGML_Q4_K) hipLaunchKernelGGL((gemm_i8_kernel<AH_GGML_Q4_K, 4>), rb_grid, blk, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_i8_kernel<AH_GGML_Q8_0, 4>), rb_grid, blk, 0, stream, a);
         return hipGetLastError();
     }
     if (form == kFormI8x2) {
-        hipLaunchKernelGGL(gemm_i8_kernel<2>, rb_grid, blk, 0, stream, a);
+        if (type == AH_GGML_Q4_K) hipLaunchKernelGGL((gemm_i8_kernel<AH_GGML_Q4_K, 2>), rb_grid, blk, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_i8_kernel<AH_GGML_Q8_0, 2>), rb_grid, blk, 0, stream, a);
         return hipGetLastError();
     }
     switch (type) {

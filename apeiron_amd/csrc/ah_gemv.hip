@@ -308,6 +308,14 @@ __global__ void __launch_bounds__(T) gemm_operand_kernel(OperandArgs o) {
             if (q == 0) {
                 const uint32_t bf = ex[u] < 0 ? 0u : (uint32_t)(ex[u] - E + 127) << 7;  // 2^(e-E) >= 2^-63
                 xsp[b] = bf | (bf << 16);
+                if (o.xsx) {
+                    // Q4_K: 2^(e-E) X_b (|X_b| <= 4064: 12 significant bits) as bf16 hi | lo << 16,
+                    // hi + lo exact
+                    const float xv = ex[u] < 0 ? 0.0f : __builtin_ldexpf((float)sum[u], ex[u] - E);
+                    const uint32_t hi = __builtin_bit_cast(uint32_t, xv) & 0xffff0000u;
+                    const uint32_t lo = __builtin_bit_cast(uint32_t, xv - __builtin_bit_cast(float, hi)) & 0xffff0000u;
+                    o.xsx[(size_t)tok * nbp + b] = (hi >> 16) | lo;
+                }
             }
         }
     }

@@ -369,6 +369,7 @@ struct OperandArgs {
     int64_t *fscales;      // [n_tok][nb32] (f32 input only; flagged rows written)
     int8_t *xc;            // int8 design: codes [n_tok][kpad] (zero past n_in), or nullptr
     uint32_t *xsp;         // int8 design: [n_tok][kpad/32] bf16 pairs of 2^(e_b - E_tok), or nullptr
+    uint32_t *xsx;         // int8 Q4_K: [n_tok][kpad/32] 2^(e_b - E_tok) X_b as bf16 (hi, lo), or nullptr
     unsigned long long *status;
     uint32_t n_tok, n_in, nb32, kpad, src;
 };

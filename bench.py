@@ -32,8 +32,8 @@ Also reported, beside the value:
                 launch floor: a graph of 113 minimal launches on one stream;
   config1       BASELINE configs[1] (Qwen2.5-0.5B, 24 layers, Q4_K) as one batched launch;
   gemm          configs[3] N = 512 GEMMs against the 5.0 POPS int8 MFMA peak (Q8_0 on both MFMA
-                designs, int8 and f16; Q4_K on the f16 and the dequantize-once tile designs), each
-                from pre-quantized codes and from the f32 input, the MFMA-only probe, the configs[4]
+                designs, int8 and f16; Q4_K on the f16, the dequantize-once tile and the int8
+                designs), each from pre-quantized codes and from the f32 input, the MFMA-only probe, the configs[4]
                 N = 512 prefill, and its FFN fused (gate/up + exact SwiGLU + hidden quant_act in one
                 launch) and two-pass (--only gemm3: the configs[3] GEMMs alone, for profiling);
   heads         configs[0] (Q8_0 4864x896) and configs[2] (151936x896 head, Q6_K and Q8_0);
@@ -458,9 +458,11 @@ def main() -> int:
             result["mfma_probe"] = probe
         gemm = []
         n_tok = 512
-        # Q8_0 on both MFMA designs (int8, the default, and f16); the K-quants have the f16 design
+        # Q8_0 on both MFMA designs (int8, the default, and f16); Q4_K on the f16 design (the
+        # default), the dequantize-once tiles and the int8 design
         for gt, design in ((synth.Q8_0, chart.Device.GEMM_INT8), (synth.Q8_0, chart.Device.GEMM_F16),
-                           (synth.Q4_K, chart.Device.GEMM_F16), (synth.Q4_K, chart.Device.GEMM_F16_TILE)):
+                           (synth.Q4_K, chart.Device.GEMM_F16), (synth.Q4_K, chart.Device.GEMM_F16_TILE),
+                           (synth.Q4_K, chart.Device.GEMM_INT8)):
             dname = {chart.Device.GEMM_INT8: "int8", chart.Device.GEMM_F16: "f16",
                      chart.Device.GEMM_F16_TILE: "f16 tiles"}[design]
             dev.set_gemm_design(gt, design)

@@ -317,7 +317,9 @@ int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
  * kern/gemm.rs:488-580); here several MFMA designs meet the same contract, selectable per context
  * and type for comparison (results agree within the tolerance, not bit for bit):
  *   AH_GEMM_DESIGN_INT8: v_mfma_i32_32x32x32_i8 exact block dots of the int8 codes, folded with
- *     d * 2^(e_b - E) formed exactly by a bf16 outer-product MFMA (no exponent band);
+ *     d * 2^(e_b - E) formed exactly by a bf16 outer-product MFMA (no exponent band); for Q4_K
+ *     the dots are per 32-element sub-block on the raw nibbles, folded with d sc_j and, for the
+ *     min term, dmin m_j times the token's scaled code sum (two more bf16 outer products);
  *   AH_GEMM_DESIGN_F16: v_mfma_f32_32x32x16_f16 on exact f16 operands (the K-quants' design);
  *   AH_GEMM_DESIGN_AUTO (the default): the F16 design, measured 17-25% faster on MI355X at the
  *     configs[3] shapes (N = 512).
@@ -326,7 +328,7 @@ int32_t ah_gemm_q8_dev(ah_ctx *ctx, const ah_tensor *w, const int8_t *d_codes,
  *     (sc * q, folded with d and the min term per super-block) once into LDS, and every wave
  *     feeds v_mfma_f32_32x32x16_f16 from that LDS copy and from activation fragments in
  *     registers.
- * Per type: Q8_0 takes AUTO, F16 or INT8; Q4_K takes AUTO (= F16), F16 or F16_TILE; Q2_K and
+ * Per type: Q8_0 takes AUTO, F16 or INT8; Q4_K takes AUTO (= F16), F16, INT8 or F16_TILE; Q2_K and
  * Q3_K take AUTO (= F16_TILE) or F16, which for these two types serves the prefill as one
  * streaming GEMV per token (the reference's matmat_q8act loop, chart/mod.rs:1955-1975); Q5_0,
  * Q6_K and Q8_K take AUTO or F16.  Any other pairing returns AH_ERR_UNSUPPORTED_QUANT. */

@@ -124,20 +124,20 @@ def test_no_slice_load_can_be_skipped(gemm_asm):
 
 
 def test_int8_design_ring(gemm_asm):
-    """The int8 Q8_0 kernel (W waves, 3-slot ring, stages of 4 blocks): each wave issues 16/W
-    activation loads and one block-factor load per stage, every ring barrier waits for one stage's
-    slice (the weights of the stage are issued before its slice, so they complete too), and no
-    slice load sits behind an execz branch."""
+    """The int8 kernels (Q8_0 and Q4_K, W waves, 3-slot ring, stages of 4 blocks): each wave
+    issues 16/W activation loads and one block-factor load per stage (Q4_K one more, the scaled
+    code sums), every ring barrier waits for one stage's slice (the weights of the stage are issued
+    before its slice, so they complete too), and no slice load sits behind an execz branch."""
     seen = set()
     for i, l in enumerate(gemm_asm):
-        m = re.match(r"^(_ZN12_GLOBAL__N_114gemm_i8_kernelILi(\d+)E\S*):", l)
+        m = re.match(r"^(_ZN12_GLOBAL__N_114gemm_i8_kernelILi(\d+)ELi(\d+)E\S*):", l)
         if not m:
             continue
-        w = int(m.group(2))
-        seen.add(w)
+        t, w = int(m.group(2)), int(m.group(3))
+        seen.add((t, w))
         end = next(j for j in range(i, len(gemm_asm)) if "s_endpgm" in gemm_asm[j])
         body = [x.strip() for x in gemm_asm[i:end]]
-        want = 16 // w + 1
+        want = 16 // w + (2 if t == 12 else 1)
         bars, _ = ring_and_epilogue_barriers(body)
         assert len(bars) == 2, (w, len(bars))  # the loop body runs two stages
         for k in bars:
@@ -149,8 +149,8 @@ def test_int8_design_ring(gemm_asm):
             mm = re.match(r"s_cbranch_execz\s+(\S+)", x)
             if mm:
                 for y in skipped_by_execz(body, k, mm.group(1)):
-                    assert not (y.startswith("buffer_load") and y.endswith(" lds")), (w, y)
-    assert seen == {2, 4}, seen
+                    assert not (y.startswith("buffer_load") and y.endswith(" lds")), (t, w, y)
+    assert seen == {(8, 2), (8, 4), (12, 2), (12, 4)}, seen
 
 
 @pytest.fixture(scope="module")

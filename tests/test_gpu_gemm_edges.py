@@ -98,6 +98,7 @@ def quantize(x2d):
 # ---- GPU calls -------------------------------------------------------------------------------
 
 def gemm_codes(dev, w, codes, scales):
+    assert codes.ndim == 2 and codes.shape[1] == w.n_in and scales.shape == (codes.shape[0], -(-w.n_in // 32))
     n_tok = codes.shape[0]
     dc, ds = to_dev(codes), to_dev(scales)
     y = torch.full((n_tok, max(w.n_out, 1)), float("nan"), dtype=torch.float32, device="cuda")
@@ -115,6 +116,8 @@ def gemv_codes(dev, w, codes, scales):
 
 
 def gemm_f32(dev, w, x2d):
+    # the library reads n_tok x n_in floats from the device copy: shapes are checked here
+    assert x2d.ndim == 2 and x2d.shape[1] == w.n_in, x2d.shape
     n_tok = x2d.shape[0]
     dx = to_dev(x2d.astype(np.float32))
     y = torch.full((n_tok, max(w.n_out, 1)), float("nan"), dtype=torch.float32, device="cuda")

@@ -150,6 +150,22 @@ def test_ffn_prefill_vs_oracle(dev, gu_type, down_type, n_embd, n_ff, n_tok, fus
     run_case(dev, gu_type, down_type, n_embd, n_ff, n_tok, fused)
 
 
+@pytest.mark.parametrize("gu_type,down_type,n_embd,n_ff,n_tok", [
+    (Q4_K, Q4_K, 896, 4864, 77),   # configs[1] FFN shapes, gate/up and down on the int8 design
+    (Q4_K, Q8_0, 512, 1000, 33),   # a Q8_0 down on its int8 design, a partial block
+])
+def test_ffn_prefill_two_pass_int8_designs(dev, gu_type, down_type, n_embd, n_ff, n_tok):
+    """The two-pass FFN with the int8 GEMM designs selected (ah_set_gemm_design): the hidden
+    QuantAct bit for bit, gate/up and down within tolerance, down equal to a GEMM on the codes."""
+    for t in {gu_type, down_type}:
+        dev.set_gemm_design(t, chart.Device.GEMM_INT8)
+    try:
+        run_case(dev, gu_type, down_type, n_embd, n_ff, n_tok, False)
+    finally:
+        for t in {gu_type, down_type}:
+            dev.set_gemm_design(t, chart.Device.GEMM_AUTO)
+
+
 @pytest.mark.parametrize("gu_type", [Q4_K, Q3_K])
 def test_ffn_prefill_wide_spread_tokens(dev, gu_type):
     """Tokens no f16 band can carry: the fused epilogue takes their gate / up from the exact path."""

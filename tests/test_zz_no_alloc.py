@@ -30,8 +30,18 @@ def run(dev, fn, w, x):
     return y
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
-def test_noalloc_gemm_equals_gemm(dev, t):
+@pytest.mark.parametrize("t,design", [(8, 0), (12, 0), (14, 0), (8, 2), (12, 2)])
+def test_noalloc_gemm_equals_gemm(dev, t, design):
+    """Every type's default design, and the int8 designs of Q8_0 and Q4_K (their codes, block
+    factors and Q4_K's scaled code sums in the fixed scratch)."""
+    dev.set_gemm_design(t, design)
+    try:
+        check_noalloc_equals_gemm(dev, t)
+    finally:
+        dev.set_gemm_design(t, chart.Device.GEMM_AUTO)
+
+
+def check_noalloc_equals_gemm(dev, t):
     L = dev.lib
     cap = ctypes.c_size_t(0)
     assert L.ah_gemm_noalloc_scratch_bytes(ctypes.byref(cap)) == 0 and cap.value == 64 << 20

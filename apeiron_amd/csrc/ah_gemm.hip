@@ -956,7 +956,7 @@ __global__ void __launch_bounds__(64 * WV, TYPE == AH_GGML_Q4_K ? 4 : 2) gemm_rb
     gemm_rb_body<TYPE, WV, RG>(a, lds);
 }
 
-// ---- int8-MFMA design (Q8_0) ------------------------------------------------------------------
+// ---- int8-MFMA design (Q8_0; Q4_K below) ------------------------------------------------------
 //
 // v_mfma_i32_32x32x32_i8 takes one whole 32-block per MFMA: the activation codes (A, M = 32
 // tokens) from LDS, the weight codes (B, N = 32 rows) straight from the GGUF bytes, and gives the
@@ -974,6 +974,15 @@ __global__ void __launch_bounds__(64 * WV, TYPE == AH_GGML_Q4_K ? 4 : 2) gemm_rb
 // Bounds per 32-block and 32x32 tile: two MFMAs on the matrix core (the int8 one at twice the f16
 // rate) against 32 VALU instructions of 64 lanes (4 cycles each): the VALU bounds this design at
 // about 128 cycles per 65536 int8 operations a SIMD, a quarter of the int8 MFMA peak.
+//
+// Q4_K takes the same tiles with a stage of half a super-block (four 32-element sub-blocks): the
+// int8 MFMA dots the raw nibbles (0..15) of each sub-block, and the fold per sub-block is
+// y += D * (S' d sc_j) - (S' X_j) (dmin m_j), X_j the token's code sum of the sub-block.  Both
+// products come from bf16 outer-product MFMAs: d sc_j and dmin m_j (an f16 times a 6-bit integer,
+// at most 17 significant bits) split exactly into three bf16 each, S' as one bf16 and S' X_j (at
+// most 12 significant bits) as two, hi and lo, which the operand pass writes beside the block
+// factors.  The scale product is exact; the min product rounds once in the MFMA's f32 sum.  The
+// fold is one convert, one FMA and one subtract per element and sub-block.
 //
 // Tiling: W waves, each owning 32 weight rows and the workgroup's 128 tokens (4 token tiles); a
 // stage is 4 blocks (K = 128).  The stage's activation codes (128 tokens x 128 B, chunk-XOR
